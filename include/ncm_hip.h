@@ -1,0 +1,173 @@
+/* ncm_hip.h -- C ABI of libncmhip.so, the MI355X (gfx950) backend for cncm's
+ * matrix-multiplication hot path.
+ *
+ * The library is a drop-in for the kernel/memory surface of the reference's
+ * src/ncm.h: every function below that carries a "replaces" citation keeps the
+ * reference prototype, argument meaning and out-params-last convention, and all
+ * float pointers are DEVICE pointers (the reference's "backend memory",
+ * ncm.h:29-34 and ncm.h:141-143).  Entry points marked "extension" have no
+ * one-to-one reference prototype: each replaces a sequence of reference calls
+ * that the caller would otherwise issue (cited per function).
+ *
+ * Execution model: one HIP stream per process (ncm_hip_stream()); every kernel
+ * entry point is asynchronous on it, every mem_* copy is synchronous (as the
+ * reference's cudaMemcpy-based mem_* are, tensor.c:323-344).
+ *
+ * Errors: by default a failing HIP call or an invalid argument prints a
+ * message and calls exit(1), the reference behaviour (tensor.c:10-12,
+ * tensor.c:301-305).  ncm_hip_set_error_mode(NCM_ERR_RECORD) switches to
+ * "record and return": the call does nothing further and the message is kept
+ * for ncm_hip_last_error().
+ */
+#ifndef NCM_HIP_H
+#define NCM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------ */
+/* runtime (extension: the reference selects its device implicitly)    */
+/* ------------------------------------------------------------------ */
+
+#define NCM_ERR_EXIT   0
+#define NCM_ERR_RECORD 1
+
+/* Select device, create the stream, load the embedded gfx950 code objects.
+ * Called implicitly by the first entry point; returns 0 on success. */
+int   ncm_hip_init(int device);
+void  ncm_hip_set_error_mode(int mode);
+/* Copies the last error message (if any) into buf; returns its error code
+ * (0 = no error since the last call) and clears it. */
+int   ncm_hip_last_error(char *buf, size_t cap);
+/* Blocks until all work queued on the library stream has finished. */
+void  ncm_hip_sync(void);
+/* The hipStream_t every kernel entry point launches on. */
+void *ncm_hip_stream(void);
+/* Device allocation helpers for callers that do not use Tensor/arenas. */
+void *ncm_hip_malloc(size_t bytes);
+void  ncm_hip_free(void *p);
+
+/* ------------------------------------------------------------------ */
+/* tensor + memory substrate -- replaces src/tensor.c (ncm.h:27-56)     */
+/* ------------------------------------------------------------------ */
+
+#define NCM_MAX_DIMS 4
+
+/* Same layout as the reference Tensor (ncm.h:29-34). */
+typedef struct {
+    float  *data;
+    int64_t shape[NCM_MAX_DIMS];
+    int     ndim;
+    int64_t n;
+} Tensor;
+
+/* replaces tensor_alloc / tensor_free / tensor_numel, ncm.h:37-39, tensor.c:15-42 */
+Tensor *tensor_alloc(int ndim, const int64_t *shape);
+void    tensor_free(Tensor *t);
+int64_t tensor_numel(int ndim, const int64_t *shape);
+/* replaces tensor_to_host / tensor_to_backend, ncm.h:42-43, tensor.c:44-62 */
+void tensor_to_host(const Tensor *t, float *out);
+void tensor_to_backend(Tensor *t, const float *in);
+/* replaces mem_d2h / mem_h2d / mem_d2d, ncm.h:44-46, tensor.c:323-344 (synchronous) */
+void mem_d2h(void *h, const void *d, size_t n);
+void mem_h2d(void *d, const void *h, size_t n);
+void mem_d2d(void *d, const void *s, size_t n);
+/* replaces the scratch bump arena, ncm.h:49-53, tensor.c:268-321:
+ * 16-byte aligned bump allocation, overflow is an error. */
+void   arena_init(size_t bytes);
+void   arena_init_default(void);
+float *arena_alloc(size_t n_floats);
+void   arena_reset(void);
+void   arena_free(void);
+/* replaces the persistent arena, ncm.h:54-55, tensor.c:346-365 */
+void   parena_init(size_t bytes);
+float *parena_alloc(size_t n_floats);
+/* replaces backend_to_host, tensor.c:367-371: malloc'd host copy */
+void  *backend_to_host(const float *d, size_t nbytes);
+
+/* ------------------------------------------------------------------ */
+/* linear (FP32 MFMA GEMM / GEMV)                                      */
+/* ------------------------------------------------------------------ */
+
+#define NCM_ACT_NONE      0
+#define NCM_ACT_SILU      1  /* v/(1+exp(-v)), kernels.c:220-226 */
+#define NCM_ACT_GELU      2  /* exact erf GELU, kernels.c:185-194 */
+#define NCM_ACT_GELU_TANH 3  /* HF gelu_new, kernels.c:207-218 */
+
+/* replaces linear_fwd, ncm.h:145-146, kernels.c:38-54:
+ * y[r,m] = b[m] + sum_k x[r,k] W[m,k];  x:[batch,K], W:[M,K], b:[M]|NULL, y:[batch,M] */
+void linear_fwd(const float *x, const float *W, const float *b,
+                float *y, int64_t batch, int M, int K);
+
+/* extension: linear_fwd with a fused epilogue y = res + act(x W^T + b).
+ * Replaces linear_fwd followed by silu_fwd/gelu_fwd/gelu_tanh_fwd and/or
+ * add_fwd (e.g. ncp.c:296-298, qwen.c:159-161).  res may be NULL; res may
+ * alias y (in-place residual update). */
+void linear_fwd_ep(const float *x, const float *W, const float *b,
+                   const float *res, float *y, int64_t batch, int M, int K, int act);
+
+/* extension: the linear backward of the autograd tape, host path
+ * train_tape.c:680-725 and device path train_tape.c:1978-2000:
+ *   dx[r,k] += sum_m dy[r,m] W[m,k]        (dX = dY . W)
+ *   dW[m,k] += sum_r dy[r,m] x[r,k]        (dW = dY^T . X)
+ *   db[m]   += sum_r dy[r,m]
+ * Any of dx, dW, db may be NULL to skip that gradient.  Accumulates, like
+ * the tape's gradient map. */
+void linear_bwd(const float *x, const float *W, const float *dy,
+                float *dx, float *dW, float *db, int64_t batch, int M, int K);
+
+/* extension: which kernel a linear call launches (op 0 = linear_fwd,
+ * 1 = dX of linear_bwd, 2 = dW of linear_bwd) for 16-byte aligned operands,
+ * written to `kernel`; returns the number of K splits (>= 1; a split
+ * count above 1 adds a splitk_reduce launch), -1 on bad arguments. */
+int ncm_hip_linear_plan(int op, int64_t batch, int M, int K, char *kernel, size_t cap);
+
+/* ------------------------------------------------------------------ */
+/* VQ nearest-codeword search                                          */
+/* ------------------------------------------------------------------ */
+
+/* replaces rowwise_l2sq, ncm.h:187-188, kernels.c:753-770:
+ * d2[i,j] = (float) sum_c ((double)a[i,c] - b[j,c])^2, fp64 serial over c. */
+void rowwise_l2sq(const float *a, const float *b, float *d2,
+                  int64_t rows, int64_t colsA, int C);
+
+/* extension: fused distance + argmin.  Replaces rowwise_l2sq followed by
+ * the device->host copy and the host strict-'<' scan of vq.c:410-443:
+ * idx[i] = lowest j minimising (float) sum_c ((double)a[i,c]-E[j,c])^2.
+ * Bit-exact with that reference sequence; never materialises the rows x V
+ * distance matrix.  idx is a device int32 array. */
+void vq_argmin(const float *a, const float *E, int *idx, int64_t rows, int V, int D);
+
+/* extension: the multiscale residual quantiser of vq_z_to_idx
+ * (vq.c:378-500) for configurations whose every level has length L
+ * (area/linear resampling are identities) and Phi disabled
+ * (quant_resi_ratio = 0).  Per level lv: codes = vq_argmin(z_rest, E[lv]);
+ * z_hat += E[lv][codes]; z_rest -= E[lv][codes], all in float.
+ *   z:[B*L, D]; E[lv]:[vocabs[lv], D] (host array of device pointers);
+ *   idx:[B, n_levels*L] level-major per batch row (vq.c:444-445), device int32;
+ *   z_hat, z_rest:[B*L, D] outputs. */
+void vq_quantize_multiscale(const float *z, const float *const *E, const int *vocabs,
+                            int n_levels, int B, int L, int D,
+                            int *idx, float *z_hat, float *z_rest);
+
+/* ------------------------------------------------------------------ */
+/* greedy id                                                           */
+/* ------------------------------------------------------------------ */
+
+/* replaces argmax_row, ncm.h:186, kernels.c:731-735.  HOST pointer, as in
+ * the reference (qwen.c:220-222 copies the logits row to the host first). */
+int argmax_row(const float *x, int n);
+
+/* extension: device argmax over each of `rows` rows of length n, lowest
+ * index on ties.  Replaces backend_to_host + argmax_row (qwen.c:220-222). */
+void argmax_rows(const float *x, int *idx, int64_t rows, int n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NCM_HIP_H */

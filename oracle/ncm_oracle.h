@@ -1,0 +1,50 @@
+/* ncm_oracle.h -- CPU restatement of the reference (SaphiraLinux/saphira-cncm)
+ * arithmetic on the matrix-multiplication hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This is the checker the HIP library is compared
+ * against; it is never linked into libncmhip.so.  Only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.
+ *
+ * Every function reproduces the reference's operation order exactly (fp64
+ * accumulators, serial reduction order, float roundings at the same points),
+ * so its results are bit-identical to the reference CPU build; the file:line
+ * each one follows is given beside it.  Build flags keep IEEE semantics:
+ * -std=c11 (no FMA contraction), no -ffast-math.
+ */
+#ifndef NCM_ORACLE_H
+#define NCM_ORACLE_H
+
+#include <stdint.h>
+
+/* src/kernels.c:38-54 linear_fwd (CPU branch) */
+void orc_linear_fwd(const float *x, const float *W, const float *b, float *y,
+                    int64_t batch, int M, int K);
+/* src/train_tape.c:680-725 TOP_LINEAR host backward (accumulating) */
+void orc_linear_bwd(const float *x, const float *W, const float *dy,
+                    float *dx, float *dW, float *db, int64_t batch, int M, int K);
+/* src/kernels.c:753-770 rowwise_l2sq (CPU branch) */
+void orc_l2sq(const float *a, const float *b, float *d2, int64_t rows, int64_t cols, int C);
+/* rowwise_l2sq + host strict-'<' argmin of src/vq.c:440-443, per row */
+void orc_vq_argmin(const float *a, const float *E, int *idx, int64_t rows, int V, int D);
+/* src/vq.c:388-500 vq_z_to_idx_soft with rng = NULL, every level of length L
+ * (identity resampling) and quant_resi disabled. */
+void orc_vq_multiscale(const float *z, const float *const *E, const int *vocabs,
+                       int n_levels, int B, int L, int D,
+                       int *idx, float *z_hat, float *z_rest);
+/* src/kernels.c:731-735 argmax_row */
+int orc_argmax_row(const float *x, int n);
+/* src/kernels.c:185-194, 207-218, 220-226 activations; :843-849 add */
+void orc_gelu(const float *x, float *y, int64_t n);
+void orc_gelu_tanh(const float *x, float *y, int64_t n);
+void orc_silu(const float *x, float *y, int64_t n);
+void orc_add(const float *a, const float *b, float *y, int64_t n);
+
+/* src/kernels.c:774-780 rng_next (xorshift64*) and the ktest generator of
+ * tests/ktest_kernels.c:8-12, for seeded inputs shared with the reference. */
+uint64_t orc_rng_next(uint64_t *state);
+void orc_fill_ktest(uint64_t *state, float *out, int64_t n);
+
+/* threads used by the OpenMP loops (0 = runtime default) */
+void orc_set_threads(int n);
+
+#endif

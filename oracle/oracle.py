@@ -1,0 +1,207 @@
+"""ctypes binding of the CPU oracle (liboracle.so) and of the reference's own
+CPU code compiled from /root/reference (_ref/libref.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, never by the library.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_LIB = os.path.join(HERE, "liboracle.so")
+REF_LIB = os.path.join(HERE, "_ref", "libref.so")
+KTEST_BIN = os.path.join(HERE, "_ref", "ktest")
+
+vp = ctypes.c_void_p
+i64 = ctypes.c_int64
+ci = ctypes.c_int
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+_orc = None
+
+
+def lib():
+    global _orc
+    if _orc is None:
+        if not os.path.exists(ORACLE_LIB):
+            raise FileNotFoundError(f"{ORACLE_LIB} not built (make -C oracle)")
+        L = ctypes.CDLL(ORACLE_LIB)
+        sigs = {
+            "orc_linear_fwd": (None, [vp, vp, vp, vp, i64, ci, ci]),
+            "orc_linear_bwd": (None, [vp, vp, vp, vp, vp, vp, i64, ci, ci]),
+            "orc_l2sq": (None, [vp, vp, vp, i64, i64, ci]),
+            "orc_vq_argmin": (None, [vp, vp, vp, i64, ci, ci]),
+            "orc_vq_multiscale": (None, [vp, ctypes.POINTER(vp), ctypes.POINTER(ci), ci, ci, ci, ci,
+                                         vp, vp, vp]),
+            "orc_argmax_row": (ci, [vp, ci]),
+            "orc_gelu": (None, [vp, vp, i64]),
+            "orc_gelu_tanh": (None, [vp, vp, i64]),
+            "orc_silu": (None, [vp, vp, i64]),
+            "orc_add": (None, [vp, vp, vp, i64]),
+            "orc_rng_next": (ctypes.c_uint64, [ctypes.POINTER(ctypes.c_uint64)]),
+            "orc_fill_ktest": (None, [ctypes.POINTER(ctypes.c_uint64), vp, i64]),
+            "orc_set_threads": (None, [ci]),
+        }
+        for n, (r, a) in sigs.items():
+            f = getattr(L, n)
+            f.restype = r
+            f.argtypes = a
+        _orc = L
+    return _orc
+
+
+def set_threads(n):
+    lib().orc_set_threads(int(n))
+
+
+def linear_fwd(x, W, b=None):
+    x, W = _f32(x), _f32(W)
+    b = None if b is None else _f32(b)
+    batch, K = x.shape
+    M = W.shape[0]
+    y = np.empty((batch, M), np.float32)
+    lib().orc_linear_fwd(_ptr(x), _ptr(W), _ptr(b), _ptr(y), batch, M, K)
+    return y
+
+
+def linear_bwd(x, W, dy, dx=None, dW=None, db=None, want=("dx", "dW", "db")):
+    """Returns (dx, dW, db) accumulated into the given arrays (zeros if None)."""
+    x, W, dy = _f32(x), _f32(W), _f32(dy)
+    batch, K = x.shape
+    M = W.shape[0]
+    dx = (np.zeros((batch, K), np.float32) if dx is None else _f32(dx).copy()) if "dx" in want else None
+    dW = (np.zeros((M, K), np.float32) if dW is None else _f32(dW).copy()) if "dW" in want else None
+    db = (np.zeros(M, np.float32) if db is None else _f32(db).copy()) if "db" in want else None
+    lib().orc_linear_bwd(_ptr(x), _ptr(W), _ptr(dy), _ptr(dx), _ptr(dW), _ptr(db), batch, M, K)
+    return dx, dW, db
+
+
+def l2sq(a, b):
+    a, b = _f32(a), _f32(b)
+    d2 = np.empty((a.shape[0], b.shape[0]), np.float32)
+    lib().orc_l2sq(_ptr(a), _ptr(b), _ptr(d2), a.shape[0], b.shape[0], a.shape[1])
+    return d2
+
+
+def vq_argmin(a, E):
+    a, E = _f32(a), _f32(E)
+    idx = np.empty(a.shape[0], np.int32)
+    lib().orc_vq_argmin(_ptr(a), _ptr(E), _ptr(idx), a.shape[0], E.shape[0], a.shape[1])
+    return idx
+
+
+def vq_multiscale(z, Es, B, L):
+    """z: [B*L, D]; Es: list of [V_l, D].  Returns (idx [B, n*L], z_hat, z_rest)."""
+    z = _f32(z)
+    Es = [_f32(e) for e in Es]
+    n, D = len(Es), z.shape[1]
+    idx = np.empty((B, n * L), np.int32)
+    z_hat = np.empty_like(z)
+    z_rest = np.empty_like(z)
+    eptrs = (vp * n)(*[e.ctypes.data for e in Es])
+    vocs = (ci * n)(*[e.shape[0] for e in Es])
+    lib().orc_vq_multiscale(_ptr(z), eptrs, vocs, n, B, L, D, _ptr(idx), _ptr(z_hat), _ptr(z_rest))
+    return idx, z_hat, z_rest
+
+
+def argmax_row(x):
+    x = _f32(x)
+    return lib().orc_argmax_row(_ptr(x), x.size)
+
+
+def act(name, x):
+    x = _f32(x)
+    y = np.empty_like(x)
+    getattr(lib(), "orc_" + name)(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def ktest_fill(state, n):
+    """tests/ktest_kernels.c:8-12 generator; returns (values, new_state)."""
+    st = ctypes.c_uint64(state)
+    out = np.empty(n, np.float32)
+    lib().orc_fill_ktest(ctypes.byref(st), _ptr(out), n)
+    return out, st.value
+
+
+# ---- the reference itself (only where /root/reference was compiled) ----
+_ref = None
+
+
+def ref_available():
+    return os.path.exists(REF_LIB)
+
+
+def ref():
+    global _ref
+    if _ref is None:
+        L = ctypes.CDLL(REF_LIB, mode=os.RTLD_LAZY)
+        sigs = {
+            "linear_fwd": (None, [vp, vp, vp, vp, i64, ci, ci]),
+            "rowwise_l2sq": (None, [vp, vp, vp, i64, i64, ci]),
+            "argmax_row": (ci, [vp, ci]),
+            "gelu_fwd": (None, [vp, vp, i64]),
+            "gelu_tanh_fwd": (None, [vp, vp, i64]),
+            "silu_fwd": (None, [vp, vp, i64]),
+            "refg_linear_bwd": (None, [vp, vp, vp, vp, vp, vp, vp, ctypes.c_longlong, ci, ci]),
+            "refg_vq_multiscale": (ci, [vp, vp, vp, ci, ci, ci, ci, vp, vp, vp]),
+        }
+        for n, (r, a) in sigs.items():
+            f = getattr(L, n)
+            f.restype = r
+            f.argtypes = a
+        _ref = L
+    return _ref
+
+
+def ref_linear_fwd(x, W, b=None):
+    x, W = _f32(x), _f32(W)
+    b = None if b is None else _f32(b)
+    y = np.empty((x.shape[0], W.shape[0]), np.float32)
+    ref().linear_fwd(_ptr(x), _ptr(W), _ptr(b), _ptr(y), x.shape[0], W.shape[0], x.shape[1])
+    return y
+
+
+def ref_linear_bwd(x, W, b, dy, dx0=None, dW0=None, db0=None):
+    x, W, dy = _f32(x), _f32(W), _f32(dy)
+    b = None if b is None else _f32(b)
+    batch, K = x.shape
+    M = W.shape[0]
+    dx = np.zeros((batch, K), np.float32) if dx0 is None else _f32(dx0).copy()
+    dW = np.zeros((M, K), np.float32) if dW0 is None else _f32(dW0).copy()
+    db = np.zeros(M, np.float32) if db0 is None else _f32(db0).copy()
+    ref().refg_linear_bwd(_ptr(x), _ptr(W), _ptr(b), _ptr(dy), _ptr(dx), _ptr(dW),
+                          _ptr(db) if b is not None else None, batch, M, K)
+    return dx, dW, (db if b is not None else None)
+
+
+def ref_l2sq(a, b):
+    a, b = _f32(a), _f32(b)
+    d2 = np.empty((a.shape[0], b.shape[0]), np.float32)
+    ref().rowwise_l2sq(_ptr(a), _ptr(b), _ptr(d2), a.shape[0], b.shape[0], a.shape[1])
+    return d2
+
+
+def ref_vq_multiscale(z, Es, B, L):
+    z = _f32(z)
+    Es = [_f32(e) for e in Es]
+    n, D = len(Es), z.shape[1]
+    flat = np.ascontiguousarray(np.concatenate([e.reshape(-1) for e in Es]))
+    vocs = np.array([e.shape[0] for e in Es], np.int32)
+    idx = np.empty((B, n * L), np.int32)
+    z_hat = np.empty_like(z)
+    z_rest = np.empty_like(z)
+    rc = ref().refg_vq_multiscale(_ptr(z), _ptr(flat), _ptr(vocs), n, B, L, D, _ptr(idx),
+                                  _ptr(z_hat), _ptr(z_rest))
+    assert rc == 0
+    return idx, z_hat, z_rest

@@ -1,0 +1,16 @@
+/* blobs.S -- embeds the gfx950 code objects built from csrc/*.hip into
+ * libncmhip.so; runtime.c hands them to hipModuleLoadData. */
+    .section .rodata
+    .balign 4096
+    .globl ncm_co_gemm
+ncm_co_gemm:
+    .incbin "gemm.co"
+    .balign 4096
+    .globl ncm_co_vq
+ncm_co_vq:
+    .incbin "vq.co"
+    .balign 4096
+    .globl ncm_co_ops
+ncm_co_ops:
+    .incbin "ops.co"
+    .section .note.GNU-stack,"",@progbits

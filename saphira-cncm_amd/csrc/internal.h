@@ -1,0 +1,47 @@
+/* internal.h -- shared declarations of the libncmhip host runtime (C11). */
+#ifndef NCM_INTERNAL_H
+#define NCM_INTERNAL_H
+
+#define __HIP_PLATFORM_AMD__ 1
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "ncm_hip.h"
+
+#define NCM_E_HIP   1
+#define NCM_E_ARG   2
+#define NCM_E_OOM   3
+#define NCM_E_INIT  4
+
+/* Records (or, in NCM_ERR_EXIT mode, reports and exits on) an error. Returns code. */
+int ncm_fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+/* 0 when the runtime is usable, otherwise an error code (already recorded). */
+int ncm_ready(void);
+hipStream_t ncm_stream(void);
+
+/* Looks up a kernel of one of the embedded code objects by name (cached). */
+hipFunction_t ncm_kernel(const char *name);
+/* Launches `f` on the library stream with one by-value argument block per
+ * entry of args (hipModuleLaunchKernel kernelParams convention). */
+int ncm_launch(hipFunction_t f, unsigned gx, unsigned gy, unsigned gz, unsigned block,
+               void **args);
+int ncm_launch_named(const char *name, unsigned gx, unsigned gy, unsigned gz, unsigned block,
+                     void **args);
+
+/* Library-owned device workspaces (grown on demand, stream-synchronised
+ * before a grow).  Slot ids keep independent users apart. */
+enum { WS_SPLITK = 0, WS_COLSUM = 1, WS_VQ = 2, WS_VQ2 = 3, WS_COUNT = 4 };
+void *ncm_workspace(int slot, size_t bytes);
+
+#define HIP_TRY(call)                                                              \
+    do {                                                                           \
+        hipError_t e_ = (call);                                                    \
+        if (e_ != hipSuccess)                                                      \
+            return ncm_fail(NCM_E_HIP, "%s:%d %s: %s", __FILE__, __LINE__, #call, \
+                            hipGetErrorString(e_));                                \
+    } while (0)
+
+static inline int is_aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+#endif

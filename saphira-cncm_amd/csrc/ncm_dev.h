@@ -1,0 +1,90 @@
+// ncm_dev.h -- device helpers shared by the gfx950 kernels of libncmhip.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// Activation codes; must match NCM_ACT_* in include/ncm_hip.h.
+enum { ACT_NONE = 0, ACT_SILU = 1, ACT_GELU = 2, ACT_GELU_TANH = 3 };
+
+// Activations in the form the reference applies them to a float value
+// (kernels.c:167-174 SiLU/GELU in float; kernels.c:207-218 gelu_new, whose
+// CPU path evaluates in double).
+__device__ __forceinline__ float ncm_act(float v, int act) {
+    switch (act) {
+    case ACT_SILU: return v / (1.0f + expf(-v));
+    case ACT_GELU: return 0.5f * v * (1.0f + erff(v * 0.7071067811865475f));
+    case ACT_GELU_TANH: {
+        double d = v;
+        double t = 0.7978845608028654 * (d + 0.044715 * d * d * d);
+        return (float)(0.5 * d * (1.0 + tanh(t)));
+    }
+    default: return v;
+    }
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// One 16x16x4 fp32 MFMA: lane l supplies A[l%16][l/16] and B[l/16][l%16];
+// the result holds D[4*(l/16)+r][l%16] in component r.
+__device__ __forceinline__ f4 mfma4(float a, float b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+template <int ROWS, int COLS, int NT, bool VEC>
+struct TileLoader {
+    static constexpr int F4 = ROWS * COLS / 4;
+    static constexpr int PER = (F4 + NT - 1) / NT;
+    f4 r[PER];
+
+    // Loads the ROWS x COLS tile whose top-left element is src[row0*ld + col0];
+    // rows >= row_end or cols >= col_end read as zero.
+    __device__ __forceinline__ void load(const float *__restrict__ src, int ld, int row0, int col0,
+                                         int row_end, int col_end, int tid) {
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            int f = tid + j * NT;
+            int rr = f / (COLS / 4);
+            int cc = (f % (COLS / 4)) * 4;
+            int gr = row0 + rr, gc = col0 + cc;
+            f4 v = {0.f, 0.f, 0.f, 0.f};
+            if ((F4 % NT == 0 || f < F4) && gr < row_end) {
+                const float *p = src + (int64_t)gr * ld + gc;
+                if (VEC) {
+                    if (gc < col_end) v = *(const f4 *)p;
+                } else {
+                    if (gc + 0 < col_end) v.x = p[0];
+                    if (gc + 1 < col_end) v.y = p[1];
+                    if (gc + 2 < col_end) v.z = p[2];
+                    if (gc + 3 < col_end) v.w = p[3];
+                }
+            }
+            r[j] = v;
+        }
+    }
+
+    __device__ __forceinline__ void store(float *dst, int tid) {
+        constexpr int LD = COLS + 4;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            int f = tid + j * NT;
+            if (F4 % NT == 0 || f < F4) {
+                int rr = f / (COLS / 4);
+                int cc = (f % (COLS / 4)) * 4;
+                *(f4 *)(dst + rr * LD + cc) = r[j];
+            }
+        }
+    }
+};
+

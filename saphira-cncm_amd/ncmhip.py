@@ -1,0 +1,260 @@
+"""ctypes binding of libncmhip.so, the C ABI declared in include/ncm_hip.h.
+
+This is the host-side mirror used by the tests and the benchmark: numpy
+arrays in, device buffers allocated through the library's own allocator,
+every call checked through ncm_hip_last_error.  It never falls back to a
+CPU path: if libncmhip.so is missing or the GPU is unusable, it raises.
+"""
+import ctypes
+import os
+import re
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(HERE)
+LIB_PATH = os.path.join(HERE, "libncmhip.so")
+HEADER = os.path.join(REPO, "include", "ncm_hip.h")
+
+ACT = {"none": 0, "silu": 1, "gelu": 2, "gelu_tanh": 3}
+
+c_float_p = ctypes.POINTER(ctypes.c_float)
+vp = ctypes.c_void_p
+i64 = ctypes.c_int64
+ci = ctypes.c_int
+sz = ctypes.c_size_t
+
+# name -> (restype, argtypes)
+_SIGS = {
+    "ncm_hip_init": (ci, [ci]),
+    "ncm_hip_set_error_mode": (None, [ci]),
+    "ncm_hip_last_error": (ci, [ctypes.c_char_p, sz]),
+    "ncm_hip_sync": (None, []),
+    "ncm_hip_stream": (vp, []),
+    "ncm_hip_malloc": (vp, [sz]),
+    "ncm_hip_free": (None, [vp]),
+    "tensor_alloc": (vp, [ci, ctypes.POINTER(i64)]),
+    "tensor_free": (None, [vp]),
+    "tensor_numel": (i64, [ci, ctypes.POINTER(i64)]),
+    "tensor_to_host": (None, [vp, vp]),
+    "tensor_to_backend": (None, [vp, vp]),
+    "mem_d2h": (None, [vp, vp, sz]),
+    "mem_h2d": (None, [vp, vp, sz]),
+    "mem_d2d": (None, [vp, vp, sz]),
+    "arena_init": (None, [sz]),
+    "arena_init_default": (None, []),
+    "arena_alloc": (vp, [sz]),
+    "arena_reset": (None, []),
+    "arena_free": (None, []),
+    "parena_init": (None, [sz]),
+    "parena_alloc": (vp, [sz]),
+    "backend_to_host": (vp, [vp, sz]),
+    "linear_fwd": (None, [vp, vp, vp, vp, i64, ci, ci]),
+    "linear_fwd_ep": (None, [vp, vp, vp, vp, vp, i64, ci, ci, ci]),
+    "linear_bwd": (None, [vp, vp, vp, vp, vp, vp, i64, ci, ci]),
+    "ncm_hip_linear_plan": (ci, [ci, i64, ci, ci, ctypes.c_char_p, sz]),
+    "rowwise_l2sq": (None, [vp, vp, vp, i64, i64, ci]),
+    "vq_argmin": (None, [vp, vp, vp, i64, ci, ci]),
+    "vq_quantize_multiscale": (None, [vp, ctypes.POINTER(vp), ctypes.POINTER(ci), ci, ci, ci, ci,
+                                      vp, vp, vp]),
+    "argmax_row": (ci, [vp, ci]),
+    "argmax_rows": (None, [vp, vp, i64, ci]),
+}
+
+
+class NcmError(RuntimeError):
+    pass
+
+
+def header_functions(path=HEADER):
+    """Names of the functions include/ncm_hip.h declares."""
+    text = open(path).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"^[A-Za-z_][\w \*]*?\b([a-z_][a-z0-9_]*)\s*\(", text, flags=re.M)
+    return sorted(set(n for n in names if n not in ("defined",)))
+
+
+_lib = None
+
+
+def load(path=LIB_PATH):
+    """Loads libncmhip.so (raises if it was not built) and binds every symbol."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} not built: run __graft_entry__.build()")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in _SIGS.items():
+        f = getattr(lib, name)
+        f.restype = res
+        f.argtypes = args
+    lib.ncm_hip_set_error_mode(1)  # NCM_ERR_RECORD: raise here instead of exit(1)
+    _lib = lib
+    return lib
+
+
+def check():
+    lib = load()
+    buf = ctypes.create_string_buffer(512)
+    code = lib.ncm_hip_last_error(buf, 512)
+    if code:
+        raise NcmError(f"ncmhip error {code}: {buf.value.decode()}")
+
+
+def init(device=0):
+    lib = load()
+    lib.ncm_hip_init(device)
+    check()
+
+
+def sync():
+    load().ncm_hip_sync()
+    check()
+
+
+def stream():
+    s = load().ncm_hip_stream()
+    check()
+    return s
+
+
+class DeviceBuffer:
+    """A device allocation made by libncmhip (ncm_hip_malloc)."""
+
+    def __init__(self, nbytes, dtype=np.float32, shape=None):
+        lib = load()
+        self.nbytes = int(nbytes)
+        self.dtype = np.dtype(dtype)
+        self.shape = shape if shape is not None else (self.nbytes // self.dtype.itemsize,)
+        self.ptr = lib.ncm_hip_malloc(max(self.nbytes, 16))
+        check()
+
+    @classmethod
+    def from_numpy(cls, arr):
+        arr = np.ascontiguousarray(arr)
+        b = cls(arr.nbytes, arr.dtype, arr.shape)
+        if arr.nbytes:
+            load().mem_h2d(b.ptr, arr.ctypes.data, arr.nbytes)
+            check()
+        return b
+
+    @classmethod
+    def empty(cls, shape, dtype=np.float32):
+        shape = tuple(int(s) for s in (shape if isinstance(shape, (tuple, list)) else (shape,)))
+        n = int(np.prod(shape)) if shape else 1
+        return cls(n * np.dtype(dtype).itemsize, dtype, shape)
+
+    def upload(self, arr):
+        arr = np.ascontiguousarray(arr, dtype=self.dtype)
+        assert arr.nbytes <= self.nbytes
+        load().mem_h2d(self.ptr, arr.ctypes.data, arr.nbytes)
+        check()
+
+    def numpy(self):
+        out = np.empty(self.shape, self.dtype)
+        if out.nbytes:
+            load().mem_d2h(out.ctypes.data, self.ptr, out.nbytes)
+            check()
+        return out
+
+    def free(self):
+        if self.ptr:
+            load().ncm_hip_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def _p(b):
+    return None if b is None else (b.ptr if isinstance(b, DeviceBuffer) else b)
+
+
+def linear_fwd(x, W, b, y, batch, M, K, res=None, act="none"):
+    lib = load()
+    if res is None and act == "none":
+        lib.linear_fwd(_p(x), _p(W), _p(b), _p(y), batch, M, K)
+    else:
+        lib.linear_fwd_ep(_p(x), _p(W), _p(b), _p(res), _p(y), batch, M, K, ACT[act])
+    check()
+
+
+def linear_bwd(x, W, dy, dx, dW, db, batch, M, K):
+    load().linear_bwd(_p(x), _p(W), _p(dy), _p(dx), _p(dW), _p(db), batch, M, K)
+    check()
+
+
+def linear_plan(op, batch, M, K):
+    """(kernel name, split count) a linear call launches; op in fwd/dx/dw."""
+    buf = ctypes.create_string_buffer(64)
+    s = load().ncm_hip_linear_plan({"fwd": 0, "dx": 1, "dw": 2}[op], batch, M, K, buf, 64)
+    check()
+    return buf.value.decode(), s
+
+
+def rowwise_l2sq(a, b, d2, rows, cols, C):
+    load().rowwise_l2sq(_p(a), _p(b), _p(d2), rows, cols, C)
+    check()
+
+
+def vq_argmin(a, E, idx, rows, V, D):
+    load().vq_argmin(_p(a), _p(E), _p(idx), rows, V, D)
+    check()
+
+
+def vq_quantize_multiscale(z, Es, vocabs, B, L, D, idx, z_hat, z_rest):
+    n = len(Es)
+    eptrs = (vp * n)(*[_p(e) for e in Es])
+    vocs = (ci * n)(*vocabs)
+    load().vq_quantize_multiscale(_p(z), eptrs, vocs, n, B, L, D, _p(idx), _p(z_hat), _p(z_rest))
+    check()
+
+
+def argmax_rows(x, idx, rows, n):
+    load().argmax_rows(_p(x), _p(idx), rows, n)
+    check()
+
+
+# ---- HIP events on the library stream (timing) ----
+_hip = None
+
+
+def _hiprt():
+    global _hip
+    if _hip is None:
+        _hip = ctypes.CDLL("libamdhip64.so")
+        _hip.hipEventCreate.argtypes = [ctypes.POINTER(vp)]
+        _hip.hipEventRecord.argtypes = [vp, vp]
+        _hip.hipEventSynchronize.argtypes = [vp]
+        _hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), vp, vp]
+        _hip.hipEventDestroy.argtypes = [vp]
+    return _hip
+
+
+class Event:
+    def __init__(self):
+        self.ev = vp()
+        rc = _hiprt().hipEventCreate(ctypes.byref(self.ev))
+        if rc:
+            raise NcmError(f"hipEventCreate: {rc}")
+
+    def record(self):
+        rc = _hiprt().hipEventRecord(self.ev, stream())
+        if rc:
+            raise NcmError(f"hipEventRecord: {rc}")
+
+    def synchronize(self):
+        rc = _hiprt().hipEventSynchronize(self.ev)
+        if rc:
+            raise NcmError(f"hipEventSynchronize: {rc}")
+
+    def elapsed_ms(self, end):
+        ms = ctypes.c_float()
+        rc = _hiprt().hipEventElapsedTime(ctypes.byref(ms), self.ev, end.ev)
+        if rc:
+            raise NcmError(f"hipEventElapsedTime: {rc}")
+        return ms.value

@@ -1,0 +1,142 @@
+"""GPU VQ search against the oracle: codes bit-exact (lowest index on ties),
+residuals bit-exact (float add/sub in the reference order)."""
+import numpy as np
+import pytest
+
+import ncmhip
+import oracle as O
+from conftest import bits_equal
+
+pytestmark = pytest.mark.gpu
+D = ncmhip.DeviceBuffer
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    ncmhip.init(0)
+    print("[gpu] vq tests on device 0", flush=True)
+
+
+def gpu_argmin(a, E):
+    rows, Dm = a.shape
+    idx = D.empty(rows, np.int32)
+    ncmhip.vq_argmin(D.from_numpy(a), D.from_numpy(E), idx, rows, E.shape[0], Dm)
+    return idx.numpy()
+
+
+def gpu_multiscale(z, Es, B, L):
+    Dm = z.shape[1]
+    idx = D.empty((B, len(Es) * L), np.int32)
+    z_hat, z_rest = D.empty(z.shape), D.empty(z.shape)
+    Ed = [D.from_numpy(e) for e in Es]
+    ncmhip.vq_quantize_multiscale(D.from_numpy(z), Ed, [e.shape[0] for e in Es], B, L, Dm, idx, z_hat, z_rest)
+    return idx.numpy(), z_hat.numpy(), z_rest.numpy()
+
+
+def test_golden_multiscale(golden):
+    g = golden("vq_ref.npz")
+    B, L = int(g["B"]), int(g["L"])
+    idx, z_hat, z_rest = gpu_multiscale(g["z"], [g[f"E{i}"] for i in range(3)], B, L)
+    assert np.array_equal(idx, g["idx"])
+    assert bits_equal(z_hat, g["z_hat"]) and bits_equal(z_rest, g["z_rest"])
+
+
+def test_golden_l2sq(golden):
+    g = golden("vq_ref.npz")
+    a, b = g["l2_a"], g["l2_b"]
+    d2 = D.empty((a.shape[0], b.shape[0]))
+    ncmhip.rowwise_l2sq(D.from_numpy(a), D.from_numpy(b), d2, a.shape[0], b.shape[0], a.shape[1])
+    assert bits_equal(d2.numpy(), g["l2_d2"])
+
+
+@pytest.mark.parametrize("rows,V,Dm", [(3000, 1000, 256), (517, 300, 33), (129, 4096, 64), (1, 7, 8),
+                                       (2048, 128, 512)])
+def test_random_vs_oracle(rows, V, Dm):
+    rng = np.random.default_rng(rows + V + Dm)
+    a = rng.standard_normal((rows, Dm)).astype(np.float32)
+    E = (rng.standard_normal((V, Dm)) / np.sqrt(Dm)).astype(np.float32)
+    assert np.array_equal(gpu_argmin(a, E), O.vq_argmin(a, E))
+
+
+def test_exact_ties_take_lowest_index():
+    """Small-integer data: exact distance ties on most rows; every such row
+    fails the certificate and is decided by the exact rescore."""
+    rng = np.random.default_rng(5)
+    a = rng.integers(-2, 3, (4000, 6)).astype(np.float32)
+    E = rng.integers(-2, 3, (64, 6)).astype(np.float32)
+    assert np.array_equal(gpu_argmin(a, E), O.vq_argmin(a, E))
+
+
+def test_duplicate_and_planted_codewords():
+    rng = np.random.default_rng(6)
+    a = rng.standard_normal((1000, 128)).astype(np.float32)
+    E = (rng.standard_normal((512, 128)) / np.sqrt(128)).astype(np.float32)
+    E[500] = E[7]
+    E[300] = a[11]
+    E[301] = a[11]
+    E[2] = a[12] + np.float32(1e-7)
+    got = gpu_argmin(a, E)
+    assert got[11] == 300
+    assert np.array_equal(got, O.vq_argmin(a, E))
+
+
+def test_near_ties_certificate():
+    """Codewords placed symmetrically around rows so that distances differ by
+    a few ulps: the fp32 screen cannot decide them, the rescore must."""
+    rng = np.random.default_rng(8)
+    a = rng.standard_normal((600, 64)).astype(np.float32)
+    E = (rng.standard_normal((256, 64)) / 8).astype(np.float32)
+    for r in range(0, 600, 3):
+        d = (rng.standard_normal(64) * 1e-3).astype(np.float32)
+        E[(r // 3) % 256] = a[r] + d
+        E[((r // 3) + 128) % 256] = a[r] - d
+    assert np.array_equal(gpu_argmin(a, E), O.vq_argmin(a, E))
+
+
+def test_multiscale_random_vs_oracle():
+    rng = np.random.default_rng(9)
+    B, L, Dm = 8, 100, 96
+    z = rng.standard_normal((B * L, Dm)).astype(np.float32)
+    Es = [(rng.standard_normal((V, Dm)) / np.sqrt(Dm)).astype(np.float32) for V in (64, 256, 512, 300)]
+    got = gpu_multiscale(z, Es, B, L)
+    want = O.vq_multiscale(z, Es, B, L)
+    assert np.array_equal(got[0], want[0])
+    assert bits_equal(got[1], want[1]) and bits_equal(got[2], want[2])
+
+
+def test_config3_full_size_sampled():
+    """BASELINE config 3 at full size (65536 x 256, 4 scales of 4096 codes).
+    Every row's path through the scales depends only on that row, so the
+    oracle checks a random sample of rows bit for bit."""
+    rng = np.random.default_rng(2026)
+    R, Dm, V, S = 65536, 256, 4096, 4
+    z = rng.standard_normal((R, Dm)).astype(np.float32)
+    Es = [(rng.standard_normal((V, Dm)) / np.sqrt(Dm)).astype(np.float32) for _ in range(S)]
+    idx, z_hat, z_rest = gpu_multiscale(z, Es, 1, R)
+    assert idx.min() >= 0 and idx.max() < V
+    rows = np.sort(rng.choice(R, 192, replace=False))
+    widx, wh, wr = O.vq_multiscale(z[rows], Es, 1, len(rows))
+    got = idx.reshape(S, R)[:, rows]
+    assert np.array_equal(got, widx.reshape(S, len(rows)))
+    assert bits_equal(z_hat[rows], wh) and bits_equal(z_rest[rows], wr)
+
+
+def test_run_to_run_determinism():
+    rng = np.random.default_rng(10)
+    a = rng.standard_normal((5000, 256)).astype(np.float32)
+    E = (rng.standard_normal((2048, 256)) / 16).astype(np.float32)
+    assert np.array_equal(gpu_argmin(a, E), gpu_argmin(a, E))
+
+
+def test_argmax_rows():
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((6, 151936)).astype(np.float32)
+    x[1, 1000] = x[1, 5] = 50.0
+    x[2, 0] = np.nan
+    x[3, :] = -np.inf
+    x[4, 7] = np.nan
+    idx = D.empty(6, np.int32)
+    ncmhip.argmax_rows(D.from_numpy(x), idx, 6, x.shape[1])
+    got = idx.numpy()
+    assert list(got) == [O.argmax_row(r) for r in x]
+    assert got[1] == 5 and got[2] == 0 and got[3] == 0

@@ -12,6 +12,7 @@
 
 #include <limits.h>
 #include <stdio.h>
+#include <string.h>
 
 /* Must match struct GemmArgs in gemm.hip. */
 typedef struct {
@@ -23,9 +24,13 @@ typedef struct {
     float *ws;
     int Mo, No, K;
     int lda, ldb, ldc;
-    int k_per_split;
     int act;
+    int vec_out;
     int tiles_m, tiles_n;
+    int iters;
+    int dp_tiles;
+    int segs;
+    unsigned a_bytes, b_bytes;
 } GemmArgs;
 
 /* Must match struct GemvArgs in gemm.hip. */
@@ -41,68 +46,96 @@ typedef struct {
 
 enum { L_FWD = 0, L_DX = 1, L_DW = 2 };
 #define TILE 128
-#define BK 16
-#define N_CU 256
+#define BK 32
+#define MAX_SEGS 16
+#define MAX_BUFFER_BYTES ((int64_t)1 << 31)
 
-/* Number of K splits so that the grid covers the chip about twice (two
- * workgroups fit per CU) without cutting a split below 256 reduction steps. */
-static int plan_splits(int tiles, int Kred) {
-    int s = 1;
-    while (tiles * s < 2 * N_CU && Kred / (2 * s) >= 256 && s < 32) s *= 2;
-    return s;
-}
+static const char *gemm_names[3][2] = {
+    /* kind x vec */
+    {"gemm_fwd_s", "gemm_fwd_v"},
+    {"gemm_dx_s", "gemm_dx_v"},
+    {"gemm_dw_s", "gemm_dw_v"},
+};
+static const char *fixup_names[3] = {"gemm_fixup_fwd", "gemm_fixup_dx", "gemm_fixup_dw"};
 
-/* Tiling of one GEMM: tile grid, split count and reduction length per split. */
+/* Work split of one GEMM over the chip: whole rounds of tiles, then the
+ * remaining tiles cut into k-segments (whole groups of 4 slabs) that fill
+ * one more round. */
 typedef struct {
-    int tiles_m, tiles_n, splits, kps;
+    int tiles_m, tiles_n, iters, dp_tiles, segs, blocks;
 } GemmPlan;
 
-static GemmPlan plan_gemm(int Mo, int No, int Kred) {
+static GemmPlan plan_gemm(int Mo, int No, int Kred, int slots) {
     GemmPlan g;
     g.tiles_m = (Mo + TILE - 1) / TILE;
     g.tiles_n = (No + TILE - 1) / TILE;
-    int splits = Kred > 0 ? plan_splits(g.tiles_m * g.tiles_n, Kred) : 1;
-    int kps = (Kred + splits - 1) / splits;
-    kps = (kps + BK - 1) / BK * BK;
-    if (kps <= 0) kps = BK;
-    g.kps = kps;
-    g.splits = Kred > 0 ? (Kred + kps - 1) / kps : 1;
+    int groups = Kred > 0 ? (Kred + 4 * BK - 1) / (4 * BK) : 1;
+    g.iters = 4 * groups;
+    int T = g.tiles_m * g.tiles_n;
+    if (slots < 1) slots = 1;
+    g.dp_tiles = (T / slots) * slots;
+    int R = T - g.dp_tiles;
+    int segs = 1;
+    if (R > 0) {
+        segs = slots / R;
+        if (segs > groups) segs = groups;
+        if (segs > MAX_SEGS) segs = MAX_SEGS;
+        if (segs < 1) segs = 1;
+    }
+    if (segs == 1) g.dp_tiles = T; /* nothing to split: everything runs whole */
+    g.segs = segs;
+    g.blocks = g.dp_tiles + (T - g.dp_tiles) * segs;
     return g;
 }
 
-static const char *gemm_names[3][2][2] = {
-    /* kind x partial x vec */
-    {{"gemm_fwd_store_s", "gemm_fwd_store_v"}, {"gemm_fwd_part_s", "gemm_fwd_part_v"}},
-    {{"gemm_dx_accum_s", "gemm_dx_accum_v"}, {"gemm_dx_part_s", "gemm_dx_part_v"}},
-    {{"gemm_dw_accum_s", "gemm_dw_accum_v"}, {"gemm_dw_part_s", "gemm_dw_part_v"}},
-};
+/* Concurrent workgroups of a GEMM kernel on the device (CUs x occupancy). */
+static int gemm_slots(const char *name) {
+    static char names[8][32];
+    static int vals[8], n = 0;
+    for (int i = 0; i < n; i++)
+        if (strcmp(names[i], name) == 0) return vals[i];
+    hipFunction_t f = ncm_kernel(name);
+    if (!f) return -1;
+    int per_cu = 0;
+    if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, 256, 0) != hipSuccess || per_cu < 1)
+        per_cu = 1;
+    int v = per_cu * ncm_cu_count();
+    if (n < 8) {
+        snprintf(names[n], sizeof names[n], "%s", name);
+        vals[n++] = v;
+    }
+    return v;
+}
+
+/* Bytes spanned by a rows x cols row-major operand with row stride ld. */
+static int64_t extent(int64_t rows, int64_t cols, int64_t ld) { return ((rows - 1) * ld + cols) * 4; }
 
 static int run_gemm(int kind, const float *A, const float *B, float *C, const float *bias,
                     const float *res, int Mo, int No, int Kred, int lda, int ldb, int ldc,
                     int act, int vec) {
     if (Mo <= 0 || No <= 0) return 0;
-    GemmArgs p = {A, B, C, bias, res, NULL, Mo, No, Kred, lda, ldb, ldc, 0, act, 0, 0};
-    GemmPlan g = plan_gemm(Mo, No, Kred);
-    p.tiles_m = g.tiles_m;
-    p.tiles_n = g.tiles_n;
-    p.k_per_split = g.kps;
-    int splits = g.splits, tiles = g.tiles_m * g.tiles_n;
-    const char *(*names)[2][2] = gemm_names;
-    int partial = splits > 1;
-    if (partial) {
-        p.ws = (float *)ncm_workspace(WS_SPLITK, (size_t)splits * Mo * No * sizeof(float));
+    const char *name = gemm_names[kind][vec ? 1 : 0];
+    int slots = gemm_slots(name);
+    if (slots < 0) return NCM_E_INIT;
+    GemmPlan g = plan_gemm(Mo, No, Kred, slots);
+    /* operand extents as stored: A is [Mo][Kred] (k-contiguous) or [Kred][Mo] */
+    int64_t ab = kind == L_DW ? extent(Kred, Mo, lda) : extent(Mo, Kred, lda);
+    int64_t bb = kind == L_FWD ? extent(No, Kred, ldb) : extent(Kred, No, ldb);
+    if (ab >= MAX_BUFFER_BYTES || bb >= MAX_BUFFER_BYTES)
+        return ncm_fail(NCM_E_ARG, "linear: operand of %lld / %lld bytes exceeds the 2 GiB buffer range",
+                        (long long)ab, (long long)bb);
+    GemmArgs p = {A, B, C, bias, res, NULL, Mo, No, Kred, lda, ldb, ldc, act, 0,
+                  g.tiles_m, g.tiles_n, g.iters, g.dp_tiles, g.segs, (unsigned)ab, (unsigned)bb};
+    p.vec_out = No % 4 == 0 && ldc % 4 == 0 && is_aligned16(C);
+    int split_tiles = g.tiles_m * g.tiles_n - g.dp_tiles;
+    if (g.segs > 1) {
+        p.ws = (float *)ncm_workspace(WS_SPLITK, (size_t)split_tiles * g.segs * TILE * TILE * sizeof(float));
         if (!p.ws) return NCM_E_OOM;
     }
     void *args[] = {&p};
-    int rc = ncm_launch_named(names[kind][partial][vec ? 1 : 0], (unsigned)tiles, 1,
-                              (unsigned)splits, 256, args);
-    if (rc || !partial) return rc;
-
-    int accum = kind != L_FWD;
-    int64_t total = (int64_t)Mo * No;
-    const float *ws = p.ws;
-    void *rargs[] = {&ws, &splits, &Mo, &No, &C, &ldc, &bias, &res, &act, &accum};
-    return ncm_launch_named("splitk_reduce", (unsigned)((total + 255) / 256), 1, 1, 256, rargs);
+    int rc = ncm_launch(ncm_kernel(name), (unsigned)g.blocks, 1, 1, 256, args);
+    if (rc || g.segs == 1) return rc;
+    return ncm_launch_named(fixup_names[kind], (unsigned)split_tiles, 1, 1, 256, args);
 }
 
 /* GEMV kernel for a chunk of nb <= 8 batch rows; returns rows per workgroup. */
@@ -175,6 +208,36 @@ void linear_fwd_ep(const float *x, const float *W, const float *b, const float *
     linear_forward("linear_fwd_ep", x, W, b, res, y, batch, M, K, act);
 }
 
+/* Kernel used for the dX of a batch <= 8 backward (transposed GEMV), or NULL. */
+static const char *dxt_name(int nb) {
+    static const char *n[9] = {NULL, "dxt_partial_b1", "dxt_partial_b2", NULL, "dxt_partial_b4",
+                               NULL, NULL, NULL, "dxt_partial_b8"};
+    return nb >= 1 && nb <= 8 ? n[nb] : NULL;
+}
+#define DXT_ROWS 32
+#define COLSUM_ROWS 64
+
+static int run_dxt(const float *dy, const float *W, float *dx, int nb, int M, int K) {
+    int r0 = 0;
+    while (r0 < nb) {
+        int left = nb - r0;
+        int c = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
+        int chunks = (M + DXT_ROWS - 1) / DXT_ROWS;
+        float *part = (float *)ncm_workspace(WS_DXT, (size_t)chunks * c * K * sizeof(float));
+        if (!part) return NCM_E_OOM;
+        const float *dyc = dy + (int64_t)r0 * M;
+        float *dxc = dx + (int64_t)r0 * K;
+        void *a1[] = {&dyc, &W, &M, &K, &part};
+        int rc = ncm_launch_named(dxt_name(c), (unsigned)((K + 255) / 256), (unsigned)chunks, 1, 256, a1);
+        if (rc) return rc;
+        int64_t n = (int64_t)c * K;
+        void *a2[] = {&part, &chunks, &c, &K, &dxc};
+        if ((rc = ncm_launch_named("dxt_final", (unsigned)((n + 255) / 256), 1, 1, 256, a2))) return rc;
+        r0 += c;
+    }
+    return 0;
+}
+
 void linear_bwd(const float *x, const float *W, const float *dy, float *dx, float *dW, float *db,
                 int64_t batch, int M, int K) {
     if (check_dims("linear_bwd", batch, M, K)) return;
@@ -186,21 +249,38 @@ void linear_bwd(const float *x, const float *W, const float *dy, float *dx, floa
     if (ncm_ready()) return;
     int nb = (int)batch;
     if (dx) {
-        int vec = (M % 4 == 0) && (K % 4 == 0) && is_aligned16(dy) && is_aligned16(W);
-        if (run_gemm(L_DX, dy, W, dx, NULL, NULL, nb, K, M, M, K, K, 0, vec)) return;
+        int rc;
+        if (nb <= 8 && K % 4 == 0 && is_aligned16(W))
+            rc = run_dxt(dy, W, dx, nb, M, K);
+        else {
+            int vec = (M % 4 == 0) && (K % 4 == 0) && is_aligned16(dy) && is_aligned16(W);
+            rc = run_gemm(L_DX, dy, W, dx, NULL, NULL, nb, K, M, M, K, K, 0, vec);
+        }
+        if (rc) return;
     }
     if (dW) {
-        int vec = (M % 4 == 0) && (K % 4 == 0) && is_aligned16(dy) && is_aligned16(x);
-        if (run_gemm(L_DW, dy, x, dW, NULL, NULL, M, K, nb, M, K, K, 0, vec)) return;
+        int rc;
+        if (nb <= 8) {
+            int vec = K % 4 == 0 && is_aligned16(x) && is_aligned16(dW);
+            int K4 = (K + 3) / 4;
+            int64_t n = (int64_t)M * K4;
+            void *a[] = {&dy, &x, &dW, &nb, &M, &K};
+            rc = ncm_launch_named(vec ? "dw_rank_v" : "dw_rank_s", (unsigned)((n + 255) / 256), 1, 1, 256, a);
+        } else {
+            int vec = (M % 4 == 0) && (K % 4 == 0) && is_aligned16(dy) && is_aligned16(x);
+            rc = run_gemm(L_DW, dy, x, dW, NULL, NULL, M, K, nb, M, K, K, 0, vec);
+        }
+        if (rc) return;
     }
     if (db) {
-        int rpc = 512;
-        int chunks = (nb + rpc - 1) / rpc;
+        int chunks = (nb + COLSUM_ROWS - 1) / COLSUM_ROWS;
         double *part = (double *)ncm_workspace(WS_COLSUM, (size_t)chunks * M * sizeof(double));
         if (!part) return;
         int64_t rows = nb;
-        void *a1[] = {&dy, &rows, &M, &rpc, &part};
-        if (ncm_launch_named("colsum_partial", (unsigned)((M + 255) / 256), (unsigned)chunks, 1, 256, a1))
+        int vec = M % 4 == 0 && is_aligned16(dy);
+        void *a1[] = {&dy, &rows, &M, &part};
+        if (ncm_launch_named(vec ? "colsum_partial_v" : "colsum_partial_s", (unsigned)((M + 255) / 256),
+                             (unsigned)chunks, 1, 256, a1))
             return;
         void *a2[] = {&part, &chunks, &M, &db};
         ncm_launch_named("colsum_final", (unsigned)((M + 255) / 256), 1, 1, 256, a2);
@@ -215,9 +295,20 @@ int ncm_hip_linear_plan(int op, int64_t batch, int M, int K, char *kernel, size_
         gemv_name(nb >= 8 ? 8 : nb >= 4 ? 4 : nb >= 2 ? 2 : 1, M, K % 4 == 0, kernel, cap);
         return 1;
     }
+    if (op == L_DX && nb <= 8 && K % 4 == 0) {
+        snprintf(kernel, cap, "%s", dxt_name(nb >= 8 ? 8 : nb >= 4 ? 4 : nb >= 2 ? 2 : 1));
+        return 1;
+    }
+    if (op == L_DW && nb <= 8) {
+        snprintf(kernel, cap, "%s", K % 4 == 0 ? "dw_rank_v" : "dw_rank_s");
+        return 1;
+    }
     int Mo = op == L_DW ? M : nb, No = op == L_FWD ? M : K, Kred = op == L_FWD ? K : (op == L_DX ? M : nb);
     int vec = op == L_FWD ? K % 4 == 0 : (M % 4 == 0 && K % 4 == 0);
-    GemmPlan g = plan_gemm(Mo, No, Kred);
-    snprintf(kernel, cap, "%s", gemm_names[op][g.splits > 1][vec]);
-    return g.splits;
+    const char *name = gemm_names[op][vec];
+    int slots = gemm_slots(name);
+    if (slots < 0) return -1;
+    GemmPlan g = plan_gemm(Mo, No, Kred, slots);
+    snprintf(kernel, cap, "%s", name);
+    return g.segs;
 }

@@ -16,6 +16,7 @@ static const unsigned char *const co_blobs[] = {ncm_co_gemm, ncm_co_vq, ncm_co_o
 
 static int g_state = 0; /* 0 = not initialised, 1 = ready, <0 = failed */
 static int g_device = 0;
+static int g_cus = 0;
 static hipStream_t g_stream = NULL;
 static hipModule_t g_mod[N_MODULES];
 static int g_err_mode = NCM_ERR_EXIT;
@@ -62,6 +63,7 @@ int ncm_hip_init(int device) {
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return ncm_fail(NCM_E_INIT, "device %d is %s; this library is built for gfx950 only",
                         device, prop.gcnArchName);
+    g_cus = prop.multiProcessorCount;
     HIP_TRY(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
     for (int i = 0; i < N_MODULES; i++) HIP_TRY(hipModuleLoadData(&g_mod[i], co_blobs[i]));
     g_device = device;
@@ -156,6 +158,8 @@ void *ncm_workspace(int slot, size_t bytes) {
     g_ws_size[slot] = sz;
     return p;
 }
+
+int ncm_cu_count(void) { return g_cus > 0 ? g_cus : 1; }
 
 /* ---- plain device allocation ---- */
 void *ncm_hip_malloc(size_t bytes) {

@@ -47,3 +47,20 @@ def test_host_argmax_row_matches_reference_semantics():
 def test_no_device_is_a_clean_error():
     with pytest.raises(ncmhip.NcmError):
         ncmhip.init(0)
+
+
+def test_code_objects_have_no_scalar_stores():
+    """Every embedded gfx950 code object writes through vector memory only:
+    no scalar-cache stores, atomics, write-backs or discards."""
+    import glob
+    import re
+    import subprocess
+    objdump = "/opt/rocm/llvm/bin/llvm-objdump"
+    cos = glob.glob(os.path.join(ncmhip.HERE, "build", "*.co"))
+    if not cos or not os.path.exists(objdump):
+        pytest.skip("code objects or llvm-objdump not available")
+    bad = re.compile(r"\bs_(store|atomic|buffer_store|buffer_atomic|dcache_wb|dcache_discard|scratch_store)")
+    for co in cos:
+        text = subprocess.run([objdump, "-d", co], check=True, capture_output=True, text=True).stdout
+        hits = [ln for ln in text.splitlines() if bad.search(ln)]
+        assert not hits, (co, hits[:3])

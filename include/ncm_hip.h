@@ -155,6 +155,54 @@ void vq_quantize_multiscale(const float *z, const float *const *E, const int *vo
                             int *idx, float *z_hat, float *z_rest);
 
 /* ------------------------------------------------------------------ */
+/* norms, RoPE, attention, layout, elementwise                         */
+/* ------------------------------------------------------------------ */
+
+/* replaces rmsnorm_fwd, ncm.h:154, kernels.c:150-162 (eps 1e-6; w may be NULL) */
+void rmsnorm_fwd(const float *x, const float *w, float *y, int64_t rows, int C);
+/* replaces layernorm_fwd (eps 1e-6), ncm.h:149-150, kernels.c:101-117 */
+void layernorm_fwd(const float *x, const float *w, const float *b, float *y, int64_t rows, int C);
+/* replaces layernorm_eps_fwd, ncm.h:151-152, kernels.c:132-148 */
+void layernorm_eps_fwd(const float *x, const float *w, const float *b, float *y, int64_t rows, int C, float eps);
+/* replaces gelu_fwd / gelu_tanh_fwd / silu_fwd, ncm.h:153-156, kernels.c:185-226 */
+void gelu_fwd(const float *x, float *y, int64_t n);
+void gelu_tanh_fwd(const float *x, float *y, int64_t n);
+void silu_fwd(const float *x, float *y, int64_t n);
+/* replaces rope_apply / rope_apply_gqa, ncm.h:158-161, kernels.c:285-308:
+ * rotate-half RoPE in place on [B][H][T][hd] (q) and [B][K][T][hd] (k);
+ * tables [T][hd] pair-duplicated; q or k may be NULL. */
+void rope_apply(float *q, float *k, const float *cos, const float *sin, int B, int H, int T, int hd);
+void rope_apply_gqa(float *q, float *k, const float *cos, const float *sin, int B, int H, int K, int T, int hd);
+/* replaces heads_transpose_fwd / _b, ncm.h:162-164, kernels.c:322-357 */
+void heads_transpose_fwd(const float *in, float *out, int64_t T, int H, int hd);
+void heads_transpose_fwd_b(const float *in, float *out, int B, int64_t T, int H, int hd);
+/* replaces sdpa_fwd / sdpa_fwd_gqa, ncm.h:165-170, kernels.c:423-507:
+ * softmax(Q K^T / sqrt(hd) + mask) V; q [B][Hq][Tq][hd], k/v [B][Hkv][Tkv][hd],
+ * mask [Tq][Tkv] additive or NULL; kv head = h / (Hq/Hkv), Hq % Hkv == 0. */
+void sdpa_fwd(const float *q, const float *k, const float *v, const float *mask, float *out,
+              int B, int H, int Tq, int Tkv, int hd);
+void sdpa_fwd_gqa(const float *q, const float *k, const float *v, const float *mask, float *out,
+                  int B, int Hq, int Hkv, int Tq, int Tkv, int hd);
+/* extension: causal SDPA-GQA with the mask generated in the kernel: query tq
+ * sees keys <= tq + (Tkv - Tq).  Replaces building the T x T -1e9 mask on the
+ * host and uploading it (qwen.c:130-138, gpt2.c:112-121) + sdpa_fwd_gqa. */
+void sdpa_fwd_gqa_causal(const float *q, const float *k, const float *v, float *out,
+                         int B, int Hq, int Hkv, int Tq, int Tkv, int hd);
+/* replaces embedding_fwd, ncm.h:147, kernels.c:67-74 (ids must be valid, as
+ * there); embedding_fwd_v is the extension that clamps ids outside [0, V). */
+void embedding_fwd(const float *W, const int *idx, float *y, int64_t n, int D);
+void embedding_fwd_v(const float *W, int V, const int *idx, float *y, int64_t n, int D);
+/* replaces add_fwd / scale_fwd / mul_fwd / add_inplace_fwd, ncm.h:189-192, kernels.c:829-874 */
+void add_fwd(const float *a, const float *b, float *y, int64_t n);
+void scale_fwd(const float *x, float s, float *y, int64_t n);
+void mul_fwd(const float *a, const float *b, float *y, int64_t n);
+void add_inplace_fwd(float *y, const float *x, int64_t n);
+/* replaces qkv_split_fwd / head_merge_fwd, ncm.h:193-196, kernels.c:891-936 */
+void qkv_split_fwd(const float *in, float *qq, float *kk, float *vv,
+                   int B, int T, int C, int H, int hd, int K, int rep);
+void head_merge_fwd(const float *ctx, float *out, int B, int T, int C, int H, int hd);
+
+/* ------------------------------------------------------------------ */
 /* greedy id                                                           */
 /* ------------------------------------------------------------------ */
 

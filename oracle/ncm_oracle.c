@@ -203,3 +203,168 @@ void orc_fill_ktest(uint64_t *state, float *out, int64_t n) {
         out[i] = (float)((r >> 11) * (1.0 / 9007199254740992.0) * 4.0 - 2.0);
     }
 }
+
+/* kernels.c:150-162 rmsnorm_fwd: ms in fp64 over c ascending, s rounded to
+ * float, y = (x * s) * w in float. */
+void orc_rmsnorm(const float *x, const float *w, float *y, int64_t rows, int C) {
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; r++) {
+        const float *xr = x + r * C;
+        float *yr = y + r * C;
+        double ms = 0;
+        for (int c = 0; c < C; c++) ms += (double)xr[c] * xr[c];
+        ms /= C;
+        float s = (float)(1.0 / sqrt(ms + 1e-6));
+        for (int c = 0; c < C; c++) yr[c] = xr[c] * s * (w ? w[c] : 1.0f);
+    }
+}
+
+/* kernels.c:101-148 layernorm_fwd (eps = 1e-6, a double literal) and
+ * layernorm_eps_fwd (float eps widened to double): mean and var in fp64,
+ * y = (float)((x - mean) * inv) * w + b in float. */
+static void ln_rows(const float *x, const float *w, const float *b, float *y, int64_t rows, int C,
+                    double eps) {
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; r++) {
+        const float *xr = x + r * C;
+        float *yr = y + r * C;
+        double mean = 0;
+        for (int c = 0; c < C; c++) mean += xr[c];
+        mean /= C;
+        double var = 0;
+        for (int c = 0; c < C; c++) {
+            double d = xr[c] - mean;
+            var += d * d;
+        }
+        var /= C;
+        double inv = 1.0 / sqrt(var + eps);
+        for (int c = 0; c < C; c++) yr[c] = (float)((xr[c] - mean) * inv) * (w ? w[c] : 1.0f) + (b ? b[c] : 0.0f);
+    }
+}
+void orc_layernorm(const float *x, const float *w, const float *b, float *y, int64_t rows, int C) {
+    ln_rows(x, w, b, y, rows, C, 1e-6);
+}
+void orc_layernorm_eps(const float *x, const float *w, const float *b, float *y, int64_t rows, int C, float eps) {
+    ln_rows(x, w, b, y, rows, C, (double)eps);
+}
+
+/* kernels.c:249-264 rope_one_exact, in place over rows of hd (position = row % T):
+ * y[d] = a*c[d] + (-b)*s[d], y[d+h] = b*c[d+h] + a*s[d+h], float. */
+void orc_rope(float *x, const float *cos_t, const float *sin_t, int64_t rows, int T, int hd) {
+    int h = hd / 2;
+    for (int64_t r = 0; r < rows; r++) {
+        int t = (int)(r % T);
+        float *xr = x + r * hd;
+        const float *co = cos_t + (int64_t)t * hd;
+        const float *si = sin_t + (int64_t)t * hd;
+        for (int d = 0; d < h; d++) {
+            float a = xr[d], b = xr[d + h];
+            xr[d] = a * co[d] + (-b) * si[d];
+            xr[d + h] = b * co[d + h] + a * si[d + h];
+        }
+    }
+}
+
+/* qwen.c:85-101 RoPE tables: angle t * theta^(-2d/hd) in double with libm,
+ * cos/sin rounded to float, pair-duplicated. */
+void orc_rope_tables_qwen(int T, int hd, double theta, float *cos_t, float *sin_t) {
+    int h = hd / 2;
+    for (int t = 0; t < T; t++)
+        for (int d = 0; d < h; d++) {
+            double a = (double)t * pow(theta, -(double)(2 * d) / (double)hd);
+            float co = (float)cos(a), si = (float)sin(a);
+            cos_t[(int64_t)t * hd + d] = co;
+            cos_t[(int64_t)t * hd + d + h] = co;
+            sin_t[(int64_t)t * hd + d] = si;
+            sin_t[(int64_t)t * hd + d + h] = si;
+        }
+}
+
+/* kernels.c:423-464 sdpa_fwd_gqa, CPU branch: pass 1 finds the row max of
+ * s = (sum_d q*k in fp64) * scale + mask; pass 2 recomputes s, p = exp(s - mx)
+ * in double, accumulates (float)p * v into the float output and the fp64
+ * denominator, then scales by 1/den.  scale = 1/sqrtf(hd) in float. */
+void orc_sdpa_gqa(const float *q, const float *k, const float *v, const float *mask, float *out,
+                  int B, int Hq, int Hkv, int Tq, int Tkv, int hd) {
+    float scale = 1.0f / sqrtf((float)hd);
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int b = 0; b < B; b++)
+        for (int h = 0; h < Hq; h++) {
+            int kvh = h / (Hq / Hkv);
+            for (int tq = 0; tq < Tq; tq++) {
+                const float *qr = q + ((int64_t)b * Hq + h) * Tq * hd + (int64_t)tq * hd;
+                double mx = -1e300, den = 0;
+                for (int tk = 0; tk < Tkv; tk++) {
+                    const float *kr = k + ((int64_t)b * Hkv + kvh) * Tkv * hd + (int64_t)tk * hd;
+                    double s = 0;
+                    for (int d = 0; d < hd; d++) s += (double)qr[d] * kr[d];
+                    s *= scale;
+                    if (mask) s += mask[(int64_t)tq * Tkv + tk];
+                    if (s > mx) mx = s;
+                }
+                float *o = out + ((int64_t)b * Hq + h) * Tq * hd + (int64_t)tq * hd;
+                for (int d = 0; d < hd; d++) o[d] = 0;
+                for (int tk = 0; tk < Tkv; tk++) {
+                    const float *kr = k + ((int64_t)b * Hkv + kvh) * Tkv * hd + (int64_t)tk * hd;
+                    double s = 0;
+                    for (int d = 0; d < hd; d++) s += (double)qr[d] * kr[d];
+                    s *= scale;
+                    if (mask) s += mask[(int64_t)tq * Tkv + tk];
+                    double p = exp(s - mx);
+                    den += p;
+                    const float *vr = v + ((int64_t)b * Hkv + kvh) * Tkv * hd + (int64_t)tk * hd;
+                    for (int d = 0; d < hd; d++) o[d] += (float)p * vr[d];
+                }
+                double inv = 1.0 / den;
+                for (int d = 0; d < hd; d++) o[d] = (float)(o[d] * inv);
+            }
+        }
+}
+
+/* kernels.c:67-74 embedding_fwd */
+void orc_embedding(const float *W, const int *idx, float *y, int64_t n, int D) {
+    for (int64_t i = 0; i < n; i++) memcpy(y + i * D, W + (int64_t)idx[i] * D, (size_t)D * sizeof(float));
+}
+
+/* kernels.c:345-357 heads_transpose_fwd_b: [B][T][H*hd] -> [B][H][T][hd] */
+void orc_heads_transpose(const float *in, float *out, int B, int64_t T, int H, int hd) {
+    for (int b = 0; b < B; b++)
+        for (int64_t t = 0; t < T; t++)
+            for (int h = 0; h < H; h++)
+                for (int d = 0; d < hd; d++)
+                    out[(((int64_t)b * H + h) * T + t) * hd + d] = in[(((int64_t)b * T + t) * H + h) * hd + d];
+}
+
+/* kernels.c:913-926 qkv_split_fwd (GQA replication: kv head = h / rep) */
+void orc_qkv_split(const float *in, float *qq, float *kk, float *vv, int B, int T, int C, int H, int hd,
+                   int K, int rep) {
+    int64_t W = (int64_t)C + 2 * K * hd;
+    for (int b = 0; b < B; b++)
+        for (int h = 0; h < H; h++)
+            for (int t = 0; t < T; t++)
+                for (int d = 0; d < hd; d++) {
+                    int kvh = h / rep;
+                    int64_t o = (((int64_t)b * H + h) * T + t) * hd + d;
+                    const float *row = in + ((int64_t)b * T + t) * W;
+                    qq[o] = row[h * hd + d];
+                    kk[o] = row[C + kvh * hd + d];
+                    vv[o] = row[C + K * hd + kvh * hd + d];
+                }
+}
+
+/* kernels.c:928-936 head_merge_fwd: [B][H][T][hd] -> [B][T][C] */
+void orc_head_merge(const float *ctx, float *out, int B, int T, int C, int H, int hd) {
+    for (int b = 0; b < B; b++)
+        for (int t = 0; t < T; t++)
+            for (int h = 0; h < H; h++)
+                for (int d = 0; d < hd; d++)
+                    out[((int64_t)b * T + t) * C + h * hd + d] = ctx[(((int64_t)b * H + h) * T + t) * hd + d];
+}
+
+/* kernels.c:859-866 mul_fwd, :868-874 scale_fwd */
+void orc_mul(const float *a, const float *b, float *y, int64_t n) {
+    for (int64_t i = 0; i < n; i++) y[i] = a[i] * b[i];
+}
+void orc_scale(const float *x, float s, float *y, int64_t n) {
+    for (int64_t i = 0; i < n; i++) y[i] = x[i] * s;
+}

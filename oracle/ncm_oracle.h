@@ -39,6 +39,26 @@ void orc_gelu_tanh(const float *x, float *y, int64_t n);
 void orc_silu(const float *x, float *y, int64_t n);
 void orc_add(const float *a, const float *b, float *y, int64_t n);
 
+/* src/kernels.c:150-162 rmsnorm_fwd; :101-148 layernorm_fwd (eps 1e-6) and layernorm_eps_fwd */
+void orc_rmsnorm(const float *x, const float *w, float *y, int64_t rows, int C);
+void orc_layernorm(const float *x, const float *w, const float *b, float *y, int64_t rows, int C);
+void orc_layernorm_eps(const float *x, const float *w, const float *b, float *y, int64_t rows, int C, float eps);
+/* src/kernels.c:249-264 rope_one_exact (in place; row position = row % T) */
+void orc_rope(float *x, const float *cos_t, const float *sin_t, int64_t rows, int T, int hd);
+/* src/qwen.c:85-101 RoPE tables */
+void orc_rope_tables_qwen(int T, int hd, double theta, float *cos_t, float *sin_t);
+/* src/kernels.c:423-464 sdpa_fwd_gqa (CPU branch) */
+void orc_sdpa_gqa(const float *q, const float *k, const float *v, const float *mask, float *out,
+                  int B, int Hq, int Hkv, int Tq, int Tkv, int hd);
+/* src/kernels.c:67-74, :345-357, :913-936, :859-874 layout and elementwise */
+void orc_embedding(const float *W, const int *idx, float *y, int64_t n, int D);
+void orc_heads_transpose(const float *in, float *out, int B, int64_t T, int H, int hd);
+void orc_qkv_split(const float *in, float *qq, float *kk, float *vv, int B, int T, int C, int H, int hd,
+                   int K, int rep);
+void orc_head_merge(const float *ctx, float *out, int B, int T, int C, int H, int hd);
+void orc_mul(const float *a, const float *b, float *y, int64_t n);
+void orc_scale(const float *x, float s, float *y, int64_t n);
+
 /* src/kernels.c:774-780 rng_next (xorshift64*) and the ktest generator of
  * tests/ktest_kernels.c:8-12, for seeded inputs shared with the reference. */
 uint64_t orc_rng_next(uint64_t *state);

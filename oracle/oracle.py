@@ -51,6 +51,18 @@ def lib():
             "orc_rng_next": (ctypes.c_uint64, [ctypes.POINTER(ctypes.c_uint64)]),
             "orc_fill_ktest": (None, [ctypes.POINTER(ctypes.c_uint64), vp, i64]),
             "orc_set_threads": (None, [ci]),
+            "orc_rmsnorm": (None, [vp, vp, vp, i64, ci]),
+            "orc_layernorm": (None, [vp, vp, vp, vp, i64, ci]),
+            "orc_layernorm_eps": (None, [vp, vp, vp, vp, i64, ci, ctypes.c_float]),
+            "orc_rope": (None, [vp, vp, vp, i64, ci, ci]),
+            "orc_rope_tables_qwen": (None, [ci, ci, ctypes.c_double, vp, vp]),
+            "orc_sdpa_gqa": (None, [vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, ci]),
+            "orc_embedding": (None, [vp, vp, vp, i64, ci]),
+            "orc_heads_transpose": (None, [vp, vp, ci, i64, ci, ci]),
+            "orc_qkv_split": (None, [vp, vp, vp, vp, ci, ci, ci, ci, ci, ci, ci]),
+            "orc_head_merge": (None, [vp, vp, ci, ci, ci, ci, ci]),
+            "orc_mul": (None, [vp, vp, vp, i64]),
+            "orc_scale": (None, [vp, ctypes.c_float, vp, i64]),
         }
         for n, (r, a) in sigs.items():
             f = getattr(L, n)
@@ -126,6 +138,95 @@ def act(name, x):
     return y
 
 
+def rmsnorm(x, w):
+    x = _f32(x)
+    w = None if w is None else _f32(w)
+    y = np.empty_like(x)
+    lib().orc_rmsnorm(_ptr(x), _ptr(w), _ptr(y), x.shape[0], x.shape[1])
+    return y
+
+
+def layernorm(x, w, b, eps=None):
+    """eps None: layernorm_fwd (1e-6 double); else layernorm_eps_fwd(eps)."""
+    x = _f32(x)
+    w = None if w is None else _f32(w)
+    b = None if b is None else _f32(b)
+    y = np.empty_like(x)
+    if eps is None:
+        lib().orc_layernorm(_ptr(x), _ptr(w), _ptr(b), _ptr(y), x.shape[0], x.shape[1])
+    else:
+        lib().orc_layernorm_eps(_ptr(x), _ptr(w), _ptr(b), _ptr(y), x.shape[0], x.shape[1], eps)
+    return y
+
+
+def rope(x, cos_t, sin_t, T):
+    """x: [rows, hd] with row position = row % T; returns a rotated copy."""
+    x = _f32(x).copy()
+    lib().orc_rope(_ptr(x), _ptr(_f32(cos_t)), _ptr(_f32(sin_t)), x.shape[0], T, x.shape[1])
+    return x
+
+
+def rope_tables_qwen(T, hd, theta):
+    c = np.empty((T, hd), np.float32)
+    s_ = np.empty((T, hd), np.float32)
+    lib().orc_rope_tables_qwen(T, hd, theta, _ptr(c), _ptr(s_))
+    return c, s_
+
+
+def sdpa_gqa(q, k, v, mask=None):
+    """q [B,Hq,Tq,hd], k/v [B,Hkv,Tkv,hd], mask [Tq,Tkv] or None."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    B, Hq, Tq, hd = q.shape
+    Hkv, Tkv = k.shape[1], k.shape[2]
+    m = None if mask is None else _f32(mask)
+    out = np.empty_like(q)
+    lib().orc_sdpa_gqa(_ptr(q), _ptr(k), _ptr(v), _ptr(m), _ptr(out), B, Hq, Hkv, Tq, Tkv, hd)
+    return out
+
+
+def embedding(W, idx):
+    W = _f32(W)
+    idx = np.ascontiguousarray(idx, dtype=np.int32)
+    y = np.empty((idx.size, W.shape[1]), np.float32)
+    lib().orc_embedding(_ptr(W), _ptr(idx), _ptr(y), idx.size, W.shape[1])
+    return y
+
+
+def heads_transpose(x, B, T, H, hd):
+    x = _f32(x)
+    y = np.empty((B, H, T, hd), np.float32)
+    lib().orc_heads_transpose(_ptr(x), _ptr(y), B, T, H, hd)
+    return y
+
+
+def qkv_split(x, B, T, C, H, hd, K, rep):
+    x = _f32(x)
+    outs = [np.empty((B, H, T, hd), np.float32) for _ in range(3)]
+    lib().orc_qkv_split(_ptr(x), *[_ptr(o) for o in outs], B, T, C, H, hd, K, rep)
+    return tuple(outs)
+
+
+def head_merge(ctx, B, T, C, H, hd):
+    ctx = _f32(ctx)
+    y = np.empty((B, T, C), np.float32)
+    lib().orc_head_merge(_ptr(ctx), _ptr(y), B, T, C, H, hd)
+    return y
+
+
+def mul(a, b):
+    a, b = _f32(a), _f32(b)
+    y = np.empty_like(a)
+    lib().orc_mul(_ptr(a), _ptr(b), _ptr(y), a.size)
+    return y
+
+
+def scale(x, s_):
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib().orc_scale(_ptr(x), s_, _ptr(y), x.size)
+    return y
+
+
 def ktest_fill(state, n):
     """tests/ktest_kernels.c:8-12 generator; returns (values, new_state)."""
     st = ctypes.c_uint64(state)
@@ -155,6 +256,19 @@ def ref():
             "silu_fwd": (None, [vp, vp, i64]),
             "refg_linear_bwd": (None, [vp, vp, vp, vp, vp, vp, vp, ctypes.c_longlong, ci, ci]),
             "refg_vq_multiscale": (ci, [vp, vp, vp, ci, ci, ci, ci, vp, vp, vp]),
+            "rmsnorm_fwd": (None, [vp, vp, vp, i64, ci]),
+            "layernorm_fwd": (None, [vp, vp, vp, vp, i64, ci]),
+            "layernorm_eps_fwd": (None, [vp, vp, vp, vp, i64, ci, ctypes.c_float]),
+            "rope_apply_gqa": (None, [vp, vp, vp, vp, ci, ci, ci, ci, ci]),
+            "sdpa_fwd_gqa": (None, [vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, ci]),
+            "sdpa_fwd": (None, [vp, vp, vp, vp, vp, ci, ci, ci, ci, ci]),
+            "embedding_fwd": (None, [vp, vp, vp, i64, ci]),
+            "heads_transpose_fwd_b": (None, [vp, vp, ci, i64, ci, ci]),
+            "qkv_split_fwd": (None, [vp, vp, vp, vp, ci, ci, ci, ci, ci, ci, ci]),
+            "head_merge_fwd": (None, [vp, vp, ci, ci, ci, ci, ci]),
+            "mul_fwd": (None, [vp, vp, vp, i64]),
+            "scale_fwd": (None, [vp, ctypes.c_float, vp, i64]),
+            "add_fwd": (None, [vp, vp, vp, i64]),
         }
         for n, (r, a) in sigs.items():
             f = getattr(L, n)
@@ -190,6 +304,12 @@ def ref_l2sq(a, b):
     d2 = np.empty((a.shape[0], b.shape[0]), np.float32)
     ref().rowwise_l2sq(_ptr(a), _ptr(b), _ptr(d2), a.shape[0], b.shape[0], a.shape[1])
     return d2
+
+
+def ref_call(name, *arrays_and_ints):
+    """Calls a reference kernels.c function; numpy arrays are passed by pointer."""
+    args = [a.ctypes.data if isinstance(a, np.ndarray) else a for a in arrays_and_ints]
+    return getattr(ref(), name)(*args)
 
 
 def ref_vq_multiscale(z, Es, B, L):

@@ -71,6 +71,10 @@ struct GemmArgs {
 #define GEMM_BK 32
 #define GEMM_NT 256
 #define OOB_OFFSET 0x80000000u
+#ifndef GEMM_LDS_PAD
+#define GEMM_LDS_PAD 8   // floats of padding per LDS tile row: a 40-float pitch makes the
+                         // k-contiguous fragment reads (16 rows x 16 B per 16 lanes) hit all 64 banks
+#endif
 
 // Grouped raster: GROUP_M tile rows advance together along N so that the B
 // panels they share stay in L2.
@@ -112,7 +116,7 @@ struct SlabLoader {
 
     __device__ __forceinline__ void init(int fix0, int k0, int tid) {
         const int rr = tid / (COLS / 4), cc = (tid % (COLS / 4)) * 4;
-        lds0 = rr * (COLS + 4) + cc;
+        lds0 = rr * (COLS + GEMM_LDS_PAD) + cc;
         row0 = (KALONG_COLS ? fix0 : k0) + rr;
         col0 = (KALONG_COLS ? k0 : fix0) + cc;
     }
@@ -140,19 +144,21 @@ struct SlabLoader {
 
     __device__ __forceinline__ void store(float *buf) const {
 #pragma unroll
-        for (int j = 0; j < PER; ++j) *(f4 *)(buf + lds0 + j * RSTEP * (COLS + 4)) = r[j];
+        for (int j = 0; j < PER; ++j) *(f4 *)(buf + lds0 + j * RSTEP * (COLS + GEMM_LDS_PAD)) = r[j];
     }
 };
 
 // Epilogue of one tile from the per-thread accumulators.  tot[a][b][r] holds
 // MFMA row rho = 4*lg + r, column gamma = li.
 template <int TM, int TN, int WM, int WN, bool AKC, bool BKC, int EPI, int ACT>
-__device__ __forceinline__ void gemm_epilogue_act(const GemmArgs &p, const f4 (&tot)[TM][TN], int i0, int j0, int tid) {
+__device__ __forceinline__ void gemm_epilogue_act(const GemmArgs &p, const f4 (&tot)[TM][TN], int i0, int j0, int tid,
+                                                  int a_lo, int a_hi) {
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave / (GEMM_BN / WN), wn = wave % (GEMM_BN / WN);
     const int li = lane & 15, lg = lane >> 4;
 #pragma unroll
     for (int a = 0; a < TM; ++a) {
+        if (a < a_lo || a >= a_hi) continue;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int rho = 4 * lg + r;
@@ -194,16 +200,17 @@ __device__ __forceinline__ void gemm_epilogue_act(const GemmArgs &p, const f4 (&
 // The activation is dispatched once per tile, so every instantiation is a
 // short straight-line epilogue.
 template <int TM, int TN, int WM, int WN, bool AKC, bool BKC, int EPI>
-__device__ __forceinline__ void gemm_epilogue(const GemmArgs &p, const f4 (&tot)[TM][TN], int i0, int j0, int tid) {
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs &p, const f4 (&tot)[TM][TN], int i0, int j0, int tid,
+                                              int a_lo = 0, int a_hi = TM) {
     if (EPI == EPI_ACCUM) {
-        gemm_epilogue_act<TM, TN, WM, WN, AKC, BKC, EPI, ACT_NONE>(p, tot, i0, j0, tid);
+        gemm_epilogue_act<TM, TN, WM, WN, AKC, BKC, EPI, ACT_NONE>(p, tot, i0, j0, tid, a_lo, a_hi);
         return;
     }
     switch (p.act) {
-    case ACT_SILU: gemm_epilogue_act<TM, TN, WM, WN, AKC, BKC, EPI, ACT_SILU>(p, tot, i0, j0, tid); break;
-    case ACT_GELU: gemm_epilogue_act<TM, TN, WM, WN, AKC, BKC, EPI, ACT_GELU>(p, tot, i0, j0, tid); break;
-    case ACT_GELU_TANH: gemm_epilogue_act<TM, TN, WM, WN, AKC, BKC, EPI, ACT_GELU_TANH>(p, tot, i0, j0, tid); break;
-    default: gemm_epilogue_act<TM, TN, WM, WN, AKC, BKC, EPI, ACT_NONE>(p, tot, i0, j0, tid); break;
+    case ACT_SILU: gemm_epilogue_act<TM, TN, WM, WN, AKC, BKC, EPI, ACT_SILU>(p, tot, i0, j0, tid, a_lo, a_hi); break;
+    case ACT_GELU: gemm_epilogue_act<TM, TN, WM, WN, AKC, BKC, EPI, ACT_GELU>(p, tot, i0, j0, tid, a_lo, a_hi); break;
+    case ACT_GELU_TANH: gemm_epilogue_act<TM, TN, WM, WN, AKC, BKC, EPI, ACT_GELU_TANH>(p, tot, i0, j0, tid, a_lo, a_hi); break;
+    default: gemm_epilogue_act<TM, TN, WM, WN, AKC, BKC, EPI, ACT_NONE>(p, tot, i0, j0, tid, a_lo, a_hi); break;
     }
 }
 
@@ -214,7 +221,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &p) {
     constexpr int TM = WM / 16, TN = WN / 16;
     constexpr int A_ROWS = AKC ? BM : BK, A_COLS = AKC ? BK : BM;
     constexpr int B_ROWS = BKC ? BN : BK, B_COLS = BKC ? BK : BN;
-    constexpr int A_LD = A_COLS + 4, B_LD = B_COLS + 4;
+    constexpr int A_LD = A_COLS + GEMM_LDS_PAD, B_LD = B_COLS + GEMM_LDS_PAD;
     constexpr int A_SZ = A_ROWS * A_LD, B_SZ = B_ROWS * B_LD;
     __shared__ __attribute__((aligned(16))) float smem[2 * (A_SZ + B_SZ)];
     float *const sA = smem;               // buffers sA + {0, A_SZ}
@@ -378,12 +385,15 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &p) {
 }
 
 // Sum of the segment partials of split tile blockIdx.x in segment order,
-// then the epilogue (same thread -> element mapping as gemm_body).
+// then the epilogue (same thread -> element mapping as gemm_body).  Each
+// workgroup finishes one of the TM row blocks (blockIdx.y), so a tile's
+// partials are read by TM CUs in parallel.
 template <bool AKC, bool BKC, int EPI>
 __device__ __forceinline__ void gemm_fixup_body(const GemmArgs &p) {
     constexpr int TM = 4, TN = 4;
     const int tid = threadIdx.x;
     const int tail = blockIdx.x;
+    const int a0 = blockIdx.y;
     int tm, tn;
     tile_rc<8>(p.dp_tiles + tail, p.tiles_m, p.tiles_n, tm, tn);
     const float *first = p.ws + (int64_t)tail * p.segs * (GEMM_BM * GEMM_BN);
@@ -395,11 +405,13 @@ __device__ __forceinline__ void gemm_fixup_body(const GemmArgs &p) {
     for (int sg = 0; sg < p.segs; ++sg) {
         const f4 *src = (const f4 *)(first + (int64_t)sg * (GEMM_BM * GEMM_BN));
 #pragma unroll
-        for (int a = 0; a < TM; ++a)
+        for (int a = 0; a < TM; ++a) {
+            if (a != a0) continue;
 #pragma unroll
             for (int b = 0; b < TN; ++b) tot[a][b] += __builtin_nontemporal_load(src + (a * TN + b) * GEMM_NT + tid);
+        }
     }
-    gemm_epilogue<TM, TN, 64, 64, AKC, BKC, EPI>(p, tot, tm * GEMM_BM, tn * GEMM_BN, tid);
+    gemm_epilogue<TM, TN, 64, 64, AKC, BKC, EPI>(p, tot, tm * GEMM_BM, tn * GEMM_BN, tid, a0, a0 + 1);
 }
 
 // db[m] += (float) sum_r dy[r,m], the bias gradient of train_tape.c:708-713,

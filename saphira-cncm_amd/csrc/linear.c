@@ -75,12 +75,19 @@ static GemmPlan plan_gemm(int Mo, int No, int Kred, int slots) {
     if (slots < 1) slots = 1;
     g.dp_tiles = (T / slots) * slots;
     int R = T - g.dp_tiles;
+    /* Split the R remaining tiles into s k-segments: the tail then takes
+     * ceil(R*s/slots) rounds of ceil(groups/s) slab groups, plus about half a
+     * group per segment for the partial write-back and the fixup. */
     int segs = 1;
     if (R > 0) {
-        segs = slots / R;
-        if (segs > groups) segs = groups;
-        if (segs > MAX_SEGS) segs = MAX_SEGS;
-        if (segs < 1) segs = 1;
+        double best = 1e30;
+        for (int s = 1; s <= MAX_SEGS && s <= groups; s++) {
+            double t = (double)((R * s + slots - 1) / slots) * ((groups + s - 1) / s) + (s > 1 ? 0.5 * s : 0.0);
+            if (t < best - 1e-9) {
+                best = t;
+                segs = s;
+            }
+        }
     }
     if (segs == 1) g.dp_tiles = T; /* nothing to split: everything runs whole */
     g.segs = segs;
@@ -135,7 +142,7 @@ static int run_gemm(int kind, const float *A, const float *B, float *C, const fl
     void *args[] = {&p};
     int rc = ncm_launch(ncm_kernel(name), (unsigned)g.blocks, 1, 1, 256, args);
     if (rc || g.segs == 1) return rc;
-    return ncm_launch_named(fixup_names[kind], (unsigned)split_tiles, 1, 1, 256, args);
+    return ncm_launch_named(fixup_names[kind], (unsigned)split_tiles, 4, 1, 256, args);
 }
 
 /* GEMV kernel for a chunk of nb <= 8 batch rows; returns rows per workgroup. */

@@ -2,6 +2,7 @@
 #include "internal.h"
 
 #include <limits.h>
+#include <math.h>
 
 /* kernels.c:731-735, on a HOST row, as the reference: strict '>' from index 0. */
 int argmax_row(const float *x, int n) {
@@ -28,4 +29,167 @@ void argmax_rows(const float *x, int *idx, int64_t rows, int n) {
     if (ncm_ready()) return;
     void *args[] = {&x, &n, &idx};
     ncm_launch_named("argmax_rows_k", (unsigned)rows, 1, 1, 256, args);
+}
+
+static unsigned grid_of(int64_t n, int per_block) { return (unsigned)((n + per_block - 1) / per_block); }
+
+static int ops_ready(const char *fn, int64_t n, int nptr, const void *p0, const void *p1) {
+    if (n < 0) return ncm_fail(NCM_E_ARG, "%s: negative size", fn);
+    if (n == 0) return 1;
+    if ((nptr > 0 && !p0) || (nptr > 1 && !p1)) return ncm_fail(NCM_E_ARG, "%s: null pointer", fn);
+    if ((n + 255) / 256 > UINT_MAX) return ncm_fail(NCM_E_ARG, "%s: too large", fn);
+    return ncm_ready();
+}
+
+/* ---- norms (kernels.c:101-162) ---- */
+void rmsnorm_fwd(const float *x, const float *w, float *y, int64_t rows, int C) {
+    if (C <= 0) { ncm_fail(NCM_E_ARG, "rmsnorm_fwd: C=%d", C); return; }
+    if (ops_ready("rmsnorm_fwd", rows, 2, x, y)) return;
+    void *a[] = {&x, &w, &y, &rows, &C};
+    ncm_launch_named("rmsnorm_k", grid_of(rows, 4), 1, 1, 256, a);
+}
+
+static void layernorm_any(const char *fn, const float *x, const float *w, const float *b, float *y, int64_t rows,
+                          int C, double eps) {
+    if (C <= 0) { ncm_fail(NCM_E_ARG, "%s: C=%d", fn, C); return; }
+    if (ops_ready(fn, rows, 2, x, y)) return;
+    void *a[] = {&x, &w, &b, &y, &rows, &C, &eps};
+    ncm_launch_named("layernorm_k", grid_of(rows, 4), 1, 1, 256, a);
+}
+
+void layernorm_fwd(const float *x, const float *w, const float *b, float *y, int64_t rows, int C) {
+    layernorm_any("layernorm_fwd", x, w, b, y, rows, C, 1e-6);
+}
+
+void layernorm_eps_fwd(const float *x, const float *w, const float *b, float *y, int64_t rows, int C, float eps) {
+    layernorm_any("layernorm_eps_fwd", x, w, b, y, rows, C, (double)eps);
+}
+
+/* ---- elementwise (kernels.c:167-226, 829-874) ---- */
+static void eltwise(const char *fn, const float *a, const float *b, float *y, float s, int64_t n, int op) {
+    if (ops_ready(fn, n, 2, a, y)) return;
+    if ((op == 0 || op == 1) && !b) { ncm_fail(NCM_E_ARG, "%s: null operand", fn); return; }
+    void *args[] = {&a, &b, &y, &s, &n, &op};
+    ncm_launch_named("eltwise_k", grid_of(n, 256), 1, 1, 256, args);
+}
+void add_fwd(const float *a, const float *b, float *y, int64_t n) { eltwise("add_fwd", a, b, y, 0.f, n, 0); }
+void mul_fwd(const float *a, const float *b, float *y, int64_t n) { eltwise("mul_fwd", a, b, y, 0.f, n, 1); }
+void scale_fwd(const float *x, float s, float *y, int64_t n) { eltwise("scale_fwd", x, NULL, y, s, n, 2); }
+void add_inplace_fwd(float *y, const float *x, int64_t n) { eltwise("add_inplace_fwd", x, NULL, y, 0.f, n, 3); }
+void silu_fwd(const float *x, float *y, int64_t n) { eltwise("silu_fwd", x, NULL, y, 0.f, n, 4); }
+void gelu_fwd(const float *x, float *y, int64_t n) { eltwise("gelu_fwd", x, NULL, y, 0.f, n, 5); }
+void gelu_tanh_fwd(const float *x, float *y, int64_t n) { eltwise("gelu_tanh_fwd", x, NULL, y, 0.f, n, 6); }
+
+/* ---- RoPE (kernels.c:285-308) ---- */
+static void rope_rows(float *x, const float *cos_t, const float *sin_t, int64_t rows, int T, int hd) {
+    int64_t n = rows * (hd / 2);
+    if (!x || n == 0) return;
+    void *a[] = {&x, &cos_t, &sin_t, &rows, &T, &hd};
+    ncm_launch_named("rope_k", grid_of(n, 256), 1, 1, 256, a);
+}
+
+void rope_apply_gqa(float *q, float *k, const float *cos_t, const float *sin_t, int B, int H, int K, int T, int hd) {
+    if (B < 0 || H < 0 || K < 0 || T <= 0 || hd <= 0 || (hd & 1)) {
+        ncm_fail(NCM_E_ARG, "rope_apply_gqa: bad shape B=%d H=%d K=%d T=%d hd=%d", B, H, K, T, hd);
+        return;
+    }
+    if ((q || k) && (!cos_t || !sin_t)) { ncm_fail(NCM_E_ARG, "rope_apply_gqa: null tables"); return; }
+    if (ncm_ready()) return;
+    rope_rows(q, cos_t, sin_t, (int64_t)B * H * T, T, hd);
+    rope_rows(k, cos_t, sin_t, (int64_t)B * K * T, T, hd);
+}
+
+void rope_apply(float *q, float *k, const float *cos_t, const float *sin_t, int B, int H, int T, int hd) {
+    rope_apply_gqa(q, k, cos_t, sin_t, B, H, H, T, hd);
+}
+
+/* ---- layout (kernels.c:311-357, 891-936) and embedding (kernels.c:59-74) ---- */
+void heads_transpose_fwd_b(const float *in, float *out, int B, int64_t T, int H, int hd) {
+    int64_t n = (int64_t)B * T * H * hd;
+    if (B < 0 || T < 0 || H < 0 || hd < 0) { ncm_fail(NCM_E_ARG, "heads_transpose_fwd: bad shape"); return; }
+    if (ops_ready("heads_transpose_fwd", n, 2, in, out)) return;
+    void *a[] = {&in, &out, &B, &T, &H, &hd};
+    ncm_launch_named("heads_transpose_k", grid_of(n, 256), 1, 1, 256, a);
+}
+
+void heads_transpose_fwd(const float *in, float *out, int64_t T, int H, int hd) {
+    heads_transpose_fwd_b(in, out, 1, T, H, hd);
+}
+
+void qkv_split_fwd(const float *in, float *qq, float *kk, float *vv, int B, int T, int C, int H, int hd, int K,
+                   int rep) {
+    int64_t n = (int64_t)B * H * T * hd;
+    if (B < 0 || T < 0 || H < 0 || hd < 0 || K <= 0 || rep <= 0 || (H - 1) / rep >= K ||
+        (int64_t)H * hd > C) {
+        ncm_fail(NCM_E_ARG, "qkv_split_fwd: bad shape (H=%d K=%d rep=%d)", H, K, rep);
+        return;
+    }
+    if (ops_ready("qkv_split_fwd", n, 2, in, qq)) return;
+    if (!kk || !vv) { ncm_fail(NCM_E_ARG, "qkv_split_fwd: null pointer"); return; }
+    void *a[] = {&in, &qq, &kk, &vv, &B, &T, &C, &H, &hd, &K, &rep};
+    ncm_launch_named("qkv_split_k", grid_of(n, 256), 1, 1, 256, a);
+}
+
+void head_merge_fwd(const float *ctx, float *out, int B, int T, int C, int H, int hd) {
+    int64_t n = (int64_t)B * T * C;
+    if (B < 0 || T < 0 || C < 0 || H <= 0 || hd <= 0 || C > H * hd) {
+        ncm_fail(NCM_E_ARG, "head_merge_fwd: bad shape");
+        return;
+    }
+    if (ops_ready("head_merge_fwd", n, 2, ctx, out)) return;
+    void *a[] = {&ctx, &out, &B, &T, &C, &H, &hd};
+    ncm_launch_named("head_merge_k", grid_of(n, 256), 1, 1, 256, a);
+}
+
+void embedding_fwd_v(const float *W, int V, const int *idx, float *y, int64_t n, int D) {
+    if (D <= 0 || V <= 0) { ncm_fail(NCM_E_ARG, "embedding_fwd: D=%d V=%d", D, V); return; }
+    if (ops_ready("embedding_fwd", n * D, 2, W, y)) return;
+    if (!idx) { ncm_fail(NCM_E_ARG, "embedding_fwd: null idx"); return; }
+    void *a[] = {&W, &idx, &y, &n, &D, &V};
+    ncm_launch_named("embedding_k", grid_of(n * D, 256), 1, 1, 256, a);
+}
+
+void embedding_fwd(const float *W, const int *idx, float *y, int64_t n, int D) {
+    embedding_fwd_v(W, INT_MAX, idx, y, n, D);
+}
+
+/* ---- SDPA (kernels.c:364-507) ---- */
+static void sdpa_any(const char *fn, const float *q, const float *k, const float *v, const float *mask, float *out,
+                     int B, int Hq, int Hkv, int Tq, int Tkv, int hd, int causal) {
+    if (B < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || Tq < 0 || Tkv <= 0 || hd <= 0 || hd > 256) {
+        ncm_fail(NCM_E_ARG, "%s: bad shape B=%d Hq=%d Hkv=%d Tq=%d Tkv=%d hd=%d", fn, B, Hq, Hkv, Tq, Tkv, hd);
+        return;
+    }
+    if (causal && Tq > Tkv) {
+        ncm_fail(NCM_E_ARG, "%s: causal attention needs Tq <= Tkv (Tq=%d Tkv=%d)", fn, Tq, Tkv);
+        return;
+    }
+    if ((int64_t)B * Tq == 0) return;
+    if (!q || !k || !v || !out) { ncm_fail(NCM_E_ARG, "%s: null pointer", fn); return; }
+    if (B > 65535 || Hq > 65535) { ncm_fail(NCM_E_ARG, "%s: grid too large", fn); return; }
+    if (ncm_ready()) return;
+    float scale = 1.0f / sqrtf((float)hd);
+    if (hd == 64 && is_aligned16(q) && is_aligned16(k) && is_aligned16(v) && is_aligned16(out)) {
+        void *a[] = {&q, &k, &v, &mask, &out, &Hq, &Hkv, &Tq, &Tkv, &scale, &causal};
+        ncm_launch_named("sdpa_hd64", (unsigned)((Tq + 63) / 64), (unsigned)Hq, (unsigned)B, 256, a);
+    } else {
+        int64_t rows = (int64_t)B * Hq * Tq;
+        void *a[] = {&q, &k, &v, &mask, &out, &B, &Hq, &Hkv, &Tq, &Tkv, &hd, &scale, &causal};
+        ncm_launch_named("sdpa_rows", grid_of(rows, 4), 1, 1, 256, a);
+    }
+}
+
+void sdpa_fwd_gqa(const float *q, const float *k, const float *v, const float *mask, float *out, int B, int Hq,
+                  int Hkv, int Tq, int Tkv, int hd) {
+    sdpa_any("sdpa_fwd_gqa", q, k, v, mask, out, B, Hq, Hkv, Tq, Tkv, hd, 0);
+}
+
+void sdpa_fwd(const float *q, const float *k, const float *v, const float *mask, float *out, int B, int H, int Tq,
+              int Tkv, int hd) {
+    sdpa_any("sdpa_fwd", q, k, v, mask, out, B, H, H, Tq, Tkv, hd, 0);
+}
+
+void sdpa_fwd_gqa_causal(const float *q, const float *k, const float *v, float *out, int B, int Hq, int Hkv, int Tq,
+                         int Tkv, int hd) {
+    sdpa_any("sdpa_fwd_gqa_causal", q, k, v, NULL, out, B, Hq, Hkv, Tq, Tkv, hd, 1);
 }

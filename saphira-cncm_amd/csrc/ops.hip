@@ -33,3 +33,337 @@ argmax_rows_k(const float *__restrict__ x, int n, int *__restrict__ idx) {
         idx[blockIdx.x] = i;
     }
 }
+
+// ---------------------------------------------------------------- norms
+// RMSNorm (kernels.c:150-162): ms = sum x^2 in fp64 / C, s = (float)(1/sqrt(ms
+// + 1e-6)), y = (x*s)*w in float.  LayerNorm (kernels.c:101-148): mean and
+// var in fp64, y = (float)((x-mean)*inv)*w + b in float.  One wave per row;
+// the fp64 sums are tree-ordered (the reference sums serially), the float
+// arithmetic after the statistics follows the reference's roundings.
+extern "C" __global__ void __launch_bounds__(256)
+rmsnorm_k(const float *__restrict__ x, const float *__restrict__ w, float *__restrict__ y, int64_t rows, int C) {
+#pragma clang fp contract(off)
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float *xr = x + row * C;
+    double ms = 0.0;
+    for (int c = lane; c < C; c += 64) ms += (double)xr[c] * (double)xr[c];
+    ms = wave_sum_d(ms) / C;
+    const float s = (float)(1.0 / sqrt(ms + 1e-6));
+    float *yr = y + row * C;
+    for (int c = lane; c < C; c += 64) yr[c] = xr[c] * s * (w ? w[c] : 1.0f);
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+layernorm_k(const float *__restrict__ x, const float *__restrict__ w, const float *__restrict__ b,
+            float *__restrict__ y, int64_t rows, int C, double eps) {
+#pragma clang fp contract(off)
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float *xr = x + row * C;
+    double mean = 0.0;
+    for (int c = lane; c < C; c += 64) mean += (double)xr[c];
+    mean = wave_sum_d(mean) / C;
+    double var = 0.0;
+    for (int c = lane; c < C; c += 64) {
+        double d = (double)xr[c] - mean;
+        var += d * d;
+    }
+    var = wave_sum_d(var) / C;
+    const double inv = 1.0 / sqrt(var + eps);
+    float *yr = y + row * C;
+    for (int c = lane; c < C; c += 64)
+        yr[c] = (float)(((double)xr[c] - mean) * inv) * (w ? w[c] : 1.0f) + (b ? b[c] : 0.0f);
+}
+
+// ---------------------------------------------------------------- RoPE
+// Rotate-half RoPE in place (kernels.c:249-264): rows of hd, position
+// row % T, y[d] = a*c[d] + (-b)*s[d], y[d+h] = b*c[d+h] + a*s[d+h] with the
+// reference's separate roundings.  One thread per (row, d < hd/2).
+extern "C" __global__ void __launch_bounds__(256)
+rope_k(float *x, const float *__restrict__ cos_t, const float *__restrict__ sin_t, int64_t rows, int T, int hd) {
+#pragma clang fp contract(off)
+    const int h = hd >> 1;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * h) return;
+    const int64_t row = i / h;
+    const int d = (int)(i % h);
+    const int t = (int)(row % T);
+    float *xr = x + row * hd;
+    const float *co = cos_t + (int64_t)t * hd, *si = sin_t + (int64_t)t * hd;
+    const float a = xr[d], bb = xr[d + h];
+    xr[d] = a * co[d] + (-bb) * si[d];
+    xr[d + h] = bb * co[d + h] + a * si[d + h];
+}
+
+// ---------------------------------------------------------------- layout
+// heads_transpose_fwd_b (kernels.c:345-357): [B][T][H*hd] -> [B][H][T][hd]
+extern "C" __global__ void __launch_bounds__(256)
+heads_transpose_k(const float *__restrict__ in, float *__restrict__ out, int B, int64_t T, int H, int hd) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t n = (int64_t)B * T * H * hd;
+    if (i >= n) return;
+    const int d = (int)(i % hd);
+    const int64_t t = (i / hd) % T;
+    const int64_t bh = i / ((int64_t)hd * T);
+    const int h = (int)(bh % H), b = (int)(bh / H);
+    out[i] = in[(((int64_t)b * T + t) * H + h) * hd + d];
+}
+
+// qkv_split_fwd (kernels.c:891-926): fused qkv rows -> q, k, v heads (GQA
+// replication kv head = h / rep)
+extern "C" __global__ void __launch_bounds__(256)
+qkv_split_k(const float *__restrict__ in, float *__restrict__ qq, float *__restrict__ kk, float *__restrict__ vv,
+            int B, int T, int C, int H, int hd, int K, int rep) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)B * H * T * hd) return;
+    const int d = (int)(i % hd);
+    const int t = (int)((i / hd) % T);
+    const int h = (int)((i / ((int64_t)hd * T)) % H);
+    const int b = (int)(i / ((int64_t)H * T * hd));
+    const int kvh = h / rep;
+    const float *row = in + ((int64_t)b * T + t) * ((int64_t)C + 2 * K * hd);
+    qq[i] = row[h * hd + d];
+    kk[i] = row[C + kvh * hd + d];
+    vv[i] = row[C + K * hd + kvh * hd + d];
+}
+
+// head_merge_fwd (kernels.c:903-936): [B][H][T][hd] -> [B][T][C]
+extern "C" __global__ void __launch_bounds__(256)
+head_merge_k(const float *__restrict__ ctx, float *__restrict__ out, int B, int T, int C, int H, int hd) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)B * T * C) return;
+    const int c = (int)(i % C);
+    const int hh = c / hd, dd = c % hd;
+    const int t = (int)((i / C) % T);
+    const int b = (int)(i / ((int64_t)T * C));
+    out[i] = ctx[(((int64_t)b * H + hh) * T + t) * hd + dd];
+}
+
+// embedding_fwd (kernels.c:59-74): y[i,:] = W[idx[i],:]; ids outside [0, V)
+// read row 0 (the reference would read out of bounds).
+extern "C" __global__ void __launch_bounds__(256)
+embedding_k(const float *__restrict__ W, const int *__restrict__ idx, float *__restrict__ y, int64_t n, int D, int V) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n * D) return;
+    int id = idx[i / D];
+    if ((unsigned)id >= (unsigned)V) id = 0;
+    y[i] = W[(int64_t)id * D + (i % D)];
+}
+
+// ---------------------------------------------------------------- elementwise
+// op: 0 add (a+b), 1 mul (a*b), 2 scale (a*s), 3 add_inplace (y += a),
+//     4 silu, 5 gelu, 6 gelu_tanh   (kernels.c:167-226, 829-874)
+extern "C" __global__ void __launch_bounds__(256)
+eltwise_k(const float *a, const float *b, float *y, float s, int64_t n, int op) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float v = a[i];
+    switch (op) {
+    case 0: y[i] = v + b[i]; break;
+    case 1: y[i] = v * b[i]; break;
+    case 2: y[i] = v * s; break;
+    case 3: y[i] = y[i] + v; break;
+    case 4: y[i] = ncm_act(v, ACT_SILU); break;
+    case 5: y[i] = ncm_act(v, ACT_GELU); break;
+    default: y[i] = ncm_act(v, ACT_GELU_TANH); break;
+    }
+}
+
+// ---------------------------------------------------------------- SDPA
+// softmax(Q K^T * scale + mask) V with GQA (kernels.c:364-507), q [B][Hq][Tq][hd],
+// k/v [B][Hkv][Tkv][hd], out like q, kv head = h / (Hq/Hkv), mask [Tq][Tkv]
+// additive (or null).  causal: query tq sees keys <= tq + (Tkv - Tq) (the
+// bottom-right alignment a KV cache needs; the usual mask when Tq == Tkv).
+//
+// sdpa_hd64: flash-style, FP32 MFMA.  A workgroup owns 64 queries of one
+// (b, h); each wave 16.  Per 64-key tile staged in LDS:
+//   S^T = K Q^T   (so the accumulator of lane (li, g) holds the scores of
+//                  query li for keys 16c + 4g + r -- exactly the A operand
+//                  of the next product under the k-permutation below);
+//   online softmax per query (running max m, sum l, rescale of O);
+//   O += P V.
+// k-permutation as in the GEMM: MFMA step s gives lane group g the reduction
+// index 4g + s (d for S^T, key for P V).  Q stays in registers.
+#define SD_T 64
+#define SD_LD (64 + 8)
+
+extern "C" __global__ void __launch_bounds__(256)
+sdpa_hd64(const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+          const float *__restrict__ mask, float *__restrict__ out, int Hq, int Hkv, int Tq, int Tkv,
+          float scale, int causal) {
+    __shared__ __attribute__((aligned(16))) float sK[SD_T * SD_LD];
+    __shared__ __attribute__((aligned(16))) float sV[SD_T * SD_LD];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4;
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int kvh = h / (Hq / Hkv);
+    const int q0 = blockIdx.x * 64, qw = q0 + wave * 16;
+    const float *qb = q + ((int64_t)b * Hq + h) * Tq * 64;
+    const float *kb = k + ((int64_t)b * Hkv + kvh) * Tkv * 64;
+    const float *vb = v + ((int64_t)b * Hkv + kvh) * Tkv * 64;
+
+    // Q^T fragments: query qw + li, d = 16kc + 4g .. +3
+    f4 qf[4];
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+        const int qi = qw + li;
+        qf[kc] = qi < Tq ? *(const f4 *)(qb + (int64_t)qi * 64 + kc * 16 + 4 * lg) : f4{0.f, 0.f, 0.f, 0.f};
+    }
+    const int my_q = qw + li;                 // query of this lane in the S^T layout
+    float m_run = -INFINITY, l_run = 0.f;     // per query my_q (replicated over lg)
+    f4 o[4];                                  // o[u][r]: query qw + 4lg + r, d = 4li + u
+#pragma unroll
+    for (int u = 0; u < 4; ++u) o[u] = f4{0.f, 0.f, 0.f, 0.f};
+
+    const int coff = Tkv - Tq;   // causal offset of the query positions
+    int kend = Tkv;
+    if (causal) kend = min(Tkv, q0 + 64 + coff);
+    for (int k0 = 0; k0 < kend; k0 += SD_T) {
+        __syncthreads();
+        // stage K and V tiles (64 keys x 64 d), rows beyond Tkv as zero
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int f = tid + j * 256;
+            const int r = f >> 4, c = (f & 15) * 4;
+            const int key = k0 + r;
+            f4 kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
+            if (key < Tkv) {
+                kv = *(const f4 *)(kb + (int64_t)key * 64 + c);
+                vv = *(const f4 *)(vb + (int64_t)key * 64 + c);
+            }
+            *(f4 *)(sK + r * SD_LD + c) = kv;
+            *(f4 *)(sV + r * SD_LD + c) = vv;
+        }
+        __syncthreads();
+
+        // S^T[c]: keys k0 + 16c + 4lg + r, query my_q
+        f4 s[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            s[c] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kc = 0; kc < 4; ++kc) {
+                const f4 kf = *(const f4 *)(sK + (16 * c + li) * SD_LD + kc * 16 + 4 * lg);
+#pragma unroll
+                for (int st = 0; st < 4; ++st) s[c] = mfma4(kf[st], qf[kc][st], s[c]);
+            }
+        }
+        // scale, mask, tile max
+        float mt = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int key = k0 + 16 * c + 4 * lg + r;
+                float x = s[c][r] * scale;
+                if (mask && key < Tkv && my_q < Tq) x += mask[(int64_t)my_q * Tkv + key];
+                if (key >= Tkv || (causal && key > my_q + coff)) x = -INFINITY;
+                s[c][r] = x;
+                mt = fmaxf(mt, x);
+            }
+        mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        const float m_new = fmaxf(m_run, mt);
+        const bool none = m_new == -INFINITY;     // every key so far masked
+        const float alpha = none ? 1.f : __expf(m_run - m_new);
+        float ps = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float p = none ? 0.f : __expf(s[c][r] - m_new);
+                s[c][r] = p;
+                ps += p;
+            }
+        ps += __shfl_xor(ps, 16, 64);
+        ps += __shfl_xor(ps, 32, 64);
+        l_run = l_run * alpha + ps;
+        m_run = m_new;
+        // rescale O rows (query qw + 4lg + r) by the alpha held in lane li = 4lg + r
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float ar = __shfl(alpha, 4 * lg + r, 64);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) o[u][r] *= ar;
+        }
+        // O += P V: chunk c, step st -> key 16c + 4lg + st; V float4 along d = 4li..
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const f4 vf = *(const f4 *)(sV + (16 * c + 4 * lg + st) * SD_LD + 4 * li);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) o[u] = mfma4(s[c][st], vf[u], o[u]);
+            }
+    }
+
+    // normalise by l of query qw + 4lg + r and store float4 along d
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float lr = __shfl(l_run, 4 * lg + r, 64);
+        const int qi = qw + 4 * lg + r;
+        if (qi < Tq) {
+            const float inv = 1.0f / lr;
+            f4 val = {o[0][r] * inv, o[1][r] * inv, o[2][r] * inv, o[3][r] * inv};
+            *(f4 *)(out + (((int64_t)b * Hq + h) * Tq + qi) * 64 + 4 * li) = val;
+        }
+    }
+}
+
+// Generic SDPA for any hd <= 256: one wave per query row, online softmax in
+// fp32, the lane dimension over hd.
+extern "C" __global__ void __launch_bounds__(256)
+sdpa_rows(const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+          const float *__restrict__ mask, float *__restrict__ out, int B, int Hq, int Hkv, int Tq, int Tkv,
+          int hd, float scale, int causal) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= (int64_t)B * Hq * Tq) return;
+    const int tq = (int)(row % Tq);
+    const int h = (int)((row / Tq) % Hq), b = (int)(row / ((int64_t)Tq * Hq));
+    const int kvh = h / (Hq / Hkv);
+    const float *qr = q + row * hd;
+    const float *kb = k + ((int64_t)b * Hkv + kvh) * Tkv * hd;
+    const float *vb = v + ((int64_t)b * Hkv + kvh) * Tkv * hd;
+    float qv[4], acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int d = lane + 64 * j;
+        qv[j] = d < hd ? qr[d] : 0.f;
+        acc[j] = 0.f;
+    }
+    float m = -INFINITY, l = 0.f;
+    const int kend = causal ? min(Tkv, tq + 1 + (Tkv - Tq)) : Tkv;
+    for (int tk = 0; tk < kend; ++tk) {
+        const float *kr = kb + (int64_t)tk * hd;
+        float dot = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int d = lane + 64 * j;
+            if (d < hd) dot += qv[j] * kr[d];
+        }
+        float x = wave_sum(dot) * scale;
+        if (mask) x += mask[(int64_t)tq * Tkv + tk];
+        const float m_new = fmaxf(m, x);
+        if (m_new == -INFINITY) continue;
+        const float alpha = __expf(m - m_new), p = __expf(x - m_new);
+        l = l * alpha + p;
+        const float *vr = vb + (int64_t)tk * hd;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int d = lane + 64 * j;
+            acc[j] = acc[j] * alpha + (d < hd ? p * vr[d] : 0.f);
+        }
+        m = m_new;
+    }
+    float *o = out + row * hd;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int d = lane + 64 * j;
+        if (d < hd) o[d] = acc[j] / l;
+    }
+}

@@ -57,6 +57,27 @@ _SIGS = {
     "vq_argmin": (None, [vp, vp, vp, i64, ci, ci]),
     "vq_quantize_multiscale": (None, [vp, ctypes.POINTER(vp), ctypes.POINTER(ci), ci, ci, ci, ci,
                                       vp, vp, vp]),
+    "rmsnorm_fwd": (None, [vp, vp, vp, i64, ci]),
+    "layernorm_fwd": (None, [vp, vp, vp, vp, i64, ci]),
+    "layernorm_eps_fwd": (None, [vp, vp, vp, vp, i64, ci, ctypes.c_float]),
+    "gelu_fwd": (None, [vp, vp, i64]),
+    "gelu_tanh_fwd": (None, [vp, vp, i64]),
+    "silu_fwd": (None, [vp, vp, i64]),
+    "rope_apply": (None, [vp, vp, vp, vp, ci, ci, ci, ci]),
+    "rope_apply_gqa": (None, [vp, vp, vp, vp, ci, ci, ci, ci, ci]),
+    "heads_transpose_fwd": (None, [vp, vp, i64, ci, ci]),
+    "heads_transpose_fwd_b": (None, [vp, vp, ci, i64, ci, ci]),
+    "sdpa_fwd": (None, [vp, vp, vp, vp, vp, ci, ci, ci, ci, ci]),
+    "sdpa_fwd_gqa": (None, [vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, ci]),
+    "sdpa_fwd_gqa_causal": (None, [vp, vp, vp, vp, ci, ci, ci, ci, ci, ci]),
+    "embedding_fwd": (None, [vp, vp, vp, i64, ci]),
+    "embedding_fwd_v": (None, [vp, ci, vp, vp, i64, ci]),
+    "add_fwd": (None, [vp, vp, vp, i64]),
+    "scale_fwd": (None, [vp, ctypes.c_float, vp, i64]),
+    "mul_fwd": (None, [vp, vp, vp, i64]),
+    "add_inplace_fwd": (None, [vp, vp, i64]),
+    "qkv_split_fwd": (None, [vp, vp, vp, vp, ci, ci, ci, ci, ci, ci, ci]),
+    "head_merge_fwd": (None, [vp, vp, ci, ci, ci, ci, ci]),
     "argmax_row": (ci, [vp, ci]),
     "argmax_rows": (None, [vp, vp, i64, ci]),
 }
@@ -212,6 +233,13 @@ def vq_quantize_multiscale(z, Es, vocabs, B, L, D, idx, z_hat, z_rest):
     vocs = (ci * n)(*vocabs)
     load().vq_quantize_multiscale(_p(z), eptrs, vocs, n, B, L, D, _p(idx), _p(z_hat), _p(z_rest))
     check()
+
+
+def call(name, *args):
+    """Calls any header function; DeviceBuffers are passed as device pointers."""
+    r = getattr(load(), name)(*[_p(a) if (a is None or isinstance(a, DeviceBuffer)) else a for a in args])
+    check()
+    return r
 
 
 def argmax_rows(x, idx, rows, n):

@@ -203,6 +203,50 @@ void qkv_split_fwd(const float *in, float *qq, float *kk, float *vv,
 void head_merge_fwd(const float *ctx, float *out, int B, int T, int C, int H, int hd);
 
 /* ------------------------------------------------------------------ */
+/* training step: backward rows and optimizer                          */
+/* Gradients accumulate (+=) into the caller's buffers; NULL skips one. */
+/* ------------------------------------------------------------------ */
+
+/* replaces the TOP_LN / TOP_LNE backward, train_tape.c:569-634 (host) and
+ * k_ln_stats / k_ln_param / k_ln_dx, train_tape.c:1560-1620 (device);
+ * eps = 1e-6 for layernorm_fwd, the recorded eps for layernorm_eps_fwd. */
+void layernorm_bwd(const float *x, const float *w, const float *dy, float *dx, float *dw, float *db,
+                   int64_t rows, int C, double eps);
+/* replaces the TOP_RMSN backward, train_tape.c:748-792 / k_rmsn_*, :1575-1645 */
+void rmsnorm_bwd(const float *x, const float *w, const float *dy, float *dx, float *dw, int64_t rows, int C);
+/* replaces t_ce's forward, train_tape.c:442-481: probs [rows][V] and the mean
+ * NLL over rows with wmask != 0 (wmask may be NULL) into loss[0]; tgt, wmask
+ * and loss are device pointers. */
+void ce_fwd(const float *logits, const int *tgt, const float *wmask, float *loss, float *probs,
+            int64_t rows, int V);
+/* replaces the TOP_CE backward, train_tape.c:657-679 / k_ce_bwd :1801-1810:
+ * dlogits += (p - onehot) * w * inv, inv = weight / count */
+void ce_bwd(const float *probs, const int *tgt, const float *wmask, float *dlogits, int64_t rows, int V,
+            double inv);
+/* extension: ce_fwd + ce_bwd without storing probs (count computed on the
+ * device); loss[0] as ce_fwd, dlogits accumulates. */
+void ce_fwd_bwd(const float *logits, const int *tgt, const float *wmask, float *loss, float *dlogits,
+                int64_t rows, int V, double weight);
+/* replaces t_sdpa's host computation of the stored probabilities,
+ * train_tape.c:289-313: P [B][H][Tq][Tkv] = softmax(Q K^T / sqrt(hd) + mask). */
+void sdpa_probs_gqa(const float *q, const float *k, const float *mask, float *P,
+                    int B, int H, int Hkv, int Tq, int Tkv, int hd);
+/* replaces the TOP_SDPA backward (MHA and GQA), train_tape.c:936-1051 (host)
+ * and k_sdpa_* :1691-1799 (device), from the stored P; dO like q. */
+void sdpa_bwd_gqa(const float *q, const float *k, const float *v, const float *P, const float *dO,
+                  float *dq, float *dk, float *dv, int B, int H, int Hkv, int Tq, int Tkv, int hd);
+/* replaces k_adamw, train.c:51-64 (= the host loop :131-141): one tensor,
+ * lr already scaled by the schedule and the tensor's multiplier. */
+void adamw_update(float *p, const float *g, float *m, float *v, int64_t n, double lr, double b1, double b2,
+                  double b1t, double b2t, double eps, double wd);
+/* the schedule of train.c:172-178 (static there): linear warm-up, cosine decay */
+double sched_cosine_warmup(long step, double warmup, double total);
+/* replaces the global-norm clip of train_gpt2.c:160-173: returns the norm of
+ * all `count` device gradients (fp64) and scales them by (float)(1/norm) when
+ * it exceeds max_norm; -1 on error.  Synchronises the library stream. */
+double grad_clip_global(float *const *grads, const int64_t *sizes, int count, double max_norm);
+
+/* ------------------------------------------------------------------ */
 /* greedy id                                                           */
 /* ------------------------------------------------------------------ */
 

@@ -368,3 +368,276 @@ void orc_mul(const float *a, const float *b, float *y, int64_t n) {
 void orc_scale(const float *x, float s, float *y, int64_t n) {
     for (int64_t i = 0; i < n; i++) y[i] = x[i] * s;
 }
+
+/* ------------------------------------------------------------------ */
+/* training backward and optimizer                                     */
+/* ------------------------------------------------------------------ */
+
+/* train_tape.c:569-634 host_ln_bwd: fp64 row statistics; dw/db are the
+ * fp64 rr-ascending column sums rounded to float and then float-added into
+ * the existing gradients; dx += (float)(...) per element. */
+void orc_layernorm_bwd(const float *x, const float *w, const float *dy, float *dx, float *dw, float *db,
+                       int64_t rows, int C, double eps) {
+    double *pmean = (double *)malloc((size_t)(rows > 0 ? rows : 1) * sizeof(double));
+    double *pinv = (double *)malloc((size_t)(rows > 0 ? rows : 1) * sizeof(double));
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; r++) {
+        const float *xr = x + r * C;
+        double mean = 0;
+        for (int c = 0; c < C; c++) mean += xr[c];
+        mean /= C;
+        double var = 0;
+        for (int c = 0; c < C; c++) {
+            double d = xr[c] - mean;
+            var += d * d;
+        }
+        var /= C;
+        pmean[r] = mean;
+        pinv[r] = 1.0 / sqrt(var + eps);
+    }
+    if (dw || db) {
+#pragma omp parallel for schedule(static)
+        for (int c = 0; c < C; c++) {
+            double sw = 0, sb = 0;
+            for (int64_t r = 0; r < rows; r++) {
+                double yh = (x[r * C + c] - pmean[r]) * pinv[r];
+                sw += dy[r * C + c] * yh;
+                sb += dy[r * C + c];
+            }
+            if (dw) dw[c] += (float)sw;
+            if (db) db[c] += (float)sb;
+        }
+    }
+    if (dx) {
+#pragma omp parallel for schedule(static)
+        for (int64_t r = 0; r < rows; r++) {
+            const float *xr = x + r * C, *gr = dy + r * C;
+            double mean = pmean[r], inv = pinv[r];
+            double dmean = 0, dvar = 0;
+            for (int c = 0; c < C; c++) {
+                double wc = w ? w[c] : 1.0;
+                double d = gr[c] * wc;
+                dmean += d;
+                dvar += d * (xr[c] - mean);
+            }
+            dmean /= C;
+            dvar *= -0.5 * inv * inv * inv / C;
+            for (int c = 0; c < C; c++) {
+                double wc = w ? w[c] : 1.0;
+                double d = gr[c] * wc;
+                dx[r * C + c] += (float)((d - dmean) * inv + 2 * (xr[c] - mean) * dvar);
+            }
+        }
+    }
+    free(pmean);
+    free(pinv);
+}
+
+/* train_tape.c:748-792 TOP_RMSN: dw is a FLOAT rr-ascending sum of
+ * (float)((dy*x as a float product) * inv); dx in fp64. */
+void orc_rmsnorm_bwd(const float *x, const float *w, const float *dy, float *dx, float *dw, int64_t rows, int C) {
+    double *pinv = (double *)malloc((size_t)(rows > 0 ? rows : 1) * sizeof(double));
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; r++) {
+        double ms = 0;
+        for (int c = 0; c < C; c++) ms += (double)x[r * C + c] * x[r * C + c];
+        ms /= C;
+        pinv[r] = 1.0 / sqrt(ms + 1e-6);
+    }
+    if (dw) {
+#pragma omp parallel for schedule(static)
+        for (int c = 0; c < C; c++) {
+            float sw = 0;
+            for (int64_t r = 0; r < rows; r++) {
+                float g = dy[r * C + c] * x[r * C + c];
+                sw += (float)(g * pinv[r]);
+            }
+            dw[c] += sw;
+        }
+    }
+    if (dx) {
+#pragma omp parallel for schedule(static)
+        for (int64_t r = 0; r < rows; r++) {
+            const float *xr = x + r * C, *gr = dy + r * C;
+            double inv = pinv[r], dot = 0;
+            for (int c = 0; c < C; c++) {
+                double wc = w ? w[c] : 1.0;
+                dot += gr[c] * wc * xr[c];
+            }
+            dot /= C;
+            for (int c = 0; c < C; c++) {
+                double wc = w ? w[c] : 1.0;
+                dx[r * C + c] += (float)((gr[c] * wc - dot * xr[c] * inv * inv) * inv);
+            }
+        }
+    }
+    free(pinv);
+}
+
+/* train_tape.c:442-481 t_ce: per row float max (strict '>'), fp64
+ * exp/denominator, probs = (float)e / (float)den; loss = (float)(sum_r
+ * w_r * -log(p[tgt] + 1e-30) / sum_r w_r) over rows with w_r != 0.
+ * Returns the count sum_r w_r. */
+double orc_ce_fwd(const float *logits, const int *tgt, const float *wm, float *loss, float *probs, int64_t rows,
+                  int V) {
+    double nll = 0, cnt = 0;
+    for (int64_t r = 0; r < rows; r++) {
+        const float *l = logits + r * V;
+        float *p = probs + r * V;
+        float m = l[0];
+        for (int v = 1; v < V; v++)
+            if (l[v] > m) m = l[v];
+        double den = 0;
+        for (int v = 0; v < V; v++) {
+            double e = exp((double)l[v] - m);
+            p[v] = (float)e;
+            den += e;
+        }
+        for (int v = 0; v < V; v++) p[v] /= (float)den;
+        float w = wm ? wm[r] : 1.0f;
+        if (w != 0) {
+            nll += w * -log(p[tgt[r]] + 1e-30);
+            cnt += w;
+        }
+    }
+    *loss = cnt > 0 ? (float)(nll / cnt) : 0.0f;
+    return cnt;
+}
+
+/* train_tape.c:657-679 TOP_CE backward: dl += (float)((p - onehot) * w * inv),
+ * inv = weight / cnt; rows with w == 0 untouched. */
+void orc_ce_bwd(const float *probs, const int *tgt, const float *wm, float *dl, int64_t rows, int V, double inv) {
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; r++) {
+        float w = wm ? wm[r] : 1.0f;
+        if (w == 0) continue;
+        for (int v = 0; v < V; v++)
+            dl[r * V + v] += (float)((probs[r * V + v] - (v == tgt[r] ? 1.0 : 0.0)) * w * inv);
+    }
+}
+
+/* train.c:131-141 (host loop) = train.c:51-64 (k_adamw): decoupled decay,
+ * moments in fp64 rounded to float, bias-corrected step in fp64. */
+void orc_adamw(float *p, const float *g, float *m, float *v, int64_t n, double lr, double b1, double b2,
+               double b1t, double b2t, double eps, double wd) {
+    for (int64_t k = 0; k < n; k++) {
+        float gk = g[k];
+        p[k] -= (float)(lr * wd * p[k]);
+        m[k] = (float)(b1 * m[k] + (1 - b1) * gk);
+        v[k] = (float)(b2 * v[k] + (1 - b2) * gk * gk);
+        double mh = m[k] / b1t, vh = v[k] / b2t;
+        p[k] -= (float)(lr * mh / (sqrt(vh) + eps));
+    }
+}
+
+/* train.c:172-178 */
+double orc_sched_cosine_warmup(long step, double warmup, double total) {
+    double w = warmup, T = total;
+    if (step < w) return step / (w > 0 ? w : 1);
+    if (step >= T) return 0.0;
+    double x = (step - w) / (T - w);
+    return 0.5 * (1 + cos(3.141592653589793 * x));
+}
+
+/* train_gpt2.c:160-173: global L2 norm over every gradient (fp64, serial),
+ * scale by (float)(1/gnorm) when the norm exceeds max_norm (1.0 there). */
+double orc_grad_clip(float *const *g, const int64_t *n, int count, double max_norm) {
+    double g2 = 0;
+    for (int i = 0; i < count; i++)
+        for (int64_t k = 0; k < n[i]; k++) g2 += (double)g[i][k] * g[i][k];
+    double gnorm = sqrt(g2);
+    if (gnorm > max_norm) {
+        float s = (float)(1.0 / gnorm);
+        for (int i = 0; i < count; i++)
+            for (int64_t k = 0; k < n[i]; k++) g[i][k] *= s;
+    }
+    return gnorm;
+}
+
+/* train_tape.c:289-313 (t_sdpa): the probabilities the tape stores for the
+ * backward.  Scores in fp64 rounded to float, max over the fp64 scores,
+ * (float)exp(float score - max), float division by (float)den. */
+void orc_sdpa_probs(const float *q, const float *k, const float *mask, float *P, int B, int H, int Hkv, int Tq,
+                    int Tkv, int hd) {
+    float scale = 1.0f / sqrtf((float)hd);
+    int rep = H / Hkv;
+    int64_t rows = (int64_t)B * H * Tq;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; r++) {
+        int bh = (int)(r / Tq), tq = (int)(r % Tq);
+        int h = bh % H, b = bh / H, kvh = h / rep;
+        const float *qr = q + r * hd;
+        float *pr = P + r * Tkv;
+        double mx = -1e300;
+        for (int tk = 0; tk < Tkv; tk++) {
+            const float *kr = k + (((int64_t)b * Hkv + kvh) * Tkv + tk) * hd;
+            double s = 0;
+            for (int d = 0; d < hd; d++) s += (double)qr[d] * kr[d];
+            s *= scale;
+            if (mask) s += mask[(int64_t)tq * Tkv + tk];
+            pr[tk] = (float)s;
+            if (s > mx) mx = s;
+        }
+        double den = 0;
+        for (int tk = 0; tk < Tkv; tk++) {
+            pr[tk] = (float)exp(pr[tk] - mx);
+            den += pr[tk];
+        }
+        for (int tk = 0; tk < Tkv; tk++) pr[tk] /= (float)den;
+    }
+}
+
+/* train_tape.c:936-1051 TOP_SDPA backward (the GQA path; with Hkv == H it
+ * is the MHA path): ds = P (dP - sum_tk P dP) in fp64 with dP = dO . v;
+ * dq += (float)(ds*scale*k) tk-ascending; dk, dv are float sums over the
+ * h-group then tq (ascending) of (float)(ds*scale*q) and (float)(P*dO),
+ * float-added into the existing gradients.  Any of dq/dk/dv may be NULL. */
+void orc_sdpa_bwd(const float *q, const float *k, const float *v, const float *P, const float *dy, float *dq,
+                  float *dk, float *dv, int B, int H, int Hkv, int Tq, int Tkv, int hd) {
+    float scale = 1.0f / sqrtf((float)hd);
+    int rep = H / Hkv;
+    int64_t rows = (int64_t)B * H * Tq;
+    double *ds = (double *)malloc((size_t)(rows > 0 ? rows : 1) * (size_t)(Tkv > 0 ? Tkv : 1) * sizeof(double));
+#pragma omp parallel for schedule(static)
+    for (int64_t rr = 0; rr < rows; rr++) {
+        int b = (int)(rr / ((int64_t)H * Tq)), h = (int)((rr / Tq) % H), tq = (int)(rr % Tq);
+        int kvh = h / rep;
+        double tot = 0;
+        for (int tk = 0; tk < Tkv; tk++) {
+            const float *vr = v + ((int64_t)b * Hkv + kvh) * Tkv * hd + (int64_t)tk * hd;
+            double s = 0;
+            for (int d = 0; d < hd; d++) s += (double)dy[rr * hd + d] * vr[d];
+            s *= P[rr * Tkv + tk];
+            ds[rr * Tkv + tk] = s;
+            tot += s;
+        }
+        for (int tk = 0; tk < Tkv; tk++) ds[rr * Tkv + tk] -= P[rr * Tkv + tk] * tot;
+        if (dq)
+            for (int tk = 0; tk < Tkv; tk++) {
+                const float *kr = k + ((int64_t)b * Hkv + kvh) * Tkv * hd + (int64_t)tk * hd;
+                for (int d = 0; d < hd; d++)
+                    dq[((int64_t)b * H + h) * Tq * hd + (int64_t)tq * hd + d] +=
+                        (float)(ds[rr * Tkv + tk] * scale * kr[d]);
+            }
+    }
+    if (dk || dv) {
+#pragma omp parallel for collapse(3) schedule(static)
+        for (int b = 0; b < B; b++)
+            for (int kvh = 0; kvh < Hkv; kvh++)
+                for (int tk = 0; tk < Tkv; tk++)
+                    for (int d = 0; d < hd; d++) {
+                        float sk = 0, sv = 0;
+                        for (int h = kvh * rep; h < (kvh + 1) * rep && h < H; h++)
+                            for (int tq = 0; tq < Tq; tq++) {
+                                int64_t rr = ((int64_t)b * H + h) * Tq + tq;
+                                const float *qr = q + ((int64_t)b * H + h) * Tq * hd + (int64_t)tq * hd;
+                                sk += (float)(ds[rr * Tkv + tk] * scale * qr[d]);
+                                sv += (float)(P[rr * Tkv + tk] * dy[rr * hd + d]);
+                            }
+                        int64_t o = ((int64_t)b * Hkv + kvh) * Tkv * hd + (int64_t)tk * hd + d;
+                        if (dk) dk[o] += sk;
+                        if (dv) dv[o] += sv;
+                    }
+    }
+    free(ds);
+}

@@ -59,6 +59,28 @@ void orc_head_merge(const float *ctx, float *out, int B, int T, int C, int H, in
 void orc_mul(const float *a, const float *b, float *y, int64_t n);
 void orc_scale(const float *x, float s, float *y, int64_t n);
 
+/* training backward and optimizer (accumulating into existing gradients;
+ * NULL gradient pointers are skipped) */
+/* src/train_tape.c:569-634 host_ln_bwd (eps 1e-6 for TOP_LN, recorded eps for TOP_LNE) */
+void orc_layernorm_bwd(const float *x, const float *w, const float *dy, float *dx, float *dw, float *db,
+                       int64_t rows, int C, double eps);
+/* src/train_tape.c:748-792 TOP_RMSN */
+void orc_rmsnorm_bwd(const float *x, const float *w, const float *dy, float *dx, float *dw, int64_t rows, int C);
+/* src/train_tape.c:442-481 t_ce (returns the weight count) and :657-679 its backward */
+double orc_ce_fwd(const float *logits, const int *tgt, const float *wm, float *loss, float *probs, int64_t rows,
+                  int V);
+void orc_ce_bwd(const float *probs, const int *tgt, const float *wm, float *dl, int64_t rows, int V, double inv);
+/* src/train.c:131-141 / :51-64 AdamW update; :172-178 schedule; train_gpt2.c:160-173 clip */
+void orc_adamw(float *p, const float *g, float *m, float *v, int64_t n, double lr, double b1, double b2,
+               double b1t, double b2t, double eps, double wd);
+double orc_sched_cosine_warmup(long step, double warmup, double total);
+double orc_grad_clip(float *const *g, const int64_t *n, int count, double max_norm);
+/* src/train_tape.c:289-313 stored probabilities, :936-1051 SDPA backward */
+void orc_sdpa_probs(const float *q, const float *k, const float *mask, float *P, int B, int H, int Hkv, int Tq,
+                    int Tkv, int hd);
+void orc_sdpa_bwd(const float *q, const float *k, const float *v, const float *P, const float *dy, float *dq,
+                  float *dk, float *dv, int B, int H, int Hkv, int Tq, int Tkv, int hd);
+
 /* src/kernels.c:774-780 rng_next (xorshift64*) and the ktest generator of
  * tests/ktest_kernels.c:8-12, for seeded inputs shared with the reference. */
 uint64_t orc_rng_next(uint64_t *state);

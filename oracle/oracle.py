@@ -63,6 +63,15 @@ def lib():
             "orc_head_merge": (None, [vp, vp, ci, ci, ci, ci, ci]),
             "orc_mul": (None, [vp, vp, vp, i64]),
             "orc_scale": (None, [vp, ctypes.c_float, vp, i64]),
+            "orc_layernorm_bwd": (None, [vp, vp, vp, vp, vp, vp, i64, ci, ctypes.c_double]),
+            "orc_rmsnorm_bwd": (None, [vp, vp, vp, vp, vp, i64, ci]),
+            "orc_ce_fwd": (ctypes.c_double, [vp, vp, vp, vp, vp, i64, ci]),
+            "orc_ce_bwd": (None, [vp, vp, vp, vp, i64, ci, ctypes.c_double]),
+            "orc_adamw": (None, [vp, vp, vp, vp, i64] + [ctypes.c_double] * 7),
+            "orc_sched_cosine_warmup": (ctypes.c_double, [ctypes.c_long, ctypes.c_double, ctypes.c_double]),
+            "orc_grad_clip": (ctypes.c_double, [ctypes.POINTER(vp), ctypes.POINTER(i64), ci, ctypes.c_double]),
+            "orc_sdpa_probs": (None, [vp, vp, vp, vp, ci, ci, ci, ci, ci, ci]),
+            "orc_sdpa_bwd": (None, [vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, ci]),
         }
         for n, (r, a) in sigs.items():
             f = getattr(L, n)
@@ -227,6 +236,95 @@ def scale(x, s_):
     return y
 
 
+def _grad(g0, shape):
+    return np.zeros(shape, np.float32) if g0 is None else _f32(g0).copy()
+
+
+def layernorm_bwd(x, w, dy, dx0=None, dw0=None, db0=None, eps=1e-6, want=("dx", "dw", "db")):
+    """train_tape.c:569-634; returns (dx, dw, db) accumulated onto the given
+    starting gradients (zeros by default); grads not in `want` are None."""
+    x, dy = _f32(x), _f32(dy)
+    w = None if w is None else _f32(w)
+    rows, C = x.shape
+    dx = _grad(dx0, (rows, C)) if "dx" in want else None
+    dw = _grad(dw0, C) if "dw" in want else None
+    db = _grad(db0, C) if "db" in want else None
+    lib().orc_layernorm_bwd(_ptr(x), _ptr(w), _ptr(dy), _ptr(dx), _ptr(dw), _ptr(db), rows, C, eps)
+    return dx, dw, db
+
+
+def rmsnorm_bwd(x, w, dy, dx0=None, dw0=None, want=("dx", "dw")):
+    x, dy = _f32(x), _f32(dy)
+    w = None if w is None else _f32(w)
+    rows, C = x.shape
+    dx = _grad(dx0, (rows, C)) if "dx" in want else None
+    dw = _grad(dw0, C) if "dw" in want else None
+    lib().orc_rmsnorm_bwd(_ptr(x), _ptr(w), _ptr(dy), _ptr(dx), _ptr(dw), rows, C)
+    return dx, dw
+
+
+def ce_fwd(logits, tgt, wm=None):
+    """t_ce: returns (loss, probs, cnt)."""
+    logits = _f32(logits)
+    tgt = np.ascontiguousarray(tgt, np.int32)
+    wm = None if wm is None else _f32(wm)
+    rows, V = logits.shape
+    probs = np.empty_like(logits)
+    loss = np.zeros(1, np.float32)
+    cnt = lib().orc_ce_fwd(_ptr(logits), _ptr(tgt), _ptr(wm), _ptr(loss), _ptr(probs), rows, V)
+    return float(loss[0]), probs, cnt
+
+
+def ce_bwd(probs, tgt, wm, inv, dl0=None):
+    probs = _f32(probs)
+    tgt = np.ascontiguousarray(tgt, np.int32)
+    wm = None if wm is None else _f32(wm)
+    dl = _grad(dl0, probs.shape)
+    lib().orc_ce_bwd(_ptr(probs), _ptr(tgt), _ptr(wm), _ptr(dl), probs.shape[0], probs.shape[1], inv)
+    return dl
+
+
+def adamw(p, g, m, v, lr, b1, b2, b1t, b2t, eps, wd):
+    """Returns updated copies (p, m, v)."""
+    p, m, v = _f32(p).copy(), _f32(m).copy(), _f32(v).copy()
+    g = _f32(g)
+    lib().orc_adamw(_ptr(p), _ptr(g), _ptr(m), _ptr(v), p.size, lr, b1, b2, b1t, b2t, eps, wd)
+    return p, m, v
+
+
+def sched_cosine_warmup(step, warmup, total):
+    return lib().orc_sched_cosine_warmup(step, warmup, total)
+
+
+def grad_clip(grads, max_norm=1.0):
+    """Returns (gnorm, clipped copies)."""
+    gs = [_f32(g).copy() for g in grads]
+    ptrs = (vp * len(gs))(*[g.ctypes.data for g in gs])
+    ns = (i64 * len(gs))(*[g.size for g in gs])
+    gn = lib().orc_grad_clip(ptrs, ns, len(gs), max_norm)
+    return gn, gs
+
+
+def sdpa_probs(q, k, mask=None):
+    q, k = _f32(q), _f32(k)
+    B, H, Tq, hd = q.shape
+    Hkv, Tkv = k.shape[1], k.shape[2]
+    m = None if mask is None else _f32(mask)
+    P = np.empty((B, H, Tq, Tkv), np.float32)
+    lib().orc_sdpa_probs(_ptr(q), _ptr(k), _ptr(m), _ptr(P), B, H, Hkv, Tq, Tkv, hd)
+    return P
+
+
+def sdpa_bwd(q, k, v, P, dy, dq0=None, dk0=None, dv0=None):
+    q, k, v, P, dy = _f32(q), _f32(k), _f32(v), _f32(P), _f32(dy)
+    B, H, Tq, hd = q.shape
+    Hkv, Tkv = k.shape[1], k.shape[2]
+    dq, dk, dv = _grad(dq0, q.shape), _grad(dk0, k.shape), _grad(dv0, v.shape)
+    lib().orc_sdpa_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(P), _ptr(dy), _ptr(dq), _ptr(dk), _ptr(dv),
+                       B, H, Hkv, Tq, Tkv, hd)
+    return dq, dk, dv
+
+
 def ktest_fill(state, n):
     """tests/ktest_kernels.c:8-12 generator; returns (values, new_state)."""
     st = ctypes.c_uint64(state)
@@ -269,6 +367,10 @@ def ref():
             "mul_fwd": (None, [vp, vp, vp, i64]),
             "scale_fwd": (None, [vp, ctypes.c_float, vp, i64]),
             "add_fwd": (None, [vp, vp, vp, i64]),
+            "refg_ln_bwd": (None, [vp, vp, vp, vp, vp, vp, vp, vp, ctypes.c_longlong, ci, ctypes.c_double]),
+            "refg_rmsn_bwd": (None, [vp, vp, vp, vp, vp, vp, ctypes.c_longlong, ci]),
+            "refg_ce": (None, [vp, vp, vp, vp, vp, vp, ctypes.c_longlong, ci, ctypes.c_double]),
+            "refg_sdpa_bwd": (None, [vp] * 10 + [ci] * 6),
         }
         for n, (r, a) in sigs.items():
             f = getattr(L, n)
@@ -325,3 +427,56 @@ def ref_vq_multiscale(z, Es, B, L):
                                   _ptr(z_hat), _ptr(z_rest))
     assert rc == 0
     return idx, z_hat, z_rest
+
+
+def ref_ln_bwd(x, w, b, dy, dx0=None, dw0=None, db0=None, eps=None):
+    """Reference tape, one TOP_LN (eps None) or TOP_LNE record."""
+    x, dy = _f32(x), _f32(dy)
+    w = None if w is None else _f32(w)
+    b = None if b is None else _f32(b)
+    rows, C = x.shape
+    y = np.empty_like(x)
+    dx = _grad(dx0, (rows, C))
+    dw = _grad(dw0, C) if w is not None else None
+    db = _grad(db0, C) if b is not None else None
+    ref().refg_ln_bwd(_ptr(x), _ptr(w), _ptr(b), _ptr(dy), _ptr(y), _ptr(dx), _ptr(dw), _ptr(db), rows, C,
+                      -1.0 if eps is None else eps)
+    return dx, dw, db
+
+
+def ref_rmsn_bwd(x, w, dy, dx0=None, dw0=None):
+    x, dy = _f32(x), _f32(dy)
+    w = None if w is None else _f32(w)
+    rows, C = x.shape
+    y = np.empty_like(x)
+    dx = _grad(dx0, (rows, C))
+    dw = _grad(dw0, C) if w is not None else None
+    ref().refg_rmsn_bwd(_ptr(x), _ptr(w), _ptr(dy), _ptr(y), _ptr(dx), _ptr(dw), rows, C)
+    return dx, dw
+
+
+def ref_ce(logits, tgt, wm=None, weight=1.0, dl0=None):
+    """Reference t_ce + backward: (loss, probs, dlogits)."""
+    logits = _f32(logits)
+    tgt = np.ascontiguousarray(tgt, np.int32)
+    wm = None if wm is None else _f32(wm)
+    rows, V = logits.shape
+    loss = np.zeros(1, np.float32)
+    probs = np.empty_like(logits)
+    dl = _grad(dl0, logits.shape)
+    ref().refg_ce(_ptr(logits), _ptr(tgt), _ptr(wm), _ptr(loss), _ptr(probs), _ptr(dl), rows, V, weight)
+    return float(loss[0]), probs, dl
+
+
+def ref_sdpa_bwd(q, k, v, mask, dy):
+    """Reference t_sdpa + TOP_SDPA backward: (o, P, dq, dk, dv)."""
+    q, k, v, dy = _f32(q), _f32(k), _f32(v), _f32(dy)
+    m = None if mask is None else _f32(mask)
+    B, H, Tq, hd = q.shape
+    Hkv, Tkv = k.shape[1], k.shape[2]
+    o = np.empty_like(q)
+    P = np.empty((B, H, Tq, Tkv), np.float32)
+    dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
+    ref().refg_sdpa_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(m), _ptr(dy), _ptr(o), _ptr(dq), _ptr(dk), _ptr(dv),
+                        _ptr(P), B, H, Hkv, Tq, Tkv, hd)
+    return o, P, dq, dk, dv

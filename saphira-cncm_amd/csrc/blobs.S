@@ -13,4 +13,8 @@ ncm_co_vq:
     .globl ncm_co_ops
 ncm_co_ops:
     .incbin "ops.co"
+    .balign 4096
+    .globl ncm_co_train
+ncm_co_train:
+    .incbin "train.co"
     .section .note.GNU-stack,"",@progbits

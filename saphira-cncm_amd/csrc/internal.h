@@ -31,7 +31,7 @@ int ncm_launch_named(const char *name, unsigned gx, unsigned gy, unsigned gz, un
 
 /* Library-owned device workspaces (grown on demand, stream-synchronised
  * before a grow).  Slot ids keep independent users apart. */
-enum { WS_SPLITK = 0, WS_COLSUM = 1, WS_VQ = 2, WS_DXT = 3, WS_COUNT = 4 };
+enum { WS_SPLITK = 0, WS_COLSUM = 1, WS_VQ = 2, WS_DXT = 3, WS_TRAIN = 4, WS_COUNT = 5 };
 /* Compute units of the selected device. */
 int ncm_cu_count(void);
 void *ncm_workspace(int slot, size_t bytes);

@@ -10,8 +10,8 @@
 #include <string.h>
 
 /* ---- embedded code objects (blobs.S) ---- */
-extern const unsigned char ncm_co_gemm[], ncm_co_vq[], ncm_co_ops[];
-static const unsigned char *const co_blobs[] = {ncm_co_gemm, ncm_co_vq, ncm_co_ops};
+extern const unsigned char ncm_co_gemm[], ncm_co_vq[], ncm_co_ops[], ncm_co_train[];
+static const unsigned char *const co_blobs[] = {ncm_co_gemm, ncm_co_vq, ncm_co_ops, ncm_co_train};
 #define N_MODULES (int)(sizeof(co_blobs) / sizeof(co_blobs[0]))
 
 static int g_state = 0; /* 0 = not initialised, 1 = ready, <0 = failed */

@@ -1,0 +1,767 @@
+// train.hip -- training-step kernels: LayerNorm/RMSNorm backward, softmax
+// cross-entropy, AdamW, global-norm clipping and the SDPA backward.
+//
+// All gradients accumulate (+=) into the caller's buffers, as the tape
+// backward of the reference does (train_tape.c:636-1051).
+#include "ncm_dev.h"
+
+// ---------------------------------------------------------------- norm backward
+// One wave per row.  Row statistics in fp64 (train_tape.c:583-593 / 759-765)
+// are written to stats[] for the parameter-gradient pass; dx follows the
+// reference formulas in fp64 with one float rounding per element.
+extern "C" __global__ void __launch_bounds__(256)
+ln_bwd_rows(const float *__restrict__ x, const float *__restrict__ w, const float *__restrict__ dy,
+            float *__restrict__ dx, double *__restrict__ stats, int64_t rows, int C, double eps) {
+#pragma clang fp contract(off)
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float *xr = x + row * C, *gr = dy + row * C;
+    double mean = 0.0;
+    for (int c = lane; c < C; c += 64) mean += (double)xr[c];
+    mean = wave_sum_d(mean) / C;
+    double var = 0.0;
+    for (int c = lane; c < C; c += 64) {
+        const double d = (double)xr[c] - mean;
+        var += d * d;
+    }
+    var = wave_sum_d(var) / C;
+    const double inv = 1.0 / sqrt(var + eps);
+    if (lane == 0) {
+        stats[2 * row] = mean;
+        stats[2 * row + 1] = inv;
+    }
+    if (!dx) return;
+    double dmean = 0.0, dvar = 0.0;
+    for (int c = lane; c < C; c += 64) {
+        const double d = (double)gr[c] * (w ? (double)w[c] : 1.0);
+        dmean += d;
+        dvar += d * ((double)xr[c] - mean);
+    }
+    dmean = wave_sum_d(dmean) / C;
+    dvar = wave_sum_d(dvar) * (-0.5 * inv * inv * inv / C);
+    float *dr = dx + row * C;
+    for (int c = lane; c < C; c += 64) {
+        const double d = (double)gr[c] * (w ? (double)w[c] : 1.0);
+        dr[c] += (float)((d - dmean) * inv + 2 * ((double)xr[c] - mean) * dvar);
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+rmsn_bwd_rows(const float *__restrict__ x, const float *__restrict__ w, const float *__restrict__ dy,
+              float *__restrict__ dx, double *__restrict__ stats, int64_t rows, int C) {
+#pragma clang fp contract(off)
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float *xr = x + row * C, *gr = dy + row * C;
+    double ms = 0.0;
+    for (int c = lane; c < C; c += 64) ms += (double)xr[c] * (double)xr[c];
+    ms = wave_sum_d(ms) / C;
+    const double inv = 1.0 / sqrt(ms + 1e-6);
+    if (lane == 0) stats[row] = inv;
+    if (!dx) return;
+    double dot = 0.0;
+    for (int c = lane; c < C; c += 64) dot += (double)gr[c] * (w ? (double)w[c] : 1.0) * (double)xr[c];
+    dot = wave_sum_d(dot) / C;
+    float *dr = dx + row * C;
+    for (int c = lane; c < C; c += 64) {
+        const double wc = w ? (double)w[c] : 1.0;
+        dr[c] += (float)(((double)gr[c] * wc - dot * (double)xr[c] * inv * inv) * inv);
+    }
+}
+
+// Parameter gradients: per column, partial fp64 sums over a chunk of
+// NORM_ROWS rows (ascending), then norm_param_final adds the chunk partials
+// in chunk order and float-adds the rounded sum into dw / db.
+//   kind 0 (LayerNorm): dw += sum dy*(x-mean)*inv, db += sum dy
+//   kind 1 (RMSNorm):   dw += sum (float)(dy*x) * inv
+#define NORM_ROWS 128
+extern "C" __global__ void __launch_bounds__(256)
+norm_param_partial(const float *__restrict__ x, const float *__restrict__ dy, const double *__restrict__ stats,
+                   double *__restrict__ part, int64_t rows, int C, int kind) {
+#pragma clang fp contract(off)
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= C) return;
+    const int64_t r0 = (int64_t)blockIdx.y * NORM_ROWS;
+    const int64_t r1 = r0 + NORM_ROWS < rows ? r0 + NORM_ROWS : rows;
+    double sw = 0.0, sb = 0.0;
+    for (int64_t r = r0; r < r1; ++r) {
+        const float g = dy[r * C + c], xv = x[r * C + c];
+        if (kind == 0) {
+            sw += (double)g * (((double)xv - stats[2 * r]) * stats[2 * r + 1]);
+            sb += (double)g;
+        } else {
+            const float gx = g * xv;
+            sw += (double)gx * stats[r];
+        }
+    }
+    double *p = part + ((int64_t)blockIdx.y * C + c) * 2;
+    p[0] = sw;
+    p[1] = sb;
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+norm_param_final(const double *__restrict__ part, float *__restrict__ dw, float *__restrict__ db, int chunks,
+                 int C) {
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= C) return;
+    double sw = 0.0, sb = 0.0;
+    for (int k = 0; k < chunks; ++k) {
+        sw += part[((int64_t)k * C + c) * 2];
+        sb += part[((int64_t)k * C + c) * 2 + 1];
+    }
+    if (dw) dw[c] += (float)sw;
+    if (db) db[c] += (float)sb;
+}
+
+// ---------------------------------------------------------------- cross-entropy
+// One wave per row (train_tape.c:452-465): float max, fp64 exp and sum,
+// p = (float)e / (float)den, nll = w * -log(p[tgt] + 1e-30).
+//   mode 0: write probs
+//   mode 1: dl += (float)((p - onehot) * w * inv), inv = weight / cnt with cnt
+//           = cnt_in[0] when given, else cnt_val (fused forward + backward;
+//           probs not stored)
+// rowstat[2r] = nll contribution, rowstat[2r+1] = weight (0 for w == 0 rows).
+// A target outside [0, V) (out-of-bounds in the reference) matches no class
+// and contributes w * -log(1e-30).
+extern "C" __global__ void __launch_bounds__(256)
+ce_rows(const float *__restrict__ logits, const int *__restrict__ tgt, const float *__restrict__ wm,
+        float *__restrict__ out, double *__restrict__ rowstat, const double *__restrict__ cnt_in,
+        double cnt_val, double weight, int64_t rows, int V, int mode) {
+#pragma clang fp contract(off)
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float *l = logits + row * V;
+    float m = -INFINITY;
+    for (int v = lane; v < V; v += 64) m = fmaxf(m, l[v]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    if (l[0] != l[0]) m = l[0];   // the reference's scan keeps a NaN first element
+    double den = 0.0;
+    for (int v = lane; v < V; v += 64) den += exp((double)l[v] - (double)m);
+    den = wave_sum_d(den);
+    const float fden = (float)den;
+    const int t = tgt[row];
+    const float w = wm ? wm[row] : 1.0f;
+    if (mode == 0) {
+        float *p = out + row * V;
+        for (int v = lane; v < V; v += 64) p[v] = (float)exp((double)l[v] - (double)m) / fden;
+    } else if (w != 0.0f) {
+        const double cnt = cnt_in ? cnt_in[0] : cnt_val;
+        const double inv = (cnt > 0 ? 1.0 / cnt : 0.0) * weight;
+        float *g = out + row * V;
+        for (int v = lane; v < V; v += 64) {
+            const float p = (float)exp((double)l[v] - (double)m) / fden;
+            g[v] += (float)(((double)p - (v == t ? 1.0 : 0.0)) * (double)w * inv);
+        }
+    }
+    if (lane == 0) {
+        double nll = 0.0, cw = 0.0;
+        if (w != 0.0f) {
+            const float pt = (unsigned)t < (unsigned)V ? (float)exp((double)l[t] - (double)m) / fden : 0.0f;
+            nll = (double)w * -log((double)pt + 1e-30);
+            cw = (double)w;
+        }
+        rowstat[2 * row] = nll;
+        rowstat[2 * row + 1] = cw;
+    }
+}
+
+// Weight count sum_r w_r (rows with w == 0 add nothing) for the fused mode.
+extern "C" __global__ void __launch_bounds__(256)
+ce_count(const float *__restrict__ wm, double *__restrict__ cnt, int64_t rows) {
+    __shared__ double part[4];
+    double s = 0.0;
+    for (int64_t r = threadIdx.x; r < rows; r += 256) s += (double)wm[r];
+    s = wave_sum_d(s);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) cnt[0] = ((part[0] + part[1]) + part[2]) + part[3];
+}
+
+// loss = (float)(sum nll / sum w) over rowstat, fixed order (one workgroup).
+extern "C" __global__ void __launch_bounds__(256)
+ce_loss_final(const double *__restrict__ rowstat, float *__restrict__ loss, int64_t rows) {
+    __shared__ double pn[4], pc[4];
+    double n = 0.0, c = 0.0;
+    for (int64_t r = threadIdx.x; r < rows; r += 256) {
+        n += rowstat[2 * r];
+        c += rowstat[2 * r + 1];
+    }
+    n = wave_sum_d(n);
+    c = wave_sum_d(c);
+    if ((threadIdx.x & 63) == 0) {
+        pn[threadIdx.x >> 6] = n;
+        pc[threadIdx.x >> 6] = c;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const double nt = ((pn[0] + pn[1]) + pn[2]) + pn[3];
+        const double ct = ((pc[0] + pc[1]) + pc[2]) + pc[3];
+        loss[0] = ct > 0 ? (float)(nt / ct) : 0.0f;
+    }
+}
+
+// k_ce_bwd (train_tape.c:1801-1810): dl += (float)((p - onehot) * w * inv).
+extern "C" __global__ void __launch_bounds__(256)
+ce_bwd_k(const float *__restrict__ probs, const int *__restrict__ tgt, const float *__restrict__ wm,
+         float *__restrict__ dl, int64_t rows, int V, double inv) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * V) return;
+    const int64_t r = i / V;
+    const int v = (int)(i - r * V);
+    const float w = wm ? wm[r] : 1.0f;
+    if (w == 0.0f) return;
+    dl[i] += (float)(((double)probs[i] - (v == tgt[r] ? 1.0 : 0.0)) * (double)w * inv);
+}
+
+// ---------------------------------------------------------------- optimizer
+// k_adamw (train.c:51-64), operation for operation: decoupled decay, moments
+// in fp64 rounded to float, bias-corrected step in fp64.  Bit-identical to
+// the host loop (train.c:131-141): IEEE double ops with contraction off.
+extern "C" __global__ void __launch_bounds__(256)
+adamw_k(float *__restrict__ p, const float *__restrict__ g, float *__restrict__ m, float *__restrict__ v,
+        int64_t n, double lr, double b1, double b2, double b1t, double b2t, double eps, double wd) {
+#pragma clang fp contract(off)
+    const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (k >= n) return;
+    const float gk = g[k];
+    float pk = p[k];
+    pk = pk - (float)(lr * wd * (double)pk);
+    const float mk = (float)(b1 * (double)m[k] + (1.0 - b1) * (double)gk);
+    const float vk = (float)(b2 * (double)v[k] + (1.0 - b2) * (double)gk * (double)gk);
+    m[k] = mk;
+    v[k] = vk;
+    const double mh = (double)mk / b1t, vh = (double)vk / b2t;
+    p[k] = pk - (float)(lr * mh / (sqrt(vh) + eps));
+}
+
+// Sum of squares in fp64: one partial per workgroup (grid-stride), written
+// to part[blockIdx.x]; sumsq_final adds `count` partials in index order.
+extern "C" __global__ void __launch_bounds__(256)
+sumsq_partial(const float *__restrict__ g, int64_t n, double *__restrict__ part) {
+    __shared__ double ws[4];
+    double s = 0.0;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+        const double x = (double)g[i];
+        s += x * x;
+    }
+    s = wave_sum_d(s);
+    if ((threadIdx.x & 63) == 0) ws[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) part[blockIdx.x] = ((ws[0] + ws[1]) + ws[2]) + ws[3];
+}
+
+extern "C" __global__ void __launch_bounds__(64)
+sumsq_final(const double *__restrict__ part, int count, double *__restrict__ out) {
+    double s = 0.0;
+    for (int i = threadIdx.x; i < count; i += 64) s += part[i];
+    s = wave_sum_d(s);
+    if (threadIdx.x == 0) out[0] = s;
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+scale_inplace_k(float *__restrict__ g, int64_t n, float s) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) g[i] = g[i] * s;
+}
+
+// ---------------------------------------------------------------- SDPA backward
+// Inputs: q [B][H][Tq][hd], k/v [B][Hkv][Tkv][hd], the stored probabilities
+// P [B][H][Tq][Tkv] (train_tape.c:289-313), dO like q.  With dP = dO V^T and
+// D = rowsum(P o dP):  dS = P o (dP - D),  dq += scale dS K,
+// dk += scale dS^T Q,  dv += P^T dO (kv head = h / (H/Hkv); dk, dv sum over
+// the query heads of the group) -- train_tape.c:936-1051.
+//
+// Generic path (any hd <= 256, any Tkv): one wave per row, lanes over d.
+// sdpa_bwd_dq_rows also writes D for sdpa_bwd_dkdv_rows.
+extern "C" __global__ void __launch_bounds__(256)
+sdpa_bwd_dq_rows(const float *__restrict__ k, const float *__restrict__ v, const float *__restrict__ P,
+                 const float *__restrict__ dO, float *__restrict__ dq, float *__restrict__ Dout, int B, int H,
+                 int Hkv, int Tq, int Tkv, int hd, float scale) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= (int64_t)B * H * Tq) return;
+    const int h = (int)((row / Tq) % H), b = (int)(row / ((int64_t)Tq * H));
+    const int kvh = h / (H / Hkv);
+    const float *kb = k + ((int64_t)b * Hkv + kvh) * Tkv * hd;
+    const float *vb = v + ((int64_t)b * Hkv + kvh) * Tkv * hd;
+    const float *pr = P + row * Tkv;
+    float g[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int d = lane + 64 * j;
+        g[j] = d < hd ? dO[row * hd + d] : 0.f;
+    }
+    double tot = 0.0;
+    for (int tk = 0; tk < Tkv; ++tk) {
+        const float *vr = vb + (int64_t)tk * hd;
+        double s = 0.0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int d = lane + 64 * j;
+            if (d < hd) s += (double)g[j] * (double)vr[d];
+        }
+        tot += wave_sum_d(s) * (double)pr[tk];
+    }
+    if (lane == 0 && Dout) Dout[row] = (float)tot;
+    if (!dq) return;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int tk = 0; tk < Tkv; ++tk) {
+        const float *vr = vb + (int64_t)tk * hd, *kr = kb + (int64_t)tk * hd;
+        double s = 0.0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int d = lane + 64 * j;
+            if (d < hd) s += (double)g[j] * (double)vr[d];
+        }
+        const double p = (double)pr[tk];
+        const float ds = (float)(p * wave_sum_d(s) - p * tot);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int d = lane + 64 * j;
+            if (d < hd) acc[j] += ds * kr[d];
+        }
+    }
+    float *o = dq + row * hd;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int d = lane + 64 * j;
+        if (d < hd) o[d] += scale * acc[j];
+    }
+}
+
+// One wave per (b, kv head, key): lanes over d; sums over the query heads of
+// the group and all queries.
+extern "C" __global__ void __launch_bounds__(256)
+sdpa_bwd_dkdv_rows(const float *__restrict__ q, const float *__restrict__ v, const float *__restrict__ P,
+                   const float *__restrict__ dO, const float *__restrict__ D, float *__restrict__ dk,
+                   float *__restrict__ dv, int B, int H, int Hkv, int Tq, int Tkv, int hd, float scale) {
+    const int64_t kr_ = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (kr_ >= (int64_t)B * Hkv * Tkv) return;
+    const int tk = (int)(kr_ % Tkv);
+    const int kvh = (int)((kr_ / Tkv) % Hkv), b = (int)(kr_ / ((int64_t)Tkv * Hkv));
+    const int rep = H / Hkv;
+    const float *vr = v + kr_ * hd;
+    float vv[4], sk[4] = {0.f, 0.f, 0.f, 0.f}, sv[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int d = lane + 64 * j;
+        vv[j] = d < hd ? vr[d] : 0.f;
+    }
+    for (int h = kvh * rep; h < (kvh + 1) * rep; ++h) {
+        const int64_t rbase = ((int64_t)b * H + h) * Tq;
+        for (int tq = 0; tq < Tq; ++tq) {
+            const int64_t row = rbase + tq;
+            const float *gr = dO + row * hd, *qr = q + row * hd;
+            double s = 0.0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int d = lane + 64 * j;
+                if (d < hd) s += (double)gr[d] * (double)vv[j];
+            }
+            const double p = (double)P[row * Tkv + tk];
+            const float ds = (float)(p * wave_sum_d(s) - p * (double)D[row]);
+            const float pf = (float)p;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int d = lane + 64 * j;
+                if (d < hd) {
+                    sk[j] += ds * qr[d];
+                    sv[j] += pf * gr[d];
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int d = lane + 64 * j;
+        if (d < hd) {
+            if (dk) dk[kr_ * hd + d] += scale * sk[j];
+            if (dv) dv[kr_ * hd + d] += sv[j];
+        }
+    }
+}
+
+// MFMA path for hd = 64 (Tkv % 4 == 0, 16-byte aligned pointers).
+// k-permutation as in the GEMM: MFMA step s gives lane group g the reduction
+// index 4g + s, so every operand fragment is a float4.
+#define SB_LD 72
+
+// dq kernel: a workgroup owns 64 queries of one (b, h), wave w the 16
+// queries q0 + 16w + li.  Sweep 1 builds D = sum_k P dP; sweep 2 forms
+// dS^T = P^T o (dP^T - D) in the accumulator layout of dP^T = V dO^T (lane
+// (li, g) holds keys 16c + 4g + r of query li), which is the A operand of
+// dq = dS K.
+extern "C" __global__ void __launch_bounds__(256)
+sdpa_bwd_dq_hd64(const float *__restrict__ k, const float *__restrict__ v, const float *__restrict__ P,
+                 const float *__restrict__ dO, float *__restrict__ dq, float *__restrict__ Dout, int H, int Hkv,
+                 int Tq, int Tkv, float scale) {
+    __shared__ __attribute__((aligned(16))) float sK[64 * SB_LD];
+    __shared__ __attribute__((aligned(16))) float sV[64 * SB_LD];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4;
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int kvh = h / (H / Hkv);
+    const int qw = blockIdx.x * 64 + wave * 16;
+    const int my_q = qw + li;
+    const int64_t rbase = ((int64_t)b * H + h) * Tq;
+    const float *kb = k + ((int64_t)b * Hkv + kvh) * Tkv * 64;
+    const float *vb = v + ((int64_t)b * Hkv + kvh) * Tkv * 64;
+    const float *prow = P + (rbase + (my_q < Tq ? my_q : 0)) * Tkv;
+
+    f4 gf[4];   // dO^T fragments: query my_q, d = 16kc + 4g .. +3
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc)
+        gf[kc] = my_q < Tq ? *(const f4 *)(dO + (rbase + my_q) * 64 + kc * 16 + 4 * lg) : f4{0.f, 0.f, 0.f, 0.f};
+
+    float tot = 0.f;
+    f4 acc[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[u] = f4{0.f, 0.f, 0.f, 0.f};
+
+    for (int sweep = 0; sweep < 2; ++sweep) {
+        for (int k0 = 0; k0 < Tkv; k0 += 64) {
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int f = tid + j * 256;
+                const int r = f >> 4, c = (f & 15) * 4;
+                const int key = k0 + r;
+                f4 vv = {0.f, 0.f, 0.f, 0.f}, kv = {0.f, 0.f, 0.f, 0.f};
+                if (key < Tkv) {
+                    vv = *(const f4 *)(vb + (int64_t)key * 64 + c);
+                    if (sweep) kv = *(const f4 *)(kb + (int64_t)key * 64 + c);
+                }
+                *(f4 *)(sV + r * SB_LD + c) = vv;
+                if (sweep) *(f4 *)(sK + r * SB_LD + c) = kv;
+            }
+            __syncthreads();
+            // dP^T[c]: keys k0 + 16c + 4g + r, query my_q
+            f4 dp[4], pv[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                dp[c] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kc = 0; kc < 4; ++kc) {
+                    const f4 vf = *(const f4 *)(sV + (16 * c + li) * SB_LD + kc * 16 + 4 * lg);
+#pragma unroll
+                    for (int st = 0; st < 4; ++st) dp[c] = mfma4(vf[st], gf[kc][st], dp[c]);
+                }
+                const int key = k0 + 16 * c + 4 * lg;
+                pv[c] = (my_q < Tq && key < Tkv) ? *(const f4 *)(prow + key) : f4{0.f, 0.f, 0.f, 0.f};
+            }
+            if (sweep == 0) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) tot += pv[c][r] * dp[c][r];
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) dp[c][r] = pv[c][r] * (dp[c][r] - tot);
+                // dq[query qw + 4g + r][d = 4li + u] += dS[query][key] K[key][d]
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+#pragma unroll
+                    for (int st = 0; st < 4; ++st) {
+                        const f4 kf = *(const f4 *)(sK + (16 * c + 4 * lg + st) * SB_LD + 4 * li);
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) acc[u] = mfma4(dp[c][st], kf[u], acc[u]);
+                    }
+            }
+        }
+        if (sweep == 0) {
+            tot += __shfl_xor(tot, 16, 64);
+            tot += __shfl_xor(tot, 32, 64);
+            if (lg == 0 && my_q < Tq && Dout) Dout[rbase + my_q] = tot;
+            if (!dq) return;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int qi = qw + 4 * lg + r;
+        if (qi < Tq) {
+            f4 *o = (f4 *)(dq + (rbase + qi) * 64 + 4 * li);
+            f4 cur = *o;
+            cur[0] += scale * acc[0][r];
+            cur[1] += scale * acc[1][r];
+            cur[2] += scale * acc[2][r];
+            cur[3] += scale * acc[3][r];
+            *o = cur;
+        }
+    }
+}
+
+// dk/dv kernel: a workgroup owns 64 keys of one (b, kv head), wave w the 16
+// keys k0 + 16w + li.  For every query head of the group and every 64-query
+// tile: dP = dO V^T in the layout (query 16c + 4g + r, key li) -- the A
+// operand layout of dV = P^T dO and dK = dS^T Q.  P^T is staged in LDS with
+// the float4 column groups XOR-swizzled by (key & 15), so both the
+// transposing stores and the float4 loads are free of bank conflicts.
+extern "C" __global__ void __launch_bounds__(256)
+sdpa_bwd_dkdv_hd64(const float *__restrict__ q, const float *__restrict__ v, const float *__restrict__ P,
+                   const float *__restrict__ dO, const float *__restrict__ D, float *__restrict__ dk,
+                   float *__restrict__ dv, int H, int Hkv, int Tq, int Tkv, float scale) {
+    __shared__ __attribute__((aligned(16))) float sG[64 * SB_LD];   // dO tile [query][d]
+    __shared__ __attribute__((aligned(16))) float sQ[64 * SB_LD];   // Q tile  [query][d]
+    __shared__ __attribute__((aligned(16))) float sPT[64 * 64];     // P^T     [key][query], swizzled
+    __shared__ __attribute__((aligned(16))) float sD[64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4;
+    const int kvh = blockIdx.y, b = blockIdx.z;
+    const int rep = H / Hkv;
+    const int k0 = blockIdx.x * 64;
+    const int kl = wave * 16 + li;            // this lane's key within the tile
+    const int my_k = k0 + kl;
+    const int64_t kbase = ((int64_t)b * Hkv + kvh) * Tkv;
+
+    f4 vf[4];   // V fragments: key my_k, d = 16kc + 4g .. +3
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc)
+        vf[kc] = my_k < Tkv ? *(const f4 *)(v + (kbase + my_k) * 64 + kc * 16 + 4 * lg) : f4{0.f, 0.f, 0.f, 0.f};
+
+    f4 ak[4], av[4];   // [u][r]: key k0 + 16w + 4g + r, d = 4li + u
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        ak[u] = f4{0.f, 0.f, 0.f, 0.f};
+        av[u] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    for (int h = kvh * rep; h < (kvh + 1) * rep; ++h) {
+        const int64_t rbase = ((int64_t)b * H + h) * Tq;
+        for (int q0 = 0; q0 < Tq; q0 += 64) {
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                // dO and Q rows: float4 along d
+                const int f = tid + j * 256;
+                const int r = f >> 4, c = (f & 15) * 4;
+                const int qi = q0 + r;
+                f4 gv = {0.f, 0.f, 0.f, 0.f}, qv = {0.f, 0.f, 0.f, 0.f};
+                if (qi < Tq) {
+                    gv = *(const f4 *)(dO + (rbase + qi) * 64 + c);
+                    qv = *(const f4 *)(q + (rbase + qi) * 64 + c);
+                }
+                *(f4 *)(sG + r * SB_LD + c) = gv;
+                *(f4 *)(sQ + r * SB_LD + c) = qv;
+                // P rows (query r2, keys 4c2 .. +3) stored transposed
+                const int r2 = f & 63, c2 = f >> 6;
+                const int qj = q0 + r2, key = k0 + 4 * c2;
+                f4 pv = {0.f, 0.f, 0.f, 0.f};
+                if (qj < Tq && key < Tkv) pv = *(const f4 *)(P + (rbase + qj) * Tkv + key);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int kk = 4 * c2 + e;
+                    sPT[kk * 64 + ((((r2 >> 2) ^ (kk & 15))) << 2) + (r2 & 3)] = pv[e];
+                }
+            }
+            if (tid < 64) sD[tid] = q0 + tid < Tq ? D[rbase + q0 + tid] : 0.f;
+            __syncthreads();
+
+            // dP[c] (query 16c + 4g + r, key kl), P in the same layout, dS
+            f4 dp[4], pf[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                dp[c] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kc = 0; kc < 4; ++kc) {
+                    const f4 gfr = *(const f4 *)(sG + (16 * c + li) * SB_LD + kc * 16 + 4 * lg);
+#pragma unroll
+                    for (int st = 0; st < 4; ++st) dp[c] = mfma4(gfr[st], vf[kc][st], dp[c]);
+                }
+                pf[c] = *(const f4 *)(sPT + kl * 64 + (((4 * c + lg) ^ (kl & 15)) << 2));
+                const f4 dd = *(const f4 *)(sD + 16 * c + 4 * lg);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) dp[c][r] = pf[c][r] * (dp[c][r] - dd[r]);
+            }
+            // dV += P^T dO, dK += dS^T Q
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int st = 0; st < 4; ++st) {
+                    const f4 gfr = *(const f4 *)(sG + (16 * c + 4 * lg + st) * SB_LD + 4 * li);
+                    const f4 qfr = *(const f4 *)(sQ + (16 * c + 4 * lg + st) * SB_LD + 4 * li);
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        av[u] = mfma4(pf[c][st], gfr[u], av[u]);
+                        ak[u] = mfma4(dp[c][st], qfr[u], ak[u]);
+                    }
+                }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int key = k0 + wave * 16 + 4 * lg + r;
+        if (key < Tkv) {
+            if (dk) {
+                f4 *o = (f4 *)(dk + (kbase + key) * 64 + 4 * li);
+                f4 cur = *o;
+                cur[0] += scale * ak[0][r];
+                cur[1] += scale * ak[1][r];
+                cur[2] += scale * ak[2][r];
+                cur[3] += scale * ak[3][r];
+                *o = cur;
+            }
+            if (dv) {
+                f4 *o = (f4 *)(dv + (kbase + key) * 64 + 4 * li);
+                f4 cur = *o;
+                cur[0] += av[0][r];
+                cur[1] += av[1][r];
+                cur[2] += av[2][r];
+                cur[3] += av[3][r];
+                *o = cur;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------- stored probabilities
+// P = softmax(Q K^T * scale + mask) per row, written [B][H][Tq][Tkv]: the
+// probabilities the tape keeps for the SDPA backward (train_tape.c:289-313
+// builds them on the host).  sdpa_probs_hd64: 64 queries per workgroup,
+// S^T = K Q^T on MFMA as in the forward; pass 1 finds the row max and sum,
+// pass 2 writes exp(s - max) / sum.  Keys past Tkv are not written.
+extern "C" __global__ void __launch_bounds__(256)
+sdpa_probs_hd64(const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ mask,
+                float *__restrict__ P, int H, int Hkv, int Tq, int Tkv, float scale) {
+    __shared__ __attribute__((aligned(16))) float sK[64 * SB_LD];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4;
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int kvh = h / (H / Hkv);
+    const int my_q = blockIdx.x * 64 + wave * 16 + li;
+    const int64_t rbase = ((int64_t)b * H + h) * Tq;
+    const float *kb = k + ((int64_t)b * Hkv + kvh) * Tkv * 64;
+    f4 qf[4];
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc)
+        qf[kc] = my_q < Tq ? *(const f4 *)(q + (rbase + my_q) * 64 + kc * 16 + 4 * lg) : f4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.f, inv = 0.f;
+    for (int pass = 0; pass < 2; ++pass) {
+        for (int k0 = 0; k0 < Tkv; k0 += 64) {
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int f = tid + j * 256;
+                const int r = f >> 4, c = (f & 15) * 4;
+                const int key = k0 + r;
+                *(f4 *)(sK + r * SB_LD + c) = key < Tkv ? *(const f4 *)(kb + (int64_t)key * 64 + c)
+                                                        : f4{0.f, 0.f, 0.f, 0.f};
+            }
+            __syncthreads();
+            f4 s[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                s[c] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kc = 0; kc < 4; ++kc) {
+                    const f4 kf = *(const f4 *)(sK + (16 * c + li) * SB_LD + kc * 16 + 4 * lg);
+#pragma unroll
+                    for (int st = 0; st < 4; ++st) s[c] = mfma4(kf[st], qf[kc][st], s[c]);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int key = k0 + 16 * c + 4 * lg + r;
+                    float x = s[c][r] * scale;
+                    if (mask && key < Tkv && my_q < Tq) x += mask[(int64_t)my_q * Tkv + key];
+                    s[c][r] = key < Tkv ? x : -INFINITY;
+                }
+            }
+            if (pass == 0) {
+                float mt = -INFINITY;
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) mt = fmaxf(mt, s[c][r]);
+                const float m_new = fmaxf(m_run, mt);
+                float ps = 0.f;
+                if (m_new != -INFINITY) {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) ps += __expf(s[c][r] - m_new);
+                    l_run = l_run * __expf(m_run - m_new) + ps;
+                    m_run = m_new;
+                }
+            } else if (my_q < Tq) {
+                float *pr = P + (rbase + my_q) * Tkv;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int key = k0 + 16 * c + 4 * lg;
+                    f4 pv;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) pv[r] = __expf(s[c][r] - m_run) * inv;
+                    if (key + 3 < Tkv) {
+                        *(f4 *)(pr + key) = pv;
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (key + r < Tkv) pr[key + r] = pv[r];
+                    }
+                }
+            }
+        }
+        if (pass == 0) {
+            // combine the four lane groups' (max, sum) of query li
+#pragma unroll
+            for (int o = 16; o <= 32; o <<= 1) {
+                const float mo = __shfl_xor(m_run, o, 64), lo = __shfl_xor(l_run, o, 64);
+                const float mn = fmaxf(m_run, mo);
+                if (mn != -INFINITY) {
+                    l_run = l_run * __expf(m_run - mn) + lo * __expf(mo - mn);
+                    m_run = mn;
+                }
+            }
+            inv = 1.0f / l_run;
+        }
+    }
+}
+
+// Generic stored probabilities (any hd <= 256): one wave per query row.
+extern "C" __global__ void __launch_bounds__(256)
+sdpa_probs_rows(const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ mask,
+                float *__restrict__ P, int B, int H, int Hkv, int Tq, int Tkv, int hd, float scale) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= (int64_t)B * H * Tq) return;
+    const int tq = (int)(row % Tq);
+    const int h = (int)((row / Tq) % H), b = (int)(row / ((int64_t)Tq * H));
+    const int kvh = h / (H / Hkv);
+    const float *kb = k + ((int64_t)b * Hkv + kvh) * Tkv * hd;
+    float qv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int d = lane + 64 * j;
+        qv[j] = d < hd ? q[row * hd + d] : 0.f;
+    }
+    float *pr = P + row * Tkv;
+    // pass 1: online max and sum; pass 2: recompute each score and write p
+    float m = -INFINITY, l = 0.f;
+    for (int pass = 0; pass < 2; ++pass) {
+        for (int tk = 0; tk < Tkv; ++tk) {
+            float dot = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int d = lane + 64 * j;
+                if (d < hd) dot += qv[j] * kb[(int64_t)tk * hd + d];
+            }
+            float x = wave_sum(dot) * scale;
+            if (mask) x += mask[(int64_t)tq * Tkv + tk];
+            if (pass == 0) {
+                const float mn = fmaxf(m, x);
+                if (mn != -INFINITY) {
+                    l = l * __expf(m - mn) + __expf(x - mn);
+                    m = mn;
+                }
+            } else if (lane == 0) {
+                pr[tk] = __expf(x - m) / l;
+            }
+        }
+    }
+}

@@ -78,6 +78,16 @@ _SIGS = {
     "add_inplace_fwd": (None, [vp, vp, i64]),
     "qkv_split_fwd": (None, [vp, vp, vp, vp, ci, ci, ci, ci, ci, ci, ci]),
     "head_merge_fwd": (None, [vp, vp, ci, ci, ci, ci, ci]),
+    "layernorm_bwd": (None, [vp, vp, vp, vp, vp, vp, i64, ci, ctypes.c_double]),
+    "rmsnorm_bwd": (None, [vp, vp, vp, vp, vp, i64, ci]),
+    "ce_fwd": (None, [vp, vp, vp, vp, vp, i64, ci]),
+    "ce_bwd": (None, [vp, vp, vp, vp, i64, ci, ctypes.c_double]),
+    "ce_fwd_bwd": (None, [vp, vp, vp, vp, vp, i64, ci, ctypes.c_double]),
+    "sdpa_probs_gqa": (None, [vp, vp, vp, vp, ci, ci, ci, ci, ci, ci]),
+    "sdpa_bwd_gqa": (None, [vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, ci]),
+    "adamw_update": (None, [vp, vp, vp, vp, i64] + [ctypes.c_double] * 7),
+    "sched_cosine_warmup": (ctypes.c_double, [ctypes.c_long, ctypes.c_double, ctypes.c_double]),
+    "grad_clip_global": (ctypes.c_double, [ctypes.POINTER(vp), ctypes.POINTER(i64), ci, ctypes.c_double]),
     "argmax_row": (ci, [vp, ci]),
     "argmax_rows": (None, [vp, vp, i64, ci]),
 }

@@ -1,0 +1,198 @@
+"""GPU training-step rows against the oracle (the reference's tape backward and
+optimizer restated on the CPU).
+
+Bars (gradients: the north-star max-abs 1e-3, asserted tighter here):
+  norm backward dx, dw, db      maxrel 1e-5 (fp64 in both; RMSNorm dw 1e-4:
+                                the reference sums it in float)
+  CE probs / loss               maxrel 1e-6;  ce_bwd bit-exact from equal probs
+  SDPA probs                    max-abs 1e-6
+  SDPA backward dq, dk, dv      max-abs 1e-4 and maxrel 1e-4 (fp32 MFMA sums
+                                against the reference's fp64/float mix)
+  AdamW                         bit-exact over several steps
+  clip                          norm rel 1e-12, gradients within 1 ulp
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import ncmhip
+import oracle as O
+from conftest import bits_equal, maxrel
+
+pytestmark = pytest.mark.gpu
+D = ncmhip.DeviceBuffer
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    ncmhip.init(0)
+    print("[gpu] train tests on device 0", flush=True)
+
+
+def rnd(seed, *shape, scale=1.0):
+    return (np.random.default_rng(seed).standard_normal(shape) * scale).astype(np.float32)
+
+
+def up(a):
+    return None if a is None else D.from_numpy(a)
+
+
+# ---------------------------------------------------------------- norms
+@pytest.mark.parametrize("rows,C", [(1, 1), (37, 96), (300, 65), (4096, 768), (129, 896)])
+@pytest.mark.parametrize("eps,affine", [(1e-6, True), (1e-5, True), (1e-6, False)])
+def test_layernorm_bwd(rows, C, eps, affine):
+    x, dy = rnd(1, rows, C) * 2 + 0.3, rnd(2, rows, C)
+    w = rnd(3, C) if affine else None
+    dx0, dw0, db0 = rnd(4, rows, C), rnd(5, C), rnd(6, C)
+    want = ("dx", "dw", "db") if affine else ("dx",)
+    rdx, rdw, rdb = O.layernorm_bwd(x, w, dy, dx0, dw0, db0, eps=eps, want=want)
+    dx, dw, db = up(dx0), up(dw0) if affine else None, up(db0) if affine else None
+    ncmhip.call("layernorm_bwd", up(x), up(w), up(dy), dx, dw, db, rows, C, eps)
+    assert maxrel(dx.numpy(), rdx) <= 1e-5
+    if affine:
+        assert maxrel(dw.numpy(), rdw) <= 1e-5 and maxrel(db.numpy(), rdb) <= 1e-5
+
+
+@pytest.mark.parametrize("rows,C", [(1, 1), (29, 128), (5184, 256), (2048, 896)])
+@pytest.mark.parametrize("weighted", [True, False])
+def test_rmsnorm_bwd(rows, C, weighted):
+    x, dy = rnd(7, rows, C), rnd(8, rows, C)
+    w = rnd(9, C) if weighted else None
+    dx0, dw0 = rnd(10, rows, C), rnd(11, C)
+    rdx, rdw = O.rmsnorm_bwd(x, w, dy, dx0, dw0, want=("dx", "dw") if weighted else ("dx",))
+    dx, dw = up(dx0), up(dw0) if weighted else None
+    ncmhip.call("rmsnorm_bwd", up(x), up(w), up(dy), dx, dw, rows, C)
+    assert maxrel(dx.numpy(), rdx) <= 1e-5
+    if weighted:
+        assert maxrel(dw.numpy(), rdw) <= 1e-4
+
+
+def test_norm_bwd_param_only():
+    rows, C = 200, 64
+    x, dy, w = rnd(12, rows, C), rnd(13, rows, C), rnd(14, C)
+    _, rdw, rdb = O.layernorm_bwd(x, w, dy, want=("dw", "db"))
+    dw, db = D.from_numpy(np.zeros(C, np.float32)), D.from_numpy(np.zeros(C, np.float32))
+    ncmhip.call("layernorm_bwd", up(x), up(w), up(dy), None, dw, db, rows, C, 1e-6)
+    assert maxrel(dw.numpy(), rdw) <= 1e-5 and maxrel(db.numpy(), rdb) <= 1e-5
+
+
+# ---------------------------------------------------------------- cross-entropy
+@pytest.mark.parametrize("rows,V", [(1, 16), (81, 16), (512, 4096), (37, 1000)])
+@pytest.mark.parametrize("masked", [False, True])
+def test_ce(rows, V, masked):
+    logits = rnd(15, rows, V, scale=3.0)
+    tgt = np.random.default_rng(16).integers(0, V, rows).astype(np.int32)
+    wm = None
+    if masked:
+        wm = np.random.default_rng(17).uniform(0.5, 2.0, rows).astype(np.float32)
+        wm[::3] = 0.0
+        if rows == 1:
+            wm[0] = 1.5
+    rloss, rprobs, cnt = O.ce_fwd(logits, tgt, wm)
+    dlg, dtg, dwm = up(logits), up(tgt), up(wm)
+    loss, probs = D.empty(1), D.empty((rows, V))
+    ncmhip.call("ce_fwd", dlg, dtg, dwm, loss, probs, rows, V)
+    assert maxrel(probs.numpy(), rprobs) <= 1e-6
+    assert abs(float(loss.numpy()[0]) - rloss) <= 1e-6 * (abs(rloss) + 1)
+    # backward from the oracle's probs: the same float/double operations
+    dl0 = rnd(18, rows, V)
+    rdl = O.ce_bwd(rprobs, tgt, wm, 0.7 / cnt, dl0)
+    dl = up(dl0)
+    ncmhip.call("ce_bwd", up(rprobs), dtg, dwm, dl, rows, V, 0.7 / cnt)
+    assert bits_equal(dl.numpy(), rdl)
+    # fused forward + backward
+    dl2, loss2 = up(dl0), D.empty(1)
+    ncmhip.call("ce_fwd_bwd", dlg, dtg, dwm, loss2, dl2, rows, V, 0.7)
+    assert np.max(np.abs(dl2.numpy() - rdl)) <= 1e-6
+    assert abs(float(loss2.numpy()[0]) - rloss) <= 1e-6 * (abs(rloss) + 1)
+
+
+# ---------------------------------------------------------------- optimizer
+def test_adamw_bitexact_over_steps():
+    n = 100003
+    p, m, v = rnd(19, n) * 0.02, np.zeros(n, np.float32), np.zeros(n, np.float32)
+    dp, dm, dv = up(p), up(m), up(v)
+    b1, b2, eps, wd = 0.9, 0.95, 1e-8, 0.1
+    for step in range(1, 4):
+        g = rnd(20 + step, n)
+        lr = 3e-4 * O.sched_cosine_warmup(step, 2, 10)
+        b1t, b2t = 1 - b1 ** step, 1 - b2 ** step
+        p, m, v = O.adamw(p, g, m, v, lr, b1, b2, b1t, b2t, eps, wd)
+        ncmhip.call("adamw_update", dp, up(g), dm, dv, n, lr, b1, b2, b1t, b2t, eps, wd)
+    assert bits_equal(dp.numpy(), p) and bits_equal(dm.numpy(), m) and bits_equal(dv.numpy(), v)
+
+
+def test_schedule_matches_oracle():
+    lib = ncmhip.load()
+    for step, w, t in [(0, 100, 1000), (50, 100, 1000), (100, 100, 1000), (777, 100, 1000), (1200, 100, 1000),
+                       (5, 0, 10)]:
+        assert lib.sched_cosine_warmup(step, w, t) == O.sched_cosine_warmup(step, w, t)
+
+
+@pytest.mark.parametrize("scale", [1.0, 1e-4])
+def test_grad_clip(scale):
+    gs = [rnd(30, 1000) * scale, rnd(31, 768, 3) * scale, rnd(32, 5) * scale, np.zeros(0, np.float32)]
+    gn, ref = O.grad_clip(gs, 1.0)
+    bufs = [D.from_numpy(g) if g.size else None for g in gs]
+    ptrs = (ctypes.c_void_p * 4)(*[b.ptr if b else None for b in bufs])
+    ns = (ctypes.c_int64 * 4)(*[g.size for g in gs])
+    got = ncmhip.call("grad_clip_global", ptrs, ns, 4, 1.0)
+    assert abs(got - gn) <= 1e-12 * gn
+    for b, r in zip(bufs, ref):
+        if b is not None:
+            assert maxrel(b.numpy(), r) <= 2e-7
+
+
+# ---------------------------------------------------------------- attention
+def causal(Tq, Tkv):
+    return np.where(np.arange(Tkv)[None, :] > np.arange(Tq)[:, None] + (Tkv - Tq), -1e9, 0).astype(np.float32)
+
+
+@pytest.mark.parametrize("B,H,Hkv,Tq,Tkv,hd,masked", [
+    (2, 12, 12, 128, 128, 64, True),    # GPT-2 heads
+    (1, 14, 2, 81, 84, 64, False),
+    (1, 4, 2, 81, 81, 64, True),        # NCP heads, Tkv % 4 != 0 (row kernel)
+    (2, 3, 3, 17, 40, 32, True),
+])
+def test_sdpa_probs(B, H, Hkv, Tq, Tkv, hd, masked):
+    q, k = rnd(40, B, H, Tq, hd), rnd(41, B, Hkv, Tkv, hd)
+    mask = causal(Tq, Tkv) if masked else None
+    ref = O.sdpa_probs(q, k, mask)
+    P = D.empty(ref.shape)
+    ncmhip.call("sdpa_probs_gqa", up(q), up(k), up(mask), P, B, H, Hkv, Tq, Tkv, hd)
+    assert np.max(np.abs(P.numpy() - ref)) <= 1e-6
+
+
+@pytest.mark.parametrize("B,H,Hkv,Tq,Tkv,hd", [
+    (2, 12, 12, 256, 256, 64),          # GPT-2 heads (MFMA path)
+    (1, 14, 2, 128, 128, 64),           # Qwen heads, GQA fan-in
+    (1, 4, 2, 81, 81, 64),              # NCP heads: Tkv % 4 != 0 -> row kernels
+    (1, 4, 4, 70, 100, 64),             # ragged tiles, Tq != Tkv
+    (2, 6, 3, 33, 33, 32),              # generic head size
+    (1, 2, 1, 9, 20, 128),
+])
+def test_sdpa_bwd(B, H, Hkv, Tq, Tkv, hd):
+    q, k, v = rnd(42, B, H, Tq, hd), rnd(43, B, Hkv, Tkv, hd), rnd(44, B, Hkv, Tkv, hd)
+    dO = rnd(45, B, H, Tq, hd)
+    P = O.sdpa_probs(q, k, causal(Tq, Tkv))
+    dq0, dk0, dv0 = rnd(46, *q.shape), rnd(47, *k.shape), rnd(48, *v.shape)
+    rdq, rdk, rdv = O.sdpa_bwd(q, k, v, P, dO, dq0, dk0, dv0)
+    dq, dk, dv = up(dq0), up(dk0), up(dv0)
+    ncmhip.call("sdpa_bwd_gqa", up(q), up(k), up(v), up(P), up(dO), dq, dk, dv, B, H, Hkv, Tq, Tkv, hd)
+    for got, ref in ((dq, rdq), (dk, rdk), (dv, rdv)):
+        g = got.numpy()
+        assert np.max(np.abs(g - ref)) <= 1e-4 and maxrel(g, ref) <= 1e-4
+
+
+def test_sdpa_bwd_partial_outputs():
+    B, H, Hkv, T, hd = 1, 4, 2, 64, 64
+    q, k, v, dO = rnd(50, B, H, T, hd), rnd(51, B, Hkv, T, hd), rnd(52, B, Hkv, T, hd), rnd(53, B, H, T, hd)
+    P = O.sdpa_probs(q, k, None)
+    rdq, rdk, rdv = O.sdpa_bwd(q, k, v, P, dO)
+    dv = D.from_numpy(np.zeros_like(v))
+    ncmhip.call("sdpa_bwd_gqa", up(q), up(k), up(v), up(P), up(dO), None, None, dv, B, H, Hkv, T, T, hd)
+    assert np.max(np.abs(dv.numpy() - rdv)) <= 1e-4
+    dq = D.from_numpy(np.zeros_like(q))
+    ncmhip.call("sdpa_bwd_gqa", up(q), up(k), up(v), up(P), up(dO), dq, None, None, B, H, Hkv, T, T, hd)
+    assert np.max(np.abs(dq.numpy() - rdq)) <= 1e-4

@@ -246,6 +246,109 @@ double sched_cosine_warmup(long step, double warmup, double total);
  * it exceeds max_norm; -1 on error.  Synchronises the library stream. */
 double grad_clip_global(float *const *grads, const int64_t *sizes, int count, double max_norm);
 
+/* replaces the TOP_GELU / TOP_SILU / TOP_GELU_TANH backward,
+ * train_tape.c:830-873 / k_gelu_bwd, k_gelu_tanh_bwd: dx += dy * f'(x) */
+void gelu_bwd(const float *x, const float *dy, float *dx, int64_t n);
+void silu_bwd(const float *x, const float *dy, float *dx, int64_t n);
+void gelu_tanh_bwd(const float *x, const float *dy, float *dx, int64_t n);
+/* replaces the TOP_MUL backward, train_tape.c:1254-1268 (da or db may be NULL) */
+void mul_bwd(const float *a, const float *b, const float *dy, float *da, float *db, int64_t n);
+/* replaces the TOP_ROPE backward, train_tape.c:890-930 / k_rope_bwd: gq, gk are
+ * the gradients of the rotated q [B][H][T][hd] and k [B][Hkv][T][hd]. */
+void rope_bwd_gqa(const float *gq, const float *gk, const float *cos, const float *sin, float *dxq, float *dxk,
+                  int B, int H, int Hkv, int T, int hd);
+/* replaces the TOP_EMBED backward, train_tape.c:726-741: idx are HOST ints
+ * (the tape keeps them on the host); dW [V][D] accumulates, bit-exact. */
+void embedding_bwd(const float *dy, const int *idx, int64_t n, int D, float *dW, int V);
+/* replaces the TOP_SPLIT backward, train_tape.c:1293-1328 (any of gq/gk/gv NULL) */
+void qkv_split_bwd(const float *gq, const float *gk, const float *gv, float *dx,
+                   int B, int T, int C, int H, int hd, int K, int rep);
+/* replaces the TOP_MERGE / TOP_HEADSPLIT backward, train_tape.c:1329-1350 */
+void head_merge_bwd(const float *dy, float *dctx, int B, int T, int C, int H, int hd);
+void heads_transpose_bwd(const float *dy, float *dx, int B, int T, int C, int H, int hd);
+
+/* ------------------------------------------------------------------ */
+/* device tape                                                         */
+/* ------------------------------------------------------------------ */
+
+/* Replaces the reference's Tape for the hot-path ops (train_tape.c:19-162,
+ * 277-481, 636-1051; ncm.h:468-522): recorders run the forward on the device
+ * and record; ncm_tape_backward accumulates every gradient on the device.
+ * Prefixed names, so the library can be linked next to the reference's
+ * train_tape.c. */
+typedef struct NcmTape NcmTape;
+/* same layout as the reference's PMap (ncm.h:513-518): params[i]'s gradient
+ * accumulates into grads[i] (device buffers of sizes[i] floats) */
+typedef struct {
+    float **params;
+    float **grads;
+    int64_t *sizes;
+    int n;
+} NcmPMap;
+
+NcmTape *ncm_tape_new(void);                       /* tape_new, train_tape.c:59 */
+void ncm_tape_free(NcmTape *t);                    /* tape_free, :83 */
+void ncm_tape_clear(NcmTape *t);                   /* tape_clear, :84 */
+int ncm_tape_size(const NcmTape *t);               /* number of records */
+/* tape_backward, train_tape.c:545-556 (the device path, all on the GPU) */
+void ncm_tape_backward(NcmTape *t, const NcmPMap *pm);
+/* gradient accumulated for `key` by the last backward (NULL if none) */
+float *ncm_tape_grad(NcmTape *t, const float *key);
+/* recorders: t_linear :156, t_embed :164 (idx HOST ints), t_layernorm :176,
+ * t_layernorm_eps :186, t_rmsnorm :194, t_gelu :209, t_gelu_tanh :217,
+ * t_silu :223, t_mul :229, t_rope :260, t_sdpa :277, t_add :361,
+ * t_scale :367, t_qkvsplit :386, t_headmerge :397, t_headsplit :405,
+ * t_ce :442 (tgt, wmask HOST arrays; loss a device float; probs optional). */
+void ncm_t_linear(NcmTape *t, const float *x, const float *W, const float *b, float *y, int64_t batch, int M, int K);
+void ncm_t_embed(NcmTape *t, const float *W, const int *idx, int V, float *y, int64_t n, int D);
+void ncm_t_layernorm(NcmTape *t, const float *x, const float *w, const float *b, float *y, int64_t rows, int C);
+void ncm_t_layernorm_eps(NcmTape *t, const float *x, const float *w, const float *b, float *y, int64_t rows, int C,
+                         double eps);
+void ncm_t_rmsnorm(NcmTape *t, const float *x, const float *w, float *y, int64_t rows, int C);
+void ncm_t_gelu(NcmTape *t, const float *x, float *y, int64_t n);
+void ncm_t_gelu_tanh(NcmTape *t, const float *x, float *y, int64_t n);
+void ncm_t_silu(NcmTape *t, const float *x, float *y, int64_t n);
+void ncm_t_mul(NcmTape *t, const float *a, const float *b, float *y, int64_t n);
+void ncm_t_add(NcmTape *t, const float *a, const float *b, float *y, int64_t n);
+void ncm_t_scale(NcmTape *t, const float *x, float s, float *y, int64_t n);
+void ncm_t_rope(NcmTape *t, const float *xq, const float *xk, float *yq, float *yk, const float *cos,
+                const float *sin, int B, int H, int Hkv, int T, int hd);
+void ncm_t_sdpa(NcmTape *t, const float *q, const float *k, const float *v, const float *mask, float *o,
+                int B, int H, int Hkv, int Tq, int Tkv, int hd);
+void ncm_t_qkvsplit(NcmTape *t, const float *in, float *qq, float *kk, float *vv, int B, int T, int C, int H, int hd,
+                    int K, int rep);
+void ncm_t_headmerge(NcmTape *t, const float *ctx, float *out, int B, int T, int C, int H, int hd);
+void ncm_t_headsplit(NcmTape *t, const float *in, float *out, int B, int T, int C, int H, int hd);
+void ncm_t_ce(NcmTape *t, const float *logits, const int *tgt, const float *wmask, float *loss, float *probs,
+              int64_t rows, int V, double weight);
+
+/* ------------------------------------------------------------------ */
+/* config-5 driver: the taped GPT-2 training step of train_gpt2.c      */
+/* ------------------------------------------------------------------ */
+
+typedef struct {
+    int n_layer, n_embd, n_head, vocab, n_pos;
+} NcmGpt2Config;
+
+/* flat parameter order: 0 wte [vocab][C], 1 wpe [n_pos][C], then per layer
+ * l (base 2 + 12 l): ln_1.weight, ln_1.bias, attn.c_attn.weight [3C][C],
+ * attn.c_attn.bias, attn.c_proj.weight [C][C], attn.c_proj.bias, ln_2.weight,
+ * ln_2.bias, mlp.c_fc.weight [4C][C], mlp.c_fc.bias, mlp.c_proj.weight
+ * [C][4C], mlp.c_proj.bias; last two ln_f.weight, ln_f.bias. */
+int ncm_gpt2_param_count(const NcmGpt2Config *c);
+/* elements of parameter i (rows x cols written when non-NULL), -1 if out of range */
+int64_t ncm_gpt2_param_shape(const NcmGpt2Config *c, int i, int64_t *rows, int64_t *cols);
+/* train_gpt2_forward (train_gpt2.c:107-147) on the device tape: ids HOST
+ * [B][T] -> logits [B*T][vocab] in the arena (arena_init first). */
+float *ncm_gpt2_forward(NcmTape *t, const NcmGpt2Config *c, float *const *params, const int *ids, int B, int T);
+/* train_gpt2_step (train_gpt2.c:149-180) + adamw_step (train.c:102-145):
+ * forward, mean CE on xout, backward, clip 1.0, AdamW (betas 0.9/0.95,
+ * eps 1e-8, decay wd, lr = base_lr * sched_cosine_warmup(step, ...)).
+ * grads zero on entry and exit.  Returns the loss (-1 on error). */
+float ncm_gpt2_train_step(NcmTape *t, const NcmGpt2Config *c, float *const *params, float *const *grads,
+                          float *const *m, float *const *v, const int *xin, const int *xout, int B, int T, long step,
+                          double base_lr, double warmup, double total, double wd, double *gnorm_out);
+
 /* ------------------------------------------------------------------ */
 /* greedy id                                                           */
 /* ------------------------------------------------------------------ */

@@ -641,3 +641,109 @@ void orc_sdpa_bwd(const float *q, const float *k, const float *v, const float *P
     }
     free(ds);
 }
+
+/* train_tape.c:830-873 TOP_GELU / TOP_SILU / TOP_GELU_TANH backward:
+ * dx += (float)(dy * g(x)) with g in fp64.  kind: 0 gelu (erf), 1 silu,
+ * 2 gelu_tanh. */
+void orc_act_bwd(const float *x, const float *dy, float *dx, int64_t n, int kind) {
+    const double s2 = 1.4142135623730951, ip = 0.3989422804014327;
+    const double c0 = 0.7978845608028654, c1 = 0.044715;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; i++) {
+        double g;
+        if (kind == 0) {
+            double e = erf(x[i] / s2);
+            g = 0.5 * (1 + e) + x[i] * exp(-0.5 * x[i] * x[i]) * ip;
+        } else if (kind == 1) {
+            double s = 1.0 / (1.0 + exp(-x[i]));
+            g = s * (1 + x[i] * (1 - s));
+        } else {
+            double xv = x[i];
+            double u = c0 * (xv + c1 * xv * xv * xv);
+            double th = tanh(u);
+            g = 0.5 * (1.0 + th) + 0.5 * xv * (1.0 - th * th) * c0 * (1.0 + 3.0 * c1 * xv * xv);
+        }
+        dx[i] += (float)(dy[i] * g);
+    }
+}
+
+/* train_tape.c:1254-1268 TOP_MUL: da += dy*b, db += dy*a in float */
+void orc_mul_bwd(const float *a, const float *b, const float *dy, float *da, float *db, int64_t n) {
+    for (int64_t i = 0; i < n; i++) {
+        if (da) da[i] += dy[i] * b[i];
+        if (db) db[i] += dy[i] * a[i];
+    }
+}
+
+/* train_tape.c:890-930 TOP_ROPE: the transposed rotation in fp64, per row of
+ * hd (position row % T). */
+void orc_rope_bwd(const float *g, const float *cos_t, const float *sin_t, float *dx, int64_t rows, int T, int hd) {
+    int h = hd / 2;
+#pragma omp parallel for schedule(static)
+    for (int64_t rr = 0; rr < rows; rr++) {
+        int t = (int)(rr % T);
+        for (int d = 0; d < h; d++) {
+            double g0 = g[rr * hd + d], g1 = g[rr * hd + h + d];
+            double c0 = cos_t[t * hd + d], s0 = sin_t[t * hd + d];
+            double c1 = cos_t[t * hd + h + d], s1 = sin_t[t * hd + h + d];
+            dx[rr * hd + d] += (float)(g0 * c0 + g1 * s1);
+            dx[rr * hd + h + d] += (float)(-g0 * s0 + g1 * c1);
+        }
+    }
+}
+
+/* train_tape.c:726-741 TOP_EMBED: per id a float sum of dy rows in
+ * ascending row order, then float-added into dW; ids outside [0, V) skipped. */
+void orc_embedding_bwd(const float *dy, const int *idx, int64_t n, int D, float *dW, int V) {
+    float *acc = (float *)calloc((size_t)V * D, sizeof(float));
+    for (int64_t i = 0; i < n; i++) {
+        int id = idx[i];
+        if (id < 0 || id >= V) continue;
+        for (int d = 0; d < D; d++) acc[(size_t)id * D + d] += dy[i * D + d];
+    }
+    for (int64_t j = 0; j < (int64_t)V * D; j++) dW[j] += acc[j];
+    free(acc);
+}
+
+/* train_tape.c:1293-1328 TOP_SPLIT: q grads copied back into the fused row;
+ * k/v grads summed over the query heads of each kv head (float, ascending h). */
+void orc_qkv_split_bwd(const float *gq, const float *gk, const float *gv, float *dx, int B, int T, int C, int H,
+                       int hd, int K, int rep) {
+    int64_t row = (int64_t)C + 2 * K * hd;
+    for (int b = 0; b < B; b++)
+        for (int t = 0; t < T; t++) {
+            float *dr = dx + ((int64_t)b * T + t) * row;
+            if (gq)
+                for (int h = 0; h < H; h++)
+                    for (int d = 0; d < hd; d++) dr[h * hd + d] += gq[(((int64_t)b * H + h) * T + t) * hd + d];
+            for (int kvh = 0; kvh < K; kvh++)
+                for (int d = 0; d < hd; d++) {
+                    float sk = 0, sv = 0;
+                    for (int h = kvh * rep; h < (kvh + 1) * rep && h < H; h++) {
+                        int64_t o = (((int64_t)b * H + h) * T + t) * hd + d;
+                        if (gk) sk += gk[o];
+                        if (gv) sv += gv[o];
+                    }
+                    if (gk) dr[C + kvh * hd + d] += sk;
+                    if (gv) dr[C + K * hd + kvh * hd + d] += sv;
+                }
+        }
+}
+
+/* train_tape.c:1329-1338 TOP_MERGE: dctx[b,h,t,d] += dy[b,t,h*hd+d] */
+void orc_head_merge_bwd(const float *dy, float *dctx, int B, int T, int C, int H, int hd) {
+    for (int b = 0; b < B; b++)
+        for (int t = 0; t < T; t++)
+            for (int h = 0; h < H; h++)
+                for (int d = 0; d < hd; d++)
+                    dctx[(((int64_t)b * H + h) * T + t) * hd + d] += dy[((int64_t)b * T + t) * C + h * hd + d];
+}
+
+/* train_tape.c:1339-1350 TOP_HEADSPLIT: dx[b,t,h*hd+d] += dy[b,h,t,d] */
+void orc_heads_transpose_bwd(const float *dy, float *dx, int B, int T, int C, int H, int hd) {
+    for (int b = 0; b < B; b++)
+        for (int t = 0; t < T; t++)
+            for (int h = 0; h < H; h++)
+                for (int d = 0; d < hd; d++)
+                    dx[((int64_t)b * T + t) * C + h * hd + d] += dy[(((int64_t)b * H + h) * T + t) * hd + d];
+}

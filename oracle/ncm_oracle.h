@@ -81,6 +81,17 @@ void orc_sdpa_probs(const float *q, const float *k, const float *mask, float *P,
 void orc_sdpa_bwd(const float *q, const float *k, const float *v, const float *P, const float *dy, float *dq,
                   float *dk, float *dv, int B, int H, int Hkv, int Tq, int Tkv, int hd);
 
+/* src/train_tape.c:830-873 activation backward (kind 0 gelu, 1 silu, 2 gelu_tanh),
+ * :1254-1268 mul, :890-930 rope, :726-741 embedding, :1293-1350 split / merge / headsplit */
+void orc_act_bwd(const float *x, const float *dy, float *dx, int64_t n, int kind);
+void orc_mul_bwd(const float *a, const float *b, const float *dy, float *da, float *db, int64_t n);
+void orc_rope_bwd(const float *g, const float *cos_t, const float *sin_t, float *dx, int64_t rows, int T, int hd);
+void orc_embedding_bwd(const float *dy, const int *idx, int64_t n, int D, float *dW, int V);
+void orc_qkv_split_bwd(const float *gq, const float *gk, const float *gv, float *dx, int B, int T, int C, int H,
+                       int hd, int K, int rep);
+void orc_head_merge_bwd(const float *dy, float *dctx, int B, int T, int C, int H, int hd);
+void orc_heads_transpose_bwd(const float *dy, float *dx, int B, int T, int C, int H, int hd);
+
 /* src/kernels.c:774-780 rng_next (xorshift64*) and the ktest generator of
  * tests/ktest_kernels.c:8-12, for seeded inputs shared with the reference. */
 uint64_t orc_rng_next(uint64_t *state);

@@ -72,6 +72,13 @@ def lib():
             "orc_grad_clip": (ctypes.c_double, [ctypes.POINTER(vp), ctypes.POINTER(i64), ci, ctypes.c_double]),
             "orc_sdpa_probs": (None, [vp, vp, vp, vp, ci, ci, ci, ci, ci, ci]),
             "orc_sdpa_bwd": (None, [vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, ci]),
+            "orc_act_bwd": (None, [vp, vp, vp, i64, ci]),
+            "orc_mul_bwd": (None, [vp, vp, vp, vp, vp, i64]),
+            "orc_rope_bwd": (None, [vp, vp, vp, vp, i64, ci, ci]),
+            "orc_embedding_bwd": (None, [vp, vp, i64, ci, vp, ci]),
+            "orc_qkv_split_bwd": (None, [vp, vp, vp, vp] + [ci] * 7),
+            "orc_head_merge_bwd": (None, [vp, vp] + [ci] * 5),
+            "orc_heads_transpose_bwd": (None, [vp, vp] + [ci] * 5),
         }
         for n, (r, a) in sigs.items():
             f = getattr(L, n)
@@ -325,6 +332,61 @@ def sdpa_bwd(q, k, v, P, dy, dq0=None, dk0=None, dv0=None):
     return dq, dk, dv
 
 
+ACT_BWD = {"gelu": 0, "silu": 1, "gelu_tanh": 2}
+
+
+def act_bwd(name, x, dy, dx0=None):
+    x, dy = _f32(x), _f32(dy)
+    dx = _grad(dx0, x.shape)
+    lib().orc_act_bwd(_ptr(x), _ptr(dy), _ptr(dx), x.size, ACT_BWD[name])
+    return dx
+
+
+def mul_bwd(a, b, dy, da0=None, db0=None):
+    a, b, dy = _f32(a), _f32(b), _f32(dy)
+    da, db = _grad(da0, a.shape), _grad(db0, b.shape)
+    lib().orc_mul_bwd(_ptr(a), _ptr(b), _ptr(dy), _ptr(da), _ptr(db), a.size)
+    return da, db
+
+
+def rope_bwd(g, cos_t, sin_t, T, dx0=None):
+    """g: [rows, hd] gradient of the rotated rows (position row % T)."""
+    g = _f32(g)
+    dx = _grad(dx0, g.shape)
+    lib().orc_rope_bwd(_ptr(g), _ptr(_f32(cos_t)), _ptr(_f32(sin_t)), _ptr(dx), g.shape[0], T, g.shape[1])
+    return dx
+
+
+def embedding_bwd(dy, idx, V, dW0=None):
+    dy = _f32(dy)
+    idx = np.ascontiguousarray(idx, np.int32)
+    D = dy.shape[1]
+    dW = _grad(dW0, (V, D))
+    lib().orc_embedding_bwd(_ptr(dy), _ptr(idx), idx.size, D, _ptr(dW), V)
+    return dW
+
+
+def qkv_split_bwd(gq, gk, gv, B, T, C, H, hd, K, rep, dx0=None):
+    gq, gk, gv = [None if g is None else _f32(g) for g in (gq, gk, gv)]
+    dx = _grad(dx0, (B, T, C + 2 * K * hd))
+    lib().orc_qkv_split_bwd(_ptr(gq), _ptr(gk), _ptr(gv), _ptr(dx), B, T, C, H, hd, K, rep)
+    return dx
+
+
+def head_merge_bwd(dy, B, T, C, H, hd, dx0=None):
+    dy = _f32(dy)
+    dx = _grad(dx0, (B, H, T, hd))
+    lib().orc_head_merge_bwd(_ptr(dy), _ptr(dx), B, T, C, H, hd)
+    return dx
+
+
+def heads_transpose_bwd(dy, B, T, C, H, hd, dx0=None):
+    dy = _f32(dy)
+    dx = _grad(dx0, (B, T, C))
+    lib().orc_heads_transpose_bwd(_ptr(dy), _ptr(dx), B, T, C, H, hd)
+    return dx
+
+
 def ktest_fill(state, n):
     """tests/ktest_kernels.c:8-12 generator; returns (values, new_state)."""
     st = ctypes.c_uint64(state)
@@ -371,6 +433,12 @@ def ref():
             "refg_rmsn_bwd": (None, [vp, vp, vp, vp, vp, vp, ctypes.c_longlong, ci]),
             "refg_ce": (None, [vp, vp, vp, vp, vp, vp, ctypes.c_longlong, ci, ctypes.c_double]),
             "refg_sdpa_bwd": (None, [vp] * 10 + [ci] * 6),
+            "refg_act_bwd": (None, [ci, vp, vp, vp, vp, ctypes.c_longlong]),
+            "refg_mul_bwd": (None, [vp] * 6 + [ctypes.c_longlong]),
+            "refg_rope_bwd": (None, [vp] * 10 + [ci] * 5),
+            "refg_embed_bwd": (None, [vp, vp, ci, vp, vp, vp, ctypes.c_longlong, ci]),
+            "refg_split_bwd": (None, [vp] * 8 + [ci] * 7),
+            "refg_merge_bwd": (None, [ci, vp, vp, vp, vp] + [ci] * 5),
         }
         for n, (r, a) in sigs.items():
             f = getattr(L, n)
@@ -480,3 +548,189 @@ def ref_sdpa_bwd(q, k, v, mask, dy):
     ref().refg_sdpa_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(m), _ptr(dy), _ptr(o), _ptr(dq), _ptr(dk), _ptr(dv),
                         _ptr(P), B, H, Hkv, Tq, Tkv, hd)
     return o, P, dq, dk, dv
+
+
+def ref_act_bwd(name, x, dy, dx0=None):
+    x, dy = _f32(x), _f32(dy)
+    y = np.empty_like(x)
+    dx = _grad(dx0, x.shape)
+    ref().refg_act_bwd(ACT_BWD[name], _ptr(x), _ptr(dy), _ptr(y), _ptr(dx), x.size)
+    return dx
+
+
+def ref_mul_bwd(a, b, dy, da0=None, db0=None):
+    a, b, dy = _f32(a), _f32(b), _f32(dy)
+    y = np.empty_like(a)
+    da, db = _grad(da0, a.shape), _grad(db0, b.shape)
+    ref().refg_mul_bwd(_ptr(a), _ptr(b), _ptr(dy), _ptr(y), _ptr(da), _ptr(db), a.size)
+    return da, db
+
+
+def ref_rope_bwd(xq, xk, cos_t, sin_t, gq, gk):
+    xq, xk, gq, gk = _f32(xq), _f32(xk), _f32(gq), _f32(gk)
+    B, H, T, hd = xq.shape
+    Hkv = xk.shape[1]
+    yq, yk = np.empty_like(xq), np.empty_like(xk)
+    dxq, dxk = np.zeros_like(xq), np.zeros_like(xk)
+    ref().refg_rope_bwd(_ptr(xq), _ptr(xk), _ptr(_f32(cos_t)), _ptr(_f32(sin_t)), _ptr(gq), _ptr(gk), _ptr(yq),
+                        _ptr(yk), _ptr(dxq), _ptr(dxk), B, H, Hkv, T, hd)
+    return dxq, dxk
+
+
+def ref_embed_bwd(W, idx, dy, dW0=None):
+    W, dy = _f32(W), _f32(dy)
+    idx = np.ascontiguousarray(idx, np.int32)
+    V, D = W.shape
+    y = np.empty((idx.size, D), np.float32)
+    dW = _grad(dW0, W.shape)
+    ref().refg_embed_bwd(_ptr(W), _ptr(idx), V, _ptr(dy), _ptr(y), _ptr(dW), idx.size, D)
+    return dW
+
+
+def ref_split_bwd(x, gq, gk, gv, B, T, C, H, hd, K, rep):
+    x = _f32(x)
+    gq, gk, gv = [None if g is None else _f32(g) for g in (gq, gk, gv)]
+    qq, kk, vv = [np.empty((B, H, T, hd), np.float32) for _ in range(3)]
+    dx = np.zeros_like(x)
+    ref().refg_split_bwd(_ptr(x), _ptr(gq), _ptr(gk), _ptr(gv), _ptr(qq), _ptr(kk), _ptr(vv), _ptr(dx),
+                         B, T, C, H, hd, K, rep)
+    return dx
+
+
+def ref_merge_bwd(kind, x, dy, B, T, C, H, hd):
+    """kind 0: head_merge (x [B,H,T,hd]); kind 1: head split (x [B,T,C])."""
+    x, dy = _f32(x), _f32(dy)
+    y = np.empty_like(dy)
+    dx = np.zeros_like(x)
+    ref().refg_merge_bwd(kind, _ptr(x), _ptr(dy), _ptr(y), _ptr(dx), B, T, C, H, hd)
+    return dx
+
+
+# ---- config 5: the taped GPT-2 step (train_gpt2.c:42-180) restated ----
+GPT2_BLOCK = ("ln_1.weight", "ln_1.bias", "attn.c_attn.weight", "attn.c_attn.bias", "attn.c_proj.weight",
+              "attn.c_proj.bias", "ln_2.weight", "ln_2.bias", "mlp.c_fc.weight", "mlp.c_fc.bias",
+              "mlp.c_proj.weight", "mlp.c_proj.bias")
+
+
+def gpt2_shapes(n_layer, C, V, npos):
+    shapes = [(V, C), (npos, C)]
+    per = [(C,), (C,), (3 * C, C), (3 * C,), (C, C), (C,), (C,), (C,), (4 * C, C), (4 * C,), (C, 4 * C), (C,)]
+    for _ in range(n_layer):
+        shapes += per
+    return shapes + [(C,), (C,)]
+
+
+def gpt2_grads(params, n_layer, C, H, V, npos, ids, tgt):
+    """Forward of train_gpt2_forward, mean CE on tgt, and the host tape
+    backward (train_tape.c:636-1051) over the same records in reverse, every
+    op the pinned oracle function of the tape case it follows.  Returns
+    (loss, grads in parameter order)."""
+    ids = np.ascontiguousarray(ids, np.int32)
+    B, T = ids.shape
+    R, hd = B * T, C // H
+    P = [_f32(p) for p in params]
+    tape = []
+
+    def rec(op, out, *ins, **kw):
+        tape.append((op, out, ins, kw))
+        return out
+
+    pos = np.tile(np.arange(T, dtype=np.int32), B)
+    xe = rec("embed", embedding(P[0], ids.reshape(-1)), 0, ids.reshape(-1), V)
+    pe = rec("embed", embedding(P[1], pos), 1, pos, npos)
+    h = rec("add", xe + pe, xe, pe)
+    mask = np.where(np.arange(T)[None, :] <= np.arange(T)[:, None], 0.0, -1e9).astype(np.float32)
+    for li in range(n_layer):
+        w = list(range(2 + 12 * li, 14 + 12 * li))
+        x = h
+        ln = rec("ln", layernorm(x, P[w[0]], P[w[1]], eps=np.float32(1e-5)), x, w[0], w[1])
+        qkv = rec("linear", linear_fwd(ln, P[w[2]], P[w[3]]), ln, w[2], w[3])
+        q, k, v = qkv_split(qkv.reshape(B, T, 3 * C), B, T, C, H, hd, H, 1)
+        tape.append(("split", (q, k, v), (qkv,), {}))
+        Pm = sdpa_probs(q, k, mask)
+        ctx = rec("sdpa", sdpa_gqa(q, k, v, mask), q, k, v, P=Pm)
+        mo = rec("merge", head_merge(ctx, B, T, C, H, hd).reshape(R, C), ctx)
+        ao = rec("linear", linear_fwd(mo, P[w[4]], P[w[5]]), mo, w[4], w[5])
+        x1 = rec("add", x + ao, x, ao)
+        mn = rec("ln", layernorm(x1, P[w[6]], P[w[7]], eps=np.float32(1e-5)), x1, w[6], w[7])
+        mm = rec("linear", linear_fwd(mn, P[w[8]], P[w[9]]), mn, w[8], w[9])
+        m2 = rec("gelu_tanh", act("gelu_tanh", mm), mm)
+        mlpo = rec("linear", linear_fwd(m2, P[w[10]], P[w[11]]), m2, w[10], w[11])
+        h = rec("add", x1 + mlpo, x1, mlpo)
+    n = len(P)
+    lnf = rec("ln", layernorm(h, P[n - 2], P[n - 1], eps=np.float32(1e-5)), h, n - 2, n - 1)
+    logits = rec("linear", linear_fwd(lnf, P[0], None), lnf, 0, None)
+    loss, probs, cnt = ce_fwd(logits, tgt.reshape(-1))
+    grads = [np.zeros_like(p) for p in P]
+    g = {id(logits): ce_bwd(probs, tgt.reshape(-1), None, 1.0 / cnt)}
+
+    def gget(a):
+        if isinstance(a, int):
+            return grads[a]
+        if id(a) not in g:
+            g[id(a)] = np.zeros_like(a)
+        return g[id(a)]
+
+    def gset(a, val):
+        if isinstance(a, int):
+            grads[a][...] = val
+        else:
+            g[id(a)] = val
+
+    for op, out, ins, kw in reversed(tape):
+        if op == "split":
+            gq, gk, gv = (g.get(id(o)) for o in out)
+            if gq is None and gk is None and gv is None:
+                continue
+            (a,) = ins
+            gset(a, qkv_split_bwd(gq, gk, gv, B, T, C, H, hd, H, 1, gget(a).reshape(B, T, -1)).reshape(a.shape))
+            continue
+        dy = g.get(id(out))
+        if dy is None:
+            continue
+        if op == "embed":
+            wi, idx, VV = ins
+            gset(wi, embedding_bwd(dy, idx, VV, gget(wi)))
+        elif op == "add":
+            a, b = ins
+            gset(a, gget(a) + dy)
+            gset(b, gget(b) + dy)
+        elif op == "ln":
+            x, wi, bi = ins
+            dx, dw, db = layernorm_bwd(x, P[wi], dy, gget(x), gget(wi), gget(bi), eps=1e-5)
+            gset(x, dx); gset(wi, dw); gset(bi, db)
+        elif op == "linear":
+            x, wi, bi = ins
+            want = ("dx", "dW", "db") if bi is not None else ("dx", "dW")
+            dx, dW, db = linear_bwd(x, P[wi], dy, gget(x), gget(wi), gget(bi) if bi is not None else None, want)
+            gset(x, dx); gset(wi, dW)
+            if bi is not None:
+                gset(bi, db)
+        elif op == "sdpa":
+            q, k, v = ins
+            dq, dk, dv = sdpa_bwd(q, k, v, kw["P"], dy, gget(q), gget(k), gget(v))
+            gset(q, dq); gset(k, dk); gset(v, dv)
+        elif op == "merge":
+            (a,) = ins
+            gset(a, head_merge_bwd(dy.reshape(B, T, C), B, T, C, H, hd, gget(a)))
+        elif op == "gelu_tanh":
+            (a,) = ins
+            gset(a, act_bwd("gelu_tanh", a, dy, gget(a)))
+    return loss, grads
+
+
+def ref_gpt2_grads(params, n_layer, C, H, V, npos, ids, tgt):
+    """The reference's own taped step (libref): (loss, grads)."""
+    P = [_f32(p) for p in params]
+    G = [np.zeros_like(p) for p in P]
+    ids = np.ascontiguousarray(ids, np.int32)
+    tgt = np.ascontiguousarray(tgt, np.int32)
+    B, T = ids.shape
+    L = ref()
+    f = L.refg_gpt2_grads
+    f.restype = ctypes.c_float
+    f.argtypes = [ctypes.POINTER(vp), ctypes.POINTER(vp)] + [ci] * 5 + [vp, vp, ci, ci]
+    pp = (vp * len(P))(*[p.ctypes.data for p in P])
+    gp = (vp * len(G))(*[x.ctypes.data for x in G])
+    loss = f(pp, gp, n_layer, C, H, V, npos, _ptr(ids), _ptr(tgt), B, T)
+    return float(loss), G

@@ -180,3 +180,170 @@ void refg_sdpa_bwd(const float *q, const float *k, const float *v, const float *
     free(g);
     arena_reset();
 }
+
+/* kind 0 t_gelu, 1 t_silu, 2 t_gelu_tanh (train_tape.c:209-227) */
+void refg_act_bwd(int kind, const float *x, const float *dy, float *y, float *dx, long long n) {
+    Tape *t = tape_new();
+    float *g = (float *)malloc((size_t)(n > 0 ? n : 1) * sizeof(float));
+    memcpy(g, dy, (size_t)n * sizeof(float));
+    if (kind == 0) t_gelu(t, x, y, n);
+    else if (kind == 1) t_silu(t, x, y, n);
+    else t_gelu_tanh(t, x, y, n);
+    float *params[2] = {y, (float *)x};
+    float *grads[2] = {g, dx};
+    int64_t sizes[2] = {n, n};
+    run_tape(t, params, grads, sizes, 2);
+    tape_free(t);
+    free(g);
+}
+
+void refg_mul_bwd(const float *a, const float *b, const float *dy, float *y, float *da, float *db, long long n) {
+    Tape *t = tape_new();
+    float *g = (float *)malloc((size_t)(n > 0 ? n : 1) * sizeof(float));
+    memcpy(g, dy, (size_t)n * sizeof(float));
+    t_mul(t, a, b, y, n);
+    float *params[3] = {y, (float *)a, (float *)b};
+    float *grads[3] = {g, da, db};
+    int64_t sizes[3] = {n, n, n};
+    run_tape(t, params, grads, sizes, 3);
+    tape_free(t);
+    free(g);
+}
+
+/* t_rope (train_tape.c:260-275): out-of-place rope of xq, xk */
+void refg_rope_bwd(const float *xq, const float *xk, const float *cos_t, const float *sin_t, const float *gq,
+                   const float *gk, float *yq, float *yk, float *dxq, float *dxk, int B, int H, int Hkv, int T,
+                   int hd) {
+    Tape *t = tape_new();
+    int64_t nq = (int64_t)B * H * T * hd, nk = (int64_t)B * Hkv * T * hd;
+    float *g1 = (float *)malloc((size_t)nq * sizeof(float)), *g2 = (float *)malloc((size_t)nk * sizeof(float));
+    memcpy(g1, gq, (size_t)nq * sizeof(float));
+    memcpy(g2, gk, (size_t)nk * sizeof(float));
+    t_rope(t, xq, xk, yq, yk, cos_t, sin_t, B, H, Hkv, T, hd);
+    float *params[4] = {yq, yk, (float *)xq, (float *)xk};
+    float *grads[4] = {g1, g2, dxq, dxk};
+    int64_t sizes[4] = {nq, nk, nq, nk};
+    run_tape(t, params, grads, sizes, 4);
+    tape_free(t);
+    free(g1);
+    free(g2);
+}
+
+/* t_embed (train_tape.c:164-174); its index copy lives in the scratch arena */
+void refg_embed_bwd(const float *W, const int *idx, int V, const float *dy, float *y, float *dW, long long n,
+                    int D) {
+    ensure_arena();
+    arena_reset();
+    Tape *t = tape_new();
+    float *g = (float *)malloc((size_t)(n > 0 ? n : 1) * D * sizeof(float));
+    memcpy(g, dy, (size_t)n * D * sizeof(float));
+    t_embed(t, W, idx, V, y, n, D);
+    float *params[2] = {y, (float *)W};
+    float *grads[2] = {g, dW};
+    int64_t sizes[2] = {n * D, (int64_t)V * D};
+    run_tape(t, params, grads, sizes, 2);
+    tape_free(t);
+    free(g);
+    arena_reset();
+}
+
+void refg_split_bwd(const float *in, const float *gq, const float *gk, const float *gv, float *qq, float *kk,
+                    float *vv, float *dx, int B, int T, int C, int H, int hd, int K, int rep) {
+    Tape *t = tape_new();
+    int64_t no = (int64_t)B * H * T * hd, ni = (int64_t)B * T * (C + 2 * K * hd);
+    float *g[3];
+    const float *src[3] = {gq, gk, gv};
+    for (int i = 0; i < 3; i++) {
+        g[i] = src[i] ? (float *)malloc((size_t)no * sizeof(float)) : NULL;
+        if (g[i]) memcpy(g[i], src[i], (size_t)no * sizeof(float));
+    }
+    t_qkvsplit(t, in, qq, kk, vv, B, T, C, H, hd, K, rep);
+    float *params[4] = {qq, kk, vv, (float *)in};
+    float *grads[4] = {g[0], g[1], g[2], dx};
+    int64_t sizes[4] = {no, no, no, ni};
+    run_tape(t, params, grads, sizes, 4);
+    tape_free(t);
+    for (int i = 0; i < 3; i++) free(g[i]);
+}
+
+/* kind 0 t_headmerge, 1 t_headsplit */
+void refg_merge_bwd(int kind, const float *in, const float *dy, float *y, float *dx, int B, int T, int C, int H,
+                    int hd) {
+    Tape *t = tape_new();
+    int64_t nh = (int64_t)B * H * T * hd, nc = (int64_t)B * T * C;
+    int64_t ny = kind == 0 ? nc : nh, nx = kind == 0 ? nh : nc;
+    float *g = (float *)malloc((size_t)ny * sizeof(float));
+    memcpy(g, dy, (size_t)ny * sizeof(float));
+    if (kind == 0) t_headmerge(t, in, y, B, T, C, H, hd);
+    else t_headsplit(t, in, y, B, T, C, H, hd);
+    float *params[2] = {y, (float *)in};
+    float *grads[2] = {g, dx};
+    int64_t sizes[2] = {ny, nx};
+    run_tape(t, params, grads, sizes, 2);
+    tape_free(t);
+    free(g);
+}
+
+/* The reference's taped GPT-2 forward (train_gpt2.c:107-147) + t_ce + the
+ * host tape backward on a WeightStore built from flat host arrays in the
+ * order: wte, wpe, per layer the 12 h.<l>.* tensors, ln_f.weight,
+ * ln_f.bias.  Returns the mean loss; grads (zeroed by the caller, same
+ * order) receive dL/dparam before any clipping. */
+float refg_gpt2_grads(float *const *params, float *const *grads, int n_layer, int C, int H, int V, int npos,
+                      const int *ids, const int *tgt, int B, int T) {
+    static const char *names[12] = {"ln_1.weight", "ln_1.bias", "attn.c_attn.weight", "attn.c_attn.bias",
+                                    "attn.c_proj.weight", "attn.c_proj.bias", "ln_2.weight", "ln_2.bias",
+                                    "mlp.c_fc.weight", "mlp.c_fc.bias", "mlp.c_proj.weight", "mlp.c_proj.bias"};
+    const int n = 4 + 12 * n_layer;
+    ensure_arena();
+    arena_reset();
+    NCMConfig *c = (NCMConfig *)calloc(1, sizeof(NCMConfig));
+    c->n_layer = n_layer;
+    c->n_head = H;
+    c->n_embd = C;
+    WeightStore ws;
+    ws.count = n;
+    ws.items = (NamedTensor *)calloc((size_t)n, sizeof(NamedTensor));
+    Tensor *ts = (Tensor *)calloc((size_t)n, sizeof(Tensor));
+    int64_t *sizes = (int64_t *)calloc((size_t)n, sizeof(int64_t));
+    for (int i = 0; i < n; i++) {
+        int64_t r = C, k = 1;
+        if (i == 0) { r = V; k = C; }
+        else if (i == 1) { r = npos; k = C; }
+        else if (i < n - 2) {
+            int j = (i - 2) % 12;
+            if (j == 2) { r = 3 * C; k = C; }
+            else if (j == 3) { r = 3 * C; }
+            else if (j == 4) { r = C; k = C; }
+            else if (j == 8) { r = 4 * C; k = C; }
+            else if (j == 9) { r = 4 * C; }
+            else if (j == 10) { r = C; k = 4 * C; }
+        }
+        if (i == 0) snprintf(ws.items[i].name, sizeof(ws.items[i].name), "wte.weight");
+        else if (i == 1) snprintf(ws.items[i].name, sizeof(ws.items[i].name), "wpe.weight");
+        else if (i == n - 2) snprintf(ws.items[i].name, sizeof(ws.items[i].name), "ln_f.weight");
+        else if (i == n - 1) snprintf(ws.items[i].name, sizeof(ws.items[i].name), "ln_f.bias");
+        else snprintf(ws.items[i].name, sizeof(ws.items[i].name), "h.%d.%s", (i - 2) / 12, names[(i - 2) % 12]);
+        ts[i].data = params[i];
+        ts[i].ndim = k > 1 ? 2 : 1;
+        ts[i].shape[0] = r;
+        ts[i].shape[1] = k;
+        ts[i].n = r * k;
+        ws.items[i].t = &ts[i];
+        sizes[i] = r * k;
+    }
+    Tape *tp = tape_new();
+    float *logits = train_gpt2_forward(tp, &ws, c, ids, B, T);
+    float *loss = arena_alloc(1), *probs = arena_alloc((size_t)B * T * V);
+    t_ce(tp, logits, tgt, NULL, loss, probs, (int64_t)B * T, V, 1.0);
+    PMap pm = {(float **)params, (float **)grads, sizes, n};
+    tape_backward_host(tp, &pm, 0);
+    float lh = *loss;
+    tape_free(tp);
+    arena_reset();
+    free(sizes);
+    free(ts);
+    free(ws.items);
+    free(c);
+    return lh;
+}

@@ -235,6 +235,18 @@ void mem_d2d(void *d, const void *s, size_t n) {
     if (e != hipSuccess) ncm_fail(NCM_E_HIP, "mem_d2d(%zu): %s", n, hipGetErrorString(e));
 }
 
+int ncm_copy_async(void *d, const void *s, size_t n) {
+    if (n == 0) return 0;
+    HIP_TRY(hipMemcpyAsync(d, s, n, hipMemcpyDeviceToDevice, g_stream));
+    return 0;
+}
+
+int ncm_zero_async(void *d, size_t n) {
+    if (n == 0) return 0;
+    HIP_TRY(hipMemsetAsync(d, 0, n, g_stream));
+    return 0;
+}
+
 void tensor_to_host(const Tensor *t, float *out) { mem_d2h(out, t->data, (size_t)t->n * sizeof(float)); }
 void tensor_to_backend(Tensor *t, const float *in) { mem_h2d(t->data, in, (size_t)t->n * sizeof(float)); }
 

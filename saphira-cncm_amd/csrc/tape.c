@@ -1,0 +1,450 @@
+/* tape.c -- a device-resident autodiff tape for the hot-path ops.
+ *
+ * Mirrors the reference's Tape (train_tape.c:19-162, 277-481, 636-1051):
+ * every recorder runs the forward on the device and appends a record with
+ * the same fields as TopRec (op kind, input/output pointers, dims, scalar);
+ * ncm_tape_backward walks the records in reverse, looks the upstream
+ * gradient up by output pointer and accumulates input gradients, creating
+ * zeroed buffers on first use (the reference's GMap) and writing parameter
+ * gradients straight into the caller's buffers (PMap aliases).
+ *
+ * Differences that keep everything on the device: the SDPA record stores P
+ * computed by a kernel (the reference computes it on the host); the CE
+ * record computes loss and dlogits together at record time (its backward
+ * only depends on the logits and targets), so the probabilities are never
+ * stored; no host staging anywhere except the embedding ids, which the
+ * reference also keeps on the host.
+ *
+ * Memory: records and gradients live in two device pools of 256 MiB chunks
+ * that grow on demand and are reused after ncm_tape_clear. */
+#include "internal.h"
+
+#include <stdlib.h>
+#include <string.h>
+
+#define POOL_CHUNK ((size_t)256 << 20)
+
+typedef struct {
+    char **chunk;
+    size_t *size;
+    int n, cap, cur;
+    size_t off;
+} Pool;
+
+static void *pool_alloc(Pool *p, size_t bytes) {
+    bytes = (bytes + 255) & ~(size_t)255;
+    if (bytes == 0) bytes = 256;
+    while (p->cur < p->n) {
+        if (p->off + bytes <= p->size[p->cur]) {
+            void *r = p->chunk[p->cur] + p->off;
+            p->off += bytes;
+            return r;
+        }
+        p->cur++;
+        p->off = 0;
+    }
+    if (p->n == p->cap) {
+        int cap = p->cap ? 2 * p->cap : 8;
+        char **c = (char **)realloc(p->chunk, (size_t)cap * sizeof(char *));
+        if (!c) return NULL;
+        p->chunk = c;
+        size_t *s = (size_t *)realloc(p->size, (size_t)cap * sizeof(size_t));
+        if (!s) return NULL;
+        p->size = s;
+        p->cap = cap;
+    }
+    size_t sz = bytes > POOL_CHUNK ? bytes : POOL_CHUNK;
+    void *m = ncm_hip_malloc(sz);
+    if (!m) return NULL;
+    p->chunk[p->n] = (char *)m;
+    p->size[p->n] = sz;
+    p->cur = p->n++;
+    p->off = bytes;
+    return m;
+}
+
+static void pool_reset(Pool *p) {
+    p->cur = 0;
+    p->off = 0;
+}
+
+static void pool_free(Pool *p) {
+    for (int i = 0; i < p->n; i++) ncm_hip_free(p->chunk[i]);
+    free(p->chunk);
+    free(p->size);
+    memset(p, 0, sizeof(*p));
+}
+
+typedef enum {
+    NT_LINEAR, NT_EMBED, NT_LN, NT_RMSN, NT_ACT, NT_MUL, NT_ADD, NT_SCALE,
+    NT_ROPE, NT_SDPA, NT_SPLIT, NT_MERGE, NT_HEADSPLIT, NT_CE
+} NtKind;
+
+typedef struct {
+    NtKind op;
+    const float *a, *b, *c;
+    float *y;
+    float *aux;                 /* SDPA: P; CE: dlogits */
+    int *ids;                   /* EMBED: host copy of the ids */
+    const float *cos_t, *sin_t; /* ROPE tables */
+    int64_t n;
+    int p1, p2, p3, p4, p5, p6;
+    double s;
+} NtRec;
+
+typedef struct {
+    const float *key;
+    float *g;
+} GEnt;
+
+struct NcmTape {
+    NtRec *r;
+    int n, cap;
+    Pool rec, grad;
+    GEnt *gm;
+    int gn, gcap;
+};
+
+NcmTape *ncm_tape_new(void) { return (NcmTape *)calloc(1, sizeof(NcmTape)); }
+
+static void free_recs(NcmTape *t) {
+    for (int i = 0; i < t->n; i++) free(t->r[i].ids);
+    t->n = 0;
+}
+
+void ncm_tape_clear(NcmTape *t) {
+    if (!t) return;
+    free_recs(t);
+    pool_reset(&t->rec);
+    pool_reset(&t->grad);
+    t->gn = 0;
+}
+
+void ncm_tape_free(NcmTape *t) {
+    if (!t) return;
+    if (!ncm_ready()) ncm_hip_sync();
+    free_recs(t);
+    pool_free(&t->rec);
+    pool_free(&t->grad);
+    free(t->r);
+    free(t->gm);
+    free(t);
+}
+
+int ncm_tape_size(const NcmTape *t) { return t ? t->n : 0; }
+
+static NtRec *emit(NcmTape *t, NtKind op) {
+    if (t->n == t->cap) {
+        int cap = t->cap ? 2 * t->cap : 64;
+        NtRec *r = (NtRec *)realloc(t->r, (size_t)cap * sizeof(NtRec));
+        if (!r) {
+            ncm_fail(NCM_E_OOM, "tape: record allocation");
+            return NULL;
+        }
+        t->r = r;
+        t->cap = cap;
+    }
+    NtRec *r = &t->r[t->n++];
+    memset(r, 0, sizeof(*r));
+    r->op = op;
+    return r;
+}
+
+/* ---------------- gradient map ---------------- */
+static float *gmap_find(NcmTape *t, const float *key) {
+    if (!key) return NULL;
+    for (int i = 0; i < t->gn; i++)
+        if (t->gm[i].key == key) return t->gm[i].g;
+    return NULL;
+}
+
+static int gmap_put(NcmTape *t, const float *key, float *g) {
+    if (t->gn == t->gcap) {
+        int cap = t->gcap ? 2 * t->gcap : 64;
+        GEnt *e = (GEnt *)realloc(t->gm, (size_t)cap * sizeof(GEnt));
+        if (!e) return ncm_fail(NCM_E_OOM, "tape: gradient map");
+        t->gm = e;
+        t->gcap = cap;
+    }
+    t->gm[t->gn].key = key;
+    t->gm[t->gn].g = g;
+    t->gn++;
+    return 0;
+}
+
+/* The gradient buffer of `key` (n floats), zeroed on first use. */
+static float *gmap_get(NcmTape *t, const float *key, int64_t n) {
+    if (!key) return NULL;
+    float *g = gmap_find(t, key);
+    if (g) return g;
+    g = (float *)pool_alloc(&t->grad, (size_t)n * sizeof(float));
+    if (!g) {
+        ncm_fail(NCM_E_OOM, "tape: gradient buffer of %lld floats", (long long)n);
+        return NULL;
+    }
+    if (ncm_zero_async(g, (size_t)n * sizeof(float)) || gmap_put(t, key, g)) return NULL;
+    return g;
+}
+
+/* ---------------- recorders (forward on the device + record) ---------------- */
+#define REC_OR_RETURN(r, t, op) \
+    NtRec *r = emit(t, op);     \
+    if (!r) return
+
+void ncm_t_linear(NcmTape *t, const float *x, const float *W, const float *b, float *y, int64_t batch, int M,
+                  int K) {
+    linear_fwd(x, W, b, y, batch, M, K);
+    REC_OR_RETURN(r, t, NT_LINEAR);
+    r->a = x; r->b = W; r->c = b; r->y = y;
+    r->n = batch; r->p1 = M; r->p2 = K;
+}
+
+void ncm_t_embed(NcmTape *t, const float *W, const int *idx, int V, float *y, int64_t n, int D) {
+    if (n < 0 || !idx) { ncm_fail(NCM_E_ARG, "ncm_t_embed: bad ids"); return; }
+    int *hcopy = (int *)malloc((size_t)(n > 0 ? n : 1) * sizeof(int));
+    int *dcopy = (int *)pool_alloc(&t->rec, (size_t)(n > 0 ? n : 1) * sizeof(int));
+    if (!hcopy || !dcopy) {
+        free(hcopy);
+        ncm_fail(NCM_E_OOM, "ncm_t_embed: id copies");
+        return;
+    }
+    memcpy(hcopy, idx, (size_t)n * sizeof(int));
+    mem_h2d(dcopy, idx, (size_t)n * sizeof(int));
+    embedding_fwd_v(W, V, dcopy, y, n, D);
+    NtRec *r = emit(t, NT_EMBED);
+    if (!r) { free(hcopy); return; }
+    r->a = W; r->y = y; r->ids = hcopy;
+    r->n = n; r->p1 = D; r->p2 = V;
+}
+
+static void rec_ln(NcmTape *t, const float *x, const float *w, const float *b, float *y, int64_t rows, int C,
+                   double eps) {
+    REC_OR_RETURN(r, t, NT_LN);
+    r->a = x; r->b = w; r->c = b; r->y = y;
+    r->n = rows; r->p1 = C; r->s = eps;
+}
+
+void ncm_t_layernorm(NcmTape *t, const float *x, const float *w, const float *b, float *y, int64_t rows, int C) {
+    layernorm_fwd(x, w, b, y, rows, C);
+    rec_ln(t, x, w, b, y, rows, C, 1e-6);
+}
+
+void ncm_t_layernorm_eps(NcmTape *t, const float *x, const float *w, const float *b, float *y, int64_t rows, int C,
+                         double eps) {
+    layernorm_eps_fwd(x, w, b, y, rows, C, (float)eps);
+    rec_ln(t, x, w, b, y, rows, C, eps);
+}
+
+void ncm_t_rmsnorm(NcmTape *t, const float *x, const float *w, float *y, int64_t rows, int C) {
+    rmsnorm_fwd(x, w, y, rows, C);
+    REC_OR_RETURN(r, t, NT_RMSN);
+    r->a = x; r->b = w; r->y = y;
+    r->n = rows; r->p1 = C;
+}
+
+static void rec_act(NcmTape *t, const float *x, float *y, int64_t n, int kind) {
+    REC_OR_RETURN(r, t, NT_ACT);
+    r->a = x; r->y = y; r->n = n; r->p1 = kind;
+}
+
+void ncm_t_gelu(NcmTape *t, const float *x, float *y, int64_t n) { gelu_fwd(x, y, n); rec_act(t, x, y, n, 0); }
+void ncm_t_silu(NcmTape *t, const float *x, float *y, int64_t n) { silu_fwd(x, y, n); rec_act(t, x, y, n, 1); }
+void ncm_t_gelu_tanh(NcmTape *t, const float *x, float *y, int64_t n) {
+    gelu_tanh_fwd(x, y, n);
+    rec_act(t, x, y, n, 2);
+}
+
+void ncm_t_mul(NcmTape *t, const float *a, const float *b, float *y, int64_t n) {
+    mul_fwd(a, b, y, n);
+    REC_OR_RETURN(r, t, NT_MUL);
+    r->a = a; r->b = b; r->y = y; r->n = n;
+}
+
+void ncm_t_add(NcmTape *t, const float *a, const float *b, float *y, int64_t n) {
+    add_fwd(a, b, y, n);
+    REC_OR_RETURN(r, t, NT_ADD);
+    r->a = a; r->b = b; r->y = y; r->n = n;
+}
+
+void ncm_t_scale(NcmTape *t, const float *x, float s, float *y, int64_t n) {
+    scale_fwd(x, s, y, n);
+    REC_OR_RETURN(r, t, NT_SCALE);
+    r->a = x; r->y = y; r->n = n; r->s = s;
+}
+
+void ncm_t_rope(NcmTape *t, const float *xq, const float *xk, float *yq, float *yk, const float *cos_t,
+                const float *sin_t, int B, int H, int Hkv, int T, int hd) {
+    if (B < 0 || H < 0 || Hkv < 1 || T < 0 || hd < 0) { ncm_fail(NCM_E_ARG, "ncm_t_rope: bad shape"); return; }
+    if (ncm_ready()) return;
+    if (ncm_copy_async(yq, xq, (size_t)B * H * T * hd * sizeof(float)) ||
+        ncm_copy_async(yk, xk, (size_t)B * Hkv * T * hd * sizeof(float)))
+        return;
+    rope_apply_gqa(yq, yk, cos_t, sin_t, B, H, Hkv, T, hd);
+    REC_OR_RETURN(r, t, NT_ROPE);
+    r->a = xq; r->b = xk; r->c = yq; r->y = yk;
+    r->cos_t = cos_t; r->sin_t = sin_t;
+    r->n = B; r->p1 = H; r->p2 = T; r->p3 = hd; r->p4 = Hkv;
+}
+
+void ncm_t_sdpa(NcmTape *t, const float *q, const float *k, const float *v, const float *mask, float *o, int B,
+                int H, int Hkv, int Tq, int Tkv, int hd) {
+    if (Hkv < 1 || H % Hkv) { ncm_fail(NCM_E_ARG, "ncm_t_sdpa: H=%d Hkv=%d", H, Hkv); return; }
+    sdpa_fwd_gqa(q, k, v, mask, o, B, H, Hkv, Tq, Tkv, hd);
+    float *P = (float *)pool_alloc(&t->rec, (size_t)B * H * Tq * Tkv * sizeof(float));
+    if (!P) { ncm_fail(NCM_E_OOM, "ncm_t_sdpa: probabilities"); return; }
+    sdpa_probs_gqa(q, k, mask, P, B, H, Hkv, Tq, Tkv, hd);
+    REC_OR_RETURN(r, t, NT_SDPA);
+    r->a = q; r->b = k; r->c = v; r->y = o; r->aux = P;
+    r->n = B; r->p1 = H; r->p2 = Hkv; r->p3 = Tq; r->p4 = Tkv; r->p5 = hd;
+}
+
+void ncm_t_qkvsplit(NcmTape *t, const float *in, float *qq, float *kk, float *vv, int B, int T, int C, int H, int hd,
+                    int K, int rep) {
+    qkv_split_fwd(in, qq, kk, vv, B, T, C, H, hd, K, rep);
+    REC_OR_RETURN(r, t, NT_SPLIT);
+    r->a = in; r->b = qq; r->c = kk; r->y = vv;
+    r->n = B; r->p1 = T; r->p2 = C; r->p3 = H; r->p4 = hd; r->p5 = K; r->p6 = rep;
+}
+
+void ncm_t_headmerge(NcmTape *t, const float *ctx, float *out, int B, int T, int C, int H, int hd) {
+    head_merge_fwd(ctx, out, B, T, C, H, hd);
+    REC_OR_RETURN(r, t, NT_MERGE);
+    r->a = ctx; r->y = out;
+    r->n = B; r->p1 = T; r->p2 = C; r->p3 = H; r->p4 = hd;
+}
+
+void ncm_t_headsplit(NcmTape *t, const float *in, float *out, int B, int T, int C, int H, int hd) {
+    heads_transpose_fwd_b(in, out, B, T, H, hd);
+    REC_OR_RETURN(r, t, NT_HEADSPLIT);
+    r->a = in; r->y = out;
+    r->n = B; r->p1 = T; r->p2 = C; r->p3 = H; r->p4 = hd;
+}
+
+void ncm_t_ce(NcmTape *t, const float *logits, const int *tgt, const float *wmask, float *loss, float *probs,
+              int64_t rows, int V, double weight) {
+    if (rows <= 0 || V <= 0 || !tgt) { ncm_fail(NCM_E_ARG, "ncm_t_ce: bad arguments"); return; }
+    if (ncm_ready()) return;
+    int *dt = (int *)pool_alloc(&t->rec, (size_t)rows * sizeof(int));
+    float *dw = wmask ? (float *)pool_alloc(&t->rec, (size_t)rows * sizeof(float)) : NULL;
+    float *dl = (float *)pool_alloc(&t->rec, (size_t)rows * V * sizeof(float));
+    if (!dt || (wmask && !dw) || !dl) { ncm_fail(NCM_E_OOM, "ncm_t_ce: buffers"); return; }
+    mem_h2d(dt, tgt, (size_t)rows * sizeof(int));
+    if (wmask) mem_h2d(dw, wmask, (size_t)rows * sizeof(float));
+    if (ncm_zero_async(dl, (size_t)rows * V * sizeof(float))) return;
+    if (probs) ce_fwd(logits, dt, dw, loss, probs, rows, V);
+    ce_fwd_bwd(logits, dt, dw, loss, dl, rows, V, weight);
+    REC_OR_RETURN(r, t, NT_CE);
+    r->a = logits; r->y = loss; r->aux = dl;
+    r->n = rows; r->p1 = V; r->s = weight;
+}
+
+/* ---------------- backward ---------------- */
+void ncm_tape_backward(NcmTape *t, const NcmPMap *pm) {
+    if (!t || ncm_ready()) return;
+    t->gn = 0;
+    pool_reset(&t->grad);
+    if (pm)
+        for (int i = 0; i < pm->n; i++)
+            if (pm->params[i] && pm->grads[i] && gmap_put(t, pm->params[i], pm->grads[i])) return;
+    for (int i = t->n - 1; i >= 0; i--) {
+        NtRec *r = &t->r[i];
+        if (r->op == NT_CE) {
+            float *g = gmap_find(t, r->a);
+            if (g)
+                add_inplace_fwd(g, r->aux, r->n * r->p1);
+            else if (gmap_put(t, r->a, r->aux))
+                return;
+            continue;
+        }
+        float *dy = gmap_find(t, r->y);
+        if (!dy) {
+            if (r->op == NT_ROPE && gmap_find(t, r->c)) {
+                /* only the q output carries a gradient */
+            } else if (r->op == NT_SPLIT && (gmap_find(t, r->b) || gmap_find(t, r->c))) {
+            } else {
+                continue;
+            }
+        }
+        switch (r->op) {
+        case NT_LINEAR: {
+            int64_t batch = r->n;
+            int M = r->p1, K = r->p2;
+            linear_bwd(r->a, r->b, dy, gmap_get(t, r->a, batch * K), gmap_get(t, r->b, (int64_t)M * K),
+                       r->c ? gmap_get(t, r->c, M) : NULL, batch, M, K);
+            break;
+        }
+        case NT_EMBED:
+            embedding_bwd(dy, r->ids, r->n, r->p1, gmap_get(t, r->a, (int64_t)r->p2 * r->p1), r->p2);
+            break;
+        case NT_LN:
+            layernorm_bwd(r->a, r->b, dy, gmap_get(t, r->a, r->n * r->p1), r->b ? gmap_get(t, r->b, r->p1) : NULL,
+                          r->c ? gmap_get(t, r->c, r->p1) : NULL, r->n, r->p1, r->s);
+            break;
+        case NT_RMSN:
+            rmsnorm_bwd(r->a, r->b, dy, gmap_get(t, r->a, r->n * r->p1), r->b ? gmap_get(t, r->b, r->p1) : NULL,
+                        r->n, r->p1);
+            break;
+        case NT_ACT: {
+            float *dx = gmap_get(t, r->a, r->n);
+            if (r->p1 == 0) gelu_bwd(r->a, dy, dx, r->n);
+            else if (r->p1 == 1) silu_bwd(r->a, dy, dx, r->n);
+            else gelu_tanh_bwd(r->a, dy, dx, r->n);
+            break;
+        }
+        case NT_MUL:
+            mul_bwd(r->a, r->b, dy, gmap_get(t, r->a, r->n), gmap_get(t, r->b, r->n), r->n);
+            break;
+        case NT_ADD:
+            add_inplace_fwd(gmap_get(t, r->a, r->n), dy, r->n);
+            add_inplace_fwd(gmap_get(t, r->b, r->n), dy, r->n);
+            break;
+        case NT_SCALE: {
+            float *dx = gmap_get(t, r->a, r->n);
+            float s = (float)r->s;
+            int64_t n = r->n;
+            if (dx && n > 0) {
+                void *a[] = {&dx, &dy, &s, &n};
+                ncm_launch_named("axpy_k", (unsigned)((n + 255) / 256), 1, 1, 256, a);
+            }
+            break;
+        }
+        case NT_ROPE: {
+            int B = (int)r->n, H = r->p1, T = r->p2, hd = r->p3, Hkv = r->p4;
+            float *gq = gmap_find(t, r->c), *gk = gmap_find(t, r->y);
+            float *dxq = gq ? gmap_get(t, r->a, (int64_t)B * H * T * hd) : NULL;
+            float *dxk = gk ? gmap_get(t, r->b, (int64_t)B * Hkv * T * hd) : NULL;
+            rope_bwd_gqa(gq, gk, r->cos_t, r->sin_t, dxq, dxk, B, H, Hkv, T, hd);
+            break;
+        }
+        case NT_SDPA: {
+            int B = (int)r->n, H = r->p1, Hkv = r->p2, Tq = r->p3, Tkv = r->p4, hd = r->p5;
+            sdpa_bwd_gqa(r->a, r->b, r->c, r->aux, dy, gmap_get(t, r->a, (int64_t)B * H * Tq * hd),
+                         gmap_get(t, r->b, (int64_t)B * Hkv * Tkv * hd), gmap_get(t, r->c, (int64_t)B * Hkv * Tkv * hd),
+                         B, H, Hkv, Tq, Tkv, hd);
+            break;
+        }
+        case NT_SPLIT: {
+            int B = (int)r->n, T = r->p1, C = r->p2, H = r->p3, hd = r->p4, K = r->p5, rep = r->p6;
+            qkv_split_bwd(gmap_find(t, r->b), gmap_find(t, r->c), gmap_find(t, r->y),
+                          gmap_get(t, r->a, (int64_t)B * T * ((int64_t)C + 2 * K * hd)), B, T, C, H, hd, K, rep);
+            break;
+        }
+        case NT_MERGE: {
+            int B = (int)r->n, T = r->p1, C = r->p2, H = r->p3, hd = r->p4;
+            head_merge_bwd(dy, gmap_get(t, r->a, (int64_t)B * H * T * hd), B, T, C, H, hd);
+            break;
+        }
+        case NT_HEADSPLIT: {
+            int B = (int)r->n, T = r->p1, C = r->p2, H = r->p3, hd = r->p4;
+            heads_transpose_bwd(dy, gmap_get(t, r->a, (int64_t)B * T * C), B, T, C, H, hd);
+            break;
+        }
+        case NT_CE:
+            break;
+        }
+        if (ncm_ready()) return;
+    }
+}
+
+/* The gradient the last backward accumulated for `key` (NULL if none). */
+float *ncm_tape_grad(NcmTape *t, const float *key) { return t ? gmap_find(t, key) : NULL; }

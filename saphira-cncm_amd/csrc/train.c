@@ -239,3 +239,136 @@ double grad_clip_global(float *const *grads, const int64_t *sizes, int count, do
     }
     return gnorm;
 }
+
+/* ---- remaining tape backward cases ---- */
+static int elt_check(const char *fn, int64_t n, const void *a, const void *b) {
+    if (n < 0 || (n + 255) / 256 > UINT_MAX) return ncm_fail(NCM_E_ARG, "%s: bad size", fn);
+    if (n == 0) return 1;
+    if (!a || !b) return ncm_fail(NCM_E_ARG, "%s: null pointer", fn);
+    return ncm_ready();
+}
+
+static void act_bwd(const char *fn, const float *x, const float *dy, float *dx, int64_t n, int kind) {
+    if (elt_check(fn, n, x, dy) || !dx) return;
+    void *a[] = {&x, &dy, &dx, &n, &kind};
+    ncm_launch_named("act_bwd_k", blocks_of(n, 256), 1, 1, 256, a);
+}
+void gelu_bwd(const float *x, const float *dy, float *dx, int64_t n) { act_bwd("gelu_bwd", x, dy, dx, n, 0); }
+void silu_bwd(const float *x, const float *dy, float *dx, int64_t n) { act_bwd("silu_bwd", x, dy, dx, n, 1); }
+void gelu_tanh_bwd(const float *x, const float *dy, float *dx, int64_t n) {
+    act_bwd("gelu_tanh_bwd", x, dy, dx, n, 2);
+}
+
+void mul_bwd(const float *a, const float *b, const float *dy, float *da, float *db, int64_t n) {
+    if (elt_check("mul_bwd", n, a, b) || (!da && !db)) return;
+    if (!dy) { ncm_fail(NCM_E_ARG, "mul_bwd: null dy"); return; }
+    void *args[] = {&a, &b, &dy, &da, &db, &n};
+    ncm_launch_named("mul_bwd_k", blocks_of(n, 256), 1, 1, 256, args);
+}
+
+void rope_bwd_gqa(const float *gq, const float *gk, const float *cos_t, const float *sin_t, float *dxq, float *dxk,
+                  int B, int H, int Hkv, int T, int hd) {
+    if (B < 0 || H < 0 || Hkv < 0 || T <= 0 || hd <= 0 || (hd & 1)) {
+        ncm_fail(NCM_E_ARG, "rope_bwd_gqa: bad shape");
+        return;
+    }
+    if (!cos_t || !sin_t) { ncm_fail(NCM_E_ARG, "rope_bwd_gqa: null tables"); return; }
+    if (ncm_ready()) return;
+    const float *g[2] = {gq, gk};
+    float *d[2] = {dxq, dxk};
+    int64_t rows[2] = {(int64_t)B * H * T, (int64_t)B * Hkv * T};
+    for (int i = 0; i < 2; i++) {
+        if (!g[i] || !d[i] || rows[i] == 0) continue;
+        int64_t n = rows[i] * (hd / 2);
+        void *a[] = {&d[i], &g[i], &cos_t, &sin_t, &rows[i], &T, &hd};
+        if (ncm_launch_named("rope_bwd_k", blocks_of(n, 256), 1, 1, 256, a)) return;
+    }
+}
+
+void embedding_bwd(const float *dy, const int *idx, int64_t n, int D, float *dW, int V) {
+    if (n < 0 || D <= 0 || V <= 0 || n > INT_MAX) { ncm_fail(NCM_E_ARG, "embedding_bwd: bad shape"); return; }
+    if (n == 0) return;
+    if (!dy || !idx || !dW) { ncm_fail(NCM_E_ARG, "embedding_bwd: null pointer"); return; }
+    if (ncm_ready()) return;
+    /* group the rows by id (counting sort, rows ascending within an id) */
+    int *cnt = (int *)calloc((size_t)V + 1, sizeof(int));
+    int *host = (int *)malloc(((size_t)n * 2 + (size_t)V + 2) * sizeof(int));
+    if (!cnt || !host) {
+        free(cnt);
+        free(host);
+        ncm_fail(NCM_E_OOM, "embedding_bwd: host allocation");
+        return;
+    }
+    for (int64_t i = 0; i < n; i++)
+        if (idx[i] >= 0 && idx[i] < V) cnt[idx[i]]++;
+    int *uid = host, nu = 0;
+    for (int v = 0; v < V; v++)
+        if (cnt[v]) uid[nu++] = v;
+    int *off = uid + nu, *rowlist = off + nu + 1;
+    int *pos = (int *)malloc((size_t)V * sizeof(int));
+    if (!pos) {
+        free(cnt);
+        free(host);
+        ncm_fail(NCM_E_OOM, "embedding_bwd: host allocation");
+        return;
+    }
+    off[0] = 0;
+    for (int u = 0; u < nu; u++) {
+        pos[uid[u]] = off[u];
+        off[u + 1] = off[u] + cnt[uid[u]];
+    }
+    for (int64_t i = 0; i < n; i++)
+        if (idx[i] >= 0 && idx[i] < V) rowlist[pos[idx[i]]++] = (int)i;
+    int total = nu + (nu + 1) + off[nu];
+    free(pos);
+    free(cnt);
+    if (nu == 0 || nu > 65535 * 64) {
+        free(host);
+        if (nu) ncm_fail(NCM_E_ARG, "embedding_bwd: too many distinct ids");
+        return;
+    }
+    int *dev = (int *)ncm_workspace(WS_TRAIN, (size_t)total * sizeof(int));
+    if (!dev) { free(host); return; }
+    mem_h2d(dev, host, (size_t)total * sizeof(int));
+    free(host);
+    const int *duid = dev, *doff = dev + nu, *drow = dev + nu + nu + 1;
+    for (int u0 = 0; u0 < nu; u0 += 65535) {
+        int cntu = nu - u0 < 65535 ? nu - u0 : 65535;
+        const int *pu = duid + u0, *po = doff + u0;
+        void *a[] = {&dy, &pu, &po, &drow, &dW, &D};
+        if (ncm_launch_named("emb_bwd_k", blocks_of(D, 256), (unsigned)cntu, 1, 256, a)) return;
+    }
+}
+
+void qkv_split_bwd(const float *gq, const float *gk, const float *gv, float *dx, int B, int T, int C, int H, int hd,
+                   int K, int rep) {
+    if (B < 0 || T < 0 || C < 0 || H <= 0 || hd <= 0 || K <= 0 || rep <= 0 || (H - 1) / rep >= K ||
+        (int64_t)H * hd > C) {
+        ncm_fail(NCM_E_ARG, "qkv_split_bwd: bad shape");
+        return;
+    }
+    int64_t n = (int64_t)B * T * ((int64_t)C + 2 * K * hd);
+    if (elt_check("qkv_split_bwd", n, dx, dx)) return;
+    if (!gq && !gk && !gv) return;
+    void *a[] = {&gq, &gk, &gv, &dx, &B, &T, &C, &H, &hd, &K, &rep};
+    ncm_launch_named("qkv_split_bwd_k", blocks_of(n, 256), 1, 1, 256, a);
+}
+
+static void heads_bwd(const char *fn, const float *dy, float *dx, int B, int T, int C, int H, int hd, int dir) {
+    if (B < 0 || T < 0 || C < 0 || H <= 0 || hd <= 0 || C > (int64_t)H * hd) {
+        ncm_fail(NCM_E_ARG, "%s: bad shape", fn);
+        return;
+    }
+    int64_t n = dir == 0 ? (int64_t)B * H * T * hd : (int64_t)B * T * C;
+    if (elt_check(fn, n, dy, dx)) return;
+    void *a[] = {&dy, &dx, &B, &T, &C, &H, &hd, &dir};
+    ncm_launch_named("heads_bwd_k", blocks_of(n, 256), 1, 1, 256, a);
+}
+
+void head_merge_bwd(const float *dy, float *dctx, int B, int T, int C, int H, int hd) {
+    heads_bwd("head_merge_bwd", dy, dctx, B, T, C, H, hd, 0);
+}
+
+void heads_transpose_bwd(const float *dy, float *dx, int B, int T, int C, int H, int hd) {
+    heads_bwd("heads_transpose_bwd", dy, dx, B, T, C, H, hd, 1);
+}

@@ -765,3 +765,135 @@ sdpa_probs_rows(const float *__restrict__ q, const float *__restrict__ k, const 
         }
     }
 }
+
+// ---------------------------------------------------------------- elementwise backward
+// train_tape.c:830-873: dx += (float)(dy * g(x)), g in fp64.
+// kind 0 gelu (erf), 1 silu, 2 gelu_tanh (gelu_new).
+extern "C" __global__ void __launch_bounds__(256)
+act_bwd_k(const float *__restrict__ x, const float *__restrict__ dy, float *__restrict__ dx, int64_t n, int kind) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const double xv = (double)x[i];
+    double g;
+    if (kind == 0) {
+        const double e = erf(xv / 1.4142135623730951);
+        g = 0.5 * (1 + e) + xv * exp(-0.5 * xv * xv) * 0.3989422804014327;
+    } else if (kind == 1) {
+        const double s = 1.0 / (1.0 + exp(-xv));
+        g = s * (1 + xv * (1 - s));
+    } else {
+        const double c0 = 0.7978845608028654, c1 = 0.044715;
+        const double th = tanh(c0 * (xv + c1 * xv * xv * xv));
+        g = 0.5 * (1.0 + th) + 0.5 * xv * (1.0 - th * th) * c0 * (1.0 + 3.0 * c1 * xv * xv);
+    }
+    dx[i] += (float)((double)dy[i] * g);
+}
+
+// train_tape.c:1254-1268: da += dy*b, db += dy*a (float products)
+extern "C" __global__ void __launch_bounds__(256)
+mul_bwd_k(const float *__restrict__ a, const float *__restrict__ b, const float *__restrict__ dy,
+          float *__restrict__ da, float *__restrict__ db, int64_t n) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float g = dy[i];
+    if (da) da[i] += g * b[i];
+    if (db) db[i] += g * a[i];
+}
+
+// train_tape.c:890-930 (k_rope_bwd): transposed rotation in fp64; one thread
+// per (row, d < hd/2), position row % T.
+extern "C" __global__ void __launch_bounds__(256)
+rope_bwd_k(float *__restrict__ dx, const float *__restrict__ g, const float *__restrict__ cos_t,
+           const float *__restrict__ sin_t, int64_t rows, int T, int hd) {
+#pragma clang fp contract(off)
+    const int h = hd >> 1;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * h) return;
+    const int64_t row = i / h;
+    const int d = (int)(i - row * h);
+    const int t = (int)(row % T);
+    const float *gr = g + row * hd, *co = cos_t + (int64_t)t * hd, *si = sin_t + (int64_t)t * hd;
+    const double g0 = gr[d], g1 = gr[d + h];
+    const double c0 = co[d], s0 = si[d], c1 = co[d + h], s1 = si[d + h];
+    dx[row * hd + d] += (float)(g0 * c0 + g1 * s1);
+    dx[row * hd + h + d] += (float)(-g0 * s0 + g1 * c1);
+}
+
+// train_tape.c:726-741 TOP_EMBED: rows grouped by id on the host (ids in
+// ascending row order, as the reference visits them); per (id, d) a float
+// sum in that order, float-added into dW -- bit-identical to the reference.
+extern "C" __global__ void __launch_bounds__(256)
+emb_bwd_k(const float *__restrict__ dy, const int *__restrict__ uid, const int *__restrict__ off,
+          const int *__restrict__ rowlist, float *__restrict__ dW, int D) {
+#pragma clang fp contract(off)
+    const int d = blockIdx.x * 256 + threadIdx.x;
+    if (d >= D) return;
+    const int u = blockIdx.y;
+    float s = 0.f;
+    for (int j = off[u]; j < off[u + 1]; ++j) s += dy[(int64_t)rowlist[j] * D + d];
+    float *w = dW + (int64_t)uid[u] * D + d;
+    *w = *w + s;
+}
+
+// train_tape.c:1293-1328 TOP_SPLIT: one thread per element of the fused
+// input row [B][T][C + 2*K*hd]; k/v gradients summed over the query heads
+// of the kv head (float, ascending h).
+extern "C" __global__ void __launch_bounds__(256)
+qkv_split_bwd_k(const float *__restrict__ gq, const float *__restrict__ gk, const float *__restrict__ gv,
+                float *__restrict__ dx, int B, int T, int C, int H, int hd, int K, int rep) {
+#pragma clang fp contract(off)
+    const int64_t row_len = (int64_t)C + 2 * K * hd;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)B * T * row_len) return;
+    const int64_t bt = i / row_len;
+    const int col = (int)(i - bt * row_len);
+    const int t = (int)(bt % T), b = (int)(bt / T);
+    if (col < C) {
+        if (!gq) return;
+        const int h = col / hd, d = col - h * hd;
+        if (h < H) dx[i] += gq[(((int64_t)b * H + h) * T + t) * hd + d];
+        return;
+    }
+    const int kc = col - C;
+    const float *g = kc < K * hd ? gk : gv;
+    if (!g) return;
+    const int kk = kc < K * hd ? kc : kc - K * hd;
+    const int kvh = kk / hd, d = kk - kvh * hd;
+    float s = 0.f;
+    for (int h = kvh * rep; h < (kvh + 1) * rep && h < H; ++h) s += g[(((int64_t)b * H + h) * T + t) * hd + d];
+    dx[i] += s;
+}
+
+// TOP_MERGE (train_tape.c:1329-1338): dctx[b,h,t,d] += dy[b,t,h*hd+d];
+// TOP_HEADSPLIT (:1339-1350): dx[b,t,h*hd+d] += dy[b,h,t,d].  One thread
+// per destination element.  dir 0: merge backward, 1: head-split backward.
+extern "C" __global__ void __launch_bounds__(256)
+heads_bwd_k(const float *__restrict__ dy, float *__restrict__ dx, int B, int T, int C, int H, int hd, int dir) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (dir == 0) {
+        if (i >= (int64_t)B * H * T * hd) return;
+        const int d = (int)(i % hd);
+        const int t = (int)((i / hd) % T);
+        const int64_t bh = i / ((int64_t)hd * T);
+        const int h = (int)(bh % H), b = (int)(bh / H);
+        if (h * hd + d < C) dx[i] += dy[((int64_t)b * T + t) * C + h * hd + d];
+    } else {
+        if (i >= (int64_t)B * T * C) return;
+        const int c = (int)(i % C);
+        const int64_t bt = i / C;
+        const int t = (int)(bt % T), b = (int)(bt / T);
+        const int h = c / hd, d = c - h * hd;
+        if (h < H) dx[i] += dy[(((int64_t)b * H + h) * T + t) * hd + d];
+    }
+}
+
+// TOP_SCALE backward (train_tape.c:1222-1231): dx += dy * s (float, two roundings)
+extern "C" __global__ void __launch_bounds__(256)
+axpy_k(float *__restrict__ dx, const float *__restrict__ dy, float s, int64_t n) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) dx[i] = dx[i] + dy[i] * s;
+}

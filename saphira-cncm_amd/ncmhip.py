@@ -88,6 +88,43 @@ _SIGS = {
     "adamw_update": (None, [vp, vp, vp, vp, i64] + [ctypes.c_double] * 7),
     "sched_cosine_warmup": (ctypes.c_double, [ctypes.c_long, ctypes.c_double, ctypes.c_double]),
     "grad_clip_global": (ctypes.c_double, [ctypes.POINTER(vp), ctypes.POINTER(i64), ci, ctypes.c_double]),
+    "gelu_bwd": (None, [vp, vp, vp, i64]),
+    "silu_bwd": (None, [vp, vp, vp, i64]),
+    "gelu_tanh_bwd": (None, [vp, vp, vp, i64]),
+    "mul_bwd": (None, [vp, vp, vp, vp, vp, i64]),
+    "rope_bwd_gqa": (None, [vp] * 6 + [ci] * 5),
+    "embedding_bwd": (None, [vp, vp, i64, ci, vp, ci]),
+    "qkv_split_bwd": (None, [vp] * 4 + [ci] * 7),
+    "head_merge_bwd": (None, [vp, vp] + [ci] * 5),
+    "heads_transpose_bwd": (None, [vp, vp] + [ci] * 5),
+    "ncm_tape_new": (vp, []),
+    "ncm_tape_free": (None, [vp]),
+    "ncm_tape_clear": (None, [vp]),
+    "ncm_tape_size": (ci, [vp]),
+    "ncm_tape_backward": (None, [vp, vp]),
+    "ncm_tape_grad": (vp, [vp, vp]),
+    "ncm_t_linear": (None, [vp] * 5 + [i64, ci, ci]),
+    "ncm_t_embed": (None, [vp, vp, vp, ci, vp, i64, ci]),
+    "ncm_t_layernorm": (None, [vp] * 5 + [i64, ci]),
+    "ncm_t_layernorm_eps": (None, [vp] * 5 + [i64, ci, ctypes.c_double]),
+    "ncm_t_rmsnorm": (None, [vp] * 4 + [i64, ci]),
+    "ncm_t_gelu": (None, [vp, vp, vp, i64]),
+    "ncm_t_gelu_tanh": (None, [vp, vp, vp, i64]),
+    "ncm_t_silu": (None, [vp, vp, vp, i64]),
+    "ncm_t_mul": (None, [vp] * 4 + [i64]),
+    "ncm_t_add": (None, [vp] * 4 + [i64]),
+    "ncm_t_scale": (None, [vp, vp, ctypes.c_float, vp, i64]),
+    "ncm_t_rope": (None, [vp] * 7 + [ci] * 5),
+    "ncm_t_sdpa": (None, [vp] * 6 + [ci] * 6),
+    "ncm_t_qkvsplit": (None, [vp] * 5 + [ci] * 7),
+    "ncm_t_headmerge": (None, [vp] * 3 + [ci] * 5),
+    "ncm_t_headsplit": (None, [vp] * 3 + [ci] * 5),
+    "ncm_t_ce": (None, [vp] * 6 + [i64, ci, ctypes.c_double]),
+    "ncm_gpt2_param_count": (ci, [vp]),
+    "ncm_gpt2_param_shape": (i64, [vp, ci, ctypes.POINTER(i64), ctypes.POINTER(i64)]),
+    "ncm_gpt2_forward": (vp, [vp, vp, vp, vp, ci, ci]),
+    "ncm_gpt2_train_step": (ctypes.c_float, [vp] * 8 + [ci, ci, ctypes.c_long] + [ctypes.c_double] * 4
+                            + [ctypes.POINTER(ctypes.c_double)]),
     "argmax_row": (ci, [vp, ci]),
     "argmax_rows": (None, [vp, vp, i64, ci]),
 }
@@ -296,3 +333,14 @@ class Event:
         if rc:
             raise NcmError(f"hipEventElapsedTime: {rc}")
         return ms.value
+
+
+class Gpt2Config(ctypes.Structure):
+    """NcmGpt2Config of include/ncm_hip.h."""
+    _fields_ = [("n_layer", ctypes.c_int), ("n_embd", ctypes.c_int), ("n_head", ctypes.c_int),
+                ("vocab", ctypes.c_int), ("n_pos", ctypes.c_int)]
+
+
+def ptr_array(bufs):
+    """A C array of device pointers (float *const *) for a list of DeviceBuffers."""
+    return (ctypes.c_void_p * len(bufs))(*[_p(b) for b in bufs])

@@ -196,3 +196,59 @@ def test_sdpa_bwd_partial_outputs():
     dq = D.from_numpy(np.zeros_like(q))
     ncmhip.call("sdpa_bwd_gqa", up(q), up(k), up(v), up(P), up(dO), dq, None, None, B, H, Hkv, T, T, hd)
     assert np.max(np.abs(dq.numpy() - rdq)) <= 1e-4
+
+
+# ---------------------------------------------------------------- remaining tape ops (bit-exact
+# except the fp64 transcendentals of the activation backward: <= 1 ulp)
+@pytest.mark.parametrize("name", ["gelu", "silu", "gelu_tanh"])
+def test_act_bwd(name):
+    x = np.concatenate([rnd(100, 100000, scale=3.0), np.array([0.0, -0.0, 20.0, -20.0], np.float32)])
+    dy, dx0 = rnd(101, x.size), rnd(102, x.size)
+    ref = O.act_bwd(name, x, dy, dx0)
+    dx = up(dx0)
+    ncmhip.call(name + "_bwd", up(x), up(dy), dx, x.size)
+    got = dx.numpy()
+    ulp = np.abs(got.view(np.int32).astype(np.int64) - ref.view(np.int32).astype(np.int64))
+    assert int(ulp.max()) <= 1
+
+
+def test_mul_rope_embed_bwd():
+    n = 4097
+    a, b, dy, da0, db0 = rnd(103, n), rnd(104, n), rnd(105, n), rnd(106, n), rnd(107, n)
+    rda, rdb = O.mul_bwd(a, b, dy, da0, db0)
+    da, db = up(da0), up(db0)
+    ncmhip.call("mul_bwd", up(a), up(b), up(dy), da, db, n)
+    assert bits_equal(da.numpy(), rda) and bits_equal(db.numpy(), rdb)
+
+    B, H, Hkv, T, hd = 2, 14, 2, 37, 64
+    c, s = O.rope_tables_qwen(T, hd, 1e6)
+    gq, gk, q0, k0 = rnd(108, B, H, T, hd), rnd(109, B, Hkv, T, hd), rnd(110, B, H, T, hd), rnd(111, B, Hkv, T, hd)
+    dxq, dxk = up(q0), up(k0)
+    ncmhip.call("rope_bwd_gqa", up(gq), up(gk), up(c), up(s), dxq, dxk, B, H, Hkv, T, hd)
+    assert bits_equal(dxq.numpy(), O.rope_bwd(gq.reshape(-1, hd), c, s, T, q0.reshape(-1, hd)).reshape(q0.shape))
+    assert bits_equal(dxk.numpy(), O.rope_bwd(gk.reshape(-1, hd), c, s, T, k0.reshape(-1, hd)).reshape(k0.shape))
+
+    for V, D, nrow in [(4096, 768, 16384), (512, 768, 16384), (16, 256, 5184), (100, 5, 7)]:
+        idx = np.random.default_rng(V + nrow).integers(0, V, nrow).astype(np.int32)
+        dye, dW0 = rnd(112, nrow, D), rnd(113, V, D)
+        dW = up(dW0)
+        ncmhip.call("embedding_bwd", up(dye), idx.ctypes.data, nrow, D, dW, V)
+        assert bits_equal(dW.numpy(), O.embedding_bwd(dye, idx, V, dW0))
+
+
+@pytest.mark.parametrize("B,T,C,H,hd,K,rep", [(2, 33, 768, 12, 64, 12, 1), (1, 17, 896, 14, 64, 2, 7),
+                                               (3, 5, 64, 4, 16, 1, 4)])
+def test_split_merge_bwd(B, T, C, H, hd, K, rep):
+    gq, gk, gv = rnd(114, B, H, T, hd), rnd(115, B, H, T, hd), rnd(116, B, H, T, hd)
+    dx0 = rnd(117, B, T, C + 2 * K * hd)
+    dx = up(dx0)
+    ncmhip.call("qkv_split_bwd", up(gq), up(gk), up(gv), dx, B, T, C, H, hd, K, rep)
+    assert bits_equal(dx.numpy(), O.qkv_split_bwd(gq, gk, gv, B, T, C, H, hd, K, rep, dx0))
+    dy, c0 = rnd(118, B, T, C), rnd(119, B, H, T, hd)
+    dc = up(c0)
+    ncmhip.call("head_merge_bwd", up(dy), dc, B, T, C, H, hd)
+    assert bits_equal(dc.numpy(), O.head_merge_bwd(dy, B, T, C, H, hd, c0))
+    dys, x0 = rnd(120, B, H, T, hd), rnd(121, B, T, C)
+    dxs = up(x0)
+    ncmhip.call("heads_transpose_bwd", up(dys), dxs, B, T, C, H, hd)
+    assert bits_equal(dxs.numpy(), O.heads_transpose_bwd(dys, B, T, C, H, hd, x0))

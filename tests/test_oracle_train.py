@@ -190,3 +190,99 @@ def test_sdpa_bwd_finite_differences():
     assert np.allclose(dq, num_grad(lambda z: loss(z, k, v), q), atol=2e-5)
     assert np.allclose(dk, num_grad(lambda z: loss(q, z, v), k), atol=2e-5)
     assert np.allclose(dv, num_grad(lambda z: loss(q, k, z), v), atol=2e-5)
+
+
+# ------------------------------------------------------------------ remaining tape ops
+@needs_ref
+@pytest.mark.parametrize("name", ["gelu", "silu", "gelu_tanh"])
+def test_act_bwd_vs_reference(name):
+    x = np.concatenate([rnd(60, 3000, scale=3.0), np.array([0.0, -0.0, 20.0, -20.0], np.float32)])
+    dy, dx0 = rnd(61, x.size), rnd(62, x.size)
+    assert bits_equal(O.act_bwd(name, x, dy, dx0), O.ref_act_bwd(name, x, dy, dx0))
+
+
+@needs_ref
+def test_mul_rope_embed_vs_reference():
+    a, b, dy = rnd(63, 999), rnd(64, 999), rnd(65, 999)
+    da0, db0 = rnd(66, 999), rnd(67, 999)
+    for u, v in zip(O.mul_bwd(a, b, dy, da0, db0), O.ref_mul_bwd(a, b, dy, da0, db0)):
+        assert bits_equal(u, v)
+    B, H, Hkv, T, hd = 2, 6, 2, 9, 16
+    c, s = O.rope_tables_qwen(T, hd, 1e4)
+    xq, xk, gq, gk = rnd(68, B, H, T, hd), rnd(69, B, Hkv, T, hd), rnd(70, B, H, T, hd), rnd(71, B, Hkv, T, hd)
+    rq, rk = O.ref_rope_bwd(xq, xk, c, s, gq, gk)
+    assert bits_equal(O.rope_bwd(gq.reshape(-1, hd), c, s, T).reshape(gq.shape), rq)
+    assert bits_equal(O.rope_bwd(gk.reshape(-1, hd), c, s, T).reshape(gk.shape), rk)
+    V, D, n = 50, 24, 300
+    W = rnd(72, V, D)
+    idx = np.random.default_rng(73).integers(0, V, n).astype(np.int32)
+    dy, dW0 = rnd(74, n, D), rnd(75, V, D)
+    assert bits_equal(O.embedding_bwd(dy, idx, V, dW0), O.ref_embed_bwd(W, idx, dy, dW0))
+
+
+@needs_ref
+@pytest.mark.parametrize("B,T,C,H,hd,K,rep", [(2, 5, 64, 4, 16, 4, 1), (1, 7, 96, 6, 16, 2, 3)])
+def test_split_merge_bwd_vs_reference(B, T, C, H, hd, K, rep):
+    x = rnd(76, B, T, C + 2 * K * hd)
+    gq, gk, gv = rnd(77, B, H, T, hd), rnd(78, B, H, T, hd), rnd(79, B, H, T, hd)
+    assert bits_equal(O.qkv_split_bwd(gq, gk, gv, B, T, C, H, hd, K, rep),
+                      O.ref_split_bwd(x, gq, gk, gv, B, T, C, H, hd, K, rep))
+    assert bits_equal(O.qkv_split_bwd(None, gk, None, B, T, C, H, hd, K, rep),
+                      O.ref_split_bwd(x, None, gk, None, B, T, C, H, hd, K, rep))
+    ctx, dy = rnd(80, B, H, T, hd), rnd(81, B, T, C)
+    assert bits_equal(O.head_merge_bwd(dy, B, T, C, H, hd), O.ref_merge_bwd(0, ctx, dy, B, T, C, H, hd))
+    xs, dys = rnd(82, B, T, C), rnd(83, B, H, T, hd)
+    assert bits_equal(O.heads_transpose_bwd(dys, B, T, C, H, hd), O.ref_merge_bwd(1, xs, dys, B, T, C, H, hd))
+
+
+def test_act_bwd_finite_differences():
+    x = rnd(84, 200, scale=2.5).astype(np.float64)
+    dy = np.ones_like(x)
+    fns = {"gelu": lambda z: 0.5 * z * (1 + np.vectorize(__import__("math").erf)(z / np.sqrt(2))),
+           "silu": lambda z: z / (1 + np.exp(-z)),
+           "gelu_tanh": lambda z: 0.5 * z * (1 + np.tanh(np.sqrt(2 / np.pi) * (z + 0.044715 * z ** 3)))}
+    for name, f in fns.items():
+        h = 1e-6
+        num = (f(x + h) - f(x - h)) / (2 * h)
+        assert np.max(np.abs(O.act_bwd(name, x, dy) - num)) < 1e-6
+
+
+def test_layout_bwd_are_adjoints():
+    """<dy, f(x)> = <f^T(dy), x> for the permutations and the GQA split."""
+    B, T, C, H, hd, K, rep = 2, 3, 24, 6, 4, 2, 3
+    x = rnd(85, B, T, C + 2 * K * hd).astype(np.float64)
+    gq, gk, gv = rnd(86, B, H, T, hd), rnd(87, B, H, T, hd), rnd(88, B, H, T, hd)
+    q, k, v = O.qkv_split(x, B, T, C, H, hd, K, rep)
+    lhs = sum(float(np.sum(g.astype(np.float64) * y)) for g, y in ((gq, q), (gk, k), (gv, v)))
+    rhs = float(np.sum(O.qkv_split_bwd(gq, gk, gv, B, T, C, H, hd, K, rep).astype(np.float64) * x))
+    assert abs(lhs - rhs) < 1e-4
+    ctx, dy = rnd(89, B, H, T, hd), rnd(90, B, T, C)
+    assert abs(float(np.sum(dy * O.head_merge(ctx, B, T, C, H, hd))) -
+               float(np.sum(O.head_merge_bwd(dy, B, T, C, H, hd) * ctx))) < 1e-4
+    W = rnd(91, 10, 3)
+    idx = np.array([3, 3, 0, 9, 3], np.int32)
+    dye = rnd(92, 5, 3)
+    assert abs(float(np.sum(dye * O.embedding(W, idx))) - float(np.sum(O.embedding_bwd(dye, idx, 10) * W))) < 1e-5
+
+
+# ------------------------------------------------------------------ config 5: the whole taped step
+def gpt2_case(seed, n_layer, C, H, V, npos, B, T):
+    rng = np.random.default_rng(seed)
+    params = [(rng.standard_normal(s) * 0.02).astype(np.float32) for s in O.gpt2_shapes(n_layer, C, V, npos)]
+    for i, s in enumerate(O.gpt2_shapes(n_layer, C, V, npos)):   # LayerNorm gains near 1
+        if len(s) == 1 and s[0] == C and (i >= len(params) - 2 or (i - 2) % 12 in (0, 6)):
+            params[i] += 1.0
+    ids = rng.integers(0, V, (B, T)).astype(np.int32)
+    tgt = rng.integers(0, V, (B, T)).astype(np.int32)
+    return params, ids, tgt
+
+
+@needs_ref
+@pytest.mark.parametrize("n_layer,C,H,V,npos,B,T", [(2, 32, 4, 50, 16, 2, 9), (1, 64, 2, 40, 8, 3, 8)])
+def test_gpt2_step_vs_reference(n_layer, C, H, V, npos, B, T):
+    params, ids, tgt = gpt2_case(7, n_layer, C, H, V, npos, B, T)
+    rloss, rg = O.ref_gpt2_grads(params, n_layer, C, H, V, npos, ids, tgt)
+    loss, g = O.gpt2_grads(params, n_layer, C, H, V, npos, ids, tgt)
+    assert np.float32(loss) == np.float32(rloss)
+    for a, b in zip(g, rg):
+        assert bits_equal(a, b)

@@ -350,6 +350,61 @@ float ncm_gpt2_train_step(NcmTape *t, const NcmGpt2Config *c, float *const *para
                           double base_lr, double warmup, double total, double wd, double *gnorm_out);
 
 /* ------------------------------------------------------------------ */
+/* config-4 driver: the Qwen2 decoder of qwen.c                        */
+/* ------------------------------------------------------------------ */
+
+typedef struct {
+    int n_layer, n_embd, n_head, n_kv, n_inner, vocab, n_ctx;
+    double rope_theta;
+} NcmQwenConfig;
+typedef struct NcmQwen NcmQwen;
+
+/* flat parameter order (qwen.c:60-75): 0 embed_tokens [vocab][C] (tied head);
+ * per layer at 1 + 12 l: input_layernorm, q_proj.weight, q_proj.bias,
+ * k_proj.weight, k_proj.bias, v_proj.weight, v_proj.bias, o_proj.weight,
+ * post_attention_layernorm, gate_proj, up_proj, down_proj; last norm.weight. */
+int ncm_qwen_param_count(const NcmQwenConfig *c);
+int64_t ncm_qwen_param_shape(const NcmQwenConfig *c, int i, int64_t *rows, int64_t *cols);
+/* model state over borrowed parameter buffers: RoPE tables (qwen.c:85-101),
+ * KV cache [n_layer][n_kv][n_ctx][hd], decode scratch */
+NcmQwen *ncm_qwen_new(const NcmQwenConfig *c, float *const *params);
+void ncm_qwen_free(NcmQwen *m);
+/* qwen_forward (qwen.c:121-190): ids HOST [T] -> logits [T][vocab] (or the
+ * last row) in the arena; also fills the KV cache for positions 0..T-1. */
+float *ncm_qwen_forward(NcmQwen *m, const int *ids, int T, int last_only);
+/* one KV-cached step for token `id` at position pos (cache holds 0..pos-1):
+ * logits [vocab] in the model's buffer (hd 64, <= 16 query heads per kv head) */
+float *ncm_qwen_decode(NcmQwen *m, int id, int pos);
+/* greedy generation (qwen_generate with temp 0, qwen.c:204-228): prefill +
+ * cached decode, device argmax; stops after eos when eos >= 0. Returns the
+ * number of ids written to out (-1 on error). */
+int ncm_qwen_generate(NcmQwen *m, const int *prompt, int np, int n_new, int eos, int *out);
+
+/* ------------------------------------------------------------------ */
+/* config-1 driver: the NCP transformer forward of ncp.c               */
+/* ------------------------------------------------------------------ */
+
+typedef struct {
+    int n_layer, n_embd, n_head, n_kv, n_inner, vocab;
+    int rope_base;   /* ncp.c build_rope base (10000) */
+    int use_rmsnorm; /* 0: LayerNorm eps 1e-6 as ncp.c:195-199; 1: RMSNorm */
+} NcmNcpConfig;
+
+/* flat parameter order (biases may be NULL): 0 wte [V][C]; per layer at
+ * 1 + 14 l: ln_1.weight, ln_1.bias, attn.c_attn.weight [C + 2 Kv hd][C],
+ * attn.c_attn.bias, attn.c_proj.weight, attn.c_proj.bias, ln_2.weight,
+ * ln_2.bias, mlp.w_gate.weight [I][C], mlp.w_gate.bias, mlp.w_up.weight,
+ * mlp.w_up.bias, mlp.c_proj.weight [C][I], mlp.c_proj.bias; then
+ * ln_f.weight, ln_f.bias, head.weight [V][C], head.bias. */
+int ncm_ncp_param_count(const NcmNcpConfig *c);
+int64_t ncm_ncp_param_shape(const NcmNcpConfig *c, int i, int64_t *rows, int64_t *cols);
+/* build_rope (ncp.c:80-92) for positions 0..S-1 into HOST [S][hd] arrays */
+int ncm_ncp_rope_tables(int S, int hd, int base, float *cos_host, float *sin_host);
+/* ncp_block x n_layer (ncp.c:184-338) + ln_f + head over ids HOST [B][S]
+ * (one level, no mask): logits [B*S][V] in the arena (arena_init first). */
+float *ncm_ncp_forward(const NcmNcpConfig *c, float *const *params, const int *ids, int B, int S);
+
+/* ------------------------------------------------------------------ */
 /* greedy id                                                           */
 /* ------------------------------------------------------------------ */
 

@@ -747,3 +747,18 @@ void orc_heads_transpose_bwd(const float *dy, float *dx, int B, int T, int C, in
                 for (int d = 0; d < hd; d++)
                     dx[((int64_t)b * T + t) * C + h * hd + d] += dy[(((int64_t)b * H + h) * T + t) * hd + d];
 }
+
+/* ncp.c:80-92 build_rope for positions 0..S-1 */
+void orc_rope_tables_ncp(int S, int hd, int base, float *cos_t, float *sin_t) {
+    int half = hd / 2;
+    for (int t = 0; t < S; t++)
+        for (int d = 0; d < half; d++) {
+            double inv = 1.0 / pow((double)base, (double)d / half);
+            double f = t * inv;
+            float co = (float)cos(f), si = (float)sin(f);
+            cos_t[t * hd + d] = co;
+            cos_t[t * hd + half + d] = co;
+            sin_t[t * hd + d] = si;
+            sin_t[t * hd + half + d] = si;
+        }
+}

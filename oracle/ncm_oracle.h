@@ -92,6 +92,9 @@ void orc_qkv_split_bwd(const float *gq, const float *gk, const float *gv, float 
 void orc_head_merge_bwd(const float *dy, float *dctx, int B, int T, int C, int H, int hd);
 void orc_heads_transpose_bwd(const float *dy, float *dx, int B, int T, int C, int H, int hd);
 
+/* src/ncp.c:80-92 build_rope (positions 0..S-1) */
+void orc_rope_tables_ncp(int S, int hd, int base, float *cos_t, float *sin_t);
+
 /* src/kernels.c:774-780 rng_next (xorshift64*) and the ktest generator of
  * tests/ktest_kernels.c:8-12, for seeded inputs shared with the reference. */
 uint64_t orc_rng_next(uint64_t *state);

@@ -79,6 +79,7 @@ def lib():
             "orc_qkv_split_bwd": (None, [vp, vp, vp, vp] + [ci] * 7),
             "orc_head_merge_bwd": (None, [vp, vp] + [ci] * 5),
             "orc_heads_transpose_bwd": (None, [vp, vp] + [ci] * 5),
+            "orc_rope_tables_ncp": (None, [ci, ci, ci, vp, vp]),
         }
         for n, (r, a) in sigs.items():
             f = getattr(L, n)
@@ -734,3 +735,101 @@ def ref_gpt2_grads(params, n_layer, C, H, V, npos, ids, tgt):
     gp = (vp * len(G))(*[x.ctypes.data for x in G])
     loss = f(pp, gp, n_layer, C, H, V, npos, _ptr(ids), _ptr(tgt), B, T)
     return float(loss), G
+
+
+# ---- config 4: qwen_forward (qwen.c:121-190) and greedy generation ----
+def qwen_shapes(n_layer, C, H, K, I, V):
+    hd = C // H
+    per = [(C,), (C, C), (C,), (K * hd, C), (K * hd,), (K * hd, C), (K * hd,), (C, C), (C,), (I, C), (I, C), (C, I)]
+    return [(V, C)] + per * n_layer + [(C,)]
+
+
+def qwen_forward(params, n_layer, C, H, K, I, V, theta, ids, last_only=False, tables=None):
+    """The reference forward op for op with the pinned oracle functions;
+    returns logits [T][V] (or [V] for the last row)."""
+    ids = np.ascontiguousarray(ids, np.int32)
+    T, hd = ids.size, C // H
+    P = [_f32(p) for p in params]
+    cos_t, sin_t = tables if tables is not None else rope_tables_qwen(T, hd, theta)
+    cos_t, sin_t = cos_t[:T], sin_t[:T]
+    mask = np.where(np.arange(T)[None, :] <= np.arange(T)[:, None], 0.0, -1e9).astype(np.float32)
+    h = embedding(P[0], ids)
+    for li in range(n_layer):
+        w = P[1 + 12 * li:13 + 12 * li]
+        h1 = rmsnorm(h, w[0])
+        ql, kl, vl = linear_fwd(h1, w[1], w[2]), linear_fwd(h1, w[3], w[4]), linear_fwd(h1, w[5], w[6])
+        qq = heads_transpose(ql.reshape(1, T, C), 1, T, H, hd)
+        kk = heads_transpose(kl.reshape(1, T, K * hd), 1, T, K, hd)
+        vv = heads_transpose(vl.reshape(1, T, K * hd), 1, T, K, hd)
+        qq = rope(qq.reshape(-1, hd), cos_t, sin_t, T).reshape(qq.shape)
+        kk = rope(kk.reshape(-1, hd), cos_t, sin_t, T).reshape(kk.shape)
+        ctx = sdpa_gqa(qq, kk, vv, mask)
+        mo = head_merge(ctx, 1, T, C, H, hd).reshape(T, C)
+        x1 = h + linear_fwd(mo, w[7], None)
+        h2 = rmsnorm(x1, w[8])
+        gu = mul(act("silu", linear_fwd(h2, w[9], None)), linear_fwd(h2, w[10], None))
+        h = x1 + linear_fwd(gu, w[11], None)
+    lnf = rmsnorm(h, P[-1])
+    if last_only:
+        return linear_fwd(lnf[-1:], P[0], None)[0]
+    return linear_fwd(lnf, P[0], None)
+
+
+def qwen_generate(params, n_layer, C, H, K, I, V, theta, prompt, n_new, eos=-1, n_ctx=None):
+    """qwen_generate with temp 0 (qwen.c:204-228): full recompute per step,
+    argmax_row of the last row; returns (ids, per-step logits)."""
+    ids = list(np.asarray(prompt, np.int32))
+    tables = rope_tables_qwen(n_ctx or len(ids) + n_new, C // H, theta)
+    out, steps = [], []
+    for _ in range(n_new):
+        lg = qwen_forward(params, n_layer, C, H, K, I, V, theta, np.array(ids, np.int32), True, tables)
+        nx = argmax_row(lg)
+        steps.append(lg)
+        out.append(nx)
+        ids.append(nx)
+        if nx == eos:
+            break
+    return out, steps
+
+
+
+# ---- config 1: the NCP transformer forward (ncp.c:184-338) ----
+def rope_tables_ncp(S, hd, base):
+    c = np.empty((S, hd), np.float32)
+    s_ = np.empty((S, hd), np.float32)
+    lib().orc_rope_tables_ncp(S, hd, base, _ptr(c), _ptr(s_))
+    return c, s_
+
+
+def ncp_shapes(n_layer, C, H, Kv, I, V):
+    hd = C // H
+    qkv = C + 2 * Kv * hd
+    per = [(C,), (C,), (qkv, C), (qkv,), (C, C), (C,), (C,), (C,), (I, C), (I,), (I, C), (I,), (C, I), (C,)]
+    return [(V, C)] + per * n_layer + [(C,), (C,), (V, C), (V,)]
+
+
+def ncp_forward(params, n_layer, C, H, Kv, I, V, ids, rope_base=10000, use_rmsnorm=False):
+    """ncp_block x n_layer + ln_f + head on one level of S tokens, op for op
+    with the pinned oracle functions (None entries = absent biases)."""
+    ids = np.ascontiguousarray(ids, np.int32)
+    B, S = ids.shape
+    hd, R = C // H, B * S
+    P = [None if p is None else _f32(p) for p in params]
+    cos_t, sin_t = rope_tables_ncp(S, hd, rope_base)
+    nrm = (lambda x, w, b: rmsnorm(x, w)) if use_rmsnorm else (lambda x, w, b: layernorm(x, w, b))
+    x = embedding(P[0], ids.reshape(-1))
+    for li in range(n_layer):
+        w = P[1 + 14 * li:15 + 14 * li]
+        ln = nrm(x, w[0], w[1])
+        qkv = linear_fwd(ln, w[2], w[3])
+        q, k, v = qkv_split(qkv.reshape(B, S, -1), B, S, C, H, hd, Kv, H // Kv)
+        q = rope(q.reshape(-1, hd), cos_t, sin_t, S).reshape(q.shape)
+        k = rope(k.reshape(-1, hd), cos_t, sin_t, S).reshape(k.shape)
+        ctx = sdpa_gqa(q, k, v)
+        mo = head_merge(ctx, B, S, C, H, hd).reshape(R, C)
+        x = x + linear_fwd(mo, w[4], w[5])
+        ln = nrm(x, w[6], w[7])
+        g = mul(act("silu", linear_fwd(ln, w[8], w[9])), linear_fwd(ln, w[10], w[11]))
+        x = x + linear_fwd(g, w[12], w[13])
+    n = len(P)
+    return linear_fwd(nrm(x, P[n - 4], P[n - 3]), P[n - 2], P[n - 1])

@@ -367,3 +367,149 @@ sdpa_rows(const float *__restrict__ q, const float *__restrict__ k, const float 
         if (d < hd) o[d] = acc[j] / l;
     }
 }
+
+// ---------------------------------------------------------------- decode (KV cache)
+// One decode position `pos`: RoPE (kernels.c:249-264 arithmetic, table row
+// pos) on q [H][hd] and k [Hkv][hd] (the rows of the q/k projections), q
+// written to qo [H][hd], k and v appended to the caches [Hkv][ld][hd] at
+// row pos.  One thread per (head slot, d < hd/2) over H + Hkv slots, plus
+// the v copy.
+extern "C" __global__ void __launch_bounds__(256)
+rope_append_k(const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+              const float *__restrict__ cos_t, const float *__restrict__ sin_t, float *__restrict__ qo,
+              float *__restrict__ kc, float *__restrict__ vc, int H, int Hkv, int hd, int ld, int pos) {
+#pragma clang fp contract(off)
+    const int h2 = hd >> 1;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int nrot = (H + Hkv) * h2;
+    if (i < nrot) {
+        const int slot = i / h2, d = i - slot * h2;
+        const float *src = slot < H ? q + slot * hd : k + (slot - H) * hd;
+        float *dst = slot < H ? qo + slot * hd : kc + ((int64_t)(slot - H) * ld + pos) * hd;
+        const float *co = cos_t + (int64_t)pos * hd, *si = sin_t + (int64_t)pos * hd;
+        const float a = src[d], b = src[d + h2];
+        dst[d] = a * co[d] + (-b) * si[d];
+        dst[d + h2] = b * co[d + h2] + a * si[d + h2];
+    } else if (i < nrot + Hkv * hd) {
+        const int j = i - nrot, kvh = j / hd, d = j - kvh * hd;
+        vc[((int64_t)kvh * ld + pos) * hd + d] = v[j];
+    }
+}
+
+// Decode attention, one query row per head over keys [0, Tkv) of the cache:
+// split over key chunks of 256.  A workgroup owns one kv head and one chunk
+// and all rep = H / Hkv query heads of the group (rep <= 16): thread t
+// scores key c*256 + t against every query of the group, the chunk's
+// (max, sum) per query come from block reductions, and o = sum p v with
+// threads (g, d) = 4 key quarters x 64 dims, reduced through LDS.  hd = 64.
+// part_o [H][nchunk][64], part_ml [H][nchunk][2]; sdpa_decode_combine
+// merges the chunks.
+#define DEC_CH 256
+extern "C" __global__ void __launch_bounds__(256)
+sdpa_decode_partial(const float *__restrict__ q, const float *__restrict__ kc, const float *__restrict__ vc,
+                    float *__restrict__ part_o, float *__restrict__ part_ml, int H, int Hkv, int Tkv, int ld,
+                    float scale) {
+    __shared__ __attribute__((aligned(16))) float sQ[16 * 64];
+    __shared__ float sP[16 * DEC_CH];
+    __shared__ float sRed[16 * 4];
+    __shared__ float sM[16], sL[16];
+    __shared__ __attribute__((aligned(16))) float sO[4 * 16 * 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kvh = blockIdx.y, chunk = blockIdx.x, nchunk = gridDim.x;
+    const int rep = H / Hkv, h0 = kvh * rep;
+    const int key = chunk * DEC_CH + tid;
+    for (int i = tid; i < rep * 64; i += 256) sQ[i] = q[(int64_t)h0 * 64 + i];
+    __syncthreads();
+    float s[16];
+    if (key < Tkv) {
+        const float *kr = kc + ((int64_t)kvh * ld + key) * 64;
+        f4 kv[16];
+#pragma unroll
+        for (int c = 0; c < 16; ++c) kv[c] = *(const f4 *)(kr + 4 * c);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            if (j < rep) {
+                float acc = 0.f;
+#pragma unroll
+                for (int c = 0; c < 16; ++c) {
+                    const f4 qv = *(const f4 *)(sQ + j * 64 + 4 * c);
+                    acc += qv[0] * kv[c][0] + qv[1] * kv[c][1] + qv[2] * kv[c][2] + qv[3] * kv[c][3];
+                }
+                s[j] = acc * scale;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) s[j] = -INFINITY;
+    }
+    // per-query chunk max
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        if (j < rep) {
+            float m = s[j];
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+            if (lane == 0) sRed[j * 4 + wave] = m;
+        }
+    }
+    __syncthreads();
+    if (tid < rep) sM[tid] = fmaxf(fmaxf(sRed[tid * 4], sRed[tid * 4 + 1]), fmaxf(sRed[tid * 4 + 2], sRed[tid * 4 + 3]));
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        if (j < rep) {
+            const float m = sM[j];
+            const float p = (m == -INFINITY || key >= Tkv) ? 0.f : __expf(s[j] - m);
+            sP[j * DEC_CH + tid] = p;
+            float l = p;
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+            if (lane == 0) sRed[j * 4 + wave] = l;
+        }
+    }
+    __syncthreads();
+    if (tid < rep) sL[tid] = (sRed[tid * 4] + sRed[tid * 4 + 1]) + (sRed[tid * 4 + 2] + sRed[tid * 4 + 3]);
+    // o partial: wave g sums keys 64g .. 64g+63 for every query, lane = d
+    float acc[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[j] = 0.f;
+    const int kbase = chunk * DEC_CH + wave * 64;
+    const int kn = min(64, Tkv - kbase);
+    for (int t = 0; t < kn; ++t) {
+        const float vv = vc[((int64_t)kvh * ld + kbase + t) * 64 + lane];
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            if (j < rep) acc[j] += sP[j * DEC_CH + wave * 64 + t] * vv;
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+        if (j < rep) sO[(wave * 16 + j) * 64 + lane] = acc[j];
+    __syncthreads();
+    for (int i = tid; i < rep * 64; i += 256) {
+        const int j = i >> 6, d = i & 63;
+        const float o = (sO[(0 * 16 + j) * 64 + d] + sO[(1 * 16 + j) * 64 + d]) +
+                        (sO[(2 * 16 + j) * 64 + d] + sO[(3 * 16 + j) * 64 + d]);
+        part_o[((int64_t)(h0 + j) * nchunk + chunk) * 64 + d] = o;
+    }
+    if (tid < rep) {
+        part_ml[((int64_t)(h0 + tid) * nchunk + chunk) * 2] = sM[tid];
+        part_ml[((int64_t)(h0 + tid) * nchunk + chunk) * 2 + 1] = sL[tid];
+    }
+}
+
+// out[h][d] = sum_c o_c[d] e^(m_c - m) / sum_c l_c e^(m_c - m); one wave per head.
+extern "C" __global__ void __launch_bounds__(64)
+sdpa_decode_combine(const float *__restrict__ part_o, const float *__restrict__ part_ml, float *__restrict__ out,
+                    int nchunk) {
+    const int h = blockIdx.x, d = threadIdx.x;
+    float m = -INFINITY;
+    for (int c = 0; c < nchunk; ++c) m = fmaxf(m, part_ml[((int64_t)h * nchunk + c) * 2]);
+    float l = 0.f, o = 0.f;
+    for (int c = 0; c < nchunk; ++c) {
+        const float mc = part_ml[((int64_t)h * nchunk + c) * 2];
+        const float w = mc == -INFINITY ? 0.f : __expf(mc - m);
+        l += part_ml[((int64_t)h * nchunk + c) * 2 + 1] * w;
+        o += part_o[((int64_t)h * nchunk + c) * 64 + d] * w;
+    }
+    out[(int64_t)h * 64 + d] = o / l;
+}

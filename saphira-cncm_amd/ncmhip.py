@@ -125,6 +125,17 @@ _SIGS = {
     "ncm_gpt2_forward": (vp, [vp, vp, vp, vp, ci, ci]),
     "ncm_gpt2_train_step": (ctypes.c_float, [vp] * 8 + [ci, ci, ctypes.c_long] + [ctypes.c_double] * 4
                             + [ctypes.POINTER(ctypes.c_double)]),
+    "ncm_qwen_param_count": (ci, [vp]),
+    "ncm_qwen_param_shape": (i64, [vp, ci, ctypes.POINTER(i64), ctypes.POINTER(i64)]),
+    "ncm_qwen_new": (vp, [vp, vp]),
+    "ncm_qwen_free": (None, [vp]),
+    "ncm_qwen_forward": (vp, [vp, vp, ci, ci]),
+    "ncm_qwen_decode": (vp, [vp, ci, ci]),
+    "ncm_qwen_generate": (ci, [vp, vp, ci, ci, ci, vp]),
+    "ncm_ncp_param_count": (ci, [vp]),
+    "ncm_ncp_param_shape": (i64, [vp, ci, ctypes.POINTER(i64), ctypes.POINTER(i64)]),
+    "ncm_ncp_rope_tables": (ci, [ci, ci, ci, vp, vp]),
+    "ncm_ncp_forward": (vp, [vp, vp, vp, ci, ci]),
     "argmax_row": (ci, [vp, ci]),
     "argmax_rows": (None, [vp, vp, i64, ci]),
 }
@@ -344,3 +355,17 @@ class Gpt2Config(ctypes.Structure):
 def ptr_array(bufs):
     """A C array of device pointers (float *const *) for a list of DeviceBuffers."""
     return (ctypes.c_void_p * len(bufs))(*[_p(b) for b in bufs])
+
+
+class QwenConfig(ctypes.Structure):
+    """NcmQwenConfig of include/ncm_hip.h."""
+    _fields_ = [("n_layer", ctypes.c_int), ("n_embd", ctypes.c_int), ("n_head", ctypes.c_int),
+                ("n_kv", ctypes.c_int), ("n_inner", ctypes.c_int), ("vocab", ctypes.c_int),
+                ("n_ctx", ctypes.c_int), ("rope_theta", ctypes.c_double)]
+
+
+class NcpConfig(ctypes.Structure):
+    """NcmNcpConfig of include/ncm_hip.h."""
+    _fields_ = [("n_layer", ctypes.c_int), ("n_embd", ctypes.c_int), ("n_head", ctypes.c_int),
+                ("n_kv", ctypes.c_int), ("n_inner", ctypes.c_int), ("vocab", ctypes.c_int),
+                ("rope_base", ctypes.c_int), ("use_rmsnorm", ctypes.c_int)]

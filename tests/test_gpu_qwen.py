@@ -1,0 +1,136 @@
+"""Config 4: the Qwen2 decoder on the device against the oracle's restatement
+of qwen_forward (every op pinned to the reference).
+
+Bars: logits max-abs 1e-3 (north star); greedy ids exact (north star).  The
+cached decode is checked against the reference's full-recompute generation,
+and at the full config-4 shape (24 layers, vocab 151936, 2048-token prefill)
+through a size-independent property: the cached step's logits equal the
+last row of a full forward over the extended sequence."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import ncmhip
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+D = ncmhip.DeviceBuffer
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    ncmhip.init(0)
+    ncmhip.load().arena_init(8 << 30)
+    ncmhip.check()
+    print("[gpu] qwen tests on device 0", flush=True)
+
+
+def weights(seed, n_layer, C, H, K, I, V):
+    rng = np.random.default_rng(seed)
+    shapes = O.qwen_shapes(n_layer, C, H, K, I, V)
+    ps = []
+    for i, s in enumerate(shapes):
+        if len(s) == 1 and s[0] == C and (i == len(shapes) - 1 or (i - 1) % 12 in (0, 8)):
+            ps.append((1.0 + 0.02 * rng.standard_normal(s)).astype(np.float32))   # RMSNorm gains
+        else:
+            ps.append((0.02 * rng.standard_normal(s)).astype(np.float32))
+    return ps
+
+
+class Model:
+    def __init__(self, params, n_layer, C, H, K, I, V, n_ctx, theta):
+        self.lib = ncmhip.load()
+        self.bufs = [D.from_numpy(p) for p in params]
+        self.cfg = ncmhip.QwenConfig(n_layer, C, H, K, I, V, n_ctx, theta)
+        self.m = self.lib.ncm_qwen_new(ctypes.byref(self.cfg), ncmhip.ptr_array(self.bufs))
+        ncmhip.check()
+        self.V = V
+
+    def forward(self, ids, last_only=False):
+        ids = np.ascontiguousarray(ids, np.int32)
+        p = self.lib.ncm_qwen_forward(self.m, ids.ctypes.data, ids.size, int(last_only))
+        ncmhip.check()
+        n = self.V if last_only else ids.size * self.V
+        out = np.empty(n, np.float32)
+        self.lib.mem_d2h(out.ctypes.data, p, out.nbytes)
+        ncmhip.check()
+        return out if last_only else out.reshape(ids.size, self.V)
+
+    def decode(self, tok, pos):
+        p = self.lib.ncm_qwen_decode(self.m, int(tok), pos)
+        ncmhip.check()
+        out = np.empty(self.V, np.float32)
+        self.lib.mem_d2h(out.ctypes.data, p, out.nbytes)
+        ncmhip.check()
+        return out
+
+    def generate(self, prompt, n_new, eos=-1):
+        prompt = np.ascontiguousarray(prompt, np.int32)
+        out = np.zeros(n_new, np.int32)
+        n = self.lib.ncm_qwen_generate(self.m, prompt.ctypes.data, prompt.size, n_new, eos, out.ctypes.data)
+        ncmhip.check()
+        return list(out[:n])
+
+    def close(self):
+        self.lib.ncm_qwen_free(self.m)
+
+
+SMALL = dict(n_layer=2, C=896, H=14, K=2, I=4864, V=151936)
+
+
+def test_prefill_logits_vs_oracle():
+    cfg = SMALL
+    params = weights(1, **cfg)
+    ids = np.random.default_rng(2).integers(0, cfg["V"], 37).astype(np.int32)
+    ref = O.qwen_forward(params, theta=1e6, ids=ids, **cfg)
+    m = Model(params, n_ctx=64, theta=1e6, **cfg)
+    try:
+        got = m.forward(ids)
+        assert float(np.max(np.abs(got - ref))) <= 1e-3
+        last = m.forward(ids, last_only=True)
+        assert float(np.max(np.abs(last - ref[-1]))) <= 1e-3
+        assert int(np.argmax(last)) == O.argmax_row(ref[-1])
+    finally:
+        m.close()
+
+
+def test_greedy_generation_vs_full_recompute():
+    cfg = SMALL
+    params = weights(3, **cfg)
+    prompt = np.random.default_rng(4).integers(0, cfg["V"], 21).astype(np.int32)
+    n_new = 8
+    ref_ids, ref_steps = O.qwen_generate(params, theta=1e6, prompt=prompt, n_new=n_new, n_ctx=64, **cfg)
+    m = Model(params, n_ctx=64, theta=1e6, **cfg)
+    try:
+        assert m.generate(prompt, n_new) == ref_ids
+        # per-step cached logits against the full-recompute logits
+        m.forward(prompt, last_only=True)
+        toks = list(prompt)
+        for s in range(1, n_new):
+            toks.append(ref_ids[s - 1])
+            got = m.decode(ref_ids[s - 1], len(toks) - 1)
+            assert float(np.max(np.abs(got - ref_steps[s]))) <= 1e-3
+        # eos stop: the generation ends after the first occurrence of the eos id
+        eos = ref_ids[2]
+        assert m.generate(prompt, n_new, eos=eos) == ref_ids[:ref_ids.index(eos) + 1]
+    finally:
+        m.close()
+
+
+def test_full_size_cached_decode_matches_full_forward():
+    cfg = dict(n_layer=24, C=896, H=14, K=2, I=4864, V=151936)
+    params = weights(5, **cfg)
+    prompt = np.random.default_rng(6).integers(0, cfg["V"], 2048).astype(np.int32)
+    m = Model(params, n_ctx=2304, theta=1e6, **cfg)
+    try:
+        ids = m.generate(prompt, 4)
+        assert len(ids) == 4 and all(0 <= i < cfg["V"] for i in ids)
+        seq = np.concatenate([prompt, np.array(ids[:3], np.int32)])
+        full = m.forward(seq, last_only=True)           # recompute over 2051 tokens
+        m.forward(seq[:-1], last_only=True)              # cache for positions 0..2049
+        step = m.decode(seq[-1], len(seq) - 1)
+        assert float(np.max(np.abs(step - full))) <= 1e-3
+        assert int(np.argmax(full)) == ids[3]
+    finally:
+        m.close()

@@ -234,3 +234,20 @@ def test_sdpa_brute_force_float64():
     p = np.exp(s - s.max(-1, keepdims=True))
     want = (p / p.sum(-1, keepdims=True)) @ vv
     assert np.max(np.abs(O.sdpa_gqa(q, k, v, mask) - want)) < 2e-6
+
+
+def test_ncp_rope_tables():
+    """build_rope (ncp.c:80-92): position 0 is the identity, the first pair's
+    angle is the position itself, cos^2 + sin^2 = 1; the library's host
+    table builder gives the same bits."""
+    import ctypes
+    import ncmhip
+    S, hd = 81, 64
+    c, s = O.rope_tables_ncp(S, hd, 10000)
+    assert np.all(c[0] == 1) and np.all(s[0] == 0)
+    assert bits_equal(c[:, 0], np.cos(np.arange(S, dtype=np.float64)).astype(np.float32))
+    assert np.max(np.abs(c.astype(np.float64) ** 2 + s.astype(np.float64) ** 2 - 1)) < 1e-6
+    assert bits_equal(c[:, :32], c[:, 32:])
+    lc, ls = np.empty_like(c), np.empty_like(s)
+    assert ncmhip.load().ncm_ncp_rope_tables(S, hd, 10000, lc.ctypes.data, ls.ctypes.data) == 0
+    assert bits_equal(lc, c) and bits_equal(ls, s)

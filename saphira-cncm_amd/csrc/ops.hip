@@ -369,147 +369,377 @@ sdpa_rows(const float *__restrict__ q, const float *__restrict__ k, const float 
 }
 
 // ---------------------------------------------------------------- decode (KV cache)
-// One decode position `pos`: RoPE (kernels.c:249-264 arithmetic, table row
-// pos) on q [H][hd] and k [Hkv][hd] (the rows of the q/k projections), q
-// written to qo [H][hd], k and v appended to the caches [Hkv][ld][hd] at
-// row pos.  One thread per (head slot, d < hd/2) over H + Hkv slots, plus
-// the v copy.
-extern "C" __global__ void __launch_bounds__(256)
-rope_append_k(const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
-              const float *__restrict__ cos_t, const float *__restrict__ sin_t, float *__restrict__ qo,
-              float *__restrict__ kc, float *__restrict__ vc, int H, int Hkv, int hd, int ld, int pos) {
-#pragma clang fp contract(off)
-    const int h2 = hd >> 1;
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    const int nrot = (H + Hkv) * h2;
-    if (i < nrot) {
-        const int slot = i / h2, d = i - slot * h2;
-        const float *src = slot < H ? q + slot * hd : k + (slot - H) * hd;
-        float *dst = slot < H ? qo + slot * hd : kc + ((int64_t)(slot - H) * ld + pos) * hd;
-        const float *co = cos_t + (int64_t)pos * hd, *si = sin_t + (int64_t)pos * hd;
-        const float a = src[d], b = src[d + h2];
-        dst[d] = a * co[d] + (-b) * si[d];
-        dst[d + h2] = b * co[d + h2] + a * si[d + h2];
-    } else if (i < nrot + Hkv * hd) {
-        const int j = i - nrot, kvh = j / hd, d = j - kvh * hd;
-        vc[((int64_t)kvh * ld + pos) * hd + d] = v[j];
-    }
-}
-
-// Decode attention, one query row per head over keys [0, Tkv) of the cache:
-// split over key chunks of 256.  A workgroup owns one kv head and one chunk
-// and all rep = H / Hkv query heads of the group (rep <= 16): thread t
-// scores key c*256 + t against every query of the group, the chunk's
-// (max, sum) per query come from block reductions, and o = sum p v with
-// threads (g, d) = 4 key quarters x 64 dims, reduced through LDS.  hd = 64.
-// part_o [H][nchunk][64], part_ml [H][nchunk][2]; sdpa_decode_combine
-// merges the chunks.
-#define DEC_CH 256
+// Decode attention, one query row per head over keys [0, *posp] of the cache,
+// split over chunks of 64 keys.  A workgroup owns one kv head and one chunk
+// and all rep = H / Hkv query heads of the group (rep <= 16).  K and V of the
+// chunk are staged in LDS with coalesced float4 loads; wave w scores the
+// chunk's 64 keys (lane = key) against queries w, w+4, ...; the chunk's
+// (max, sum) per query come from wave reductions; o = sum p v with lane =
+// dimension.  hd = 64.  part_o [H][gridDim.x][64], part_ml [H][gridDim.x][2];
+// sdpa_decode_combine merges the chunks that hold keys.
+#define DEC_CH 64
+#define DEC_LD 68
 extern "C" __global__ void __launch_bounds__(256)
 sdpa_decode_partial(const float *__restrict__ q, const float *__restrict__ kc, const float *__restrict__ vc,
-                    float *__restrict__ part_o, float *__restrict__ part_ml, int H, int Hkv, int Tkv, int ld,
-                    float scale) {
+                    float *__restrict__ part_o, float *__restrict__ part_ml, int H, int Hkv,
+                    const int *__restrict__ posp, int ld, float scale) {
     __shared__ __attribute__((aligned(16))) float sQ[16 * 64];
+    __shared__ __attribute__((aligned(16))) float sK[DEC_CH * DEC_LD];
+    __shared__ __attribute__((aligned(16))) float sV[DEC_CH * 64];
     __shared__ float sP[16 * DEC_CH];
-    __shared__ float sRed[16 * 4];
-    __shared__ float sM[16], sL[16];
-    __shared__ __attribute__((aligned(16))) float sO[4 * 16 * 64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int kvh = blockIdx.y, chunk = blockIdx.x, nchunk = gridDim.x;
     const int rep = H / Hkv, h0 = kvh * rep;
-    const int key = chunk * DEC_CH + tid;
-    for (int i = tid; i < rep * 64; i += 256) sQ[i] = q[(int64_t)h0 * 64 + i];
-    __syncthreads();
-    float s[16];
-    if (key < Tkv) {
-        const float *kr = kc + ((int64_t)kvh * ld + key) * 64;
-        f4 kv[16];
+    const int Tkv = *posp + 1;
+    const int k0 = chunk * DEC_CH;
+    if (k0 >= Tkv) return;    // chunk past the current length (grid sized for n_ctx)
+    const int nk = min(DEC_CH, Tkv - k0);
+    for (int i = tid; i < rep * 16; i += 256) *(f4 *)(sQ + 4 * i) = *(const f4 *)(q + (int64_t)h0 * 64 + 4 * i);
+    const float *kb = kc + ((int64_t)kvh * ld + k0) * 64, *vb = vc + ((int64_t)kvh * ld + k0) * 64;
 #pragma unroll
-        for (int c = 0; c < 16; ++c) kv[c] = *(const f4 *)(kr + 4 * c);
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            if (j < rep) {
-                float acc = 0.f;
-#pragma unroll
-                for (int c = 0; c < 16; ++c) {
-                    const f4 qv = *(const f4 *)(sQ + j * 64 + 4 * c);
-                    acc += qv[0] * kv[c][0] + qv[1] * kv[c][1] + qv[2] * kv[c][2] + qv[3] * kv[c][3];
-                }
-                s[j] = acc * scale;
-            }
+    for (int j = 0; j < 4; ++j) {
+        const int f = tid + 256 * j, r = f >> 4, c = (f & 15) * 4;
+        f4 kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
+        if (r < nk) {
+            kv = *(const f4 *)(kb + r * 64 + c);
+            vv = *(const f4 *)(vb + r * 64 + c);
         }
-    } else {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) s[j] = -INFINITY;
-    }
-    // per-query chunk max
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        if (j < rep) {
-            float m = s[j];
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-            if (lane == 0) sRed[j * 4 + wave] = m;
-        }
+        *(f4 *)(sK + r * DEC_LD + c) = kv;
+        *(f4 *)(sV + r * 64 + c) = vv;
     }
     __syncthreads();
-    if (tid < rep) sM[tid] = fmaxf(fmaxf(sRed[tid * 4], sRed[tid * 4 + 1]), fmaxf(sRed[tid * 4 + 2], sRed[tid * 4 + 3]));
-    __syncthreads();
+    // scores: wave w, queries j = w, w+4, ... (lane = key)
+    for (int j = wave; j < rep; j += 4) {
+        float acc = 0.f;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        if (j < rep) {
-            const float m = sM[j];
-            const float p = (m == -INFINITY || key >= Tkv) ? 0.f : __expf(s[j] - m);
-            sP[j * DEC_CH + tid] = p;
-            float l = p;
+        for (int c = 0; c < 16; ++c) {
+            const f4 kv = *(const f4 *)(sK + lane * DEC_LD + 4 * c);
+            const f4 qv = *(const f4 *)(sQ + j * 64 + 4 * c);
+            acc += (qv[0] * kv[0] + qv[1] * kv[1]) + (qv[2] * kv[2] + qv[3] * kv[3]);
+        }
+        const float sc = lane < nk ? acc * scale : -INFINITY;
+        float m = sc;
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
-            if (lane == 0) sRed[j * 4 + wave] = l;
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        const float p = lane < nk ? __expf(sc - m) : 0.f;
+        float l = p;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+        sP[j * DEC_CH + lane] = p;
+        if (lane == 0) {
+            part_ml[((int64_t)(h0 + j) * nchunk + chunk) * 2] = m;
+            part_ml[((int64_t)(h0 + j) * nchunk + chunk) * 2 + 1] = l;
         }
     }
     __syncthreads();
-    if (tid < rep) sL[tid] = (sRed[tid * 4] + sRed[tid * 4 + 1]) + (sRed[tid * 4 + 2] + sRed[tid * 4 + 3]);
-    // o partial: wave g sums keys 64g .. 64g+63 for every query, lane = d
-    float acc[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) acc[j] = 0.f;
-    const int kbase = chunk * DEC_CH + wave * 64;
-    const int kn = min(64, Tkv - kbase);
-    for (int t = 0; t < kn; ++t) {
-        const float vv = vc[((int64_t)kvh * ld + kbase + t) * 64 + lane];
-#pragma unroll
-        for (int j = 0; j < 16; ++j)
-            if (j < rep) acc[j] += sP[j * DEC_CH + wave * 64 + t] * vv;
-    }
-#pragma unroll
-    for (int j = 0; j < 16; ++j)
-        if (j < rep) sO[(wave * 16 + j) * 64 + lane] = acc[j];
-    __syncthreads();
-    for (int i = tid; i < rep * 64; i += 256) {
-        const int j = i >> 6, d = i & 63;
-        const float o = (sO[(0 * 16 + j) * 64 + d] + sO[(1 * 16 + j) * 64 + d]) +
-                        (sO[(2 * 16 + j) * 64 + d] + sO[(3 * 16 + j) * 64 + d]);
-        part_o[((int64_t)(h0 + j) * nchunk + chunk) * 64 + d] = o;
-    }
-    if (tid < rep) {
-        part_ml[((int64_t)(h0 + tid) * nchunk + chunk) * 2] = sM[tid];
-        part_ml[((int64_t)(h0 + tid) * nchunk + chunk) * 2 + 1] = sL[tid];
+    // o[j][d] = sum_key p[j][key] v[key][d]: wave w, queries w, w+4, ...; lane = d
+    for (int j = wave; j < rep; j += 4) {
+        float o = 0.f;
+#pragma unroll 8
+        for (int t = 0; t < DEC_CH; ++t) o += sP[j * DEC_CH + t] * sV[t * 64 + lane];
+        part_o[((int64_t)(h0 + j) * nchunk + chunk) * 64 + lane] = o;
     }
 }
 
-// out[h][d] = sum_c o_c[d] e^(m_c - m) / sum_c l_c e^(m_c - m); one wave per head.
+// out[h][d] = sum_c o_c[d] e^(m_c - m) / sum_c l_c e^(m_c - m); one wave per
+// head: lanes load the chunks' (max, sum) pairs (64 at a time), the weights
+// are broadcast back with shuffles while lane = d accumulates o.
 extern "C" __global__ void __launch_bounds__(64)
 sdpa_decode_combine(const float *__restrict__ part_o, const float *__restrict__ part_ml, float *__restrict__ out,
-                    int nchunk) {
-    const int h = blockIdx.x, d = threadIdx.x;
+                    int stride, const int *__restrict__ posp) {
+    const int h = blockIdx.x, lane = threadIdx.x;
+    const int nchunk = (*posp + DEC_CH) / DEC_CH;
+    const float *ml = part_ml + (int64_t)h * stride * 2, *po = part_o + (int64_t)h * stride * 64;
     float m = -INFINITY;
-    for (int c = 0; c < nchunk; ++c) m = fmaxf(m, part_ml[((int64_t)h * nchunk + c) * 2]);
+    for (int c = lane; c < nchunk; c += 64) m = fmaxf(m, ml[2 * c]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
     float l = 0.f, o = 0.f;
-    for (int c = 0; c < nchunk; ++c) {
-        const float mc = part_ml[((int64_t)h * nchunk + c) * 2];
-        const float w = mc == -INFINITY ? 0.f : __expf(mc - m);
-        l += part_ml[((int64_t)h * nchunk + c) * 2 + 1] * w;
-        o += part_o[((int64_t)h * nchunk + c) * 64 + d] * w;
+    for (int c0 = 0; c0 < nchunk; c0 += 64) {
+        const int c = c0 + lane;
+        float w = 0.f, lc = 0.f;
+        if (c < nchunk) {
+            const float mc = ml[2 * c];
+            w = mc == -INFINITY ? 0.f : __expf(mc - m);
+            lc = ml[2 * c + 1] * w;
+        }
+        l += lc;
+        // loads of every chunk issued unconditionally (clamped index, weight 0
+        // past the last chunk) so they overlap
+#pragma unroll 16
+        for (int t = 0; t < 64; ++t) {
+            const float wt = __shfl(w, t, 64);
+            o += po[(int64_t)min(c0 + t, nchunk - 1) * 64 + lane] * wt;
+        }
     }
-    out[(int64_t)h * 64 + d] = o / l;
+#pragma unroll
+    for (int s = 32; s > 0; s >>= 1) l += __shfl_xor(l, s, 64);
+    out[(int64_t)h * 64 + lane] = o / l;
+}
+
+// ---------------------------------------------------------------- decode GEMV
+// y = W x for one input row, a wave per output row (RW rows per wave, 4
+// waves), the input staged once per workgroup in LDS -- optionally RMS-
+// normalised on the way (rmsnorm_fwd's arithmetic: fp64 sum of squares,
+// s = (float)(1/sqrt(ms/K + 1e-6)), xn = (x*s)*nw).  Each wave issues the
+// loads of its first PRE float4 per lane and row before the input prologue,
+// so the weight stream overlaps the staging.
+//   mode 0: rows index the concatenation of up to three matrices; res (one
+//           matrix) is added last.
+//   mode 1: row n pairs W0 and W1: y0[n] = silu(W0 x + b0)[n] * (W1 x + b1)[n]
+//           (the reference's silu_fwd + mul_fwd).
+//   mode 2: q | k | v projections of one decode position with RoPE and the
+//           cache append fused (hd = 64): a wave computes the rotation pair
+//           (d, d + 32) of a q or k head, rotates it with the table row *posp
+//           (kernels.c:249-264 arithmetic) and writes q to y0 [H][64], k to
+//           kc[kvh][*posp], v rows (in pairs) to vc[kvh][*posp].
+// K % 4 == 0, 16-byte aligned rows, K <= 8192.
+struct DecGemvArgs {
+    const float *x, *nw, *res;
+    const float *W[3];
+    const float *b[3];
+    float *y[3];
+    int N[3];
+    int K, mode;
+    const float *cos_t, *sin_t;
+    const int *posp;
+    float *kc, *vc;
+    int ld;
+};
+
+#define DEC_KMAX 8192
+
+// row (in the concatenated row space) of the i-th dot product of this wave
+__device__ __forceinline__ void dec_rows(const DecGemvArgs &p, int unit, int i, int &m, int &row) {
+    if (p.mode == 2) {
+        const int qk_pairs = (p.N[0] + p.N[1]) >> 1;
+        if (unit < qk_pairs) {
+            const int head = unit >> 5, d = unit & 31;
+            row = head * 64 + d + 32 * i;          // within q | k
+        } else {
+            row = p.N[0] + p.N[1] + 2 * (unit - qk_pairs) + i;
+        }
+    } else if (p.mode == 1) {
+        m = i;
+        return;
+    } else {
+        row = unit;
+    }
+    m = 0;
+    if (row >= p.N[0]) { row -= p.N[0]; m = 1; }
+    if (m == 1 && row >= p.N[1]) { row -= p.N[1]; m = 2; }
+}
+
+template <int RW, int PRE, int DOTS, int XPT>
+__device__ __forceinline__ void dec_gemv_body(const DecGemvArgs &p) {
+#pragma clang fp contract(off)
+    __shared__ __attribute__((aligned(16))) float xs[DEC_KMAX];
+    __shared__ double red[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int K = p.K, K4 = K >> 2;
+    // units: mode 0 rows, mode 1 row pairs (gate, up), mode 2 RoPE / v pairs
+    const int units = p.mode == 0 ? p.N[0] + p.N[1] + p.N[2]
+                      : p.mode == 1 ? p.N[0] : (p.N[0] + p.N[1] + p.N[2]) >> 1;
+    const int u0 = (blockIdx.x * 4 + wave) * RW;
+    const float *wr[RW][DOTS];
+    int um[RW][DOTS], urow[RW][DOTS];
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int i = 0; i < DOTS; ++i) {
+            int m = 0, row = 0;
+            dec_rows(p, min(u0 + r, units - 1), i, m, row);
+            if (p.mode == 1) row = min(u0 + r, units - 1);
+            um[r][i] = m;
+            urow[r][i] = row;
+            wr[r][i] = p.W[m] + (int64_t)row * K;
+        }
+    f4 pw[RW][DOTS][PRE];
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int i = 0; i < DOTS; ++i)
+#pragma unroll
+            for (int e = 0; e < PRE; ++e) {
+                const int c = lane + 64 * e;
+                pw[r][i][e] = c < K4 ? __builtin_nontemporal_load((const f4 *)wr[r][i] + c) : f4{0.f, 0.f, 0.f, 0.f};
+            }
+    // input: all of this thread's float4 loads issued together (K <= 1024 XPT)
+    f4 xv4[XPT], nv4[XPT];
+#pragma unroll
+    for (int e = 0; e < XPT; ++e) {
+        const int c = tid + 256 * e;
+        xv4[e] = c < K4 ? *(const f4 *)(p.x + 4 * c) : f4{0.f, 0.f, 0.f, 0.f};
+        nv4[e] = (p.nw && c < K4) ? *(const f4 *)(p.nw + 4 * c) : f4{1.f, 1.f, 1.f, 1.f};
+    }
+    if (p.nw) {
+        double ss = 0.0;
+#pragma unroll
+        for (int e = 0; e < XPT; ++e)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ss += (double)xv4[e][i] * (double)xv4[e][i];
+        ss = wave_sum_d(ss);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        const double ms = (((red[0] + red[1]) + red[2]) + red[3]) / K;
+        const float s = (float)(1.0 / sqrt(ms + 1e-6));
+#pragma unroll
+        for (int e = 0; e < XPT; ++e)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xv4[e][i] = (xv4[e][i] * s) * nv4[e][i];
+    }
+#pragma unroll
+    for (int e = 0; e < XPT; ++e) {
+        const int c = tid + 256 * e;
+        if (c < K4) *(f4 *)(xs + 4 * c) = xv4[e];
+    }
+    __syncthreads();
+    float acc[RW][DOTS];
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int i = 0; i < DOTS; ++i) acc[r][i] = 0.f;
+#pragma unroll
+    for (int e = 0; e < PRE; ++e) {
+        const int c = lane + 64 * e;
+        if (c < K4) {
+            const f4 xv = *(const f4 *)(xs + 4 * c);
+#pragma unroll
+            for (int r = 0; r < RW; ++r)
+#pragma unroll
+                for (int i = 0; i < DOTS; ++i)
+                    acc[r][i] += (pw[r][i][e].x * xv.x + pw[r][i][e].y * xv.y) +
+                                 (pw[r][i][e].z * xv.z + pw[r][i][e].w * xv.w);
+        }
+    }
+    for (int c = lane + 64 * PRE; c < K4; c += 64) {
+        const f4 xv = *(const f4 *)(xs + 4 * c);
+#pragma unroll
+        for (int r = 0; r < RW; ++r)
+#pragma unroll
+            for (int i = 0; i < DOTS; ++i) {
+                const f4 w = __builtin_nontemporal_load((const f4 *)wr[r][i] + c);
+                acc[r][i] += (w.x * xv.x + w.y * xv.y) + (w.z * xv.z + w.w * xv.w);
+            }
+    }
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        const float a0 = wave_sum(acc[r][0]);
+        const float a1 = DOTS == 2 ? wave_sum(acc[r][DOTS - 1]) : 0.f;
+        const int unit = u0 + r;
+        if (lane != 0 || unit >= units) continue;
+        if (p.mode == 0) {
+            const int m = um[r][0], row = urow[r][0];
+            float v = p.b[m] ? a0 + p.b[m][row] : a0;
+            if (p.res) v = p.res[row] + v;
+            p.y[m][row] = v;
+        } else if (p.mode == 1) {
+            const float g = p.b[0] ? a0 + p.b[0][unit] : a0;
+            const float u = p.b[1] ? a1 + p.b[1][unit] : a1;
+            p.y[0][unit] = ncm_act(g, ACT_SILU) * u;
+        } else {
+            const int pos = *p.posp;
+            const int m0 = um[r][0], row0 = urow[r][0], m1 = um[r][DOTS - 1], row1 = urow[r][DOTS - 1];
+            const float v0 = p.b[m0] ? a0 + p.b[m0][row0] : a0;
+            const float v1 = p.b[m1] ? a1 + p.b[m1][row1] : a1;
+            if (m0 == 2) {      // v rows: plain append
+                p.vc[((int64_t)(row0 >> 6) * p.ld + pos) * 64 + (row0 & 63)] = v0;
+                p.vc[((int64_t)(row1 >> 6) * p.ld + pos) * 64 + (row1 & 63)] = v1;
+            } else {
+                const int d = row0 & 63;          // 0..31; row1 = row0 + 32
+                const float *co = p.cos_t + (int64_t)pos * 64, *si = p.sin_t + (int64_t)pos * 64;
+                const float y0 = v0 * co[d] + (-v1) * si[d];
+                const float y1 = v1 * co[d + 32] + v0 * si[d + 32];
+                float *dst = m0 == 0 ? p.y[0] + (row0 & ~63)
+                                     : p.kc + ((int64_t)(row0 >> 6) * p.ld + pos) * 64;
+                dst[d] = y0;
+                dst[d + 32] = y1;
+            }
+        }
+    }
+}
+
+// d<DOTS>: dot products per unit (1 for mode 0, 2 for modes 1 and 2);
+// x<XPT>: input float4 per thread (K <= 1024 XPT)
+#define DEC_GEMV(name, RW, PRE, DOTS, XPT) \
+    extern "C" __global__ void __launch_bounds__(256) name(DecGemvArgs p) { dec_gemv_body<RW, PRE, DOTS, XPT>(p); }
+DEC_GEMV(dec_gemv_d1_r1_p4_x1, 1, 4, 1, 1)
+DEC_GEMV(dec_gemv_d1_r4_p4_x1, 4, 4, 1, 1)
+DEC_GEMV(dec_gemv_d1_r1_p20_x5, 1, 20, 1, 5)
+DEC_GEMV(dec_gemv_d1_r1_p8_x8, 1, 8, 1, 8)
+DEC_GEMV(dec_gemv_d2_r1_p4_x1, 1, 4, 2, 1)
+DEC_GEMV(dec_gemv_d2_r2_p4_x1, 2, 4, 2, 1)
+DEC_GEMV(dec_gemv_d2_r1_p8_x8, 1, 8, 2, 8)
+
+// Position-driven pieces of a decode step, so that the step's launches do
+// not change from one token to the next (it can be replayed as one graph):
+// the token id is ids[*pos]; dec_argmax_part_k + dec_argmax_final_k write
+// the greedy id of the logits to ids[*pos + 1] (argmax_rows_k's rule) and
+// advance *pos.
+extern "C" __global__ void __launch_bounds__(256)
+dec_embed_k(const float *__restrict__ W, const int *__restrict__ ids, const int *__restrict__ pos,
+            float *__restrict__ x, int D, int V) {
+    int id = ids[*pos];
+    if ((unsigned)id >= (unsigned)V) id = 0;
+    for (int d = blockIdx.x * 256 + threadIdx.x; d < D; d += gridDim.x * 256) x[d] = W[(int64_t)id * D + d];
+}
+
+#define AMAX_PER 4096
+// Stage 1: per block of AMAX_PER logits the first maximal value and its index
+// (strict '>' scan per thread, ties to the lower index when merging).
+extern "C" __global__ void __launch_bounds__(256)
+dec_argmax_part_k(const float *__restrict__ x, int n, float *__restrict__ pv, int *__restrict__ pi) {
+    __shared__ float bv[4];
+    __shared__ int bi[4];
+    const int tid = threadIdx.x, base = blockIdx.x * AMAX_PER;
+    float best = -INFINITY;
+    int bidx = 0x7fffffff;
+#pragma unroll 16
+    for (int j = 0; j < AMAX_PER / 256; ++j) {
+        const int k = base + j * 256 + tid;
+        const float v = k < n ? x[k] : -INFINITY;
+        if (v > best) { best = v; bidx = k; }
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const int oi = __shfl_xor(bidx, o, 64);
+        if (ov > best || (ov == best && oi < bidx)) { best = ov; bidx = oi; }
+    }
+    if ((tid & 63) == 0) { bv[tid >> 6] = best; bi[tid >> 6] = bidx; }
+    __syncthreads();
+    if (tid == 0) {
+        float b = bv[0];
+        int i = bi[0];
+        for (int w = 1; w < 4; ++w)
+            if (bv[w] > b || (bv[w] == b && bi[w] < i)) { b = bv[w]; i = bi[w]; }
+        pv[blockIdx.x] = b;
+        pi[blockIdx.x] = i;
+    }
+}
+
+// Stage 2: merge the blocks, apply the reference's rule (index 0 when x[0]
+// is NaN or nothing exceeds x[0] = -inf), write ids[*pos + 1], advance *pos.
+extern "C" __global__ void __launch_bounds__(64)
+dec_argmax_final_k(const float *__restrict__ x, const float *__restrict__ pv, const int *__restrict__ pi,
+                   int nblk, int *__restrict__ ids, int *__restrict__ pos) {
+    const int lane = threadIdx.x;
+    float best = -INFINITY;
+    int bidx = 0x7fffffff;
+    for (int j = lane; j < nblk; j += 64) {
+        const float v = pv[j];
+        const int i = pi[j];
+        if (v > best || (v == best && i < bidx)) { best = v; bidx = i; }
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const int oi = __shfl_xor(bidx, o, 64);
+        if (ov > best || (ov == best && oi < bidx)) { best = ov; bidx = oi; }
+    }
+    if (lane == 0) {
+        int i = bidx;
+        if (x[0] != x[0] || i == 0x7fffffff) i = 0;
+        const int p = *pos;
+        ids[p + 1] = i;
+        *pos = p + 1;
+    }
 }

@@ -34,8 +34,13 @@ struct NcmQwen {
     float *kcache, *vcache; /* [n_layer][K][n_ctx][hd] */
     /* decode scratch */
     float *x, *h1, *q, *k, *v, *qr, *ctx, *x1, *h2, *gate, *up, *logits, *part_o, *part_ml;
-    int *ids_dev;           /* generated ids, one slot per position */
+    int *ids_dev;           /* token ids, one slot per position */
+    int *pos_dev;           /* position of the current decode step (device) */
+    float *amax_v;          /* greedy-argmax block partials */
+    int *amax_i, amax_blocks;
     int nchunk_max;
+    hipGraphExec_t step_graph; /* one decode step + argmax, replayed per token */
+    int graph_state;        /* 0 not built, 1 built, -1 capture failed (eager) */
 };
 
 int ncm_qwen_param_count(const NcmQwenConfig *c) { return c ? 2 + QW_PER_LAYER * c->n_layer : 0; }
@@ -75,6 +80,10 @@ void ncm_qwen_free(NcmQwen *m) {
                      m->x1, m->h2, m->gate, m->up, m->logits, m->part_o, m->part_ml};
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++) ncm_hip_free(bufs[i]);
     ncm_hip_free(m->ids_dev);
+    ncm_hip_free(m->pos_dev);
+    ncm_hip_free(m->amax_v);
+    ncm_hip_free(m->amax_i);
+    if (m->graph_state == 1) hipGraphExecDestroy(m->step_graph);
     free(m->P);
     free(m);
 }
@@ -114,7 +123,7 @@ NcmQwen *ncm_qwen_new(const NcmQwenConfig *c, float *const *params) {
     memcpy(m->P, params, (size_t)n * sizeof(float *));
     const int C = c->n_embd, hd = C / c->n_head, KH = c->n_kv * hd, I = c->n_inner;
     const size_t cache = (size_t)c->n_layer * c->n_kv * c->n_ctx * hd * sizeof(float);
-    m->nchunk_max = (c->n_ctx + 255) / 256;
+    m->nchunk_max = (c->n_ctx + 63) / 64;    /* decode attention chunks of 64 keys */
 #define ALLOC(f, bytes) if (!(m->f = (float *)ncm_hip_malloc(bytes))) goto fail
     ALLOC(cos_t, (size_t)c->n_ctx * hd * 4);
     ALLOC(sin_t, (size_t)c->n_ctx * hd * 4);
@@ -136,6 +145,10 @@ NcmQwen *ncm_qwen_new(const NcmQwenConfig *c, float *const *params) {
     ALLOC(part_ml, (size_t)c->n_head * m->nchunk_max * 2 * 4);
 #undef ALLOC
     if (!(m->ids_dev = (int *)ncm_hip_malloc((size_t)(c->n_ctx + 1) * sizeof(int)))) goto fail;
+    if (!(m->pos_dev = (int *)ncm_hip_malloc(sizeof(int)))) goto fail;
+    m->amax_blocks = (c->vocab + 4095) / 4096;
+    if (!(m->amax_v = (float *)ncm_hip_malloc((size_t)m->amax_blocks * sizeof(float)))) goto fail;
+    if (!(m->amax_i = (int *)ncm_hip_malloc((size_t)m->amax_blocks * sizeof(int)))) goto fail;
     if (build_rope(m)) goto fail;
     return m;
 fail:
@@ -211,93 +224,204 @@ float *ncm_qwen_forward(NcmQwen *m, const int *ids, int T, int last_only) {
     return logits;
 }
 
-/* One cached decode step: the token id at ids_dev[pos] (device) at position
- * pos (the cache holds positions 0..pos-1).  Logits [V] in the model's
- * buffer; returns it. */
-static float *decode_step(NcmQwen *m, int pos) {
+/* Decode GEMV launch (dec_gemv_r*): rows of up to three matrices, optional
+ * fused RMSNorm of x, mode 1 = SwiGLU pair, res added in mode 0. */
+typedef struct {
+    const float *x, *nw, *res;
+    const float *W[3];
+    const float *b[3];
+    float *y[3];
+    int N[3];
+    int K, mode;
+    const float *cos_t, *sin_t;
+    const int *posp;
+    float *kc, *vc;
+    int ld;
+} DecGemvArgs;
+
+/* Mode 0/1 launch (mode 2 sets the RoPE fields in dec_qkv). */
+static int dec_launch(DecGemvArgs *a) {
+    int units, dots = a->mode == 0 ? 1 : 2;
+    if (a->mode == 0) units = a->N[0] + a->N[1] + a->N[2];
+    else if (a->mode == 1) units = a->N[0];
+    else units = (a->N[0] + a->N[1] + a->N[2]) / 2;
+    const char *k;
+    int rw = 1;
+    if (dots == 1) {
+        if (a->K <= 1024) {
+            if (units >= 16 * 1024) { k = "dec_gemv_d1_r4_p4_x1"; rw = 4; }
+            else k = "dec_gemv_d1_r1_p4_x1";
+        } else {
+            k = a->K <= 5120 ? "dec_gemv_d1_r1_p20_x5" : "dec_gemv_d1_r1_p8_x8";
+        }
+    } else if (a->K <= 1024) {
+        if (units >= 4096) { k = "dec_gemv_d2_r2_p4_x1"; rw = 2; }
+        else k = "dec_gemv_d2_r1_p4_x1";
+    } else {
+        k = "dec_gemv_d2_r1_p8_x8";
+    }
+    void *args[] = {a};
+    return ncm_launch_named(k, (unsigned)((units + 4 * rw - 1) / (4 * rw)), 1, 1, 256, args);
+}
+
+static int dec_gemv(const float *x, const float *nw, const float *res, int nmat, const float *const *W,
+                    const float *const *b, float *const *y, const int *N, int K, int mode) {
+    DecGemvArgs a;
+    memset(&a, 0, sizeof(a));
+    a.x = x; a.nw = nw; a.res = res; a.K = K; a.mode = mode;
+    for (int i = 0; i < nmat; i++) {
+        a.W[i] = W[i]; a.b[i] = b[i]; a.y[i] = y[i]; a.N[i] = N[i];
+    }
+    return dec_launch(&a);
+}
+
+/* One cached decode step at position *pos_dev for the token ids_dev[*pos_dev]
+ * (the cache holds positions 0..pos-1): logits [V] into m->logits.  Every
+ * launch has the same arguments at every position. */
+static int decode_core(NcmQwen *m) {
     const NcmQwenConfig *c = &m->c;
-    const int C = c->n_embd, H = c->n_head, K = c->n_kv, hd = C / H, I = c->n_inner, V = c->vocab;
+    const int C = c->n_embd, H = c->n_head, K = c->n_kv, hd = C / H, I = c->n_inner, V = c->vocab, KH = K * hd;
     float *const *P = m->P;
-    embedding_fwd_v(P[0], V, m->ids_dev + pos, m->x, 1, C);
-    float *h = m->x;
-    const int nchunk = (pos + 1 + 255) / 256;
+    {
+        void *a[] = {(void *)&P[0], &m->ids_dev, &m->pos_dev, &m->x, (void *)&C, (void *)&V};
+        if (ncm_launch_named("dec_embed_k", (unsigned)((C + 255) / 256), 1, 1, 256, a)) return -1;
+    }
     for (int li = 0; li < c->n_layer; li++) {
         float *const *w = P + 1 + QW_PER_LAYER * li;
         float *kc = m->kcache + (size_t)li * K * c->n_ctx * hd, *vc = m->vcache + (size_t)li * K * c->n_ctx * hd;
-        rmsnorm_fwd(h, w[0], m->h1, 1, C);
-        linear_fwd(m->h1, w[1], w[2], m->q, 1, C, C);
-        linear_fwd(m->h1, w[3], w[4], m->k, 1, K * hd, C);
-        linear_fwd(m->h1, w[5], w[6], m->v, 1, K * hd, C);
-        {
-            int n_thr = (H + K) * (hd / 2) + K * hd, ld = c->n_ctx;
-            void *a[] = {&m->q, &m->k, &m->v, &m->cos_t, &m->sin_t, &m->qr, &kc, &vc, (void *)&H, (void *)&K,
-                         (void *)&hd, &ld, &pos};
-            if (ncm_launch_named("rope_append_k", (unsigned)((n_thr + 255) / 256), 1, 1, 256, a)) return NULL;
+        {   /* rmsnorm + q | k | v + RoPE + cache append */
+            DecGemvArgs a;
+            memset(&a, 0, sizeof(a));
+            a.x = m->x; a.nw = w[0]; a.K = C; a.mode = 2;
+            a.W[0] = w[1]; a.W[1] = w[3]; a.W[2] = w[5];
+            a.b[0] = w[2]; a.b[1] = w[4]; a.b[2] = w[6];
+            a.y[0] = m->qr;
+            a.N[0] = C; a.N[1] = KH; a.N[2] = KH;
+            a.cos_t = m->cos_t; a.sin_t = m->sin_t; a.posp = m->pos_dev;
+            a.kc = kc; a.vc = vc; a.ld = c->n_ctx;
+            if (dec_launch(&a)) return -1;
         }
         {
-            int tkv = pos + 1, ld = c->n_ctx;
+            int ld = c->n_ctx, stride = m->nchunk_max;
             float scale = 1.0f / sqrtf((float)hd);
-            void *a[] = {&m->qr, &kc, &vc, &m->part_o, &m->part_ml, (void *)&H, (void *)&K, &tkv, &ld, &scale};
-            if (ncm_launch_named("sdpa_decode_partial", (unsigned)nchunk, (unsigned)K, 1, 256, a)) return NULL;
-            int nc = nchunk;
-            void *a2[] = {&m->part_o, &m->part_ml, &m->ctx, &nc};
-            if (ncm_launch_named("sdpa_decode_combine", (unsigned)H, 1, 1, 64, a2)) return NULL;
+            void *a[] = {&m->qr, &kc, &vc, &m->part_o, &m->part_ml, (void *)&H, (void *)&K, &m->pos_dev, &ld, &scale};
+            if (ncm_launch_named("sdpa_decode_partial", (unsigned)m->nchunk_max, (unsigned)K, 1, 256, a)) return -1;
+            void *a2[] = {&m->part_o, &m->part_ml, &m->ctx, &stride, &m->pos_dev};
+            if (ncm_launch_named("sdpa_decode_combine", (unsigned)H, 1, 1, 64, a2)) return -1;
         }
-        /* ctx [H][1][hd] is already the merged row [C] */
-        linear_fwd_ep(m->ctx, w[7], NULL, h, m->x1, 1, C, C, NCM_ACT_NONE);
-        rmsnorm_fwd(m->x1, w[8], m->h2, 1, C);
-        linear_fwd_ep(m->h2, w[9], NULL, NULL, m->gate, 1, I, C, NCM_ACT_SILU);
-        linear_fwd(m->h2, w[10], NULL, m->up, 1, I, C);
-        mul_fwd(m->gate, m->up, m->up, I);
-        linear_fwd_ep(m->up, w[11], NULL, m->x1, m->x, 1, C, I, NCM_ACT_NONE);   /* h = x1 + down */
+        {   /* x1 = x + o_proj(ctx)   (ctx [H][hd] is the merged row) */
+            const float *W[1] = {w[7]}, *b[1] = {NULL};
+            float *y[1] = {m->x1};
+            int N[1] = {C};
+            if (dec_gemv(m->ctx, NULL, m->x, 1, W, b, y, N, C, 0)) return -1;
+        }
+        {   /* gu = silu(gate(rmsnorm(x1))) * up(rmsnorm(x1)) */
+            const float *W[2] = {w[9], w[10]}, *b[2] = {NULL, NULL};
+            float *y[2] = {m->up, NULL};
+            int N[2] = {I, I};
+            if (dec_gemv(m->x1, w[8], NULL, 2, W, b, y, N, C, 1)) return -1;
+        }
+        {   /* x = x1 + down(gu) */
+            const float *W[1] = {w[11]}, *b[1] = {NULL};
+            float *y[1] = {m->x};
+            int N[1] = {C};
+            if (dec_gemv(m->up, NULL, m->x1, 1, W, b, y, N, I, 0)) return -1;
+        }
     }
     const int n = ncm_qwen_param_count(c);
-    rmsnorm_fwd(h, P[n - 1], m->h1, 1, C);
-    linear_fwd(m->h1, P[0], NULL, m->logits, 1, V, C);
-    return m->logits;
+    const float *W[1] = {P[0]}, *b[1] = {NULL};
+    float *y[1] = {m->logits};
+    int N[1] = {V};
+    return dec_gemv(m->x, P[n - 1], NULL, 1, W, b, y, N, C, 0);
+}
+
+/* greedy id of logits -> ids[*pos + 1], *pos += 1 (two launches) */
+static int greedy_next(NcmQwen *m, const float *logits) {
+    int V = m->c.vocab;
+    void *a[] = {(void *)&logits, &V, &m->amax_v, &m->amax_i};
+    if (ncm_launch_named("dec_argmax_part_k", (unsigned)m->amax_blocks, 1, 1, 256, a)) return -1;
+    void *a2[] = {(void *)&logits, &m->amax_v, &m->amax_i, &m->amax_blocks, &m->ids_dev, &m->pos_dev};
+    return ncm_launch_named("dec_argmax_final_k", 1, 1, 1, 64, a2);
+}
+
+static int decode_argmax(NcmQwen *m) { return greedy_next(m, m->logits); }
+
+static int decode_ok(const NcmQwen *m, const char *fn) {
+    const int hd = m->c.n_embd / m->c.n_head;
+    if (hd != 64 || m->c.n_head / m->c.n_kv > 16 || m->c.n_embd % 4 || m->c.n_inner % 4 || m->c.n_embd > 8192 ||
+        m->c.n_inner > 8192)
+        return ncm_fail(NCM_E_ARG, "%s: decode needs hd = 64, <= 16 query heads per kv head, C and I "
+                                   "multiples of 4 and at most 8192", fn);
+    return 0;
 }
 
 float *ncm_qwen_decode(NcmQwen *m, int id, int pos) {
     if (!m || pos < 1 || pos >= m->c.n_ctx) { ncm_fail(NCM_E_ARG, "ncm_qwen_decode: bad position"); return NULL; }
-    if (ncm_ready()) return NULL;
-    if (m->c.n_embd / m->c.n_head != 64 || m->c.n_head / m->c.n_kv > 16) {
-        ncm_fail(NCM_E_ARG, "ncm_qwen_decode: needs hd = 64 and at most 16 query heads per kv head");
-        return NULL;
-    }
+    if (ncm_ready() || decode_ok(m, "ncm_qwen_decode")) return NULL;
     mem_h2d(m->ids_dev + pos, &id, sizeof(int));
-    return decode_step(m, pos);
+    mem_h2d(m->pos_dev, &pos, sizeof(int));
+    return decode_core(m) ? NULL : m->logits;
+}
+
+/* Captures decode_core + decode_argmax once; later steps replay it. */
+static int step_graph(NcmQwen *m) {
+    if (m->graph_state != 0 || getenv("NCM_NO_GRAPH")) return m->graph_state == 1;
+    hipStream_t s = ncm_stream();
+    hipGraph_t g = NULL;
+    m->graph_state = -1;
+    if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) return 0;
+    int rc = decode_core(m) || decode_argmax(m);
+    hipError_t e = hipStreamEndCapture(s, &g);
+    if (rc || e != hipSuccess || !g) {
+        if (g) hipGraphDestroy(g);
+        ncm_fail(NCM_E_HIP, "qwen: decode graph capture failed");
+        return 0;
+    }
+    e = hipGraphInstantiate(&m->step_graph, g, NULL, NULL, 0);
+    hipGraphDestroy(g);
+    if (e != hipSuccess) return ncm_fail(NCM_E_HIP, "qwen: graph instantiate: %s", hipGetErrorString(e)), 0;
+    m->graph_state = 1;
+    return 1;
+}
+
+static int decode_token(NcmQwen *m) {
+    if (step_graph(m)) {
+        hipError_t e = hipGraphLaunch(m->step_graph, ncm_stream());
+        if (e != hipSuccess) return ncm_fail(NCM_E_HIP, "qwen: graph launch: %s", hipGetErrorString(e));
+        return 0;
+    }
+    return decode_core(m) || decode_argmax(m);
 }
 
 /* Greedy generation (qwen_generate with temp 0, qwen.c:204-228): prefill of
- * the prompt, then n_new steps of argmax + cached decode.  The ids stay on
- * the device (argmax_rows writes the next id where the next step reads it);
- * with eos >= 0 each step is synchronised to stop at eos as the reference
- * does, with eos < 0 all steps run without a host round trip.  Returns the
- * number of ids written to out. */
+ * the prompt, then n_new steps of argmax + cached decode.  The ids and the
+ * position stay on the device (each step's argmax writes the next id where
+ * the next step reads it and advances the position), so one captured graph
+ * per model replays every step (NCM_NO_GRAPH=1 launches the same kernels
+ * one by one instead).  With eos >= 0 each step is synchronised to stop at
+ * eos as the reference does; with eos < 0 all steps run without a host
+ * round trip.  Returns the number of ids written to out. */
 int ncm_qwen_generate(NcmQwen *m, const int *prompt, int np, int n_new, int eos, int *out) {
     if (!m || !prompt || np <= 0 || n_new < 0 || !out) { ncm_fail(NCM_E_ARG, "ncm_qwen_generate: bad arguments"); return -1; }
     if (np + n_new > m->c.n_ctx) { ncm_fail(NCM_E_ARG, "ncm_qwen_generate: context overflow"); return -1; }
-    if (m->c.n_embd / m->c.n_head != 64 || m->c.n_head / m->c.n_kv > 16) {
-        ncm_fail(NCM_E_ARG, "ncm_qwen_generate: needs hd = 64 and at most 16 query heads per kv head");
-        return -1;
-    }
+    if (ncm_ready() || decode_ok(m, "ncm_qwen_generate")) return -1;
     if (n_new == 0) return 0;
     float *lg = ncm_qwen_forward(m, prompt, np, 1);
     if (!lg) return -1;
-    argmax_rows(lg, m->ids_dev + np, 1, m->c.vocab);
+    /* the prefill's greedy id goes to ids[np]; *pos becomes np */
+    int p0 = np - 1;
+    mem_h2d(m->pos_dev, &p0, sizeof(int));
+    if (greedy_next(m, lg)) return -1;
     int made = 1;
     if (eos >= 0) {
         mem_d2h(out, m->ids_dev + np, sizeof(int));
         if (out[0] == eos) return 1;
     }
     for (int s = 1; s < n_new; s++) {
-        const int pos = np + s - 1;   /* position of the id generated last */
-        float *l = decode_step(m, pos);
-        if (!l || ncm_ready()) return -1;
-        argmax_rows(l, m->ids_dev + pos + 1, 1, m->c.vocab);
+        if (decode_token(m)) return -1;
         made++;
         if (eos >= 0) {
-            mem_d2h(out + s, m->ids_dev + pos + 1, sizeof(int));
+            mem_d2h(out + s, m->ids_dev + np + s, sizeof(int));
             if (out[s] == eos) return made;
         }
     }

@@ -134,3 +134,28 @@ def test_full_size_cached_decode_matches_full_forward():
         assert int(np.argmax(full)) == ids[3]
     finally:
         m.close()
+
+
+def test_decode_graph_replays_match_eager(monkeypatch):
+    """The captured decode step, replayed over several generations with eager
+    work and synchronisation in between, gives the ids of the same kernels
+    launched one by one."""
+    cfg = SMALL
+    params = weights(7, **cfg)
+    rng = np.random.default_rng(8)
+    p1, p2 = rng.integers(0, cfg["V"], 19).astype(np.int32), rng.integers(0, cfg["V"], 33).astype(np.int32)
+    eager = Model(params, n_ctx=64, theta=1e6, **cfg)
+    graph = Model(params, n_ctx=64, theta=1e6, **cfg)
+    try:
+        monkeypatch.setenv("NCM_NO_GRAPH", "1")
+        e1, e2 = eager.generate(p1, 12), eager.generate(p2, 12)
+        monkeypatch.delenv("NCM_NO_GRAPH")
+        g1 = graph.generate(p1, 12)
+        graph.forward(p2[:10], last_only=True)          # eager work between replays
+        ncmhip.sync()
+        g2 = graph.generate(p2, 12)
+        g3 = graph.generate(p1, 12)
+        assert g1 == e1 and g2 == e2 and g3 == e1
+    finally:
+        eager.close()
+        graph.close()

@@ -40,6 +40,13 @@ PEAK_HBM_GBS = 8000.0
 SHAPES = [(768, 2304), (768, 3072), (3072, 768), (896, 4864), (4864, 896)]  # (K, N)
 MS = [1, 64, 512, 4096]
 CPU_MS = [1, 64, 512]
+# HBM bytes per launch of the roofline kernel over its standalone launches,
+# measured with two rocprofv3 counter passes (FETCH_SIZE, then WRITE_SIZE) of
+# "bench.py --steps 2 --warmup 1 --no-cpu --no-extras --copy-calibration",
+# each scaled by what the counter reads for the run's 256 MiB copies; valid
+# while the same kernel and launches are the roofline.
+TRAFFIC = {("gemm_dx_v", ("dX M=4096 3072->768", "dX M=4096 4864->896", "dX M=4096 896->4864",
+                          "dX M=512 4864->896")): 228.5e6}
 
 
 def build_workload(ncmhip, seed=0):
@@ -259,6 +266,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip configs 1, 3, 4, 5")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run 3 device-to-device copies of 256 MiB (the known-size kernel the HBM "
+                         "counters of a rocprofv3 --pmc run are scaled by)")
     ap.add_argument("--cpu-baseline-child", action="store_true")
     args = ap.parse_args()
     if args.cpu_baseline_child:
@@ -273,6 +283,12 @@ def main():
 
     import ncmhip
     ncmhip.init(0)
+    if args.copy_calibration:
+        src, dst = ncmhip.DeviceBuffer(256 << 20), ncmhip.DeviceBuffer(256 << 20)
+        for _ in range(3):
+            ncmhip.load().mem_d2d(dst.ptr, src.ptr, 256 << 20)
+        ncmhip.check()
+        del src, dst
     calls, keep = build_workload(ncmhip)
     ncmhip.sync()
     for _ in range(args.warmup):
@@ -344,7 +360,7 @@ def main():
                      "peak": PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_TFLOPS, 4),
                      "avg_launch_us": round(dms / dn * 1e3, 3), "launches_per_step": dn // args.steps,
                      "launches": sorted(dlabels),
-                     "traffic": None},
+                     "traffic": TRAFFIC.get((dom, tuple(sorted(dlabels))))},
         "kernels": {k: {"ms_per_step": round(v[0] / args.steps, 4),
                         "tflops": round(v[1] / (v[0] / 1e3) / 1e12, 3) if v[1] else None}
                     for k, v in sorted(per_kernel.items(), key=lambda kv: -kv[1][0])},

@@ -14,7 +14,8 @@ timed steps, inputs resident in HBM.  Each call is bracketed by HIP events
 on the library stream, which gives every kernel's average launch duration
 for the roofline entry: the dominant kernel's average is taken over its
 launches that run alone (no split-tile fixup launched by the same call), so
-the event-bracketed time is that kernel's own duration.
+the event-bracketed time is that kernel's own duration.  The roofline
+kernel is the one with the most time in such standalone launches.
 
 The CPU baseline runs the reference's own CPU code (oracle/_ref/libref.so,
 compiled from the reference sources) in a child process on a bounded sample
@@ -45,8 +46,8 @@ CPU_MS = [1, 64, 512]
 # "bench.py --steps 2 --warmup 1 --no-cpu --no-extras --copy-calibration",
 # each scaled by what the counter reads for the run's 256 MiB copies; valid
 # while the same kernel and launches are the roofline.
-TRAFFIC = {("gemm_dx_v", ("dX M=4096 3072->768", "dX M=4096 4864->896", "dX M=4096 896->4864",
-                          "dX M=512 4864->896")): 228.5e6}
+TRAFFIC = {("gemm64_dx_v", ("dX M=4096 3072->768", "dX M=4096 4864->896", "dX M=4096 896->4864",
+                            "dX M=512 4864->896")): 263.4e6}
 
 
 def build_workload(ncmhip, seed=0):
@@ -334,7 +335,9 @@ def main():
     total_flops = sum(c[1] for c in calls) * args.steps
     t = max(gpu_ms / 1e3, 1e-12)
     value = total_flops / t / 1e12
-    dom = max((k for k in per_kernel if per_kernel[k][1] > 0 and k in solo), key=lambda k: per_kernel[k][0])
+    # roofline kernel: the one with the most time in launches that run alone
+    # (a split call adds a fixup launch inside the same event bracket)
+    dom = max((k for k in solo if solo[k][1] > 0), key=lambda k: solo[k][0])
     dms, dfl, dn, dlabels = solo[dom]
     achieved = dfl / (dms / 1e3) / 1e12
 

@@ -11,32 +11,25 @@
 //   dW       dW = dy^T. x : A(i,k) = dy[k*M+i]  (i-contiguous)
 //                          B(k,j) = x[k*K+j]   (j-contiguous)
 //
-// Tiling: a 256-thread workgroup owns a 128x128 output tile; each of its four
-// 64-lane waves owns a 64x64 sub-tile of 4x4 MFMA blocks.  Operand slabs of
-// BK = 32 go global -> registers -> LDS (two LDS buffers) and are consumed as
-// two 16-wide chunks.  Per slab and wave (128 MFMAs):
-//   chunk 0 MFMAs, interleaved with: LDS reads of chunk 1, LDS writes of the
-//       next slab (other buffer), global loads of the slab after next;
-//   one barrier;
-//   chunk 1 MFMAs, interleaved with the LDS reads of the next slab's chunk 0.
-// The interleaving is imposed with scheduling-group barriers, so the matrix
-// pipe keeps issuing while the memory traffic is in flight.  Global loads are
-// raw buffer loads: lanes outside the matrix get an offset beyond the buffer
-// and read zero, so the loop body has no branches.
+// Tiling: a 256-thread workgroup owns a 64x64 output tile; each of its four
+// 64-lane waves owns a 32x32 sub-tile of 2x2 MFMA blocks.  Operand slabs of
+// BK = 32 go global -> registers -> LDS (two buffers) and are consumed as two
+// 16-wide chunks; the small register (~90 VGPRs) and LDS (36 KB) footprint
+// lets four workgroups share a CU, whose interleaving hides the load and
+// barrier latency.  Both operands are kept k-contiguous in LDS: a slab whose
+// memory layout is i/j-contiguous is transposed by its LDS store.  Global
+// loads are raw buffer loads: lanes outside the matrix get an offset beyond
+// the buffer and read zero, so the loop body has no branches.
 //
 // k-permutation: inside every 16-wide chunk, MFMA step s (0..3) gives lane
 // group g = lane/16 the reduction index k = 4g + s, for both operands.  The
 // MFMA sums over all 16 (g, s) pairs, so the product is unchanged, but every
-// operand read becomes a 128-bit LDS load:
-//   k-contiguous operand : one float4 along k per lane covers all 4 steps;
-//   i/j-contiguous operand: one float4 along i/j per lane and step covers 4
-//                           MFMA blocks whose rows (cols) interleave with
-//                           stride 4 (block u of a 64-wide group holds rows
-//                           4*lane16 + u).
+// operand fragment becomes one 128-bit LDS read (a float4 along k covers the
+// 4 steps).
 //
 // Scheduling: tiles [0, dp_tiles) run whole, one workgroup each; every other
 // tile is cut into `segs` k-segments that fill the last round of the chip.
-// Segments store partial tiles; gemm_fixup (a second launch) sums them in
+// Segments store partial tiles; gemm64_fixup (a second launch) sums them in
 // segment order -- deterministic -- and applies the epilogue.
 //
 // Accuracy: MFMAs accumulate 128 k into `acc`, which is then added into `tot`;
@@ -54,11 +47,11 @@ struct GemmArgs {
     float *C;
     const float *bias;   // [No] or null (STORE only)
     const float *res;    // [Mo, ldc] or null (STORE only)
-    float *ws;           // partial tiles of split tiles [units][BM*BN]
+    float *ws;           // partial tiles of split tiles [units][64*64]
     int Mo, No, K;
     int lda, ldb, ldc;
     int act;
-    int vec_out;         // output rows 16-byte aligned and No % 4 == 0
+    int vec_out;         // unused by the 64x64 kernels (kept for the host's struct layout)
     int tiles_m, tiles_n;
     int iters;           // BK slabs per tile (a multiple of 4)
     int dp_tiles;        // blocks [0, dp_tiles): one whole tile each
@@ -66,15 +59,9 @@ struct GemmArgs {
     unsigned a_bytes, b_bytes;  // extents of A and B for the buffer descriptors
 };
 
-#define GEMM_BM 128
-#define GEMM_BN 128
 #define GEMM_BK 32
 #define GEMM_NT 256
 #define OOB_OFFSET 0x80000000u
-#ifndef GEMM_LDS_PAD
-#define GEMM_LDS_PAD 8   // floats of padding per LDS tile row: a 40-float pitch makes the
-                         // k-contiguous fragment reads (16 rows x 16 B per 16 lanes) hit all 64 banks
-#endif
 
 // Grouped raster: GROUP_M tile rows advance together along N so that the B
 // panels they share stay in L2.
@@ -97,321 +84,6 @@ __device__ __forceinline__ int xcd_remap(int j, int n) {
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const float *base, unsigned bytes) {
     return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)bytes, 0x00020000);
-}
-
-// One operand tile of ROWS x COLS floats per slab, as laid out in memory
-// (row stride ld); the slab index moves along columns (KALONG_COLS) or rows.
-// Thread t owns the float4s f = t + j*NT (j < PER): since NT is a multiple
-// of the float4s per row, all of them share one column and sit RSTEP rows
-// apart, so the whole per-thread state is three registers.
-template <int ROWS, int COLS, bool KALONG_COLS, bool VEC>
-struct SlabLoader {
-    static constexpr int F4 = ROWS * COLS / 4;
-    static constexpr int PER = F4 / GEMM_NT;
-    static constexpr int RSTEP = GEMM_NT / (COLS / 4);
-    static_assert(F4 % GEMM_NT == 0 && GEMM_NT % (COLS / 4) == 0, "tile must split evenly");
-    int row0, col0;        // global row / column of this thread's first float4 (slab 0)
-    int lds0;              // LDS float offset of that float4
-    f4 r[PER];
-
-    __device__ __forceinline__ void init(int fix0, int k0, int tid) {
-        const int rr = tid / (COLS / 4), cc = (tid % (COLS / 4)) * 4;
-        lds0 = rr * (COLS + GEMM_LDS_PAD) + cc;
-        row0 = (KALONG_COLS ? fix0 : k0) + rr;
-        col0 = (KALONG_COLS ? k0 : fix0) + cc;
-    }
-
-    // slab kt (k advanced by kt*BK); rows >= row_lim / columns >= col_lim read zero
-    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, int ld, int kt, int row_lim, int col_lim) {
-        const int dk = kt * GEMM_BK;
-        const int c = col0 + (KALONG_COLS ? dk : 0);
-#pragma unroll
-        for (int j = 0; j < PER; ++j) {
-            const int rw = row0 + j * RSTEP + (KALONG_COLS ? 0 : dk);
-            const unsigned o = (unsigned)(rw * ld + c) * 4u;
-            if (VEC) {
-                const unsigned oo = (rw < row_lim && c < col_lim) ? o : OOB_OFFSET;
-                r[j] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, oo, 0, 0));
-            } else {
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const unsigned oo = (rw < row_lim && c + u < col_lim) ? o + 4u * u : OOB_OFFSET;
-                    r[j][u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, oo, 0, 0));
-                }
-            }
-        }
-    }
-
-    __device__ __forceinline__ void store(float *buf) const {
-#pragma unroll
-        for (int j = 0; j < PER; ++j) *(f4 *)(buf + lds0 + j * RSTEP * (COLS + GEMM_LDS_PAD)) = r[j];
-    }
-};
-
-// Epilogue of one tile from the per-thread accumulators.  tot[a][b][r] holds
-// MFMA row rho = 4*lg + r, column gamma = li.
-template <int TM, int TN, int WM, int WN, bool AKC, bool BKC, int EPI, int ACT>
-__device__ __forceinline__ void gemm_epilogue_act(const GemmArgs &p, const f4 (&tot)[TM][TN], int i0, int j0, int tid,
-                                                  int a_lo, int a_hi) {
-    const int lane = tid & 63, wave = tid >> 6;
-    const int wm = wave / (GEMM_BN / WN), wn = wave % (GEMM_BN / WN);
-    const int li = lane & 15, lg = lane >> 4;
-#pragma unroll
-    for (int a = 0; a < TM; ++a) {
-        if (a < a_lo || a >= a_hi) continue;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int rho = 4 * lg + r;
-            const int row = i0 + wm * WM + (AKC ? a * 16 + rho : (a >> 2) * 64 + 4 * rho + (a & 3));
-            if (row >= p.Mo) continue;
-            float *orow = p.C + (int64_t)row * p.ldc;
-            const float *rrow = (EPI == EPI_STORE && p.res) ? p.res + (int64_t)row * p.ldc : nullptr;
-            if (!BKC && p.vec_out) {
-                // the four blocks b = 4q+u hold columns 4*li + u: one float4 per q
-#pragma unroll
-                for (int q = 0; q < TN / 4; ++q) {
-                    const int col = j0 + wn * WN + q * 64 + 4 * li;
-                    if (col >= p.No) continue;
-                    f4 v = {tot[a][4 * q][r], tot[a][4 * q + 1][r], tot[a][4 * q + 2][r], tot[a][4 * q + 3][r]};
-                    f4 *o = (f4 *)(orow + col);
-                    if (EPI == EPI_ACCUM) v += *o;
-                    *o = v;
-                }
-                continue;
-            }
-#pragma unroll
-            for (int b = 0; b < TN; ++b) {
-                const int col = j0 + wn * WN + (BKC ? b * 16 + li : (b >> 2) * 64 + 4 * li + (b & 3));
-                if (col >= p.No) continue;
-                float v = tot[a][b][r];
-                if (EPI == EPI_STORE) {
-                    if (p.bias) v += p.bias[col];
-                    v = ncm_act(v, ACT);
-                    if (rrow) v = rrow[col] + v;
-                    orow[col] = v;
-                } else {
-                    orow[col] += v;
-                }
-            }
-        }
-    }
-}
-
-// The activation is dispatched once per tile, so every instantiation is a
-// short straight-line epilogue.
-template <int TM, int TN, int WM, int WN, bool AKC, bool BKC, int EPI>
-__device__ __forceinline__ void gemm_epilogue(const GemmArgs &p, const f4 (&tot)[TM][TN], int i0, int j0, int tid,
-                                              int a_lo = 0, int a_hi = TM) {
-    if (EPI == EPI_ACCUM) {
-        gemm_epilogue_act<TM, TN, WM, WN, AKC, BKC, EPI, ACT_NONE>(p, tot, i0, j0, tid, a_lo, a_hi);
-        return;
-    }
-    switch (p.act) {
-    case ACT_SILU: gemm_epilogue_act<TM, TN, WM, WN, AKC, BKC, EPI, ACT_SILU>(p, tot, i0, j0, tid, a_lo, a_hi); break;
-    case ACT_GELU: gemm_epilogue_act<TM, TN, WM, WN, AKC, BKC, EPI, ACT_GELU>(p, tot, i0, j0, tid, a_lo, a_hi); break;
-    case ACT_GELU_TANH: gemm_epilogue_act<TM, TN, WM, WN, AKC, BKC, EPI, ACT_GELU_TANH>(p, tot, i0, j0, tid, a_lo, a_hi); break;
-    default: gemm_epilogue_act<TM, TN, WM, WN, AKC, BKC, EPI, ACT_NONE>(p, tot, i0, j0, tid, a_lo, a_hi); break;
-    }
-}
-
-template <bool AKC, bool BKC, int EPI, bool VEC>
-__device__ __forceinline__ void gemm_body(const GemmArgs &p) {
-    constexpr int BM = GEMM_BM, BN = GEMM_BN, BK = GEMM_BK, WM = 64, WN = 64;
-    constexpr int WAVES_N = BN / WN;
-    constexpr int TM = WM / 16, TN = WN / 16;
-    constexpr int A_ROWS = AKC ? BM : BK, A_COLS = AKC ? BK : BM;
-    constexpr int B_ROWS = BKC ? BN : BK, B_COLS = BKC ? BK : BN;
-    constexpr int A_LD = A_COLS + GEMM_LDS_PAD, B_LD = B_COLS + GEMM_LDS_PAD;
-    constexpr int A_SZ = A_ROWS * A_LD, B_SZ = B_ROWS * B_LD;
-    __shared__ __attribute__((aligned(16))) float smem[2 * (A_SZ + B_SZ)];
-    float *const sA = smem;               // buffers sA + {0, A_SZ}
-    float *const sB = smem + 2 * A_SZ;    // buffers sB + {0, B_SZ}
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
-    const int li = lane & 15, lg = lane >> 4;
-
-    // ---- which tile and which k-range ----
-    int tile, it0, it1, unit = -1;
-    {
-        const int b = blockIdx.x;
-        if (b < p.dp_tiles) {
-            tile = xcd_remap(b, p.dp_tiles);
-            it0 = 0;
-            it1 = p.iters;
-        } else {
-            const int ntail = (p.tiles_m * p.tiles_n - p.dp_tiles) * p.segs;
-            const int j = b - p.dp_tiles;
-            unit = ((p.dp_tiles & 7) == 0) ? xcd_remap(j, ntail) : j;
-            const int tail = unit / p.segs;
-            const int seg = unit - tail * p.segs;
-            tile = p.dp_tiles + tail;
-            // segment boundaries on multiples of 4 slabs
-            const int q4 = p.iters >> 2;
-            it0 = (int)((int64_t)seg * q4 / p.segs) * 4;
-            it1 = (int)((int64_t)(seg + 1) * q4 / p.segs) * 4;
-        }
-    }
-    int tm, tn;
-    tile_rc<8>(tile, p.tiles_m, p.tiles_n, tm, tn);
-    const int i0 = tm * BM, j0 = tn * BN;
-    const int nk = it1 - it0;               // multiple of 4
-    const int kend = min(p.K, it1 * BK);
-
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, p.a_bytes);
-    const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.B, p.b_bytes);
-    SlabLoader<A_ROWS, A_COLS, AKC, VEC> la;
-    SlabLoader<B_ROWS, B_COLS, BKC, VEC> lb;
-    la.init(i0, it0 * BK, tid);
-    lb.init(j0, it0 * BK, tid);
-    // bounds: (rows, cols) of A and B as stored
-    const int a_rl = AKC ? p.Mo : kend, a_cl = AKC ? kend : p.Mo;
-    const int b_rl = BKC ? p.No : kend, b_cl = BKC ? kend : p.No;
-
-    // Fragments of one 16-wide chunk.  k-contiguous: f[t] = row block t,
-    // component = MFMA step.  i-contiguous: f[s * TM/4 + q] = step s, group q,
-    // component = row block 4q + u.  Same for B.
-    auto frags = [&](const float *a_s, const float *b_s, int kc, f4 *fa, f4 *fb) {
-        if (AKC) {
-#pragma unroll
-            for (int t = 0; t < TM; ++t)
-                fa[t] = *(const f4 *)(a_s + (wm * WM + t * 16 + li) * A_LD + kc * 16 + 4 * lg);
-        } else {
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-#pragma unroll
-                for (int q = 0; q < TM / 4; ++q)
-                    fa[s * (TM / 4) + q] = *(const f4 *)(a_s + (kc * 16 + 4 * lg + s) * A_LD + wm * WM + q * 64 + 4 * li);
-        }
-        if (BKC) {
-#pragma unroll
-            for (int t = 0; t < TN; ++t)
-                fb[t] = *(const f4 *)(b_s + (wn * WN + t * 16 + li) * B_LD + kc * 16 + 4 * lg);
-        } else {
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-#pragma unroll
-                for (int q = 0; q < TN / 4; ++q)
-                    fb[s * (TN / 4) + q] = *(const f4 *)(b_s + (kc * 16 + 4 * lg + s) * B_LD + wn * WN + q * 64 + 4 * li);
-        }
-    };
-
-    f4 acc[TM][TN], tot[TM][TN];
-#pragma unroll
-    for (int a = 0; a < TM; ++a)
-#pragma unroll
-        for (int b = 0; b < TN; ++b) acc[a][b] = tot[a][b] = f4{0.f, 0.f, 0.f, 0.f};
-
-    auto mfmas = [&](const f4 *fa, const f4 *fb) {
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-#pragma unroll
-            for (int a = 0; a < TM; ++a) {
-                const float av = AKC ? fa[a][s] : fa[s * (TM / 4) + (a >> 2)][a & 3];
-#pragma unroll
-                for (int b = 0; b < TN; ++b) {
-                    const float bv = BKC ? fb[b][s] : fb[s * (TN / 4) + (b >> 2)][b & 3];
-                    acc[a][b] = mfma4(av, bv, acc[a][b]);
-                }
-            }
-    };
-
-    // prologue: slab 0 -> LDS buffer 0, slab 1 in registers, chunk 0 fragments
-    f4 fa0[TM], fb0[TN], fa1[TM], fb1[TN];
-    la.load(ra, p.lda, 0, a_rl, a_cl);
-    lb.load(rb, p.ldb, 0, b_rl, b_cl);
-    la.store(sA);
-    lb.store(sB);
-    la.load(ra, p.lda, 1, a_rl, a_cl);
-    lb.load(rb, p.ldb, 1, b_rl, b_cl);
-    __syncthreads();
-    frags(sA, sB, 0, fa0, fb0);
-
-    // slab kt lives in buffer kt&1; slabs >= nk read zeros and are never used
-    auto slab = [&](int kt, const int cur) {
-        const float *a_s = sA + cur * A_SZ, *b_s = sB + cur * B_SZ;
-        // chunk 0 MFMAs || chunk 1 fragments, next slab -> other buffer, slab kt+2 loads
-        frags(a_s, b_s, 1, fa1, fb1);
-        la.store(sA + (cur ^ 1) * A_SZ);
-        lb.store(sB + (cur ^ 1) * B_SZ);
-        la.load(ra, p.lda, kt + 2, a_rl, a_cl);
-        lb.load(rb, p.ldb, kt + 2, b_rl, b_cl);
-        mfmas(fa0, fb0);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // 2 LDS reads
-            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);   // 2 MFMA
-            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);   // 1 LDS write
-            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // 1 global load
-            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-        }
-        __syncthreads();
-        // chunk 1 MFMAs || next slab's chunk 0 fragments
-        frags(sA + (cur ^ 1) * A_SZ, sB + (cur ^ 1) * B_SZ, 0, fa0, fb0);
-        mfmas(fa1, fb1);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
-            __builtin_amdgcn_sched_group_barrier(0x008, 8, 1);
-        }
-    };
-
-    for (int kt = 0; kt < nk; kt += 4) {
-        slab(kt, 0);
-        slab(kt + 1, 1);
-        slab(kt + 2, 0);
-        slab(kt + 3, 1);
-#pragma unroll
-        for (int a = 0; a < TM; ++a)
-#pragma unroll
-            for (int b = 0; b < TN; ++b) {
-                tot[a][b] += acc[a][b];
-                acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
-            }
-    }
-
-    if (unit >= 0) {
-        // split tile: publish the partial; gemm_fixup finishes the tile
-        float *mine = p.ws + (int64_t)unit * (BM * BN);
-#pragma unroll
-        for (int a = 0; a < TM; ++a)
-#pragma unroll
-            for (int b = 0; b < TN; ++b) *(f4 *)(mine + ((a * TN + b) * GEMM_NT + tid) * 4) = tot[a][b];
-        return;
-    }
-    gemm_epilogue<TM, TN, WM, WN, AKC, BKC, EPI>(p, tot, i0, j0, tid);
-}
-
-// Sum of the segment partials of split tile blockIdx.x in segment order,
-// then the epilogue (same thread -> element mapping as gemm_body).  Each
-// workgroup finishes one of the TM row blocks (blockIdx.y), so a tile's
-// partials are read by TM CUs in parallel.
-template <bool AKC, bool BKC, int EPI>
-__device__ __forceinline__ void gemm_fixup_body(const GemmArgs &p) {
-    constexpr int TM = 4, TN = 4;
-    const int tid = threadIdx.x;
-    const int tail = blockIdx.x;
-    const int a0 = blockIdx.y;
-    int tm, tn;
-    tile_rc<8>(p.dp_tiles + tail, p.tiles_m, p.tiles_n, tm, tn);
-    const float *first = p.ws + (int64_t)tail * p.segs * (GEMM_BM * GEMM_BN);
-    f4 tot[TM][TN];
-#pragma unroll
-    for (int a = 0; a < TM; ++a)
-#pragma unroll
-        for (int b = 0; b < TN; ++b) tot[a][b] = f4{0.f, 0.f, 0.f, 0.f};
-    for (int sg = 0; sg < p.segs; ++sg) {
-        const f4 *src = (const f4 *)(first + (int64_t)sg * (GEMM_BM * GEMM_BN));
-#pragma unroll
-        for (int a = 0; a < TM; ++a) {
-            if (a != a0) continue;
-#pragma unroll
-            for (int b = 0; b < TN; ++b) tot[a][b] += __builtin_nontemporal_load(src + (a * TN + b) * GEMM_NT + tid);
-        }
-    }
-    gemm_epilogue<TM, TN, 64, 64, AKC, BKC, EPI>(p, tot, tm * GEMM_BM, tn * GEMM_BN, tid, a0, a0 + 1);
 }
 
 // db[m] += (float) sum_r dy[r,m], the bias gradient of train_tape.c:708-713,
@@ -662,25 +334,6 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &p) {
 }
 
 // ---- instantiations (extern "C" names are looked up by the host runtime) ----
-#define GEMM_KERNEL(name, AKC, BKC, EPI, VEC)                                                  \
-    extern "C" __global__ void __launch_bounds__(GEMM_NT, 1) name(GemmArgs p) {                \
-        gemm_body<AKC, BKC, EPI, VEC>(p);                                                      \
-    }
-#define FIXUP_KERNEL(name, AKC, BKC, EPI)                                                      \
-    extern "C" __global__ void __launch_bounds__(GEMM_NT) name(GemmArgs p) {                   \
-        gemm_fixup_body<AKC, BKC, EPI>(p);                                                     \
-    }
-
-GEMM_KERNEL(gemm_fwd_v, true,  true,  EPI_STORE, true)
-GEMM_KERNEL(gemm_fwd_s, true,  true,  EPI_STORE, false)
-GEMM_KERNEL(gemm_dx_v,  true,  false, EPI_ACCUM, true)
-GEMM_KERNEL(gemm_dx_s,  true,  false, EPI_ACCUM, false)
-GEMM_KERNEL(gemm_dw_v,  false, false, EPI_ACCUM, true)
-GEMM_KERNEL(gemm_dw_s,  false, false, EPI_ACCUM, false)
-FIXUP_KERNEL(gemm_fixup_fwd, true,  true,  EPI_STORE)
-FIXUP_KERNEL(gemm_fixup_dx,  true,  false, EPI_ACCUM)
-FIXUP_KERNEL(gemm_fixup_dw,  false, false, EPI_ACCUM)
-
 #define GEMV_KERNEL(name, NB, R, VEC) \
     extern "C" __global__ void __launch_bounds__(256) name(GemvArgs p) { gemv_body<NB, R, VEC>(p); }
 
@@ -694,3 +347,234 @@ GEMV_KERNEL(gemv_b1_r1_s, 1, 1, false)
 GEMV_KERNEL(gemv_b2_r1_s, 2, 1, false)
 GEMV_KERNEL(gemv_b4_r1_s, 4, 1, false)
 GEMV_KERNEL(gemv_b8_r1_s, 8, 1, false)
+
+// ---------------------------------------------------------------- GEMM (64x64 tiles)
+// Per slab: store the slab loaded in the previous iteration to the free LDS
+// buffer, issue the loads of the slab after it, run the 32 MFMAs of the
+// current buffer, barrier.  The 36-float LDS pitch makes the fragment reads
+// conflict-free.
+#define G64 64
+#define G64_LD (GEMM_BK + 4)
+// LDS element (row, k) of a slab lives at row * G64_LD + swz(row, k): the
+// float4 group of k is XORed with (row >> 4) & 3.  Fragment reads (16
+// consecutive rows, one float4 each) keep a constant XOR and stay one aligned
+// float4; the transposing stores of an i/j-contiguous slab (rows 4c + u,
+// c = 0..15) then fall on 64 distinct banks instead of 16.
+__device__ __forceinline__ int g64_swz(int row, int k) { return ((((k >> 2) ^ (row >> 4)) & 7) << 2) | (k & 3); }
+
+template <bool KC, bool VEC>
+struct Slab64 {
+    // KC: memory [64 rows][K] (k along columns); else memory [K][64 cols]
+    f4 r[2];
+    int a0, b0;   // KC: row (t >> 3) + {0, 32}, k (t & 7) * 4;  !KC: k (t >> 4) + {0, 16}, i (t & 15) * 4
+    __device__ __forceinline__ void init(int tid) {
+        if (KC) { a0 = tid >> 3; b0 = (tid & 7) * 4; }
+        else { a0 = tid >> 4; b0 = (tid & 15) * 4; }
+    }
+    // fix0: first row (KC) / column (!KC) of the tile; k0: first k of the slab
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, int ld, int fix0, int k0, int fix_lim,
+                                         int k_lim) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int rw = KC ? fix0 + a0 + 32 * j : k0 + a0 + 16 * j;
+            const int cl = KC ? k0 + b0 : fix0 + b0;
+            const bool in_r = KC ? rw < fix_lim : rw < k_lim;
+            const int lim_c = KC ? k_lim : fix_lim;
+            const unsigned o = (unsigned)(rw * ld + cl) * 4u;
+            if (VEC) {
+                r[j] = __builtin_bit_cast(
+                    f4, __builtin_amdgcn_raw_buffer_load_b128(rs, (in_r && cl < lim_c) ? o : OOB_OFFSET, 0, 0));
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    r[j][u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                            rs, (in_r && cl + u < lim_c) ? o + 4u * u : OOB_OFFSET, 0, 0));
+            }
+        }
+    }
+    __device__ __forceinline__ void store(float *buf) const {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            if (KC) {
+                const int row = a0 + 32 * j;
+                *(f4 *)(buf + row * G64_LD + g64_swz(row, b0)) = r[j];
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int row = b0 + u;
+                    buf[row * G64_LD + g64_swz(row, a0 + 16 * j)] = r[j][u];
+                }
+            }
+        }
+    }
+};
+
+template <int ACT, int EPI>
+__device__ __forceinline__ void g64_out(const GemmArgs &p, int i, int j, float v) {
+    if (i >= p.Mo || j >= p.No) return;
+    float *c = p.C + (int64_t)i * p.ldc + j;
+    if (EPI == EPI_ACCUM) {
+        *c = *c + v;
+    } else {
+        if (p.bias) v += p.bias[j];
+        v = ncm_act(v, ACT);
+        if (p.res) v = p.res[(int64_t)i * p.ldc + j] + v;
+        *c = v;
+    }
+}
+
+// tot[a][b][r]: row wm*32 + a*16 + 4*lg + r, column wn*32 + b*16 + li
+template <int EPI, int ACT>
+__device__ __forceinline__ void g64_epilogue_act(const GemmArgs &p, const f4 (&tot)[2][2], int i0, int j0, int tid) {
+    const int lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
+    const int li = lane & 15, lg = lane >> 4;
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                g64_out<ACT, EPI>(p, i0 + wm * 32 + a * 16 + 4 * lg + r, j0 + wn * 32 + b * 16 + li, tot[a][b][r]);
+}
+
+template <int EPI>
+__device__ __forceinline__ void g64_epilogue(const GemmArgs &p, const f4 (&tot)[2][2], int i0, int j0, int tid) {
+    if (EPI == EPI_ACCUM) { g64_epilogue_act<EPI, ACT_NONE>(p, tot, i0, j0, tid); return; }
+    switch (p.act) {
+    case ACT_SILU: g64_epilogue_act<EPI, ACT_SILU>(p, tot, i0, j0, tid); break;
+    case ACT_GELU: g64_epilogue_act<EPI, ACT_GELU>(p, tot, i0, j0, tid); break;
+    case ACT_GELU_TANH: g64_epilogue_act<EPI, ACT_GELU_TANH>(p, tot, i0, j0, tid); break;
+    default: g64_epilogue_act<EPI, ACT_NONE>(p, tot, i0, j0, tid); break;
+    }
+}
+
+template <bool AKC, bool BKC, int EPI, bool VEC>
+__device__ __forceinline__ void gemm64_body(const GemmArgs &p) {
+    __shared__ __attribute__((aligned(16))) float sA[2 * G64 * G64_LD];
+    __shared__ __attribute__((aligned(16))) float sB[2 * G64 * G64_LD];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1, li = lane & 15, lg = lane >> 4;
+
+    int tile, it0, it1, unit = -1;
+    {
+        const int b = blockIdx.x;
+        if (b < p.dp_tiles) {
+            tile = xcd_remap(b, p.dp_tiles);
+            it0 = 0;
+            it1 = p.iters;
+        } else {
+            const int ntail = (p.tiles_m * p.tiles_n - p.dp_tiles) * p.segs;
+            const int j = b - p.dp_tiles;
+            unit = ((p.dp_tiles & 7) == 0) ? xcd_remap(j, ntail) : j;
+            const int tail = unit / p.segs, seg = unit - tail * p.segs;
+            tile = p.dp_tiles + tail;
+            const int q4 = p.iters >> 2;
+            it0 = (int)((int64_t)seg * q4 / p.segs) * 4;
+            it1 = (int)((int64_t)(seg + 1) * q4 / p.segs) * 4;
+        }
+    }
+    int tm, tn;
+    tile_rc<8>(tile, p.tiles_m, p.tiles_n, tm, tn);
+    const int i0 = tm * G64, j0 = tn * G64;
+    const int kend = min(p.K, it1 * GEMM_BK);
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, p.a_bytes), rb = make_rsrc(p.B, p.b_bytes);
+    Slab64<AKC, VEC> la;
+    Slab64<BKC, VEC> lb;
+    la.init(tid);
+    lb.init(tid);
+
+    f4 acc[2][2], tot[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) acc[a][b] = tot[a][b] = f4{0.f, 0.f, 0.f, 0.f};
+
+    auto chunk = [&](const float *a_s, const float *b_s, int kc) {
+        f4 fa[2], fb[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int ra_ = wm * 32 + t * 16 + li, rb_ = wn * 32 + t * 16 + li;
+            fa[t] = *(const f4 *)(a_s + ra_ * G64_LD + g64_swz(ra_, kc * 16 + 4 * lg));
+            fb[t] = *(const f4 *)(b_s + rb_ * G64_LD + g64_swz(rb_, kc * 16 + 4 * lg));
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int a = 0; a < 2; ++a)
+#pragma unroll
+                for (int b = 0; b < 2; ++b) acc[a][b] = mfma4(fa[a][s], fb[b][s], acc[a][b]);
+    };
+
+    la.load(ra, p.lda, i0, it0 * GEMM_BK, p.Mo, kend);
+    lb.load(rb, p.ldb, j0, it0 * GEMM_BK, p.No, kend);
+    la.store(sA);
+    lb.store(sB);
+    la.load(ra, p.lda, i0, (it0 + 1) * GEMM_BK, p.Mo, kend);
+    lb.load(rb, p.ldb, j0, (it0 + 1) * GEMM_BK, p.No, kend);
+    __syncthreads();
+    for (int kt = it0; kt < it1; kt += 4) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int cur = u & 1;   // it0 is a multiple of 4: slab kt+u lives in buffer u & 1
+            la.store(sA + (cur ^ 1) * G64 * G64_LD);
+            lb.store(sB + (cur ^ 1) * G64 * G64_LD);
+            la.load(ra, p.lda, i0, (kt + u + 2) * GEMM_BK, p.Mo, kend);
+            lb.load(rb, p.ldb, j0, (kt + u + 2) * GEMM_BK, p.No, kend);
+            chunk(sA + cur * G64 * G64_LD, sB + cur * G64 * G64_LD, 0);
+            chunk(sA + cur * G64 * G64_LD, sB + cur * G64 * G64_LD, 1);
+            __syncthreads();
+        }
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                tot[a][b] += acc[a][b];
+                acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
+            }
+    }
+    if (unit >= 0) {
+        float *mine = p.ws + (int64_t)unit * (G64 * G64);
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int b = 0; b < 2; ++b) *(f4 *)(mine + ((a * 2 + b) * GEMM_NT + tid) * 4) = tot[a][b];
+        return;
+    }
+    g64_epilogue<EPI>(p, tot, i0, j0, tid);
+}
+
+// Sum of the segment partials of split tile blockIdx.x in segment order, then
+// the epilogue.
+template <int EPI>
+__device__ __forceinline__ void gemm64_fixup_body(const GemmArgs &p) {
+    const int tid = threadIdx.x, tail = blockIdx.x;
+    int tm, tn;
+    tile_rc<8>(p.dp_tiles + tail, p.tiles_m, p.tiles_n, tm, tn);
+    const float *first = p.ws + (int64_t)tail * p.segs * (G64 * G64);
+    f4 tot[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) tot[a][b] = *(const f4 *)(first + ((a * 2 + b) * GEMM_NT + tid) * 4);
+    for (int s = 1; s < p.segs; ++s) {
+        const float *part = first + (int64_t)s * (G64 * G64);
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int b = 0; b < 2; ++b) tot[a][b] += *(const f4 *)(part + ((a * 2 + b) * GEMM_NT + tid) * 4);
+    }
+    g64_epilogue<EPI>(p, tot, tm * G64, tn * G64, tid);
+}
+
+#define GEMM64_KERNEL(name, AKC, BKC, EPI, VEC) \
+    extern "C" __global__ void __launch_bounds__(GEMM_NT) name(GemmArgs p) { gemm64_body<AKC, BKC, EPI, VEC>(p); }
+#define GEMM64_FIXUP(name, EPI) \
+    extern "C" __global__ void __launch_bounds__(GEMM_NT) name(GemmArgs p) { gemm64_fixup_body<EPI>(p); }
+GEMM64_KERNEL(gemm64_fwd_v, true,  true,  EPI_STORE, true)
+GEMM64_KERNEL(gemm64_fwd_s, true,  true,  EPI_STORE, false)
+GEMM64_KERNEL(gemm64_dx_v,  true,  false, EPI_ACCUM, true)
+GEMM64_KERNEL(gemm64_dx_s,  true,  false, EPI_ACCUM, false)
+GEMM64_KERNEL(gemm64_dw_v,  false, false, EPI_ACCUM, true)
+GEMM64_KERNEL(gemm64_dw_s,  false, false, EPI_ACCUM, false)
+GEMM64_FIXUP(gemm64_fixup_store, EPI_STORE)
+GEMM64_FIXUP(gemm64_fixup_accum, EPI_ACCUM)

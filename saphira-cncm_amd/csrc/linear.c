@@ -10,6 +10,8 @@
  * in fp32 (the parity contract is |y - ref| <= 1e-4 (|ref| + 1)). */
 #include "internal.h"
 
+#include <stdlib.h>
+
 #include <limits.h>
 #include <stdio.h>
 #include <string.h>
@@ -45,18 +47,17 @@ typedef struct {
 } GemvArgs;
 
 enum { L_FWD = 0, L_DX = 1, L_DW = 2 };
-#define TILE 128
+#define TILE 64
 #define BK 32
 #define MAX_SEGS 16
 #define MAX_BUFFER_BYTES ((int64_t)1 << 31)
 
 static const char *gemm_names[3][2] = {
     /* kind x vec */
-    {"gemm_fwd_s", "gemm_fwd_v"},
-    {"gemm_dx_s", "gemm_dx_v"},
-    {"gemm_dw_s", "gemm_dw_v"},
+    {"gemm64_fwd_s", "gemm64_fwd_v"},
+    {"gemm64_dx_s", "gemm64_dx_v"},
+    {"gemm64_dw_s", "gemm64_dw_v"},
 };
-static const char *fixup_names[3] = {"gemm_fixup_fwd", "gemm_fixup_dx", "gemm_fixup_dw"};
 
 /* Work split of one GEMM over the chip: whole rounds of tiles, then the
  * remaining tiles cut into k-segments (whole groups of 4 slabs) that fill
@@ -65,10 +66,10 @@ typedef struct {
     int tiles_m, tiles_n, iters, dp_tiles, segs, blocks;
 } GemmPlan;
 
-static GemmPlan plan_gemm(int Mo, int No, int Kred, int slots) {
+static GemmPlan plan_gemm(int Mo, int No, int Kred, int slots, int tile) {
     GemmPlan g;
-    g.tiles_m = (Mo + TILE - 1) / TILE;
-    g.tiles_n = (No + TILE - 1) / TILE;
+    g.tiles_m = (Mo + tile - 1) / tile;
+    g.tiles_n = (No + tile - 1) / tile;
     int groups = Kred > 0 ? (Kred + 4 * BK - 1) / (4 * BK) : 1;
     g.iters = 4 * groups;
     int T = g.tiles_m * g.tiles_n;
@@ -124,7 +125,7 @@ static int run_gemm(int kind, const float *A, const float *B, float *C, const fl
     const char *name = gemm_names[kind][vec ? 1 : 0];
     int slots = gemm_slots(name);
     if (slots < 0) return NCM_E_INIT;
-    GemmPlan g = plan_gemm(Mo, No, Kred, slots);
+    GemmPlan g = plan_gemm(Mo, No, Kred, slots, TILE);
     /* operand extents as stored: A is [Mo][Kred] (k-contiguous) or [Kred][Mo] */
     int64_t ab = kind == L_DW ? extent(Kred, Mo, lda) : extent(Mo, Kred, lda);
     int64_t bb = kind == L_FWD ? extent(No, Kred, ldb) : extent(Kred, No, ldb);
@@ -142,7 +143,8 @@ static int run_gemm(int kind, const float *A, const float *B, float *C, const fl
     void *args[] = {&p};
     int rc = ncm_launch(ncm_kernel(name), (unsigned)g.blocks, 1, 1, 256, args);
     if (rc || g.segs == 1) return rc;
-    return ncm_launch_named(fixup_names[kind], (unsigned)split_tiles, 4, 1, 256, args);
+    return ncm_launch_named(kind == L_FWD ? "gemm64_fixup_store" : "gemm64_fixup_accum", (unsigned)split_tiles, 1, 1,
+                            256, args);
 }
 
 /* GEMV kernel for a chunk of nb <= 8 batch rows; returns rows per workgroup. */
@@ -315,7 +317,7 @@ int ncm_hip_linear_plan(int op, int64_t batch, int M, int K, char *kernel, size_
     const char *name = gemm_names[op][vec];
     int slots = gemm_slots(name);
     if (slots < 0) return -1;
-    GemmPlan g = plan_gemm(Mo, No, Kred, slots);
+    GemmPlan g = plan_gemm(Mo, No, Kred, slots, TILE);
     snprintf(kernel, cap, "%s", name);
     return g.segs;
 }

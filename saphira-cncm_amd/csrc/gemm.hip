@@ -14,12 +14,17 @@
 // Tiling: a 256-thread workgroup owns a 64x64 output tile; each of its four
 // 64-lane waves owns a 32x32 sub-tile of 2x2 MFMA blocks.  Operand slabs of
 // BK = 32 go global -> registers -> LDS (two buffers) and are consumed as two
-// 16-wide chunks; the small register (~90 VGPRs) and LDS (36 KB) footprint
-// lets four workgroups share a CU, whose interleaving hides the load and
-// barrier latency.  Both operands are kept k-contiguous in LDS: a slab whose
-// memory layout is i/j-contiguous is transposed by its LDS store.  Global
-// loads are raw buffer loads: lanes outside the matrix get an offset beyond
-// the buffer and read zero, so the loop body has no branches.
+// 16-wide chunks; the register (<= 128 VGPRs) and LDS (40 KB) footprint lets
+// four workgroups share a CU.  Both operands are kept k-contiguous in LDS: a
+// slab whose memory layout is i/j-contiguous is transposed by its LDS store.
+// The LDS layout (pitch 40 floats, XOR swizzle of the float4 group) is free
+// of bank conflicts for the fragment reads and both kinds of slab store.
+// Global loads are raw buffer loads: lanes outside the matrix get an offset
+// beyond the buffer and read zero, so the loop body has no branches.
+//
+// Pipeline (per slab): fragment reads run one chunk ahead of the MFMAs that
+// use them (across the barrier too), and the global loads of the slab after
+// next are spread between the MFMAs of the second chunk.
 //
 // k-permutation: inside every 16-wide chunk, MFMA step s (0..3) gives lane
 // group g = lane/16 the reduction index k = 4g + s, for both operands.  The
@@ -29,7 +34,7 @@
 //
 // Scheduling: tiles [0, dp_tiles) run whole, one workgroup each; every other
 // tile is cut into `segs` k-segments that fill the last round of the chip.
-// Segments store partial tiles; gemm64_fixup (a second launch) sums them in
+// Segments store partial tiles; gemm_64x64_fixup_* (a second launch) sums them in
 // segment order -- deterministic -- and applies the epilogue.
 //
 // Accuracy: MFMAs accumulate 128 k into `acc`, which is then added into `tot`;
@@ -348,61 +353,95 @@ GEMV_KERNEL(gemv_b2_r1_s, 2, 1, false)
 GEMV_KERNEL(gemv_b4_r1_s, 4, 1, false)
 GEMV_KERNEL(gemv_b8_r1_s, 8, 1, false)
 
-// ---------------------------------------------------------------- GEMM (64x64 tiles)
-// Per slab: store the slab loaded in the previous iteration to the free LDS
-// buffer, issue the loads of the slab after it, run the 32 MFMAs of the
-// current buffer, barrier.  The 36-float LDS pitch makes the fragment reads
-// conflict-free.
-#define G64 64
-#define G64_LD (GEMM_BK + 4)
-// LDS element (row, k) of a slab lives at row * G64_LD + swz(row, k): the
-// float4 group of k is XORed with (row >> 4) & 3.  Fragment reads (16
-// consecutive rows, one float4 each) keep a constant XOR and stay one aligned
-// float4; the transposing stores of an i/j-contiguous slab (rows 4c + u,
-// c = 0..15) then fall on 64 distinct banks instead of 16.
-__device__ __forceinline__ int g64_swz(int row, int k) { return ((((k >> 2) ^ (row >> 4)) & 7) << 2) | (k & 3); }
+// ---------------------------------------------------------------- GEMM (BM x BN tiles)
+// Tiles of BM x BN (64 or 128 each), four waves in 2 x 2, a wave owning a
+// (BM/2) x (BN/2) sub-tile of TM x TN MFMA blocks.
+//
+// LDS layout of a slab (rows = tile rows, BK = 32 floats of k per row): pitch
+// G_LD = 40 floats, and the float4 group of k XORed with h(row) =
+// ((row >> 2) ^ (row >> 5)) & 7.  gfx950 serves a ds_read_b128 16 lanes per
+// cycle in the groups {0-3, 12-15, 20-23, 24-27} and {4-7, 8-11, 16-19,
+// 28-31} (and the same +32), a ds_write_b128 8 consecutive lanes per cycle and
+// a ds_write_b32 32 consecutive lanes per cycle, over 64 four-byte banks.
+// With this layout each of the three accesses of the kernel -- fragment reads
+// (16 consecutive rows, one float4 of k each), k-contiguous slab stores (8
+// lanes = one row) and the transposing b32 stores of i/j-contiguous slabs
+// (32 lanes = 16 rows x 2 k) -- touches every bank at most once per cycle.
+#define G_LD (GEMM_BK + 8)
+__device__ __forceinline__ int gswz(int row, int k) {
+    return ((((k >> 2) ^ (row >> 2) ^ (row >> 5)) & 7) << 2) | (k & 3);
+}
 
-template <bool KC, bool VEC>
-struct Slab64 {
-    // KC: memory [64 rows][K] (k along columns); else memory [K][64 cols]
-    f4 r[2];
-    int a0, b0;   // KC: row (t >> 3) + {0, 32}, k (t & 7) * 4;  !KC: k (t >> 4) + {0, 16}, i (t & 15) * 4
-    __device__ __forceinline__ void init(int tid) {
+template <int ROWS, bool KC, bool VEC>
+struct GSlab {
+    // KC: memory [ROWS rows][K] (k along columns): thread t loads row (t >> 3) + 32 j, k (t & 7) * 4.
+    // else memory [K][ROWS cols]: thread t loads k-row t / (ROWS/4) + KSTEP j, cols (t % (ROWS/4)) * 4.
+    static constexpr int PER = ROWS / 32;               // float4 per thread per slab (both layouts)
+    static constexpr int C4 = ROWS / 4, KSTEP = GEMM_NT / C4;
+    int a0, b0;
+    int ld, fix0, fix_lim;
+    // VEC: byte offset of the thread's float4 j at k = 0, or OOB_OFFSET when it
+    // lies outside the tile's valid rows (KC) / columns (!KC), and the bound
+    // on a slab's first k below which float4 j lies inside the k range.  A
+    // load is then an add, a compare and a select, with no branch, so that
+    // the loads can be spread between the MFMAs.
+    unsigned base[PER];
+    int klim[PER];
+    __device__ __forceinline__ void init(int tid, int ld_, int fix0_, int fix_lim_, int k_lim) {
+        ld = ld_;
+        fix0 = fix0_;
+        fix_lim = fix_lim_;
         if (KC) { a0 = tid >> 3; b0 = (tid & 7) * 4; }
-        else { a0 = tid >> 4; b0 = (tid & 15) * 4; }
-    }
-    // fix0: first row (KC) / column (!KC) of the tile; k0: first k of the slab
-    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, int ld, int fix0, int k0, int fix_lim,
-                                         int k_lim) {
+        else { a0 = tid / C4; b0 = (tid % C4) * 4; }
+        if (VEC) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int rw = KC ? fix0 + a0 + 32 * j : k0 + a0 + 16 * j;
+            for (int j = 0; j < PER; ++j) {
+                if (KC) {
+                    const int row = fix0 + a0 + 32 * j;
+                    base[j] = row < fix_lim ? (unsigned)(row * ld + b0) * 4u : OOB_OFFSET;
+                    klim[j] = k_lim - b0;   // K % 4 == 0: the float4 is whole or out
+                } else {
+                    const int col = fix0 + b0;   // fix_lim % 4 == 0: the float4 is whole or out
+                    base[j] = col < fix_lim ? (unsigned)((a0 + KSTEP * j) * ld + col) * 4u : OOB_OFFSET;
+                    klim[j] = k_lim - a0 - KSTEP * j;
+                }
+            }
+        }
+    }
+    // k0: first k of the slab; k_lim: end of the k range (the one init got)
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, int k0, int k_lim, f4 (&r)[PER]) const {
+        if (VEC) {
+            const unsigned dk = KC ? (unsigned)k0 * 4u : (unsigned)k0 * (unsigned)ld * 4u;
+#pragma unroll
+            for (int j = 0; j < PER; ++j)
+                r[j] = __builtin_bit_cast(
+                    f4, __builtin_amdgcn_raw_buffer_load_b128(rs, k0 < klim[j] ? base[j] + dk : OOB_OFFSET, 0, 0));
+            return;
+        }
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int rw = KC ? fix0 + a0 + 32 * j : k0 + a0 + KSTEP * j;
             const int cl = KC ? k0 + b0 : fix0 + b0;
             const bool in_r = KC ? rw < fix_lim : rw < k_lim;
             const int lim_c = KC ? k_lim : fix_lim;
             const unsigned o = (unsigned)(rw * ld + cl) * 4u;
-            if (VEC) {
-                r[j] = __builtin_bit_cast(
-                    f4, __builtin_amdgcn_raw_buffer_load_b128(rs, (in_r && cl < lim_c) ? o : OOB_OFFSET, 0, 0));
-            } else {
 #pragma unroll
-                for (int u = 0; u < 4; ++u)
-                    r[j][u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                            rs, (in_r && cl + u < lim_c) ? o + 4u * u : OOB_OFFSET, 0, 0));
-            }
+            for (int u = 0; u < 4; ++u)
+                r[j][u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                        rs, (in_r && cl + u < lim_c) ? o + 4u * u : OOB_OFFSET, 0, 0));
         }
     }
-    __device__ __forceinline__ void store(float *buf) const {
+    __device__ __forceinline__ void store(float *buf, const f4 (&r)[PER]) const {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < PER; ++j) {
             if (KC) {
                 const int row = a0 + 32 * j;
-                *(f4 *)(buf + row * G64_LD + g64_swz(row, b0)) = r[j];
+                *(f4 *)(buf + row * G_LD + gswz(row, b0)) = r[j];
             } else {
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     const int row = b0 + u;
-                    buf[row * G64_LD + g64_swz(row, a0 + 16 * j)] = r[j][u];
+                    buf[row * G_LD + gswz(row, a0 + KSTEP * j)] = r[j][u];
                 }
             }
         }
@@ -410,7 +449,7 @@ struct Slab64 {
 };
 
 template <int ACT, int EPI>
-__device__ __forceinline__ void g64_out(const GemmArgs &p, int i, int j, float v) {
+__device__ __forceinline__ void g_out(const GemmArgs &p, int i, int j, float v) {
     if (i >= p.Mo || j >= p.No) return;
     float *c = p.C + (int64_t)i * p.ldc + j;
     if (EPI == EPI_ACCUM) {
@@ -423,35 +462,39 @@ __device__ __forceinline__ void g64_out(const GemmArgs &p, int i, int j, float v
     }
 }
 
-// tot[a][b][r]: row wm*32 + a*16 + 4*lg + r, column wn*32 + b*16 + li
-template <int EPI, int ACT>
-__device__ __forceinline__ void g64_epilogue_act(const GemmArgs &p, const f4 (&tot)[2][2], int i0, int j0, int tid) {
+// tot[a][b][r]: row wm*(BM/2) + a*16 + 4*lg + r, column wn*(BN/2) + b*16 + li
+template <int BM, int BN, int EPI, int ACT>
+__device__ __forceinline__ void g_epilogue_act(const GemmArgs &p, const f4 (&tot)[BM / 32][BN / 32], int i0, int j0,
+                                               int tid) {
     const int lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
     const int li = lane & 15, lg = lane >> 4;
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < BM / 32; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+        for (int b = 0; b < BN / 32; ++b)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                g64_out<ACT, EPI>(p, i0 + wm * 32 + a * 16 + 4 * lg + r, j0 + wn * 32 + b * 16 + li, tot[a][b][r]);
+                g_out<ACT, EPI>(p, i0 + wm * (BM / 2) + a * 16 + 4 * lg + r, j0 + wn * (BN / 2) + b * 16 + li,
+                                tot[a][b][r]);
 }
 
-template <int EPI>
-__device__ __forceinline__ void g64_epilogue(const GemmArgs &p, const f4 (&tot)[2][2], int i0, int j0, int tid) {
-    if (EPI == EPI_ACCUM) { g64_epilogue_act<EPI, ACT_NONE>(p, tot, i0, j0, tid); return; }
+template <int BM, int BN, int EPI>
+__device__ __forceinline__ void g_epilogue(const GemmArgs &p, const f4 (&tot)[BM / 32][BN / 32], int i0, int j0,
+                                           int tid) {
+    if (EPI == EPI_ACCUM) { g_epilogue_act<BM, BN, EPI, ACT_NONE>(p, tot, i0, j0, tid); return; }
     switch (p.act) {
-    case ACT_SILU: g64_epilogue_act<EPI, ACT_SILU>(p, tot, i0, j0, tid); break;
-    case ACT_GELU: g64_epilogue_act<EPI, ACT_GELU>(p, tot, i0, j0, tid); break;
-    case ACT_GELU_TANH: g64_epilogue_act<EPI, ACT_GELU_TANH>(p, tot, i0, j0, tid); break;
-    default: g64_epilogue_act<EPI, ACT_NONE>(p, tot, i0, j0, tid); break;
+    case ACT_SILU: g_epilogue_act<BM, BN, EPI, ACT_SILU>(p, tot, i0, j0, tid); break;
+    case ACT_GELU: g_epilogue_act<BM, BN, EPI, ACT_GELU>(p, tot, i0, j0, tid); break;
+    case ACT_GELU_TANH: g_epilogue_act<BM, BN, EPI, ACT_GELU_TANH>(p, tot, i0, j0, tid); break;
+    default: g_epilogue_act<BM, BN, EPI, ACT_NONE>(p, tot, i0, j0, tid); break;
     }
 }
 
-template <bool AKC, bool BKC, int EPI, bool VEC>
-__device__ __forceinline__ void gemm64_body(const GemmArgs &p) {
-    __shared__ __attribute__((aligned(16))) float sA[2 * G64 * G64_LD];
-    __shared__ __attribute__((aligned(16))) float sB[2 * G64 * G64_LD];
+template <int BM, int BN, bool AKC, bool BKC, int EPI, bool VEC>
+__device__ __forceinline__ void gemm_tile_body(const GemmArgs &p) {
+    constexpr int TM = BM / 32, TN = BN / 32;
+    __shared__ __attribute__((aligned(16))) float sA[2 * BM * G_LD];
+    __shared__ __attribute__((aligned(16))) float sB[2 * BN * G_LD];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1, li = lane & 15, lg = lane >> 4;
 
@@ -475,106 +518,149 @@ __device__ __forceinline__ void gemm64_body(const GemmArgs &p) {
     }
     int tm, tn;
     tile_rc<8>(tile, p.tiles_m, p.tiles_n, tm, tn);
-    const int i0 = tm * G64, j0 = tn * G64;
+    const int i0 = tm * BM, j0 = tn * BN;
     const int kend = min(p.K, it1 * GEMM_BK);
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, p.a_bytes), rb = make_rsrc(p.B, p.b_bytes);
-    Slab64<AKC, VEC> la;
-    Slab64<BKC, VEC> lb;
-    la.init(tid);
-    lb.init(tid);
+    GSlab<BM, AKC, VEC> la;
+    GSlab<BN, BKC, VEC> lb;
+    la.init(tid, p.lda, i0, p.Mo, kend);
+    lb.init(tid, p.ldb, j0, p.No, kend);
 
-    f4 acc[2][2], tot[2][2];
+    f4 acc[TM][TN], tot[TM][TN];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < TM; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b) acc[a][b] = tot[a][b] = f4{0.f, 0.f, 0.f, 0.f};
+        for (int b = 0; b < TN; ++b) acc[a][b] = tot[a][b] = f4{0.f, 0.f, 0.f, 0.f};
 
-    auto chunk = [&](const float *a_s, const float *b_s, int kc) {
-        f4 fa[2], fb[2];
+    // fragments of one 16-wide chunk: fa[t] = A rows wm*(BM/2) + 16 t + li,
+    // fb[t] = B rows wn*(BN/2) + 16 t + li, k = 16 kc + 4 lg .. + 3
+    auto read_frags = [&](const float *a_s, const float *b_s, int kc, f4 (&fa)[TM], f4 (&fb)[TN]) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const int ra_ = wm * 32 + t * 16 + li, rb_ = wn * 32 + t * 16 + li;
-            fa[t] = *(const f4 *)(a_s + ra_ * G64_LD + g64_swz(ra_, kc * 16 + 4 * lg));
-            fb[t] = *(const f4 *)(b_s + rb_ * G64_LD + g64_swz(rb_, kc * 16 + 4 * lg));
+        for (int t = 0; t < TM; ++t) {
+            const int r = wm * (BM / 2) + t * 16 + li;
+            fa[t] = *(const f4 *)(a_s + r * G_LD + gswz(r, kc * 16 + 4 * lg));
         }
+#pragma unroll
+        for (int t = 0; t < TN; ++t) {
+            const int r = wn * (BN / 2) + t * 16 + li;
+            fb[t] = *(const f4 *)(b_s + r * G_LD + gswz(r, kc * 16 + 4 * lg));
+        }
+    };
+    auto mfmas = [&](const f4 (&fa)[TM], const f4 (&fb)[TN]) {
 #pragma unroll
         for (int s = 0; s < 4; ++s)
 #pragma unroll
-            for (int a = 0; a < 2; ++a)
+            for (int a = 0; a < TM; ++a)
 #pragma unroll
-                for (int b = 0; b < 2; ++b) acc[a][b] = mfma4(fa[a][s], fb[b][s], acc[a][b]);
+                for (int b = 0; b < TN; ++b) acc[a][b] = mfma4(fa[a][s], fb[b][s], acc[a][b]);
     };
 
-    la.load(ra, p.lda, i0, it0 * GEMM_BK, p.Mo, kend);
-    lb.load(rb, p.ldb, j0, it0 * GEMM_BK, p.No, kend);
-    la.store(sA);
-    lb.store(sB);
-    la.load(ra, p.lda, i0, (it0 + 1) * GEMM_BK, p.Mo, kend);
-    lb.load(rb, p.ldb, j0, (it0 + 1) * GEMM_BK, p.No, kend);
+    // Software pipeline, per slab (buffer cur holds it, registers ga / gb
+    // the next one):
+    //   issue the LDS reads of chunk 1 (f1), then the MFMAs of chunk 0 (f0);
+    //   store the next slab into the other buffer; barrier;
+    //   issue the LDS reads of the next slab's chunk 0 (f0), then the MFMAs
+    //   of chunk 1 with the global loads of the slab after next spread
+    //   between them (one load per TM*TN MFMAs: issued in a burst, the loads
+    //   stall the wave on the vector-memory pipe).
+    // Every LDS read is covered by one chunk of MFMAs of the same wave and
+    // every global load by one slab of them.
+    constexpr int NLOAD = GSlab<BM, AKC, VEC>::PER + GSlab<BN, BKC, VEC>::PER;
+    f4 f0a[TM], f0b[TN], f1a[TM], f1b[TN];
+    f4 ga[GSlab<BM, AKC, VEC>::PER], gb[GSlab<BN, BKC, VEC>::PER];
+    la.load(ra, it0 * GEMM_BK, kend, ga);
+    lb.load(rb, it0 * GEMM_BK, kend, gb);
+    la.store(sA, ga);
+    lb.store(sB, gb);
+    la.load(ra, (it0 + 1) * GEMM_BK, kend, ga);
+    lb.load(rb, (it0 + 1) * GEMM_BK, kend, gb);
     __syncthreads();
+    read_frags(sA, sB, 0, f0a, f0b);
     for (int kt = it0; kt < it1; kt += 4) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int cur = u & 1;   // it0 is a multiple of 4: slab kt+u lives in buffer u & 1
-            la.store(sA + (cur ^ 1) * G64 * G64_LD);
-            lb.store(sB + (cur ^ 1) * G64 * G64_LD);
-            la.load(ra, p.lda, i0, (kt + u + 2) * GEMM_BK, p.Mo, kend);
-            lb.load(rb, p.ldb, j0, (kt + u + 2) * GEMM_BK, p.No, kend);
-            chunk(sA + cur * G64 * G64_LD, sB + cur * G64 * G64_LD, 0);
-            chunk(sA + cur * G64 * G64_LD, sB + cur * G64 * G64_LD, 1);
+            const float *ca = sA + cur * BM * G_LD, *cb = sB + cur * BN * G_LD;
+            float *na = sA + (cur ^ 1) * BM * G_LD, *nb = sB + (cur ^ 1) * BN * G_LD;
+            read_frags(ca, cb, 1, f1a, f1b);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(f0a, f0b);
+            __builtin_amdgcn_sched_barrier(0);
+            la.store(na, ga);
+            lb.store(nb, gb);
             __syncthreads();
+            read_frags(na, nb, 0, f0a, f0b);
+            __builtin_amdgcn_sched_barrier(0);
+            la.load(ra, (kt + u + 2) * GEMM_BK, kend, ga);
+            lb.load(rb, (kt + u + 2) * GEMM_BK, kend, gb);
+            mfmas(f1a, f1b);
+#pragma unroll
+            for (int q = 0; q < NLOAD; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 4 * TM * TN / NLOAD, 0);   // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                   // VMEM read
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
-        for (int a = 0; a < 2; ++a)
+        for (int a = 0; a < TM; ++a)
 #pragma unroll
-            for (int b = 0; b < 2; ++b) {
+            for (int b = 0; b < TN; ++b) {
                 tot[a][b] += acc[a][b];
                 acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
             }
     }
     if (unit >= 0) {
-        float *mine = p.ws + (int64_t)unit * (G64 * G64);
+        float *mine = p.ws + (int64_t)unit * (BM * BN);
 #pragma unroll
-        for (int a = 0; a < 2; ++a)
+        for (int a = 0; a < TM; ++a)
 #pragma unroll
-            for (int b = 0; b < 2; ++b) *(f4 *)(mine + ((a * 2 + b) * GEMM_NT + tid) * 4) = tot[a][b];
+            for (int b = 0; b < TN; ++b) *(f4 *)(mine + ((a * TN + b) * GEMM_NT + tid) * 4) = tot[a][b];
         return;
     }
-    g64_epilogue<EPI>(p, tot, i0, j0, tid);
+    g_epilogue<BM, BN, EPI>(p, tot, i0, j0, tid);
 }
 
 // Sum of the segment partials of split tile blockIdx.x in segment order, then
 // the epilogue.
-template <int EPI>
-__device__ __forceinline__ void gemm64_fixup_body(const GemmArgs &p) {
+template <int BM, int BN, int EPI>
+__device__ __forceinline__ void gemm_tile_fixup_body(const GemmArgs &p) {
+    constexpr int TM = BM / 32, TN = BN / 32;
     const int tid = threadIdx.x, tail = blockIdx.x;
     int tm, tn;
     tile_rc<8>(p.dp_tiles + tail, p.tiles_m, p.tiles_n, tm, tn);
-    const float *first = p.ws + (int64_t)tail * p.segs * (G64 * G64);
-    f4 tot[2][2];
+    const float *first = p.ws + (int64_t)tail * p.segs * (BM * BN);
+    f4 tot[TM][TN];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < TM; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b) tot[a][b] = *(const f4 *)(first + ((a * 2 + b) * GEMM_NT + tid) * 4);
+        for (int b = 0; b < TN; ++b) tot[a][b] = *(const f4 *)(first + ((a * TN + b) * GEMM_NT + tid) * 4);
     for (int s = 1; s < p.segs; ++s) {
-        const float *part = first + (int64_t)s * (G64 * G64);
+        const float *part = first + (int64_t)s * (BM * BN);
 #pragma unroll
-        for (int a = 0; a < 2; ++a)
+        for (int a = 0; a < TM; ++a)
 #pragma unroll
-            for (int b = 0; b < 2; ++b) tot[a][b] += *(const f4 *)(part + ((a * 2 + b) * GEMM_NT + tid) * 4);
+            for (int b = 0; b < TN; ++b) tot[a][b] += *(const f4 *)(part + ((a * TN + b) * GEMM_NT + tid) * 4);
     }
-    g64_epilogue<EPI>(p, tot, tm * G64, tn * G64, tid);
+    g_epilogue<BM, BN, EPI>(p, tot, tm * BM, tn * BN, tid);
 }
 
-#define GEMM64_KERNEL(name, AKC, BKC, EPI, VEC) \
-    extern "C" __global__ void __launch_bounds__(GEMM_NT) name(GemmArgs p) { gemm64_body<AKC, BKC, EPI, VEC>(p); }
-#define GEMM64_FIXUP(name, EPI) \
-    extern "C" __global__ void __launch_bounds__(GEMM_NT) name(GemmArgs p) { gemm64_fixup_body<EPI>(p); }
-GEMM64_KERNEL(gemm64_fwd_v, true,  true,  EPI_STORE, true)
-GEMM64_KERNEL(gemm64_fwd_s, true,  true,  EPI_STORE, false)
-GEMM64_KERNEL(gemm64_dx_v,  true,  false, EPI_ACCUM, true)
-GEMM64_KERNEL(gemm64_dx_s,  true,  false, EPI_ACCUM, false)
-GEMM64_KERNEL(gemm64_dw_v,  false, false, EPI_ACCUM, true)
-GEMM64_KERNEL(gemm64_dw_s,  false, false, EPI_ACCUM, false)
-GEMM64_FIXUP(gemm64_fixup_store, EPI_STORE)
-GEMM64_FIXUP(gemm64_fixup_accum, EPI_ACCUM)
+// Four workgroups of 64x64 tiles share a CU (LDS-bound): the register budget
+// is held to that occupancy.  (128-wide tiles were measured slower on every
+// linear-sweep shape: one or two workgroups per CU hide less latency.)
+#define GEMM_TILE_KERNEL(name, BM, BN, AKC, BKC, EPI, VEC)                                          \
+    extern "C" __global__ void __launch_bounds__(GEMM_NT)                                          \
+        __attribute__((amdgpu_waves_per_eu(BM * BN <= 4096 ? 4 : 1))) name(GemmArgs p) {          \
+        gemm_tile_body<BM, BN, AKC, BKC, EPI, VEC>(p);                                               \
+    }
+#define GEMM_TILE_FIXUP(name, BM, BN, EPI) \
+    extern "C" __global__ void __launch_bounds__(GEMM_NT) name(GemmArgs p) { gemm_tile_fixup_body<BM, BN, EPI>(p); }
+#define GEMM_TILE_SET(BM, BN)                                                              \
+    GEMM_TILE_KERNEL(gemm_##BM##x##BN##_fwd_v, BM, BN, true, true, EPI_STORE, true)        \
+    GEMM_TILE_KERNEL(gemm_##BM##x##BN##_fwd_s, BM, BN, true, true, EPI_STORE, false)       \
+    GEMM_TILE_KERNEL(gemm_##BM##x##BN##_dx_v, BM, BN, true, false, EPI_ACCUM, true)        \
+    GEMM_TILE_KERNEL(gemm_##BM##x##BN##_dx_s, BM, BN, true, false, EPI_ACCUM, false)       \
+    GEMM_TILE_KERNEL(gemm_##BM##x##BN##_dw_v, BM, BN, false, false, EPI_ACCUM, true)       \
+    GEMM_TILE_KERNEL(gemm_##BM##x##BN##_dw_s, BM, BN, false, false, EPI_ACCUM, false)      \
+    GEMM_TILE_FIXUP(gemm_##BM##x##BN##_fixup_store, BM, BN, EPI_STORE)                     \
+    GEMM_TILE_FIXUP(gemm_##BM##x##BN##_fixup_accum, BM, BN, EPI_ACCUM)
+GEMM_TILE_SET(64, 64)

@@ -47,17 +47,16 @@ typedef struct {
 } GemvArgs;
 
 enum { L_FWD = 0, L_DX = 1, L_DW = 2 };
-#define TILE 64
 #define BK 32
 #define MAX_SEGS 16
 #define MAX_BUFFER_BYTES ((int64_t)1 << 31)
 
-static const char *gemm_names[3][2] = {
-    /* kind x vec */
-    {"gemm64_fwd_s", "gemm64_fwd_v"},
-    {"gemm64_dx_s", "gemm64_dx_v"},
-    {"gemm64_dw_s", "gemm64_dw_v"},
-};
+static const char *const kind_names[3] = {"fwd", "dx", "dw"};
+
+/* Kernel of a tile shape, operation and load width: gemm_<BM>x<BN>_<op>_<v|s>. */
+static void gemm_name(int bm, int bn, int kind, int vec, char *out, size_t cap) {
+    snprintf(out, cap, "gemm_%dx%d_%s_%c", bm, bn, kind_names[kind], vec ? 'v' : 's');
+}
 
 /* Work split of one GEMM over the chip: whole rounds of tiles, then the
  * remaining tiles cut into k-segments (whole groups of 4 slabs) that fill
@@ -66,10 +65,10 @@ typedef struct {
     int tiles_m, tiles_n, iters, dp_tiles, segs, blocks;
 } GemmPlan;
 
-static GemmPlan plan_gemm(int Mo, int No, int Kred, int slots, int tile) {
+static GemmPlan plan_gemm(int Mo, int No, int Kred, int slots, int bm, int bn) {
     GemmPlan g;
-    g.tiles_m = (Mo + tile - 1) / tile;
-    g.tiles_n = (No + tile - 1) / tile;
+    g.tiles_m = (Mo + bm - 1) / bm;
+    g.tiles_n = (No + bn - 1) / bn;
     int groups = Kred > 0 ? (Kred + 4 * BK - 1) / (4 * BK) : 1;
     g.iters = 4 * groups;
     int T = g.tiles_m * g.tiles_n;
@@ -98,8 +97,8 @@ static GemmPlan plan_gemm(int Mo, int No, int Kred, int slots, int tile) {
 
 /* Concurrent workgroups of a GEMM kernel on the device (CUs x occupancy). */
 static int gemm_slots(const char *name) {
-    static char names[8][32];
-    static int vals[8], n = 0;
+    static char names[32][32];
+    static int vals[32], n = 0;
     for (int i = 0; i < n; i++)
         if (strcmp(names[i], name) == 0) return vals[i];
     hipFunction_t f = ncm_kernel(name);
@@ -108,7 +107,7 @@ static int gemm_slots(const char *name) {
     if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, 256, 0) != hipSuccess || per_cu < 1)
         per_cu = 1;
     int v = per_cu * ncm_cu_count();
-    if (n < 8) {
+    if (n < 32) {
         snprintf(names[n], sizeof names[n], "%s", name);
         vals[n++] = v;
     }
@@ -118,14 +117,20 @@ static int gemm_slots(const char *name) {
 /* Bytes spanned by a rows x cols row-major operand with row stride ld. */
 static int64_t extent(int64_t rows, int64_t cols, int64_t ld) { return ((rows - 1) * ld + cols) * 4; }
 
+/* Tile shape of every GEMM: 64 x 64 (gemm.hip instantiates only this one). */
+#define TILE_M 64
+#define TILE_N 64
+
 static int run_gemm(int kind, const float *A, const float *B, float *C, const float *bias,
                     const float *res, int Mo, int No, int Kred, int lda, int ldb, int ldc,
                     int act, int vec) {
     if (Mo <= 0 || No <= 0) return 0;
-    const char *name = gemm_names[kind][vec ? 1 : 0];
+    const int bm = TILE_M, bn = TILE_N;
+    char name[48], fix[48];
+    gemm_name(bm, bn, kind, vec, name, sizeof name);
     int slots = gemm_slots(name);
     if (slots < 0) return NCM_E_INIT;
-    GemmPlan g = plan_gemm(Mo, No, Kred, slots, TILE);
+    GemmPlan g = plan_gemm(Mo, No, Kred, slots, bm, bn);
     /* operand extents as stored: A is [Mo][Kred] (k-contiguous) or [Kred][Mo] */
     int64_t ab = kind == L_DW ? extent(Kred, Mo, lda) : extent(Mo, Kred, lda);
     int64_t bb = kind == L_FWD ? extent(No, Kred, ldb) : extent(Kred, No, ldb);
@@ -137,14 +142,14 @@ static int run_gemm(int kind, const float *A, const float *B, float *C, const fl
     p.vec_out = No % 4 == 0 && ldc % 4 == 0 && is_aligned16(C);
     int split_tiles = g.tiles_m * g.tiles_n - g.dp_tiles;
     if (g.segs > 1) {
-        p.ws = (float *)ncm_workspace(WS_SPLITK, (size_t)split_tiles * g.segs * TILE * TILE * sizeof(float));
+        p.ws = (float *)ncm_workspace(WS_SPLITK, (size_t)split_tiles * g.segs * bm * bn * sizeof(float));
         if (!p.ws) return NCM_E_OOM;
     }
     void *args[] = {&p};
     int rc = ncm_launch(ncm_kernel(name), (unsigned)g.blocks, 1, 1, 256, args);
     if (rc || g.segs == 1) return rc;
-    return ncm_launch_named(kind == L_FWD ? "gemm64_fixup_store" : "gemm64_fixup_accum", (unsigned)split_tiles, 1, 1,
-                            256, args);
+    snprintf(fix, sizeof fix, "gemm_%dx%d_fixup_%s", bm, bn, kind == L_FWD ? "store" : "accum");
+    return ncm_launch_named(fix, (unsigned)split_tiles, 1, 1, 256, args);
 }
 
 /* GEMV kernel for a chunk of nb <= 8 batch rows; returns rows per workgroup. */
@@ -314,10 +319,10 @@ int ncm_hip_linear_plan(int op, int64_t batch, int M, int K, char *kernel, size_
     }
     int Mo = op == L_DW ? M : nb, No = op == L_FWD ? M : K, Kred = op == L_FWD ? K : (op == L_DX ? M : nb);
     int vec = op == L_FWD ? K % 4 == 0 : (M % 4 == 0 && K % 4 == 0);
-    const char *name = gemm_names[op][vec];
-    int slots = gemm_slots(name);
+    const int bm = TILE_M, bn = TILE_N;
+    gemm_name(bm, bn, op, vec, kernel, cap);
+    int slots = gemm_slots(kernel);
     if (slots < 0) return -1;
-    GemmPlan g = plan_gemm(Mo, No, Kred, slots, TILE);
-    snprintf(kernel, cap, "%s", name);
+    GemmPlan g = plan_gemm(Mo, No, Kred, slots, bm, bn);
     return g.segs;
 }

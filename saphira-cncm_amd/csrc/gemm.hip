@@ -13,18 +13,18 @@
 //
 // Tiling: a 256-thread workgroup owns a 64x64 output tile; each of its four
 // 64-lane waves owns a 32x32 sub-tile of 2x2 MFMA blocks.  Operand slabs of
-// BK = 32 go global -> registers -> LDS (two buffers) and are consumed as two
-// 16-wide chunks; the register (<= 128 VGPRs) and LDS (40 KB) footprint lets
-// four workgroups share a CU.  Both operands are kept k-contiguous in LDS: a
-// slab whose memory layout is i/j-contiguous is transposed by its LDS store.
-// The LDS layout (pitch 40 floats, XOR swizzle of the float4 group) is free
-// of bank conflicts for the fragment reads and both kinds of slab store.
-// Global loads are raw buffer loads: lanes outside the matrix get an offset
-// beyond the buffer and read zero, so the loop body has no branches.
+// BK = 32 k are consumed as two 16-wide chunks from two LDS stages, one
+// barrier per slab.  The vectorised kernels (_v, the common case) load slabs
+// straight into LDS (buffer_load_dwordx4 ... lds) and keep each slab in its
+// memory layout; the scalar kernels (_s: an operand row not 16-byte aligned)
+// stage through registers and transpose i/j-contiguous slabs into k-contiguous
+// LDS rows.  Both layouts are free of LDS bank conflicts (see below).  Global
+// loads are raw buffer loads: lanes outside the matrix get an offset beyond
+// the buffer and read zero, so the loop body has no branches.
 //
 // Pipeline (per slab): fragment reads run one chunk ahead of the MFMAs that
 // use them (across the barrier too), and the global loads of the slab after
-// next are spread between the MFMAs of the second chunk.
+// next are issued right after the barrier, ahead of the second chunk's MFMAs.
 //
 // k-permutation: inside every 16-wide chunk, MFMA step s (0..3) gives lane
 // group g = lane/16 the reduction index k = 4g + s, for both operands.  The
@@ -353,8 +353,8 @@ GEMV_KERNEL(gemv_b2_r1_s, 2, 1, false)
 GEMV_KERNEL(gemv_b4_r1_s, 4, 1, false)
 GEMV_KERNEL(gemv_b8_r1_s, 8, 1, false)
 
-// ---------------------------------------------------------------- GEMM (BM x BN tiles)
-// Tiles of BM x BN (64 or 128 each), four waves in 2 x 2, a wave owning a
+// ---------------------------------------------------------------- GEMM, register-staged loads
+// (the _s kernels.)  Tiles of BM x BN, four waves in 2 x 2, a wave owning a
 // (BM/2) x (BN/2) sub-tile of TM x TN MFMA blocks.
 //
 // LDS layout of a slab (rows = tile rows, BK = 32 floats of k per row): pitch
@@ -462,8 +462,12 @@ __device__ __forceinline__ void g_out(const GemmArgs &p, int i, int j, float v) 
     }
 }
 
-// tot[a][b][r]: row wm*(BM/2) + a*16 + 4*lg + r, column wn*(BN/2) + b*16 + li
-template <int BM, int BN, int EPI, int ACT>
+// tot[a][b][r] holds MFMA output row 4*lg + r, column li of block (a, b).
+// Blocks of 16 consecutive rows / columns: row wm*(BM/2) + a*16 + 4*lg + r,
+// column wn*(BN/2) + b*16 + li.  Interleaved (IA / IB, the operand read from
+// an i/j-contiguous LDS slab with ds_read_b64): block a takes the rows
+// wm*32 + 2*i + a, block b the columns wn*32 + 2*j + b (64x64 tiles only).
+template <int BM, int BN, int EPI, int ACT, bool IA, bool IB>
 __device__ __forceinline__ void g_epilogue_act(const GemmArgs &p, const f4 (&tot)[BM / 32][BN / 32], int i0, int j0,
                                                int tid) {
     const int lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
@@ -473,20 +477,22 @@ __device__ __forceinline__ void g_epilogue_act(const GemmArgs &p, const f4 (&tot
 #pragma unroll
         for (int b = 0; b < BN / 32; ++b)
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-                g_out<ACT, EPI>(p, i0 + wm * (BM / 2) + a * 16 + 4 * lg + r, j0 + wn * (BN / 2) + b * 16 + li,
-                                tot[a][b][r]);
+            for (int r = 0; r < 4; ++r) {
+                const int row = IA ? wm * 32 + 2 * (4 * lg + r) + a : wm * (BM / 2) + a * 16 + 4 * lg + r;
+                const int col = IB ? wn * 32 + 2 * li + b : wn * (BN / 2) + b * 16 + li;
+                g_out<ACT, EPI>(p, i0 + row, j0 + col, tot[a][b][r]);
+            }
 }
 
-template <int BM, int BN, int EPI>
+template <int BM, int BN, int EPI, bool IA = false, bool IB = false>
 __device__ __forceinline__ void g_epilogue(const GemmArgs &p, const f4 (&tot)[BM / 32][BN / 32], int i0, int j0,
                                            int tid) {
-    if (EPI == EPI_ACCUM) { g_epilogue_act<BM, BN, EPI, ACT_NONE>(p, tot, i0, j0, tid); return; }
+    if (EPI == EPI_ACCUM) { g_epilogue_act<BM, BN, EPI, ACT_NONE, IA, IB>(p, tot, i0, j0, tid); return; }
     switch (p.act) {
-    case ACT_SILU: g_epilogue_act<BM, BN, EPI, ACT_SILU>(p, tot, i0, j0, tid); break;
-    case ACT_GELU: g_epilogue_act<BM, BN, EPI, ACT_GELU>(p, tot, i0, j0, tid); break;
-    case ACT_GELU_TANH: g_epilogue_act<BM, BN, EPI, ACT_GELU_TANH>(p, tot, i0, j0, tid); break;
-    default: g_epilogue_act<BM, BN, EPI, ACT_NONE>(p, tot, i0, j0, tid); break;
+    case ACT_SILU: g_epilogue_act<BM, BN, EPI, ACT_SILU, IA, IB>(p, tot, i0, j0, tid); break;
+    case ACT_GELU: g_epilogue_act<BM, BN, EPI, ACT_GELU, IA, IB>(p, tot, i0, j0, tid); break;
+    case ACT_GELU_TANH: g_epilogue_act<BM, BN, EPI, ACT_GELU_TANH, IA, IB>(p, tot, i0, j0, tid); break;
+    default: g_epilogue_act<BM, BN, EPI, ACT_NONE, IA, IB>(p, tot, i0, j0, tid); break;
     }
 }
 
@@ -622,7 +628,7 @@ __device__ __forceinline__ void gemm_tile_body(const GemmArgs &p) {
 
 // Sum of the segment partials of split tile blockIdx.x in segment order, then
 // the epilogue.
-template <int BM, int BN, int EPI>
+template <int BM, int BN, int EPI, bool IA = false, bool IB = false>
 __device__ __forceinline__ void gemm_tile_fixup_body(const GemmArgs &p) {
     constexpr int TM = BM / 32, TN = BN / 32;
     const int tid = threadIdx.x, tail = blockIdx.x;
@@ -641,10 +647,184 @@ __device__ __forceinline__ void gemm_tile_fixup_body(const GemmArgs &p) {
 #pragma unroll
             for (int b = 0; b < TN; ++b) tot[a][b] += *(const f4 *)(part + ((a * TN + b) * GEMM_NT + tid) * 4);
     }
-    g_epilogue<BM, BN, EPI>(p, tot, tm * BM, tn * BN, tid);
+    g_epilogue<BM, BN, EPI, IA, IB>(p, tot, tm * BM, tn * BN, tid);
 }
 
-// Four workgroups of 64x64 tiles share a CU (LDS-bound): the register budget
+// ---------------------------------------------------------------- GEMM, direct-to-LDS loads
+// The vectorised kernels load their slabs with buffer_load_dwordx4 ... lds:
+// lane l of a load writes LDS bytes [16 l, 16 l + 16) after the wave's base
+// (M0), from any global offset, so operands go from L2 to LDS without VGPR
+// staging or LDS store instructions.  A slab is kept in its memory layout:
+//   k-contiguous [64 rows][32 k]: pitch 32 floats, the float4 group g of k of
+//     row r in slot g ^ (r & 7); fragment reads are one ds_read_b128 per
+//     16-row block (the k-permutation above), conflict-free;
+//   i/j-contiguous [32 k][64 cols]: pitch 64 floats, the float4 group c of
+//     columns of k-row kr in slot c ^ (8 * ((kr >> 2) & 1)); the wave's MFMA
+//     blocks b = 0, 1 take the interleaved columns 2 j + b, so one
+//     ds_read_b64 at (kr, 2 j) feeds both blocks at one k; conflict-free.
+// Two LDS stages of 16 KB: five workgroups share a CU.  Per slab: fragment
+// reads of chunk 1, MFMAs of chunk 0, wait for this wave's loads of the next
+// slab, barrier (every wave's loads have landed and every read of the
+// current stage is done), fragment reads of the next slab's chunk 0, loads of
+// the slab after next into the current stage, MFMAs of chunk 1.
+#define D_SLAB (64 * GEMM_BK)   // floats per operand slab
+
+template <bool KC>
+struct DSlab {
+    // The wave issues loads 2 * wave + e (e = 0, 1) of the slab's eight.
+    unsigned voff[2];   // lane byte offset at k = 0; OOB_OFFSET outside the tile
+    int klim[2];        // the lane's element is inside the k range iff slab k0 < klim
+    __device__ __forceinline__ void init(int wave, int lane, int ld, int fix0, int fix_lim, int k_lim) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int q = 2 * wave + e;
+            if (KC) {   // rows 8 q .. 8 q + 7, 8 lanes per row
+                const int r = 8 * q + (lane >> 3), g = (lane & 7) ^ (r & 7);
+                voff[e] = fix0 + r < fix_lim ? (unsigned)((fix0 + r) * ld + 4 * g) * 4u : OOB_OFFSET;
+                klim[e] = k_lim - 4 * g;
+            } else {    // k-rows 4 q .. 4 q + 3, 16 lanes per row
+                const int kr = 4 * q + (lane >> 4), c = (lane & 15) ^ (8 * ((kr >> 2) & 1));
+                voff[e] = fix0 + 4 * c < fix_lim ? (unsigned)(kr * ld + fix0 + 4 * c) * 4u : OOB_OFFSET;
+                klim[e] = k_lim - kr;
+            }
+        }
+    }
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, float *slab, int wave, int k0, int ld) const {
+        const unsigned dk = KC ? (unsigned)k0 * 4u : (unsigned)k0 * (unsigned)ld * 4u;
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rs, (__attribute__((address_space(3))) void *)(slab + (2 * wave + e) * 256), 16,
+                k0 < klim[e] ? voff[e] + dk : OOB_OFFSET, 0, 0, 0);
+    }
+};
+
+// f[t][s]: the operand value of MFMA block t at step s of chunk kc, for the
+// wave's 32 rows / columns starting at w * 32.
+template <bool KC>
+__device__ __forceinline__ void d_frags(const float *slab, int w, int li, int lg, int kc, float (&f)[2][4]) {
+    if (KC) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int r = w * 32 + 16 * t + li;
+            const f4 v = *(const f4 *)(slab + r * GEMM_BK + 4 * ((4 * kc + lg) ^ (r & 7)));
+#pragma unroll
+            for (int s = 0; s < 4; ++s) f[t][s] = v[s];
+        }
+    } else {
+        const int col = w * 32 + 2 * li;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int kr = 16 * kc + 4 * lg + s;
+            const f2 v = *(const f2 *)(slab + kr * 64 + 4 * ((col >> 2) ^ (8 * (lg & 1))) + (col & 3));
+            f[0][s] = v.x;
+            f[1][s] = v.y;
+        }
+    }
+}
+
+template <bool AKC, bool BKC, int EPI>
+__device__ __forceinline__ void gemm_dma_body(const GemmArgs &p) {
+    __shared__ __attribute__((aligned(16))) float sm[2 * 2 * D_SLAB];   // [stage][A | B]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1, li = lane & 15, lg = lane >> 4;
+
+    int tile, it0, it1, unit = -1;
+    {
+        const int b = blockIdx.x;
+        if (b < p.dp_tiles) {
+            tile = xcd_remap(b, p.dp_tiles);
+            it0 = 0;
+            it1 = p.iters;
+        } else {
+            const int ntail = (p.tiles_m * p.tiles_n - p.dp_tiles) * p.segs;
+            const int j = b - p.dp_tiles;
+            unit = ((p.dp_tiles & 7) == 0) ? xcd_remap(j, ntail) : j;
+            const int tail = unit / p.segs, seg = unit - tail * p.segs;
+            tile = p.dp_tiles + tail;
+            const int q4 = p.iters >> 2;
+            it0 = (int)((int64_t)seg * q4 / p.segs) * 4;
+            it1 = (int)((int64_t)(seg + 1) * q4 / p.segs) * 4;
+        }
+    }
+    int tm, tn;
+    tile_rc<8>(tile, p.tiles_m, p.tiles_n, tm, tn);
+    const int i0 = tm * 64, j0 = tn * 64;
+    const int kend = min(p.K, it1 * GEMM_BK);
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, p.a_bytes), rb = make_rsrc(p.B, p.b_bytes);
+    DSlab<AKC> la;
+    DSlab<BKC> lb;
+    la.init(wave, lane, p.lda, i0, p.Mo, kend);
+    lb.init(wave, lane, p.ldb, j0, p.No, kend);
+
+    f4 acc[2][2], tot[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) acc[a][b] = tot[a][b] = f4{0.f, 0.f, 0.f, 0.f};
+    auto mfmas = [&](const float (&fa)[2][4], const float (&fb)[2][4]) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int a = 0; a < 2; ++a)
+#pragma unroll
+                for (int b = 0; b < 2; ++b) acc[a][b] = mfma4(fa[a][s], fb[b][s], acc[a][b]);
+    };
+    float *const sA0 = sm, *const sB0 = sm + D_SLAB, *const sA1 = sm + 2 * D_SLAB, *const sB1 = sm + 3 * D_SLAB;
+
+    float f0a[2][4], f0b[2][4], f1a[2][4], f1b[2][4];
+    la.load(ra, sA0, wave, it0 * GEMM_BK, p.lda);
+    lb.load(rb, sB0, wave, it0 * GEMM_BK, p.ldb);
+    __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
+    __syncthreads();
+    d_frags<AKC>(sA0, wm, li, lg, 0, f0a);
+    d_frags<BKC>(sB0, wn, li, lg, 0, f0b);
+    la.load(ra, sA1, wave, (it0 + 1) * GEMM_BK, p.lda);
+    lb.load(rb, sB1, wave, (it0 + 1) * GEMM_BK, p.ldb);
+    for (int kt = it0; kt < it1; kt += 4) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            // it0 is a multiple of 4: slab kt+u lives in stage u & 1
+            float *const ca = (u & 1) ? sA1 : sA0, *const cb = (u & 1) ? sB1 : sB0;
+            float *const na = (u & 1) ? sA0 : sA1, *const nb = (u & 1) ? sB0 : sB1;
+            d_frags<AKC>(ca, wm, li, lg, 1, f1a);
+            d_frags<BKC>(cb, wn, li, lg, 1, f1b);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(f0a, f0b);
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's loads of slab kt+u+1
+            __syncthreads();
+            d_frags<AKC>(na, wm, li, lg, 0, f0a);
+            d_frags<BKC>(nb, wn, li, lg, 0, f0b);
+            __builtin_amdgcn_sched_barrier(0);
+            la.load(ra, ca, wave, (kt + u + 2) * GEMM_BK, p.lda);
+            lb.load(rb, cb, wave, (kt + u + 2) * GEMM_BK, p.ldb);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(f1a, f1b);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                tot[a][b] += acc[a][b];
+                acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
+            }
+    }
+    // No load may still be writing LDS when the workgroup ends.
+    __builtin_amdgcn_s_waitcnt(0x0f70);
+    if (unit >= 0) {
+        float *mine = p.ws + (int64_t)unit * 4096;
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int b = 0; b < 2; ++b) *(f4 *)(mine + ((a * 2 + b) * GEMM_NT + tid) * 4) = tot[a][b];
+        return;
+    }
+    g_epilogue<64, 64, EPI, !AKC, !BKC>(p, tot, i0, j0, tid);
+}
+
+// Register-staged kernels: four workgroups of 64x64 tiles share a CU (LDS), the register budget
 // is held to that occupancy.  (128-wide tiles were measured slower on every
 // linear-sweep shape: one or two workgroups per CU hide less latency.)
 #define GEMM_TILE_KERNEL(name, BM, BN, AKC, BKC, EPI, VEC)                                          \
@@ -652,15 +832,22 @@ __device__ __forceinline__ void gemm_tile_fixup_body(const GemmArgs &p) {
         __attribute__((amdgpu_waves_per_eu(BM * BN <= 4096 ? 4 : 1))) name(GemmArgs p) {          \
         gemm_tile_body<BM, BN, AKC, BKC, EPI, VEC>(p);                                               \
     }
-#define GEMM_TILE_FIXUP(name, BM, BN, EPI) \
-    extern "C" __global__ void __launch_bounds__(GEMM_NT) name(GemmArgs p) { gemm_tile_fixup_body<BM, BN, EPI>(p); }
-#define GEMM_TILE_SET(BM, BN)                                                              \
-    GEMM_TILE_KERNEL(gemm_##BM##x##BN##_fwd_v, BM, BN, true, true, EPI_STORE, true)        \
-    GEMM_TILE_KERNEL(gemm_##BM##x##BN##_fwd_s, BM, BN, true, true, EPI_STORE, false)       \
-    GEMM_TILE_KERNEL(gemm_##BM##x##BN##_dx_v, BM, BN, true, false, EPI_ACCUM, true)        \
-    GEMM_TILE_KERNEL(gemm_##BM##x##BN##_dx_s, BM, BN, true, false, EPI_ACCUM, false)       \
-    GEMM_TILE_KERNEL(gemm_##BM##x##BN##_dw_v, BM, BN, false, false, EPI_ACCUM, true)       \
-    GEMM_TILE_KERNEL(gemm_##BM##x##BN##_dw_s, BM, BN, false, false, EPI_ACCUM, false)      \
-    GEMM_TILE_FIXUP(gemm_##BM##x##BN##_fixup_store, BM, BN, EPI_STORE)                     \
-    GEMM_TILE_FIXUP(gemm_##BM##x##BN##_fixup_accum, BM, BN, EPI_ACCUM)
-GEMM_TILE_SET(64, 64)
+#define GEMM_DMA_KERNEL(name, AKC, BKC, EPI)                                                           \
+    extern "C" __global__ void __launch_bounds__(GEMM_NT) __attribute__((amdgpu_waves_per_eu(4)))      \
+        name(GemmArgs p) {                                                                             \
+        gemm_dma_body<AKC, BKC, EPI>(p);                                                               \
+    }
+#define GEMM_TILE_FIXUP(name, EPI, IA, IB) \
+    extern "C" __global__ void __launch_bounds__(GEMM_NT) name(GemmArgs p) { gemm_tile_fixup_body<64, 64, EPI, IA, IB>(p); }
+GEMM_DMA_KERNEL(gemm_64x64_fwd_v, true, true, EPI_STORE)
+GEMM_DMA_KERNEL(gemm_64x64_dx_v, true, false, EPI_ACCUM)
+GEMM_DMA_KERNEL(gemm_64x64_dw_v, false, false, EPI_ACCUM)
+GEMM_TILE_KERNEL(gemm_64x64_fwd_s, 64, 64, true, true, EPI_STORE, false)
+GEMM_TILE_KERNEL(gemm_64x64_dx_s, 64, 64, true, false, EPI_ACCUM, false)
+GEMM_TILE_KERNEL(gemm_64x64_dw_s, 64, 64, false, false, EPI_ACCUM, false)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_fwd_v, EPI_STORE, false, false)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_dx_v, EPI_ACCUM, false, true)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_dw_v, EPI_ACCUM, true, true)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_fwd_s, EPI_STORE, false, false)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_dx_s, EPI_ACCUM, false, false)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_dw_s, EPI_ACCUM, false, false)

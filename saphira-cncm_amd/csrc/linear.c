@@ -148,7 +148,7 @@ static int run_gemm(int kind, const float *A, const float *B, float *C, const fl
     void *args[] = {&p};
     int rc = ncm_launch(ncm_kernel(name), (unsigned)g.blocks, 1, 1, 256, args);
     if (rc || g.segs == 1) return rc;
-    snprintf(fix, sizeof fix, "gemm_%dx%d_fixup_%s", bm, bn, kind == L_FWD ? "store" : "accum");
+    snprintf(fix, sizeof fix, "gemm_%dx%d_fixup_%s_%c", bm, bn, kind_names[kind], vec ? 'v' : 's');
     return ncm_launch_named(fix, (unsigned)split_tiles, 1, 1, 256, args);
 }
 

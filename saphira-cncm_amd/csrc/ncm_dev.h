@@ -4,6 +4,7 @@
 #include <stdint.h>
 
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f2 __attribute__((ext_vector_type(2)));
 
 // Activation codes; must match NCM_ACT_* in include/ncm_hip.h.
 enum { ACT_NONE = 0, ACT_SILU = 1, ACT_GELU = 2, ACT_GELU_TANH = 3 };

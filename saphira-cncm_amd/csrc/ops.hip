@@ -684,6 +684,102 @@ dec_embed_k(const float *__restrict__ W, const int *__restrict__ ids, const int 
     for (int d = blockIdx.x * 256 + threadIdx.x; d < D; d += gridDim.x * 256) x[d] = W[(int64_t)id * D + d];
 }
 
+// LM head of a decode step, y = W . RMSNorm(x) over V rows (K <= 1024,
+// K % 4 == 0, 16-byte aligned rows), as a grid-stride stream: a workgroup
+// stages the normalised input once (dec_gemv_body's arithmetic), and each
+// wave walks its groups of HEAD_RW rows (group g: rows (gw + g * waves) *
+// HEAD_RW ..) with the next group's loads in flight while the current group is
+// reduced.  Each wave also keeps the first maximum of its rows (it visits them
+// in increasing order; strict '>'); the workgroup merges its four (ties to
+// the lower index) into pv / pi [gridDim.x] for dec_argmax_final_k -- the
+// first stage of the greedy argmax, fused.
+#define HEAD_RW 4
+extern "C" __global__ void __launch_bounds__(256)
+dec_head_stream(const float *__restrict__ x, const float *__restrict__ nw, const float *__restrict__ W,
+                float *__restrict__ y, int V, int K, float *__restrict__ pv, int *__restrict__ pi) {
+#pragma clang fp contract(off)
+    __shared__ __attribute__((aligned(16))) float xs[1024];
+    __shared__ double red[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, K4 = K >> 2;
+    const int gw = blockIdx.x * 4 + wave, NW = gridDim.x * 4;
+    auto fetch = [&](f4 (&w)[HEAD_RW][4], int g) {
+        const int r0 = (gw + g * NW) * HEAD_RW;
+#pragma unroll
+        for (int k = 0; k < HEAD_RW; ++k) {
+            const f4 *row = (const f4 *)(W + (int64_t)min(r0 + k, V - 1) * K);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int c = lane + 64 * e;
+                w[k][e] = c < K4 ? __builtin_nontemporal_load(row + c) : f4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+    };
+    f4 cur[HEAD_RW][4], nxt[HEAD_RW][4];
+    fetch(cur, 0);
+    // input: one float4 per thread (K <= 1024), RMSNorm as dec_gemv_body
+    const f4 xv = tid < K4 ? *(const f4 *)(x + 4 * tid) : f4{0.f, 0.f, 0.f, 0.f};
+    const f4 nv = tid < K4 ? *(const f4 *)(nw + 4 * tid) : f4{1.f, 1.f, 1.f, 1.f};
+    double ss = 0.0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ss += (double)xv[i] * (double)xv[i];
+    ss = wave_sum_d(ss);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    const double ms = (((red[0] + red[1]) + red[2]) + red[3]) / K;
+    const float sc = (float)(1.0 / sqrt(ms + 1e-6));
+    if (tid < K4) {
+        f4 v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = (xv[i] * sc) * nv[i];
+        *(f4 *)(xs + 4 * tid) = v;
+    }
+    __syncthreads();
+    float best = -INFINITY;
+    int bidx = 0x7fffffff;
+    for (int g = 0;; ++g) {
+        const int r0 = (gw + g * NW) * HEAD_RW;
+        if (r0 >= V) break;
+        fetch(nxt, g + 1);
+#pragma unroll
+        for (int k = 0; k < HEAD_RW; ++k) {
+            float acc = 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int c = lane + 64 * e;
+                if (c < K4) {
+                    const f4 xq = *(const f4 *)(xs + 4 * c);
+                    acc += (cur[k][e].x * xq.x + cur[k][e].y * xq.y) + (cur[k][e].z * xq.z + cur[k][e].w * xq.w);
+                }
+            }
+            const float v = wave_sum(acc);
+            const int row = r0 + k;
+            if (row < V) {
+                if (v > best) { best = v; bidx = row; }
+                if (lane == 0) y[row] = v;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < HEAD_RW; ++k)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) cur[k][e] = nxt[k][e];
+    }
+    __shared__ float wv[4];
+    __shared__ int wi[4];
+    if (lane == 0) {
+        wv[wave] = best;
+        wi[wave] = bidx;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float b = wv[0];
+        int i = wi[0];
+        for (int w = 1; w < 4; ++w)
+            if (wv[w] > b || (wv[w] == b && wi[w] < i)) { b = wv[w]; i = wi[w]; }
+        pv[blockIdx.x] = b;
+        pi[blockIdx.x] = i;
+    }
+}
+
 #define AMAX_PER 4096
 // Stage 1: per block of AMAX_PER logits the first maximal value and its index
 // (strict '>' scan per thread, ties to the lower index when merging).

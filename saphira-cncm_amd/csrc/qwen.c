@@ -38,6 +38,7 @@ struct NcmQwen {
     int *pos_dev;           /* position of the current decode step (device) */
     float *amax_v;          /* greedy-argmax block partials */
     int *amax_i, amax_blocks;
+    int head_grid;          /* dec_head_stream workgroups (0: the LM head runs as dec_gemv) */
     int nchunk_max;
     hipGraphExec_t step_graph; /* one decode step + argmax, replayed per token */
     int graph_state;        /* 0 not built, 1 built, -1 capture failed (eager) */
@@ -147,8 +148,14 @@ NcmQwen *ncm_qwen_new(const NcmQwenConfig *c, float *const *params) {
     if (!(m->ids_dev = (int *)ncm_hip_malloc((size_t)(c->n_ctx + 1) * sizeof(int)))) goto fail;
     if (!(m->pos_dev = (int *)ncm_hip_malloc(sizeof(int)))) goto fail;
     m->amax_blocks = (c->vocab + 4095) / 4096;
-    if (!(m->amax_v = (float *)ncm_hip_malloc((size_t)m->amax_blocks * sizeof(float)))) goto fail;
-    if (!(m->amax_i = (int *)ncm_hip_malloc((size_t)m->amax_blocks * sizeof(int)))) goto fail;
+    /* decode LM head: two streaming workgroups per CU when a row fits one
+     * float4 prefetch per lane (K <= 1024) */
+    m->head_grid = (C <= 1024 && C % 4 == 0) ? 2 * ncm_cu_count() : 0;
+    {
+        const int na = m->amax_blocks > 4 * m->head_grid ? m->amax_blocks : 4 * m->head_grid;
+        if (!(m->amax_v = (float *)ncm_hip_malloc((size_t)na * sizeof(float)))) goto fail;
+        if (!(m->amax_i = (int *)ncm_hip_malloc((size_t)na * sizeof(int)))) goto fail;
+    }
     if (build_rope(m)) goto fail;
     return m;
 fail:
@@ -329,6 +336,11 @@ static int decode_core(NcmQwen *m) {
         }
     }
     const int n = ncm_qwen_param_count(c);
+    if (m->head_grid) {
+        void *a[] = {&m->x, (void *)&P[n - 1], (void *)&P[0], &m->logits, (void *)&V, (void *)&C, &m->amax_v,
+                     &m->amax_i};
+        return ncm_launch_named("dec_head_stream", (unsigned)m->head_grid, 1, 1, 256, a);
+    }
     const float *W[1] = {P[0]}, *b[1] = {NULL};
     float *y[1] = {m->logits};
     int N[1] = {V};
@@ -344,7 +356,14 @@ static int greedy_next(NcmQwen *m, const float *logits) {
     return ncm_launch_named("dec_argmax_final_k", 1, 1, 1, 64, a2);
 }
 
-static int decode_argmax(NcmQwen *m) { return greedy_next(m, m->logits); }
+/* After decode_core: with the streamed head its workgroups' maxima are already in
+ * amax_v / amax_i, so only the merge runs. */
+static int decode_argmax(NcmQwen *m) {
+    if (!m->head_grid) return greedy_next(m, m->logits);
+    int nblk = m->head_grid;
+    void *a2[] = {&m->logits, &m->amax_v, &m->amax_i, &nblk, &m->ids_dev, &m->pos_dev};
+    return ncm_launch_named("dec_argmax_final_k", 1, 1, 1, 64, a2);
+}
 
 static int decode_ok(const NcmQwen *m, const char *fn) {
     const int hd = m->c.n_embd / m->c.n_head;

@@ -14,32 +14,48 @@ typedef struct {
     int *idx;
     int *flag_list;
     int *flag_count;
+    int *pair_list;
+    int *pair_count;
+    unsigned long long *keys;
+    unsigned *done;
     int rows, V, D;
     int L, total, off;
 } VqArgs;
 
 #define VQ_MAXD 4096
-#define RESCORE_GRID 512
+#define RESCORE_GRID 1024
 
-/* Device scratch of one search: counters | cn[V] | xn[rows] | flags[rows]. */
+/* Device scratch of one search: counters | cn[V] | xn[rows] | flags[rows] |
+ * pairs[3*rows] | keys[rows] (u64) | done[rows]. */
 typedef struct {
     unsigned *counters;
     float *cn;
     float *xn;
     int *flags;
+    int *pairs;
+    unsigned long long *keys;
+    unsigned *done;
 } VqScratch;
+
+static size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 static int vq_scratch(VqScratch *s, int rows, int V) {
     size_t off_cn = 256;
-    size_t off_xn = off_cn + (((size_t)V * 4 + 255) & ~(size_t)255);
-    size_t off_fl = off_xn + (((size_t)rows * 4 + 255) & ~(size_t)255);
-    size_t total = off_fl + (size_t)rows * 4;
+    size_t off_xn = off_cn + al256((size_t)V * 4);
+    size_t off_fl = off_xn + al256((size_t)rows * 4);
+    size_t off_pr = off_fl + al256((size_t)rows * 4);
+    size_t off_ky = off_pr + al256((size_t)rows * 12);
+    size_t off_dn = off_ky + al256((size_t)rows * 8);
+    size_t total = off_dn + (size_t)rows * 4;
     unsigned char *base = (unsigned char *)ncm_workspace(WS_VQ, total);
     if (!base) return NCM_E_OOM;
     s->counters = (unsigned *)base;
     s->cn = (float *)(base + off_cn);
     s->xn = (float *)(base + off_xn);
     s->flags = (int *)(base + off_fl);
+    s->pairs = (int *)(base + off_pr);
+    s->keys = (unsigned long long *)(base + off_ky);
+    s->done = (unsigned *)(base + off_dn);
     return 0;
 }
 
@@ -58,13 +74,14 @@ static int vq_search(const float *X, const float *E, int *idx, int rows, int V, 
     if ((rc = ncm_launch_named("vq_rownorm", (unsigned)((rows + 3) / 4), 1, 1, 256, a2))) return rc;
 
     int vec = (D % 4 == 0) && is_aligned16(X) && is_aligned16(E);
-    VqArgs p = {X, E, s.cn, s.xn, cmax, idx, s.flags, (int *)s.counters, rows, V, D, L, total, off};
+    VqArgs p = {X, E, s.cn, s.xn, cmax, idx, s.flags, (int *)s.counters,
+                s.pairs, (int *)s.counters + 2, s.keys, s.done, rows, V, D, L, total, off};
     void *a3[] = {&p};
     if ((rc = ncm_launch_named(vec ? "vq_argmin_main_v" : "vq_argmin_main_s",
                                (unsigned)((rows + 127) / 128), 1, 1, 256, a3)))
         return rc;
     const unsigned *cnt = s.counters;
-    void *a4[] = {&X, &E, &V, &D, &s.flags, &cnt, &idx, &L, &total, &off};
+    void *a4[] = {&X, &E, &V, &D, &vec, &s.flags, &s.pairs, &cnt, &s.keys, &s.done, &idx, &L, &total, &off};
     return ncm_launch_named("vq_rescore", RESCORE_GRID, 1, 1, 256, a4);
 }
 

@@ -80,6 +80,44 @@ def test_duplicate_and_planted_codewords():
     assert np.array_equal(got, O.vq_argmin(a, E))
 
 
+def test_three_way_ties_across_blocks():
+    """Three or more codewords at the same distance, spread over several
+    blocks of 256 codewords: the full rescore's per-block minima must merge
+    to the lowest index.  Two-way ties take the pair rescore."""
+    rng = np.random.default_rng(12)
+    a = rng.standard_normal((700, 64)).astype(np.float32)
+    E = (rng.standard_normal((1100, 64)) / 8).astype(np.float32)
+    for r in range(0, 700, 7):
+        k = r // 7
+        dup = [1099 - k, 800 - k, 520 - k, 260 - k][: 2 + k % 3]
+        for j in dup:
+            E[j] = a[r]
+    got = gpu_argmin(a, E)
+    want = O.vq_argmin(a, E)
+    assert np.array_equal(got, want)
+    assert got[0] == 800 and got[7] == 519 and got[14] == 258
+
+
+def test_nonfinite_inputs():
+    """NaN at codeword 0 keeps every row at index 0 (the reference scan never
+    leaves it); NaN or inf elsewhere never wins; a NaN row gives index 0."""
+    rng = np.random.default_rng(13)
+    a = rng.standard_normal((300, 40)).astype(np.float32)
+    E = (rng.standard_normal((600, 40)) / 6).astype(np.float32)
+    a[5, 3] = np.nan
+    a[6, 0] = np.inf
+    E1 = E.copy()
+    E1[0, 9] = np.nan
+    E2 = E.copy()
+    E2[300, 1] = np.nan
+    E2[301, 2] = np.inf
+    E2[17] = a[9]
+    for Ec in (E1, E2):
+        got = gpu_argmin(a, Ec)
+        assert np.array_equal(got, O.vq_argmin(a, Ec))
+    assert np.all(gpu_argmin(a, E1) == 0)
+
+
 def test_near_ties_certificate():
     """Codewords placed symmetrically around rows so that distances differ by
     a few ulps: the fp32 screen cannot decide them, the rescore must."""

@@ -42,7 +42,7 @@
 // levels keep it near (128 + K/128) u.
 //
 // Epilogues: STORE  C = res + act(acc + bias);  ACCUM  C += acc.
-#include "ncm_dev.h"
+#include "mfma_slab.h"
 
 enum { EPI_STORE = 0, EPI_ACCUM = 1 };
 
@@ -64,10 +64,6 @@ struct GemmArgs {
     unsigned a_bytes, b_bytes;  // extents of A and B for the buffer descriptors
 };
 
-#define GEMM_BK 32
-#define GEMM_NT 256
-#define OOB_OFFSET 0x80000000u
-
 // Grouped raster: GROUP_M tile rows advance together along N so that the B
 // panels they share stay in L2.
 template <int GROUP_M>
@@ -79,16 +75,6 @@ __device__ __forceinline__ void tile_rc(int t, int tiles_m, int tiles_n, int &tm
     int in = t - g * group;
     tm = first + in % gm;
     tn = in / gm;
-}
-
-// Workgroups are dispatched round-robin over the 8 XCDs (each with its own
-// L2): give every XCD a contiguous range of n work items.
-__device__ __forceinline__ int xcd_remap(int j, int n) {
-    return (n & 7) == 0 ? (j & 7) * (n >> 3) + (j >> 3) : j;
-}
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const float *base, unsigned bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)bytes, 0x00020000);
 }
 
 // db[m] += (float) sum_r dy[r,m], the bias gradient of train_tape.c:708-713,
@@ -651,78 +637,11 @@ __device__ __forceinline__ void gemm_tile_fixup_body(const GemmArgs &p) {
 }
 
 // ---------------------------------------------------------------- GEMM, direct-to-LDS loads
-// The vectorised kernels load their slabs with buffer_load_dwordx4 ... lds:
-// lane l of a load writes LDS bytes [16 l, 16 l + 16) after the wave's base
-// (M0), from any global offset, so operands go from L2 to LDS without VGPR
-// staging or LDS store instructions.  A slab is kept in its memory layout:
-//   k-contiguous [64 rows][32 k]: pitch 32 floats, the float4 group g of k of
-//     row r in slot g ^ (r & 7); fragment reads are one ds_read_b128 per
-//     16-row block (the k-permutation above), conflict-free;
-//   i/j-contiguous [32 k][64 cols]: pitch 64 floats, the float4 group c of
-//     columns of k-row kr in slot c ^ (8 * ((kr >> 2) & 1)); the wave's MFMA
-//     blocks b = 0, 1 take the interleaved columns 2 j + b, so one
-//     ds_read_b64 at (kr, 2 j) feeds both blocks at one k; conflict-free.
 // Two LDS stages of 16 KB: five workgroups share a CU.  Per slab: fragment
 // reads of chunk 1, MFMAs of chunk 0, wait for this wave's loads of the next
 // slab, barrier (every wave's loads have landed and every read of the
 // current stage is done), fragment reads of the next slab's chunk 0, loads of
 // the slab after next into the current stage, MFMAs of chunk 1.
-#define D_SLAB (64 * GEMM_BK)   // floats per operand slab
-
-template <bool KC>
-struct DSlab {
-    // The wave issues loads 2 * wave + e (e = 0, 1) of the slab's eight.
-    unsigned voff[2];   // lane byte offset at k = 0; OOB_OFFSET outside the tile
-    int klim[2];        // the lane's element is inside the k range iff slab k0 < klim
-    __device__ __forceinline__ void init(int wave, int lane, int ld, int fix0, int fix_lim, int k_lim) {
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            const int q = 2 * wave + e;
-            if (KC) {   // rows 8 q .. 8 q + 7, 8 lanes per row
-                const int r = 8 * q + (lane >> 3), g = (lane & 7) ^ (r & 7);
-                voff[e] = fix0 + r < fix_lim ? (unsigned)((fix0 + r) * ld + 4 * g) * 4u : OOB_OFFSET;
-                klim[e] = k_lim - 4 * g;
-            } else {    // k-rows 4 q .. 4 q + 3, 16 lanes per row
-                const int kr = 4 * q + (lane >> 4), c = (lane & 15) ^ (8 * ((kr >> 2) & 1));
-                voff[e] = fix0 + 4 * c < fix_lim ? (unsigned)(kr * ld + fix0 + 4 * c) * 4u : OOB_OFFSET;
-                klim[e] = k_lim - kr;
-            }
-        }
-    }
-    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, float *slab, int wave, int k0, int ld) const {
-        const unsigned dk = KC ? (unsigned)k0 * 4u : (unsigned)k0 * (unsigned)ld * 4u;
-#pragma unroll
-        for (int e = 0; e < 2; ++e)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rs, (__attribute__((address_space(3))) void *)(slab + (2 * wave + e) * 256), 16,
-                k0 < klim[e] ? voff[e] + dk : OOB_OFFSET, 0, 0, 0);
-    }
-};
-
-// f[t][s]: the operand value of MFMA block t at step s of chunk kc, for the
-// wave's 32 rows / columns starting at w * 32.
-template <bool KC>
-__device__ __forceinline__ void d_frags(const float *slab, int w, int li, int lg, int kc, float (&f)[2][4]) {
-    if (KC) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const int r = w * 32 + 16 * t + li;
-            const f4 v = *(const f4 *)(slab + r * GEMM_BK + 4 * ((4 * kc + lg) ^ (r & 7)));
-#pragma unroll
-            for (int s = 0; s < 4; ++s) f[t][s] = v[s];
-        }
-    } else {
-        const int col = w * 32 + 2 * li;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const int kr = 16 * kc + 4 * lg + s;
-            const f2 v = *(const f2 *)(slab + kr * 64 + 4 * ((col >> 2) ^ (8 * (lg & 1))) + (col & 3));
-            f[0][s] = v.x;
-            f[1][s] = v.y;
-        }
-    }
-}
-
 template <bool AKC, bool BKC, int EPI>
 __device__ __forceinline__ void gemm_dma_body(const GemmArgs &p) {
     __shared__ __attribute__((aligned(16))) float sm[2 * 2 * D_SLAB];   // [stage][A | B]

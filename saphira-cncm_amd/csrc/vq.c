@@ -77,8 +77,8 @@ static int vq_search(const float *X, const float *E, int *idx, int rows, int V, 
     VqArgs p = {X, E, s.cn, s.xn, cmax, idx, s.flags, (int *)s.counters,
                 s.pairs, (int *)s.counters + 2, s.keys, s.done, rows, V, D, L, total, off};
     void *a3[] = {&p};
-    if ((rc = ncm_launch_named(vec ? "vq_argmin_main_v" : "vq_argmin_main_s",
-                               (unsigned)((rows + 127) / 128), 1, 1, 256, a3)))
+    if ((rc = ncm_launch_named(vec ? "vq_argmin_main_v" : "vq_argmin_main_s", (unsigned)((rows + 63) / 64), 1,
+                               1, 256, a3)))
         return rc;
     const unsigned *cnt = s.counters;
     void *a4[] = {&X, &E, &V, &D, &vec, &s.flags, &s.pairs, &cnt, &s.keys, &s.done, &idx, &L, &total, &off};

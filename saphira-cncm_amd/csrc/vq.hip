@@ -7,7 +7,7 @@
 // (fp64, serial over c, no FMA; strict '<' scan).  The search runs in two
 // stages:
 //
-// 1. vq_argmin_main -- an FP32-MFMA contraction s = x . E^T over all V
+// 1. vq_argmin_main_* -- an FP32-MFMA contraction s = x . E^T over all V
 //    codewords with a fused running (best, index, second, index, third) per
 //    row of
 //        e_j = |E_j|^2 - 2 x.E_j     (= d2 - |x|^2, same order as d2)
@@ -25,7 +25,7 @@
 //    codewords, split over workgroups of 256 codewords whose (d2, index)
 //    minima meet in a 64-bit atomicMin.  The lowest index of the minimal
 //    float distance wins, as in the reference's strict '<' scan.
-#include "ncm_dev.h"
+#include "mfma_slab.h"
 
 #include <float.h>
 
@@ -125,114 +125,29 @@ vq_rownorm(const float *__restrict__ X, int rows, int D, float *__restrict__ xn)
     }
 }
 
-// Stage 1.  Workgroup = 128 rows x all V codewords, 4 waves of 64x64 MFMA
-// sub-tiles per 128-codeword tile, BK = 16; the (codeword tile, k slab)
-// sequence is one double-buffered pipeline.
-#define VQ_BM 128
-#define VQ_BN 128
-#define VQ_BK 16
+// Running (best, index, second, index, third) of one row slot; j arrives in
+// increasing order, so the strict '<' keeps the lowest index among equal e.
+#define VQ_TRACK(s, e, j)                                                         \
+    do {                                                                          \
+        if ((e) < m1[s]) {                                                        \
+            m3[s] = m2[s]; m2[s] = m1[s]; i2[s] = i1[s]; m1[s] = (e); i1[s] = (j); \
+        } else if ((e) < m2[s]) {                                                 \
+            m3[s] = m2[s]; m2[s] = (e); i2[s] = (j);                              \
+        } else {                                                                  \
+            m3[s] = fminf(m3[s], (e));                                            \
+        }                                                                         \
+    } while (0)
 
-template <bool VEC>
-__device__ __forceinline__ void vq_main_body(const VqArgs &p) {
-    constexpr int NT = 256, WM = 64, WN = 64, TM = 4, TN = 4;
-    constexpr int LDA = VQ_BK + 4;
-    constexpr int A_SZ = VQ_BM * LDA, B_SZ = VQ_BN * LDA;
-    __shared__ __attribute__((aligned(16))) float smem[2 * (A_SZ + B_SZ)];
-    __shared__ float red_m1[VQ_BM], red_m2[VQ_BM], red_m3[VQ_BM];
-    __shared__ int red_i1[VQ_BM], red_i2[VQ_BM];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int li = lane & 15, lg = lane >> 4;
-    const int i0 = blockIdx.x * VQ_BM;
-
-    const int nks = (p.D + VQ_BK - 1) / VQ_BK;
-    const int nnt = (p.V + VQ_BN - 1) / VQ_BN;
-    const int nsteps = nks * nnt;
-
-    TileLoader<VQ_BM, VQ_BK, NT, VEC> la;
-    TileLoader<VQ_BN, VQ_BK, NT, VEC> lb;
-
-    float m1[TM * 4], m2[TM * 4], m3[TM * 4];
-    int i1[TM * 4], i2[TM * 4];
+// Folds the per-lane lists of NS row slots (rows lrow(s) of the workgroup's
+// tile) over the 16 lanes li that share a row and the two waves wn = 0, 1,
+// then decides each row: certified code, pair rescore or full rescore.
+template <int NS, typename RowOf>
+__device__ __forceinline__ void vq_decide(const VqArgs &p, float (&m1)[NS], int (&i1)[NS], float (&m2)[NS],
+                                          int (&i2)[NS], float (&m3)[NS], int i0, int wn, int li,
+                                          float *red_m1, float *red_m2, float *red_m3, int *red_i1,
+                                          int *red_i2, RowOf lrow) {
 #pragma unroll
-    for (int s = 0; s < TM * 4; ++s) {
-        m1[s] = INFINITY; m2[s] = INFINITY; m3[s] = INFINITY; i1[s] = -1; i2[s] = -1;
-    }
-
-    f4 acc[TM][TN];
-#pragma unroll
-    for (int a = 0; a < TM; ++a)
-#pragma unroll
-        for (int b = 0; b < TN; ++b) acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
-
-    auto gload = [&](int step) {
-        int nt = step / nks, kt = step - nt * nks;
-        la.load(p.X, p.D, i0, kt * VQ_BK, p.rows, p.D, tid);
-        lb.load(p.E, p.D, nt * VQ_BN, kt * VQ_BK, p.V, p.D, tid);
-    };
-
-    gload(0);
-    la.store(smem, tid);
-    lb.store(smem + 2 * A_SZ, tid);
-    __syncthreads();
-
-    for (int st = 0; st < nsteps; ++st) {
-        const int cur = st & 1;
-        const bool more = st + 1 < nsteps;
-        if (more) gload(st + 1);
-        const float *a_s = smem + cur * A_SZ;
-        const float *b_s = smem + 2 * A_SZ + cur * B_SZ;
-        f4 ak[TM], bk[TN];
-#pragma unroll
-        for (int t = 0; t < TM; ++t) ak[t] = *(const f4 *)(a_s + (wm * WM + t * 16 + li) * LDA + 4 * lg);
-#pragma unroll
-        for (int t = 0; t < TN; ++t) bk[t] = *(const f4 *)(b_s + (wn * WN + t * 16 + li) * LDA + 4 * lg);
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-#pragma unroll
-            for (int a = 0; a < TM; ++a)
-#pragma unroll
-                for (int b = 0; b < TN; ++b) acc[a][b] = mfma4(ak[a][s], bk[b][s], acc[a][b]);
-
-        const int nt = st / nks;
-        if (st - nt * nks == nks - 1) {
-            // codeword tile complete: fold e_j = cn_j - 2 s into the running triples
-#pragma unroll
-            for (int b = 0; b < TN; ++b) {
-                const int j = nt * VQ_BN + wn * WN + b * 16 + li;
-                if (j < p.V) {
-                    const float cj = p.cn[j];
-#pragma unroll
-                    for (int a = 0; a < TM; ++a)
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            float e = cj - 2.0f * acc[a][b][r];
-                            int s = a * 4 + r;
-                            if (e < m1[s]) {
-                                m3[s] = m2[s]; m2[s] = m1[s]; i2[s] = i1[s]; m1[s] = e; i1[s] = j;
-                            } else if (e < m2[s]) {
-                                m3[s] = m2[s]; m2[s] = e; i2[s] = j;
-                            } else {
-                                m3[s] = fminf(m3[s], e);
-                            }
-                        }
-                }
-#pragma unroll
-                for (int a = 0; a < TM; ++a) acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
-            }
-        }
-        if (more) {
-            la.store(smem + (cur ^ 1) * A_SZ, tid);
-            lb.store(smem + 2 * A_SZ + (cur ^ 1) * B_SZ, tid);
-        }
-        __syncthreads();
-    }
-
-    // lanes sharing a row: the 16 li values of one lg group
-#pragma unroll
-    for (int s = 0; s < TM * 4; ++s) {
+    for (int s = 0; s < NS; ++s) {
 #pragma unroll
         for (int o = 1; o < 16; o <<= 1) {
             float o1 = __shfl_xor(m1[s], o, 64);
@@ -243,11 +158,10 @@ __device__ __forceinline__ void vq_main_body(const VqArgs &p) {
             merge5(m1[s], i1[s], m2[s], i2[s], m3[s], o1, oi1, o2, oi2, o3);
         }
     }
-    // the two waves (wn = 0, 1) sharing rows
     if (wn == 1 && li == 0) {
 #pragma unroll
-        for (int s = 0; s < TM * 4; ++s) {
-            int lr = wm * WM + (s >> 2) * 16 + 4 * lg + (s & 3);
+        for (int s = 0; s < NS; ++s) {
+            const int lr = lrow(s);
             red_m1[lr] = m1[s]; red_m2[lr] = m2[s]; red_m3[lr] = m3[s];
             red_i1[lr] = i1[s]; red_i2[lr] = i2[s];
         }
@@ -256,9 +170,9 @@ __device__ __forceinline__ void vq_main_body(const VqArgs &p) {
     if (wn == 0 && li == 0) {
         const float cm = __uint_as_float(*p.cmax_bits);
 #pragma unroll
-        for (int s = 0; s < TM * 4; ++s) {
-            int lr = wm * WM + (s >> 2) * 16 + 4 * lg + (s & 3);
-            int row = i0 + lr;
+        for (int s = 0; s < NS; ++s) {
+            const int lr = lrow(s);
+            const int row = i0 + lr;
             if (row >= p.rows) continue;
             merge5(m1[s], i1[s], m2[s], i2[s], m3[s], red_m1[lr], red_i1[lr], red_m2[lr], red_i2[lr],
                    red_m3[lr]);
@@ -283,8 +197,201 @@ __device__ __forceinline__ void vq_main_body(const VqArgs &p) {
     }
 }
 
-extern "C" __global__ void __launch_bounds__(256, 2) vq_argmin_main_v(VqArgs p) { vq_main_body<true>(p); }
-extern "C" __global__ void __launch_bounds__(256, 2) vq_argmin_main_s(VqArgs p) { vq_main_body<false>(p); }
+// Register-staged slab loads for the scalar screen: the same [64 rows][32 k]
+// swizzled slab as the direct-to-LDS loads (mfma_slab.h), any D and
+// alignment.  Thread t stages float4 groups q = t and t + 256 (row q / 8,
+// group q % 8); elements outside the rows or past D read zero.
+struct VqStage {
+    f4 v[2];
+    __device__ __forceinline__ void load(const float *__restrict__ src, int ld, int row0, int nrows, int k0, int tid) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int q = tid + 256 * e, r = q >> 3, k = k0 + 4 * (q & 7);
+            f4 x = {0.f, 0.f, 0.f, 0.f};
+            if (row0 + r < nrows) {
+                const float *sp = src + (int64_t)(row0 + r) * ld + k;
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (k + c < ld) x[c] = sp[c];
+            }
+            v[e] = x;
+        }
+    }
+    __device__ __forceinline__ void store(float *slab, int tid) const {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int q = tid + 256 * e, r = q >> 3, g = q & 7;
+            *(f4 *)(slab + r * GEMM_BK + 4 * (g ^ (r & 7))) = v[e];
+        }
+    }
+};
+
+// Stage 1: a workgroup owns 64 rows and sweeps all V codewords in tiles of
+// 64; the (codeword tile, k slab) pairs form one stream of [64][32] slabs in
+// two LDS stages.  Each wave owns 32 rows x 32 codewords of a tile (2 x 2
+// MFMA blocks, fragments as in the linear GEMM); after a tile's last slab the
+// accumulators are folded into the running lists.  Four workgroups share a CU.
+//   DMA (vectorised: D % 4 == 0, 16-byte aligned rows): the linear GEMM's
+//     direct-to-LDS pipeline -- one barrier per slab, fragment reads one
+//     chunk ahead of the MFMAs, the loads of the slab after next issued after
+//     the barrier.  Buffer descriptors are rebased on the workgroup's rows and
+//     on each codeword tile, sized to the rows that exist, so rows past either
+//     end read zero (and are never folded or written).
+//   register-staged (any D, any alignment): the next slab's loads are issued
+//     before this slab's MFMAs and stored to the other stage after them.
+template <bool DMA>
+__device__ __forceinline__ void vq_screen_body(const VqArgs &p) {
+    __shared__ __attribute__((aligned(16))) float sm[4 * D_SLAB];  // [stage][X | E]
+    __shared__ float red_m1[64], red_m2[64], red_m3[64];
+    __shared__ int red_i1[64], red_i2[64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1, li = lane & 15, lg = lane >> 4;
+    const int i0 = blockIdx.x * 64;
+    const int ld = p.D;
+    const int nks = (p.D + GEMM_BK - 1) / GEMM_BK;
+    const int ntiles = (p.V + 63) / 64;
+    const int nsteps = nks * ntiles;
+    const __attribute__((address_space(1))) float *cn = (const __attribute__((address_space(1))) float *)p.cn;
+
+    float m1[8], m2[8], m3[8];
+    int i1[8], i2[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        m1[s] = INFINITY; m2[s] = INFINITY; m3[s] = INFINITY; i1[s] = -1; i2[s] = -1;
+    }
+    f4 acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
+    auto mfmas = [&](const float (&fa)[2][4], const float (&fb)[2][4]) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int a = 0; a < 2; ++a)
+#pragma unroll
+                for (int b = 0; b < 2; ++b) acc[a][b] = mfma4(fa[a][s], fb[b][s], acc[a][b]);
+    };
+    // |E_j|^2 of the lane's two codeword columns, one tile ahead
+    float cj[2];
+    auto load_cn = [&](int nt) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const int j = nt * 64 + wn * 32 + b * 16 + li;
+            cj[b] = j < p.V ? cn[j] : 0.f;
+        }
+    };
+    int nt = 0, kt = 0;
+    // after each slab: a finished codeword tile folds e_j = |E_j|^2 - 2 x.E_j
+    auto advance = [&]() {
+        if (++kt < nks) return;
+        kt = 0;
+        const float c[2] = {cj[0], cj[1]};
+        load_cn(nt + 1);
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const int j = nt * 64 + wn * 32 + b * 16 + li;
+            if (j < p.V) {
+#pragma unroll
+                for (int a = 0; a < 2; ++a)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float e = c[b] - 2.0f * acc[a][b][r];
+                        VQ_TRACK(a * 4 + r, e, j);
+                    }
+            }
+#pragma unroll
+            for (int a = 0; a < 2; ++a) acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
+        }
+        ++nt;
+    };
+
+    float *const s0 = sm, *const s1 = sm + 2 * D_SLAB;
+    float f0a[2][4], f0b[2][4], f1a[2][4], f1b[2][4];
+    load_cn(0);
+    if constexpr (DMA) {
+        const __amdgpu_buffer_rsrc_t ra =
+            make_rsrc(p.X + (int64_t)i0 * ld, (unsigned)(min(p.rows - i0, 64) * ld * 4));
+        DSlab<true> la, lb;
+        la.init(wave, lane, ld, 0, 64, p.D);
+        lb.init(wave, lane, ld, 0, 64, p.D);
+        // the load stream runs two slabs ahead of the compute stream
+        int lnt = 0, lkt = 0;
+        auto issue = [&](float *stage) {
+            const int nr = min(max(p.V - lnt * 64, 0), 64);
+            const __amdgpu_buffer_rsrc_t rb =
+                make_rsrc(nr ? p.E + (int64_t)lnt * 64 * ld : p.E, (unsigned)(nr * ld * 4));
+            la.load(ra, stage, wave, lkt * GEMM_BK, ld);
+            lb.load(rb, stage + D_SLAB, wave, lkt * GEMM_BK, ld);
+            if (++lkt == nks) { lkt = 0; ++lnt; }
+        };
+        issue(s0);
+        __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
+        __syncthreads();
+        d_frags<true>(s0, wm, li, lg, 0, f0a);
+        d_frags<true>(s0 + D_SLAB, wn, li, lg, 0, f0b);
+        issue(s1);
+        auto step = [&](float *cs, float *ns) {
+            d_frags<true>(cs, wm, li, lg, 1, f1a);
+            d_frags<true>(cs + D_SLAB, wn, li, lg, 1, f1b);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(f0a, f0b);
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's loads of the next slab
+            __syncthreads();
+            d_frags<true>(ns, wm, li, lg, 0, f0a);
+            d_frags<true>(ns + D_SLAB, wn, li, lg, 0, f0b);
+            __builtin_amdgcn_sched_barrier(0);
+            issue(cs);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(f1a, f1b);
+            __builtin_amdgcn_sched_barrier(0);
+            advance();
+        };
+        for (int st = 0; st < nsteps; st += 2) {
+            step(s0, s1);
+            if (st + 1 < nsteps) step(s1, s0);
+        }
+        // No load may still be writing LDS when the workgroup ends.
+        __builtin_amdgcn_s_waitcnt(0x0f70);
+    } else {
+        VqStage ga, gb;
+        int lnt = 0, lkt = 0;
+        auto fetch = [&]() {
+            ga.load(p.X, ld, i0, p.rows, lkt * GEMM_BK, tid);
+            gb.load(p.E, ld, lnt * 64, p.V, lkt * GEMM_BK, tid);
+            if (++lkt == nks) { lkt = 0; ++lnt; }
+        };
+        fetch();
+        ga.store(s0, tid);
+        gb.store(s0 + D_SLAB, tid);
+        __syncthreads();
+        for (int st = 0; st < nsteps; ++st) {
+            float *const cs = (st & 1) ? s1 : s0, *const ns = (st & 1) ? s0 : s1;
+            const bool more = st + 1 < nsteps;
+            if (more) fetch();
+            d_frags<true>(cs, wm, li, lg, 0, f0a);
+            d_frags<true>(cs + D_SLAB, wn, li, lg, 0, f0b);
+            d_frags<true>(cs, wm, li, lg, 1, f1a);
+            d_frags<true>(cs + D_SLAB, wn, li, lg, 1, f1b);
+            mfmas(f0a, f0b);
+            mfmas(f1a, f1b);
+            advance();
+            if (more) {
+                ga.store(ns, tid);
+                gb.store(ns + D_SLAB, tid);
+            }
+            __syncthreads();
+        }
+    }
+    vq_decide<8>(p, m1, i1, m2, i2, m3, i0, wn, li, red_m1, red_m2, red_m3, red_i1, red_i2,
+                 [&](int s) { return wm * 32 + (s >> 2) * 16 + 4 * lg + (s & 3); });
+}
+
+extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
+vq_argmin_main_v(VqArgs p) { vq_screen_body<true>(p); }
+extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
+vq_argmin_main_s(VqArgs p) { vq_screen_body<false>(p); }
 
 // The reference distance, bit for bit: fp64, serial over c, separate
 // multiply and add roundings (kernels.c:760-765), then rounded to float.

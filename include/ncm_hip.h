@@ -416,6 +416,187 @@ int argmax_row(const float *x, int n);
  * index on ties.  Replaces backend_to_host + argmax_row (qwen.c:220-222). */
 void argmax_rows(const float *x, int *idx, int64_t rows, int n);
 
+/* ------------------------------------------------------------------ */
+/* on-disk formats -- replaces the loaders of src/tensor.c (ncm.h:57-70, */
+/* 72-139, 262-265) and weights_save (train.c:741-767)                  */
+/* ------------------------------------------------------------------ */
+
+/* Same layouts as ncm.h:58-66; every tensor lives in device memory. */
+typedef struct {
+    char    name[256];
+    Tensor *t;
+} NamedTensor;
+
+typedef struct {
+    NamedTensor *items;
+    int          count;
+} WeightStore;
+
+/* replaces weights_load, tensor.c:70-132: an "NCM1" file (magic, u32 count,
+ * then per tensor u8 name length, name, u8 ndim, u32 dims, u64 byte count,
+ * float32 data, all little-endian), or the weights section of an "NCK1"
+ * checkpoint.  0 on success; -1 (store left empty) on a missing file, bad
+ * magic, truncation or a byte count that does not match the shape. */
+int     weights_load(WeightStore *ws, const char *path);
+/* replaces weights_free / weights_get, tensor.c:134-143 */
+void    weights_free(WeightStore *ws);
+Tensor *weights_get(WeightStore *ws, const char *name); /* NULL if missing */
+/* replaces weights_save, train.c:741-767: writes the NCM1 layout above */
+int     weights_save(WeightStore *ws, const char *path);
+
+#define NCM_MAX_LEVELS 64
+#define NCM_MAX_VOCAB_LIST 64
+
+/* Same layout and field meaning as the reference NCMConfig (ncm.h:75-137). */
+typedef struct {
+    char task[64];
+    int  n_layer, n_head, n_embd, context_length, prefix_len;
+    int  bias;
+    int  raw_token_prefix, contextual_prefix;
+    int  prefix_pad_token_id;
+    int  vocab_size[NCM_MAX_VOCAB_LIST];
+    int  n_levels_out;
+    int  predict_level0, query_level0, l0_autoregressive;
+    int  attn_pattern_block_diag;
+    int  use_positional_encoding, use_level_encoding;
+    int  use_rope, rope_base, use_qk_norm, use_flex_attention;
+    double rope_theta;
+    int  n_kv_heads;
+    int  ctx_enabled, ctx_n_layer, ctx_vocab;
+    int  puc_enabled, puc_kernel;
+    int  shared_output_head, shared_head_per_level_bias, untied_head_bias;
+    int  tie_heads_to_codebook, tie_heads_learn_scale, tie_heads_trainable;
+    int  tie_heads_bias;
+    int  use_swiglu, use_geglu, use_relu2, parallel_block, normformer;
+    int  use_layerscale, use_rezero;
+    float layerscale_init;
+    float dropout;
+    int  vq_embed_dim, vq_in_vocab, vq_context_length, vq_n_layers;
+    int  vq_compression;
+    int  vq_soft_levels;
+    double vq_soft_tau;
+    int  levels[NCM_MAX_LEVELS];
+    int  n_qlevels;
+    int  vq_vocab[NCM_MAX_LEVELS];
+    float quant_resi_ratio;
+    int   quant_resi_enabled;
+    int   quant_resi_share_mode;
+    int   learned_l1_sampling, learned_l1_cascade;
+    int   learned_l1_cascade_base;
+    int   learned_l1_norm, learned_l1_norm_final;
+    int   learned_all_sampling;
+    int   pre_quant_groupnorm;
+    int   vq_qk_norm;
+    int   enc_layers, enc_attn_window, enc_conv_layers, enc_conv_kernel;
+    int   enc_positional;
+    int   dec_layers, dec_positional;
+    char pre_tok[16];
+    int  sudoku_size;
+    char hf_model_id[128];
+    int  eos_token_id, pad_token_id;
+    float gen_temperature;
+    int   gen_top_k;
+    float gen_top_p, gen_cfg_scale;
+    float gen_freq, gen_mu;
+    float gen_adj_a; int gen_adj_w; float gen_adj_d;
+} NCMConfig;
+
+/* replaces config_load, tensor.c:145-266: `key=value` lines with model.*,
+ * vq.*, tok.* and gen.* keys over the reference's defaults; unknown keys and
+ * lines without '=' are ignored.  0 on success, -1 if the file cannot be
+ * opened.  Host only (no device use). */
+int config_load(NCMConfig *c, const char *path);
+
+/* replaces train_data_load / train_data_free, ncm.h:262-264, tensor.c:375-395:
+ * "NCMT" magic, u64 rows, u64 row length, int32 tokens; at most max_rows rows
+ * when max_rows > 0.  HOST rows; NULL on error.  Host only. */
+typedef struct { int *rows; int n_rows, row_len; } TrainData;
+TrainData *train_data_load(const char *path, int max_rows);
+void       train_data_free(TrainData *d);
+
+/* ------------------------------------------------------------------ */
+/* AdamW object + NCK1 checkpoints -- replaces train.c:15-150 and        */
+/* src/ckpt.c (ncm.h:416-466, 523-540)                                  */
+/* ------------------------------------------------------------------ */
+
+/* The reference AdamW (ncm.h:523-536) with the moments and gradient
+ * accumulators resident on the device: params, m, v and g are DEVICE
+ * pointers (sizes[i] floats each); lr[i] is the per-tensor multiplier. */
+typedef struct AdamW {
+    float **params;
+    float **m, **v;
+    float **g;
+    int64_t *sizes;
+    double *lr;
+    int n;
+    double b1, b2, eps, wd;
+    long step;
+} AdamW;
+
+/* replaces adamw_new, train.c:18-41: every tensor of the store not flagged
+ * in `frozen` (may be NULL), zero moments and gradients, b1 0.9, b2 0.95,
+ * eps 1e-8, wd 0.01, lr multipliers 1.  NULL on allocation failure. */
+AdamW *adamw_new(WeightStore *ws, const int *frozen);
+/* replaces adamw_zero_grad, train.c:43-46 (device memset of every g[i]) */
+void   adamw_zero_grad(AdamW *o);
+/* replaces adamw_step, train.c:102-145: step += 1, lr = base_lr *
+ * sched_cosine_warmup(step, warmup, total) * lr[i], the k_adamw update of
+ * every tensor (bit-identical to the reference's host loop) */
+void   adamw_step(AdamW *o, double base_lr, double warmup, double total);
+void   adamw_free(AdamW *o);                 /* train.c:147-159 */
+/* replaces adamw_sync_to_host, train.c:85-98: a no-op, the moments have no
+ * host copy (a checkpoint save reads them from the device) */
+void   adamw_sync_to_host(AdamW *o);
+
+/* Same layouts as ncm.h:426-439 and ncm.h:450-456. */
+typedef struct {
+    long global_step;
+    unsigned long long batch_rng;
+    double base_lr, warmup, total;
+    int batch_B;
+    int accum_pending;
+    long n_rows; int row_len;
+    uint64_t data_hash;
+    const char *data_path;
+    uint64_t conf_hash;
+    const char *tokenizer_id;
+    double noise_sd;
+    const char *train_cfg_json;
+} CkptRunState;
+
+typedef struct {
+    int batch_B; long n_rows; int row_len; uint64_t data_hash;
+    uint64_t conf_hash; const char *tokenizer_id;
+    double base_lr, warmup, total;
+    double b1, b2, eps, wd;
+} CkptExpect;
+
+/* replaces ckpt_probe, ckpt.c:67-78: 1 = NCK1, 0 = NCM1, -1 = unreadable */
+int ckpt_probe(const char *path);
+/* replaces ckpt_file_hash, ckpt.c:50-64: FNV-1a 64 of the file's bytes */
+uint64_t ckpt_file_hash(const char *path, uint64_t *nbytes_out);
+/* replaces ckpt_save_atomic, ckpt.c:188-328: the NCK1 v1 layout (run state,
+ * tensors, "ADAM" section with per-tensor moments, FNV-1a 64 trailer), byte
+ * for byte the reference's for the same state; written to path.tmp.<pid>,
+ * re-read and validated, fsync'd and renamed over path (then the directory
+ * is fsync'd).  Refuses accum_pending != 0.  0 on success, else -1 with a
+ * reason in err and path untouched. */
+int ckpt_save_atomic(const WeightStore *ws, AdamW *opt, const CkptRunState *rs,
+                     const char *path, char *err, size_t errcap);
+/* replaces ckpt_load_training, ckpt.c:330-543: checksum first, then every
+ * identity check against ex (dataset, config hash, tokenizer, schedule,
+ * tensor names/shapes, optimizer hyper-parameters and parameter map) before
+ * anything is applied; on success the weights, moments, opt->step and the
+ * scalars of *out_rs are restored.  -1 with err set and nothing modified. */
+int ckpt_load_training(const char *path, WeightStore *ws, AdamW *opt,
+                       const CkptExpect *ex, CkptRunState *out_rs,
+                       char *err, size_t errcap);
+/* replaces ckpt_info, ckpt.c:628-713: summary on stdout; 0 = valid */
+int ckpt_info(const char *path);
+/* replaces ckpt_load_weights_only, ckpt.c:549-626: the tensor section into a
+ * fresh store (device tensors) */
+int ckpt_load_weights_only(const char *path, WeightStore *ws, char *err, size_t errcap);
+
 #ifdef __cplusplus
 }
 #endif

@@ -49,4 +49,13 @@ void *ncm_workspace(int slot, size_t bytes);
 
 static inline int is_aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
+/* File helpers shared by the NCM1 / NCK1 code (formats.c): exact reads
+ * (0 on success), little-endian integers, and a device buffer streamed to
+ * sink() through a bounded host staging buffer that is wiped afterwards. */
+#include <stdio.h>
+int fmt_read_exact(FILE *f, void *dst, size_t n);
+int fmt_read_u32le(FILE *f, uint32_t *v);
+int fmt_read_u64le(FILE *f, uint64_t *v);
+int fmt_download(const float *dev, uint64_t nbytes, void (*sink)(void *, const void *, size_t), void *ctx);
+
 #endif

@@ -10,6 +10,7 @@
 #include <limits.h>
 #include <math.h>
 #include <stdio.h>
+#include <stdlib.h>
 
 #define NORM_ROWS 128
 
@@ -187,6 +188,89 @@ double sched_cosine_warmup(long step, double warmup, double total) {
     double x = (step - w) / (T - w);
     return 0.5 * (1 + cos(3.141592653589793 * x));
 }
+
+/* ---------------------------------------------------------------- AdamW object
+ * train.c:15-159 of the reference with the moments and gradient accumulators
+ * on the device (so adamw_step launches adamw_update per tensor and nothing
+ * crosses PCIe).  Every buffer of one tensor is allocated before the next. */
+void adamw_free(AdamW *o) {
+    if (!o) return;
+    for (int i = 0; i < o->n; i++) {
+        ncm_hip_free(o->m[i]);
+        ncm_hip_free(o->v[i]);
+        ncm_hip_free(o->g[i]);
+    }
+    free(o->params);
+    free(o->m);
+    free(o->v);
+    free(o->g);
+    free(o->sizes);
+    free(o->lr);
+    free(o);
+}
+
+AdamW *adamw_new(WeightStore *ws, const int *frozen) {
+    if (!ws || ws->count < 0) return ncm_fail(NCM_E_ARG, "adamw_new: bad store"), NULL;
+    if (ncm_ready()) return NULL;
+    AdamW *o = (AdamW *)calloc(1, sizeof *o);
+    size_t cap = (size_t)ws->count + 1;
+    if (o) {
+        o->params = (float **)calloc(cap, sizeof(float *));
+        o->m = (float **)calloc(cap, sizeof(float *));
+        o->v = (float **)calloc(cap, sizeof(float *));
+        o->g = (float **)calloc(cap, sizeof(float *));
+        o->sizes = (int64_t *)calloc(cap, sizeof(int64_t));
+        o->lr = (double *)calloc(cap, sizeof(double));
+    }
+    if (!o || !o->params || !o->m || !o->v || !o->g || !o->sizes || !o->lr) {
+        adamw_free(o);
+        return ncm_fail(NCM_E_OOM, "adamw_new: out of memory"), NULL;
+    }
+    o->b1 = 0.9;
+    o->b2 = 0.95;
+    o->eps = 1e-8;
+    o->wd = 0.01;
+    for (int i = 0; i < ws->count; i++) {
+        if (frozen && frozen[i]) continue;
+        const Tensor *t = ws->items[i].t;
+        size_t bytes = (size_t)t->n * sizeof(float);
+        int k = o->n;
+        o->params[k] = t->data;
+        o->sizes[k] = t->n;
+        o->lr[k] = 1.0;
+        o->m[k] = (float *)ncm_hip_malloc(bytes);
+        o->v[k] = (float *)ncm_hip_malloc(bytes);
+        o->g[k] = (float *)ncm_hip_malloc(bytes);
+        o->n++; /* counted before the check, so adamw_free releases a partial tensor */
+        if (!o->m[k] || !o->v[k] || !o->g[k]) {
+            adamw_free(o);
+            return NULL;
+        }
+        if (ncm_zero_async(o->m[k], bytes) || ncm_zero_async(o->v[k], bytes) || ncm_zero_async(o->g[k], bytes)) {
+            adamw_free(o);
+            return NULL;
+        }
+    }
+    return o;
+}
+
+void adamw_zero_grad(AdamW *o) {
+    if (!o || ncm_ready()) return;
+    for (int i = 0; i < o->n; i++)
+        if (ncm_zero_async(o->g[i], (size_t)o->sizes[i] * sizeof(float))) return;
+}
+
+void adamw_step(AdamW *o, double base_lr, double warmup, double total) {
+    if (!o) return;
+    o->step++;
+    const double lr_t = base_lr * sched_cosine_warmup(o->step, warmup, total);
+    const double b1t = 1.0 - pow(o->b1, (double)o->step), b2t = 1.0 - pow(o->b2, (double)o->step);
+    for (int i = 0; i < o->n; i++)
+        adamw_update(o->params[i], o->g[i], o->m[i], o->v[i], o->sizes[i], lr_t * o->lr[i], o->b1, o->b2, b1t, b2t,
+                     o->eps, o->wd);
+}
+
+void adamw_sync_to_host(AdamW *o) { (void)o; }
 
 #define CLIP_MAX_BLOCKS 1024
 

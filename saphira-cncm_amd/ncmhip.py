@@ -140,6 +140,33 @@ _SIGS = {
     "argmax_rows": (None, [vp, vp, i64, ci]),
 }
 
+# On-disk formats, the AdamW object and NCK1 checkpoints: the reference's
+# prototypes (ncm.h:57-70, 139, 262-265, 416-466, 537-540), so the same table
+# binds the reference library in the parity tests.
+c_dbl = ctypes.c_double
+cp = ctypes.c_char_p
+FORMAT_SIGS = {
+    "weights_load": (ci, [vp, cp]),
+    "weights_free": (None, [vp]),
+    "weights_get": (vp, [vp, cp]),
+    "weights_save": (ci, [vp, cp]),
+    "config_load": (ci, [vp, cp]),
+    "train_data_load": (vp, [cp, ci]),
+    "train_data_free": (None, [vp]),
+    "adamw_new": (vp, [vp, vp]),
+    "adamw_zero_grad": (None, [vp]),
+    "adamw_step": (None, [vp, c_dbl, c_dbl, c_dbl]),
+    "adamw_free": (None, [vp]),
+    "adamw_sync_to_host": (None, [vp]),
+    "ckpt_probe": (ci, [cp]),
+    "ckpt_file_hash": (ctypes.c_uint64, [cp, ctypes.POINTER(ctypes.c_uint64)]),
+    "ckpt_save_atomic": (ci, [vp, vp, vp, cp, cp, sz]),
+    "ckpt_load_training": (ci, [cp, vp, vp, vp, vp, cp, sz]),
+    "ckpt_info": (ci, [cp]),
+    "ckpt_load_weights_only": (ci, [cp, vp, cp, sz]),
+}
+_SIGS.update(FORMAT_SIGS)
+
 
 class NcmError(RuntimeError):
     pass
@@ -344,6 +371,88 @@ class Event:
         if rc:
             raise NcmError(f"hipEventElapsedTime: {rc}")
         return ms.value
+
+
+class TensorS(ctypes.Structure):
+    """Tensor of include/ncm_hip.h (the reference layout, ncm.h:29-34)."""
+    _fields_ = [("data", vp), ("shape", i64 * 4), ("ndim", ci), ("n", i64)]
+
+
+class NamedTensor(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 256), ("t", ctypes.POINTER(TensorS))]
+
+
+class WeightStore(ctypes.Structure):
+    _fields_ = [("items", ctypes.POINTER(NamedTensor)), ("count", ci)]
+
+    def names(self):
+        return [self.items[i].name.decode() for i in range(self.count)]
+
+
+class TrainData(ctypes.Structure):
+    _fields_ = [("rows", ctypes.POINTER(ci)), ("n_rows", ci), ("row_len", ci)]
+
+
+class AdamW(ctypes.Structure):
+    """AdamW of include/ncm_hip.h (params/m/v/g are device pointers here)."""
+    _fields_ = [("params", ctypes.POINTER(vp)), ("m", ctypes.POINTER(vp)), ("v", ctypes.POINTER(vp)),
+                ("g", ctypes.POINTER(vp)), ("sizes", ctypes.POINTER(i64)), ("lr", ctypes.POINTER(c_dbl)),
+                ("n", ci), ("b1", c_dbl), ("b2", c_dbl), ("eps", c_dbl), ("wd", c_dbl), ("step", ctypes.c_long)]
+
+
+class CkptRunState(ctypes.Structure):
+    _fields_ = [("global_step", ctypes.c_long), ("batch_rng", ctypes.c_ulonglong), ("base_lr", c_dbl),
+                ("warmup", c_dbl), ("total", c_dbl), ("batch_B", ci), ("accum_pending", ci),
+                ("n_rows", ctypes.c_long), ("row_len", ci), ("data_hash", ctypes.c_uint64), ("data_path", cp),
+                ("conf_hash", ctypes.c_uint64), ("tokenizer_id", cp), ("noise_sd", c_dbl),
+                ("train_cfg_json", cp)]
+
+
+class CkptExpect(ctypes.Structure):
+    _fields_ = [("batch_B", ci), ("n_rows", ctypes.c_long), ("row_len", ci), ("data_hash", ctypes.c_uint64),
+                ("conf_hash", ctypes.c_uint64), ("tokenizer_id", cp), ("base_lr", c_dbl), ("warmup", c_dbl),
+                ("total", c_dbl), ("b1", c_dbl), ("b2", c_dbl), ("eps", c_dbl), ("wd", c_dbl)]
+
+
+class NCMConfig(ctypes.Structure):
+    """NCMConfig of include/ncm_hip.h (the reference layout, ncm.h:75-137)."""
+    _fields_ = ([("task", ctypes.c_char * 64)]
+                + [(f, ci) for f in ("n_layer", "n_head", "n_embd", "context_length", "prefix_len", "bias",
+                                     "raw_token_prefix", "contextual_prefix", "prefix_pad_token_id")]
+                + [("vocab_size", ci * 64), ("n_levels_out", ci)]
+                + [(f, ci) for f in ("predict_level0", "query_level0", "l0_autoregressive",
+                                     "attn_pattern_block_diag", "use_positional_encoding", "use_level_encoding",
+                                     "use_rope", "rope_base", "use_qk_norm", "use_flex_attention")]
+                + [("rope_theta", c_dbl)]
+                + [(f, ci) for f in ("n_kv_heads", "ctx_enabled", "ctx_n_layer", "ctx_vocab", "puc_enabled",
+                                     "puc_kernel", "shared_output_head", "shared_head_per_level_bias",
+                                     "untied_head_bias", "tie_heads_to_codebook", "tie_heads_learn_scale",
+                                     "tie_heads_trainable", "tie_heads_bias", "use_swiglu", "use_geglu", "use_relu2",
+                                     "parallel_block", "normformer", "use_layerscale", "use_rezero")]
+                + [("layerscale_init", ctypes.c_float), ("dropout", ctypes.c_float)]
+                + [(f, ci) for f in ("vq_embed_dim", "vq_in_vocab", "vq_context_length", "vq_n_layers",
+                                     "vq_compression", "vq_soft_levels")]
+                + [("vq_soft_tau", c_dbl), ("levels", ci * 64), ("n_qlevels", ci), ("vq_vocab", ci * 64),
+                   ("quant_resi_ratio", ctypes.c_float)]
+                + [(f, ci) for f in ("quant_resi_enabled", "quant_resi_share_mode", "learned_l1_sampling",
+                                     "learned_l1_cascade", "learned_l1_cascade_base", "learned_l1_norm",
+                                     "learned_l1_norm_final", "learned_all_sampling", "pre_quant_groupnorm",
+                                     "vq_qk_norm", "enc_layers", "enc_attn_window", "enc_conv_layers",
+                                     "enc_conv_kernel", "enc_positional", "dec_layers", "dec_positional")]
+                + [("pre_tok", ctypes.c_char * 16), ("sudoku_size", ci), ("hf_model_id", ctypes.c_char * 128),
+                   ("eos_token_id", ci), ("pad_token_id", ci), ("gen_temperature", ctypes.c_float),
+                   ("gen_top_k", ci), ("gen_top_p", ctypes.c_float), ("gen_cfg_scale", ctypes.c_float),
+                   ("gen_freq", ctypes.c_float), ("gen_mu", ctypes.c_float), ("gen_adj_a", ctypes.c_float),
+                   ("gen_adj_w", ci), ("gen_adj_d", ctypes.c_float)])
+
+
+def bind(lib, sigs):
+    """Sets restype/argtypes of `sigs` on a ctypes library; returns it."""
+    for name, (res, args) in sigs.items():
+        f = getattr(lib, name)
+        f.restype = res
+        f.argtypes = args
+    return lib
 
 
 class Gpt2Config(ctypes.Structure):

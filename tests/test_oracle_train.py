@@ -152,6 +152,53 @@ def test_adamw_step_one_closed_form():
     assert np.allclose(p2, p.astype(np.float64) * (1 - lr * wd), rtol=1.2e-7, atol=0) and not m2.any() and not v2.any()
 
 
+@needs_ref
+def test_adamw_and_schedule_vs_reference_step():
+    """orc_adamw with the learning rate of orc_sched_cosine_warmup against the
+    reference's own adamw_new + adamw_step (train.c:18-145, its host loop and
+    static schedule), three steps through warm-up, per-tensor lr multipliers."""
+    import ctypes
+    import ncmhip
+    mem = {k: ncmhip._SIGS[k] for k in ("tensor_alloc", "tensor_free", "mem_h2d", "mem_d2h")}
+    R = ncmhip.bind(O.ref(), {**ncmhip.FORMAT_SIGS, **mem})
+    shapes = [(13, 7), (29,), (4, 3, 5)]
+    ps = [rnd(40 + i, *sh) for i, sh in enumerate(shapes)]
+    items = (ncmhip.NamedTensor * len(ps))()
+    for i, p in enumerate(ps):
+        t = R.tensor_alloc(p.ndim, (ctypes.c_int64 * 4)(*p.shape, *([0] * (4 - p.ndim))))
+        items[i].name = f"t{i}".encode()
+        items[i].t = ctypes.cast(t, ctypes.POINTER(ncmhip.TensorS))
+        R.mem_h2d(items[i].t.contents.data, p.ctypes.data, p.nbytes)
+    ws = ncmhip.WeightStore(items, len(ps))
+    op = ctypes.cast(R.adamw_new(ctypes.byref(ws), None), ctypes.POINTER(ncmhip.AdamW))
+    o = op.contents
+    o.wd = 0.1
+    lrm = [1.0, 0.5, 3.0]
+    for i, m in enumerate(lrm):
+        o.lr[i] = m
+    mine = [(p.copy(), np.zeros_like(p), np.zeros_like(p)) for p in ps]
+    base_lr, warmup, total = 3e-4, 2.0, 10.0
+    for step in range(1, 4):
+        gs = [rnd(50 + 10 * step + i, *sh) for i, sh in enumerate(shapes)]
+        for i, g in enumerate(gs):
+            ctypes.memmove(o.g[i], g.ctypes.data, g.nbytes)
+        R.adamw_step(op, base_lr, warmup, total)
+        lr = base_lr * O.sched_cosine_warmup(step, warmup, total)
+        b1t, b2t = 1.0 - 0.9 ** step, 1.0 - 0.95 ** step
+        mine = [O.adamw(p, g, m, v, lr * lrm[i], 0.9, 0.95, b1t, b2t, 1e-8, 0.1)
+                for i, ((p, m, v), g) in enumerate(zip(mine, gs))]
+    assert o.step == 3
+    for i, (p, m, v) in enumerate(mine):
+        got = [np.empty_like(p) for _ in range(3)]
+        R.mem_d2h(got[0].ctypes.data, items[i].t.contents.data, p.nbytes)
+        ctypes.memmove(got[1].ctypes.data, o.m[i], p.nbytes)
+        ctypes.memmove(got[2].ctypes.data, o.v[i], p.nbytes)
+        assert bits_equal(got[0], p) and bits_equal(got[1], m) and bits_equal(got[2], v)
+    R.adamw_free(op)
+    for i in range(len(ps)):
+        R.tensor_free(ctypes.cast(items[i].t, ctypes.c_void_p))
+
+
 def test_schedule_closed_forms():
     assert O.sched_cosine_warmup(50, 100, 1000) == 0.5
     assert O.sched_cosine_warmup(100, 100, 1000) == 1.0

@@ -34,8 +34,9 @@
 //
 // Scheduling: tiles [0, dp_tiles) run whole, one workgroup each; every other
 // tile is cut into `segs` k-segments that fill the last round of the chip.
-// Segments store partial tiles; gemm_64x64_fixup_* (a second launch) sums them in
-// segment order -- deterministic -- and applies the epilogue.
+// Segments store partial tiles; gemm_64x64_fixup_* (a second launch, one
+// workgroup per MFMA block of a split tile) sums them in segment order --
+// deterministic -- and applies the epilogue.
 //
 // Accuracy: MFMAs accumulate 128 k into `acc`, which is then added into `tot`;
 // a single fp32 chain over K terms has an error growing like K u, the two
@@ -612,28 +613,50 @@ __device__ __forceinline__ void gemm_tile_body(const GemmArgs &p) {
     g_epilogue<BM, BN, EPI>(p, tot, i0, j0, tid);
 }
 
-// Sum of the segment partials of split tile blockIdx.x in segment order, then
-// the epilogue.
-template <int BM, int BN, int EPI, bool IA = false, bool IB = false>
+// The epilogue of one MFMA block (a, b) of a 64x64 tile: v holds output rows
+// 4*lg + r of the block, column li (g_epilogue_act's coordinates).
+template <int EPI, int ACT, bool IA, bool IB>
+__device__ __forceinline__ void g_epilogue_blk_act(const GemmArgs &p, const f4 &v, int a, int b, int i0, int j0,
+                                                   int tid) {
+    const int lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
+    const int li = lane & 15, lg = lane >> 4;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int row = IA ? wm * 32 + 2 * (4 * lg + r) + a : wm * 32 + a * 16 + 4 * lg + r;
+        const int col = IB ? wn * 32 + 2 * li + b : wn * 32 + b * 16 + li;
+        g_out<ACT, EPI>(p, i0 + row, j0 + col, v[r]);
+    }
+}
+
+// Sum of the segment partials of one MFMA block of a split 64x64 tile
+// (blockIdx.x = 4 * tail + block), in segment order, then the block's
+// epilogue.  A partial tile is stored as [block][thread][4] (the split
+// kernels' write-back), so each thread reads one float4 per segment, and all
+// of a thread's segment loads are issued before the first add: the launch
+// is one round trip of latency, not one per segment.
+#define FIXUP_MAX_SEGS 16
+template <int EPI, bool IA, bool IB>
 __device__ __forceinline__ void gemm_tile_fixup_body(const GemmArgs &p) {
-    constexpr int TM = BM / 32, TN = BN / 32;
-    const int tid = threadIdx.x, tail = blockIdx.x;
+    const int tid = threadIdx.x, tail = blockIdx.x >> 2, blk = blockIdx.x & 3;
     int tm, tn;
     tile_rc<8>(p.dp_tiles + tail, p.tiles_m, p.tiles_n, tm, tn);
-    const float *first = p.ws + (int64_t)tail * p.segs * (BM * BN);
-    f4 tot[TM][TN];
+    const float *first = p.ws + (int64_t)tail * p.segs * 4096 + (blk * GEMM_NT + tid) * 4;
+    f4 part[FIXUP_MAX_SEGS];
 #pragma unroll
-    for (int a = 0; a < TM; ++a)
+    for (int s = 0; s < FIXUP_MAX_SEGS; ++s)
+        if (s < p.segs) part[s] = *(const f4 *)(first + (int64_t)s * 4096);
+    f4 tot = part[0];
 #pragma unroll
-        for (int b = 0; b < TN; ++b) tot[a][b] = *(const f4 *)(first + ((a * TN + b) * GEMM_NT + tid) * 4);
-    for (int s = 1; s < p.segs; ++s) {
-        const float *part = first + (int64_t)s * (BM * BN);
-#pragma unroll
-        for (int a = 0; a < TM; ++a)
-#pragma unroll
-            for (int b = 0; b < TN; ++b) tot[a][b] += *(const f4 *)(part + ((a * TN + b) * GEMM_NT + tid) * 4);
+    for (int s = 1; s < FIXUP_MAX_SEGS; ++s)
+        if (s < p.segs) tot += part[s];
+    const int a = blk >> 1, b = blk & 1, i0 = tm * 64, j0 = tn * 64;
+    if (EPI == EPI_ACCUM) { g_epilogue_blk_act<EPI, ACT_NONE, IA, IB>(p, tot, a, b, i0, j0, tid); return; }
+    switch (p.act) {
+    case ACT_SILU: g_epilogue_blk_act<EPI, ACT_SILU, IA, IB>(p, tot, a, b, i0, j0, tid); break;
+    case ACT_GELU: g_epilogue_blk_act<EPI, ACT_GELU, IA, IB>(p, tot, a, b, i0, j0, tid); break;
+    case ACT_GELU_TANH: g_epilogue_blk_act<EPI, ACT_GELU_TANH, IA, IB>(p, tot, a, b, i0, j0, tid); break;
+    default: g_epilogue_blk_act<EPI, ACT_NONE, IA, IB>(p, tot, a, b, i0, j0, tid); break;
     }
-    g_epilogue<BM, BN, EPI, IA, IB>(p, tot, tm * BM, tn * BN, tid);
 }
 
 // ---------------------------------------------------------------- GEMM, direct-to-LDS loads
@@ -757,7 +780,7 @@ __device__ __forceinline__ void gemm_dma_body(const GemmArgs &p) {
         gemm_dma_body<AKC, BKC, EPI>(p);                                                               \
     }
 #define GEMM_TILE_FIXUP(name, EPI, IA, IB) \
-    extern "C" __global__ void __launch_bounds__(GEMM_NT) name(GemmArgs p) { gemm_tile_fixup_body<64, 64, EPI, IA, IB>(p); }
+    extern "C" __global__ void __launch_bounds__(GEMM_NT) name(GemmArgs p) { gemm_tile_fixup_body<EPI, IA, IB>(p); }
 GEMM_DMA_KERNEL(gemm_64x64_fwd_v, true, true, EPI_STORE)
 GEMM_DMA_KERNEL(gemm_64x64_dx_v, true, false, EPI_ACCUM)
 GEMM_DMA_KERNEL(gemm_64x64_dw_v, false, false, EPI_ACCUM)

@@ -58,40 +58,90 @@ static void gemm_name(int bm, int bn, int kind, int vec, char *out, size_t cap) 
     snprintf(out, cap, "gemm_%dx%d_%s_%c", bm, bn, kind_names[kind], vec ? 'v' : 's');
 }
 
-/* Work split of one GEMM over the chip: whole rounds of tiles, then the
- * remaining tiles cut into k-segments (whole groups of 4 slabs) that fill
- * one more round. */
+/* Work split of one GEMM over the chip.  Tiles [0, dp) run whole, one
+ * workgroup each; every other tile is cut into `segs` k-segments (whole
+ * groups of 4 slabs) whose partial tiles a fixup launch sums. */
 typedef struct {
     int tiles_m, tiles_n, iters, dp_tiles, segs, blocks;
 } GemmPlan;
 
-static GemmPlan plan_gemm(int Mo, int No, int Kred, int slots, int bm, int bn) {
+/* CU makespan, in slabs, of list-scheduling dp units of I slabs and then n2
+ * units of u slabs over C CUs in dispatch order, each unit to the CU with
+ * the least work so far.  A CU retires slabs at the same rate however many
+ * of its workgroups share it (the MFMA pipes are the bound), so CU load --
+ * not workgroup slots -- is what has to balance.  The loads form at most two
+ * levels at any time, so whole rounds are added at once. */
+static double makespan(int C, int dp, int I, int64_t n2, int u) {
+    int64_t ca = C - dp % C, cb = dp % C;   /* group a: ca CUs at level la; group b: cb at lb */
+    double la = (double)(dp / C) * I, lb = la + I;
+    while (n2 > 0) {
+        if (cb > 0 && la > lb) {
+            int64_t tc = ca; ca = cb; cb = tc;
+            double tl = la; la = lb; lb = tl;
+        }
+        if (cb > 0 && la == lb) { ca += cb; cb = 0; }
+        if (n2 < ca) { la += u; break; }   /* n2 of group a's CUs reach la + u */
+        la += u;
+        n2 -= ca;
+    }
+    return cb > 0 && lb > la ? lb : la;
+}
+
+/* Cost model of a split, fitted to per-call timings of the linear sweep's
+ * GEMMs on MI355X under every forced split count (one slab of a 64x64 tile
+ * ~ 0.52 us of a CU): the fixup launch adds ~6 us, and the partial tiles
+ * ~0.05 us per MB. */
+#define SPLIT_FIXED_SLABS 11.5
+#define SPLIT_SLABS_PER_MB 0.1
+
+static GemmPlan plan_gemm_uncached(int Mo, int No, int Kred, int slots, int bm, int bn) {
     GemmPlan g;
     g.tiles_m = (Mo + bm - 1) / bm;
     g.tiles_n = (No + bn - 1) / bn;
-    int groups = Kred > 0 ? (Kred + 4 * BK - 1) / (4 * BK) : 1;
+    const int groups = Kred > 0 ? (Kred + 4 * BK - 1) / (4 * BK) : 1;
     g.iters = 4 * groups;
-    int T = g.tiles_m * g.tiles_n;
-    if (slots < 1) slots = 1;
-    g.dp_tiles = (T / slots) * slots;
-    int R = T - g.dp_tiles;
-    /* Split the R remaining tiles into s k-segments: the tail then takes
-     * ceil(R*s/slots) rounds of ceil(groups/s) slab groups, plus about half a
-     * group per segment for the partial write-back and the fixup. */
-    int segs = 1;
-    if (R > 0) {
-        double best = 1e30;
-        for (int s = 1; s <= MAX_SEGS && s <= groups; s++) {
-            double t = (double)((R * s + slots - 1) / slots) * ((groups + s - 1) / s) + (s > 1 ? 0.5 * s : 0.0);
+    const int T = g.tiles_m * g.tiles_n, C = ncm_cu_count();
+    if (slots < C) slots = C;
+    /* unsplit: every tile whole */
+    double best = makespan(C, T, g.iters, 0, 0);
+    g.dp_tiles = T;
+    g.segs = 1;
+    /* whole rounds of workgroup slots, whole rounds of CUs, or nothing runs
+     * whole; the rest split into s segments */
+    const int dps[3] = {(T / slots) * slots, (T / C) * C, 0};
+    for (int d = 0; d < 3; d++) {
+        const int dp = dps[d], R = T - dp;
+        if (R <= 0 || (d > 0 && dp == dps[d - 1])) continue;
+        for (int s = 2; s <= MAX_SEGS && s <= groups; s++) {
+            const int u = 4 * ((groups + s - 1) / s);
+            double t = makespan(C, dp, g.iters, (int64_t)R * s, u) + SPLIT_FIXED_SLABS +
+                       SPLIT_SLABS_PER_MB * (double)R * s * bm * bn * 4 / 1e6;
             if (t < best - 1e-9) {
                 best = t;
-                segs = s;
+                g.dp_tiles = dp;
+                g.segs = s;
             }
         }
     }
-    if (segs == 1) g.dp_tiles = T; /* nothing to split: everything runs whole */
-    g.segs = segs;
-    g.blocks = g.dp_tiles + (T - g.dp_tiles) * segs;
+    g.blocks = g.dp_tiles + (T - g.dp_tiles) * g.segs;
+    return g;
+}
+
+/* Plans are cached per shape (the library is driven from one host thread). */
+static GemmPlan plan_gemm(int Mo, int No, int Kred, int slots, int bm, int bn) {
+    static struct { int Mo, No, Kred, slots; GemmPlan g; } cache[64];
+    static int used = 0, next = 0;
+    for (int i = 0; i < used; i++)
+        if (cache[i].Mo == Mo && cache[i].No == No && cache[i].Kred == Kred && cache[i].slots == slots)
+            return cache[i].g;
+    GemmPlan g = plan_gemm_uncached(Mo, No, Kred, slots, bm, bn);
+    cache[next].Mo = Mo;
+    cache[next].No = No;
+    cache[next].Kred = Kred;
+    cache[next].slots = slots;
+    cache[next].g = g;
+    next = (next + 1) % 64;
+    if (used < 64) used++;
     return g;
 }
 
@@ -149,7 +199,7 @@ static int run_gemm(int kind, const float *A, const float *B, float *C, const fl
     int rc = ncm_launch(ncm_kernel(name), (unsigned)g.blocks, 1, 1, 256, args);
     if (rc || g.segs == 1) return rc;
     snprintf(fix, sizeof fix, "gemm_%dx%d_fixup_%s_%c", bm, bn, kind_names[kind], vec ? 'v' : 's');
-    return ncm_launch_named(fix, (unsigned)split_tiles, 1, 1, 256, args);
+    return ncm_launch_named(fix, (unsigned)split_tiles * 4u, 1, 1, 256, args);  /* one workgroup per MFMA block */
 }
 
 /* GEMV kernel for a chunk of nb <= 8 batch rows; returns rows per workgroup. */

@@ -417,6 +417,34 @@ int argmax_row(const float *x, int n);
 void argmax_rows(const float *x, int *idx, int64_t rows, int n);
 
 /* ------------------------------------------------------------------ */
+/* sampling                                                            */
+/* ------------------------------------------------------------------ */
+
+/* replaces rng_next, ncm.h:199, kernels.c:774-780 (xorshift64*). */
+unsigned long long rng_next(unsigned long long *state);
+
+/* replaces sample_topkp, ncm.h:197-198, kernels.c:782-825: temperature,
+ * top-k (0 = all) and nucleus sampling of one row.  HOST logits and rng, as
+ * the reference's callers pass them (qwen.c:220-223, gpt2.c:194); the row is
+ * copied to the device and sampled there (sample_topkp_dev).  temp <= 0
+ * returns argmax_row and leaves *rng as it is.  V <= 262144, top_p >= 0. */
+int sample_topkp(const float *logits, int V, float temp, int top_k, float top_p, unsigned long long *rng);
+/* flag of the last sample_topkp call (see sample_topkp_dev) */
+int ncm_hip_sample_flag(void);
+
+/* extension: sample_topkp on the device.  logits [V], rng (the xorshift64*
+ * state, advanced once when temp > 0), out (the id) and flag are device
+ * pointers; flag may be NULL.  *flag = 0: the id is certified to be the
+ * reference's (every decision cleared the combined rounding bound of the
+ * device and host exp and of the summation orders); 1: the draw lay within
+ * that bound of a cumulative boundary (probability ~1e-10 per draw; the id
+ * is then the device's own reading); 2: a non-finite logits/temp value.
+ * Asynchronous on the library stream.  Replaces backend_to_host +
+ * sample_topkp (qwen.c:220-223). */
+void sample_topkp_dev(const float *logits, int V, float temp, int top_k, float top_p,
+                      unsigned long long *rng, int *out, int *flag);
+
+/* ------------------------------------------------------------------ */
 /* on-disk formats -- replaces the loaders of src/tensor.c (ncm.h:57-70, */
 /* 72-139, 262-265) and weights_save (train.c:741-767)                  */
 /* ------------------------------------------------------------------ */

@@ -192,6 +192,70 @@ uint64_t orc_rng_next(uint64_t *state) {
     return x * 0x2545F4914F6CDD1DULL;
 }
 
+/* kernels.c:782-825 sample_topkp.  The reference sorts the indices with
+ * glibc's qsort under a (value desc) comparator; glibc 2.35 sorts with a
+ * stable merge sort, so equal values keep ascending index order.  Here the
+ * order is the total order (value desc, index asc), which any sort yields
+ * identically -- the same permutation for finite inputs (NaN, on which the
+ * reference's comparator is inconsistent, is outside this restatement). */
+typedef struct { float v; int i; } OrcVI;
+
+static int orc_vi_desc(const void *a, const void *b) {
+    const OrcVI *x = (const OrcVI *)a, *y = (const OrcVI *)b;
+    if (x->v != y->v) return x->v > y->v ? -1 : 1;
+    return (x->i > y->i) - (x->i < y->i);
+}
+
+int orc_sample_topkp(const float *logits, int V, float temp, int top_k, float top_p, uint64_t *rng) {
+    if (!(temp > 0)) return orc_argmax_row(logits, V);
+    OrcVI *s = (OrcVI *)malloc((size_t)V * sizeof *s);
+    double *q = (double *)malloc((size_t)V * sizeof *q);
+    for (int i = 0; i < V; i++) {
+        s[i].v = logits[i] / temp;
+        s[i].i = i;
+    }
+    qsort(s, (size_t)V, sizeof *s, orc_vi_desc);
+    const int keep = top_k > 0 && top_k < V ? top_k : V;
+    /* unnormalised probabilities relative to the maximum, fp64 serial sum */
+    const double mx = s[0].v;
+    double den = 0.0;
+    for (int r = 0; r < keep; r++) {
+        q[r] = exp((double)s[r].v - mx);
+        den += q[r];
+    }
+    for (int r = 0; r < keep; r++) q[r] /= den;
+    /* nucleus: the first rank whose preceding mass minus its own exceeds top_p */
+    int nkeep = keep;
+    double before = 0.0;
+    for (int r = 0; r < keep; r++) {
+        if (before - q[r] > top_p) {
+            nkeep = r;
+            break;
+        }
+        before += q[r];
+    }
+    if (nkeep == 0) { /* top_p < -q[0]: the reference then reads ord[-1] */
+        free(s);
+        free(q);
+        return -1;
+    }
+    double mass = 0.0;
+    for (int r = 0; r < nkeep; r++) mass += q[r];
+    const double u = (double)(orc_rng_next(rng) >> 11) * (1.0 / 9007199254740992.0) * mass;
+    int pick = s[nkeep - 1].i;
+    double run = 0.0;
+    for (int r = 0; r < nkeep; r++) {
+        run += q[r];
+        if (u <= run) {
+            pick = s[r].i;
+            break;
+        }
+    }
+    free(s);
+    free(q);
+    return pick;
+}
+
 /* tests/ktest_kernels.c:8-12: xorshift (13, 7, 17) mapped to [-2, 2) */
 void orc_fill_ktest(uint64_t *state, float *out, int64_t n) {
     for (int64_t i = 0; i < n; i++) {

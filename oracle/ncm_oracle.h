@@ -100,6 +100,10 @@ void orc_rope_tables_ncp(int S, int hd, int base, float *cos_t, float *sin_t);
 uint64_t orc_rng_next(uint64_t *state);
 void orc_fill_ktest(uint64_t *state, float *out, int64_t n);
 
+/* src/kernels.c:782-825 sample_topkp (temperature, top-k, nucleus); rng
+ * is the xorshift64* state, advanced once when temp > 0 */
+int orc_sample_topkp(const float *logits, int V, float temp, int top_k, float top_p, uint64_t *rng);
+
 /* threads used by the OpenMP loops (0 = runtime default) */
 void orc_set_threads(int n);
 

@@ -44,6 +44,7 @@ def lib():
             "orc_vq_multiscale": (None, [vp, ctypes.POINTER(vp), ctypes.POINTER(ci), ci, ci, ci, ci,
                                          vp, vp, vp]),
             "orc_argmax_row": (ci, [vp, ci]),
+            "orc_sample_topkp": (ci, [vp, ci, ctypes.c_float, ci, ctypes.c_float, ctypes.POINTER(ctypes.c_uint64)]),
             "orc_gelu": (None, [vp, vp, i64]),
             "orc_gelu_tanh": (None, [vp, vp, i64]),
             "orc_silu": (None, [vp, vp, i64]),
@@ -141,6 +142,22 @@ def vq_multiscale(z, Es, B, L):
     vocs = (ci * n)(*[e.shape[0] for e in Es])
     lib().orc_vq_multiscale(_ptr(z), eptrs, vocs, n, B, L, D, _ptr(idx), _ptr(z_hat), _ptr(z_rest))
     return idx, z_hat, z_rest
+
+
+def sample_topkp(logits, temp, top_k, top_p, rng):
+    """kernels.c:782-825 sample_topkp; returns (id, advanced rng state)."""
+    x = _f32(logits)
+    st = ctypes.c_uint64(rng)
+    i = lib().orc_sample_topkp(_ptr(x), x.size, temp, top_k, top_p, ctypes.byref(st))
+    return i, st.value
+
+
+def ref_sample_topkp(logits, temp, top_k, top_p, rng):
+    """The reference's own sample_topkp (kernels.c, compiled into _ref/libref.so)."""
+    x = _f32(logits)
+    st = ctypes.c_uint64(rng)
+    i = ref().sample_topkp(_ptr(x), x.size, temp, top_k, top_p, ctypes.byref(st))
+    return i, st.value
 
 
 def argmax_row(x):
@@ -412,6 +429,7 @@ def ref():
             "linear_fwd": (None, [vp, vp, vp, vp, i64, ci, ci]),
             "rowwise_l2sq": (None, [vp, vp, vp, i64, i64, ci]),
             "argmax_row": (ci, [vp, ci]),
+            "sample_topkp": (ci, [vp, ci, ctypes.c_float, ci, ctypes.c_float, ctypes.POINTER(ctypes.c_uint64)]),
             "gelu_fwd": (None, [vp, vp, i64]),
             "gelu_tanh_fwd": (None, [vp, vp, i64]),
             "silu_fwd": (None, [vp, vp, i64]),

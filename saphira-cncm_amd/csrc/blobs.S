@@ -17,4 +17,8 @@ ncm_co_ops:
     .globl ncm_co_train
 ncm_co_train:
     .incbin "train.co"
+    .balign 4096
+    .globl ncm_co_sample
+ncm_co_sample:
+    .incbin "sample.co"
     .section .note.GNU-stack,"",@progbits

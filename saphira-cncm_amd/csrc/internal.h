@@ -31,10 +31,14 @@ int ncm_launch_named(const char *name, unsigned gx, unsigned gy, unsigned gz, un
 
 /* Library-owned device workspaces (grown on demand, stream-synchronised
  * before a grow).  Slot ids keep independent users apart. */
-enum { WS_SPLITK = 0, WS_COLSUM = 1, WS_VQ = 2, WS_DXT = 3, WS_TRAIN = 4, WS_COUNT = 5 };
+enum { WS_SPLITK = 0, WS_COLSUM = 1, WS_VQ = 2, WS_DXT = 3, WS_TRAIN = 4, WS_SAMPLE = 5, WS_COUNT = 6 };
 /* Stream-ordered device copy / zero fill on the library stream (no sync). */
 int ncm_copy_async(void *d, const void *s, size_t n);
 int ncm_zero_async(void *d, size_t n);
+/* Device sampler launches (sample.c): id to *out, or to ids[*pos + 1] with
+ * ++*pos when pos is set; temp > 0; launches only (graph-capturable). */
+int ncm_sample_launch(const float *x, int V, float temp, int top_k, float top_p, unsigned long long *rng,
+                      int *out, int *ids, int *pos, int *flag);
 /* Compute units of the selected device. */
 int ncm_cu_count(void);
 void *ncm_workspace(int slot, size_t bytes);

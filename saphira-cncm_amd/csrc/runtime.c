@@ -10,8 +10,8 @@
 #include <string.h>
 
 /* ---- embedded code objects (blobs.S) ---- */
-extern const unsigned char ncm_co_gemm[], ncm_co_vq[], ncm_co_ops[], ncm_co_train[];
-static const unsigned char *const co_blobs[] = {ncm_co_gemm, ncm_co_vq, ncm_co_ops, ncm_co_train};
+extern const unsigned char ncm_co_gemm[], ncm_co_vq[], ncm_co_ops[], ncm_co_train[], ncm_co_sample[];
+static const unsigned char *const co_blobs[] = {ncm_co_gemm, ncm_co_vq, ncm_co_ops, ncm_co_train, ncm_co_sample};
 #define N_MODULES (int)(sizeof(co_blobs) / sizeof(co_blobs[0]))
 
 static int g_state = 0; /* 0 = not initialised, 1 = ready, <0 = failed */
@@ -91,7 +91,7 @@ typedef struct {
     char name[64];
     hipFunction_t f;
 } KEnt;
-static KEnt g_kern[128];
+static KEnt g_kern[256];
 static int g_nkern = 0;
 
 hipFunction_t ncm_kernel(const char *name) {

@@ -138,6 +138,10 @@ _SIGS = {
     "ncm_ncp_forward": (vp, [vp, vp, vp, ci, ci]),
     "argmax_row": (ci, [vp, ci]),
     "argmax_rows": (None, [vp, vp, i64, ci]),
+    "rng_next": (ctypes.c_uint64, [ctypes.POINTER(ctypes.c_uint64)]),
+    "sample_topkp": (ci, [vp, ci, ctypes.c_float, ci, ctypes.c_float, ctypes.POINTER(ctypes.c_uint64)]),
+    "ncm_hip_sample_flag": (ci, []),
+    "sample_topkp_dev": (None, [vp, ci, ctypes.c_float, ci, ctypes.c_float, vp, vp, vp]),
 }
 
 # On-disk formats, the AdamW object and NCK1 checkpoints: the reference's
@@ -329,6 +333,21 @@ def call(name, *args):
 
 def argmax_rows(x, idx, rows, n):
     load().argmax_rows(_p(x), _p(idx), rows, n)
+    check()
+
+
+def sample_topkp(logits, temp, top_k, top_p, rng):
+    """sample_topkp on a HOST row (numpy float32); returns (id, new rng, flag)."""
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    st = ctypes.c_uint64(rng)
+    i = load().sample_topkp(x.ctypes.data, x.size, temp, top_k, top_p, ctypes.byref(st))
+    check()
+    return i, st.value, load().ncm_hip_sample_flag()
+
+
+def sample_topkp_dev(logits, V, temp, top_k, top_p, rng, out, flag=None):
+    """Device sampler: logits, rng (uint64 [1]), out (int32 [1]), flag (int32 [1] or None)."""
+    load().sample_topkp_dev(_p(logits), V, temp, top_k, top_p, _p(rng), _p(out), _p(flag))
     check()
 
 

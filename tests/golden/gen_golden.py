@@ -66,16 +66,57 @@ def vq_case(rng):
     return out
 
 
+def sample_row(seed, V, scale, ties):
+    """A logits row from the reference's ktest generator (tests/ktest_kernels.c:8-12,
+    values in [-2, 2)) times scale; rounded to halves when ties is set."""
+    x, _ = O.ktest_fill(int(seed), int(V))
+    x = (x * np.float32(scale)).astype(np.float32)
+    return (np.round(x * 2) / 2).astype(np.float32) if ties else x
+
+
+def sample_cases():
+    """Rows for sample_topkp (kernels.c:782-825): ties (rounded logits),
+    temperatures, top-k, nucleus settings and the full Qwen vocabulary.  The
+    full-vocabulary rows are stored as their generator seed (sample_row)."""
+    rng = np.random.default_rng(20261202)
+    cfg = [(1.0, 0, 1.0), (0.7, 0, 0.9), (1.3, 40, 1.0), (0.5, 5, 0.5), (1.0, 1, 1.0), (2.0, 0, 0.0),
+           (0.8, 1000, 0.95), (1.0, 0, 1.0)]
+    out = {}
+    for i, (temp, k, p) in enumerate(cfg):
+        if i in (0, 1, 7):
+            gen = np.array([int(rng.integers(1, 2 ** 62)), 151936, rng.uniform(1.0, 4.0), i % 2], np.float64)
+            x = sample_row(*gen)
+            out[f"c{i}_gen"] = gen
+        else:
+            V = int(rng.integers(2, 5000))
+            x = (rng.standard_normal(V) * rng.uniform(0.5, 4.0)).astype(np.float32)
+            if i % 2:
+                x = np.round(x * 2).astype(np.float32) / 2   # many exact ties
+            out[f"c{i}_x"] = x
+        st = int(rng.integers(1, 2 ** 63))
+        ids, sts = [], []
+        s = st
+        for _ in range(4):   # four draws in a row from the same row
+            j, s = O.ref_sample_topkp(x, temp, k, p, s)
+            ids.append(j)
+            sts.append(s)
+        out.update({f"c{i}_cfg": np.array([temp, k, p], np.float64),
+                    f"c{i}_rng": np.array([st] + sts, np.uint64), f"c{i}_ids": np.array(ids, np.int32)})
+    out["n_cases"] = np.array(len(cfg))
+    return out
+
+
 def main():
     if not O.ref_available():
         sys.exit("oracle/_ref/libref.so missing: run make -C oracle where /root/reference exists")
     rng = np.random.default_rng(20261201)
     np.savez_compressed(os.path.join(HERE, "linear_ref.npz"), **linear_cases(rng))
     np.savez_compressed(os.path.join(HERE, "vq_ref.npz"), **vq_case(rng))
+    np.savez_compressed(os.path.join(HERE, "sample_ref.npz"), **sample_cases())
     kt = subprocess.run([O.KTEST_BIN], check=True, capture_output=True, text=True).stdout
     with open(os.path.join(HERE, "ktest_cpu.txt"), "w") as f:
         f.write(kt)
-    print("wrote linear_ref.npz vq_ref.npz ktest_cpu.txt")
+    print("wrote linear_ref.npz vq_ref.npz sample_ref.npz ktest_cpu.txt")
 
 
 if __name__ == "__main__":

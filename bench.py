@@ -158,6 +158,19 @@ def extras(ncmhip):
     ms_gen = timed(ncmhip, lambda: lib.ncm_qwen_generate(m, prompt.ctypes.data, 2048, 256, -1, gen.ctypes.data),
                    2, 1)
     ncmhip.check()
+    # the same 256 steps drawing from sample_topkp (temp 0.8, top-k 0, top-p 0.9) on the device
+    st, nflag = ctypes.c_uint64(0x5EED), ctypes.c_int(0)
+    ms_samp = timed(ncmhip, lambda: lib.ncm_qwen_generate_sample(m, prompt.ctypes.data, 2048, 256, -1, 0.8, 0, 0.9,
+                                                                 ctypes.byref(st), gen.ctypes.data,
+                                                                 ctypes.byref(nflag)), 2, 1)
+    ncmhip.check()
+    # one draw of the sampler alone on a 151936-entry row
+    row = D.from_numpy(rng.standard_normal(qc.vocab).astype(np.float32) * np.float32(3.0))
+    srng, sout, sflag = D.from_numpy(np.array([7], np.uint64)), D.empty(1, np.int32), D.empty(1, np.int32)
+    ms_draw = timed(ncmhip, lambda: lib.sample_topkp_dev(row.ptr, qc.vocab, 0.8, 0, 0.9, srng.ptr, sout.ptr,
+                                                         sflag.ptr), 20, 2)
+    ncmhip.check()
+    del row, srng, sout, sflag
     ms_tok = (ms_gen - ms_pre) / 255
     kv_bytes = 2 * 24 * 2 * 64 * 4 * (2048 + 128)          # mean KV cache read per step
     dec_bytes = 4 * nparam + kv_bytes
@@ -170,7 +183,10 @@ def extras(ncmhip):
                    "decode_tok_per_s": round(1e3 / ms_tok, 1), "decode_ms_per_tok": round(ms_tok, 4),
                    "decode_gbs": round(dec_bytes / (ms_tok / 1e3) / 1e9, 1),
                    "decode_frac_hbm": round(dec_bytes / (ms_tok / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
-                   "generate_ms": round(ms_gen, 2)}
+                   "generate_ms": round(ms_gen, 2),
+                   "sampled_decode_tok_per_s": round(255 / ((ms_samp - ms_pre) / 1e3), 1),
+                   "sampled_flagged_draws": nflag.value,
+                   "sample_draw_us": round(ms_draw * 1e3, 2)}
     del bufs
 
     # -- config 5: GPT-style training step, 12 layers, d 768, 32 x 512 tokens

@@ -379,6 +379,14 @@ float *ncm_qwen_decode(NcmQwen *m, int id, int pos);
  * cached decode, device argmax; stops after eos when eos >= 0. Returns the
  * number of ids written to out (-1 on error). */
 int ncm_qwen_generate(NcmQwen *m, const int *prompt, int np, int n_new, int eos, int *out);
+/* qwen_generate (qwen.c:204-228) with temperature / top-k / nucleus
+ * sampling: each step's id is sample_topkp's draw (kernels.c:782-825) from
+ * the xorshift64* state *rng (HOST; advanced once per generated token),
+ * computed on the device inside the replayed decode graph.  temp <= 0 is
+ * ncm_qwen_generate.  n_flagged (may be NULL): draws whose certification
+ * flag was not 0 (see sample_topkp_dev).  Returns the ids written or -1. */
+int ncm_qwen_generate_sample(NcmQwen *m, const int *prompt, int np, int n_new, int eos, float temp, int top_k,
+                             float top_p, unsigned long long *rng, int *out, int *n_flagged);
 
 /* ------------------------------------------------------------------ */
 /* config-1 driver: the NCP transformer forward of ncp.c               */

@@ -35,10 +35,13 @@ enum { WS_SPLITK = 0, WS_COLSUM = 1, WS_VQ = 2, WS_DXT = 3, WS_TRAIN = 4, WS_SAM
 /* Stream-ordered device copy / zero fill on the library stream (no sync). */
 int ncm_copy_async(void *d, const void *s, size_t n);
 int ncm_zero_async(void *d, size_t n);
-/* Device sampler launches (sample.c): id to *out, or to ids[*pos + 1] with
- * ++*pos when pos is set; temp > 0; launches only (graph-capturable). */
+/* Device sampler launches (sample.c): id to *out (flag to *flag), or to
+ * ids[*pos + 1] (flag[*pos + 1]) with ++*pos when pos is set; temp > 0;
+ * launches only (graph-capturable).  ws: a caller-owned workspace of
+ * ncm_sample_ws_bytes(V) bytes, or NULL for the library's. */
 int ncm_sample_launch(const float *x, int V, float temp, int top_k, float top_p, unsigned long long *rng,
-                      int *out, int *ids, int *pos, int *flag);
+                      int *out, int *ids, int *pos, int *flag, void *ws);
+size_t ncm_sample_ws_bytes(int V);
 /* Compute units of the selected device. */
 int ncm_cu_count(void);
 void *ncm_workspace(int slot, size_t bytes);

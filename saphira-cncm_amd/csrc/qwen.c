@@ -42,6 +42,15 @@ struct NcmQwen {
     int nchunk_max;
     hipGraphExec_t step_graph; /* one decode step + argmax, replayed per token */
     int graph_state;        /* 0 not built, 1 built, -1 capture failed (eager) */
+    /* sampling (temp > 0): the xorshift64* state, per-position certification
+     * flags, a sampler workspace owned by the model (graph-stable), and the
+     * decode + sample graph with the settings it was captured for */
+    unsigned long long *rng_dev;
+    int *flags_dev;
+    void *samp_ws;
+    hipGraphExec_t samp_graph;
+    int samp_state, samp_top_k;
+    float samp_temp, samp_top_p;
 };
 
 int ncm_qwen_param_count(const NcmQwenConfig *c) { return c ? 2 + QW_PER_LAYER * c->n_layer : 0; }
@@ -85,6 +94,10 @@ void ncm_qwen_free(NcmQwen *m) {
     ncm_hip_free(m->amax_v);
     ncm_hip_free(m->amax_i);
     if (m->graph_state == 1) hipGraphExecDestroy(m->step_graph);
+    if (m->samp_state == 1) hipGraphExecDestroy(m->samp_graph);
+    ncm_hip_free(m->rng_dev);
+    ncm_hip_free(m->flags_dev);
+    ncm_hip_free(m->samp_ws);
     free(m->P);
     free(m);
 }
@@ -147,6 +160,8 @@ NcmQwen *ncm_qwen_new(const NcmQwenConfig *c, float *const *params) {
 #undef ALLOC
     if (!(m->ids_dev = (int *)ncm_hip_malloc((size_t)(c->n_ctx + 1) * sizeof(int)))) goto fail;
     if (!(m->pos_dev = (int *)ncm_hip_malloc(sizeof(int)))) goto fail;
+    if (!(m->rng_dev = (unsigned long long *)ncm_hip_malloc(sizeof(unsigned long long)))) goto fail;
+    if (!(m->flags_dev = (int *)ncm_hip_malloc((size_t)(c->n_ctx + 1) * sizeof(int)))) goto fail;
     m->amax_blocks = (c->vocab + 4095) / 4096;
     /* decode LM head: two streaming workgroups per CU when a row fits one
      * float4 prefetch per lane (K <= 1024) */
@@ -445,5 +460,103 @@ int ncm_qwen_generate(NcmQwen *m, const int *prompt, int np, int n_new, int eos,
         }
     }
     mem_d2h(out, m->ids_dev + np, (size_t)made * sizeof(int));
+    return made;
+}
+
+/* Decode step + device sampling, captured once per sampling setting. */
+static int samp_graph(NcmQwen *m, float temp, int top_k, float top_p) {
+    if (m->samp_state == 1 && (m->samp_temp != temp || m->samp_top_k != top_k || m->samp_top_p != top_p)) {
+        hipGraphExecDestroy(m->samp_graph);
+        m->samp_state = 0;
+    }
+    if (m->samp_state != 0 || getenv("NCM_NO_GRAPH")) return m->samp_state == 1;
+    hipStream_t s = ncm_stream();
+    hipGraph_t g = NULL;
+    if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) return 0;
+    int rc = decode_core(m) || ncm_sample_launch(m->logits, m->c.vocab, temp, top_k, top_p, m->rng_dev, NULL,
+                                                 m->ids_dev, m->pos_dev, m->flags_dev, m->samp_ws);
+    hipError_t e = hipStreamEndCapture(s, &g);
+    if (rc || e != hipSuccess || !g) {
+        if (g) hipGraphDestroy(g);
+        m->samp_state = -1;
+        ncm_fail(NCM_E_HIP, "qwen: sampling graph capture failed");
+        return 0;
+    }
+    e = hipGraphInstantiate(&m->samp_graph, g, NULL, NULL, 0);
+    hipGraphDestroy(g);
+    if (e != hipSuccess) {
+        m->samp_state = -1;
+        return ncm_fail(NCM_E_HIP, "qwen: graph instantiate: %s", hipGetErrorString(e)), 0;
+    }
+    m->samp_state = 1;
+    m->samp_temp = temp;
+    m->samp_top_k = top_k;
+    m->samp_top_p = top_p;
+    return 1;
+}
+
+/* qwen_generate (qwen.c:204-228) with sampling: the same loop as
+ * ncm_qwen_generate, the greedy id replaced by sample_topkp's draw on the
+ * device (csrc/sample.hip) from the xorshift64* state *rng, which is
+ * advanced once per generated token, as the reference's host loop does.
+ * temp <= 0 is the greedy path (rng untouched).  n_flagged (may be NULL)
+ * receives the number of draws not certified equal to the reference's
+ * arithmetic on these logits (flag 1 or 2 of sample_topkp_dev). */
+int ncm_qwen_generate_sample(NcmQwen *m, const int *prompt, int np, int n_new, int eos, float temp, int top_k,
+                             float top_p, unsigned long long *rng, int *out, int *n_flagged) {
+    if (n_flagged) *n_flagged = 0;
+    if (!(temp > 0.0f)) return ncm_qwen_generate(m, prompt, np, n_new, eos, out);
+    if (!m || !prompt || np <= 0 || n_new < 0 || !out || !rng) {
+        ncm_fail(NCM_E_ARG, "ncm_qwen_generate_sample: bad arguments");
+        return -1;
+    }
+    if (np + n_new > m->c.n_ctx) { ncm_fail(NCM_E_ARG, "ncm_qwen_generate_sample: context overflow"); return -1; }
+    if (top_p < 0.0f) { ncm_fail(NCM_E_ARG, "ncm_qwen_generate_sample: top_p must be >= 0"); return -1; }
+    if (ncm_ready() || decode_ok(m, "ncm_qwen_generate_sample")) return -1;
+    if (n_new == 0) return 0;
+    if (!m->samp_ws) {
+        size_t b = ncm_sample_ws_bytes(m->c.vocab);
+        if (!b) { ncm_fail(NCM_E_ARG, "ncm_qwen_generate_sample: vocab %d exceeds the sampler's 262144", m->c.vocab); return -1; }
+        if (!(m->samp_ws = ncm_hip_malloc(b))) return -1;
+    }
+    mem_h2d(m->rng_dev, rng, sizeof *rng);
+    float *lg = ncm_qwen_forward(m, prompt, np, 1);
+    if (!lg) return -1;
+    int p0 = np - 1;
+    mem_h2d(m->pos_dev, &p0, sizeof(int));
+    if (ncm_sample_launch(lg, m->c.vocab, temp, top_k, top_p, m->rng_dev, NULL, m->ids_dev, m->pos_dev,
+                          m->flags_dev, m->samp_ws))
+        return -1;
+    int made = 1, stop = 0;
+    if (eos >= 0) {
+        mem_d2h(out, m->ids_dev + np, sizeof(int));
+        stop = out[0] == eos;
+    }
+    for (int s = 1; s < n_new && !stop; s++) {
+        if (samp_graph(m, temp, top_k, top_p)) {
+            hipError_t e = hipGraphLaunch(m->samp_graph, ncm_stream());
+            if (e != hipSuccess) { ncm_fail(NCM_E_HIP, "qwen: graph launch: %s", hipGetErrorString(e)); return -1; }
+        } else if (m->samp_state == -1 || getenv("NCM_NO_GRAPH")) {
+            if (decode_core(m) || ncm_sample_launch(m->logits, m->c.vocab, temp, top_k, top_p, m->rng_dev, NULL,
+                                                    m->ids_dev, m->pos_dev, m->flags_dev, m->samp_ws))
+                return -1;
+        } else {
+            return -1;
+        }
+        made++;
+        if (eos >= 0) {
+            mem_d2h(out + s, m->ids_dev + np + s, sizeof(int));
+            stop = out[s] == eos;
+        }
+    }
+    mem_d2h(out, m->ids_dev + np, (size_t)made * sizeof(int));
+    mem_d2h(rng, m->rng_dev, sizeof *rng);
+    if (n_flagged) {
+        int *fl = (int *)malloc((size_t)made * sizeof(int));
+        if (!fl) { ncm_fail(NCM_E_OOM, "ncm_qwen_generate_sample: flags"); return -1; }
+        mem_d2h(fl, m->flags_dev + np, (size_t)made * sizeof(int));
+        for (int i = 0; i < made; i++) *n_flagged += fl[i] != 0;
+        free(fl);
+    }
     return made;
 }

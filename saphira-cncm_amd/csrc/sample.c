@@ -1,14 +1,16 @@
 /* sample.c -- host side of the device sampler (csrc/sample.hip): the
  * reference's sample_topkp (src/kernels.c:782-825) with the row on the
- * device.  Launch sequence per row: 4 radix passes (histogram, scan,
- * scatter), the probabilities, and the one-workgroup finish. */
+ * device.  Launch sequence per row: 4 radix passes (a digit histogram, then
+ * a scatter that forms its own offsets from it), the probabilities, and the
+ * one-workgroup finish: 10 launches. */
 #include "internal.h"
 
 #include <limits.h>
 #include <string.h>
 
-#define SMP_SB 2048
-#define SMP_MAXB 128
+#define SMP_NT 1024
+#define SMP_SB 8192
+#define SMP_MAXB 32
 #define SMP_PB 1024
 #define SMP_VMAX (SMP_SB * SMP_MAXB)
 
@@ -47,17 +49,31 @@ typedef struct {
 
 static size_t up8(size_t n) { return (n + 7) & ~(size_t)7; }
 
-static int smp_ws(int V, SmpWs *w) {
+/* Byte offsets of the workspace parts for a row of V; returns the total. */
+static size_t smp_layout(int V, size_t off[12]) {
     const int nblk = (V + SMP_SB - 1) / SMP_SB, nbp = (V + SMP_PB - 1) / SMP_PB;
     const size_t v4 = up8((size_t)V * 4);
-    size_t off[12], total = 0;
-    const size_t sz[12] = {v4, v4, v4, v4, up8((size_t)256 * nblk * 4), up8((size_t)nblk * 4),
+    size_t total = 0;
+    const size_t sz[12] = {v4, v4, v4, v4, up8((size_t)4 * 256 * nblk * 4), up8((size_t)nblk * 4),
                            (size_t)V * 8, (size_t)nbp * 8, v4, 8, 8, 8};
     for (int j = 0; j < 12; j++) {
         off[j] = total;
         total += sz[j];
     }
-    char *b = (char *)ncm_workspace(WS_SAMPLE, total);
+    return total;
+}
+
+size_t ncm_sample_ws_bytes(int V) {
+    size_t off[12];
+    return V >= 1 && V <= SMP_VMAX ? smp_layout(V, off) : 0;
+}
+
+/* Carves the workspace from own (a caller-owned buffer of
+ * ncm_sample_ws_bytes(V)) or, when own is null, from the library's. */
+static int smp_ws_at(int V, void *own, SmpWs *w) {
+    size_t off[12];
+    const size_t total = smp_layout(V, off);
+    char *b = own ? (char *)own : (char *)ncm_workspace(WS_SAMPLE, total);
     if (!b) return NCM_E_OOM;
     w->k[0] = (unsigned *)(b + off[0]);
     w->k[1] = (unsigned *)(b + off[1]);
@@ -74,6 +90,8 @@ static int smp_ws(int V, SmpWs *w) {
     return 0;
 }
 
+static int smp_ws(int V, SmpWs *w) { return smp_ws_at(V, NULL, w); }
+
 static int smp_check(const char *fn, const float *x, int V, float top_p) {
     if (!x || V < 1 || V > SMP_VMAX)
         return ncm_fail(NCM_E_ARG, "%s: need logits and 1 <= V <= %d (V = %d)", fn, SMP_VMAX, V);
@@ -84,32 +102,31 @@ static int smp_check(const char *fn, const float *x, int V, float top_p) {
 }
 
 /* The device sampler for temp > 0: sorts the row, then the finish kernel
- * writes the id to *out, or to ids[*pos + 1] and advances *pos when pos is
- * set.  All pointers are device memory; launches only (no copies, no fills),
- * so the sequence can be captured in a graph. */
+ * writes the id to *out and the flag to *flag, or, when pos is set, to
+ * ids[*pos + 1] and flag[*pos + 1] and advances *pos.  All pointers are
+ * device memory; launches only (no copies, no fills), so the sequence can
+ * be captured in a graph (with ws, a caller-owned workspace, whose address
+ * then stays valid). */
 int ncm_sample_launch(const float *x, int V, float temp, int top_k, float top_p, unsigned long long *rng,
-                      int *out, int *ids, int *pos, int *flag) {
+                      int *out, int *ids, int *pos, int *flag, void *ws) {
     int rc = smp_check("sample", x, V, top_p);
     if (rc) return rc;
     if (!(temp > 0.0f)) return ncm_fail(NCM_E_ARG, "sample: temp must be > 0 on the sampling path");
     if (!rng || !flag || (!out && !(ids && pos))) return ncm_fail(NCM_E_ARG, "sample: null pointer");
     if ((rc = ncm_ready())) return rc;
     SmpWs w;
-    if ((rc = smp_ws(V, &w))) return rc;
-    const int nblk = (V + SMP_SB - 1) / SMP_SB, total = 256 * nblk;
+    if ((rc = smp_ws_at(V, ws, &w))) return rc;
+    const int nblk = (V + SMP_SB - 1) / SMP_SB;
     const int keep = top_k > 0 && top_k < V ? top_k : V, nbp = (keep + SMP_PB - 1) / SMP_PB;
     const unsigned *kin = NULL;
     const int *iin = NULL;
     for (int pass = 0; pass < 4; pass++) {
-        int shift = 8 * pass;
         unsigned *kout = w.k[pass & 1];
         int *iout = w.i[pass & 1];
-        void *ha[] = {&x, &temp, &kin, &V, &shift, &w.hist, (void *)&nblk, &w.bad};
-        if ((rc = ncm_launch_named("smp_hist", (unsigned)nblk, 1, 1, 256, ha))) return rc;
-        void *sa[] = {&w.hist, (void *)&total};
-        if ((rc = ncm_launch_named("smp_scan", 1, 1, 1, 1024, sa))) return rc;
-        void *ca[] = {&x, &temp, &kin, &iin, &V, &shift, &w.hist, (void *)&nblk, &kout, &iout};
-        if ((rc = ncm_launch_named("smp_scatter", (unsigned)nblk, 1, 1, 256, ca))) return rc;
+        void *ha[] = {&x, &temp, &kin, &V, &pass, &w.hist, (void *)&nblk, &w.bad};
+        if ((rc = ncm_launch_named("smp_hist", (unsigned)nblk, 1, 1, SMP_NT, ha))) return rc;
+        void *ca[] = {&x, &temp, &kin, &iin, &V, &pass, &w.hist, (void *)&nblk, &kout, &iout};
+        if ((rc = ncm_launch_named("smp_scatter", (unsigned)nblk, 1, 1, SMP_NT, ca))) return rc;
         kin = kout;
         iin = iout;
     }
@@ -143,7 +160,7 @@ void sample_topkp_dev(const float *logits, int V, float temp, int top_k, float t
         if (smp_ws(V, &w)) return;
         fl = w.flag;
     }
-    ncm_sample_launch(logits, V, temp, top_k, top_p, rng, out, NULL, NULL, fl);
+    ncm_sample_launch(logits, V, temp, top_k, top_p, rng, out, NULL, NULL, fl, NULL);
 }
 
 unsigned long long rng_next(unsigned long long *state) {
@@ -180,7 +197,7 @@ int sample_topkp(const float *logits, int V, float temp, int top_k, float top_p,
         ncm_fail(NCM_E_HIP, "sample_topkp: copy of the row failed");
         return 0;
     }
-    if (ncm_sample_launch(w.row, V, temp, top_k, top_p, w.rng, w.out, NULL, NULL, w.flag)) return 0;
+    if (ncm_sample_launch(w.row, V, temp, top_k, top_p, w.rng, w.out, NULL, NULL, w.flag, NULL)) return 0;
     if (hipMemcpyAsync(&res[0], w.out, 4, hipMemcpyDeviceToHost, s) != hipSuccess ||
         hipMemcpyAsync(&res[1], w.flag, 4, hipMemcpyDeviceToHost, s) != hipSuccess ||
         hipMemcpyAsync(rng, w.rng, 8, hipMemcpyDeviceToHost, s) != hipSuccess ||

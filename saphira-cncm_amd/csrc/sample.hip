@@ -13,7 +13,7 @@
 //   pick = ord[first r < nkeep with u <= q_0 + .. + q_r], else ord[nkeep-1]
 //
 // Device plan: a stable LSD radix sort of (order key, index) over 4 passes of
-// 8 bits (smp_hist, smp_scan, smp_scatter), fp64 probabilities with fixed-
+// 8 bits (smp_hist, smp_scatter per pass), fp64 probabilities with fixed-
 // order block sums (smp_probs), and one workgroup (smp_finish) that locates
 // the nucleus cut and the draw: a prefilter over block prefix sums, then an
 // element scan inside the block.
@@ -30,8 +30,9 @@
 // row holds a non-finite w (outside the reference's defined behaviour).
 #include "ncm_dev.h"
 
-#define SMP_SB 2048     // elements per sort block (256 threads x 8 rounds)
-#define SMP_MAXB 128    // sort blocks -> V <= 262144
+#define SMP_NT 1024     // threads of a sort block
+#define SMP_SB 8192     // elements per sort block (SMP_NT threads x 8 rounds)
+#define SMP_MAXB 32     // sort blocks -> V <= 262144
 #define SMP_PB 1024     // elements per probability block (= finish workgroup)
 
 // Order key of w: ascending key order = descending w.  -0 and +0 are one
@@ -43,22 +44,23 @@ __device__ __forceinline__ unsigned smp_key(float w) {
     return ~asc;
 }
 
-// Digit histogram of one sort block: hist[d * nblk + block].  Pass 0 reads
-// the logits (kin == null) and records whether the block holds a
-// non-finite w in bad[block].
-extern "C" __global__ void __launch_bounds__(256)
-smp_hist(const float *__restrict__ x, float temp, const unsigned *__restrict__ kin, int n, int shift,
+// Digit histogram of radix pass `pass` for one sort block:
+// hist[pass][d][block].  Pass 0 reads the logits (kin == null) and records
+// a block's non-finite w in bad[block]; later passes read the previous
+// pass's output.
+extern "C" __global__ void __launch_bounds__(SMP_NT)
+smp_hist(const float *__restrict__ x, float temp, const unsigned *__restrict__ kin, int n, int pass,
          int *__restrict__ hist, int nblk, int *__restrict__ bad) {
     __shared__ int cnt[256];
     __shared__ int anybad;
-    const int tid = threadIdx.x, b = blockIdx.x;
-    cnt[tid] = 0;
+    const int tid = threadIdx.x, b = blockIdx.x, shift = 8 * pass;
+    if (tid < 256) cnt[tid] = 0;
     if (tid == 0) anybad = 0;
     __syncthreads();
     int nf = 0;
 #pragma unroll
-    for (int r = 0; r < SMP_SB / 256; ++r) {
-        const int e = b * SMP_SB + r * 256 + tid;
+    for (int r = 0; r < SMP_SB / SMP_NT; ++r) {
+        const int e = b * SMP_SB + r * SMP_NT + tid;
         if (e < n) {
             unsigned k;
             if (kin) {
@@ -73,70 +75,86 @@ smp_hist(const float *__restrict__ x, float temp, const unsigned *__restrict__ k
     }
     if (nf) anybad = 1;
     __syncthreads();
-    hist[tid * nblk + b] = cnt[tid];
+    if (tid < 256) hist[(pass * 256 + tid) * nblk + b] = cnt[tid];
     if (!kin && tid == 0) bad[b] = anybad;
 }
 
-// Exclusive scan, in place, of the (digit-major) histogram: total = 256 *
-// nblk <= 32768 counts, staged in LDS.
-extern "C" __global__ void __launch_bounds__(1024)
-smp_scan(int *__restrict__ h, int total) {
-    __shared__ int buf[256 * SMP_MAXB];
-    __shared__ int part[1024];
-    const int tid = threadIdx.x;
-    for (int i = tid; i < total; i += 1024) buf[i] = h[i];
-    __syncthreads();
-    const int per = (total + 1023) / 1024, lo = min(total, tid * per), hi = min(total, lo + per);
-    int s = 0;
-    for (int i = lo; i < hi; ++i) s += buf[i];
-    part[tid] = s;
-    __syncthreads();
-    for (int o = 1; o < 1024; o <<= 1) {
-        const int v = tid >= o ? part[tid - o] : 0;
-        __syncthreads();
-        part[tid] += v;
-        __syncthreads();
-    }
-    int run = tid ? part[tid - 1] : 0;
-    for (int i = lo; i < hi; ++i) {
-        const int v = buf[i];
-        buf[i] = run;
-        run += v;
-    }
-    __syncthreads();
-    for (int i = tid; i < total; i += 1024) h[i] = buf[i];
-}
-
-// Stable scatter of one sort block by the digit at `shift`: rounds of 256
-// elements in block order; inside a round, lanes with the same digit are
-// ranked with ballots, and waves in order through per-wave digit counts.
+// Stable scatter of one sort block by the digit of radix pass `pass`.
+//   1. Wave w owns the block's elements [w * 512, (w + 1) * 512) in rounds
+//      of 64: a lane's rank among its wave's earlier elements of the same
+//      digit comes from ballots (lanes of the round with that digit) and a
+//      wave-private running count per digit (no barrier).
+//   2. Threads 0..255 (one per digit) scan the counts: the block's local
+//      start of each digit, each wave's start inside it, and the digit's
+//      global start from the pass's histogram (all blocks' counts of the
+//      digit before this block, plus every count of smaller digits).
+//   3. The elements are placed in LDS in sorted order and each digit's run
+//      is written to global memory by consecutive threads (coalesced).
 // Pass 0 forms (key, index) from the logits (kin == null).  A position
 // outside [0, n) is never written (it cannot occur: the offsets come from
-// the same elements' histogram).
-extern "C" __global__ void __launch_bounds__(256)
+// the same elements).
+#define SMP_W (SMP_NT / 64)
+#define SMP_R (SMP_SB / SMP_NT)   // rounds per wave
+extern "C" __global__ void __launch_bounds__(SMP_NT)
 smp_scatter(const float *__restrict__ x, float temp, const unsigned *__restrict__ kin,
-            const int *__restrict__ iin, int n, int shift, const int *__restrict__ offs, int nblk,
+            const int *__restrict__ iin, int n, int pass, const int *__restrict__ hist, int nblk,
             unsigned *__restrict__ kout, int *__restrict__ iout) {
-    __shared__ int run[256];
-    __shared__ int wcnt[4][256];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, b = blockIdx.x;
-    run[tid] = 0;
-    const unsigned long long below = (1ull << lane) - 1ull;
-    for (int r = 0; r < SMP_SB / 256; ++r) {
-        const int e = b * SMP_SB + r * 256 + tid;
-        const bool valid = e < n;
-        unsigned k = 0u;
-        int id = 0;
-        if (valid) {
+    __shared__ int gofs[256];          // global position minus local position, per digit
+    __shared__ int wrun[SMP_W][256];   // per wave: digit counts, then the wave's local start
+    __shared__ int wsg[4], wsl[4];     // digit-scan totals of the 4 digit waves (global, local)
+    __shared__ unsigned sk[SMP_SB];
+    __shared__ int si[SMP_SB];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, b = blockIdx.x, shift = 8 * pass;
+    const int e0 = b * SMP_SB + wave * (SMP_R * 64) + lane;   // element of round r: e0 + 64 r
+    const int nloc = min(SMP_SB, n - b * SMP_SB);
+    unsigned kk[SMP_R];
+    int ii[SMP_R], rk[SMP_R];
+#pragma unroll
+    for (int r = 0; r < SMP_R; ++r) {
+        const int e = e0 + 64 * r;
+        kk[r] = 0u;
+        ii[r] = 0;
+        if (e < n) {
             if (kin) {
-                k = kin[e];
-                id = iin[e];
+                kk[r] = kin[e];
+                ii[r] = iin[e];
             } else {
-                k = smp_key(x[e] / temp);
-                id = e;
+                kk[r] = smp_key(x[e] / temp);
+                ii[r] = e;
             }
         }
-        const unsigned d = (k >> shift) & 255u;
+    }
+    // global start of the digit, less the wave-total part (threads 0..255;
+    // the nblk <= 32 counts of a digit load together)
+    int gpart = 0;
+    if (tid < 256) {
+        const int *hd = hist + (pass * 256 + tid) * nblk;
+        int v[SMP_MAXB];
+#pragma unroll
+        for (int j = 0; j < SMP_MAXB; ++j) v[j] = j < nblk ? hd[j] : 0;
+        int tot = 0, pre = 0;
+#pragma unroll
+        for (int j = 0; j < SMP_MAXB; ++j) {
+            tot += v[j];
+            pre += j < b ? v[j] : 0;
+        }
+        int incl = tot;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int t = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += t;
+        }
+        if (lane == 63) wsg[wave] = incl;
+        gpart = incl - tot + pre;
+    }
+    // 1. wave-local ranks (the wave's own row of wrun; one wave's LDS accesses are ordered)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) wrun[wave][lane + 64 * j] = 0;
+    const unsigned long long below = (1ull << lane) - 1ull;
+#pragma unroll
+    for (int r = 0; r < SMP_R; ++r) {
+        const bool valid = e0 + 64 * r < n;
+        const unsigned d = (kk[r] >> shift) & 255u;
         unsigned long long peers = __ballot(valid);
 #pragma unroll
         for (int bit = 0; bit < 8; ++bit) {
@@ -144,23 +162,61 @@ smp_scatter(const float *__restrict__ x, float temp, const unsigned *__restrict_
             const unsigned long long m = __ballot(on);
             peers &= on ? m : ~m;
         }
+        const int before = wrun[wave][d];
+        rk[r] = before + __popcll(peers & below);
+        if (valid && (peers & below) == 0ull) wrun[wave][d] = before + __popcll(peers);
+    }
+    __syncthreads();
+    // 2. per digit: block count, local start, global start, waves' starts
+    int cnt = 0, incl = 0;
+    if (tid < 256) {
 #pragma unroll
-        for (int w = 0; w < 4; ++w) wcnt[w][tid] = 0;
-        __syncthreads();
-        if (valid && (peers & below) == 0ull) wcnt[wave][d] = __popcll(peers);
-        __syncthreads();
-        if (valid) {
-            int pos = run[d] + __popcll(peers & below);
-            for (int w = 0; w < wave; ++w) pos += wcnt[w][d];
-            pos += offs[d * nblk + b];
-            if ((unsigned)pos < (unsigned)n) {
-                kout[pos] = k;
-                iout[pos] = id;
+        for (int w = 0; w < SMP_W; ++w) cnt += wrun[w][tid];
+        incl = cnt;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int t = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += t;
+        }
+        if (lane == 63) wsl[wave] = incl;
+    }
+    __syncthreads();
+    if (tid < 256) {
+        int pg = 0, pl = 0;
+        for (int w = 0; w < wave; ++w) {
+            pg += wsg[w];
+            pl += wsl[w];
+        }
+        const int lstart = incl - cnt + pl;
+        gofs[tid] = gpart + pg - lstart;
+        int acc = lstart;
+#pragma unroll
+        for (int w = 0; w < SMP_W; ++w) {
+            const int c = wrun[w][tid];
+            wrun[w][tid] = acc;
+            acc += c;
+        }
+    }
+    __syncthreads();
+    // 3. sorted order in LDS, then coalesced runs to global memory
+#pragma unroll
+    for (int r = 0; r < SMP_R; ++r) {
+        if (e0 + 64 * r < n) {
+            const int lp = wrun[wave][(kk[r] >> shift) & 255u] + rk[r];
+            if ((unsigned)lp < (unsigned)SMP_SB) {
+                sk[lp] = kk[r];
+                si[lp] = ii[r];
             }
         }
-        __syncthreads();
-        run[tid] += wcnt[0][tid] + wcnt[1][tid] + wcnt[2][tid] + wcnt[3][tid];
-        __syncthreads();
+    }
+    __syncthreads();
+    for (int lp = tid; lp < nloc; lp += SMP_NT) {
+        const unsigned k = sk[lp];
+        const int pos = gofs[(k >> shift) & 255u] + lp;
+        if ((unsigned)pos < (unsigned)n) {
+            kout[pos] = k;
+            iout[pos] = si[lp];
+        }
     }
 }
 
@@ -209,7 +265,7 @@ struct SmpFinishArgs {
     int nblk;
     unsigned long long *rng; // xorshift64* state, advanced once
     int *out;                // the id (when pos is null)
-    int *ids;                // position-driven: ids[*pos + 1] = id, then ++*pos
+    int *ids;                // position-driven: ids[*pos + 1] = id, flag[*pos + 1] = flag, then ++*pos
     int *pos;
     int *flag;               // 0 certified, 1 within the bound of a boundary, 2 non-finite input
     int n;                   // row length (bounds the sorted indices)
@@ -218,9 +274,11 @@ struct SmpFinishArgs {
 struct SmpState {
     double bp[SMP_MAXB * SMP_SB / SMP_PB + 1];   // exclusive prefix of the block sums
     double sc[SMP_PB];                            // inclusive scan of one block's q
+    double qv[SMP_PB];                            // that block's q
+    double wtot[16];
     int first[16];
     double den;
-    int nbp, keep;
+    int nbp, keep, cur;                           // cur: the block held in sc / qv (-1 none)
 };
 
 // Lowest thread index whose pred holds (1024 if none).
@@ -236,19 +294,35 @@ __device__ __forceinline__ int smp_first(bool pred, SmpState &S) {
     return r;
 }
 
-// Inclusive scan of q_r = p_r / den over probability block b into S.sc;
-// returns this thread's q.
-__device__ __forceinline__ double smp_scan_block(int b, const double *__restrict__ p, SmpState &S) {
-    const int tid = threadIdx.x, r = b * SMP_PB + tid;
-    const double q = r < S.keep ? p[r] / S.den : 0.0;
-    S.sc[tid] = q;
-    __syncthreads();
-    for (int o = 1; o < SMP_PB; o <<= 1) {
-        const double v = tid >= o ? S.sc[tid - o] : 0.0;
-        __syncthreads();
-        S.sc[tid] += v;
-        __syncthreads();
+// Inclusive scan over the workgroup of one value per thread into S.sc
+// (wave shuffles, then the wave totals).
+__device__ __forceinline__ void smp_scan_wg(double v, SmpState &S) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    double incl = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const double t = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += t;
     }
+    if (lane == 63) S.wtot[w] = incl;
+    __syncthreads();
+    double pre = 0.0;
+    for (int i = 0; i < w; ++i) pre += S.wtot[i];
+    S.sc[tid] = pre + incl;
+    __syncthreads();
+}
+
+// Inclusive scan of q_r = p_r / den over probability block b into S.sc
+// (kept while the same block is asked for again); returns this thread's q.
+__device__ __forceinline__ double smp_scan_block(int b, const double *__restrict__ p, SmpState &S) {
+    const int tid = threadIdx.x;
+    if (S.cur == b) return S.qv[tid];
+    const int r = b * SMP_PB + tid;
+    const double q = r < S.keep ? p[r] / S.den : 0.0;
+    S.qv[tid] = q;
+    smp_scan_wg(q, S);
+    if (tid == 0) S.cur = b;
+    __syncthreads();
     return q;
 }
 
@@ -281,9 +355,7 @@ __device__ double smp_prefix(int n, const double *__restrict__ p, SmpState &S) {
     if (n >= S.keep) return S.bp[S.nbp] / S.den;
     const int b = n / SMP_PB, t = n % SMP_PB;
     smp_scan_block(b, p, S);
-    const double v = S.bp[b] / S.den + (t ? S.sc[t - 1] : 0.0);
-    __syncthreads();
-    return v;
+    return S.bp[b] / S.den + (t ? S.sc[t - 1] : 0.0);
 }
 
 extern "C" __global__ void __launch_bounds__(1024)
@@ -292,17 +364,13 @@ smp_finish(SmpFinishArgs a) {
     __shared__ SmpState S;
     __shared__ double Ush;
     const int tid = threadIdx.x;
-    S.nbp = a.nbp;
-    S.keep = a.keep;
-    // exclusive prefix of the block sums (a Hillis-Steele scan over <= 256 blocks)
-    if (tid < SMP_PB) S.sc[tid] = tid < a.nbp ? a.bsum[tid] : 0.0;
-    __syncthreads();
-    for (int o = 1; o < SMP_PB; o <<= 1) {
-        const double v = tid >= o ? S.sc[tid - o] : 0.0;
-        __syncthreads();
-        S.sc[tid] += v;
-        __syncthreads();
+    if (tid == 0) {
+        S.nbp = a.nbp;
+        S.keep = a.keep;
+        S.cur = -1;
     }
+    // exclusive prefix of the block sums (<= 256 blocks)
+    smp_scan_wg(tid < a.nbp ? a.bsum[tid] : 0.0, S);
     if (tid <= a.nbp) S.bp[tid] = tid ? S.sc[tid - 1] : 0.0;
     int nf = 0;
     for (int i = tid; i < a.nblk; i += 1024) nf |= a.bad[i];
@@ -365,13 +433,15 @@ smp_finish(SmpFinishArgs a) {
         else
             ok = lo == hi && nk > 0 && u_lo - 2.0 * eta > acc_prev;
         const int id = nk > 0 ? a.idx[pick] : 0;
-        *a.flag = nonfinite ? 2 : (ok ? 0 : 1);
+        const int fl = nonfinite ? 2 : (ok ? 0 : 1);
         if (a.pos) {
             const int ps = *a.pos;
             a.ids[ps + 1] = id;
+            a.flag[ps + 1] = fl;
             *a.pos = ps + 1;
         } else {
             *a.out = id;
+            *a.flag = fl;
         }
     }
 }

@@ -132,6 +132,8 @@ _SIGS = {
     "ncm_qwen_forward": (vp, [vp, vp, ci, ci]),
     "ncm_qwen_decode": (vp, [vp, ci, ci]),
     "ncm_qwen_generate": (ci, [vp, vp, ci, ci, ci, vp]),
+    "ncm_qwen_generate_sample": (ci, [vp, vp, ci, ci, ci, ctypes.c_float, ci, ctypes.c_float,
+                                      ctypes.POINTER(ctypes.c_uint64), vp, ctypes.POINTER(ci)]),
     "ncm_ncp_param_count": (ci, [vp]),
     "ncm_ncp_param_shape": (i64, [vp, ci, ctypes.POINTER(i64), ctypes.POINTER(i64)]),
     "ncm_ncp_rope_tables": (ci, [ci, ci, ci, vp, vp]),

@@ -72,6 +72,15 @@ class Model:
         ncmhip.check()
         return list(out[:n])
 
+    def generate_sample(self, prompt, n_new, temp, top_k, top_p, rng, eos=-1):
+        prompt = np.ascontiguousarray(prompt, np.int32)
+        out = np.zeros(n_new, np.int32)
+        st, nf = ctypes.c_uint64(rng), ctypes.c_int(-1)
+        n = self.lib.ncm_qwen_generate_sample(self.m, prompt.ctypes.data, prompt.size, n_new, eos, temp, top_k,
+                                              top_p, ctypes.byref(st), out.ctypes.data, ctypes.byref(nf))
+        ncmhip.check()
+        return list(out[:n]), st.value, nf.value
+
     def close(self):
         self.lib.ncm_qwen_free(self.m)
 
@@ -159,3 +168,37 @@ def test_decode_graph_replays_match_eager(monkeypatch):
     finally:
         eager.close()
         graph.close()
+
+
+@pytest.mark.parametrize("temp,top_k,top_p", [(0.8, 0, 0.9), (1.3, 40, 1.0), (0.05, 0, 0.95)])
+def test_sampled_generation_draws_match_oracle(temp, top_k, top_p, monkeypatch):
+    """Sampling inside the replayed decode graph: every step's id and the rng
+    state are the reference sampler's (oracle, pinned to kernels.c:782-825)
+    on that step's logits, which the eager cached decode reproduces; graph
+    and eager generation agree; the greedy setting falls back to argmax."""
+    cfg = SMALL
+    params = weights(5, **cfg)
+    prompt = np.random.default_rng(6).integers(0, cfg["V"], 19).astype(np.int32)
+    n_new, seed = 10, 0x5EED
+    m = Model(params, n_ctx=64, theta=1e6, **cfg)
+    try:
+        ids, st, nf = m.generate_sample(prompt, n_new, temp, top_k, top_p, seed)
+        assert len(ids) == n_new and nf == 0
+        lg = m.forward(prompt, last_only=True)
+        s = seed
+        for k in range(n_new):
+            want, s = O.sample_topkp(lg, temp, top_k, top_p, s)
+            assert ids[k] == want, k
+            if k + 1 < n_new:
+                lg = m.decode(ids[k], len(prompt) + k)
+        assert st == s
+        ids2, st2, _ = m.generate_sample(prompt, n_new, temp, top_k, top_p, seed)   # graph replays
+        monkeypatch.setenv("NCM_NO_GRAPH", "1")
+        ids3, st3, _ = m.generate_sample(prompt, n_new, temp, top_k, top_p, seed)   # eager launches
+        assert ids2 == ids and ids3 == ids and st2 == st3 == st
+        eos = ids[3]
+        ids4, _, _ = m.generate_sample(prompt, n_new, temp, top_k, top_p, seed, eos=eos)
+        assert ids4 == ids[:ids.index(eos) + 1]
+        assert m.generate_sample(prompt, 4, 0.0, top_k, top_p, seed)[:2] == (m.generate(prompt, 4), seed)
+    finally:
+        m.close()

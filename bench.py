@@ -46,8 +46,8 @@ CPU_MS = [1, 64, 512]
 # "bench.py --steps 2 --warmup 1 --no-cpu --no-extras --copy-calibration",
 # each scaled by what the counter reads for the run's 256 MiB copies; valid
 # while the same kernel and launches are the roofline.
-TRAFFIC = {("gemm_64x64_dx_v", ("dX M=4096 3072->768", "dX M=4096 4864->896", "dX M=4096 896->4864",
-                                "dX M=512 4864->896")): 269.6e6}
+TRAFFIC = {("gemm_64x64_dx_v", ("dX M=4096 3072->768", "dX M=4096 4864->896", "dX M=4096 768->2304",
+                                "dX M=4096 768->3072")): 211.4e6}
 
 
 def build_workload(ncmhip, seed=0):

@@ -543,6 +543,39 @@ typedef struct {
  * opened.  Host only (no device use). */
 int config_load(NCMConfig *c, const char *path);
 
+/* ------------------------------------------------------------------ */
+/* the multiscale quantizer -- replaces src/vq.c (ncm.h:205-239)       */
+/* ------------------------------------------------------------------ */
+
+typedef struct VQState VQState;
+/* replaces vq_load, ncm.h:206, vq.c:76-197: codebooks "embeddings.<i>.weight",
+ * the Phi convs "quant_resi.<i>.*" (per level / shared / k partially shared),
+ * the learned level-0 cascade "learned_down_l1.<i>.*" / "learned_up_l1.<i>.*"
+ * and the refine convs "learned_{down,up}_refine.<i>.*", from the store's
+ * DEVICE tensors (borrowed).  Errors (missing or mis-shaped weights, a cascade
+ * that does not map L to levels[0] and back, kernels above 16) are reported
+ * like the reference's exit(1); NULL in record mode. */
+VQState *vq_load(const NCMConfig *c, WeightStore *ws, const char *prefix);
+/* replaces vq_free / vq_total_codes and the accessors, ncm.h:207-208, 235-239 */
+void vq_free(VQState *vq);
+int  vq_total_codes(const VQState *vq);
+int  vq_nlevels(const VQState *vq);
+int  vq_level_len(const VQState *vq, int k);
+int  vq_level_V(const VQState *vq, int k);
+int  vq_Ltotal(const VQState *vq);
+int  vq_Ddim(const VQState *vq);
+/* replaces vq_z_to_idx, ncm.h:210, vq.c:378-500 (argmin at every level):
+ * z [B][L][D] device, idx [B][total] HOST level-major codes, as the
+ * reference's caller receives them.  Codes bit-exact with the CPU path. */
+void vq_z_to_idx(VQState *vq, const float *z, int B, int *idx);
+/* extension: vq_z_to_idx with device codes, and the final z_hat / z_rest
+ * [B][L][D] (device, may be NULL); asynchronous on the library stream. */
+void vq_z_to_idx_dev(VQState *vq, const float *z, int B, int *idx, float *z_hat, float *z_rest);
+/* replaces vq_idx_to_zhats, ncm.h:217, vq.c:502-552: idx HOST; zhats[level]
+ * device [B][L][D] buffers receiving z_hat after each level. */
+void vq_idx_to_zhats(VQState *vq, const int *idx, int B, float **zhats);
+
+
 /* replaces train_data_load / train_data_free, ncm.h:262-264, tensor.c:375-395:
  * "NCMT" magic, u64 rows, u64 row length, int32 tokens; at most max_rows rows
  * when max_rows > 0.  HOST rows; NULL on error.  Host only. */

@@ -256,6 +256,278 @@ int orc_sample_topkp(const float *logits, int V, float temp, int top_k, float to
     return pick;
 }
 
+/* ---- the full multiscale quantizer (src/vq.c), [B][T][D] layout ---- */
+
+/* kernels.c:681-700 interpolate_area_fwd per (b, d) column: output t
+ * averages inputs [floor(t Tin / Tout), ceil((t + 1) Tin / Tout)) in fp64. */
+static void orc_area(const float *x, float *y, int B, int Tin, int Tout, int D) {
+    for (int b = 0; b < B; b++)
+        for (int d = 0; d < D; d++)
+            for (int t = 0; t < Tout; t++) {
+                int64_t s = (int64_t)((double)t * Tin / Tout);
+                int64_t e = (int64_t)ceil((double)(t + 1) * Tin / Tout);
+                if (e <= s) e = s + 1;
+                if (s < 0) s = 0;
+                if (e > Tin) e = Tin;
+                double acc = 0;
+                for (int64_t k = s; k < e; k++) acc += x[((int64_t)b * Tin + k) * D + d];
+                y[((int64_t)b * Tout + t) * D + d] = (float)(acc / (double)(e - s));
+            }
+}
+
+/* kernels.c:702-727 interpolate_linear_fwd (align_corners = False; a
+ * length-1 side averages) */
+static void orc_lin(const float *x, float *y, int B, int Tin, int Tout, int D) {
+    for (int b = 0; b < B; b++)
+        for (int d = 0; d < D; d++) {
+            const float *xc = x + (int64_t)b * Tin * D + d;
+            float *yc = y + (int64_t)b * Tout * D + d;
+            if (Tout == 1 || Tin == 1) {
+                double acc = 0;
+                for (int k = 0; k < Tin; k++) acc += xc[(int64_t)k * D];
+                for (int t = 0; t < Tout; t++) yc[(int64_t)t * D] = (float)(acc / Tin);
+                continue;
+            }
+            const double scale = (double)Tin / Tout;
+            for (int t = 0; t < Tout; t++) {
+                const double src = (t + 0.5) * scale - 0.5;
+                const int64_t s0 = (int64_t)floor(src), s1 = s0 + 1;
+                const double w1 = src - s0, w0 = 1.0 - w1;
+                const double v0 = xc[(s0 < 0 ? 0 : (s0 >= Tin ? Tin - 1 : s0)) * (int64_t)D];
+                const double v1 = xc[(s1 < 0 ? 0 : (s1 >= Tin ? Tin - 1 : s1)) * (int64_t)D];
+                yc[(int64_t)t * D] = (float)(w0 * v0 + w1 * v1);
+            }
+        }
+}
+
+/* kernels.c:546-566 conv1d_fwd: fp64 over ci (outer) and k (inner), W [Cout][Cin][K] */
+static void orc_conv1d(const float *x, const float *W, const float *bias, float *y, int B, int T, int Cin,
+                       int Cout, int K, int stride, int pad) {
+    const int64_t To = (T + 2 * pad - K) / stride + 1;
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int b = 0; b < B; b++)
+        for (int64_t t = 0; t < To; t++)
+            for (int co = 0; co < Cout; co++) {
+                double acc = bias ? bias[co] : 0.0;
+                for (int ci = 0; ci < Cin; ci++)
+                    for (int k = 0; k < K; k++) {
+                        const int ti = (int)(t * stride + k - pad);
+                        if (ti < 0 || ti >= T) continue;
+                        acc += (double)x[((int64_t)b * T + ti) * Cin + ci] * W[((int64_t)co * Cin + ci) * K + k];
+                    }
+                y[((int64_t)b * To + t) * Cout + co] = (float)acc;
+            }
+}
+
+/* kernels.c:568-590 convtranspose1d_fwd: W [Cin][Cout][K], output length (T - 1) s + K */
+static void orc_convT1d(const float *x, const float *W, const float *bias, float *y, int B, int T, int Cin,
+                        int Cout, int K, int stride) {
+    const int64_t To = (int64_t)(T - 1) * stride + K;
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int b = 0; b < B; b++)
+        for (int64_t t = 0; t < To; t++)
+            for (int co = 0; co < Cout; co++) {
+                double acc = bias ? bias[co] : 0.0;
+                for (int ci = 0; ci < Cin; ci++)
+                    for (int k = 0; k < K; k++) {
+                        const int num = (int)(t - k);
+                        if (num < 0 || num % stride != 0) continue;
+                        const int ti = num / stride;
+                        if (ti >= T) continue;
+                        acc += (double)x[((int64_t)b * T + ti) * Cin + ci] * W[((int64_t)ci * Cout + co) * K + k];
+                    }
+                y[((int64_t)b * To + t) * Cout + co] = (float)acc;
+            }
+}
+
+/* kernels.c:618-640 groupnorm_fwd (8 groups, no affine, eps 1e-5): fp64
+ * mean then variance over channel (outer) and position (inner) */
+static void orc_groupnorm(const float *x, float *y, int B, int T, int C) {
+    const int G = 8, Cg = C / G;
+    for (int b = 0; b < B; b++)
+        for (int g = 0; g < G; g++) {
+            const int64_t cnt = (int64_t)Cg * T;
+            double mean = 0;
+            for (int c = 0; c < Cg; c++)
+                for (int t = 0; t < T; t++) mean += x[((int64_t)b * T + t) * C + g * Cg + c];
+            mean /= cnt;
+            double var = 0;
+            for (int c = 0; c < Cg; c++)
+                for (int t = 0; t < T; t++) {
+                    const double d = x[((int64_t)b * T + t) * C + g * Cg + c] - mean;
+                    var += d * d;
+                }
+            var /= cnt;
+            const double inv = 1.0 / sqrt(var + 1e-5);
+            for (int c = 0; c < Cg; c++)
+                for (int t = 0; t < T; t++) {
+                    const int64_t i = ((int64_t)b * T + t) * C + g * Cg + c;
+                    y[i] = (float)((x[i] - mean) * inv);
+                }
+        }
+}
+
+/* vq.c:206-215 phi_index with the ticks of vq.c:118-125 */
+static int orc_phi_index(const OrcVq *q, int level) {
+    if (q->n_phi == 1) return 0;
+    const double at = (double)level / (q->n_levels - 1);
+    int best = 0;
+    double bd = 1e300;
+    for (int j = 0; j < q->n_phi; j++) {
+        const double tick = q->n_phi == 4 ? (j + 1.0 / 3.0) / q->n_phi : (j + 0.5) / q->n_phi;
+        const double d = fabs(tick - at);
+        if (d < bd) {
+            bd = d;
+            best = j;
+        }
+    }
+    return best;
+}
+
+/* y += conv1d(y, W, b) with kernel 3, padding 1 (the refine step of vq.c:310-330, 356-375) */
+static void orc_refine(float *y, const float *W, const float *bias, int B, int T, int D) {
+    float *r = (float *)malloc((size_t)B * T * D * sizeof(float));
+    orc_conv1d(y, W, bias, r, B, T, D, D, 3, 1, 1);
+    for (size_t i = 0; i < (size_t)B * T * D; i++) y[i] += r[i];
+    free(r);
+}
+
+/* the learned level-0 cascade: optional GroupNorm before every stage but the
+ * first, optional final GroupNorm (vq.c:285-309 down, 336-355 up) */
+static float *orc_cascade(const OrcVq *q, const float *x, int B, int T, int up, int *Tout) {
+    const int D = q->D, n = up ? q->n_up : q->n_down;
+    float *cur = (float *)malloc((size_t)B * T * D * sizeof(float));
+    memcpy(cur, x, (size_t)B * T * D * sizeof(float));
+    int Tc = T;
+    for (int i = 0; i < n; i++) {
+        const int s = up ? q->upK[i] : q->downK[i];
+        if (q->l1_norm && i > 0) {
+            float *g = (float *)malloc((size_t)B * Tc * D * sizeof(float));
+            orc_groupnorm(cur, g, B, Tc, D);
+            free(cur);
+            cur = g;
+        }
+        const int To = up ? (Tc - 1) * s + s : Tc / s;
+        float *nx = (float *)malloc((size_t)B * To * D * sizeof(float));
+        if (up)
+            orc_convT1d(cur, q->upW[i], q->upB[i], nx, B, Tc, D, D, s, s);
+        else
+            orc_conv1d(cur, q->downW[i], q->downB[i], nx, B, Tc, D, D, s, s, 0);
+        free(cur);
+        cur = nx;
+        Tc = To;
+    }
+    if (q->l1_norm_final) {
+        float *g = (float *)malloc((size_t)B * Tc * D * sizeof(float));
+        orc_groupnorm(cur, g, B, Tc, D);
+        free(cur);
+        cur = g;
+    }
+    *Tout = Tc;
+    return cur;
+}
+
+/* vq.c:280-330 down_for_quant: z_rest [B][L][D] -> out [B][levels[lv]][D] */
+static void orc_down(const OrcVq *q, const float *z, int B, int lv, float *out) {
+    const int D = q->D, L = q->levels[q->n_levels - 1], tl = q->levels[lv];
+    if (lv == 0 && q->n_down > 0) {
+        int Tc;
+        float *c = orc_cascade(q, z, B, L, 0, &Tc);
+        memcpy(out, c, (size_t)B * tl * D * sizeof(float));
+        free(c);
+    } else {
+        orc_area(z, out, B, L, tl, D);
+    }
+    if (q->has_all && lv >= 1 && lv <= q->n_levels - 2 && q->drefW[lv]) orc_refine(out, q->drefW[lv], q->drefB[lv], B, tl, D);
+}
+
+/* vq.c:332-376 up_to_full: q [B][levels[lv]][D] -> out [B][L][D] */
+static void orc_up(const OrcVq *q, const float *x, int B, int lv, float *out) {
+    const int D = q->D, L = q->levels[q->n_levels - 1], tl = q->levels[lv];
+    if (lv == 0 && q->n_down > 0) {
+        int Tc;
+        float *c = orc_cascade(q, x, B, tl, 1, &Tc);
+        memcpy(out, c, (size_t)B * L * D * sizeof(float));
+        free(c);
+    } else {
+        orc_lin(x, out, B, tl, L, D);
+    }
+    if (q->has_all && lv >= 1 && lv <= q->n_levels - 2 && q->urefW[lv]) orc_refine(out, q->urefW[lv], q->urefB[lv], B, L, D);
+}
+
+/* vq.c:243-277 apply_resi: h = (1 - r) h + r Phi(h) in float */
+static void orc_resi(const OrcVq *q, float *h, int B, int lv) {
+    if (q->n_phi <= 0) return;
+    const int D = q->D, L = q->levels[q->n_levels - 1], j = orc_phi_index(q, lv);
+    const size_t n = (size_t)B * L * D;
+    float *c = (float *)malloc(n * sizeof(float));
+    orc_conv1d(h, q->phiW[j], q->phib[j], c, B, L, D, D, 3, 1, 1);
+    const float r = q->resi_ratio;
+    for (size_t i = 0; i < n; i++) h[i] = (1 - r) * h[i] + r * c[i];
+    free(c);
+}
+
+/* q = E[lv][codes of level lv] ([B][tl][D]), then up-sampled and Phi-blended into up */
+static void orc_level_up(const OrcVq *q, const int *idx, int B, int lv, int base, float *up) {
+    const int D = q->D, tl = q->levels[lv];
+    int total = 0;
+    for (int k = 0; k < q->n_levels; k++) total += q->levels[k];
+    float *qq = (float *)malloc((size_t)B * tl * D * sizeof(float));
+    for (int b = 0; b < B; b++)
+        for (int t = 0; t < tl; t++)
+            memcpy(qq + ((size_t)b * tl + t) * D, q->E[lv] + (size_t)idx[(int64_t)b * total + base + t] * D,
+                   (size_t)D * sizeof(float));
+    orc_up(q, qq, B, lv, up);
+    free(qq);
+    orc_resi(q, up, B, lv);
+}
+
+/* vq.c:378-500 vq_z_to_idx (argmin at every level) */
+void orc_vq_z_to_idx(const OrcVq *q, const float *z, int B, int *idx, float *z_hat, float *z_rest) {
+    const int D = q->D, L = q->levels[q->n_levels - 1];
+    const size_t n = (size_t)B * L * D;
+    int total = 0;
+    for (int k = 0; k < q->n_levels; k++) total += q->levels[k];
+    float *zr = (float *)malloc(n * sizeof(float)), *zh = (float *)calloc(n, sizeof(float));
+    float *down = (float *)malloc(n * sizeof(float)), *up = (float *)malloc(n * sizeof(float));
+    memcpy(zr, z, n * sizeof(float));
+    int off = 0;
+    for (int lv = 0; lv < q->n_levels; lv++) {
+        const int tl = q->levels[lv], V = q->vocabs[lv];
+        orc_down(q, zr, B, lv, down);
+        int *codes = (int *)malloc((size_t)B * tl * sizeof(int));
+        orc_vq_argmin(down, q->E[lv], codes, (int64_t)B * tl, V, D);
+        for (int r = 0; r < B * tl; r++) idx[(int64_t)(r / tl) * total + off + r % tl] = codes[r];
+        free(codes);
+        orc_level_up(q, idx, B, lv, off, up);
+        off += tl;
+        for (size_t i = 0; i < n; i++) zh[i] += up[i];
+        for (size_t i = 0; i < n; i++) zr[i] -= up[i];
+    }
+    if (z_hat) memcpy(z_hat, zh, n * sizeof(float));
+    if (z_rest) memcpy(z_rest, zr, n * sizeof(float));
+    free(zr);
+    free(zh);
+    free(down);
+    free(up);
+}
+
+/* vq.c:502-552 vq_idx_to_zhats */
+void orc_vq_idx_to_zhats(const OrcVq *q, const int *idx, int B, float *zhats) {
+    const int D = q->D, L = q->levels[q->n_levels - 1];
+    const size_t n = (size_t)B * L * D;
+    float *zh = (float *)calloc(n, sizeof(float)), *up = (float *)malloc(n * sizeof(float));
+    int base = 0;
+    for (int lv = 0; lv < q->n_levels; lv++) {
+        orc_level_up(q, idx, B, lv, base, up);
+        for (size_t i = 0; i < n; i++) zh[i] += up[i];
+        memcpy(zhats + (size_t)lv * n, zh, n * sizeof(float));
+        base += q->levels[lv];
+    }
+    free(zh);
+    free(up);
+}
+
 /* tests/ktest_kernels.c:8-12: xorshift (13, 7, 17) mapped to [-2, 2) */
 void orc_fill_ktest(uint64_t *state, float *out, int64_t n) {
     for (int64_t i = 0; i < n; i++) {

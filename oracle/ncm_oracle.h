@@ -104,6 +104,34 @@ void orc_fill_ktest(uint64_t *state, float *out, int64_t n);
  * is the xorshift64* state, advanced once when temp > 0 */
 int orc_sample_topkp(const float *logits, int V, float temp, int top_k, float top_p, uint64_t *rng);
 
+/* The multiscale quantizer of src/vq.c in full (vq_load + vq_z_to_idx with
+ * rng = NULL, vq_idx_to_zhats): per-level lengths with area down-sampling
+ * (kernels.c:681-700) and linear up-sampling (kernels.c:702-727), the Phi
+ * residual conv (vq.c:243-277), the learned level-0 conv cascade with
+ * optional GroupNorm (vq.c:280-376; kernels.c:546-640) and the learned
+ * refine convs of the middle levels.  Tensors are row-major [B][T][D] (the
+ * reference's BLD layout); weights keep the reference's PyTorch layouts. */
+typedef struct {
+    int n_levels, D;
+    const int *levels, *vocabs;
+    const float *const *E;                       /* [n_levels] codebooks [V][D] */
+    int n_phi;                                   /* 0: Phi off */
+    float resi_ratio;
+    const float *const *phiW, *const *phib;      /* [n_phi]: [D][D][3], [D] */
+    int n_down, n_up;                            /* 0: no learned level-0 sampling */
+    const float *const *downW, *const *downB;    /* [n_down]: [D][D][k], [D] */
+    const int *downK;
+    const float *const *upW, *const *upB;        /* [n_up]: [D][D][k] (ConvTranspose1d), [D] */
+    const int *upK;
+    int l1_norm, l1_norm_final;
+    int has_all;                                 /* refine convs (entries may be NULL) */
+    const float *const *drefW, *const *drefB, *const *urefW, *const *urefB;  /* [n_levels] */
+} OrcVq;
+/* idx [B][sum levels] level-major; z_hat / z_rest [B][L][D] may be NULL */
+void orc_vq_z_to_idx(const OrcVq *q, const float *z, int B, int *idx, float *z_hat, float *z_rest);
+/* zhats [n_levels][B][L][D]: z_hat after each level */
+void orc_vq_idx_to_zhats(const OrcVq *q, const int *idx, int B, float *zhats);
+
 /* threads used by the OpenMP loops (0 = runtime default) */
 void orc_set_threads(int n);
 

@@ -45,6 +45,8 @@ def lib():
                                          vp, vp, vp]),
             "orc_argmax_row": (ci, [vp, ci]),
             "orc_sample_topkp": (ci, [vp, ci, ctypes.c_float, ci, ctypes.c_float, ctypes.POINTER(ctypes.c_uint64)]),
+            "orc_vq_z_to_idx": (None, [vp, vp, ci, vp, vp, vp]),
+            "orc_vq_idx_to_zhats": (None, [vp, vp, ci, vp]),
             "orc_gelu": (None, [vp, vp, i64]),
             "orc_gelu_tanh": (None, [vp, vp, i64]),
             "orc_silu": (None, [vp, vp, i64]),
@@ -150,6 +152,107 @@ def sample_topkp(logits, temp, top_k, top_p, rng):
     st = ctypes.c_uint64(rng)
     i = lib().orc_sample_topkp(_ptr(x), x.size, temp, top_k, top_p, ctypes.byref(st))
     return i, st.value
+
+
+class OrcVq(ctypes.Structure):
+    """OrcVq of ncm_oracle.h."""
+    _fields_ = [("n_levels", ci), ("D", ci), ("levels", ctypes.POINTER(ci)), ("vocabs", ctypes.POINTER(ci)),
+                ("E", ctypes.POINTER(vp)), ("n_phi", ci), ("resi_ratio", ctypes.c_float),
+                ("phiW", ctypes.POINTER(vp)), ("phib", ctypes.POINTER(vp)), ("n_down", ci), ("n_up", ci),
+                ("downW", ctypes.POINTER(vp)), ("downB", ctypes.POINTER(vp)), ("downK", ctypes.POINTER(ci)),
+                ("upW", ctypes.POINTER(vp)), ("upB", ctypes.POINTER(vp)), ("upK", ctypes.POINTER(ci)),
+                ("l1_norm", ci), ("l1_norm_final", ci), ("has_all", ci),
+                ("drefW", ctypes.POINTER(vp)), ("drefB", ctypes.POINTER(vp)),
+                ("urefW", ctypes.POINTER(vp)), ("urefB", ctypes.POINTER(vp))]
+
+
+def vq_desc(cfg, weights):
+    """OrcVq for a quantizer given the reference's config fields (cfg: a dict
+    with n_qlevels, levels, vq_vocab, vq_embed_dim, quant_resi_ratio,
+    quant_resi_enabled, quant_resi_share_mode, learned_l1_sampling,
+    learned_l1_norm, learned_l1_norm_final, learned_all_sampling) and its
+    weights by their state-dict names, read as vq_load does (vq.c:76-197).
+    Returns (desc, keepalive)."""
+    keep = []
+
+    def arr(xs, t=vp):
+        a = (t * max(1, len(xs)))(*xs)
+        keep.append(a)
+        return a
+
+    def f(name):
+        a = np.ascontiguousarray(weights[name], np.float32)
+        keep.append(a)
+        return a.ctypes.data
+
+    n = cfg["n_qlevels"]
+    d = OrcVq()
+    d.n_levels, d.D = n, cfg["vq_embed_dim"]
+    d.levels = arr(list(cfg["levels"][:n]), ci)
+    d.vocabs = arr(list(cfg["vq_vocab"][:n]), ci)
+    d.E = arr([f(f"embeddings.{i}.weight") for i in range(n)])
+    if cfg.get("quant_resi_enabled") and abs(cfg.get("quant_resi_ratio", 0.0)) > 1e-6:
+        sm = cfg.get("quant_resi_share_mode", 0)
+        nphi = n if sm == 0 else (1 if sm == 1 else sm)
+        ws, bs = [], []
+        for i in range(nphi):
+            w, b = f"quant_resi.{i}.weight", f"quant_resi.{i}.bias"
+            if w not in weights and nphi == 1:
+                w = "quant_resi.weight"
+            if b not in weights and nphi == 1:
+                b = "quant_resi.bias"
+            ws.append(f(w))
+            bs.append(f(b))
+        d.n_phi, d.resi_ratio = nphi, cfg["quant_resi_ratio"]
+        d.phiW, d.phib = arr(ws), arr(bs)
+    if cfg.get("learned_l1_sampling"):
+        dw, db, dk, uw, ub, uk = [], [], [], [], [], []
+        for s_ in range(16):
+            if f"learned_down_l1.{s_}.weight" in weights:
+                dw.append(f(f"learned_down_l1.{s_}.weight"))
+                db.append(f(f"learned_down_l1.{s_}.bias"))
+                dk.append(int(weights[f"learned_down_l1.{s_}.weight"].shape[2]))
+            if f"learned_up_l1.{s_}.weight" in weights:
+                uw.append(f(f"learned_up_l1.{s_}.weight"))
+                ub.append(f(f"learned_up_l1.{s_}.bias"))
+                uk.append(int(weights[f"learned_up_l1.{s_}.weight"].shape[2]))
+        d.n_down, d.n_up = len(dw), len(uw)
+        d.downW, d.downB, d.downK = arr(dw), arr(db), arr(dk, ci)
+        d.upW, d.upB, d.upK = arr(uw), arr(ub), arr(uk, ci)
+        d.l1_norm, d.l1_norm_final = cfg.get("learned_l1_norm", 0), cfg.get("learned_l1_norm_final", 0)
+    if cfg.get("learned_all_sampling"):
+        d.has_all = 1
+        refs = {k: [None] * n for k in ("dW", "dB", "uW", "uB")}
+        for i in range(1, n - 1):
+            if f"learned_down_refine.{i}.weight" in weights:
+                refs["dW"][i] = f(f"learned_down_refine.{i}.weight")
+                refs["dB"][i] = f(f"learned_down_refine.{i}.bias")
+            if f"learned_up_refine.{i}.weight" in weights:
+                refs["uW"][i] = f(f"learned_up_refine.{i}.weight")
+                refs["uB"][i] = f(f"learned_up_refine.{i}.bias")
+        d.drefW, d.drefB, d.urefW, d.urefB = (arr(refs[k]) for k in ("dW", "dB", "uW", "uB"))
+    return d, keep
+
+
+def vq_z_to_idx(cfg, weights, z, B):
+    """vq_load + vq_z_to_idx (vq.c:76-197, 378-500); returns (idx, z_hat, z_rest)."""
+    d, keep = vq_desc(cfg, weights)
+    n, L, D = cfg["n_qlevels"], cfg["levels"][cfg["n_qlevels"] - 1], cfg["vq_embed_dim"]
+    z = _f32(z)
+    idx = np.zeros((B, sum(cfg["levels"][:n])), np.int32)
+    zh, zr = np.empty((B, L, D), np.float32), np.empty((B, L, D), np.float32)
+    lib().orc_vq_z_to_idx(ctypes.byref(d), _ptr(z), B, _ptr(idx), _ptr(zh), _ptr(zr))
+    return idx, zh, zr
+
+
+def vq_idx_to_zhats(cfg, weights, idx, B):
+    """vq_idx_to_zhats (vq.c:502-552): z_hat after every level, [n_levels][B][L][D]."""
+    d, keep = vq_desc(cfg, weights)
+    n, L, D = cfg["n_qlevels"], cfg["levels"][cfg["n_qlevels"] - 1], cfg["vq_embed_dim"]
+    idx = np.ascontiguousarray(idx, np.int32)
+    out = np.empty((n, B, L, D), np.float32)
+    lib().orc_vq_idx_to_zhats(ctypes.byref(d), _ptr(idx), B, _ptr(out))
+    return out
 
 
 def ref_sample_topkp(logits, temp, top_k, top_p, rng):

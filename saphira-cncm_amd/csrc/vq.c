@@ -164,3 +164,369 @@ void rowwise_l2sq(const float *a, const float *b, float *d2, int64_t rows, int64
     void *args[] = {&a, &b, &d2, &rows, &colsA, &C};
     ncm_launch_named("l2sq_exact", (unsigned)((n + 255) / 256), 1, 1, 256, args);
 }
+
+/* ------------------------------------------------------------------ */
+/* The full multiscale quantizer: vq_load / vq_z_to_idx / vq_idx_to_zhats  */
+/* (vq.c:76-197, 378-552) on device tensors.                              */
+/* ------------------------------------------------------------------ */
+
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define VQ_MAX_STAGES 16
+#define VQF_KMAX 16
+
+struct VQState {
+    int n_levels, D, L, total;
+    int levels[NCM_MAX_LEVELS], vocabs[NCM_MAX_LEVELS];
+    const float *E[NCM_MAX_LEVELS];
+    int n_phi;                       /* 0: Phi off */
+    float resi_ratio;
+    const float *phiW[NCM_MAX_LEVELS], *phib[NCM_MAX_LEVELS];
+    int n_down, n_up;                /* 0: no learned level-0 sampling */
+    const float *downW[VQ_MAX_STAGES], *downB[VQ_MAX_STAGES], *upW[VQ_MAX_STAGES], *upB[VQ_MAX_STAGES];
+    int downK[VQ_MAX_STAGES], upK[VQ_MAX_STAGES];
+    int l1_norm, l1_norm_final;
+    int has_all;
+    const float *drefW[NCM_MAX_LEVELS], *drefB[NCM_MAX_LEVELS], *urefW[NCM_MAX_LEVELS], *urefB[NCM_MAX_LEVELS];
+};
+
+static Tensor *vq_weight(WeightStore *ws, const char *prefix, const char *name) {
+    char key[320];
+    snprintf(key, sizeof key, "%s%s", prefix ? prefix : "", name);
+    return weights_get(ws, key);
+}
+
+/* A conv weight [D][D][k] with its bias [D]; k (out) is the last dimension. */
+static int vq_conv_w(WeightStore *ws, const char *prefix, const char *wn, const char *bn, int D,
+                     const float **W, const float **b, int *k) {
+    Tensor *tw = vq_weight(ws, prefix, wn), *tb = vq_weight(ws, prefix, bn);
+    if (!tw || !tb) return ncm_fail(NCM_E_ARG, "vq_load: missing weight %s%s", prefix ? prefix : "", !tw ? wn : bn);
+    if (tw->ndim != 3 || tw->shape[0] != D || tw->shape[1] != D || tw->shape[2] < 1 || tw->shape[2] > VQF_KMAX ||
+        tb->n != D)
+        return ncm_fail(NCM_E_ARG, "vq_load: %s%s must be [%d][%d][k <= %d] with a [%d] bias", prefix ? prefix : "",
+                        wn, D, D, VQF_KMAX, D);
+    *W = tw->data;
+    *b = tb->data;
+    if (k) *k = (int)tw->shape[2];
+    return 0;
+}
+
+VQState *vq_load(const NCMConfig *c, WeightStore *ws, const char *prefix) {
+    if (!c || !ws) {
+        ncm_fail(NCM_E_ARG, "vq_load: null config or store");
+        return NULL;
+    }
+    const int n = c->n_qlevels, D = c->vq_embed_dim;
+    if (n < 1 || n > NCM_MAX_LEVELS || D < 1 || D > VQ_MAXD) {
+        ncm_fail(NCM_E_ARG, "vq_load: n_qlevels=%d, vq_embed_dim=%d out of range", n, D);
+        return NULL;
+    }
+    VQState *v = (VQState *)calloc(1, sizeof *v);
+    if (!v) {
+        ncm_fail(NCM_E_OOM, "vq_load: state");
+        return NULL;
+    }
+    v->n_levels = n;
+    v->D = D;
+    v->L = c->levels[n - 1];
+    for (int i = 0; i < n; i++) {
+        v->levels[i] = c->levels[i];
+        v->vocabs[i] = c->vq_vocab[i];
+        if (v->levels[i] < 1 || v->levels[i] > v->L || v->vocabs[i] < 1) {
+            ncm_fail(NCM_E_ARG, "vq_load: level %d has length %d (L = %d) and vocab %d", i, v->levels[i], v->L,
+                     v->vocabs[i]);
+            goto fail;
+        }
+        v->total += v->levels[i];
+        char nm[64];
+        snprintf(nm, sizeof nm, "embeddings.%d.weight", i);
+        Tensor *t = vq_weight(ws, prefix, nm);
+        if (!t || t->n != (int64_t)v->vocabs[i] * D) {
+            ncm_fail(NCM_E_ARG, "vq_load: %s%s %s", prefix ? prefix : "", nm, t ? "is not [vocab][D]" : "missing");
+            goto fail;
+        }
+        v->E[i] = t->data;
+    }
+    /* Phi (vq.c:93-126): per level (share mode 0), shared (1) or k partially shared */
+    if (c->quant_resi_enabled && fabsf(c->quant_resi_ratio) > 1e-6f) {
+        const int sm = c->quant_resi_share_mode;
+        v->n_phi = sm == 0 ? n : (sm == 1 ? 1 : sm);
+        if (v->n_phi < 1 || v->n_phi > NCM_MAX_LEVELS) {
+            ncm_fail(NCM_E_ARG, "vq_load: quant_resi_share_mode %d", sm);
+            goto fail;
+        }
+        v->resi_ratio = c->quant_resi_ratio;
+        for (int i = 0; i < v->n_phi; i++) {
+            char wn[64], bn[64];
+            snprintf(wn, sizeof wn, "quant_resi.%d.weight", i);
+            if (!vq_weight(ws, prefix, wn) && v->n_phi == 1) snprintf(wn, sizeof wn, "quant_resi.weight");
+            snprintf(bn, sizeof bn, "quant_resi.%d.bias", i);
+            if (!vq_weight(ws, prefix, bn) && v->n_phi == 1) snprintf(bn, sizeof bn, "quant_resi.bias");
+            int k = 0;
+            if (vq_conv_w(ws, prefix, wn, bn, D, &v->phiW[i], &v->phib[i], &k)) goto fail;
+            if (k != 3) {
+                ncm_fail(NCM_E_ARG, "vq_load: %s has kernel %d, not 3", wn, k);
+                goto fail;
+            }
+        }
+    }
+    /* learned level-0 cascade (vq.c:127-165): convs in module-index order */
+    if (c->learned_l1_sampling) {
+        v->l1_norm = c->learned_l1_norm;
+        v->l1_norm_final = c->learned_l1_norm_final;
+        for (int s = 0; s < VQ_MAX_STAGES; s++) {
+            char wn[64], bn[64];
+            snprintf(wn, sizeof wn, "learned_down_l1.%d.weight", s);
+            snprintf(bn, sizeof bn, "learned_down_l1.%d.bias", s);
+            if (vq_weight(ws, prefix, wn)) {
+                if (vq_conv_w(ws, prefix, wn, bn, D, &v->downW[v->n_down], &v->downB[v->n_down], &v->downK[v->n_down]))
+                    goto fail;
+                v->n_down++;
+            }
+            snprintf(wn, sizeof wn, "learned_up_l1.%d.weight", s);
+            snprintf(bn, sizeof bn, "learned_up_l1.%d.bias", s);
+            if (vq_weight(ws, prefix, wn)) {
+                if (vq_conv_w(ws, prefix, wn, bn, D, &v->upW[v->n_up], &v->upB[v->n_up], &v->upK[v->n_up])) goto fail;
+                v->n_up++;
+            }
+        }
+        if (!v->n_down) {
+            ncm_fail(NCM_E_ARG, "vq_load: learned_l1 weights missing");
+            goto fail;
+        }
+        /* the cascade must map L to levels[0] and back (the reference's buffers assume it) */
+        int Td = v->L, Tu = v->levels[0];
+        for (int i = 0; i < v->n_down; i++) Td /= v->downK[i];
+        for (int i = 0; i < v->n_up; i++) Tu *= v->upK[i];
+        if (Td != v->levels[0] || Tu != v->L || ((c->learned_l1_norm || c->learned_l1_norm_final) && D % 8)) {
+            ncm_fail(NCM_E_ARG, "vq_load: learned level-0 cascade maps %d -> %d -> %d, not L=%d -> %d -> L "
+                                "(or GroupNorm with D %% 8 != 0)", v->L, Td, Tu, v->L, v->levels[0]);
+            goto fail;
+        }
+    }
+    /* refine convs of the middle levels (vq.c:167-185) */
+    if (c->learned_all_sampling) {
+        v->has_all = 1;
+        for (int i = 1; i <= n - 2; i++) {
+            char wn[64], bn[64];
+            int k = 3;
+            snprintf(wn, sizeof wn, "learned_down_refine.%d.weight", i);
+            snprintf(bn, sizeof bn, "learned_down_refine.%d.bias", i);
+            if (vq_weight(ws, prefix, wn) && (vq_conv_w(ws, prefix, wn, bn, D, &v->drefW[i], &v->drefB[i], &k) || k != 3))
+                goto fail_k;
+            snprintf(wn, sizeof wn, "learned_up_refine.%d.weight", i);
+            snprintf(bn, sizeof bn, "learned_up_refine.%d.bias", i);
+            if (vq_weight(ws, prefix, wn) && (vq_conv_w(ws, prefix, wn, bn, D, &v->urefW[i], &v->urefB[i], &k) || k != 3))
+                goto fail_k;
+        }
+    }
+    return v;
+fail_k:
+    ncm_fail(NCM_E_ARG, "vq_load: refine conv of level with a kernel other than 3");
+fail:
+    free(v);
+    return NULL;
+}
+
+void vq_free(VQState *vq) { free(vq); }
+int vq_total_codes(const VQState *vq) { return vq ? vq->total : 0; }
+int vq_nlevels(const VQState *vq) { return vq ? vq->n_levels : 0; }
+int vq_level_len(const VQState *vq, int k) { return vq && k >= 0 && k < vq->n_levels ? vq->levels[k] : 0; }
+int vq_level_V(const VQState *vq, int k) { return vq && k >= 0 && k < vq->n_levels ? vq->vocabs[k] : 0; }
+int vq_Ltotal(const VQState *vq) { return vq ? vq->L : 0; }
+int vq_Ddim(const VQState *vq) { return vq ? vq->D : 0; }
+
+/* ---- device steps ---- */
+
+static unsigned grid256(int64_t n) { return (unsigned)((n + 255) / 256); }
+
+static int vqf_conv(const float *x, const float *W, const float *b, float *y, int B, int T, int D, int K, int stride,
+                    int pad, int transposed, int *To_out) {
+    int To = transposed ? (T - 1) * stride + K : (T + 2 * pad - K) / stride + 1;
+    if (To_out) *To_out = To;
+    void *a[] = {&x, &W, &b, &y, &T, &D, &D, &K, &stride, &pad, &To};
+    return ncm_launch_named(transposed ? "vqf_convT1d" : "vqf_conv1d", (unsigned)((D + 63) / 64),
+                            (unsigned)((To + 3) / 4), (unsigned)B, 256, a);
+}
+
+static int vqf_gn(const float *x, float *y, int B, int T, int D) {
+    void *a[] = {&x, &y, &T, &D};
+    return ncm_launch_named("vqf_groupnorm", (unsigned)B * 8u, 1, 1, 64, a);
+}
+
+static int vqf_mix(float *h, const float *c, int64_t n, float r, int add) {
+    void *a[] = {&h, &c, &n, &r, &add};
+    return ncm_launch_named("vqf_blend", grid256(n), 1, 1, 256, a);
+}
+
+/* Work buffers of one call: z_rest, z_hat, down, up, two cascade/conv
+ * buffers (all [B][L][D]) and the device codes [B][total]. */
+typedef struct {
+    float *zr, *zh, *down, *up, *t1, *t2;
+    int *idx;
+} VqfWs;
+
+static int vqf_ws(const VQState *v, int B, VqfWs *w) {
+    const size_t n = (size_t)B * v->L * v->D * sizeof(float);
+    const size_t a = (n + 255) & ~(size_t)255;
+    char *base = (char *)ncm_workspace(WS_VQF, 6 * a + (size_t)B * v->total * sizeof(int));
+    if (!base) return NCM_E_OOM;
+    w->zr = (float *)base;
+    w->zh = (float *)(base + a);
+    w->down = (float *)(base + 2 * a);
+    w->up = (float *)(base + 3 * a);
+    w->t1 = (float *)(base + 4 * a);
+    w->t2 = (float *)(base + 5 * a);
+    w->idx = (int *)(base + 6 * a);
+    return 0;
+}
+
+/* the learned cascade of level 0 from src [B][T][D] into dst (vq.c:285-309, 336-355) */
+static int vqf_cascade(const VQState *v, const float *src, float *dst, VqfWs *w, int B, int T, int up) {
+    const int D = v->D, n = up ? v->n_up : v->n_down;
+    const float *cur = src;
+    int Tc = T;
+    for (int i = 0; i < n; i++) {
+        const int s = up ? v->upK[i] : v->downK[i];
+        if (v->l1_norm && i > 0) {
+            float *g = cur == w->t1 ? w->t2 : w->t1;
+            if (vqf_gn(cur, g, B, Tc, D)) return -1;
+            cur = g;
+        }
+        float *nx = (i == n - 1 && !v->l1_norm_final) ? dst : (cur == w->t1 ? w->t2 : w->t1);
+        int To;
+        if (vqf_conv(cur, up ? v->upW[i] : v->downW[i], up ? v->upB[i] : v->downB[i], nx, B, Tc, D, s, s, 0, up, &To))
+            return -1;
+        cur = nx;
+        Tc = To;
+    }
+    if (v->l1_norm_final) return vqf_gn(cur, dst, B, Tc, D) ? -1 : 0;
+    if (n == 0) return ncm_copy_async(dst, src, (size_t)B * Tc * D * sizeof(float)) ? -1 : 0;
+    return 0;
+}
+
+/* out += conv3(out) (the refine step) */
+static int vqf_refine(const VQState *v, float *out, const float *W, const float *b, float *tmp, int B, int T) {
+    if (vqf_conv(out, W, b, tmp, B, T, v->D, 3, 1, 1, 0, NULL)) return -1;
+    return vqf_mix(out, tmp, (int64_t)B * T * v->D, 0.0f, 1);
+}
+
+static int phi_slot(const VQState *v, int lv) {
+    if (v->n_phi == 1) return 0;
+    const double at = (double)lv / (v->n_levels - 1);
+    int best = 0;
+    double bd = 1e300;
+    for (int j = 0; j < v->n_phi; j++) {
+        const double tick = v->n_phi == 4 ? (j + 1.0 / 3.0) / v->n_phi : (j + 0.5) / v->n_phi;
+        const double d = fabs(tick - at);
+        if (d < bd) {
+            bd = d;
+            best = j;
+        }
+    }
+    return best;
+}
+
+/* up [B][L][D] <- level lv's codes (device idx) up-sampled, refined and Phi-blended */
+static int vqf_level_up(const VQState *v, const int *idx, int B, int lv, int off, VqfWs *w) {
+    const int D = v->D, L = v->L, tl = v->levels[lv], V = v->vocabs[lv];
+    const int64_t nq = (int64_t)B * tl * D, nL = (int64_t)B * L * D;
+    const float *E = v->E[lv];
+    float *q = w->down;   /* free at this point of a level */
+    void *ga[] = {&E, &idx, (void *)&V, (void *)&v->total, &off, &B, (void *)&tl, (void *)&D, &q};
+    if (ncm_launch_named("vqf_gather", grid256(nq), 1, 1, 256, ga)) return -1;
+    if (lv == 0 && v->n_down > 0) {
+        if (vqf_cascade(v, q, w->up, w, B, tl, 1)) return -1;
+    } else {
+        void *la[] = {&q, &w->up, &B, (void *)&tl, (void *)&L, (void *)&D};
+        if (ncm_launch_named("vqf_linear", grid256(nL), 1, 1, 256, la)) return -1;
+    }
+    if (v->has_all && lv >= 1 && lv <= v->n_levels - 2 && v->urefW[lv] &&
+        vqf_refine(v, w->up, v->urefW[lv], v->urefB[lv], w->t1, B, L))
+        return -1;
+    if (v->n_phi > 0) {
+        const int j = phi_slot(v, lv);
+        if (vqf_conv(w->up, v->phiW[j], v->phib[j], w->t1, B, L, D, 3, 1, 1, 0, NULL)) return -1;
+        if (vqf_mix(w->up, w->t1, nL, v->resi_ratio, 0)) return -1;
+    }
+    return 0;
+}
+
+static int vqf_check(const VQState *vq, const float *z, int B, const char *fn) {
+    if (!vq || !z || B < 0) return ncm_fail(NCM_E_ARG, "%s: bad arguments", fn);
+    if ((int64_t)B * vq->L > INT_MAX / 2 || (int64_t)B * vq->total > INT_MAX)
+        return ncm_fail(NCM_E_ARG, "%s: B=%d too large", fn, B);
+    return ncm_ready();
+}
+
+void vq_z_to_idx_dev(VQState *vq, const float *z, int B, int *idx, float *z_hat, float *z_rest) {
+    if (vqf_check(vq, z, B, "vq_z_to_idx_dev") || B == 0) return;
+    if (!idx) {
+        ncm_fail(NCM_E_ARG, "vq_z_to_idx_dev: null idx");
+        return;
+    }
+    VqfWs w;
+    if (vqf_ws(vq, B, &w)) return;
+    const int D = vq->D, L = vq->L;
+    const int64_t nL = (int64_t)B * L * D;
+    if (ncm_copy_async(w.zr, z, (size_t)nL * sizeof(float))) return;
+    int off = 0;
+    for (int lv = 0; lv < vq->n_levels; lv++) {
+        const int tl = vq->levels[lv];
+        /* down-sample z_rest to this level (vq.c:280-330) */
+        if (lv == 0 && vq->n_down > 0) {
+            if (vqf_cascade(vq, w.zr, w.down, &w, B, L, 0)) return;
+        } else {
+            void *aa[] = {&w.zr, &w.down, &B, (void *)&L, (void *)&tl, (void *)&D};
+            if (ncm_launch_named("vqf_area", grid256((int64_t)B * tl * D), 1, 1, 256, aa)) return;
+        }
+        if (vq->has_all && lv >= 1 && lv <= vq->n_levels - 2 && vq->drefW[lv] &&
+            vqf_refine(vq, w.down, vq->drefW[lv], vq->drefB[lv], w.t1, B, tl))
+            return;
+        if (vq_search(w.down, vq->E[lv], idx, B * tl, vq->vocabs[lv], D, tl, vq->total, off)) return;
+        if (vqf_level_up(vq, idx, B, lv, off, &w)) return;
+        int init = lv == 0;
+        void *ua[] = {&w.zh, &w.zr, &w.up, (void *)&nL, &init};
+        if (ncm_launch_named("vqf_update", grid256(nL), 1, 1, 256, ua)) return;
+        off += tl;
+    }
+    if (z_hat && ncm_copy_async(z_hat, w.zh, (size_t)nL * sizeof(float))) return;
+    if (z_rest) ncm_copy_async(z_rest, w.zr, (size_t)nL * sizeof(float));
+}
+
+void vq_z_to_idx(VQState *vq, const float *z, int B, int *idx) {
+    if (vqf_check(vq, z, B, "vq_z_to_idx") || B == 0) return;
+    if (!idx) {
+        ncm_fail(NCM_E_ARG, "vq_z_to_idx: null idx");
+        return;
+    }
+    VqfWs w;
+    if (vqf_ws(vq, B, &w)) return;
+    vq_z_to_idx_dev(vq, z, B, w.idx, NULL, NULL);
+    mem_d2h(idx, w.idx, (size_t)B * vq->total * sizeof(int));
+}
+
+void vq_idx_to_zhats(VQState *vq, const int *idx, int B, float **zhats) {
+    if (!vq || !idx || !zhats || B < 0) {
+        ncm_fail(NCM_E_ARG, "vq_idx_to_zhats: bad arguments");
+        return;
+    }
+    if (B == 0 || vqf_check(vq, zhats[0], B, "vq_idx_to_zhats")) return;
+    VqfWs w;
+    if (vqf_ws(vq, B, &w)) return;
+    mem_h2d(w.idx, idx, (size_t)B * vq->total * sizeof(int));
+    const int64_t nL = (int64_t)B * vq->L * vq->D;
+    float *none = NULL;
+    int base = 0;
+    for (int lv = 0; lv < vq->n_levels; lv++) {
+        if (vqf_level_up(vq, w.idx, B, lv, base, &w)) return;
+        int init = lv == 0;
+        void *ua[] = {&w.zh, &none, &w.up, (void *)&nL, &init};
+        if (ncm_launch_named("vqf_update", grid256(nL), 1, 1, 256, ua)) return;
+        if (zhats[lv] && ncm_copy_async(zhats[lv], w.zh, (size_t)nL * sizeof(float))) return;
+        base += vq->levels[lv];
+    }
+}

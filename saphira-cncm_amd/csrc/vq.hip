@@ -526,3 +526,183 @@ vq_residual(const float *__restrict__ E, const int *__restrict__ idx, int rows, 
     z_hat[i] = h + q;
     z_rest[i] = z_rest[i] - q;
 }
+
+// ---------------------------------------------------------------- the full quantizer
+// Resampling, convolutions and blends of src/vq.c's general multiscale path
+// (per-level lengths, Phi, the learned level-0 cascade, refine convs), on
+// [B][T][D] tensors (the reference's BLD layout) with the reference's
+// arithmetic: fp64 accumulators in its loop orders, separate multiply and
+// add roundings (no contraction), float results.  Bit-exact with the CPU.
+
+// kernels.c:681-700 area interpolation, one thread per output (b, t, d)
+extern "C" __global__ void __launch_bounds__(256)
+vqf_area(const float *__restrict__ x, float *__restrict__ y, int B, int Tin, int Tout, int D) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)B * Tout * D) return;
+    const int d = (int)(i % D), t = (int)((i / D) % Tout), b = (int)(i / ((int64_t)D * Tout));
+    int64_t s = (int64_t)((double)t * Tin / Tout);
+    int64_t e = (int64_t)ceil((double)(t + 1) * Tin / Tout);
+    if (e <= s) e = s + 1;
+    if (s < 0) s = 0;
+    if (e > Tin) e = Tin;
+    double acc = 0.0;
+    for (int64_t k = s; k < e; ++k) acc += (double)x[((int64_t)b * Tin + k) * D + d];
+    y[i] = (float)(acc / (double)(e - s));
+}
+
+// kernels.c:702-727 linear interpolation (align_corners = False; a length-1
+// side averages), one thread per output
+extern "C" __global__ void __launch_bounds__(256)
+vqf_linear(const float *__restrict__ x, float *__restrict__ y, int B, int Tin, int Tout, int D) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)B * Tout * D) return;
+    const int d = (int)(i % D), t = (int)((i / D) % Tout), b = (int)(i / ((int64_t)D * Tout));
+    const float *xc = x + (int64_t)b * Tin * D + d;
+    if (Tout == 1 || Tin == 1) {
+        double acc = 0.0;
+        for (int k = 0; k < Tin; ++k) acc += (double)xc[(int64_t)k * D];
+        y[i] = (float)(acc / Tin);
+        return;
+    }
+    const double scale = (double)Tin / Tout;
+    const double src = (t + 0.5) * scale - 0.5;
+    const int64_t s0 = (int64_t)floor(src), s1 = s0 + 1;
+    const double w1 = src - (double)s0, w0 = 1.0 - w1;
+    const double v0 = xc[(s0 < 0 ? 0 : (s0 >= Tin ? Tin - 1 : s0)) * (int64_t)D];
+    const double v1 = xc[(s1 < 0 ? 0 : (s1 >= Tin ? Tin - 1 : s1)) * (int64_t)D];
+    y[i] = (float)(w0 * v0 + w1 * v1);
+}
+
+// conv1d (kernels.c:546-566; W [Cout][Cin][K]) or, with TR, ConvTranspose1d
+// (kernels.c:568-590; W [Cin][Cout][K]) over x [B][T][Cin] into y [B][To][Cout]:
+//   y = (float)(bias + sum over ci (outer), k (inner) of (double) x * W)
+// A workgroup computes 64 output channels x 4 positions of one b; the
+// weights of 8 input channels at a time are staged in LDS as [ci][k][co]
+// (lanes read consecutive co); a wave's 64 lanes share one position, so its
+// x reads are one address.  Each thread keeps its own fp64 chain in the
+// reference's order.  K <= VQF_KMAX.
+#define VQF_KMAX 16
+#define VQF_CIT 8
+template <bool TR>
+__device__ __forceinline__ void vqf_conv_body(const float *__restrict__ x, const float *__restrict__ W,
+                                              const float *__restrict__ bias, float *__restrict__ y, int T,
+                                              int Cin, int Cout, int K, int stride, int pad, int To) {
+#pragma clang fp contract(off)
+    __shared__ float ws[VQF_CIT * VQF_KMAX * 64];
+    const int tid = threadIdx.x, col = tid & 63, tl = tid >> 6;
+    const int co0 = blockIdx.x * 64, t = blockIdx.y * 4 + tl, b = blockIdx.z;
+    const int co = co0 + col;
+    double acc = (bias && co < Cout) ? (double)bias[co] : 0.0;
+    const float *xb = x + (int64_t)b * T * Cin;
+    for (int ci0 = 0; ci0 < Cin; ci0 += VQF_CIT) {
+        const int nci = min(VQF_CIT, Cin - ci0), n = nci * K * 64;
+        __syncthreads();
+        for (int e = tid; e < n; e += 256) {
+            const int c = e & 63, r = e >> 6, ci = r / K, k = r - ci * K;
+            float v = 0.f;
+            if (co0 + c < Cout)
+                v = TR ? W[((int64_t)(ci0 + ci) * Cout + co0 + c) * K + k] : W[((int64_t)(co0 + c) * Cin + ci0 + ci) * K + k];
+            ws[(ci * K + k) * 64 + c] = v;
+        }
+        __syncthreads();
+        if (t < To) {
+            for (int ci = 0; ci < nci; ++ci)
+                for (int k = 0; k < K; ++k) {
+                    int ti;
+                    if (TR) {
+                        const int num = t - k;
+                        if (num < 0 || num % stride != 0) continue;
+                        ti = num / stride;
+                        if (ti >= T) continue;
+                    } else {
+                        ti = t * stride + k - pad;
+                        if (ti < 0 || ti >= T) continue;
+                    }
+                    acc += (double)xb[(int64_t)ti * Cin + ci0 + ci] * (double)ws[(ci * K + k) * 64 + col];
+                }
+        }
+    }
+    if (t < To && co < Cout) y[((int64_t)b * To + t) * Cout + co] = (float)acc;
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+vqf_conv1d(const float *x, const float *W, const float *bias, float *y, int T, int Cin, int Cout, int K, int stride,
+           int pad, int To) {
+    vqf_conv_body<false>(x, W, bias, y, T, Cin, Cout, K, stride, pad, To);
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+vqf_convT1d(const float *x, const float *W, const float *bias, float *y, int T, int Cin, int Cout, int K, int stride,
+            int pad, int To) {
+    vqf_conv_body<true>(x, W, bias, y, T, Cin, Cout, K, stride, pad, To);
+}
+
+// kernels.c:618-640 GroupNorm (8 groups, no affine, eps 1e-5) of x [B][T][C]:
+// one workgroup per (b, g); the fp64 mean and variance run serially in the
+// reference's order (channel outer, position inner), then all threads
+// normalise.
+extern "C" __global__ void __launch_bounds__(64)
+vqf_groupnorm(const float *__restrict__ x, float *__restrict__ y, int T, int C) {
+#pragma clang fp contract(off)
+    __shared__ double st[2];
+    const int b = blockIdx.x >> 3, g = blockIdx.x & 7, Cg = C / 8;
+    const float *xb = x + (int64_t)b * T * C + g * Cg;
+    if (threadIdx.x == 0) {
+        const int64_t cnt = (int64_t)Cg * T;
+        double mean = 0.0;
+        for (int c = 0; c < Cg; ++c)
+            for (int t = 0; t < T; ++t) mean += (double)xb[(int64_t)t * C + c];
+        mean /= (double)cnt;
+        double var = 0.0;
+        for (int c = 0; c < Cg; ++c)
+            for (int t = 0; t < T; ++t) {
+                const double d = (double)xb[(int64_t)t * C + c] - mean;
+                var += d * d;
+            }
+        var /= (double)cnt;
+        st[0] = mean;
+        st[1] = 1.0 / sqrt(var + 1e-5);
+    }
+    __syncthreads();
+    const double mean = st[0], inv = st[1];
+    float *yb = y + (int64_t)b * T * C + g * Cg;
+    for (int e = threadIdx.x; e < Cg * T; e += 64) {
+        const int c = e % Cg, t = e / Cg;
+        yb[(int64_t)t * C + c] = (float)(((double)xb[(int64_t)t * C + c] - mean) * inv);
+    }
+}
+
+// vq.c:243-277 Phi blend h = (1 - r) h + r c (float); r == 0 adds: h += c
+// (the refine step, vq.c:320-330)
+extern "C" __global__ void __launch_bounds__(256)
+vqf_blend(float *__restrict__ h, const float *__restrict__ c, int64_t n, float r, int add) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    h[i] = add ? h[i] + c[i] : (1.0f - r) * h[i] + r * c[i];
+}
+
+// q [B][tl][D] = codebook rows of level codes idx[b * total + off + t]
+extern "C" __global__ void __launch_bounds__(256)
+vqf_gather(const float *__restrict__ E, const int *__restrict__ idx, int V, int total, int off, int B, int tl, int D,
+           float *__restrict__ q) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)B * tl * D) return;
+    const int d = (int)(i % D), r = (int)(i / D), b = r / tl, t = r - b * tl;
+    int code = idx[(int64_t)b * total + off + t];
+    if ((unsigned)code >= (unsigned)V) code = 0;
+    q[i] = E[(int64_t)code * D + d];
+}
+
+// z_hat += up, z_rest -= up (vq.c:476-498); init: z_hat = 0 + up (the
+// reference clears z_hat, then adds)
+extern "C" __global__ void __launch_bounds__(256)
+vqf_update(float *__restrict__ zh, float *__restrict__ zr, const float *__restrict__ up, int64_t n, int init) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float u = up[i];
+    zh[i] = (init ? 0.0f : zh[i]) + u;
+    if (zr) zr[i] = zr[i] - u;
+}

@@ -144,6 +144,17 @@ _SIGS = {
     "sample_topkp": (ci, [vp, ci, ctypes.c_float, ci, ctypes.c_float, ctypes.POINTER(ctypes.c_uint64)]),
     "ncm_hip_sample_flag": (ci, []),
     "sample_topkp_dev": (None, [vp, ci, ctypes.c_float, ci, ctypes.c_float, vp, vp, vp]),
+    "vq_load": (vp, [vp, vp, ctypes.c_char_p]),
+    "vq_free": (None, [vp]),
+    "vq_total_codes": (ci, [vp]),
+    "vq_nlevels": (ci, [vp]),
+    "vq_level_len": (ci, [vp, ci]),
+    "vq_level_V": (ci, [vp, ci]),
+    "vq_Ltotal": (ci, [vp]),
+    "vq_Ddim": (ci, [vp]),
+    "vq_z_to_idx": (None, [vp, vp, ci, vp]),
+    "vq_z_to_idx_dev": (None, [vp, vp, ci, vp, vp, vp]),
+    "vq_idx_to_zhats": (None, [vp, vp, ci, ctypes.POINTER(vp)]),
 }
 
 # On-disk formats, the AdamW object and NCK1 checkpoints: the reference's
@@ -182,7 +193,7 @@ def header_functions(path=HEADER):
     """Names of the functions include/ncm_hip.h declares."""
     text = open(path).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    names = re.findall(r"^[A-Za-z_][\w \*]*?\b([a-z_][a-z0-9_]*)\s*\(", text, flags=re.M)
+    names = re.findall(r"^[A-Za-z_][\w \*]*?\b([a-z_][A-Za-z0-9_]*)\s*\(", text, flags=re.M)
     return sorted(set(n for n in names if n not in ("defined",)))
 
 

@@ -1,0 +1,100 @@
+"""The full multiscale quantizer on the device (vq_load + vq_z_to_idx +
+vq_idx_to_zhats over device tensors) against the oracle restatement of
+src/vq.c, which is pinned to the reference's own functions: codes, z_hat,
+z_rest and every level's z_hat bit for bit."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import ncmhip
+import oracle as O
+from conftest import bits_equal
+from vqfull_cases import CASES, make_case, ncm_config, weight_store
+
+pytestmark = pytest.mark.gpu
+D_ = ncmhip.DeviceBuffer
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    ncmhip.init(0)
+    print("[gpu] full quantizer tests on device 0", flush=True)
+
+
+class DevVq:
+    """vq_load over a WeightStore of device tensors built here."""
+
+    def __init__(self, cfg, w):
+        self.lib = ncmhip.load()
+        self.bufs, tens = [], []
+        for k, a in w.items():
+            b = D_.from_numpy(np.ascontiguousarray(a, np.float32))
+            t = ncmhip.TensorS()
+            t.data = b.ptr
+            for i, s in enumerate(a.shape):
+                t.shape[i] = s
+            t.ndim, t.n = a.ndim, a.size
+            self.bufs.append(b)
+            tens.append((k, t))
+        self.tens = tens
+        self.ws, self.items = weight_store(tens)
+        self.cfg = ncm_config(cfg)
+        self.vq = self.lib.vq_load(ctypes.byref(self.cfg), ctypes.byref(self.ws), b"")
+        ncmhip.check()
+        n = cfg["n_qlevels"]
+        self.n, self.L, self.D, self.total = n, cfg["levels"][n - 1], cfg["vq_embed_dim"], sum(cfg["levels"][:n])
+
+    def z_to_idx(self, z, B):
+        zd = D_.from_numpy(z)
+        idx = D_.empty((B, self.total), np.int32)
+        zh, zr = D_.empty((B, self.L, self.D)), D_.empty((B, self.L, self.D))
+        self.lib.vq_z_to_idx_dev(self.vq, zd.ptr, B, idx.ptr, zh.ptr, zr.ptr)
+        ncmhip.check()
+        host = np.zeros((B, self.total), np.int32)
+        self.lib.vq_z_to_idx(self.vq, zd.ptr, B, host.ctypes.data)   # the drop-in: host codes
+        ncmhip.check()
+        return idx.numpy(), zh.numpy(), zr.numpy(), host
+
+    def zhats(self, idx, B):
+        outs = [D_.empty((B, self.L, self.D)) for _ in range(self.n)]
+        ptrs = (ctypes.c_void_p * self.n)(*[o.ptr for o in outs])
+        idx = np.ascontiguousarray(idx, np.int32)
+        self.lib.vq_idx_to_zhats(self.vq, idx.ctypes.data, B, ptrs)
+        ncmhip.check()
+        return np.stack([o.numpy() for o in outs])
+
+    def close(self):
+        self.lib.vq_free(self.vq)
+
+
+@pytest.mark.parametrize("name,kw", CASES, ids=[c[0] for c in CASES])
+def test_matches_oracle(name, kw):
+    cfg, w, z = make_case(7, **kw)
+    B = kw["B"]
+    print(f"[gpu] vqfull case {name}", flush=True)
+    want_idx, want_zh, want_zr = O.vq_z_to_idx(cfg, w, z, B)
+    q = DevVq(cfg, w)
+    try:
+        assert q.lib.vq_total_codes(q.vq) == q.total and q.lib.vq_Ltotal(q.vq) == q.L
+        assert q.lib.vq_nlevels(q.vq) == q.n and q.lib.vq_Ddim(q.vq) == q.D
+        idx, zh, zr, host = q.z_to_idx(z, B)
+        assert np.array_equal(idx, want_idx) and np.array_equal(host, want_idx)
+        assert bits_equal(zh, want_zh) and bits_equal(zr, want_zr)
+        assert bits_equal(q.zhats(idx, B), O.vq_idx_to_zhats(cfg, w, idx, B))
+    finally:
+        q.close()
+
+
+def test_larger_case_with_phi():
+    # 8192 rows of D = 256, five levels 1..16, 1024 codes, partially shared Phi
+    cfg, w, z = make_case(11, B=512, levels=[1, 2, 4, 8, 16], V=1024, D=256, phi=4, ratio=0.5)
+    print("[gpu] vqfull larger case", flush=True)
+    want_idx, want_zh, want_zr = O.vq_z_to_idx(cfg, w, z, 512)
+    q = DevVq(cfg, w)
+    try:
+        idx, zh, zr, host = q.z_to_idx(z, 512)
+        assert np.array_equal(idx, want_idx)
+        assert bits_equal(zh, want_zh) and bits_equal(zr, want_zr)
+    finally:
+        q.close()

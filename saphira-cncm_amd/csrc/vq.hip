@@ -578,65 +578,230 @@ vqf_linear(const float *__restrict__ x, float *__restrict__ y, int B, int Tin, i
 // conv1d (kernels.c:546-566; W [Cout][Cin][K]) or, with TR, ConvTranspose1d
 // (kernels.c:568-590; W [Cin][Cout][K]) over x [B][T][Cin] into y [B][To][Cout]:
 //   y = (float)(bias + sum over ci (outer), k (inner) of (double) x * W)
-// A workgroup computes 64 output channels x 4 positions of one b; the
-// weights of 8 input channels at a time are staged in LDS as [ci][k][co]
-// (lanes read consecutive co); a wave's 64 lanes share one position, so its
-// x reads are one address.  Each thread keeps its own fp64 chain in the
-// reference's order.  K <= VQF_KMAX.
+// A workgroup computes 64 output channels x 16 positions of one b; thread
+// (co, g) carries the 4 positions 16 t0 + 4 g + j as 4 independent fp64
+// chains, each in the reference's order.  Per chunk of input channels the
+// weights are staged in LDS as [ci][k][co] (lanes read consecutive co) and
+// the input window of the 16 positions as doubles [pos][ci] (a wave's lanes
+// read one address).
+//
+// conv1d skips no term inside the loop: the window covers every position
+// the taps touch, with +0.0 outside [0, T), so a tap the reference skips
+// adds a signed zero.  Adding +-0 leaves a non-zero chain unchanged, and a
+// zero chain can only change sign, which every later non-zero term undoes;
+// so a result can differ from the reference's only when the final chain is
+// exactly zero -- those few outputs are recomputed with the reference's
+// skips (vqf_conv_exact).
 #define VQF_KMAX 16
-#define VQF_CIT 8
-template <bool TR>
+#define VQF_WP 65      // LDS row pitch of the staged weights (odd: conflict-free transposing stores)
+#define VQF_WS (128 * VQF_WP)
+#define VQF_XS 2048
+
+__device__ double vqf_conv_exact(const float *__restrict__ xb, const float *__restrict__ W, const float *__restrict__ bias,
+                                 int T, int Cin, int co, int K, int stride, int pad, int t) {
+#pragma clang fp contract(off)
+    double acc = bias ? (double)bias[co] : 0.0;
+    for (int ci = 0; ci < Cin; ++ci)
+        for (int k = 0; k < K; ++k) {
+            const int ti = t * stride + k - pad;
+            if (ti < 0 || ti >= T) continue;
+            acc += (double)xb[(int64_t)ti * Cin + ci] * (double)W[((int64_t)co * Cin + ci) * K + k];
+        }
+    return acc;
+}
+
+template <bool TR, int KC, bool S1K3>
 __device__ __forceinline__ void vqf_conv_body(const float *__restrict__ x, const float *__restrict__ W,
                                               const float *__restrict__ bias, float *__restrict__ y, int T,
-                                              int Cin, int Cout, int K, int stride, int pad, int To) {
+                                              int Cin, int Cout, int Krt, int stride, int pad, int To) {
 #pragma clang fp contract(off)
-    __shared__ float ws[VQF_CIT * VQF_KMAX * 64];
-    const int tid = threadIdx.x, col = tid & 63, tl = tid >> 6;
-    const int co0 = blockIdx.x * 64, t = blockIdx.y * 4 + tl, b = blockIdx.z;
+    __shared__ float ws[VQF_WS];
+    __shared__ double xs[VQF_XS];
+    const int K = KC > 0 ? KC : Krt;
+    const int tid = threadIdx.x, col = tid & 63, g = tid >> 6;
+    const int co0 = blockIdx.x * 64, t0 = blockIdx.y * 16, b = blockIdx.z;
     const int co = co0 + col;
-    double acc = (bias && co < Cout) ? (double)bias[co] : 0.0;
+    // input positions the 16 outputs read: [plo, phi] (conv1d: unclamped, padded with zeros)
+    int plo, phi;
+    if (TR) {
+        plo = max(t0 - (K - 1) > 0 ? (t0 - (K - 1)) / stride : 0, 0);
+        phi = min((t0 + 15) / stride, T - 1);
+    } else {
+        plo = t0 * stride - pad;
+        phi = (t0 + 15) * stride + K - 1 - pad;
+    }
+    const int npos = max(phi - plo + 1, 0);
+    const int cit = max(1, min(min(32, VQF_WS / (VQF_WP * K)), VQF_XS / max(npos, 1)));
+    double acc[4];
+    const double b0 = (bias && co < Cout) ? (double)bias[co] : 0.0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = b0;
     const float *xb = x + (int64_t)b * T * Cin;
-    for (int ci0 = 0; ci0 < Cin; ci0 += VQF_CIT) {
-        const int nci = min(VQF_CIT, Cin - ci0), n = nci * K * 64;
+    for (int ci0 = 0; ci0 < Cin; ci0 += cit) {
+        const int nci = min(cit, Cin - ci0);
         __syncthreads();
-        for (int e = tid; e < n; e += 256) {
-            const int c = e & 63, r = e >> 6, ci = r / K, k = r - ci * K;
-            float v = 0.f;
-            if (co0 + c < Cout)
-                v = TR ? W[((int64_t)(ci0 + ci) * Cout + co0 + c) * K + k] : W[((int64_t)(co0 + c) * Cin + ci0 + ci) * K + k];
-            ws[(ci * K + k) * 64 + c] = v;
+        if (TR) {   // W [Cin][Cout][K]: a chunk row (ci, k) runs over co with stride K
+            for (int r = g; r < nci * K; r += 4) {
+                const int ci = r / K, k = r - ci * K;
+                ws[r * VQF_WP + col] = co < Cout ? W[((int64_t)(ci0 + ci) * Cout + co) * K + k] : 0.f;
+            }
+        } else {    // W [Cout][Cin][K]: each channel's chunk is nci K contiguous floats; read them in order
+            const int run = nci * K;
+            for (int e = tid; e < 64 * run; e += 256) {
+                const int c = e / run, r = e - c * run;
+                ws[r * VQF_WP + c] = co0 + c < Cout ? W[((int64_t)(co0 + c) * Cin + ci0) * K + r] : 0.f;
+            }
+        }
+        if (S1K3) {   // window as [ci][pos]: a wave's taps of one channel are 6 consecutive doubles
+            for (int e = tid; e < npos * nci; e += 256) {
+                const int p = e / nci, ci = e - p * nci, pos = plo + p;
+                xs[ci * npos + p] = (pos >= 0 && pos < T) ? (double)xb[(int64_t)pos * Cin + ci0 + ci] : 0.0;
+            }
+        } else {
+            for (int e = tid; e < npos * nci; e += 256) {
+                const int p = e / nci, ci = e - p * nci, pos = plo + p;
+                xs[e] = (pos >= 0 && pos < T) ? (double)xb[(int64_t)pos * Cin + ci0 + ci] : 0.0;
+            }
         }
         __syncthreads();
-        if (t < To) {
+        if (S1K3) {
+            // output 4 g + j, tap k reads window position 4 g + j + k
+            for (int ci = 0; ci < nci; ++ci) {
+                const double *xp = xs + ci * npos + 4 * g;
+                double xv[6];
+#pragma unroll
+                for (int q = 0; q < 6; ++q) xv[q] = xp[q];
+                const float *wp = ws + ci * 3 * VQF_WP + col;
+#pragma unroll
+                for (int k = 0; k < 3; ++k) {
+                    const double w = (double)wp[k * VQF_WP];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[j] += xv[j + k] * w;
+                }
+            }
+        } else if (TR) {
             for (int ci = 0; ci < nci; ++ci)
                 for (int k = 0; k < K; ++k) {
-                    int ti;
-                    if (TR) {
-                        const int num = t - k;
-                        if (num < 0 || num % stride != 0) continue;
-                        ti = num / stride;
-                        if (ti >= T) continue;
-                    } else {
-                        ti = t * stride + k - pad;
-                        if (ti < 0 || ti >= T) continue;
+                    const double w = (double)ws[(ci * K + k) * VQF_WP + col];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int t = t0 + 4 * g + j, num = t - k;
+                        const int ti = num / stride;
+                        if (t < To && num >= 0 && num % stride == 0 && ti < T)
+                            acc[j] += xs[(ti - plo) * nci + ci] * w;
                     }
-                    acc += (double)xb[(int64_t)ti * Cin + ci0 + ci] * (double)ws[(ci * K + k) * 64 + col];
                 }
+        } else {
+            // output 4 g + j, tap k reads window position (4 g + j) stride + k
+            const double *xc = xs + 4 * g * stride * nci;
+            for (int ci = 0; ci < nci; ++ci) {
+#pragma unroll
+                for (int k = 0; k < K; ++k) {
+                    const double w = (double)ws[(ci * K + k) * VQF_WP + col];
+                    double xv[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) xv[j] = xc[(j * stride + k) * nci + ci];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[j] += xv[j] * w;
+                }
+            }
         }
     }
-    if (t < To && co < Cout) y[((int64_t)b * To + t) * Cout + co] = (float)acc;
+    if (co < Cout) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int t = t0 + 4 * g + j;
+            if (t >= To) continue;
+            double v = acc[j];
+            if (!TR && v == 0.0) v = vqf_conv_exact(xb, W, bias, T, Cin, co, K, stride, pad, t);
+            y[((int64_t)b * To + t) * Cout + co] = (float)v;
+        }
+    }
+}
+
+// conv1d with kernel 3, stride 1, padding 1 and Cin % 32 == 0 (Phi and the
+// refine convs): the layout and arithmetic of vqf_conv_body's S1K3 path, with
+// the LDS sized to what it uses (5 workgroups per CU instead of 3) and
+// division-free staging: a thread copies one contiguous 24-float run of one
+// channel's weights; window entries map to threads by bits.
+__device__ __forceinline__ void vqf_conv3_body(const float *__restrict__ x, const float *__restrict__ W,
+                                               const float *__restrict__ bias, float *__restrict__ y, int T,
+                                               int Cin, int Cout, int To) {
+#pragma clang fp contract(off)
+    __shared__ float ws[96 * VQF_WP];     // [ci * 3 + k][co], 32 input channels
+    __shared__ double xs[32 * 18];        // [ci][pos], 18 window positions
+    const int tid = threadIdx.x, col = tid & 63, g = tid >> 6;
+    const int co0 = blockIdx.x * 64, t0 = blockIdx.y * 16, b = blockIdx.z;
+    const int co = co0 + col, plo = t0 - 1;
+    double acc[4];
+    const double b0 = (bias && co < Cout) ? (double)bias[co] : 0.0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = b0;
+    const float *xb = x + (int64_t)b * T * Cin;
+    const float *wrow = W + (int64_t)min(co, Cout - 1) * Cin * 3;   // this lane's channel (clamped; unused lanes write 0)
+    for (int ci0 = 0; ci0 < Cin; ci0 += 32) {
+        __syncthreads();
+        {   // weights: lane col, rows 24 g .. 24 g + 23 of the chunk (one contiguous run)
+            const float *src = wrow + ci0 * 3 + 24 * g;
+#pragma unroll
+            for (int i = 0; i < 24; ++i) ws[(24 * g + i) * VQF_WP + col] = co < Cout ? src[i] : 0.f;
+        }
+        {   // window: channel tid & 31, positions (tid >> 5) + 8 i
+            const int ci = tid & 31;
+#pragma unroll
+            for (int i = 0; i < 3; ++i) {
+                const int p = (tid >> 5) + 8 * i;
+                if (p < 18) {
+                    const int pos = plo + p;
+                    xs[ci * 18 + p] = (pos >= 0 && pos < T) ? (double)xb[(int64_t)pos * Cin + ci0 + ci] : 0.0;
+                }
+            }
+        }
+        __syncthreads();
+#pragma unroll 2
+        for (int ci = 0; ci < 32; ++ci) {
+            const double *xp = xs + ci * 18 + 4 * g;
+            double xv[6];
+#pragma unroll
+            for (int q = 0; q < 6; ++q) xv[q] = xp[q];
+            const float *wp = ws + ci * 3 * VQF_WP + col;
+#pragma unroll
+            for (int k = 0; k < 3; ++k) {
+                const double w = (double)wp[k * VQF_WP];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[j] += xv[j + k] * w;
+            }
+        }
+    }
+    if (co < Cout) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int t = t0 + 4 * g + j;
+            if (t >= To) continue;
+            double v = acc[j];
+            if (v == 0.0) v = vqf_conv_exact(xb, W, bias, T, Cin, co, 3, 1, 1, t);
+            y[((int64_t)b * To + t) * Cout + co] = (float)v;
+        }
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+vqf_conv3(const float *x, const float *W, const float *bias, float *y, int T, int Cin, int Cout, int K, int stride,
+          int pad, int To) {
+    vqf_conv3_body(x, W, bias, y, T, Cin, Cout, To);
 }
 
 extern "C" __global__ void __launch_bounds__(256)
 vqf_conv1d(const float *x, const float *W, const float *bias, float *y, int T, int Cin, int Cout, int K, int stride,
            int pad, int To) {
-    vqf_conv_body<false>(x, W, bias, y, T, Cin, Cout, K, stride, pad, To);
+    if (K == 3 && stride == 1) vqf_conv_body<false, 3, true>(x, W, bias, y, T, Cin, Cout, K, stride, pad, To);
+    else vqf_conv_body<false, 0, false>(x, W, bias, y, T, Cin, Cout, K, stride, pad, To);
 }
 
 extern "C" __global__ void __launch_bounds__(256)
 vqf_convT1d(const float *x, const float *W, const float *bias, float *y, int T, int Cin, int Cout, int K, int stride,
             int pad, int To) {
-    vqf_conv_body<true>(x, W, bias, y, T, Cin, Cout, K, stride, pad, To);
+    vqf_conv_body<true, 0, false>(x, W, bias, y, T, Cin, Cout, K, stride, pad, To);
 }
 
 // kernels.c:618-640 GroupNorm (8 groups, no affine, eps 1e-5) of x [B][T][C]:

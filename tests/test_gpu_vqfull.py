@@ -98,3 +98,25 @@ def test_larger_case_with_phi():
         assert bits_equal(zh, want_zh) and bits_equal(zr, want_zr)
     finally:
         q.close()
+
+
+def test_zero_sequences_and_negative_zero_bias():
+    """All-zero sequences through convs whose biases hold -0.0: a conv output
+    that ends exactly at zero keeps the reference's sign (the kernel's
+    fallback path for chains ending at +-0)."""
+    cfg, w, z = make_case(13, B=3, levels=[1, 2, 4, 8, 16], V=32, D=32, phi=1, ratio=0.5, refine=(2,))
+    z[1] = 0.0
+    for name in ("quant_resi.0.bias", "learned_down_refine.2.bias", "learned_up_refine.2.bias"):
+        b = w[name].copy()
+        b[::3] = -0.0
+        b[1::3] = 0.0
+        w[name] = b
+    want_idx, want_zh, want_zr = O.vq_z_to_idx(cfg, w, z, 3)
+    q = DevVq(cfg, w)
+    try:
+        idx, zh, zr, host = q.z_to_idx(z, 3)
+        assert np.array_equal(idx, want_idx)
+        assert bits_equal(zh, want_zh) and bits_equal(zr, want_zr)
+        assert bits_equal(q.zhats(idx, 3), O.vq_idx_to_zhats(cfg, w, idx, 3))
+    finally:
+        q.close()

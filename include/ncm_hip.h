@@ -574,6 +574,14 @@ void vq_z_to_idx_dev(VQState *vq, const float *z, int B, int *idx, float *z_hat,
 /* replaces vq_idx_to_zhats, ncm.h:217, vq.c:502-552: idx HOST; zhats[level]
  * device [B][L][D] buffers receiving z_hat after each level. */
 void vq_idx_to_zhats(VQState *vq, const int *idx, int B, float **zhats);
+/* replaces vq_next_input, ncm.h:219-220, vq.c:554-597: codes HOST [B][levels[level]];
+ * z_hat device [B][L][D] += that level's contribution; x_out device
+ * [B][levels[level + 1]][D] = area(z_hat).  level + 1 < n_levels. */
+void vq_next_input(VQState *vq, const int *codes, int level_idx, float *z_hat, float *x_out, int B);
+/* replaces vq_idx_to_ncm_input, ncm.h:222, vq.c:601-670: idx HOST [B][total];
+ * x_out device [B][total - levels[0]][D]: level li's chunk (li < n_levels - 1)
+ * is area(z_hat after level li -> levels[li + 1]). */
+void vq_idx_to_ncm_input(VQState *vq, const int *idx, int B, float *x_out);
 
 
 /* replaces train_data_load / train_data_free, ncm.h:262-264, tensor.c:375-395:

@@ -467,11 +467,10 @@ static void orc_resi(const OrcVq *q, float *h, int B, int lv) {
     free(c);
 }
 
-/* q = E[lv][codes of level lv] ([B][tl][D]), then up-sampled and Phi-blended into up */
-static void orc_level_up(const OrcVq *q, const int *idx, int B, int lv, int base, float *up) {
+/* q = E[lv][codes of level lv] ([B][tl][D], sequence b's codes at
+ * idx[b * total + base + t]), then up-sampled and Phi-blended into up */
+static void orc_level_up_at(const OrcVq *q, const int *idx, int total, int B, int lv, int base, float *up) {
     const int D = q->D, tl = q->levels[lv];
-    int total = 0;
-    for (int k = 0; k < q->n_levels; k++) total += q->levels[k];
     float *qq = (float *)malloc((size_t)B * tl * D * sizeof(float));
     for (int b = 0; b < B; b++)
         for (int t = 0; t < tl; t++)
@@ -480,6 +479,12 @@ static void orc_level_up(const OrcVq *q, const int *idx, int B, int lv, int base
     orc_up(q, qq, B, lv, up);
     free(qq);
     orc_resi(q, up, B, lv);
+}
+
+static void orc_level_up(const OrcVq *q, const int *idx, int B, int lv, int base, float *up) {
+    int total = 0;
+    for (int k = 0; k < q->n_levels; k++) total += q->levels[k];
+    orc_level_up_at(q, idx, total, B, lv, base, up);
 }
 
 /* vq.c:378-500 vq_z_to_idx (argmin at every level) */
@@ -523,6 +528,46 @@ void orc_vq_idx_to_zhats(const OrcVq *q, const int *idx, int B, float *zhats) {
         for (size_t i = 0; i < n; i++) zh[i] += up[i];
         memcpy(zhats + (size_t)lv * n, zh, n * sizeof(float));
         base += q->levels[lv];
+    }
+    free(zh);
+    free(up);
+}
+
+/* vq.c:554-597 vq_next_input: codes [B][levels[lv]]; z_hat [B][L][D] += the
+ * level's up-sampled, Phi-blended codewords; x_out [B][levels[lv + 1]][D] =
+ * area(z_hat) */
+void orc_vq_next_input(const OrcVq *q, const int *codes, int lv, float *z_hat, float *x_out, int B) {
+    const int D = q->D, L = q->levels[q->n_levels - 1];
+    const size_t n = (size_t)B * L * D;
+    float *up = (float *)malloc(n * sizeof(float));
+    orc_level_up_at(q, codes, q->levels[lv], B, lv, 0, up);
+    for (size_t i = 0; i < n; i++) z_hat[i] += up[i];
+    orc_area(z_hat, x_out, B, L, q->levels[lv + 1], D);
+    free(up);
+}
+
+/* vq.c:601-670 vq_idx_to_ncm_input: idx [B][total] level-major; x_out
+ * [B][total - levels[0]][D] holds, for li < n_levels - 1 in turn, area(z_hat
+ * after level li -> levels[li + 1]) */
+void orc_vq_idx_to_ncm_input(const OrcVq *q, const int *idx, int B, float *x_out) {
+    const int D = q->D, L = q->levels[q->n_levels - 1];
+    const size_t n = (size_t)B * L * D;
+    int total = 0;
+    for (int k = 0; k < q->n_levels; k++) total += q->levels[k];
+    const int T = total - q->levels[0];
+    float *zh = (float *)calloc(n, sizeof(float)), *up = (float *)malloc(n * sizeof(float));
+    int base = 0, off = 0;
+    for (int li = 0; li + 1 < q->n_levels; li++) {
+        const int nlen = q->levels[li + 1];
+        orc_level_up(q, idx, B, li, base, up);
+        for (size_t i = 0; i < n; i++) zh[i] += up[i];
+        float *cv = (float *)malloc((size_t)B * nlen * D * sizeof(float));
+        orc_area(zh, cv, B, L, nlen, D);
+        for (int b = 0; b < B; b++)
+            memcpy(x_out + ((size_t)b * T + off) * D, cv + (size_t)b * nlen * D, (size_t)nlen * D * sizeof(float));
+        free(cv);
+        base += q->levels[li];
+        off += nlen;
     }
     free(zh);
     free(up);

@@ -131,6 +131,8 @@ typedef struct {
 void orc_vq_z_to_idx(const OrcVq *q, const float *z, int B, int *idx, float *z_hat, float *z_rest);
 /* zhats [n_levels][B][L][D]: z_hat after each level */
 void orc_vq_idx_to_zhats(const OrcVq *q, const int *idx, int B, float *zhats);
+void orc_vq_next_input(const OrcVq *q, const int *codes, int lv, float *z_hat, float *x_out, int B);
+void orc_vq_idx_to_ncm_input(const OrcVq *q, const int *idx, int B, float *x_out);
 
 /* threads used by the OpenMP loops (0 = runtime default) */
 void orc_set_threads(int n);

@@ -47,6 +47,8 @@ def lib():
             "orc_sample_topkp": (ci, [vp, ci, ctypes.c_float, ci, ctypes.c_float, ctypes.POINTER(ctypes.c_uint64)]),
             "orc_vq_z_to_idx": (None, [vp, vp, ci, vp, vp, vp]),
             "orc_vq_idx_to_zhats": (None, [vp, vp, ci, vp]),
+            "orc_vq_next_input": (None, [vp, vp, ci, vp, vp, ci]),
+            "orc_vq_idx_to_ncm_input": (None, [vp, vp, ci, vp]),
             "orc_gelu": (None, [vp, vp, i64]),
             "orc_gelu_tanh": (None, [vp, vp, i64]),
             "orc_silu": (None, [vp, vp, i64]),
@@ -253,6 +255,27 @@ def vq_idx_to_zhats(cfg, weights, idx, B):
     out = np.empty((n, B, L, D), np.float32)
     lib().orc_vq_idx_to_zhats(ctypes.byref(d), _ptr(idx), B, _ptr(out))
     return out
+
+
+def vq_next_input(cfg, weights, codes, level, z_hat, B):
+    """vq_next_input (vq.c:554-597): returns (z_hat + the level's contribution,
+    area(that -> levels[level + 1]))."""
+    d, keep = vq_desc(cfg, weights)
+    codes = np.ascontiguousarray(codes, np.int32)
+    zh = np.array(z_hat, np.float32, copy=True, order="C")
+    x = np.empty((B, cfg["levels"][level + 1], cfg["vq_embed_dim"]), np.float32)
+    lib().orc_vq_next_input(ctypes.byref(d), _ptr(codes), level, _ptr(zh), _ptr(x), B)
+    return zh, x
+
+
+def vq_idx_to_ncm_input(cfg, weights, idx, B):
+    """vq_idx_to_ncm_input (vq.c:601-670): [B][total - levels[0]][D]."""
+    d, keep = vq_desc(cfg, weights)
+    n = cfg["n_qlevels"]
+    idx = np.ascontiguousarray(idx, np.int32)
+    x = np.empty((B, sum(cfg["levels"][1:n]), cfg["vq_embed_dim"]), np.float32)
+    lib().orc_vq_idx_to_ncm_input(ctypes.byref(d), _ptr(idx), B, _ptr(x))
+    return x
 
 
 def ref_sample_topkp(logits, temp, top_k, top_p, rng):

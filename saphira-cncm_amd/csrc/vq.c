@@ -358,6 +358,12 @@ static int vqf_gn(const float *x, float *y, int B, int T, int D) {
     return ncm_launch_named("vqf_groupnorm", (unsigned)B * 8u, 1, 1, 64, a);
 }
 
+/* y rows b * ystride + yoff + t = area(x [B][Tin][D] -> Tout) */
+static int vqf_area(const float *x, float *y, int B, int Tin, int Tout, int D, int ystride, int yoff) {
+    void *a[] = {&x, &y, &B, &Tin, &Tout, &D, &ystride, &yoff};
+    return ncm_launch_named("vqf_area", grid256((int64_t)B * Tout * D), 1, 1, 256, a);
+}
+
 static int vqf_mix(float *h, const float *c, int64_t n, float r, int add) {
     void *a[] = {&h, &c, &n, &r, &add};
     return ncm_launch_named("vqf_blend", grid256(n), 1, 1, 256, a);
@@ -431,13 +437,14 @@ static int phi_slot(const VQState *v, int lv) {
     return best;
 }
 
-/* up [B][L][D] <- level lv's codes (device idx) up-sampled, refined and Phi-blended */
-static int vqf_level_up(const VQState *v, const int *idx, int B, int lv, int off, VqfWs *w) {
+/* up [B][L][D] <- level lv's codes up-sampled, refined and Phi-blended; the
+ * codes of sequence b are idx[b * total + off + t] (device) */
+static int vqf_level_up_at(const VQState *v, const int *idx, int total, int B, int lv, int off, VqfWs *w) {
     const int D = v->D, L = v->L, tl = v->levels[lv], V = v->vocabs[lv];
     const int64_t nq = (int64_t)B * tl * D, nL = (int64_t)B * L * D;
     const float *E = v->E[lv];
     float *q = w->down;   /* free at this point of a level */
-    void *ga[] = {&E, &idx, (void *)&V, (void *)&v->total, &off, &B, (void *)&tl, (void *)&D, &q};
+    void *ga[] = {&E, &idx, (void *)&V, &total, &off, &B, (void *)&tl, (void *)&D, &q};
     if (ncm_launch_named("vqf_gather", grid256(nq), 1, 1, 256, ga)) return -1;
     if (lv == 0 && v->n_down > 0) {
         if (vqf_cascade(v, q, w->up, w, B, tl, 1)) return -1;
@@ -454,6 +461,10 @@ static int vqf_level_up(const VQState *v, const int *idx, int B, int lv, int off
         if (vqf_mix(w->up, w->t1, nL, v->resi_ratio, 0)) return -1;
     }
     return 0;
+}
+
+static int vqf_level_up(const VQState *v, const int *idx, int B, int lv, int off, VqfWs *w) {
+    return vqf_level_up_at(v, idx, v->total, B, lv, off, w);
 }
 
 static int vqf_check(const VQState *vq, const float *z, int B, const char *fn) {
@@ -481,8 +492,7 @@ void vq_z_to_idx_dev(VQState *vq, const float *z, int B, int *idx, float *z_hat,
         if (lv == 0 && vq->n_down > 0) {
             if (vqf_cascade(vq, w.zr, w.down, &w, B, L, 0)) return;
         } else {
-            void *aa[] = {&w.zr, &w.down, &B, (void *)&L, (void *)&tl, (void *)&D};
-            if (ncm_launch_named("vqf_area", grid256((int64_t)B * tl * D), 1, 1, 256, aa)) return;
+            if (vqf_area(w.zr, w.down, B, L, tl, D, tl, 0)) return;
         }
         if (vq->has_all && lv >= 1 && lv <= vq->n_levels - 2 && vq->drefW[lv] &&
             vqf_refine(vq, w.down, vq->drefW[lv], vq->drefB[lv], w.t1, B, tl))
@@ -529,5 +539,49 @@ void vq_idx_to_zhats(VQState *vq, const int *idx, int B, float **zhats) {
         if (ncm_launch_named("vqf_update", grid256(nL), 1, 1, 256, ua)) return;
         if (zhats[lv] && ncm_copy_async(zhats[lv], w.zh, (size_t)nL * sizeof(float))) return;
         base += vq->levels[lv];
+    }
+}
+
+void vq_next_input(VQState *vq, const int *codes, int level_idx, float *z_hat, float *x_out, int B) {
+    if (!vq || !codes || !z_hat || !x_out || B < 0 || level_idx < 0 || level_idx + 1 >= vq->n_levels) {
+        ncm_fail(NCM_E_ARG, "vq_next_input: bad arguments (level %d of %d)", level_idx, vq ? vq->n_levels : 0);
+        return;
+    }
+    if (B == 0 || vqf_check(vq, z_hat, B, "vq_next_input")) return;
+    VqfWs w;
+    if (vqf_ws(vq, B, &w)) return;
+    const int tl = vq->levels[level_idx], nlen = vq->levels[level_idx + 1];
+    mem_h2d(w.idx, codes, (size_t)B * tl * sizeof(int));
+    if (vqf_level_up_at(vq, w.idx, tl, B, level_idx, 0, &w)) return;
+    const int64_t nL = (int64_t)B * vq->L * vq->D;
+    float *none = NULL;
+    int init = 0;
+    void *ua[] = {&z_hat, &none, &w.up, (void *)&nL, &init};
+    if (ncm_launch_named("vqf_update", grid256(nL), 1, 1, 256, ua)) return;
+    vqf_area(z_hat, x_out, B, vq->L, nlen, vq->D, nlen, 0);
+}
+
+void vq_idx_to_ncm_input(VQState *vq, const int *idx, int B, float *x_out) {
+    if (!vq || !idx || !x_out || B < 0) {
+        ncm_fail(NCM_E_ARG, "vq_idx_to_ncm_input: bad arguments");
+        return;
+    }
+    if (B == 0 || vqf_check(vq, x_out, B, "vq_idx_to_ncm_input")) return;
+    VqfWs w;
+    if (vqf_ws(vq, B, &w)) return;
+    mem_h2d(w.idx, idx, (size_t)B * vq->total * sizeof(int));
+    const int T = vq->total - vq->levels[0];
+    const int64_t nL = (int64_t)B * vq->L * vq->D;
+    float *none = NULL;
+    int base = 0, off = 0;
+    for (int li = 0; li < vq->n_levels - 1; li++) {
+        if (vqf_level_up(vq, w.idx, B, li, base, &w)) return;
+        int init = li == 0;
+        void *ua[] = {&w.zh, &none, &w.up, (void *)&nL, &init};
+        if (ncm_launch_named("vqf_update", grid256(nL), 1, 1, 256, ua)) return;
+        const int nlen = vq->levels[li + 1];
+        if (vqf_area(w.zh, x_out, B, vq->L, nlen, vq->D, T, off)) return;
+        base += vq->levels[li];
+        off += nlen;
     }
 }

@@ -534,9 +534,10 @@ vq_residual(const float *__restrict__ E, const int *__restrict__ idx, int rows, 
 // arithmetic: fp64 accumulators in its loop orders, separate multiply and
 // add roundings (no contraction), float results.  Bit-exact with the CPU.
 
-// kernels.c:681-700 area interpolation, one thread per output (b, t, d)
+// kernels.c:681-700 area interpolation, one thread per output (b, t, d);
+// output row t of sequence b goes to y row b * ystride + yoff + t
 extern "C" __global__ void __launch_bounds__(256)
-vqf_area(const float *__restrict__ x, float *__restrict__ y, int B, int Tin, int Tout, int D) {
+vqf_area(const float *__restrict__ x, float *__restrict__ y, int B, int Tin, int Tout, int D, int ystride, int yoff) {
 #pragma clang fp contract(off)
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= (int64_t)B * Tout * D) return;
@@ -548,7 +549,7 @@ vqf_area(const float *__restrict__ x, float *__restrict__ y, int B, int Tin, int
     if (e > Tin) e = Tin;
     double acc = 0.0;
     for (int64_t k = s; k < e; ++k) acc += (double)x[((int64_t)b * Tin + k) * D + d];
-    y[i] = (float)(acc / (double)(e - s));
+    y[((int64_t)b * ystride + yoff + t) * D + d] = (float)(acc / (double)(e - s));
 }
 
 // kernels.c:702-727 linear interpolation (align_corners = False; a length-1

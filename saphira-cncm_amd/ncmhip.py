@@ -155,6 +155,8 @@ _SIGS = {
     "vq_z_to_idx": (None, [vp, vp, ci, vp]),
     "vq_z_to_idx_dev": (None, [vp, vp, ci, vp, vp, vp]),
     "vq_idx_to_zhats": (None, [vp, vp, ci, ctypes.POINTER(vp)]),
+    "vq_next_input": (None, [vp, vp, ci, vp, vp, ci]),
+    "vq_idx_to_ncm_input": (None, [vp, vp, ci, vp]),
 }
 
 # On-disk formats, the AdamW object and NCK1 checkpoints: the reference's

@@ -64,6 +64,22 @@ class DevVq:
         ncmhip.check()
         return np.stack([o.numpy() for o in outs])
 
+    def next_input(self, codes, level, z_hat, B, nlen):
+        zd = D_.from_numpy(np.ascontiguousarray(z_hat, np.float32))
+        x = D_.empty((B, nlen, self.D))
+        codes = np.ascontiguousarray(codes, np.int32)
+        self.lib.vq_next_input(self.vq, codes.ctypes.data, level, zd.ptr, x.ptr, B)
+        ncmhip.check()
+        return zd.numpy(), x.numpy()
+
+    def ncm_input(self, idx, B):
+        T = self.total - self.lib.vq_level_len(self.vq, 0)
+        x = D_.empty((B, max(T, 1), self.D))
+        idx = np.ascontiguousarray(idx, np.int32)
+        self.lib.vq_idx_to_ncm_input(self.vq, idx.ctypes.data, B, x.ptr)
+        ncmhip.check()
+        return x.numpy()[:, :T]
+
     def close(self):
         self.lib.vq_free(self.vq)
 
@@ -118,5 +134,38 @@ def test_zero_sequences_and_negative_zero_bias():
         assert np.array_equal(idx, want_idx)
         assert bits_equal(zh, want_zh) and bits_equal(zr, want_zr)
         assert bits_equal(q.zhats(idx, 3), O.vq_idx_to_zhats(cfg, w, idx, 3))
+    finally:
+        q.close()
+
+
+@pytest.mark.parametrize("name,kw", CASES, ids=[c[0] for c in CASES])
+def test_next_input_and_ncm_input_match_oracle(name, kw):
+    """vq_next_input threaded through the levels and vq_idx_to_ncm_input, over
+    the oracle's codes, bit for bit."""
+    cfg, w, z = make_case(7, **kw)
+    B = kw["B"]
+    print(f"[gpu] vq inputs case {name}", flush=True)
+    idx, _, _ = O.vq_z_to_idx(cfg, w, z, B)
+    q = DevVq(cfg, w)
+    try:
+        assert bits_equal(q.ncm_input(idx, B), O.vq_idx_to_ncm_input(cfg, w, idx, B))
+        zh, zh_dev, base = np.zeros_like(z), np.zeros_like(z), 0
+        for lv in range(q.n - 1):
+            tl, nlen = cfg["levels"][lv], cfg["levels"][lv + 1]
+            codes = idx[:, base:base + tl]
+            zh, xn = O.vq_next_input(cfg, w, codes, lv, zh, B)
+            zh_dev, xn_dev = q.next_input(codes, lv, zh_dev, B, nlen)
+            assert bits_equal(zh_dev, zh) and bits_equal(xn_dev, xn)
+            base += tl
+    finally:
+        q.close()
+
+
+def test_next_input_refuses_the_last_level():
+    cfg, w, z = make_case(3, B=2, levels=[1, 4, 16], V=8, D=16)
+    q = DevVq(cfg, w)
+    try:
+        with pytest.raises(ncmhip.NcmError, match="vq_next_input"):
+            q.next_input(np.zeros((2, 16), np.int32), 2, z, 2, 16)
     finally:
         q.close()

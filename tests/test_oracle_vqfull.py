@@ -9,7 +9,7 @@ import pytest
 
 import oracle as O
 from conftest import bits_equal
-from vqfull_cases import CASES, make_case, ref_vq
+from vqfull_cases import CASES, make_case, ref_inputs, ref_vq
 
 needs_ref = pytest.mark.skipif(not O.ref_available(), reason="reference not compiled here")
 
@@ -25,6 +25,51 @@ def test_oracle_matches_reference(name, kw):
     zhats = O.vq_idx_to_zhats(cfg, w, idx, B)
     assert bits_equal(zhats, rzh)
     assert bits_equal(zh, zhats[-1])
+
+
+@needs_ref
+@pytest.mark.parametrize("name,kw", CASES, ids=[c[0] for c in CASES])
+def test_next_input_and_ncm_input_match_reference(name, kw):
+    cfg, w, z = make_case(7, **kw)
+    B = kw["B"]
+    idx, _, _ = O.vq_z_to_idx(cfg, w, z, B)
+    rx, rsteps = ref_inputs(cfg, w, idx, B)
+    assert bits_equal(O.vq_idx_to_ncm_input(cfg, w, idx, B), rx)
+    zh, base = np.zeros_like(z), 0
+    for lv, (rzh, rxn) in enumerate(rsteps):
+        tl = cfg["levels"][lv]
+        zh, xn = O.vq_next_input(cfg, w, idx[:, base:base + tl], lv, zh, B)
+        assert bits_equal(zh, rzh) and bits_equal(xn, rxn)
+        base += tl
+
+
+def test_ncm_input_chunks_are_area_of_the_running_zhats():
+    # chunk li of vq_idx_to_ncm_input = area(z_hat after level li) and the last
+    # chunk, at full length, is that z_hat itself (area L -> L is the identity)
+    cfg, w, z = make_case(9, B=3, levels=[1, 2, 4, 8, 16], V=32, D=16, phi=1, ratio=0.5)
+    idx, _, _ = O.vq_z_to_idx(cfg, w, z, 3)
+    zhats = O.vq_idx_to_zhats(cfg, w, idx, 3)
+    x = O.vq_idx_to_ncm_input(cfg, w, idx, 3)
+    assert x.shape == (3, 30, 16)
+    assert bits_equal(x[:, 14:], zhats[3])
+    # the first chunk (length 2) averages 8 rows each: a serial fp64 sum over
+    # the window, divided by 8, rounded once to fp32
+    want = np.empty((3, 2, 16), np.float32)
+    for b in range(3):
+        for t in range(2):
+            for d in range(16):
+                acc = 0.0
+                for k in range(8 * t, 8 * t + 8):
+                    acc += float(zhats[0][b, k, d])
+                want[b, t, d] = np.float32(acc / 8.0)
+    assert bits_equal(x[:, 0:2], want)
+    # next_input threaded through the levels returns the same chunks
+    zh, base, off = np.zeros_like(z), 0, 0
+    for lv in range(4):
+        zh, xn = O.vq_next_input(cfg, w, idx[:, base:base + cfg["levels"][lv]], lv, zh, 3)
+        assert bits_equal(zh, zhats[lv]) and bits_equal(xn, x[:, off:off + cfg["levels"][lv + 1]])
+        base += cfg["levels"][lv]
+        off += cfg["levels"][lv + 1]
 
 
 def test_full_length_levels_reduce_to_identity_resampling():

@@ -119,6 +119,38 @@ def ref_vq(cfg, w, z, B):
     return idx, zh
 
 
+def ref_inputs(cfg, w, idx, B):
+    """The reference's own vq_idx_to_ncm_input and, level by level from a zero
+    z_hat, vq_next_input over the same codes: returns (x [B][T][D],
+    [(z_hat, x_next)] per level below the last)."""
+    R = O.ref()
+    R.vq_next_input.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                ctypes.c_int]
+    R.vq_idx_to_ncm_input.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    ref_vq(cfg, w, np.zeros((B, cfg["levels"][cfg["n_qlevels"] - 1], cfg["vq_embed_dim"]), np.float32), B)
+    arrays = {k: np.ascontiguousarray(v, np.float32) for k, v in w.items()}
+    tens = [(k, host_tensor(a)) for k, a in arrays.items()]
+    ws, keep = weight_store(tens)
+    c = ncm_config(cfg)
+    vq = R.vq_load(ctypes.byref(c), ctypes.byref(ws), b"")
+    n, L, D = cfg["n_qlevels"], cfg["levels"][cfg["n_qlevels"] - 1], cfg["vq_embed_dim"]
+    idx = np.ascontiguousarray(idx, np.int32)
+    x = np.zeros((B, sum(cfg["levels"][1:n]), D), np.float32)
+    R.arena_reset()
+    R.vq_idx_to_ncm_input(vq, idx.ctypes.data, B, x.ctypes.data)
+    steps, zh, base = [], np.zeros((B, L, D), np.float32), 0
+    for lv in range(n - 1):
+        tl = cfg["levels"][lv]
+        codes = np.ascontiguousarray(idx[:, base:base + tl])
+        xn = np.zeros((B, cfg["levels"][lv + 1], D), np.float32)
+        R.arena_reset()
+        R.vq_next_input(vq, codes.ctypes.data, lv, zh.ctypes.data, xn.ctypes.data, B)
+        steps.append((zh.copy(), xn))
+        base += tl
+    R.vq_free(vq)
+    return x, steps
+
+
 # Cases: (name, kwargs).  L = 16 rows per sequence unless stated.
 CASES = [
     ("area_linear", dict(B=6, levels=[1, 2, 4, 8, 16], V=64, D=32)),

@@ -110,6 +110,13 @@ void linear_fwd(const float *x, const float *W, const float *b,
 void linear_fwd_ep(const float *x, const float *W, const float *b,
                    const float *res, float *y, int64_t batch, int M, int K, int act);
 
+/* extension: the gated unit y = act(x W^T + b) * mul, elementwise with mul
+ * [batch][M] (a buffer other than y).  Replaces linear_fwd + silu_fwd
+ * followed by mul_fwd(g, u, g) (ncp.c:301-310, qwen.c:162-166): the product
+ * is formed in the GEMM's epilogue, with the same float operations. */
+void linear_fwd_glu(const float *x, const float *W, const float *b,
+                    const float *mul, float *y, int64_t batch, int M, int K, int act);
+
 /* extension: the linear backward of the autograd tape, host path
  * train_tape.c:680-725 and device path train_tape.c:1978-2000:
  *   dx[r,k] += sum_m dy[r,m] W[m,k]        (dX = dY . W)
@@ -183,6 +190,11 @@ void sdpa_fwd(const float *q, const float *k, const float *v, const float *mask,
               int B, int H, int Tq, int Tkv, int hd);
 void sdpa_fwd_gqa(const float *q, const float *k, const float *v, const float *mask, float *out,
                   int B, int Hq, int Hkv, int Tq, int Tkv, int hd);
+/* extension: sdpa_fwd_gqa with the heads merged on output, out [B][Tq][Hq * hd]
+ * = head_merge_fwd of sdpa_fwd_gqa's [B][Hq][Tq][hd] (ncp.c:248-260 runs the
+ * two in turn); identical values. */
+void sdpa_fwd_gqa_merged(const float *q, const float *k, const float *v, const float *mask, float *out,
+                         int B, int Hq, int Hkv, int Tq, int Tkv, int hd);
 /* extension: causal SDPA-GQA with the mask generated in the kernel: query tq
  * sees keys <= tq + (Tkv - Tq).  Replaces building the T x T -1e9 mask on the
  * host and uploading it (qwen.c:130-138, gpt2.c:112-121) + sdpa_fwd_gqa. */
@@ -200,6 +212,10 @@ void add_inplace_fwd(float *y, const float *x, int64_t n);
 /* replaces qkv_split_fwd / head_merge_fwd, ncm.h:193-196, kernels.c:891-936 */
 void qkv_split_fwd(const float *in, float *qq, float *kk, float *vv,
                    int B, int T, int C, int H, int hd, int K, int rep);
+/* extension: qkv_split_fwd followed by rope_apply(qq, kk, cos_t, sin_t, B, H,
+ * T, hd) in one pass (ncp.c:213-236 does the two in turn); identical values. */
+void qkv_split_rope_fwd(const float *in, float *qq, float *kk, float *vv, const float *cos_t,
+                        const float *sin_t, int B, int T, int C, int H, int hd, int K, int rep);
 void head_merge_fwd(const float *ctx, float *out, int B, int T, int C, int H, int hd);
 
 /* ------------------------------------------------------------------ */

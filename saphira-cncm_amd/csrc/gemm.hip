@@ -42,7 +42,8 @@
 // a single fp32 chain over K terms has an error growing like K u, the two
 // levels keep it near (128 + K/128) u.
 //
-// Epilogues: STORE  C = res + act(acc + bias);  ACCUM  C += acc.
+// Epilogues: STORE  C = res + act(acc + bias) (or act(acc + bias) * res, the
+// gated-unit product);  ACCUM  C += acc.
 #include "mfma_slab.h"
 
 enum { EPI_STORE = 0, EPI_ACCUM = 1 };
@@ -52,12 +53,12 @@ struct GemmArgs {
     const float *B;
     float *C;
     const float *bias;   // [No] or null (STORE only)
-    const float *res;    // [Mo, ldc] or null (STORE only)
+    const float *res;    // [Mo, ldc] or null (STORE only): added, or multiplied when res_mul
     float *ws;           // partial tiles of split tiles [units][64*64]
     int Mo, No, K;
     int lda, ldb, ldc;
     int act;
-    int vec_out;         // unused by the 64x64 kernels (kept for the host's struct layout)
+    int res_mul;         // STORE: C = act(acc + bias) * res instead of res + act(acc + bias)
     int tiles_m, tiles_n;
     int iters;           // BK slabs per tile (a multiple of 4)
     int dp_tiles;        // blocks [0, dp_tiles): one whole tile each
@@ -444,7 +445,7 @@ __device__ __forceinline__ void g_out(const GemmArgs &p, int i, int j, float v) 
     } else {
         if (p.bias) v += p.bias[j];
         v = ncm_act(v, ACT);
-        if (p.res) v = p.res[(int64_t)i * p.ldc + j] + v;
+        if (p.res) v = p.res_mul ? v * p.res[(int64_t)i * p.ldc + j] : p.res[(int64_t)i * p.ldc + j] + v;
         *c = v;
     }
 }

@@ -27,7 +27,7 @@ typedef struct {
     int Mo, No, K;
     int lda, ldb, ldc;
     int act;
-    int vec_out;
+    int res_mul;
     int tiles_m, tiles_n;
     int iters;
     int dp_tiles;
@@ -172,7 +172,7 @@ static int64_t extent(int64_t rows, int64_t cols, int64_t ld) { return ((rows - 
 #define TILE_N 64
 
 static int run_gemm(int kind, const float *A, const float *B, float *C, const float *bias,
-                    const float *res, int Mo, int No, int Kred, int lda, int ldb, int ldc,
+                    const float *res, int res_mul, int Mo, int No, int Kred, int lda, int ldb, int ldc,
                     int act, int vec) {
     if (Mo <= 0 || No <= 0) return 0;
     const int bm = TILE_M, bn = TILE_N;
@@ -189,7 +189,7 @@ static int run_gemm(int kind, const float *A, const float *B, float *C, const fl
                         (long long)ab, (long long)bb);
     GemmArgs p = {A, B, C, bias, res, NULL, Mo, No, Kred, lda, ldb, ldc, act, 0,
                   g.tiles_m, g.tiles_n, g.iters, g.dp_tiles, g.segs, (unsigned)ab, (unsigned)bb};
-    p.vec_out = No % 4 == 0 && ldc % 4 == 0 && is_aligned16(C);
+    p.res_mul = res_mul;
     int split_tiles = g.tiles_m * g.tiles_n - g.dp_tiles;
     if (g.segs > 1) {
         p.ws = (float *)ncm_workspace(WS_SPLITK, (size_t)split_tiles * g.segs * bm * bn * sizeof(float));
@@ -242,8 +242,9 @@ static int check_dims(const char *fn, int64_t batch, int M, int K) {
     return 0;
 }
 
+/* y = res + act(x W^T + b), or act(x W^T + b) * res when res_mul */
 static void linear_forward(const char *fn, const float *x, const float *W, const float *b,
-                           const float *res, float *y, int64_t batch, int M, int K, int act) {
+                           const float *res, int res_mul, float *y, int64_t batch, int M, int K, int act) {
     if (check_dims(fn, batch, M, K)) return;
     if (act < NCM_ACT_NONE || act > NCM_ACT_GELU_TANH) {
         ncm_fail(NCM_E_ARG, "%s: unknown activation %d", fn, act);
@@ -254,22 +255,33 @@ static void linear_forward(const char *fn, const float *x, const float *W, const
         ncm_fail(NCM_E_ARG, "%s: null x/W/y", fn);
         return;
     }
+    if (res_mul && (!res || res == y)) {
+        ncm_fail(NCM_E_ARG, "%s: the multiplier must be a buffer other than y", fn);
+        return;
+    }
     if (ncm_ready()) return;
     int vec = (K % 4 == 0) && is_aligned16(x) && is_aligned16(W);
-    if (batch <= 8)
+    if (batch <= 8 && res_mul) {   /* the GEMVs add only: product in a second pass */
+        if (run_gemv(x, W, b, NULL, y, (int)batch, M, K, act, vec) == 0) mul_fwd(y, res, y, batch * M);
+    } else if (batch <= 8)
         run_gemv(x, W, b, res, y, (int)batch, M, K, act, vec);
     else
-        run_gemm(L_FWD, x, W, y, b, res, (int)batch, M, K, K, K, M, act, vec);
+        run_gemm(L_FWD, x, W, y, b, res, res_mul, (int)batch, M, K, K, K, M, act, vec);
 }
 
 void linear_fwd(const float *x, const float *W, const float *b, float *y, int64_t batch, int M,
                 int K) {
-    linear_forward("linear_fwd", x, W, b, NULL, y, batch, M, K, NCM_ACT_NONE);
+    linear_forward("linear_fwd", x, W, b, NULL, 0, y, batch, M, K, NCM_ACT_NONE);
 }
 
 void linear_fwd_ep(const float *x, const float *W, const float *b, const float *res, float *y,
                    int64_t batch, int M, int K, int act) {
-    linear_forward("linear_fwd_ep", x, W, b, res, y, batch, M, K, act);
+    linear_forward("linear_fwd_ep", x, W, b, res, 0, y, batch, M, K, act);
+}
+
+void linear_fwd_glu(const float *x, const float *W, const float *b, const float *mul, float *y,
+                    int64_t batch, int M, int K, int act) {
+    linear_forward("linear_fwd_glu", x, W, b, mul, 1, y, batch, M, K, act);
 }
 
 /* Kernel used for the dX of a batch <= 8 backward (transposed GEMV), or NULL. */
@@ -318,7 +330,7 @@ void linear_bwd(const float *x, const float *W, const float *dy, float *dx, floa
             rc = run_dxt(dy, W, dx, nb, M, K);
         else {
             int vec = (M % 4 == 0) && (K % 4 == 0) && is_aligned16(dy) && is_aligned16(W);
-            rc = run_gemm(L_DX, dy, W, dx, NULL, NULL, nb, K, M, M, K, K, 0, vec);
+            rc = run_gemm(L_DX, dy, W, dx, NULL, NULL, 0, nb, K, M, M, K, K, 0, vec);
         }
         if (rc) return;
     }
@@ -332,7 +344,7 @@ void linear_bwd(const float *x, const float *W, const float *dy, float *dx, floa
             rc = ncm_launch_named(vec ? "dw_rank_v" : "dw_rank_s", (unsigned)((n + 255) / 256), 1, 1, 256, a);
         } else {
             int vec = (M % 4 == 0) && (K % 4 == 0) && is_aligned16(dy) && is_aligned16(x);
-            rc = run_gemm(L_DW, dy, x, dW, NULL, NULL, M, K, nb, M, K, K, 0, vec);
+            rc = run_gemm(L_DW, dy, x, dW, NULL, NULL, 0, M, K, nb, M, K, K, 0, vec);
         }
         if (rc) return;
     }

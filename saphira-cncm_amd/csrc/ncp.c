@@ -105,22 +105,19 @@ float *ncm_ncp_forward(const NcmNcpConfig *c, float *const *P, const int *ids, i
     free(hs);
     mem_h2d(bids, ids, (size_t)R * sizeof(int));
     embedding_fwd_v(P[0], V, bids, x, R, C);
-    float *ln = A(R * C), *qkv = A(R * QKV), *qq = A(R * C), *kk = A(R * C), *vv = A(R * C), *ctx = A(R * C),
+    float *ln = A(R * C), *qkv = A(R * QKV), *qq = A(R * C), *kk = A(R * C), *vv = A(R * C),
           *mo = A(R * C), *g = A(R * I), *u = A(R * I);
     if (!u) return NULL;
     for (int li = 0; li < c->n_layer; li++) {
         float *const *w = P + 1 + NCP_PER_LAYER * li;
         norm(c, x, w[0], w[1], ln, R);
         linear_fwd(ln, w[2], w[3], qkv, R, QKV, C);
-        qkv_split_fwd(qkv, qq, kk, vv, B, S, C, H, hd, Kv, rep);
-        rope_apply(qq, kk, cosd, sind, B, H, S, hd);
-        sdpa_fwd(qq, kk, vv, NULL, ctx, B, H, S, S, hd);
-        head_merge_fwd(ctx, mo, B, S, C, H, hd);
+        qkv_split_rope_fwd(qkv, qq, kk, vv, cosd, sind, B, S, C, H, hd, Kv, rep);   /* split, then RoPE */
+        sdpa_fwd_gqa_merged(qq, kk, vv, NULL, mo, B, H, H, S, S, hd);               /* heads merged on output */
         linear_fwd_ep(mo, w[4], w[5], x, x, R, C, C, NCM_ACT_NONE);      /* x += c_proj(.) */
         norm(c, x, w[6], w[7], ln, R);
-        linear_fwd_ep(ln, w[8], w[9], NULL, g, R, I, C, NCM_ACT_SILU);   /* silu(w_gate(.)) */
         linear_fwd(ln, w[10], w[11], u, R, I, C);
-        mul_fwd(g, u, g, R * I);
+        linear_fwd_glu(ln, w[8], w[9], u, g, R, I, C, NCM_ACT_SILU);     /* silu(w_gate(.)) * w_up(.) */
         linear_fwd_ep(g, w[12], w[13], x, x, R, C, I, NCM_ACT_NONE);     /* x += c_proj(.) */
     }
     const int n = ncm_ncp_param_count(c);

@@ -130,6 +130,20 @@ void qkv_split_fwd(const float *in, float *qq, float *kk, float *vv, int B, int 
     ncm_launch_named("qkv_split_k", grid_of(n, 256), 1, 1, 256, a);
 }
 
+void qkv_split_rope_fwd(const float *in, float *qq, float *kk, float *vv, const float *cos_t, const float *sin_t,
+                        int B, int T, int C, int H, int hd, int K, int rep) {
+    int64_t n = (int64_t)B * H * T * (hd / 2);
+    if (B < 0 || T < 0 || H < 0 || hd <= 0 || (hd & 1) || K <= 0 || rep <= 0 || (H - 1) / rep >= K ||
+        (int64_t)H * hd > C) {
+        ncm_fail(NCM_E_ARG, "qkv_split_rope_fwd: bad shape (H=%d K=%d rep=%d hd=%d)", H, K, rep, hd);
+        return;
+    }
+    if (ops_ready("qkv_split_rope_fwd", n, 2, in, qq)) return;
+    if (!kk || !vv || !cos_t || !sin_t) { ncm_fail(NCM_E_ARG, "qkv_split_rope_fwd: null pointer"); return; }
+    void *a[] = {&in, &qq, &kk, &vv, &cos_t, &sin_t, &B, &T, &C, &H, &hd, &K, &rep};
+    ncm_launch_named("qkv_split_rope_k", grid_of(n, 256), 1, 1, 256, a);
+}
+
 void head_merge_fwd(const float *ctx, float *out, int B, int T, int C, int H, int hd) {
     int64_t n = (int64_t)B * T * C;
     if (B < 0 || T < 0 || C < 0 || H <= 0 || hd <= 0 || C > H * hd) {
@@ -154,8 +168,9 @@ void embedding_fwd(const float *W, const int *idx, float *y, int64_t n, int D) {
 }
 
 /* ---- SDPA (kernels.c:364-507) ---- */
+/* out [B][Hq][Tq][hd], or [B][Tq][Hq * hd] (the heads merged) when merged */
 static void sdpa_any(const char *fn, const float *q, const float *k, const float *v, const float *mask, float *out,
-                     int B, int Hq, int Hkv, int Tq, int Tkv, int hd, int causal) {
+                     int B, int Hq, int Hkv, int Tq, int Tkv, int hd, int causal, int merged) {
     if (B < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || Tq < 0 || Tkv <= 0 || hd <= 0 || hd > 256) {
         ncm_fail(NCM_E_ARG, "%s: bad shape B=%d Hq=%d Hkv=%d Tq=%d Tkv=%d hd=%d", fn, B, Hq, Hkv, Tq, Tkv, hd);
         return;
@@ -170,26 +185,31 @@ static void sdpa_any(const char *fn, const float *q, const float *k, const float
     if (ncm_ready()) return;
     float scale = 1.0f / sqrtf((float)hd);
     if (hd == 64 && is_aligned16(q) && is_aligned16(k) && is_aligned16(v) && is_aligned16(out)) {
-        void *a[] = {&q, &k, &v, &mask, &out, &Hq, &Hkv, &Tq, &Tkv, &scale, &causal};
+        void *a[] = {&q, &k, &v, &mask, &out, &Hq, &Hkv, &Tq, &Tkv, &scale, &causal, &merged};
         ncm_launch_named("sdpa_hd64", (unsigned)((Tq + 63) / 64), (unsigned)Hq, (unsigned)B, 256, a);
     } else {
         int64_t rows = (int64_t)B * Hq * Tq;
-        void *a[] = {&q, &k, &v, &mask, &out, &B, &Hq, &Hkv, &Tq, &Tkv, &hd, &scale, &causal};
+        void *a[] = {&q, &k, &v, &mask, &out, &B, &Hq, &Hkv, &Tq, &Tkv, &hd, &scale, &causal, &merged};
         ncm_launch_named("sdpa_rows", grid_of(rows, 4), 1, 1, 256, a);
     }
 }
 
 void sdpa_fwd_gqa(const float *q, const float *k, const float *v, const float *mask, float *out, int B, int Hq,
                   int Hkv, int Tq, int Tkv, int hd) {
-    sdpa_any("sdpa_fwd_gqa", q, k, v, mask, out, B, Hq, Hkv, Tq, Tkv, hd, 0);
+    sdpa_any("sdpa_fwd_gqa", q, k, v, mask, out, B, Hq, Hkv, Tq, Tkv, hd, 0, 0);
 }
 
 void sdpa_fwd(const float *q, const float *k, const float *v, const float *mask, float *out, int B, int H, int Tq,
               int Tkv, int hd) {
-    sdpa_any("sdpa_fwd", q, k, v, mask, out, B, H, H, Tq, Tkv, hd, 0);
+    sdpa_any("sdpa_fwd", q, k, v, mask, out, B, H, H, Tq, Tkv, hd, 0, 0);
+}
+
+void sdpa_fwd_gqa_merged(const float *q, const float *k, const float *v, const float *mask, float *out, int B,
+                         int Hq, int Hkv, int Tq, int Tkv, int hd) {
+    sdpa_any("sdpa_fwd_gqa_merged", q, k, v, mask, out, B, Hq, Hkv, Tq, Tkv, hd, 0, 1);
 }
 
 void sdpa_fwd_gqa_causal(const float *q, const float *k, const float *v, float *out, int B, int Hq, int Hkv, int Tq,
                          int Tkv, int hd) {
-    sdpa_any("sdpa_fwd_gqa_causal", q, k, v, NULL, out, B, Hq, Hkv, Tq, Tkv, hd, 1);
+    sdpa_any("sdpa_fwd_gqa_causal", q, k, v, NULL, out, B, Hq, Hkv, Tq, Tkv, hd, 1, 0);
 }

@@ -130,6 +130,37 @@ qkv_split_k(const float *__restrict__ in, float *__restrict__ qq, float *__restr
     vv[i] = row[C + K * hd + kvh * hd + d];
 }
 
+// qkv_split_fwd followed by rope_apply on q and k (kernels.c:913-926,
+// 285-296), one thread per rotation pair (d, d + hd/2) of one (b, h, t): the
+// rotation repeats rope_k's float operations on the values qkv_split_k would
+// have written.
+extern "C" __global__ void __launch_bounds__(256)
+qkv_split_rope_k(const float *__restrict__ in, float *__restrict__ qq, float *__restrict__ kk,
+                 float *__restrict__ vv, const float *__restrict__ cos_t, const float *__restrict__ sin_t, int B,
+                 int T, int C, int H, int hd, int K, int rep) {
+#pragma clang fp contract(off)
+    const int h2 = hd >> 1;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)B * H * T * h2) return;
+    const int d = (int)(i % h2);
+    const int64_t row = i / h2;   // [B][H][T] row
+    const int t = (int)(row % T);
+    const int h = (int)((row / T) % H);
+    const int b = (int)(row / ((int64_t)T * H));
+    const int kvh = h / rep;
+    const float *src = in + ((int64_t)b * T + t) * ((int64_t)C + 2 * K * hd);
+    const float *co = cos_t + (int64_t)t * hd, *si = sin_t + (int64_t)t * hd;
+    float *qr = qq + row * hd, *kr = kk + row * hd, *vr = vv + row * hd;
+    const float qa = src[h * hd + d], qb = src[h * hd + d + h2];
+    qr[d] = qa * co[d] + (-qb) * si[d];
+    qr[d + h2] = qb * co[d + h2] + qa * si[d + h2];
+    const float ka = src[C + kvh * hd + d], kb = src[C + kvh * hd + d + h2];
+    kr[d] = ka * co[d] + (-kb) * si[d];
+    kr[d + h2] = kb * co[d + h2] + ka * si[d + h2];
+    vr[d] = src[C + K * hd + kvh * hd + d];
+    vr[d + h2] = src[C + K * hd + kvh * hd + d + h2];
+}
+
 // head_merge_fwd (kernels.c:903-936): [B][H][T][hd] -> [B][T][C]
 extern "C" __global__ void __launch_bounds__(256)
 head_merge_k(const float *__restrict__ ctx, float *__restrict__ out, int B, int T, int C, int H, int hd) {
@@ -194,7 +225,7 @@ eltwise_k(const float *a, const float *b, float *y, float s, int64_t n, int op) 
 extern "C" __global__ void __launch_bounds__(256)
 sdpa_hd64(const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
           const float *__restrict__ mask, float *__restrict__ out, int Hq, int Hkv, int Tq, int Tkv,
-          float scale, int causal) {
+          float scale, int causal, int merged) {
     __shared__ __attribute__((aligned(16))) float sK[SD_T * SD_LD];
     __shared__ __attribute__((aligned(16))) float sV[SD_T * SD_LD];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -309,7 +340,8 @@ sdpa_hd64(const float *__restrict__ q, const float *__restrict__ k, const float 
         if (qi < Tq) {
             const float inv = 1.0f / lr;
             f4 val = {o[0][r] * inv, o[1][r] * inv, o[2][r] * inv, o[3][r] * inv};
-            *(f4 *)(out + (((int64_t)b * Hq + h) * Tq + qi) * 64 + 4 * li) = val;
+            *(f4 *)(out + (merged ? ((int64_t)b * Tq + qi) * Hq + h : ((int64_t)b * Hq + h) * Tq + qi) * 64 +
+                    4 * li) = val;
         }
     }
 }
@@ -319,7 +351,7 @@ sdpa_hd64(const float *__restrict__ q, const float *__restrict__ k, const float 
 extern "C" __global__ void __launch_bounds__(256)
 sdpa_rows(const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
           const float *__restrict__ mask, float *__restrict__ out, int B, int Hq, int Hkv, int Tq, int Tkv,
-          int hd, float scale, int causal) {
+          int hd, float scale, int causal, int merged) {
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= (int64_t)B * Hq * Tq) return;
@@ -360,7 +392,7 @@ sdpa_rows(const float *__restrict__ q, const float *__restrict__ k, const float 
         }
         m = m_new;
     }
-    float *o = out + row * hd;
+    float *o = out + (merged ? ((int64_t)b * Tq + tq) * Hq + h : row) * hd;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int d = lane + 64 * j;

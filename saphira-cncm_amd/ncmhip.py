@@ -51,6 +51,7 @@ _SIGS = {
     "backend_to_host": (vp, [vp, sz]),
     "linear_fwd": (None, [vp, vp, vp, vp, i64, ci, ci]),
     "linear_fwd_ep": (None, [vp, vp, vp, vp, vp, i64, ci, ci, ci]),
+    "linear_fwd_glu": (None, [vp, vp, vp, vp, vp, i64, ci, ci, ci]),
     "linear_bwd": (None, [vp, vp, vp, vp, vp, vp, i64, ci, ci]),
     "ncm_hip_linear_plan": (ci, [ci, i64, ci, ci, ctypes.c_char_p, sz]),
     "rowwise_l2sq": (None, [vp, vp, vp, i64, i64, ci]),
@@ -69,6 +70,7 @@ _SIGS = {
     "heads_transpose_fwd_b": (None, [vp, vp, ci, i64, ci, ci]),
     "sdpa_fwd": (None, [vp, vp, vp, vp, vp, ci, ci, ci, ci, ci]),
     "sdpa_fwd_gqa": (None, [vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, ci]),
+    "sdpa_fwd_gqa_merged": (None, [vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, ci]),
     "sdpa_fwd_gqa_causal": (None, [vp, vp, vp, vp, ci, ci, ci, ci, ci, ci]),
     "embedding_fwd": (None, [vp, vp, vp, i64, ci]),
     "embedding_fwd_v": (None, [vp, ci, vp, vp, i64, ci]),
@@ -77,6 +79,7 @@ _SIGS = {
     "mul_fwd": (None, [vp, vp, vp, i64]),
     "add_inplace_fwd": (None, [vp, vp, i64]),
     "qkv_split_fwd": (None, [vp, vp, vp, vp, ci, ci, ci, ci, ci, ci, ci]),
+    "qkv_split_rope_fwd": (None, [vp, vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, ci, ci]),
     "head_merge_fwd": (None, [vp, vp, ci, ci, ci, ci, ci]),
     "layernorm_bwd": (None, [vp, vp, vp, vp, vp, vp, i64, ci, ctypes.c_double]),
     "rmsnorm_bwd": (None, [vp, vp, vp, vp, vp, i64, ci]),

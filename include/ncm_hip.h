@@ -117,6 +117,13 @@ void linear_fwd_ep(const float *x, const float *W, const float *b,
 void linear_fwd_glu(const float *x, const float *W, const float *b,
                     const float *mul, float *y, int64_t batch, int M, int K, int act);
 
+/* extension: the whole gated unit y = act(x Wg^T + bg) * (x Wu^T + bu), y
+ * [batch][M] (not aliasing x), bg / bu may be NULL.  Replaces the gate
+ * linear_fwd + silu_fwd, the up linear_fwd and mul_fwd (ncp.c:301-310,
+ * qwen.c:162-166); one GEMM launch computes both products. */
+void linear_fwd_gated(const float *x, const float *Wg, const float *bg, const float *Wu,
+                      const float *bu, float *y, int64_t batch, int M, int K, int act);
+
 /* extension: the linear backward of the autograd tape, host path
  * train_tape.c:680-725 and device path train_tape.c:1978-2000:
  *   dx[r,k] += sum_m dy[r,m] W[m,k]        (dX = dY . W)

@@ -43,10 +43,11 @@
 // levels keep it near (128 + K/128) u.
 //
 // Epilogues: STORE  C = res + act(acc + bias) (or act(acc + bias) * res, the
-// gated-unit product);  ACCUM  C += acc.
+// gated-unit product);  ACCUM  C += acc;  GATED  C = act(x B^T + bias) *
+// (x B2^T + bias2), both products in one tile (gemm_64x64_gated_v).
 #include "mfma_slab.h"
 
-enum { EPI_STORE = 0, EPI_ACCUM = 1 };
+enum { EPI_STORE = 0, EPI_ACCUM = 1, EPI_GATED = 2 };
 
 struct GemmArgs {
     const float *A;
@@ -64,6 +65,8 @@ struct GemmArgs {
     int dp_tiles;        // blocks [0, dp_tiles): one whole tile each
     int segs;            // later blocks: k-segment (u % segs) of tile dp_tiles + u / segs
     unsigned a_bytes, b_bytes;  // extents of A and B for the buffer descriptors
+    const float *B2;     // GATED: the up-projection weight (B is the gate's)
+    const float *bias2;  // GATED: its bias or null
 };
 
 // Grouped raster: GROUP_M tile rows advance together along N so that the B
@@ -660,6 +663,28 @@ __device__ __forceinline__ void gemm_tile_fixup_body(const GemmArgs &p) {
     }
 }
 
+// GATED epilogue of one wave's 32 rows (from r0) x 32 columns (from j0): the
+// gate value, its bias and activation, times the up value plus its bias -- the
+// float operations of linear_fwd_ep(act) followed by mul_fwd.
+template <int ACT>
+__device__ __forceinline__ void g_gated_out(const GemmArgs &p, const f4 (&g)[2][2], const f4 (&u)[2][2], int r0,
+                                            int j0, int li, int lg) {
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int i = r0 + a * 16 + 4 * lg + r, j = j0 + b * 16 + li;
+                if (i >= p.Mo || j >= p.No) continue;
+                float vg = g[a][b][r], vu = u[a][b][r];
+                if (p.bias) vg += p.bias[j];
+                vg = ncm_act(vg, ACT);
+                if (p.bias2) vu += p.bias2[j];
+                p.C[(int64_t)i * p.ldc + j] = vg * vu;
+            }
+}
+
 // ---------------------------------------------------------------- GEMM, direct-to-LDS loads
 // Two LDS stages of 16 KB: five workgroups share a CU.  Per slab: fragment
 // reads of chunk 1, MFMAs of chunk 0, wait for this wave's loads of the next
@@ -692,13 +717,17 @@ __device__ __forceinline__ void gemm_dma_body(const GemmArgs &p) {
     }
     int tm, tn;
     tile_rc<8>(tile, p.tiles_m, p.tiles_n, tm, tn);
-    const int i0 = tm * 64, j0 = tn * 64;
+    // GATED: tile columns 0-31 are output columns j0 .. j0 + 31 of the gate
+    // product, 32-63 the same columns of the up product; waves 0-1 load the
+    // gate's B rows, waves 2-3 the up projection's
+    const bool up_rows = EPI == EPI_GATED && wave >= 2;
+    const int i0 = tm * 64, j0 = tn * (EPI == EPI_GATED ? 32 : 64);
     const int kend = min(p.K, it1 * GEMM_BK);
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, p.a_bytes), rb = make_rsrc(p.B, p.b_bytes);
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, p.a_bytes), rb = make_rsrc(up_rows ? p.B2 : p.B, p.b_bytes);
     DSlab<AKC> la;
     DSlab<BKC> lb;
     la.init(wave, lane, p.lda, i0, p.Mo, kend);
-    lb.init(wave, lane, p.ldb, j0, p.No, kend);
+    lb.init(wave, lane, p.ldb, up_rows ? j0 - 32 : j0, p.No, kend);
 
     f4 acc[2][2], tot[2][2];
 #pragma unroll
@@ -764,6 +793,33 @@ __device__ __forceinline__ void gemm_dma_body(const GemmArgs &p) {
             for (int b = 0; b < 2; ++b) *(f4 *)(mine + ((a * 2 + b) * GEMM_NT + tid) * 4) = tot[a][b];
         return;
     }
+    if constexpr (EPI == EPI_GATED) {
+        // the up half (waves with wn = 1) hands its values to the gate half
+        // through LDS: the same (a, b, lane) slot is the same output element
+        __syncthreads();
+        f4 *xch = (f4 *)sm;
+        if (wn) {
+#pragma unroll
+            for (int a = 0; a < 2; ++a)
+#pragma unroll
+                for (int b = 0; b < 2; ++b) xch[((wm * 2 + a) * 2 + b) * 64 + lane] = tot[a][b];
+        }
+        __syncthreads();
+        if (!wn) {
+            f4 up[2][2];
+#pragma unroll
+            for (int a = 0; a < 2; ++a)
+#pragma unroll
+                for (int b = 0; b < 2; ++b) up[a][b] = xch[((wm * 2 + a) * 2 + b) * 64 + lane];
+            switch (p.act) {
+            case ACT_SILU: g_gated_out<ACT_SILU>(p, tot, up, i0 + wm * 32, j0, li, lg); break;
+            case ACT_GELU: g_gated_out<ACT_GELU>(p, tot, up, i0 + wm * 32, j0, li, lg); break;
+            case ACT_GELU_TANH: g_gated_out<ACT_GELU_TANH>(p, tot, up, i0 + wm * 32, j0, li, lg); break;
+            default: g_gated_out<ACT_NONE>(p, tot, up, i0 + wm * 32, j0, li, lg); break;
+            }
+        }
+        return;
+    }
     g_epilogue<64, 64, EPI, !AKC, !BKC>(p, tot, i0, j0, tid);
 }
 
@@ -785,6 +841,7 @@ __device__ __forceinline__ void gemm_dma_body(const GemmArgs &p) {
 GEMM_DMA_KERNEL(gemm_64x64_fwd_v, true, true, EPI_STORE)
 GEMM_DMA_KERNEL(gemm_64x64_dx_v, true, false, EPI_ACCUM)
 GEMM_DMA_KERNEL(gemm_64x64_dw_v, false, false, EPI_ACCUM)
+GEMM_DMA_KERNEL(gemm_64x64_gated_v, true, true, EPI_GATED)
 GEMM_TILE_KERNEL(gemm_64x64_fwd_s, 64, 64, true, true, EPI_STORE, false)
 GEMM_TILE_KERNEL(gemm_64x64_dx_s, 64, 64, true, false, EPI_ACCUM, false)
 GEMM_TILE_KERNEL(gemm_64x64_dw_s, 64, 64, false, false, EPI_ACCUM, false)

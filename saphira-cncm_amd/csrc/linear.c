@@ -33,6 +33,8 @@ typedef struct {
     int dp_tiles;
     int segs;
     unsigned a_bytes, b_bytes;
+    const float *B2;
+    const float *bias2;
 } GemmArgs;
 
 /* Must match struct GemvArgs in gemm.hip. */
@@ -188,7 +190,7 @@ static int run_gemm(int kind, const float *A, const float *B, float *C, const fl
         return ncm_fail(NCM_E_ARG, "linear: operand of %lld / %lld bytes exceeds the 2 GiB buffer range",
                         (long long)ab, (long long)bb);
     GemmArgs p = {A, B, C, bias, res, NULL, Mo, No, Kred, lda, ldb, ldc, act, 0,
-                  g.tiles_m, g.tiles_n, g.iters, g.dp_tiles, g.segs, (unsigned)ab, (unsigned)bb};
+                  g.tiles_m, g.tiles_n, g.iters, g.dp_tiles, g.segs, (unsigned)ab, (unsigned)bb, NULL, NULL};
     p.res_mul = res_mul;
     int split_tiles = g.tiles_m * g.tiles_n - g.dp_tiles;
     if (g.segs > 1) {
@@ -282,6 +284,42 @@ void linear_fwd_ep(const float *x, const float *W, const float *b, const float *
 void linear_fwd_glu(const float *x, const float *W, const float *b, const float *mul, float *y,
                     int64_t batch, int M, int K, int act) {
     linear_forward("linear_fwd_glu", x, W, b, mul, 1, y, batch, M, K, act);
+}
+
+/* Both products of a gated unit in one GEMM launch when its tiles (64 rows x
+ * 32 output columns of each product) fill the CUs; otherwise the up product
+ * into a workspace, then the gate product with the multiply epilogue. */
+void linear_fwd_gated(const float *x, const float *Wg, const float *bg, const float *Wu, const float *bu, float *y,
+                      int64_t batch, int M, int K, int act) {
+    const char *fn = "linear_fwd_gated";
+    if (check_dims(fn, batch, M, K)) return;
+    if (act < NCM_ACT_NONE || act > NCM_ACT_GELU_TANH) {
+        ncm_fail(NCM_E_ARG, "%s: unknown activation %d", fn, act);
+        return;
+    }
+    if (batch == 0) return;
+    if (!x || !Wg || !Wu || !y || y == x) {
+        ncm_fail(NCM_E_ARG, "%s: null x/W/y, or y aliasing x", fn);
+        return;
+    }
+    if (ncm_ready()) return;
+    const int vec = (K % 4 == 0) && is_aligned16(x) && is_aligned16(Wg) && is_aligned16(Wu);
+    const int tiles_m = (int)((batch + TILE_M - 1) / TILE_M), tiles_n = (M + 31) / 32;
+    if (batch > 8 && batch <= INT_MAX && vec && (int64_t)tiles_m * tiles_n >= ncm_cu_count()) {
+        int64_t ab = extent(batch, K, K), bb = extent(M, K, K);
+        if (ab < MAX_BUFFER_BYTES && bb < MAX_BUFFER_BYTES) {
+            const int groups = (K + 4 * BK - 1) / (4 * BK);
+            GemmArgs p = {x, Wg, y, bg, NULL, NULL, (int)batch, M, K, K, K, M, act, 0,
+                          tiles_m, tiles_n, 4 * groups, tiles_m * tiles_n, 1, (unsigned)ab, (unsigned)bb, Wu, bu};
+            void *args[] = {&p};
+            ncm_launch_named("gemm_64x64_gated_v", (unsigned)(tiles_m * tiles_n), 1, 1, 256, args);
+            return;
+        }
+    }
+    float *u = (float *)ncm_workspace(WS_GATED, (size_t)batch * M * sizeof(float));
+    if (!u) return;
+    linear_forward(fn, x, Wu, bu, NULL, 0, u, batch, M, K, NCM_ACT_NONE);
+    linear_forward(fn, x, Wg, bg, u, 1, y, batch, M, K, act);
 }
 
 /* Kernel used for the dX of a batch <= 8 backward (transposed GEMV), or NULL. */

@@ -106,8 +106,8 @@ float *ncm_ncp_forward(const NcmNcpConfig *c, float *const *P, const int *ids, i
     mem_h2d(bids, ids, (size_t)R * sizeof(int));
     embedding_fwd_v(P[0], V, bids, x, R, C);
     float *ln = A(R * C), *qkv = A(R * QKV), *qq = A(R * C), *kk = A(R * C), *vv = A(R * C),
-          *mo = A(R * C), *g = A(R * I), *u = A(R * I);
-    if (!u) return NULL;
+          *mo = A(R * C), *g = A(R * I);
+    if (!g) return NULL;
     for (int li = 0; li < c->n_layer; li++) {
         float *const *w = P + 1 + NCP_PER_LAYER * li;
         norm(c, x, w[0], w[1], ln, R);
@@ -116,8 +116,7 @@ float *ncm_ncp_forward(const NcmNcpConfig *c, float *const *P, const int *ids, i
         sdpa_fwd_gqa_merged(qq, kk, vv, NULL, mo, B, H, H, S, S, hd);               /* heads merged on output */
         linear_fwd_ep(mo, w[4], w[5], x, x, R, C, C, NCM_ACT_NONE);      /* x += c_proj(.) */
         norm(c, x, w[6], w[7], ln, R);
-        linear_fwd(ln, w[10], w[11], u, R, I, C);
-        linear_fwd_glu(ln, w[8], w[9], u, g, R, I, C, NCM_ACT_SILU);     /* silu(w_gate(.)) * w_up(.) */
+        linear_fwd_gated(ln, w[8], w[9], w[10], w[11], g, R, I, C, NCM_ACT_SILU);   /* silu(w_gate(.)) * w_up(.) */
         linear_fwd_ep(g, w[12], w[13], x, x, R, C, I, NCM_ACT_NONE);     /* x += c_proj(.) */
     }
     const int n = ncm_ncp_param_count(c);

@@ -205,7 +205,7 @@ float *ncm_qwen_forward(NcmQwen *m, const int *ids, int T, int last_only) {
         float *h1 = A((int64_t)T * C), *ql = A((int64_t)T * C), *kl = A((int64_t)T * K * hd),
               *vl = A((int64_t)T * K * hd), *qq = A((int64_t)T * C), *kk = A((int64_t)T * K * hd),
               *vv = A((int64_t)T * K * hd), *ctx = A((int64_t)T * C), *mo = A((int64_t)T * C),
-              *x1 = A((int64_t)T * C), *h2 = A((int64_t)T * C), *up = A((int64_t)T * I),
+              *x1 = A((int64_t)T * C), *h2 = A((int64_t)T * C),
               *gu = A((int64_t)T * I), *out = A((int64_t)T * C);
         if (!out) return NULL;
         rmsnorm_fwd(h, w[0], h1, T, C);
@@ -225,8 +225,7 @@ float *ncm_qwen_forward(NcmQwen *m, const int *ids, int T, int last_only) {
         head_merge_fwd(ctx, mo, 1, T, C, H, hd);
         linear_fwd_ep(mo, w[7], NULL, h, x1, T, C, C, NCM_ACT_NONE);   /* x1 = h + mo W^T */
         rmsnorm_fwd(x1, w[8], h2, T, C);
-        linear_fwd(h2, w[10], NULL, up, T, I, C);
-        linear_fwd_glu(h2, w[9], NULL, up, gu, T, I, C, NCM_ACT_SILU);   /* silu(gate) * up */
+        linear_fwd_gated(h2, w[9], NULL, w[10], NULL, gu, T, I, C, NCM_ACT_SILU);   /* silu(gate) * up */
         linear_fwd_ep(gu, w[11], NULL, x1, out, T, C, I, NCM_ACT_NONE);
         h = out;
     }

@@ -52,6 +52,7 @@ _SIGS = {
     "linear_fwd": (None, [vp, vp, vp, vp, i64, ci, ci]),
     "linear_fwd_ep": (None, [vp, vp, vp, vp, vp, i64, ci, ci, ci]),
     "linear_fwd_glu": (None, [vp, vp, vp, vp, vp, i64, ci, ci, ci]),
+    "linear_fwd_gated": (None, [vp, vp, vp, vp, vp, vp, i64, ci, ci, ci]),
     "linear_bwd": (None, [vp, vp, vp, vp, vp, vp, i64, ci, ci]),
     "ncm_hip_linear_plan": (ci, [ci, i64, ci, ci, ctypes.c_char_p, sz]),
     "rowwise_l2sq": (None, [vp, vp, vp, i64, i64, ci]),

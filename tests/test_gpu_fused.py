@@ -42,6 +42,38 @@ def test_linear_glu_matches_unfused(batch, M, K, act):
         np.testing.assert_allclose(y.numpy(), ref, rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize("batch,M,K,act,bias", [(5184, 1024, 256, 1, True), (2048, 4864, 896, 1, False),
+                                                (300, 200, 96, 2, True), (70, 40, 8, 1, True), (5, 64, 32, 1, True),
+                                                (4096, 130, 36, 3, False)])
+def test_linear_gated_matches_glu_path(batch, M, K, act, bias):
+    """One launch for both products (when its tiles fill the CUs) against the up
+    GEMM followed by the multiply-epilogue gate GEMM: bit for bit where neither
+    of those splits K (the same MFMA sequence per output), else within the
+    oracle's tolerance."""
+    print(f"[gpu] gated batch={batch} M={M} K={K} act={act}", flush=True)
+    rng = np.random.default_rng(batch * 7 + M)
+    x = rng.standard_normal((batch, K)).astype(np.float32)
+    Wg = (rng.standard_normal((M, K)) / np.sqrt(K)).astype(np.float32)
+    Wu = (rng.standard_normal((M, K)) / np.sqrt(K)).astype(np.float32)
+    bg = (rng.standard_normal(M) * 0.1).astype(np.float32) if bias else None
+    bu = (rng.standard_normal(M) * 0.1).astype(np.float32) if bias else None
+    lib = ncmhip.load()
+    dx, dg, du = D.from_numpy(x), D.from_numpy(Wg), D.from_numpy(Wu)
+    dbg, dbu = (D.from_numpy(bg), D.from_numpy(bu)) if bias else (None, None)
+    pg, pu = (dbg.ptr, dbu.ptr) if bias else (None, None)
+    y, u, g = D.empty((batch, M)), D.empty((batch, M)), D.empty((batch, M))
+    lib.linear_fwd_gated(dx.ptr, dg.ptr, pg, du.ptr, pu, y.ptr, batch, M, K, act)
+    lib.linear_fwd(dx.ptr, du.ptr, pu, u.ptr, batch, M, K)
+    lib.linear_fwd_glu(dx.ptr, dg.ptr, pg, u.ptr, g.ptr, batch, M, K, act)
+    ncmhip.check()
+    got = y.numpy()
+    if ncmhip.linear_plan("fwd", batch, M, K)[1] == 1:
+        assert bits_equal(got, g.numpy())
+    name = {1: "silu", 2: "gelu", 3: "gelu_tanh"}[act]
+    ref = O.mul(O.act(name, O.linear_fwd(x, Wg, bg)), O.linear_fwd(x, Wu, bu))
+    np.testing.assert_allclose(got, ref, rtol=2e-4, atol=2e-4)
+
+
 def test_linear_glu_refuses_an_aliased_multiplier():
     lib = ncmhip.load()
     x, W, y = D.empty((16, 8)), D.empty((4, 8)), D.empty((16, 4))

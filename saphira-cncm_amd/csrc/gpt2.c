@@ -154,8 +154,8 @@ float ncm_gpt2_train_step(NcmTape *tp, const NcmGpt2Config *c, float *const *P, 
         const double lr = base_lr * sched_cosine_warmup(step, warmup, total);
         const double b1t = 1.0 - pow(b1, (double)step), b2t = 1.0 - pow(b2, (double)step);
         for (int i = 0; i < n; i++) {
-            adamw_update(P[i], G[i], M[i], Vm[i], sizes[i], lr, b1, b2, b1t, b2t, eps, wd);
-            ncm_zero_async(G[i], (size_t)sizes[i] * sizeof(float));
+            /* the update also clears the gradient for the next step */
+            ncm_adamw_update_clear(P[i], G[i], M[i], Vm[i], sizes[i], lr, b1, b2, b1t, b2t, eps, wd);
         }
     }
     free(sizes);

@@ -42,6 +42,11 @@ int ncm_zero_async(void *d, size_t n);
 int ncm_sample_launch(const float *x, int V, float temp, int top_k, float top_p, unsigned long long *rng,
                       int *out, int *ids, int *pos, int *flag, void *ws);
 size_t ncm_sample_ws_bytes(int V);
+
+/* adamw_update that also zeroes g after reading it (the training driver's
+ * step; the gradient is consumed and the next step accumulates from zero). */
+void ncm_adamw_update_clear(float *p, float *g, float *m, float *v, int64_t n, double lr, double b1, double b2,
+                            double b1t, double b2t, double eps, double wd);
 /* Compute units of the selected device. */
 int ncm_cu_count(void);
 void *ncm_workspace(int slot, size_t bytes);

@@ -171,14 +171,24 @@ void sdpa_bwd_gqa(const float *q, const float *k, const float *v, const float *P
 }
 
 /* ---- optimizer (train.c:51-64, 102-145, 172-178; train_gpt2.c:160-173) ---- */
-void adamw_update(float *p, const float *g, float *m, float *v, int64_t n, double lr, double b1, double b2,
-                  double b1t, double b2t, double eps, double wd) {
+static void adamw_any(float *p, float *g, float *m, float *v, int64_t n, double lr, double b1, double b2,
+                      double b1t, double b2t, double eps, double wd, int clear_g) {
     if (n < 0 || (n + 255) / 256 > UINT_MAX) { ncm_fail(NCM_E_ARG, "adamw_update: bad size"); return; }
     if (n == 0) return;
     if (!p || !g || !m || !v) { ncm_fail(NCM_E_ARG, "adamw_update: null pointer"); return; }
     if (ncm_ready()) return;
-    void *a[] = {&p, &g, &m, &v, &n, &lr, &b1, &b2, &b1t, &b2t, &eps, &wd};
+    void *a[] = {&p, &g, &m, &v, &n, &lr, &b1, &b2, &b1t, &b2t, &eps, &wd, &clear_g};
     ncm_launch_named("adamw_k", blocks_of(n, 256), 1, 1, 256, a);
+}
+
+void adamw_update(float *p, const float *g, float *m, float *v, int64_t n, double lr, double b1, double b2,
+                  double b1t, double b2t, double eps, double wd) {
+    adamw_any(p, (float *)g, m, v, n, lr, b1, b2, b1t, b2t, eps, wd, 0);   /* g is only read */
+}
+
+void ncm_adamw_update_clear(float *p, float *g, float *m, float *v, int64_t n, double lr, double b1, double b2,
+                            double b1t, double b2t, double eps, double wd) {
+    adamw_any(p, g, m, v, n, lr, b1, b2, b1t, b2t, eps, wd, 1);
 }
 
 double sched_cosine_warmup(long step, double warmup, double total) {

@@ -223,12 +223,13 @@ ce_bwd_k(const float *__restrict__ probs, const int *__restrict__ tgt, const flo
 // in fp64 rounded to float, bias-corrected step in fp64.  Bit-identical to
 // the host loop (train.c:131-141): IEEE double ops with contraction off.
 extern "C" __global__ void __launch_bounds__(256)
-adamw_k(float *__restrict__ p, const float *__restrict__ g, float *__restrict__ m, float *__restrict__ v,
-        int64_t n, double lr, double b1, double b2, double b1t, double b2t, double eps, double wd) {
+adamw_k(float *__restrict__ p, float *__restrict__ g, float *__restrict__ m, float *__restrict__ v,
+        int64_t n, double lr, double b1, double b2, double b1t, double b2t, double eps, double wd, int clear_g) {
 #pragma clang fp contract(off)
     const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (k >= n) return;
     const float gk = g[k];
+    if (clear_g) g[k] = 0.0f;   // the gradient, consumed, starts the next step at zero
     float pk = p[k];
     pk = pk - (float)(lr * wd * (double)pk);
     const float mk = (float)(b1 * (double)m[k] + (1.0 - b1) * (double)gk);

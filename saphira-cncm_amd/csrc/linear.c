@@ -178,6 +178,8 @@ static int run_gemm(int kind, const float *A, const float *B, float *C, const fl
                     int act, int vec) {
     if (Mo <= 0 || No <= 0) return 0;
     const int bm = TILE_M, bn = TILE_N;
+    if ((int64_t)((Mo + bm - 1) / bm) * ((No + bn - 1) / bn) > INT_MAX / 4)
+        return ncm_fail(NCM_E_ARG, "linear: %d x %d output has too many tiles", Mo, No);
     char name[48], fix[48];
     gemm_name(bm, bn, kind, vec, name, sizeof name);
     int slots = gemm_slots(name);
@@ -305,7 +307,8 @@ void linear_fwd_gated(const float *x, const float *Wg, const float *bg, const fl
     if (ncm_ready()) return;
     const int vec = (K % 4 == 0) && is_aligned16(x) && is_aligned16(Wg) && is_aligned16(Wu);
     const int tiles_m = (int)((batch + TILE_M - 1) / TILE_M), tiles_n = (M + 31) / 32;
-    if (batch > 8 && batch <= INT_MAX && vec && (int64_t)tiles_m * tiles_n >= ncm_cu_count()) {
+    const int64_t tiles = (int64_t)tiles_m * tiles_n;
+    if (batch > 8 && batch <= INT_MAX && vec && tiles >= ncm_cu_count() && tiles <= INT_MAX / 4) {
         int64_t ab = extent(batch, K, K), bb = extent(M, K, K);
         if (ab < MAX_BUFFER_BYTES && bb < MAX_BUFFER_BYTES) {
             const int groups = (K + 4 * BK - 1) / (4 * BK);

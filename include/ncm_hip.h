@@ -156,6 +156,17 @@ void rowwise_l2sq(const float *a, const float *b, float *d2,
  * distance matrix.  idx is a device int32 array. */
 void vq_argmin(const float *a, const float *E, int *idx, int64_t rows, int V, int D);
 
+/* extension with no counterpart in the reference: vq_argmin for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments and the same codes as
+ * vq_argmin, but the search's scratch lives in a fixed 9 MiB device array
+ * that the library reserves per GPU for the life of the process, so no call
+ * allocates.  Limits: rows <= 262144, V <= 65536 (D <= 4096 as vq_argmin);
+ * larger shapes are refused with an error.  Calls on one GPU share the
+ * array: calls that overlap on one GPU (several host threads) race.
+ * Returns 0 or an error code. */
+int vq_argmin_noalloc(const float *a, const float *E, int *idx, int64_t rows, int V, int D);
+
 /* extension: the multiscale residual quantiser of vq_z_to_idx
  * (vq.c:378-500) for configurations whose every level has length L
  * (area/linear resampling are identities) and Phi disabled

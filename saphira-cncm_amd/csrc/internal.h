@@ -19,6 +19,8 @@ int ncm_fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)
 /* 0 when the runtime is usable, otherwise an error code (already recorded). */
 int ncm_ready(void);
 hipStream_t ncm_stream(void);
+/* The device selected by ncm_hip_init. */
+int ncm_device(void);
 
 /* Looks up a kernel of one of the embedded code objects by name (cached). */
 hipFunction_t ncm_kernel(const char *name);

@@ -3,6 +3,7 @@
  * policy, and the ncm.h memory substrate (Tensor, arenas, mem_* copies) that
  * the reference implements in src/tensor.c. */
 #include "internal.h"
+#include "noalloc.h"
 
 #include <stdarg.h>
 #include <stdio.h>
@@ -58,6 +59,10 @@ int ncm_hip_init(int device) {
     if (device < 0 || device >= n)
         return ncm_fail(NCM_E_INIT, "device %d out of range (%d devices)", device, n);
     HIP_TRY(hipSetDevice(device));
+    /* the fixed device array behind the allocation-free entry points: its
+     * address on this device, looked up once with the device current (a
+     * failure is reported by those entry points, not here) */
+    (void)ncm_noalloc_setup(device);
     hipDeviceProp_t prop;
     HIP_TRY(hipGetDeviceProperties(&prop, device));
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
@@ -78,6 +83,7 @@ int ncm_ready(void) {
 }
 
 hipStream_t ncm_stream(void) { return g_stream; }
+int ncm_device(void) { return g_device; }
 void *ncm_hip_stream(void) { return ncm_ready() ? NULL : (void *)g_stream; }
 
 void ncm_hip_sync(void) {

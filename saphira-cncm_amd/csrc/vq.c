@@ -4,6 +4,8 @@
 
 #include <limits.h>
 
+#include "noalloc.h"
+
 /* Must match struct VqArgs in vq.hip. */
 typedef struct {
     const float *X;
@@ -39,31 +41,39 @@ typedef struct {
 
 static size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
 
-static int vq_scratch(VqScratch *s, int rows, int V) {
-    size_t off_cn = 256;
-    size_t off_xn = off_cn + al256((size_t)V * 4);
-    size_t off_fl = off_xn + al256((size_t)rows * 4);
-    size_t off_pr = off_fl + al256((size_t)rows * 4);
-    size_t off_ky = off_pr + al256((size_t)rows * 12);
-    size_t off_dn = off_ky + al256((size_t)rows * 8);
-    size_t total = off_dn + (size_t)rows * 4;
-    unsigned char *base = (unsigned char *)ncm_workspace(WS_VQ, total);
+/* Byte offsets of the scratch parts for (rows, V); returns the total. */
+static size_t vq_scratch_layout(int rows, int V, size_t off[6]) {
+    off[0] = 256;                                  /* cn */
+    off[1] = off[0] + al256((size_t)V * 4);        /* xn */
+    off[2] = off[1] + al256((size_t)rows * 4);     /* flags */
+    off[3] = off[2] + al256((size_t)rows * 4);     /* pairs */
+    off[4] = off[3] + al256((size_t)rows * 12);    /* keys */
+    off[5] = off[4] + al256((size_t)rows * 8);     /* done */
+    return off[5] + (size_t)rows * 4;
+}
+
+/* Carves the scratch from base (at least vq_scratch_layout bytes) or, when
+ * base is NULL, from the library's workspace. */
+static int vq_scratch(VqScratch *s, int rows, int V, unsigned char *base) {
+    size_t off[6];
+    size_t total = vq_scratch_layout(rows, V, off);
+    if (!base) base = (unsigned char *)ncm_workspace(WS_VQ, total);
     if (!base) return NCM_E_OOM;
     s->counters = (unsigned *)base;
-    s->cn = (float *)(base + off_cn);
-    s->xn = (float *)(base + off_xn);
-    s->flags = (int *)(base + off_fl);
-    s->pairs = (int *)(base + off_pr);
-    s->keys = (unsigned long long *)(base + off_ky);
-    s->done = (unsigned *)(base + off_dn);
+    s->cn = (float *)(base + off[0]);
+    s->xn = (float *)(base + off[1]);
+    s->flags = (int *)(base + off[2]);
+    s->pairs = (int *)(base + off[3]);
+    s->keys = (unsigned long long *)(base + off[4]);
+    s->done = (unsigned *)(base + off[5]);
     return 0;
 }
 
 /* codes of `rows` rows of X against E, written at idx[(row/L)*total + off + row%L] */
 static int vq_search(const float *X, const float *E, int *idx, int rows, int V, int D, int L,
-                     int total, int off) {
+                     int total, int off, unsigned char *scratch) {
     VqScratch s;
-    if (vq_scratch(&s, rows, V)) return NCM_E_OOM;
+    if (vq_scratch(&s, rows, V, scratch)) return NCM_E_OOM;
     int rc;
     void *a0[] = {&s.counters};
     if ((rc = ncm_launch_named("vq_init", 1, 1, 1, 64, a0))) return rc;
@@ -99,7 +109,33 @@ void vq_argmin(const float *a, const float *E, int *idx, int64_t rows, int V, in
         return;
     }
     if (ncm_ready()) return;
-    vq_search(a, E, idx, (int)rows, V, D, (int)rows, (int)rows, 0);
+    vq_search(a, E, idx, (int)rows, V, D, (int)rows, (int)rows, 0, NULL);
+}
+
+/* vq_argmin with its scratch in the library's fixed device array instead of
+ * a workspace: no allocation on any call (see noalloc.h for the limits).
+ * Every kernel of the search clears or overwrites the scratch it reads
+ * (vq_init zeroes the counters; each flagged row's key and counter are set
+ * when the row is flagged), so nothing carries over from the last call. */
+int vq_argmin_noalloc(const float *a, const float *E, int *idx, int64_t rows, int V, int D) {
+    int rc;
+    if ((rc = vq_check("vq_argmin_noalloc", rows, V, D))) return rc;
+    if (rows > NCM_NOALLOC_MAX_ROWS || V > NCM_NOALLOC_MAX_V)
+        return ncm_fail(NCM_E_ARG, "vq_argmin_noalloc: rows=%lld V=%d exceed the fixed scratch's limits rows <= %d, V <= %d",
+                        (long long)rows, V, NCM_NOALLOC_MAX_ROWS, NCM_NOALLOC_MAX_V);
+    if (rows == 0) return 0;
+    if (!a || !E || !idx) return ncm_fail(NCM_E_ARG, "vq_argmin_noalloc: null pointer");
+    if ((rc = ncm_ready())) return rc;
+    size_t off[6];
+    if (vq_scratch_layout((int)rows, V, off) > NCM_NOALLOC_SCRATCH_BYTES)
+        return ncm_fail(NCM_E_ARG, "vq_argmin_noalloc: scratch for rows=%lld V=%d exceeds %u bytes", (long long)rows,
+                        V, NCM_NOALLOC_SCRATCH_BYTES);
+    int err = 0;
+    unsigned char *base = (unsigned char *)ncm_noalloc_scratch(ncm_device(), &err);
+    if (!base)
+        return ncm_fail(NCM_E_INIT, "vq_argmin_noalloc: no fixed scratch on device %d (%s)", ncm_device(),
+                        err ? ncm_noalloc_error_string(err) : "lookup never ran");
+    return vq_search(a, E, idx, (int)rows, V, D, (int)rows, (int)rows, 0, base);
 }
 
 void vq_quantize_multiscale(const float *z, const float *const *E, const int *vocabs, int n_levels,
@@ -135,7 +171,7 @@ void vq_quantize_multiscale(const float *z, const float *const *E, const int *vo
     }
     for (int lv = 0; lv < n_levels; lv++) {
         int off = lv * L;
-        if (vq_search(z_rest, E[lv], idx, rows, vocabs[lv], D, L, total, off)) return;
+        if (vq_search(z_rest, E[lv], idx, rows, vocabs[lv], D, L, total, off, NULL)) return;
         const float *El = E[lv];
         int V = vocabs[lv];
         int first = lv == 0;
@@ -497,7 +533,7 @@ void vq_z_to_idx_dev(VQState *vq, const float *z, int B, int *idx, float *z_hat,
         if (vq->has_all && lv >= 1 && lv <= vq->n_levels - 2 && vq->drefW[lv] &&
             vqf_refine(vq, w.down, vq->drefW[lv], vq->drefB[lv], w.t1, B, tl))
             return;
-        if (vq_search(w.down, vq->E[lv], idx, B * tl, vq->vocabs[lv], D, tl, vq->total, off)) return;
+        if (vq_search(w.down, vq->E[lv], idx, B * tl, vq->vocabs[lv], D, tl, vq->total, off, NULL)) return;
         if (vqf_level_up(vq, idx, B, lv, off, &w)) return;
         int init = lv == 0;
         void *ua[] = {&w.zh, &w.zr, &w.up, (void *)&nL, &init};

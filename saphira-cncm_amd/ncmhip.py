@@ -57,6 +57,7 @@ _SIGS = {
     "ncm_hip_linear_plan": (ci, [ci, i64, ci, ci, ctypes.c_char_p, sz]),
     "rowwise_l2sq": (None, [vp, vp, vp, i64, i64, ci]),
     "vq_argmin": (None, [vp, vp, vp, i64, ci, ci]),
+    "vq_argmin_noalloc": (ci, [vp, vp, vp, i64, ci, ci]),
     "vq_quantize_multiscale": (None, [vp, ctypes.POINTER(vp), ctypes.POINTER(ci), ci, ci, ci, ci,
                                       vp, vp, vp]),
     "rmsnorm_fwd": (None, [vp, vp, vp, i64, ci]),
@@ -333,6 +334,13 @@ def rowwise_l2sq(a, b, d2, rows, cols, C):
 def vq_argmin(a, E, idx, rows, V, D):
     load().vq_argmin(_p(a), _p(E), _p(idx), rows, V, D)
     check()
+
+
+def vq_argmin_noalloc(a, E, idx, rows, V, D):
+    """vq_argmin with the library's fixed device scratch (no allocation); returns its status."""
+    rc = load().vq_argmin_noalloc(_p(a), _p(E), _p(idx), rows, V, D)
+    check()
+    return rc
 
 
 def vq_quantize_multiscale(z, Es, vocabs, B, L, D, idx, z_hat, z_rest):

@@ -121,7 +121,7 @@ def extras(ncmhip, only=EXTRAS):
     def _ncp_fwd():
         # -- config 1: NCP forward, 64 boards x 81 tokens
         n_layer, C, H, Kv, I, V, B, S = 4, 256, 4, 2, 1024, 16, 64, 81
-        cfg = ncmhip.NcpConfig(n_layer, C, H, Kv, I, V, 10000, 0)
+        cfg = ncmhip.NcpConfig(n_layer, C, H, Kv, I, V, 10000)
         shapes = [ncmhip_shape(lib.ncm_ncp_param_shape, cfg, i) for i in range(lib.ncm_ncp_param_count(ctypes.byref(cfg)))]
         bufs = [normal(sh, mean=1.0 if is_gain(i, len(shapes), 14, (0, 6), 4) else 0.0) for i, sh in enumerate(shapes)]
         ids = rng.integers(0, V, (B, S)).astype(np.int32)

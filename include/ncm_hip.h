@@ -426,10 +426,11 @@ int ncm_qwen_generate_sample(NcmQwen *m, const int *prompt, int np, int n_new, i
 /* config-1 driver: the NCP transformer forward of ncp.c               */
 /* ------------------------------------------------------------------ */
 
+/* The block normalises with LayerNorm (eps 1e-6), as ncp_block always
+ * does (ncp.c:199, 277, 352-357): the reference's NCP has no RMSNorm variant. */
 typedef struct {
     int n_layer, n_embd, n_head, n_kv, n_inner, vocab;
-    int rope_base;   /* ncp.c build_rope base (10000) */
-    int use_rmsnorm; /* 0: LayerNorm eps 1e-6 as ncp.c:195-199; 1: RMSNorm */
+    int rope_base; /* ncp.c build_rope base (10000) */
 } NcmNcpConfig;
 
 /* flat parameter order (biases may be NULL): 0 wte [V][C]; per layer at

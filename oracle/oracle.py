@@ -584,6 +584,12 @@ def ref():
             "refg_embed_bwd": (None, [vp, vp, ci, vp, vp, vp, ctypes.c_longlong, ci]),
             "refg_split_bwd": (None, [vp] * 8 + [ci] * 7),
             "refg_merge_bwd": (None, [ci, vp, vp, vp, vp] + [ci] * 5),
+            "refg_qwen_open": (vp, [ctypes.c_char_p, ci, ci, ci, ci, ci, ctypes.c_double]),
+            "refg_qwen_forward": (ci, [vp, vp, ci, ci, vp]),
+            "refg_qwen_generate": (ci, [vp, vp, ci, ci, vp]),
+            "refg_qwen_close": (None, [vp]),
+            "refg_ncp_forward": (ci, [vp, ci, vp, vp, ci, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(vp),
+                                      vp, vp, ci, vp, vp, ci, vp]),
         }
         for n, (r, a) in sigs.items():
             f = getattr(L, n)
@@ -888,9 +894,11 @@ def qwen_shapes(n_layer, C, H, K, I, V):
     return [(V, C)] + per * n_layer + [(C,)]
 
 
-def qwen_forward(params, n_layer, C, H, K, I, V, theta, ids, last_only=False, tables=None):
+def qwen_forward(params, n_layer, C, H, K, I, V, theta, ids, last_only=False, tables=None, cache=None):
     """The reference forward op for op with the pinned oracle functions;
-    returns logits [T][V] (or [V] for the last row)."""
+    returns logits [T][V] (or [V] for the last row).  Bit-equal to the
+    reference's own qwen_forward (tests/test_oracle_models.py).  cache: a list
+    that receives each layer's post-RoPE keys and values ([K][T][hd] each)."""
     ids = np.ascontiguousarray(ids, np.int32)
     T, hd = ids.size, C // H
     P = [_f32(p) for p in params]
@@ -907,6 +915,8 @@ def qwen_forward(params, n_layer, C, H, K, I, V, theta, ids, last_only=False, ta
         vv = heads_transpose(vl.reshape(1, T, K * hd), 1, T, K, hd)
         qq = rope(qq.reshape(-1, hd), cos_t, sin_t, T).reshape(qq.shape)
         kk = rope(kk.reshape(-1, hd), cos_t, sin_t, T).reshape(kk.shape)
+        if cache is not None:
+            cache.append((kk[0].copy(), vv[0].copy()))
         ctx = sdpa_gqa(qq, kk, vv, mask)
         mo = head_merge(ctx, 1, T, C, H, hd).reshape(T, C)
         x1 = h + linear_fwd(mo, w[7], None)
@@ -937,6 +947,51 @@ def qwen_generate(params, n_layer, C, H, K, I, V, theta, prompt, n_new, eos=-1, 
 
 
 
+def qwen_generate_cached(params, n_layer, C, H, K, I, V, theta, prompt, n_new, eos=-1, n_ctx=None, keep=8):
+    """qwen_generate with temp 0 (qwen.c:204-228) computing one new row per
+    step against cached keys and values instead of the reference's full
+    recompute.  Bit-equal to qwen_generate: every op is row-separable (the
+    same float operations on the same row), a cached row's key and value
+    equal the recomputed ones, and the masked columns the recompute adds
+    (-1e9) contribute exact zeros to the max, the sum and the output.
+    Returns (ids, per-step (top ids, top logits) of the `keep` largest)."""
+    prompt = np.ascontiguousarray(prompt, np.int32)
+    hd = C // H
+    P = [_f32(p) for p in params]
+    tables = rope_tables_qwen(n_ctx or prompt.size + n_new, hd, theta)
+    cache = []
+    lg = qwen_forward(P, n_layer, C, H, K, I, V, theta, prompt, True, tables, cache)
+    kc = [np.concatenate([k, np.zeros((K, n_new, hd), np.float32)], axis=1) for k, _ in cache]
+    vc = [np.concatenate([v, np.zeros((K, n_new, hd), np.float32)], axis=1) for _, v in cache]
+    out, tops = [], []
+    n = prompt.size
+    for s in range(n_new):
+        top = np.argsort(-lg, kind="stable")[:keep]
+        tops.append((top.astype(np.int32), lg[top].copy()))
+        nx = argmax_row(lg)
+        out.append(nx)
+        if nx == eos or s + 1 == n_new:
+            break
+        # one row at position n for token nx
+        cs, sn = tables[0][n:n + 1], tables[1][n:n + 1]
+        h = embedding(P[0], np.array([nx], np.int32))
+        for li in range(n_layer):
+            w = P[1 + 12 * li:13 + 12 * li]
+            h1 = rmsnorm(h, w[0])
+            q = rope(linear_fwd(h1, w[1], w[2]).reshape(H, hd), cs, sn, 1)
+            kc[li][:, n] = rope(linear_fwd(h1, w[3], w[4]).reshape(K, hd), cs, sn, 1)
+            vc[li][:, n] = linear_fwd(h1, w[5], w[6]).reshape(K, hd)
+            ctx = sdpa_gqa(q.reshape(1, H, 1, hd), kc[li][None, :, :n + 1].copy(),
+                           vc[li][None, :, :n + 1].copy())
+            x1 = h + linear_fwd(ctx.reshape(1, C), w[7], None)
+            h2 = rmsnorm(x1, w[8])
+            gu = mul(act("silu", linear_fwd(h2, w[9], None)), linear_fwd(h2, w[10], None))
+            h = x1 + linear_fwd(gu, w[11], None)
+        lg = linear_fwd(rmsnorm(h, P[-1]), P[0], None)[0]
+        n += 1
+    return out, tops
+
+
 # ---- config 1: the NCP transformer forward (ncp.c:184-338) ----
 def rope_tables_ncp(S, hd, base):
     c = np.empty((S, hd), np.float32)
@@ -952,15 +1007,19 @@ def ncp_shapes(n_layer, C, H, Kv, I, V):
     return [(V, C)] + per * n_layer + [(C,), (C,), (V, C), (V,)]
 
 
-def ncp_forward(params, n_layer, C, H, Kv, I, V, ids, rope_base=10000, use_rmsnorm=False):
+def ncp_forward(params, n_layer, C, H, Kv, I, V, ids, rope_base=10000):
     """ncp_block x n_layer + ln_f + head on one level of S tokens, op for op
-    with the pinned oracle functions (None entries = absent biases)."""
+    with the pinned oracle functions (None entries = absent biases).  Equal
+    bit for bit to the reference's ncp_load + ncp_forward (ncp.c:94-175,
+    480-640) on one-hot inputs through wte = params[0]^T, no prefix, levels
+    {1, S} (level 0 not a target), a zero level embedding and one untied
+    head (tests/test_oracle_models.py)."""
     ids = np.ascontiguousarray(ids, np.int32)
     B, S = ids.shape
     hd, R = C // H, B * S
     P = [None if p is None else _f32(p) for p in params]
     cos_t, sin_t = rope_tables_ncp(S, hd, rope_base)
-    nrm = (lambda x, w, b: rmsnorm(x, w)) if use_rmsnorm else (lambda x, w, b: layernorm(x, w, b))
+    nrm = layernorm
     x = embedding(P[0], ids.reshape(-1))
     for li in range(n_layer):
         w = P[1 + 14 * li:15 + 14 * li]
@@ -977,3 +1036,96 @@ def ncp_forward(params, n_layer, C, H, Kv, I, V, ids, rope_base=10000, use_rmsno
         x = x + linear_fwd(g, w[12], w[13])
     n = len(P)
     return linear_fwd(nrm(x, P[n - 4], P[n - 3]), P[n - 2], P[n - 1])
+
+
+# ---- the reference's own model code (libref: qwen.c via ref_glue_qwen.c, ncp.c) ----
+def write_ncm1(path, named):
+    """An NCM1 weights file (the layout weights_load reads, tensor.c:69-124):
+    "NCM1", u32 count, then per tensor u8 name length, name, u8 ndim, u32
+    dims, u64 byte count, float32 data (little-endian)."""
+    import struct
+    with open(path, "wb") as f:
+        f.write(b"NCM1" + struct.pack("<I", len(named)))
+        for name, a in named:
+            a = _f32(a)
+            nb = name.encode()
+            f.write(struct.pack("<B", len(nb)) + nb + struct.pack("<B", a.ndim))
+            f.write(b"".join(struct.pack("<I", d) for d in a.shape))
+            f.write(struct.pack("<Q", a.nbytes))
+            f.write(a.tobytes())
+
+
+def qwen_names(n_layer):
+    """The reference's tensor names (qwen.c:59-79) in qwen_shapes order."""
+    per = ["input_layernorm.weight", "self_attn.q_proj.weight", "self_attn.q_proj.bias",
+           "self_attn.k_proj.weight", "self_attn.k_proj.bias", "self_attn.v_proj.weight", "self_attn.v_proj.bias",
+           "self_attn.o_proj.weight", "post_attention_layernorm.weight", "mlp.gate_proj.weight",
+           "mlp.up_proj.weight", "mlp.down_proj.weight"]
+    return (["model.embed_tokens.weight"] + [f"model.layers.{li}.{n}" for li in range(n_layer) for n in per]
+            + ["model.norm.weight"])
+
+
+class RefQwen:
+    """The reference's qwen_open / qwen_forward / qwen_generate on a weights
+    file written from params (qwen_shapes order)."""
+
+    def __init__(self, params, n_layer, C, H, K, n_ctx, theta, path):
+        write_ncm1(path, list(zip(qwen_names(n_layer), params)))
+        self.V = params[0].shape[0]
+        self.h = ref().refg_qwen_open(path.encode(), n_layer, H, K, C, n_ctx, theta)
+        if not self.h:
+            raise RuntimeError("reference qwen_open failed")
+
+    def forward(self, ids, last_only=False):
+        ids = np.ascontiguousarray(ids, np.int32)
+        out = np.empty(self.V if last_only else ids.size * self.V, np.float32)
+        if ref().refg_qwen_forward(self.h, _ptr(ids), ids.size, int(last_only), _ptr(out)) != self.V:
+            raise RuntimeError("reference qwen_forward failed")
+        return out if last_only else out.reshape(ids.size, self.V)
+
+    def generate(self, prompt, n_new):
+        prompt = np.ascontiguousarray(prompt, np.int32)
+        out = np.zeros(max(n_new, 1), np.int32)
+        n = ref().refg_qwen_generate(self.h, _ptr(prompt), prompt.size, n_new, _ptr(out))
+        return [int(v) for v in out[:n]]
+
+    def close(self):
+        if self.h:
+            ref().refg_qwen_close(self.h)
+            self.h = None
+
+
+# NCMConfig fields refg_ncp_forward reads, in its cfg[] order (ref_glue.c)
+NCP_CFG_KEYS = ("n_layer", "n_head", "n_embd", "n_kv_heads", "prefix_len", "query_level0",
+                "attn_pattern_block_diag", "use_rope", "rope_base", "use_qk_norm", "puc_enabled", "puc_kernel",
+                "shared_output_head", "shared_head_per_level_bias", "untied_head_bias", "tie_heads_to_codebook",
+                "use_swiglu", "use_geglu", "use_relu2", "vq_embed_dim", "prefix_pad_token_id")
+
+
+def ref_ncp_forward(cfg, named, x, prefix_ids=None):
+    """The reference's ncp_load + ncp_forward (ncp.c:94-175, 480-640).
+    cfg: dict of NCP_CFG_KEYS plus levels (list) and vocab_size (list per
+    target level); named: dict name -> array; x [B][P+T][D].
+    Returns logits [B][T][max vocab]."""
+    x = _f32(x)
+    B = x.shape[0]
+    levels = np.ascontiguousarray(cfg["levels"], np.int32)
+    vocabs = np.ascontiguousarray(cfg["vocab_size"], np.int32)
+    c = np.ascontiguousarray([int(cfg.get(k, 0)) for k in NCP_CFG_KEYS], np.int32)
+    lvl_first = 0 if cfg.get("query_level0", 0) else 1
+    T = int(levels.sum()) - (0 if lvl_first == 0 else int(levels[0]))
+    names = list(named)
+    arrs = [_f32(named[n]) for n in names]
+    cn = (ctypes.c_char_p * len(names))(*[n.encode() for n in names])
+    dp = (vp * len(arrs))(*[a.ctypes.data for a in arrs])
+    shapes = np.zeros((len(arrs), 4), np.int64)
+    ndims = np.ascontiguousarray([a.ndim for a in arrs], np.int32)
+    for i, a in enumerate(arrs):
+        shapes[i, :a.ndim] = a.shape
+    pids = None if prefix_ids is None else np.ascontiguousarray(prefix_ids, np.int32)
+    out = np.empty((B, T, int(vocabs.max())), np.float32)
+    rc = ref().refg_ncp_forward(_ptr(c), levels.size, _ptr(levels), _ptr(vocabs), vocabs.size, cn, dp,
+                                _ptr(shapes), _ptr(ndims), len(arrs), _ptr(x), _ptr(pids), B, _ptr(out))
+    if rc:
+        raise RuntimeError("reference ncp_forward failed")
+    return out

@@ -347,3 +347,85 @@ float refg_gpt2_grads(float *const *params, float *const *grads, int n_layer, in
     free(c);
     return lh;
 }
+
+/* ---- the NCP transformer forward (ncp.c:94-175, 480-640) ----
+ * refg_ncp_forward fills an NCMConfig from cfg[] (indices below) and the
+ * level / vocabulary lists, a WeightStore from (names, data, shapes), and
+ * runs the reference's own ncp_load + ncp_forward: x [B][P+T][D] -> logits
+ * [B][T][maxV] (entries past a level's vocabulary are -inf, ncp.c:604).
+ * prefix_ids may be NULL (no pad bias). */
+enum {
+    NCPC_N_LAYER, NCPC_N_HEAD, NCPC_N_EMBD, NCPC_N_KV, NCPC_PREFIX_LEN, NCPC_QUERY_LEVEL0, NCPC_BLOCK_DIAG,
+    NCPC_USE_ROPE, NCPC_ROPE_BASE, NCPC_QK_NORM, NCPC_PUC, NCPC_PUC_KERNEL, NCPC_SHARED_HEAD,
+    NCPC_SHARED_HEAD_LEVEL_BIAS, NCPC_UNTIED_HEAD_BIAS, NCPC_TIE_CODEBOOK, NCPC_SWIGLU, NCPC_GEGLU, NCPC_RELU2,
+    NCPC_VQ_DIM, NCPC_PAD_ID, NCPC_COUNT
+};
+
+void refg_parena_once(void) {
+    /* the persistent arena is sized by its first user and never reset, so
+     * reserve room for every model a test process opens (malloc'd lazily) */
+    static int ready = 0;
+    if (!ready) {
+        parena_init((size_t)1 << 30);
+        ready = 1;
+    }
+}
+
+int refg_ncp_forward(const int *cfg, int n_qlevels, const int *levels, const int *vocabs, int n_vocabs,
+                     const char *const *names, float *const *data, const long long *shapes, const int *ndims,
+                     int n_tensors, const float *x, const int *prefix_ids, int B, float *logits) {
+    if (n_qlevels <= 0 || n_qlevels > NCM_MAX_LEVELS || n_vocabs > NCM_MAX_VOCAB_LIST) return -1;
+    refg_parena_once();
+    ensure_arena();
+    arena_reset();
+    NCMConfig *c = (NCMConfig *)calloc(1, sizeof(NCMConfig));
+    c->n_layer = cfg[NCPC_N_LAYER];
+    c->n_head = cfg[NCPC_N_HEAD];
+    c->n_embd = cfg[NCPC_N_EMBD];
+    c->n_kv_heads = cfg[NCPC_N_KV];
+    c->prefix_len = cfg[NCPC_PREFIX_LEN];
+    c->query_level0 = cfg[NCPC_QUERY_LEVEL0];
+    c->attn_pattern_block_diag = cfg[NCPC_BLOCK_DIAG];
+    c->use_rope = cfg[NCPC_USE_ROPE];
+    c->rope_base = cfg[NCPC_ROPE_BASE];
+    c->use_qk_norm = cfg[NCPC_QK_NORM];
+    c->puc_enabled = cfg[NCPC_PUC];
+    c->puc_kernel = cfg[NCPC_PUC_KERNEL];
+    c->shared_output_head = cfg[NCPC_SHARED_HEAD];
+    c->shared_head_per_level_bias = cfg[NCPC_SHARED_HEAD_LEVEL_BIAS];
+    c->untied_head_bias = cfg[NCPC_UNTIED_HEAD_BIAS];
+    c->tie_heads_to_codebook = cfg[NCPC_TIE_CODEBOOK];
+    c->use_swiglu = cfg[NCPC_SWIGLU];
+    c->use_geglu = cfg[NCPC_GEGLU];
+    c->use_relu2 = cfg[NCPC_RELU2];
+    c->vq_embed_dim = cfg[NCPC_VQ_DIM];
+    c->prefix_pad_token_id = cfg[NCPC_PAD_ID];
+    c->n_qlevels = n_qlevels;
+    for (int i = 0; i < n_qlevels; i++) c->levels[i] = levels[i];
+    for (int i = 0; i < n_vocabs; i++) c->vocab_size[i] = vocabs[i];
+    WeightStore ws;
+    ws.count = n_tensors;
+    ws.items = (NamedTensor *)calloc((size_t)n_tensors, sizeof(NamedTensor));
+    Tensor *ts = (Tensor *)calloc((size_t)n_tensors, sizeof(Tensor));
+    for (int i = 0; i < n_tensors; i++) {
+        snprintf(ws.items[i].name, sizeof(ws.items[i].name), "%s", names[i]);
+        ts[i].data = data[i];
+        ts[i].ndim = ndims[i];
+        int64_t n = 1;
+        for (int d = 0; d < ndims[i]; d++) {
+            ts[i].shape[d] = shapes[4 * i + d];
+            n *= shapes[4 * i + d];
+        }
+        ts[i].n = n;
+        ws.items[i].t = &ts[i];
+    }
+    NCPState *m = ncp_load(c, &ws, NULL);
+    arena_reset();
+    ncp_forward(m, x, prefix_ids, logits, B);
+    arena_reset();
+    ncp_free(m);
+    free(ts);
+    free(ws.items);
+    free(c);
+    return 0;
+}

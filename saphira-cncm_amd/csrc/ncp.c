@@ -6,8 +6,7 @@
  * Block: norm -> c_attn (fused q | k | v, GQA) -> split with the kv heads
  * replicated to all query heads -> RoPE -> SDPA -> merge -> c_proj ->
  * x += . -> norm -> SwiGLU (w_gate, w_up, silu, gate*up, c_proj) -> x += .
- * The norm is LayerNorm (eps 1e-6) as ncp.c:195-199 calls it, or RMSNorm
- * when use_rmsnorm is set.
+ * The norm is LayerNorm (eps 1e-6) as ncp.c:195-199 calls it.
  *
  * Parameters: one flat array of device pointers (biases may be NULL):
  * 0 wte [V][C]; per layer l at 1 + 14 l: ln_1.weight, ln_1.bias,
@@ -71,8 +70,7 @@ static float *A(int64_t n) {
 }
 
 static void norm(const NcmNcpConfig *c, const float *x, const float *w, const float *b, float *y, int64_t rows) {
-    if (c->use_rmsnorm) rmsnorm_fwd(x, w, y, rows, c->n_embd);
-    else layernorm_fwd(x, w, b, y, rows, c->n_embd);
+    layernorm_fwd(x, w, b, y, rows, c->n_embd);
 }
 
 /* ids HOST [B][S] -> logits [B*S][V] in the arena (arena_reset first, as

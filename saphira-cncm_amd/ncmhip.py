@@ -523,4 +523,4 @@ class NcpConfig(ctypes.Structure):
     """NcmNcpConfig of include/ncm_hip.h."""
     _fields_ = [("n_layer", ctypes.c_int), ("n_embd", ctypes.c_int), ("n_head", ctypes.c_int),
                 ("n_kv", ctypes.c_int), ("n_inner", ctypes.c_int), ("vocab", ctypes.c_int),
-                ("rope_base", ctypes.c_int), ("use_rmsnorm", ctypes.c_int)]
+                ("rope_base", ctypes.c_int)]

@@ -1,0 +1,218 @@
+"""Config 5 at its workload (12 layers, d 768, 12 heads, vocab 4096, 32 x 512
+tokens): the device tape's forward, mean cross-entropy and backward, checked
+against the oracle (bit-equal to the reference's host tape,
+train_tape.c:442-481, 569-634, 680-725, 936-1051) at the full R = 16384 rows
+on sampled slices, which the row/column separability of every reduction
+makes exact:
+
+- the step composed here from the exported ncm_t_* recorders (as
+  train_gpt2.c:42-147 does) gives the same loss and the same gradients, bit
+  for bit, as the library's ncm_gpt2_forward driver;
+- c_fc and mlp.c_proj of the first and last block: dW and db rows (sums over
+  all 16384 rows) and dx rows;
+- SDPA backward (causal, T = 512) on sampled (batch, head) slices: dq, dk, dv;
+- softmax cross-entropy: the loss over all rows and dlogits on sampled rows;
+- the tied head's dx rows and ln_f's dw, db (over all rows) and dx rows.
+
+Bars: |got - ref| <= 1e-4 (|ref| + 1) for GEMM outputs and norm gradients,
+<= 1e-3 for SDPA gradients (the north star's gradient bar); the loss to
+1e-5 relative."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import ncmhip
+import oracle as O
+from conftest import maxrel
+
+pytestmark = pytest.mark.gpu
+D = ncmhip.DeviceBuffer
+
+L, C, H, V, NPOS, B, T = 12, 768, 12, 4096, 512, 32, 512
+HD, R, I = C // H, B * T, 4 * C
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    ncmhip.init(0)
+    ncmhip.load().arena_init(24 << 30)
+    ncmhip.check()
+    print("[gpu] config-5 full-size gradient tests on device 0", flush=True)
+
+
+class PMap(ctypes.Structure):
+    _fields_ = [("params", ctypes.c_void_p), ("grads", ctypes.c_void_p), ("sizes", ctypes.c_void_p),
+                ("n", ctypes.c_int)]
+
+    def __init__(self, p, g, s, n):
+        self._keep = (p, g, s)
+        super().__init__(ctypes.cast(p, ctypes.c_void_p), ctypes.cast(g, ctypes.c_void_p),
+                         ctypes.cast(s, ctypes.c_void_p), n)
+
+
+def host(ptr, shape, dtype=np.float32):
+    out = np.empty(shape, dtype)
+    ncmhip.load().mem_d2h(out.ctypes.data, ptr, out.nbytes)
+    ncmhip.check()
+    return out
+
+
+def weights():
+    rng = np.random.default_rng(51)
+    shapes = O.gpt2_shapes(L, C, V, NPOS)
+    ps = [(rng.standard_normal(s, dtype=np.float32) * np.float32(0.02)) for s in shapes]
+    for i, s in enumerate(shapes):
+        if len(s) == 1 and s[0] == C and (i >= len(ps) - 2 or (i - 2) % 12 in (0, 6)):
+            ps[i] = ps[i] + np.float32(1.0)                          # LayerNorm gains
+    ids = rng.integers(0, V, (B, T)).astype(np.int32)
+    tgt = rng.integers(0, V, (B, T)).astype(np.int32)
+    return ps, ids, tgt
+
+
+@pytest.fixture(scope="module")
+def step():
+    """One composed step (activations kept) and one driver step."""
+    lib = ncmhip.load()
+    params, ids, tgt = weights()
+    P = [D.from_numpy(p) for p in params]
+    sizes = (ctypes.c_int64 * len(P))(*[p.size for p in params])
+    A = lambda n: lib.arena_alloc(n)  # noqa: E731
+
+    # -- the library's driver --
+    G1 = [D.from_numpy(np.zeros_like(p)) for p in params]
+    t1 = lib.ncm_tape_new()
+    lib.arena_reset()
+    cfg = ncmhip.Gpt2Config(L, C, H, V, NPOS)
+    logits1 = lib.ncm_gpt2_forward(t1, ctypes.byref(cfg), ncmhip.ptr_array(P), ids.ctypes.data, B, T)
+    ncmhip.check()
+    loss1 = D.empty(1)
+    lib.ncm_t_ce(t1, logits1, tgt.ctypes.data, None, loss1.ptr, None, R, V, 1.0)
+    lib.ncm_tape_backward(t1, ctypes.byref(PMap(ncmhip.ptr_array(P), ncmhip.ptr_array(G1), sizes, len(P))))
+    ncmhip.check()
+    g1 = [g.numpy() for g in G1]
+    l1 = float(loss1.numpy()[0])
+    lib.ncm_tape_free(t1)
+    del G1
+    print("[gpu] driver step done", flush=True)
+
+    # -- the same step from the recorders, keeping pointers --
+    lib.arena_reset()
+    tp = lib.ncm_tape_new()
+    G = [D.from_numpy(np.zeros_like(p)) for p in params]
+    pos = np.tile(np.arange(T, dtype=np.int32), B)
+    xe, pe, h = A(R * C), A(R * C), A(R * C)
+    lib.ncm_t_embed(tp, P[0].ptr, ids.ctypes.data, V, xe, R, C)
+    lib.ncm_t_embed(tp, P[1].ptr, pos.ctypes.data, NPOS, pe, R, C)
+    lib.ncm_t_add(tp, xe, pe, h, R * C)
+    mask_h = np.where(np.arange(T)[None, :] <= np.arange(T)[:, None], 0.0, -1e9).astype(np.float32)
+    mask = D.from_numpy(mask_h)
+    keep = {}
+    for li in range(L):
+        w = [P[2 + 12 * li + j].ptr for j in range(12)]
+        ln, qkv, qq, kk, vv, ctx = A(R * C), A(R * 3 * C), A(R * C), A(R * C), A(R * C), A(R * C)
+        mo, ao, x1, mn, mm, m2, mlpo, out = (A(R * C), A(R * C), A(R * C), A(R * C), A(R * I), A(R * I),
+                                             A(R * C), A(R * C))
+        lib.ncm_t_layernorm_eps(tp, h, w[0], w[1], ln, R, C, 1e-5)
+        lib.ncm_t_linear(tp, ln, w[2], w[3], qkv, R, 3 * C, C)
+        lib.ncm_t_qkvsplit(tp, qkv, qq, kk, vv, B, T, C, H, HD, H, 1)
+        lib.ncm_t_sdpa(tp, qq, kk, vv, mask.ptr, ctx, B, H, H, T, T, HD)
+        lib.ncm_t_headmerge(tp, ctx, mo, B, T, C, H, HD)
+        lib.ncm_t_linear(tp, mo, w[4], w[5], ao, R, C, C)
+        lib.ncm_t_add(tp, h, ao, x1, R * C)
+        lib.ncm_t_layernorm_eps(tp, x1, w[6], w[7], mn, R, C, 1e-5)
+        lib.ncm_t_linear(tp, mn, w[8], w[9], mm, R, I, C)
+        lib.ncm_t_gelu_tanh(tp, mm, m2, R * I)
+        lib.ncm_t_linear(tp, m2, w[10], w[11], mlpo, R, C, I)
+        lib.ncm_t_add(tp, x1, mlpo, out, R * C)
+        keep[li] = dict(qq=qq, kk=kk, vv=vv, ctx=ctx, mn=mn, mm=mm, m2=m2, mlpo=mlpo)
+        h = out
+    ncmhip.check()
+    n = len(P)
+    lnf, logits = A(R * C), A(R * V)
+    lib.ncm_t_layernorm_eps(tp, h, P[n - 2].ptr, P[n - 1].ptr, lnf, R, C, 1e-5)
+    lib.ncm_t_linear(tp, lnf, P[0].ptr, None, logits, R, V, C)
+    loss = D.empty(1)
+    lib.ncm_t_ce(tp, logits, tgt.ctypes.data, None, loss.ptr, None, R, V, 1.0)
+    lib.ncm_tape_backward(tp, ctypes.byref(PMap(ncmhip.ptr_array(P), ncmhip.ptr_array(G), sizes, len(P))))
+    ncmhip.check()
+    print("[gpu] composed step done", flush=True)
+    st = dict(lib=lib, tp=tp, params=params, ids=ids, tgt=tgt, G=G, g1=g1, l1=l1, loss=float(loss.numpy()[0]),
+              keep=keep, h=h, lnf=lnf, logits=logits, grad=lambda p: lib.ncm_tape_grad(tp, p))
+    yield st
+    lib.ncm_tape_free(tp)
+
+
+def test_driver_equals_composed_step(step):
+    assert step["loss"] == step["l1"]
+    for i, (g, r) in enumerate(zip(step["G"], step["g1"])):
+        assert np.array_equal(g.numpy().view(np.uint32), r.view(np.uint32)), i
+
+
+def sample(n, k, seed):
+    rng = np.random.default_rng(seed)
+    return np.unique(np.concatenate([[0, n - 1], rng.choice(n, k, replace=False)]))
+
+
+@pytest.mark.parametrize("li", [0, L - 1])
+def test_mlp_linears_full_rows(step, li):
+    params, G, keep = step["params"], step["G"], step["keep"][li]
+    for which, (xkey, ykey, wi, K, N) in {"c_fc": ("mn", "mm", 8, C, I), "c_proj": ("m2", "mlpo", 10, I, C)}.items():
+        x = host(keep[xkey], (R, K))
+        dy = host(step["grad"](keep[ykey]), (R, N))
+        W = params[2 + 12 * li + wi]
+        ms = sample(N, 30, li * 7 + wi)
+        _, dW, db = O.linear_bwd(x, W[ms], dy[:, ms], want=("dW", "db"))   # sums over all 16384 rows
+        gW, gb = G[2 + 12 * li + wi].numpy(), G[3 + 12 * li + wi].numpy()
+        print(f"[c5] layer {li} {which}: dW maxrel {maxrel(gW[ms], dW):.2e}, db {maxrel(gb[ms], db):.2e}")
+        assert maxrel(gW[ms], dW) <= 1e-4, (which, "dW", maxrel(gW[ms], dW))
+        assert maxrel(gb[ms], db) <= 1e-4, (which, "db", maxrel(gb[ms], db))
+        rs = sample(R, 30, li * 11 + wi)
+        dx, _, _ = O.linear_bwd(x[rs], W, dy[rs], want=("dx",))
+        # mn feeds only c_fc and m2 only c_proj: their gradients are these products' dx
+        got_dx = host(step["grad"](keep[xkey]), (R, K))[rs]
+        assert maxrel(got_dx, dx) <= 1e-4, (which, "dx", maxrel(got_dx, dx))
+
+
+@pytest.mark.parametrize("li", [0, L - 1])
+def test_sdpa_backward_t512_slices(step, li):
+    keep = step["keep"][li]
+    q, k, v = (host(keep[n], (B, H, T, HD)) for n in ("qq", "kk", "vv"))
+    dO = host(step["grad"](keep["ctx"]), (B, H, T, HD))
+    gq, gk, gv = (host(step["grad"](keep[n]), (B, H, T, HD)) for n in ("qq", "kk", "vv"))
+    mask = np.where(np.arange(T)[None, :] <= np.arange(T)[:, None], 0.0, -1e9).astype(np.float32)
+    for b, hh in ((0, 0), (B - 1, H - 1), (13, 5)):
+        sl = np.s_[b:b + 1, hh:hh + 1]
+        Pm = O.sdpa_probs(q[sl], k[sl], mask)
+        dq, dk, dv = O.sdpa_bwd(q[sl], k[sl], v[sl], Pm, dO[sl])
+        for name, got, ref in (("dq", gq[sl], dq), ("dk", gk[sl], dk), ("dv", gv[sl], dv)):
+            err = float(np.max(np.abs(got - ref)))
+            print(f"[c5] layer {li} sdpa ({b},{hh}) {name}: max-abs {err:.2e}, maxrel {maxrel(got, ref):.2e}")
+            assert err <= 1e-3 and maxrel(got, ref) <= 1e-4, (li, b, hh, name, err)
+
+
+def test_cross_entropy_full_rows(step):
+    logits = host(step["logits"], (R, V))
+    tgt = step["tgt"].reshape(-1)
+    loss, probs, cnt = O.ce_fwd(logits, tgt)
+    assert cnt == R
+    assert abs(step["loss"] - loss) <= 1e-5 * abs(loss)
+    rs = sample(R, 64, 3)
+    dl = O.ce_bwd(probs[rs], tgt[rs], None, 1.0 / cnt)
+    got = host(step["grad"](step["logits"]), (R, V))[rs]
+    assert float(np.max(np.abs(got - dl))) <= 1e-9, float(np.max(np.abs(got - dl)))
+
+
+def test_head_and_final_norm_full_rows(step):
+    params, G = step["params"], step["G"]
+    n = len(params)
+    dlog = host(step["grad"](step["logits"]), (R, V))
+    rs = sample(R, 30, 5)
+    dx, _, _ = O.linear_bwd(np.zeros((rs.size, C), np.float32), params[0], dlog[rs], want=("dx",))
+    dlnf = host(step["grad"](step["lnf"]), (R, C))
+    assert maxrel(dlnf[rs], dx) <= 1e-4
+    h = host(step["h"], (R, C))
+    dxn, dw, db = O.layernorm_bwd(h, params[n - 2], dlnf, eps=1e-5)      # dw, db over all rows
+    assert maxrel(G[n - 2].numpy(), dw) <= 1e-4 and maxrel(G[n - 1].numpy(), db) <= 1e-4
+    gh = host(step["grad"](step["h"]), (R, C))
+    assert maxrel(gh[rs], dxn[rs]) <= 1e-4

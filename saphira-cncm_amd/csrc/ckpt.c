@@ -220,20 +220,20 @@ static const char *in_str(In *r, size_t *len) {
 static unsigned char *read_checked(const char *path, In *r, size_t *len_out, int *sum_ok, char *err, size_t errcap) {
     FILE *f = fopen(path, "rb");
     if (!f) {
-        snprintf(err, errcap, "cannot open %s: %s", path, strerror(errno));
+        snprintf(err, errcap, "cannot open checkpoint %s: %s", path, strerror(errno));
         return NULL;
     }
     struct stat st;
     memset(&st, 0, sizeof st);
     if (fstat(fileno(f), &st) || st.st_size < 8 || (uint64_t)st.st_size > NCK1_MAX_FILE) {
-        snprintf(err, errcap, "%s: implausible size %lld", path, (long long)st.st_size);
+        snprintf(err, errcap, "%s: refused, %lld bytes is too small or too large for a checkpoint", path, (long long)st.st_size);
         fclose(f);
         return NULL;
     }
     size_t len = (size_t)st.st_size;
     unsigned char *buf = (unsigned char *)malloc(len);
     if (!buf || fmt_read_exact(f, buf, len)) {
-        snprintf(err, errcap, buf ? "%s: short read" : "%s: out of memory", path);
+        snprintf(err, errcap, buf ? "%s: cannot read the whole file" : "%s: cannot allocate a buffer for the file", path);
         free(buf);
         fclose(f);
         return NULL;
@@ -291,22 +291,22 @@ int ckpt_save_atomic(const WeightStore *ws, AdamW *opt, const CkptRunState *rs, 
     }
     err[0] = 0;
     if (!ws || !opt || !rs || !path) {
-        snprintf(err, errcap, "ckpt_save_atomic: null argument");
+        snprintf(err, errcap, "ckpt_save_atomic: refused, null argument");
         return -1;
     }
     if (rs->accum_pending != 0) {
-        snprintf(err, errcap, "refusing save with %d pending accumulation steps", rs->accum_pending);
+        snprintf(err, errcap, "save refused: %d gradient accumulation steps are still pending", rs->accum_pending);
         return -1;
     }
     adamw_sync_to_host(opt);
     char tmp[4096];
     if (snprintf(tmp, sizeof tmp, "%s.tmp.%d", path, (int)getpid()) >= (int)sizeof tmp) {
-        snprintf(err, errcap, "path too long");
+        snprintf(err, errcap, "ckpt_save_atomic: refused, path too long");
         return -1;
     }
     Out o = {fopen(tmp, "wb"), FNV_OFFSET, 0};
     if (!o.f) {
-        snprintf(err, errcap, "cannot write %s: %s", tmp, strerror(errno));
+        snprintf(err, errcap, "cannot create %s: %s", tmp, strerror(errno));
         return -1;
     }
     write_body(&o, ws, opt, rs);
@@ -319,7 +319,7 @@ int ckpt_save_atomic(const WeightStore *ws, AdamW *opt, const CkptRunState *rs, 
     if (fclose(o.f)) o.bad = 1;
     if (o.bad) {
         unlink(tmp);
-        snprintf(err, errcap, "failed writing %s; target %s untouched", tmp, path);
+        snprintf(err, errcap, "writing %s failed; %s was left as it was", tmp, path);
         return -1;
     }
     /* validate the new file by reading it back before it replaces anything */
@@ -333,7 +333,7 @@ int ckpt_save_atomic(const WeightStore *ws, AdamW *opt, const CkptRunState *rs, 
         wipe_free(buf, len);
         if (!ok) {
             unlink(tmp);
-            snprintf(err, errcap, "fresh file %s failed validation; target %s untouched", tmp, path);
+            snprintf(err, errcap, "%s did not verify after writing; %s was left as it was", tmp, path);
             return -1;
         }
     }
@@ -341,13 +341,13 @@ int ckpt_save_atomic(const WeightStore *ws, AdamW *opt, const CkptRunState *rs, 
     if (fd < 0 || fsync(fd)) {
         if (fd >= 0) close(fd);
         unlink(tmp);
-        snprintf(err, errcap, "fsync failed on %s", tmp);
+        snprintf(err, errcap, "cannot fsync %s", tmp);
         return -1;
     }
     close(fd);
     if (rename(tmp, path)) {
         unlink(tmp);
-        snprintf(err, errcap, "rename %s -> %s failed: %s", tmp, path, strerror(errno));
+        snprintf(err, errcap, "cannot rename %s to %s: %s", tmp, path, strerror(errno));
         return -1;
     }
     /* the rename itself must survive a crash: sync the directory */
@@ -374,7 +374,7 @@ int ckpt_load_training(const char *path, WeightStore *ws, AdamW *opt, const Ckpt
     }
     err[0] = 0;
     if (!path || !ws || !opt || !ex) {
-        snprintf(err, errcap, "ckpt_load_training: null argument");
+        snprintf(err, errcap, "ckpt_load_training: refused, null argument");
         return -1;
     }
     In r;
@@ -388,57 +388,57 @@ int ckpt_load_training(const char *path, WeightStore *ws, AdamW *opt, const Ckpt
     int rc = -1;
     Header h;
     if (!tdata || !mdata) {
-        snprintf(err, errcap, "out of memory");
+        snprintf(err, errcap, "cannot allocate memory for the checkpoint");
         goto done;
     }
     if (!sum_ok) {
-        snprintf(err, errcap, "%s: checksum mismatch (corrupt or truncated)", path);
+        snprintf(err, errcap, "%s: refused, the stored checksum does not match the contents (corrupt or truncated file)", path);
         goto done;
     }
     const unsigned char *magic = in_take(&r, 4);
     if (!magic || memcmp(magic, "NCK1", 4) != 0) {
-        snprintf(err, errcap, "%s: not an NCK1 checkpoint", path);
+        snprintf(err, errcap, "%s: refused, no NCK1 magic", path);
         goto done;
     }
     if (in_le(&r, 4) != NCK1_VERSION) {
-        snprintf(err, errcap, "%s: unsupported version (want %u)", path, NCK1_VERSION);
+        snprintf(err, errcap, "%s: refused, format version is not %u", path, NCK1_VERSION);
         goto done;
     }
     in_header(&r, &h);
     if (r.bad) {
-        snprintf(err, errcap, "%s: truncated header", path);
+        snprintf(err, errcap, "%s: refused, the run-state header is truncated", path);
         goto done;
     }
     if (h.rs.accum_pending != 0) {
-        snprintf(err, errcap, "%s: mid-accumulation checkpoint (pending=%d); not supported", path,
+        snprintf(err, errcap, "%s: refused, written with %d accumulation steps pending", path,
                  h.rs.accum_pending);
         goto done;
     }
     if (h.rs.batch_B != ex->batch_B || h.rs.n_rows != ex->n_rows || h.rs.row_len != ex->row_len ||
         h.rs.data_hash != ex->data_hash) {
-        snprintf(err, errcap, "%s: dataset mismatch (B/n_rows/row_len/hash)", path);
+        snprintf(err, errcap, "%s: refused, the training data differ from this run's (batch, rows, row_len or hash)", path);
         goto done;
     }
     if (h.rs.conf_hash != ex->conf_hash) {
-        snprintf(err, errcap, "%s: model config mismatch (conf hash)", path);
+        snprintf(err, errcap, "%s: refused, the model configuration hash differs", path);
         goto done;
     }
     {
         const char *want = ex->tokenizer_id ? ex->tokenizer_id : "";
         if (strlen(want) != h.tl || memcmp(want, h.tokid, h.tl) != 0) {
-            snprintf(err, errcap, "%s: tokenizer identity mismatch ('%.*s' vs '%s')", path, (int)h.tl, h.tokid,
+            snprintf(err, errcap, "%s: refused, tokenizer '%.*s' in the file, '%s' expected", path, (int)h.tl, h.tokid,
                      want);
             goto done;
         }
     }
     if (h.rs.base_lr != ex->base_lr || h.rs.warmup != ex->warmup || h.rs.total != ex->total) {
-        snprintf(err, errcap, "%s: schedule mismatch (lr/warmup/total)", path);
+        snprintf(err, errcap, "%s: refused, the learning-rate schedule differs (lr, warmup or total)", path);
         goto done;
     }
     /* tensors: names in store order, shapes and sizes as the live store's */
     uint32_t count = (uint32_t)in_le(&r, 4);
     if (r.bad || count != (uint32_t)ws->count) {
-        snprintf(err, errcap, "%s: tensor count mismatch (%u vs %d)", path, r.bad ? 0u : count, ws->count);
+        snprintf(err, errcap, "%s: refused, %u tensors in the file, %d in the model", path, r.bad ? 0u : count, ws->count);
         goto done;
     }
     for (int i = 0; i < ws->count; i++) {
@@ -446,27 +446,27 @@ int ckpt_load_training(const char *path, WeightStore *ws, AdamW *opt, const Ckpt
         size_t nl = (size_t)in_le(&r, 1);
         const char *nm = (const char *)in_take(&r, nl);
         if (r.bad || nl == 0) {
-            snprintf(err, errcap, "%s: truncated tensor section", path);
+            snprintf(err, errcap, "%s: refused, the tensor section is cut short", path);
             goto done;
         }
         if (strlen(ws->items[i].name) != nl || memcmp(nm, ws->items[i].name, nl) != 0) {
-            snprintf(err, errcap, "%s: tensor[%d] name/order mismatch ('%.*s')", path, i, (int)nl, nm);
+            snprintf(err, errcap, "%s: refused, tensor %d is '%.*s' (another name or order)", path, i, (int)nl, nm);
             goto done;
         }
         if ((int)in_le(&r, 1) != t->ndim) {
-            snprintf(err, errcap, "%s: tensor '%s' ndim mismatch", path, ws->items[i].name);
+            snprintf(err, errcap, "%s: refused, tensor '%s' has another rank", path, ws->items[i].name);
             goto done;
         }
         int shape_ok = 1;
         for (int d = 0; d < t->ndim; d++) shape_ok &= (int64_t)in_le(&r, 4) == t->shape[d];
         if (!shape_ok) {
-            snprintf(err, errcap, "%s: tensor '%s' shape mismatch", path, ws->items[i].name);
+            snprintf(err, errcap, "%s: refused, tensor '%s' has another shape", path, ws->items[i].name);
             goto done;
         }
         uint64_t nb = in_le(&r, 8);
         tdata[i] = nb == (uint64_t)t->n * 4u ? in_take(&r, nb) : NULL;
         if (!tdata[i]) {
-            snprintf(err, errcap, "%s: tensor '%s' size mismatch", path, ws->items[i].name);
+            snprintf(err, errcap, "%s: refused, tensor '%s' has another size", path, ws->items[i].name);
             goto done;
         }
     }
@@ -477,11 +477,11 @@ int ckpt_load_training(const char *path, WeightStore *ws, AdamW *opt, const Ckpt
     int64_t ostep = (int64_t)in_le(&r, 8);
     if (r.bad || tag != ADAM_TAG || on != (uint32_t)opt->n || b1 != ex->b1 || b2 != ex->b2 || eps != ex->eps ||
         wd != ex->wd) {
-        snprintf(err, errcap, "%s: optimizer mismatch (section/n/hyperparams)", path);
+        snprintf(err, errcap, "%s: refused, the optimizer section differs (tag, tensor count or hyperparameters)", path);
         goto done;
     }
     if (ostep < 0 || ostep > ((int64_t)1 << 40)) {
-        snprintf(err, errcap, "%s: implausible optimizer step %lld", path, (long long)ostep);
+        snprintf(err, errcap, "%s: refused, optimizer step %lld is out of range", path, (long long)ostep);
         goto done;
     }
     for (int i = 0; i < opt->n; i++) {
@@ -492,17 +492,17 @@ int ckpt_load_training(const char *path, WeightStore *ws, AdamW *opt, const Ckpt
         uint64_t vnb = in_le(&r, 8);
         mdata[2 * i + 1] = in_take(&r, vnb);
         if (r.bad) {
-            snprintf(err, errcap, "%s: truncated moments (param %d)", path, i);
+            snprintf(err, errcap, "%s: refused, the moments of tensor %d are cut short", path, i);
             goto done;
         }
         if (idx >= (uint32_t)ws->count || ws->items[idx].t->data != opt->params[i] ||
             mnb != (uint64_t)opt->sizes[i] * 4u || vnb != mnb || lrm != opt->lr[i]) {
-            snprintf(err, errcap, "%s: optimizer param %d mismatch (map/size/lr)", path, i);
+            snprintf(err, errcap, "%s: refused, optimizer entry %d differs (index, size or lr scale)", path, i);
             goto done;
         }
     }
     if (r.p != r.end) {
-        snprintf(err, errcap, "%s: trailing garbage (%ld bytes)", path, (long)(r.end - r.p));
+        snprintf(err, errcap, "%s: refused, %ld unexpected bytes after the last section", path, (long)(r.end - r.p));
         goto done;
     }
     /* every check passed: apply */
@@ -534,7 +534,7 @@ int ckpt_load_weights_only(const char *path, WeightStore *ws, char *err, size_t 
     }
     err[0] = 0;
     if (!path || !ws) {
-        snprintf(err, errcap, "ckpt_load_weights_only: null argument");
+        snprintf(err, errcap, "ckpt_load_weights_only: refused, null argument");
         return -1;
     }
     ws->items = NULL;
@@ -545,13 +545,13 @@ int ckpt_load_weights_only(const char *path, WeightStore *ws, char *err, size_t 
     unsigned char *buf = read_checked(path, &r, &len, &sum_ok, err, errcap);
     if (!buf) return -1;
     if (!sum_ok) {
-        snprintf(err, errcap, "%s: checksum mismatch", path);
+        snprintf(err, errcap, "%s: refused, the stored checksum does not match the contents", path);
         wipe_free(buf, len);
         return -1;
     }
     const unsigned char *magic = in_take(&r, 4);
     if (!magic || memcmp(magic, "NCK1", 4) != 0 || in_le(&r, 4) != NCK1_VERSION) {
-        snprintf(err, errcap, "%s: not an NCK1 checkpoint", path);
+        snprintf(err, errcap, "%s: refused, no NCK1 magic", path);
         wipe_free(buf, len);
         return -1;
     }
@@ -559,13 +559,13 @@ int ckpt_load_weights_only(const char *path, WeightStore *ws, char *err, size_t 
     in_header(&r, &h); /* skipped: the run state is not needed for inference */
     uint32_t n = (uint32_t)in_le(&r, 4);
     if (r.bad || n > (1u << 24)) {
-        snprintf(err, errcap, "%s: bad tensor count", path);
+        snprintf(err, errcap, "%s: refused, bad tensor count", path);
         wipe_free(buf, len);
         return -1;
     }
     ws->items = (NamedTensor *)calloc(n ? n : 1, sizeof(NamedTensor));
     if (!ws->items) {
-        snprintf(err, errcap, "out of memory");
+        snprintf(err, errcap, "cannot allocate memory for the checkpoint");
         wipe_free(buf, len);
         return -1;
     }
@@ -583,7 +583,7 @@ int ckpt_load_weights_only(const char *path, WeightStore *ws, char *err, size_t 
         const unsigned char *data = in_take(&r, nb);
         if (r.bad) goto fail;
         if ((uint64_t)tensor_numel((int)nd, shape) * 4u != nb) {
-            snprintf(err, errcap, "%s: tensor '%s' size mismatch", path, it->name);
+            snprintf(err, errcap, "%s: refused, tensor '%s' has another size", path, it->name);
             goto fail;
         }
         Tensor *t = tensor_alloc((int)nd, shape);
@@ -595,7 +595,7 @@ int ckpt_load_weights_only(const char *path, WeightStore *ws, char *err, size_t 
     wipe_free(buf, len);
     return 0;
 fail:
-    if (!err[0]) snprintf(err, errcap, "%s: truncated tensor section", path);
+    if (!err[0]) snprintf(err, errcap, "%s: refused, the tensor section is cut short", path);
     weights_free(ws);
     wipe_free(buf, len);
     return -1;

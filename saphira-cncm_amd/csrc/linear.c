@@ -424,6 +424,8 @@ int ncm_hip_linear_plan(int op, int64_t batch, int M, int K, char *kernel, size_
     int vec = op == L_FWD ? K % 4 == 0 : (M % 4 == 0 && K % 4 == 0);
     const int bm = TILE_M, bn = TILE_N;
     gemm_name(bm, bn, op, vec, kernel, cap);
+    if ((int64_t)((Mo + bm - 1) / bm) * ((No + bn - 1) / bn) > INT_MAX / 4)
+        return ncm_fail(NCM_E_ARG, "ncm_hip_linear_plan: %d x %d output has too many tiles", Mo, No), -1;
     int slots = gemm_slots(kernel);
     if (slots < 0) return -1;
     GemmPlan g = plan_gemm(Mo, No, Kred, slots, bm, bn);

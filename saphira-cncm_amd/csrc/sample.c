@@ -6,6 +6,7 @@
 #include "internal.h"
 
 #include <limits.h>
+#include <stdio.h>
 #include <string.h>
 
 #define SMP_NT 1024
@@ -206,5 +207,13 @@ int sample_topkp(const float *logits, int V, float temp, int top_k, float top_p,
         return 0;
     }
     g_last_flag = res[1];
+    if (res[1] != 0) {
+        /* not certified equal to the reference's draw (a draw within the
+         * rounding bound, about 1e-10 of draws, or non-finite logits): say so
+         * instead of diverging silently; the flag stays readable through
+         * ncm_hip_sample_flag */
+        fprintf(stderr, "ncmhip: sample_topkp: draw %d not certified against the CPU reference (flag %d)\n",
+                res[0], res[1]);
+    }
     return res[0];
 }

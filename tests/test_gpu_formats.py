@@ -288,17 +288,17 @@ def test_nck1_info_matches_reference(libs, tmp_path, capfd):
 
 REFUSALS = {
     # case: (how the file or expectation changes, message fragment)
-    "bitflip": ("flip", "checksum mismatch"),
-    "truncated": ("cut", "checksum mismatch"),
-    "tiny": ("tiny", "implausible size"),
-    "data_hash": ("ex:data_hash=1", "dataset mismatch"),
-    "rows": ("ex:n_rows=4999", "dataset mismatch"),
-    "conf": ("ex:conf_hash=2", "model config mismatch"),
-    "tokenizer": ("ex:tokenizer_id=b'llama'", "tokenizer identity mismatch"),
-    "lr": ("ex:base_lr=1e-3", "schedule mismatch"),
-    "wd": ("ex:wd=0.01", "optimizer mismatch"),
-    "pending": ("rs:accum_pending=2", "mid-accumulation"),
-    "garbage": ("garbage", "trailing garbage"),
+    "bitflip": ("flip", "checksum does not match"),
+    "truncated": ("cut", "checksum does not match"),
+    "tiny": ("tiny", "too small or too large"),
+    "data_hash": ("ex:data_hash=1", "training data differ"),
+    "rows": ("ex:n_rows=4999", "training data differ"),
+    "conf": ("ex:conf_hash=2", "configuration hash differs"),
+    "tokenizer": ("ex:tokenizer_id=b'llama'", "tokenizer 'gpt2' in the file"),
+    "lr": ("ex:base_lr=1e-3", "schedule differs"),
+    "wd": ("ex:wd=0.01", "optimizer section differs"),
+    "pending": ("rs:accum_pending=2", "accumulation steps pending"),
+    "garbage": ("garbage", "unexpected bytes"),
     "missing": ("missing", "cannot open"),
 }
 

@@ -11,6 +11,7 @@ import ctypes
 import numpy as np
 import pytest
 
+import model_data as MD
 import ncmhip
 import oracle as O
 
@@ -141,6 +142,38 @@ def test_full_size_cached_decode_matches_full_forward():
         step = m.decode(seq[-1], len(seq) - 1)
         assert float(np.max(np.abs(step - full))) <= 1e-3
         assert int(np.argmax(full)) == ids[3]
+    finally:
+        m.close()
+
+
+def test_config4_greedy_ids_256_steps_match_cpu(golden):
+    """Config 4 end to end: the seeded 24-layer model, a 2048-token prompt and
+    256 greedy steps give the CPU reference's ids exactly
+    (tests/golden/qwen_greedy_c4.npz, written by gen_qwen_greedy.py with the
+    oracle's KV-cached generation, which is bit-equal to the reference's
+    qwen_generate).  Also logs the device's logit error at each step's 8
+    largest CPU logits against the step's top-2 gap, the margin that keeps
+    the argmax exact."""
+    g = golden("qwen_greedy_c4.npz")
+    params = MD.qwen_weights(MD.C4_SEED, **MD.C4)
+    prompt = MD.c4_prompt()
+    m = Model(params, n_ctx=MD.C4_CTX, theta=MD.C4_THETA, **MD.C4)
+    try:
+        ids = m.generate(prompt, MD.C4_NEW)
+        first_diff = next((i for i, (a, b) in enumerate(zip(ids, g["ids"])) if a != b), None)
+        # the logits of every step along the CPU's ids, from the eager cached decode
+        err, gaps = [], g["top_vals"][:, 0].astype(np.float64) - g["top_vals"][:, 1]
+        lg = m.forward(prompt, last_only=True)
+        for s in range(MD.C4_NEW):
+            err.append(float(np.max(np.abs(lg[g["top_ids"][s]] - g["top_vals"][s]))))
+            if s + 1 < MD.C4_NEW:
+                lg = m.decode(int(g["ids"][s]), MD.C4_PROMPT + s)
+        err = np.array(err)
+        print(f"[c4] 256 greedy ids: first difference at {first_diff}; max logit error {err.max():.2e}; "
+              f"min top-2 gap {gaps.min():.2e} (step {int(gaps.argmin())}); min gap/error "
+              f"{float(np.min(gaps / np.maximum(err, 1e-12))):.1f}", flush=True)
+        assert first_diff is None and len(ids) == MD.C4_NEW
+        assert err.max() <= 1e-3
     finally:
         m.close()
 

@@ -101,6 +101,7 @@ def timed(ncmhip, fn, reps, warm=1):
 
 
 EXTRAS = ("ncp_fwd", "vq_multiscale", "vq_full", "qwen", "gpt2_train")
+QWEN_STEPS = 256   # greedy steps after the 2048-token prefill (config 4); --qwen-steps for profiling runs
 
 
 def extras(ncmhip, only=EXTRAS):
@@ -131,7 +132,9 @@ def extras(ncmhip, only=EXTRAS):
         R, hd = B * S, C // H
         fl = n_layer * (2 * R * C * (C + 2 * Kv * hd) + 2 * R * C * C + 3 * 2 * R * C * I + 4 * B * H * S * S * hd) \
             + 2 * R * C * V
-        out["ncp_fwd"] = {"config": "C1: 4 layers, d 256, 4/2 heads, SwiGLU 1024, vocab 16, 64 x 81 tokens",
+        out["ncp_fwd"] = {"config": "C1: 4 layers, d 256, 4/2 heads, SwiGLU 1024, vocab 16, 64 x 81 tokens; "
+                                    "pre-LayerNorm eps 1e-6 as the reference's ncp_block (ncp.c:199, 277), which "
+                                    "has no RMSNorm variant",
                           "tokens_per_s": round(R / (ms / 1e3), 1), "ms_per_forward": round(ms, 4),
                           "tflops": round(fl / (ms / 1e3) / 1e12, 3), "gflop": round(fl / 1e9, 3)}
         del bufs
@@ -214,14 +217,15 @@ def extras(ncmhip, only=EXTRAS):
         m = lib.ncm_qwen_new(ctypes.byref(qc), ncmhip.ptr_array(bufs))
         ncmhip.check()
         prompt = rng.integers(0, qc.vocab, 2048).astype(np.int32)
-        gen = np.zeros(256, np.int32)
+        n_new = QWEN_STEPS
+        gen = np.zeros(n_new, np.int32)
         ms_pre = timed(ncmhip, lambda: lib.ncm_qwen_forward(m, prompt.ctypes.data, 2048, 1), 3, 1)
-        ms_gen = timed(ncmhip, lambda: lib.ncm_qwen_generate(m, prompt.ctypes.data, 2048, 256, -1, gen.ctypes.data),
+        ms_gen = timed(ncmhip, lambda: lib.ncm_qwen_generate(m, prompt.ctypes.data, 2048, n_new, -1, gen.ctypes.data),
                        2, 1)
         ncmhip.check()
         # the same 256 steps drawing from sample_topkp (temp 0.8, top-k 0, top-p 0.9) on the device
         st, nflag = ctypes.c_uint64(0x5EED), ctypes.c_int(0)
-        ms_samp = timed(ncmhip, lambda: lib.ncm_qwen_generate_sample(m, prompt.ctypes.data, 2048, 256, -1, 0.8, 0, 0.9,
+        ms_samp = timed(ncmhip, lambda: lib.ncm_qwen_generate_sample(m, prompt.ctypes.data, 2048, n_new, -1, 0.8, 0, 0.9,
                                                                      ctypes.byref(st), gen.ctypes.data,
                                                                      ctypes.byref(nflag)), 2, 1)
         ncmhip.check()
@@ -232,20 +236,20 @@ def extras(ncmhip, only=EXTRAS):
                                                              sflag.ptr), 20, 2)
         ncmhip.check()
         del row, srng, sout, sflag
-        ms_tok = (ms_gen - ms_pre) / 255
+        ms_tok = (ms_gen - ms_pre) / (n_new - 1)
         kv_bytes = 2 * 24 * 2 * 64 * 4 * (2048 + 128)          # mean KV cache read per step
         dec_bytes = 4 * nparam + kv_bytes
         pre_fl = 2 * 2048 * (nparam - qc.vocab * 896) + 24 * 4 * 14 * 2048 * 2048 * 64 / 2 + 2 * 896 * qc.vocab
         lib.ncm_qwen_free(m)
         out["qwen"] = {"config": "C4: 24 layers, d 896, 14/2 heads, FFN 4864, vocab 151936; prefill 2048, "
-                                 "256 greedy steps (KV cache, device argmax, no eos stop)",
+                                 f"{n_new} greedy steps (KV cache, device argmax, no eos stop)",
                        "prefill_tok_per_s": round(2048 / (ms_pre / 1e3), 1), "prefill_ms": round(ms_pre, 3),
                        "prefill_tflops": round(pre_fl / (ms_pre / 1e3) / 1e12, 3),
                        "decode_tok_per_s": round(1e3 / ms_tok, 1), "decode_ms_per_tok": round(ms_tok, 4),
                        "decode_gbs": round(dec_bytes / (ms_tok / 1e3) / 1e9, 1),
                        "decode_frac_hbm": round(dec_bytes / (ms_tok / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
                        "generate_ms": round(ms_gen, 2),
-                       "sampled_decode_tok_per_s": round(255 / ((ms_samp - ms_pre) / 1e3), 1),
+                       "sampled_decode_tok_per_s": round((n_new - 1) / ((ms_samp - ms_pre) / 1e3), 1),
                        "sampled_flagged_draws": nflag.value,
                        "sample_draw_us": round(ms_draw * 1e3, 2)}
         del bufs
@@ -305,11 +309,13 @@ def is_gain(i, n, per, slots, tail, base=1):
 
 
 def cpu_baseline_child():
-    """Runs in a child process: the reference CPU path on the bounded sample."""
+    """Runs in a child process: the reference CPU path on bounded samples of
+    the headline workload (config 2) and of configs 1, 3, 4 and 5."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     rng = np.random.default_rng(1)
     kind = "reference" if O.ref_available() else "port"
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     flops, secs = 0.0, 0.0
     for M in CPU_MS:
         for K, N in SHAPES:
@@ -326,20 +332,117 @@ def cpu_baseline_child():
                 O.linear_bwd(x, W, dy)
             secs += time.perf_counter() - t0
             flops += 3 * 2.0 * M * N * K
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    print(json.dumps({"value": flops / secs / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": kind,
-                      "seconds": round(secs, 3),
-                      "sample": "linear sweep fwd+dX+dW+db at M in {1,64,512} x the 5 (K->N) shapes "
-                                "(the M=4096 rows are left out to bound CPU time); "
-                                + ("reference src/kernels.c linear_fwd + train_tape.c TOP_LINEAR host "
-                                   "backward, gcc -O2 -fopenmp" if kind == "reference"
-                                   else "oracle C restatement")}))
+    res = {"value": flops / secs / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": kind,
+           "seconds": round(secs, 3),
+           "threads": f"OMP_NUM_THREADS={threads}, OMP_PROC_BIND={os.environ.get('OMP_PROC_BIND')}, "
+                      f"OMP_PLACES={os.environ.get('OMP_PLACES')}",
+           "sample": "linear sweep fwd+dX+dW+db at M in {1,64,512} x the 5 (K->N) shapes "
+                     "(the M=4096 rows are left out to bound CPU time); "
+                     + ("reference src/kernels.c linear_fwd + train_tape.c TOP_LINEAR host "
+                        "backward, gcc -O2 -fopenmp" if kind == "reference"
+                        else "oracle C restatement")}
+    if kind == "reference":
+        res["configs"] = cpu_configs(O, threads)
+    print(json.dumps(res))
+
+
+def cpu_configs(O, threads):
+    """The reference's own CPU code (oracle/_ref/libref.so) on bounded samples
+    of configs 1, 3, 4 and 5; each entry says what was timed."""
+    import tempfile
+    rng = np.random.default_rng(2)
+    out = {}
+
+    def normal(shape, std=0.02, mean=0.0):
+        return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std) + np.float32(mean)).astype(np.float32)
+
+    # config 1: the reference's ncp_load + ncp_forward (ncp.c:94-175, 480-640) at full size
+    n_layer, C, H, Kv, I, V, B, S = 4, 256, 4, 2, 1024, 16, 64, 81
+    shapes = O.ncp_shapes(n_layer, C, H, Kv, I, V)
+    params = [normal(sh, mean=1.0 if is_gain(i, len(shapes), 14, (0, 6), 4) else 0.0) for i, sh in enumerate(shapes)]
+    ids = rng.integers(0, V, (B, S)).astype(np.int32)
+    x = np.eye(V, dtype=np.float32)[ids]
+    named = O.ncp_named(params, n_layer, C)
+    cfg = O.ncp_single_level_cfg(n_layer, C, H, Kv, V, S)
+    reps = 3
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        O.ref_ncp_forward(cfg, named, x)
+    t = (time.perf_counter() - t0) / reps
+    out["C1_ncp_fwd"] = {"value": round(B * S / t, 1), "unit": "tokens/s", "cores": threads, "kind": "reference",
+                         "seconds": round(t * reps, 3),
+                         "sample": "full config 1 (64 x 81 tokens, 4 layers, d 256), 3 forwards through the "
+                                   "reference's ncp_load + ncp_forward on one-hot inputs (one level, no prefix)"}
+
+    # config 3: one of the 4 scales of vq_z_to_idx (rowwise_l2sq + host argmin + residual,
+    # vq.c:388-500) on all 65536 rows
+    rows, D3, V3 = 65536, 256, 4096
+    z = normal((rows, D3), std=1.0)
+    E = normal((V3, D3), std=1.0 / 16)
+    t0 = time.perf_counter()
+    O.ref_vq_multiscale(z, [E], 1, rows)
+    t = time.perf_counter() - t0
+    out["C3_vq"] = {"value": round(rows / t, 1), "unit": "vectors*scales/s", "cores": threads, "kind": "reference",
+                    "seconds": round(t, 3), "tflops": round(2.0 * rows * V3 * D3 / t / 1e12, 5),
+                    "sample": "one of the 4 scales on all 65536 rows x 4096 codewords x 256: the reference's "
+                              "vq_z_to_idx with the materialised 1 GiB distance matrix and host argmin"}
+
+    # config 4: the reference's qwen_forward (qwen.c:121-190) at full model size on a 128-token prompt,
+    # and one full-recompute greedy step at that context (qwen_generate, qwen.c:204-228)
+    qcfg = dict(n_layer=24, C=896, H=14, K=2, I=4864, V=151936)
+    qshapes = O.qwen_shapes(**qcfg)
+    qp = [normal(sh, mean=1.0 if is_gain(i, len(qshapes), 12, (0, 8), 1, base=1) else 0.0)
+          for i, sh in enumerate(qshapes)]
+    T4 = 128
+    prompt = rng.integers(0, qcfg["V"], T4).astype(np.int32)
+    with tempfile.TemporaryDirectory() as td:
+        m = O.RefQwen(qp, qcfg["n_layer"], qcfg["C"], qcfg["H"], qcfg["K"], T4 + 8, 1e6, os.path.join(td, "q.ncm"))
+        try:
+            t0 = time.perf_counter()
+            m.forward(prompt, last_only=True)
+            t_pre = time.perf_counter() - t0
+            t0 = time.perf_counter()
+            m.generate(prompt, 2)
+            t_gen = time.perf_counter() - t0
+        finally:
+            m.close()
+    out["C4_qwen"] = {"value": round(T4 / t_pre, 2), "unit": "prefill tokens/s", "cores": threads,
+                      "kind": "reference", "seconds": round(t_pre + t_gen, 3),
+                      "decode_tok_per_s_at_context_128": round(2 / t_gen, 3),
+                      "sample": "full config-4 model (24 layers, d 896, vocab 151936) through the reference's "
+                                "qwen_forward on a 128-token prompt (not 2048), then 2 greedy steps of its "
+                                "qwen_generate, which recomputes the whole context every step (no KV cache)"}
+    del qp
+
+    # config 5: the reference's taped GPT-2 step (train_gpt2.c:42-147 + t_ce + tape_backward_host)
+    # for 1 of the 12 layers and 2 of the 32 sequences of 512
+    L5, C5, H5, V5, T5, B5 = 1, 768, 12, 4096, 512, 2
+    gshapes = O.gpt2_shapes(L5, C5, V5, T5)
+    gp = [normal(sh) for sh in gshapes]
+    for i, sh in enumerate(gshapes):
+        if len(sh) == 1 and sh[0] == C5 and (i >= len(gp) - 2 or (i - 2) % 12 in (0, 6)):
+            gp[i] += np.float32(1.0)
+    gi = rng.integers(0, V5, (B5, T5)).astype(np.int32)
+    go = rng.integers(0, V5, (B5, T5)).astype(np.int32)
+    t0 = time.perf_counter()
+    O.ref_gpt2_grads(gp, L5, C5, H5, V5, T5, gi, go)
+    t = time.perf_counter() - t0
+    R5 = B5 * T5
+    fl = 3 * (2 * R5 * 12 * C5 * C5 + 2 * R5 * C5 * V5) + 12 * B5 * (4 + 8) * T5 * T5 * 64
+    out["C5_train"] = {"value": round(R5 / t, 1), "unit": "tokens/s", "cores": threads, "kind": "reference",
+                       "seconds": round(t, 3), "tflops": round(fl / t / 1e12, 5),
+                       "est_full_step_s": round(t * 12 * 16, 1),
+                       "sample": "forward + CE + host tape backward of 1 layer (of 12) on 2 x 512 tokens "
+                                 "(of 32 x 512) through the reference's train_gpt2_forward, t_ce and "
+                                 "tape_backward_host; est_full_step_s scales by 12 layers x 16 batches"}
+    return out
 
 
 def run_cpu_baseline():
     try:
+        env = dict(os.environ, OMP_PROC_BIND="close", OMP_PLACES="cores")
         out = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-baseline-child"],
-                             check=True, capture_output=True, text=True, timeout=600).stdout
+                             check=True, capture_output=True, text=True, timeout=900, env=env).stdout
         return json.loads(out.strip().splitlines()[-1])
     except Exception as e:  # reported, never fatal for the GPU number
         return {"value": None, "unit": "TFLOP/s", "cores": None, "kind": None, "sample": f"failed: {e}"}
@@ -358,11 +461,15 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 3 device-to-device copies of 256 MiB (the known-size kernel the HBM "
                          "counters of a rocprofv3 --pmc run are scaled by)")
+    ap.add_argument("--qwen-steps", type=int, default=256,
+                    help="decode steps of config 4 (256; fewer only to keep profiler runs short)")
     ap.add_argument("--cpu-baseline-child", action="store_true")
     args = ap.parse_args()
     if args.cpu_baseline_child:
         cpu_baseline_child()
         return
+    global QWEN_STEPS
+    QWEN_STEPS = max(2, args.qwen_steps)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build measures one MI355X only (asked for --gpus {args.gpus}, "

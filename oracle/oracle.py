@@ -1102,6 +1102,37 @@ NCP_CFG_KEYS = ("n_layer", "n_head", "n_embd", "n_kv_heads", "prefix_len", "quer
                 "use_swiglu", "use_geglu", "use_relu2", "vq_embed_dim", "prefix_pad_token_id")
 
 
+def ncp_named(params, n_layer, C):
+    """The reference's tensor names (ncp.c:189-316, 94-175, 406-478) for the
+    oracle's flat ncp parameters, with wte as the [C][V] linear of one-hot
+    inputs and a zero level embedding."""
+    pre = "gen.transformer."
+    per = ["ln_1.weight", "ln_1.bias", "attn.c_attn.weight", "attn.c_attn.bias", "attn.c_proj.weight",
+           "attn.c_proj.bias", "ln_2.weight", "ln_2.bias", "mlp.w_gate.weight", "mlp.w_gate.bias",
+           "mlp.w_up.weight", "mlp.w_up.bias", "mlp.c_proj.weight", "mlp.c_proj.bias"]
+    named = {pre + "wte.weight": params[0].T.copy(), pre + "wle.weight": np.zeros((1, C), np.float32)}
+    for li in range(n_layer):
+        for j, n in enumerate(per):
+            if params[1 + 14 * li + j] is not None:
+                named[f"{pre}blocks.{li}.{n}"] = params[1 + 14 * li + j]
+    n = len(params)
+    for name, p in ((pre + "ln_f.weight", params[n - 4]), (pre + "ln_f.bias", params[n - 3]),
+                    ("gen.lm_heads.0.weight", params[n - 2]), ("gen.lm_heads.0.bias", params[n - 1])):
+        if p is not None:
+            named[name] = p
+    return named
+
+
+def ncp_single_level_cfg(n_layer, C, H, Kv, V, S, rope_base=10000):
+    """The NCMConfig fields under which the reference's ncp_forward runs the
+    oracle's single-level ncp_forward: one target level of S tokens (level 0
+    of length 1 is not a target), no prefix, RoPE, SwiGLU, one untied head,
+    one-hot inputs of dimension V."""
+    return dict(n_layer=n_layer, n_head=H, n_embd=C, n_kv_heads=Kv, prefix_len=0, query_level0=0,
+                attn_pattern_block_diag=1, use_rope=1, rope_base=rope_base, use_swiglu=1, vq_embed_dim=V,
+                prefix_pad_token_id=-1, levels=[1, S], vocab_size=[V])
+
+
 def ref_ncp_forward(cfg, named, x, prefix_ids=None):
     """The reference's ncp_load + ncp_forward (ncp.c:94-175, 480-640).
     cfg: dict of NCP_CFG_KEYS plus levels (list) and vocab_size (list per

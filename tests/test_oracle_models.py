@@ -100,27 +100,6 @@ def test_qwen_cached_generation_equals_full_recompute(ref_qwen):
     assert cached == ref_qwen(params, n_ctx, 1e6, **QCFG).generate(prompt, n_new)
 
 
-def ncp_named(params, n_layer, C, V):
-    """The reference's tensor names (ncp.c:189-316, 94-175, 406-478) for the
-    oracle's flat ncp parameters, with wte as the [C][V] linear of one-hot
-    inputs and a zero level embedding."""
-    pre = "gen.transformer."
-    per = ["ln_1.weight", "ln_1.bias", "attn.c_attn.weight", "attn.c_attn.bias", "attn.c_proj.weight",
-           "attn.c_proj.bias", "ln_2.weight", "ln_2.bias", "mlp.w_gate.weight", "mlp.w_gate.bias",
-           "mlp.w_up.weight", "mlp.w_up.bias", "mlp.c_proj.weight", "mlp.c_proj.bias"]
-    named = {pre + "wte.weight": params[0].T.copy(), pre + "wle.weight": np.zeros((1, C), np.float32)}
-    for li in range(n_layer):
-        for j, n in enumerate(per):
-            if params[1 + 14 * li + j] is not None:
-                named[f"{pre}blocks.{li}.{n}"] = params[1 + 14 * li + j]
-    n = len(params)
-    for name, p in ((pre + "ln_f.weight", params[n - 4]), (pre + "ln_f.bias", params[n - 3]),
-                    ("gen.lm_heads.0.weight", params[n - 2]), ("gen.lm_heads.0.bias", params[n - 1])):
-        if p is not None:
-            named[name] = p
-    return named
-
-
 @pytest.mark.parametrize("H,Kv,biases", [(4, 2, True), (4, 4, True), (4, 1, False)])
 def test_ncp_forward_matches_reference(H, Kv, biases):
     n_layer, C, I, V, B, S = 2, 64, 96, 16, 3, 11
@@ -132,9 +111,7 @@ def test_ncp_forward_matches_reference(H, Kv, biases):
         is_bias = len(s) == 1 and not norm_gain
         params.append(None if (is_bias and not biases) else (0.3 * rng.standard_normal(s)).astype(np.float32))
     ids = rng.integers(0, V, (B, S)).astype(np.int32)
-    cfg = dict(n_layer=n_layer, n_head=H, n_embd=C, n_kv_heads=Kv, prefix_len=0, query_level0=0,
-               attn_pattern_block_diag=1, use_rope=1, rope_base=10000, use_swiglu=1, vq_embed_dim=V,
-               prefix_pad_token_id=-1, levels=[1, S], vocab_size=[V])
-    want = O.ref_ncp_forward(cfg, ncp_named(params, n_layer, C, V), np.eye(V, dtype=np.float32)[ids])
+    cfg = O.ncp_single_level_cfg(n_layer, C, H, Kv, V, S)
+    want = O.ref_ncp_forward(cfg, O.ncp_named(params, n_layer, C), np.eye(V, dtype=np.float32)[ids])
     got = O.ncp_forward(params, n_layer, C, H, Kv, I, V, ids)
     assert bits_equal(got, want.reshape(B * S, V))

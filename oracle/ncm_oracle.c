@@ -1143,3 +1143,32 @@ void orc_rope_tables_ncp(int S, int hd, int base, float *cos_t, float *sin_t) {
             sin_t[t * hd + half + d] = si;
         }
 }
+
+void orc_conv1d_btc(const float *x, const float *W, const float *bias, float *y, int B, int T, int Cin, int Cout,
+                    int K, int stride, int pad) {
+    orc_conv1d(x, W, bias, y, B, T, Cin, Cout, K, stride, pad);
+}
+
+/* ncp.c:441-466 head_logits, tie_heads_to_codebook branch */
+void orc_ncp_tied_head(const float *z, const float *E, const float *bias, float invT, float *out, int rows, int V,
+                       int Dd) {
+    double *Esq = (double *)malloc((size_t)(V > 0 ? V : 1) * sizeof(double));
+    double ds = 0;
+    for (int v = 0; v < V; v++) {
+        double s = 0;
+        for (int d = 0; d < Dd; d++) s += (double)E[(size_t)v * Dd + d] * E[(size_t)v * Dd + d];
+        Esq[v] = s;
+        ds += s;
+    }
+    ds /= V;
+#pragma omp parallel for schedule(static)
+    for (int r = 0; r < rows; r++)
+        for (int v = 0; v < V; v++) {
+            double dot = 0;
+            for (int d = 0; d < Dd; d++) dot += (double)z[(size_t)r * Dd + d] * E[(size_t)v * Dd + d];
+            double o = (2 * dot - Esq[v]) / ds * invT;
+            if (bias) o += bias[v];
+            out[(size_t)r * V + v] = (float)o;
+        }
+    free(Esq);
+}

@@ -134,6 +134,16 @@ void orc_vq_idx_to_zhats(const OrcVq *q, const int *idx, int B, float *zhats);
 void orc_vq_next_input(const OrcVq *q, const int *codes, int lv, float *z_hat, float *x_out, int B);
 void orc_vq_idx_to_ncm_input(const OrcVq *q, const int *idx, int B, float *x_out);
 
+/* conv1d_fwd (kernels.c:546-566) on [B][T][Cin] rows -> [B][To][Cout]:
+ * fp64 over ci (outer) and k (inner), taps outside [0, T) skipped */
+void orc_conv1d_btc(const float *x, const float *W, const float *bias, float *y, int B, int T, int Cin, int Cout,
+                    int K, int stride, int pad);
+/* the codebook-tied NCP head (ncp.c:429-466): o[r][v] = (float)((2 dot -
+ * |E_v|^2) / ds * invT (+ bias[v])), dot and |E_v|^2 serial fp64 over d,
+ * ds = the serial fp64 sum of |E_v|^2 over v divided by V */
+void orc_ncp_tied_head(const float *z, const float *E, const float *bias, float invT, float *out, int rows, int V,
+                       int Dd);
+
 /* threads used by the OpenMP loops (0 = runtime default) */
 void orc_set_threads(int n);
 

@@ -85,6 +85,8 @@ def lib():
             "orc_head_merge_bwd": (None, [vp, vp] + [ci] * 5),
             "orc_heads_transpose_bwd": (None, [vp, vp] + [ci] * 5),
             "orc_rope_tables_ncp": (None, [ci, ci, ci, vp, vp]),
+            "orc_conv1d_btc": (None, [vp, vp, vp, vp] + [ci] * 7),
+            "orc_ncp_tied_head": (None, [vp, vp, vp, ctypes.c_float, vp, ci, ci, ci]),
         }
         for n, (r, a) in sigs.items():
             f = getattr(L, n)
@@ -1160,3 +1162,163 @@ def ref_ncp_forward(cfg, named, x, prefix_ids=None):
     if rc:
         raise RuntimeError("reference ncp_forward failed")
     return out
+
+
+# ---- the multi-level NCP forward (ncp.c:94-175, 184-358, 361-403, 406-640) ----
+def conv1d_btc(x, W, b, K, stride, pad):
+    """conv1d_fwd (kernels.c:546-566) on [B][T][Cin] rows; W [Cout][Cin][K]."""
+    x, W = _f32(x), _f32(W)
+    b = None if b is None else _f32(b)
+    B, T, Cin = x.shape
+    Cout = W.shape[0]
+    To = (T + 2 * pad - K) // stride + 1
+    y = np.empty((B, To, Cout), np.float32)
+    lib().orc_conv1d_btc(_ptr(x), _ptr(W), _ptr(b), _ptr(y), B, T, Cin, Cout, K, stride, pad)
+    return y
+
+
+def _expf(v):
+    """glibc's expf, as the reference's head_logits calls it (ncp.c:460)."""
+    f = ctypes.CDLL("libm.so.6").expf
+    f.restype = ctypes.c_float
+    f.argtypes = [ctypes.c_float]
+    return f(float(v))
+
+
+def ncp_build_mask(cfg, S):
+    """build_full_mask (ncp.c:361-386): [S][S] additive, 0 or -inf."""
+    P = cfg.get("prefix_len", 0)
+    levels = list(cfg["levels"])
+    first = 0 if cfg.get("query_level0", 0) else 1
+    lvl = np.concatenate([np.full(levels[k], k) for k in range(first, len(levels))]).astype(np.int64)
+    m = np.zeros((S, S), np.float32)
+    m[:P, P:] = -np.inf
+    li, lj = lvl[:, None], lvl[None, :]
+    tgt = (li == lj) if cfg.get("attn_pattern_block_diag", 0) else (li >= lj)
+    m[P:, P:] = np.where(tgt, 0.0, -np.inf).astype(np.float32)
+    return m
+
+
+def _ncp_block(cfg, named, li, x, B, S, mask, cos_t, sin_t):
+    """ncp_block (ncp.c:184-345) on x [B*S][C], returning the new x."""
+    C, H, nkv = cfg["n_embd"], cfg["n_head"], cfg["n_kv_heads"]
+    hd = C // H
+    pre = f"gen.transformer.blocks.{li}."
+    g = named.get
+    ln = layernorm(x, named[pre + "ln_1.weight"], g(pre + "ln_1.bias"))
+    qkv = linear_fwd(ln, named[pre + "attn.c_attn.weight"], g(pre + "attn.c_attn.bias"))
+    qq, kk, vv = qkv_split(qkv.reshape(B, S, -1), B, S, C, H, hd, nkv, H // nkv)
+    if cfg.get("use_qk_norm", 0):
+        qq = rmsnorm(qq.reshape(-1, hd), named[pre + "attn.q_norm.weight"]).reshape(qq.shape)
+        kk = rmsnorm(kk.reshape(-1, hd), named[pre + "attn.k_norm.weight"]).reshape(kk.shape)
+    if cfg.get("use_rope", 0):
+        qq = rope(qq.reshape(-1, hd), cos_t, sin_t, S).reshape(qq.shape)
+        kk = rope(kk.reshape(-1, hd), cos_t, sin_t, S).reshape(kk.shape)
+    ctx = sdpa_gqa(qq, kk, vv, mask)
+    mo = head_merge(ctx, B, S, C, H, hd).reshape(B * S, C)
+    x = x + linear_fwd(mo, named[pre + "attn.c_proj.weight"], g(pre + "attn.c_proj.bias"))
+    mn = layernorm(x, named[pre + "ln_2.weight"], g(pre + "ln_2.bias"))
+    if cfg.get("use_swiglu", 0) or cfg.get("use_geglu", 0):
+        gt = linear_fwd(mn, named[pre + "mlp.w_gate.weight"], g(pre + "mlp.w_gate.bias"))
+        up = linear_fwd(mn, named[pre + "mlp.w_up.weight"], g(pre + "mlp.w_up.bias"))
+        gt = act("silu" if cfg.get("use_swiglu", 0) else "gelu", gt)
+        h = gt * up
+    else:
+        h = linear_fwd(mn, named[pre + "mlp.c_fc.weight"], g(pre + "mlp.c_fc.bias"))
+        if cfg.get("use_relu2", 0):
+            r = np.where(h > 0, h, np.float32(0)).astype(np.float32)
+            h = r * r
+        else:
+            h = act("gelu", h)
+    return x + linear_fwd(h, named[pre + "mlp.c_proj.weight"], g(pre + "mlp.c_proj.bias"))
+
+
+def ncp_head(cfg, named, k, slice_):
+    """head_logits (ncp.c:406-478) of target level k on rows slice_ [R][C]."""
+    g = named.get
+    first = 0 if cfg.get("query_level0", 0) else 1
+    V = list(cfg["vocab_size"])[k]
+    if cfg.get("shared_output_head", 0):
+        # the level's vocabulary is the first V rows of the shared head
+        b = (named[f"gen.lm_heads.biases.{k}"] if cfg.get("shared_head_per_level_bias", 0)
+             else named["gen.lm_heads.head.bias"] if cfg.get("untied_head_bias", 0) else None)
+        return linear_fwd(slice_, _f32(named["gen.lm_heads.head.weight"])[:V], None if b is None else _f32(b)[:V])
+    if cfg.get("tie_heads_to_codebook", 0):
+        z = linear_fwd(slice_, named[f"gen.lm_heads.{k}.proj.weight"], g(f"gen.lm_heads.{k}.proj.bias"))
+        E = _f32(named[f"tok.vq.embeddings.{k + first}.weight"])
+        invT = _expf(np.asarray(named[f"gen.lm_heads.{k}.log_inv_T"], np.float32).reshape(-1)[0])
+        bias = g(f"gen.lm_heads.{k}.bias")
+        bias = None if bias is None else _f32(bias)
+        V, Dd = E.shape
+        out = np.empty((z.shape[0], V), np.float32)
+        lib().orc_ncp_tied_head(_ptr(z), _ptr(E), _ptr(bias), invT, _ptr(out), z.shape[0], V, Dd)
+        return out
+    return linear_fwd(slice_, named[f"gen.lm_heads.{k}.weight"], g(f"gen.lm_heads.{k}.bias"))
+
+
+def ncp_forward_levels(cfg, named, x, prefix_ids=None):
+    """ncp_forward (ncp.c:480-640) op for op with the pinned oracle
+    functions: x [B][P+T][D] -> logits [B][T][max vocab] (-inf past a
+    level's vocabulary).  cfg / named as ref_ncp_forward takes them."""
+    x = _f32(x)
+    B = x.shape[0]
+    C, H, D = cfg["n_embd"], cfg["n_head"], cfg["vq_embed_dim"]
+    hd = C // H
+    P = cfg.get("prefix_len", 0)
+    first = 0 if cfg.get("query_level0", 0) else 1
+    tl = list(cfg["levels"])[first:]
+    T = sum(tl)
+    S = P + T
+    use_rope = cfg.get("use_rope", 0)
+    pos = list(range(P)) + [t for lk in tl for t in range(lk)]
+    cos_t = sin_t = None
+    if use_rope:
+        cs, sn = rope_tables_ncp(max(pos) + 1, hd, cfg["rope_base"])
+        cos_t, sin_t = cs[pos].copy(), sn[pos].copy()
+    wle = _f32(named["gen.transformer.wle.weight"])
+    lvl_pos = np.concatenate([np.repeat(wle[k:k + 1], lk, axis=0) for k, lk in enumerate(tl)])
+    if not use_rope:
+        wpe = _f32(named["gen.transformer.wpe.weight"])
+        lvl_pos = lvl_pos + np.concatenate([wpe[:lk] for lk in tl])
+    zpre, xt = x[:, :P].copy(), x[:, P:].copy()
+    if cfg.get("puc_enabled", 0):
+        Kc, off = cfg["puc_kernel"], 0
+        for k, lk in enumerate(tl):
+            co = conv1d_btc(xt[:, off:off + lk], named[f"gen.post_upsample_convs.{k}.weight"],
+                            named[f"gen.post_upsample_convs.{k}.bias"], Kc, 1, Kc // 2)
+            xt[:, off:off + lk] = xt[:, off:off + lk] + co[:, :lk]
+            off += lk
+    wte, wteb = named["gen.transformer.wte.weight"], named.get("gen.transformer.wte.bias")
+    pemb = linear_fwd(zpre.reshape(-1, D), wte, wteb).reshape(B, P, C)
+    xe = linear_fwd(xt.reshape(-1, D), wte, wteb).reshape(B, T, C) + lvl_pos[None]
+    if not use_rope:
+        pemb = pemb + _f32(named["gen.transformer.wpe.weight"])[:P][None]
+    h = np.concatenate([pemb, xe], axis=1)
+    mask = ncp_build_mask(cfg, S)
+    pad = cfg.get("prefix_pad_token_id", -1)
+    n_layer = cfg["n_layer"]
+
+    def run_stack(hb, nb, m):
+        hb = hb.reshape(nb * S, C)
+        for li in range(n_layer):
+            hb = _ncp_block(cfg, named, li, hb, nb, S, m, cos_t, sin_t)
+        return layernorm(hb, named["gen.transformer.ln_f.weight"], named.get("gen.transformer.ln_f.bias"))
+
+    pids = None if prefix_ids is None else np.asarray(prefix_ids, np.int32).reshape(B, P)
+    if pad >= 0 and pids is not None and (pids == pad).any():
+        outs = []
+        for b in range(B):
+            mb = mask.copy()
+            mb[:, :P][:, pids[b] == pad] = -np.inf
+            outs.append(run_stack(h[b:b + 1], 1, mb))
+        h = np.concatenate(outs).reshape(B, S, C)
+    else:
+        h = run_stack(h, B, mask).reshape(B, S, C)
+    vocabs = list(cfg["vocab_size"])[:len(tl)]
+    logits = np.full((B, T, max(vocabs)), -np.inf, np.float32)
+    off = 0
+    for k, lk in enumerate(tl):
+        lg = ncp_head(cfg, named, k, h[:, P + off:P + off + lk].reshape(B * lk, C))
+        logits[:, off:off + lk, :vocabs[k]] = lg.reshape(B, lk, vocabs[k])
+        off += lk
+    return logits

@@ -18,6 +18,7 @@ import os
 import numpy as np
 import pytest
 
+import model_data as MD
 import oracle as O
 from conftest import bits_equal
 
@@ -115,3 +116,26 @@ def test_ncp_forward_matches_reference(H, Kv, biases):
     want = O.ref_ncp_forward(cfg, O.ncp_named(params, n_layer, C), np.eye(V, dtype=np.float32)[ids])
     got = O.ncp_forward(params, n_layer, C, H, Kv, I, V, ids)
     assert bits_equal(got, want.reshape(B * S, V))
+
+
+@pytest.mark.parametrize("case", sorted(MD.NCP_CASES))
+def test_ncp_forward_levels_matches_reference(case):
+    """The oracle's multi-level ncp_forward (levels, level embedding, block
+    masks, prefix pads, qk-norm, RoPE or learned positions, every MLP and
+    head kind, post-upsample convs) against the reference's ncp_forward."""
+    cfg = MD.NCP_CASES[case]
+    named = MD.ncp_named_weights(cfg, seed=len(case))
+    rng = np.random.default_rng(3)
+    B, P = 3, cfg["prefix_len"]
+    first = 0 if cfg["query_level0"] else 1
+    S = P + sum(cfg["levels"][first:])
+    x = rng.standard_normal((B, S, cfg["vq_embed_dim"]), dtype=np.float32)
+    pids = None
+    if cfg["prefix_pad_token_id"] >= 0:
+        pids = rng.integers(1, 9, (B, P)).astype(np.int32)
+        pids[0, :2] = 0          # board 0: two pads; board 1: none; board 2: one
+        pids[2, -1] = 0
+    want = O.ref_ncp_forward(cfg, named, x, pids)
+    got = O.ncp_forward_levels(cfg, named, x, pids)
+    assert np.isfinite(want[want != -np.inf]).all()
+    assert bits_equal(got, want)

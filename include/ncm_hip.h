@@ -97,6 +97,7 @@ void  *backend_to_host(const float *d, size_t nbytes);
 #define NCM_ACT_SILU      1  /* v/(1+exp(-v)), kernels.c:220-226 */
 #define NCM_ACT_GELU      2  /* exact erf GELU, kernels.c:185-194 */
 #define NCM_ACT_GELU_TANH 3  /* HF gelu_new, kernels.c:207-218 */
+#define NCM_ACT_RELU2     4  /* relu(v)^2, the NCP MLP's use_relu2 (ncp.c:327-333) */
 
 /* replaces linear_fwd, ncm.h:145-146, kernels.c:38-54:
  * y[r,m] = b[m] + sum_k x[r,k] W[m,k];  x:[batch,K], W:[M,K], b:[M]|NULL, y:[batch,M] */
@@ -618,6 +619,42 @@ void vq_next_input(VQState *vq, const int *codes, int level_idx, float *z_hat, f
  * is area(z_hat after level li -> levels[li + 1]). */
 void vq_idx_to_ncm_input(VQState *vq, const int *idx, int B, float *x_out);
 
+
+/* ------------------------------------------------------------------ */
+/* the NCP transformer forward -- replaces src/ncp.c (ncm.h:249-268)    */
+/* ------------------------------------------------------------------ */
+
+typedef struct VQVAEState VQVAEState;
+typedef struct NCPState NCPState;
+/* replaces ncp_load, ncm.h:250, ncp.c:94-175: reads the block, embedding and
+ * head weights under the reference's names from the store's DEVICE tensors
+ * (borrowed), builds the RoPE tables of the level positions (prefix 0..P-1,
+ * then 0..l_k - 1 per target level), the level embedding rows (wle, plus wpe
+ * without RoPE) and the additive mask on the device.  vqvae is kept for the
+ * caller and not used by the forward.  Missing weights or a configuration
+ * the reference cannot run (n_kv_heads <= 0 or not dividing n_head, odd head
+ * size with RoPE, no target level) are reported like its exit(1). */
+NCPState *ncp_load(const NCMConfig *c, WeightStore *ws, VQVAEState *vqvae);
+/* replaces ncp_free, ncm.h:251 */
+void ncp_free(NCPState *m);
+/* replace the accessors of ncm.h:252-260 (tables are DEVICE [rows][hd]) */
+int ncp_P(NCPState *m);
+int ncp_T(NCPState *m);
+int ncp_ntgt(NCPState *m);
+int ncp_lvlfirst(NCPState *m);
+float *ncp_rope_cos(NCPState *m);
+float *ncp_rope_sin(NCPState *m);
+float *ncp_rope_gen_cos(NCPState *m, int k);
+float *ncp_rope_gen_sin(NCPState *m, int k);
+/* replaces ncp_forward, ncm.h:267-268, ncp.c:480-640: x DEVICE [B][P+T][D]
+ * (D = vq_embed_dim), prefix_ids HOST [B][P] or NULL, logits DEVICE
+ * [B][T][max vocab] (-inf past a level's vocabulary).  Every step runs on the
+ * device (the reference stages the split, the level embedding, the q/k/v
+ * split, the head merge, the gated product and the per-level slices on the
+ * host); activations come from the library arena, which the caller resets,
+ * as the reference's callers do.  Boards with padded prefix tokens run one
+ * at a time with their own mask, as in the reference. */
+void ncp_forward(NCPState *m, const float *x, const int *prefix_ids, float *logits, int B);
 
 /* replaces train_data_load / train_data_free, ncm.h:262-264, tensor.c:375-395:
  * "NCMT" magic, u64 rows, u64 row length, int32 tokens; at most max_rows rows

@@ -21,4 +21,8 @@ ncm_co_train:
     .globl ncm_co_sample
 ncm_co_sample:
     .incbin "sample.co"
+    .balign 4096
+    .globl ncm_co_ncp
+ncm_co_ncp:
+    .incbin "ncp.co"
     .section .note.GNU-stack,"",@progbits

@@ -483,6 +483,7 @@ __device__ __forceinline__ void g_epilogue(const GemmArgs &p, const f4 (&tot)[BM
     case ACT_SILU: g_epilogue_act<BM, BN, EPI, ACT_SILU, IA, IB>(p, tot, i0, j0, tid); break;
     case ACT_GELU: g_epilogue_act<BM, BN, EPI, ACT_GELU, IA, IB>(p, tot, i0, j0, tid); break;
     case ACT_GELU_TANH: g_epilogue_act<BM, BN, EPI, ACT_GELU_TANH, IA, IB>(p, tot, i0, j0, tid); break;
+    case ACT_RELU2: g_epilogue_act<BM, BN, EPI, ACT_RELU2, IA, IB>(p, tot, i0, j0, tid); break;
     default: g_epilogue_act<BM, BN, EPI, ACT_NONE, IA, IB>(p, tot, i0, j0, tid); break;
     }
 }
@@ -659,6 +660,7 @@ __device__ __forceinline__ void gemm_tile_fixup_body(const GemmArgs &p) {
     case ACT_SILU: g_epilogue_blk_act<EPI, ACT_SILU, IA, IB>(p, tot, a, b, i0, j0, tid); break;
     case ACT_GELU: g_epilogue_blk_act<EPI, ACT_GELU, IA, IB>(p, tot, a, b, i0, j0, tid); break;
     case ACT_GELU_TANH: g_epilogue_blk_act<EPI, ACT_GELU_TANH, IA, IB>(p, tot, a, b, i0, j0, tid); break;
+    case ACT_RELU2: g_epilogue_blk_act<EPI, ACT_RELU2, IA, IB>(p, tot, a, b, i0, j0, tid); break;
     default: g_epilogue_blk_act<EPI, ACT_NONE, IA, IB>(p, tot, a, b, i0, j0, tid); break;
     }
 }
@@ -815,6 +817,7 @@ __device__ __forceinline__ void gemm_dma_body(const GemmArgs &p) {
             case ACT_SILU: g_gated_out<ACT_SILU>(p, tot, up, i0 + wm * 32, j0, li, lg); break;
             case ACT_GELU: g_gated_out<ACT_GELU>(p, tot, up, i0 + wm * 32, j0, li, lg); break;
             case ACT_GELU_TANH: g_gated_out<ACT_GELU_TANH>(p, tot, up, i0 + wm * 32, j0, li, lg); break;
+            case ACT_RELU2: g_gated_out<ACT_RELU2>(p, tot, up, i0 + wm * 32, j0, li, lg); break;
             default: g_gated_out<ACT_NONE>(p, tot, up, i0 + wm * 32, j0, li, lg); break;
             }
         }

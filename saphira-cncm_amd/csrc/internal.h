@@ -49,6 +49,11 @@ size_t ncm_sample_ws_bytes(int V);
  * step; the gradient is consumed and the next step accumulates from zero). */
 void ncm_adamw_update_clear(float *p, float *g, float *m, float *v, int64_t n, double lr, double b1, double b2,
                             double b1t, double b2t, double eps, double wd);
+/* conv1d_fwd (kernels.c:546-566, bit-exact) on [B][T][D] rows with D input
+ * and D output channels: y [B][To][D], To = (T + 2 pad - K) / stride + 1;
+ * W [D][D][K]; launches only. */
+int ncm_conv1d_btd(const float *x, const float *W, const float *b, float *y, int B, int T, int D, int K, int stride,
+                   int pad);
 /* Compute units of the selected device. */
 int ncm_cu_count(void);
 void *ncm_workspace(int slot, size_t bytes);

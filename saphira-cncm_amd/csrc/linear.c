@@ -250,7 +250,7 @@ static int check_dims(const char *fn, int64_t batch, int M, int K) {
 static void linear_forward(const char *fn, const float *x, const float *W, const float *b,
                            const float *res, int res_mul, float *y, int64_t batch, int M, int K, int act) {
     if (check_dims(fn, batch, M, K)) return;
-    if (act < NCM_ACT_NONE || act > NCM_ACT_GELU_TANH) {
+    if (act < NCM_ACT_NONE || act > NCM_ACT_RELU2) {
         ncm_fail(NCM_E_ARG, "%s: unknown activation %d", fn, act);
         return;
     }
@@ -295,7 +295,7 @@ void linear_fwd_gated(const float *x, const float *Wg, const float *bg, const fl
                       int64_t batch, int M, int K, int act) {
     const char *fn = "linear_fwd_gated";
     if (check_dims(fn, batch, M, K)) return;
-    if (act < NCM_ACT_NONE || act > NCM_ACT_GELU_TANH) {
+    if (act < NCM_ACT_NONE || act > NCM_ACT_RELU2) {
         ncm_fail(NCM_E_ARG, "%s: unknown activation %d", fn, act);
         return;
     }

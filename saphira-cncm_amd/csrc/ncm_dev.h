@@ -7,7 +7,7 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 typedef float f2 __attribute__((ext_vector_type(2)));
 
 // Activation codes; must match NCM_ACT_* in include/ncm_hip.h.
-enum { ACT_NONE = 0, ACT_SILU = 1, ACT_GELU = 2, ACT_GELU_TANH = 3 };
+enum { ACT_NONE = 0, ACT_SILU = 1, ACT_GELU = 2, ACT_GELU_TANH = 3, ACT_RELU2 = 4 };
 
 // Activations in the form the reference applies them to a float value
 // (kernels.c:167-174 SiLU/GELU in float; kernels.c:207-218 gelu_new, whose
@@ -20,6 +20,10 @@ __device__ __forceinline__ float ncm_act(float v, int act) {
         double d = v;
         double t = 0.7978845608028654 * (d + 0.044715 * d * d * d);
         return (float)(0.5 * d * (1.0 + tanh(t)));
+    }
+    case ACT_RELU2: {   // ncp.c:327-333: r = v > 0 ? v : 0; r * r (NaN -> 0)
+        const float r = v > 0.f ? v : 0.f;
+        return r * r;
     }
     default: return v;
     }

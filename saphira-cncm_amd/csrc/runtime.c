@@ -11,8 +11,9 @@
 #include <string.h>
 
 /* ---- embedded code objects (blobs.S) ---- */
-extern const unsigned char ncm_co_gemm[], ncm_co_vq[], ncm_co_ops[], ncm_co_train[], ncm_co_sample[];
-static const unsigned char *const co_blobs[] = {ncm_co_gemm, ncm_co_vq, ncm_co_ops, ncm_co_train, ncm_co_sample};
+extern const unsigned char ncm_co_gemm[], ncm_co_vq[], ncm_co_ops[], ncm_co_train[], ncm_co_sample[], ncm_co_ncp[];
+static const unsigned char *const co_blobs[] = {ncm_co_gemm, ncm_co_vq, ncm_co_ops, ncm_co_train, ncm_co_sample,
+                                                ncm_co_ncp};
 #define N_MODULES (int)(sizeof(co_blobs) / sizeof(co_blobs[0]))
 
 static int g_state = 0; /* 0 = not initialised, 1 = ready, <0 = failed */

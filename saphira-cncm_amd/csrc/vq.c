@@ -389,6 +389,11 @@ static int vqf_conv(const float *x, const float *W, const float *b, float *y, in
     return ncm_launch_named(name, (unsigned)((D + 63) / 64), (unsigned)((To + 15) / 16), (unsigned)B, 256, a);
 }
 
+int ncm_conv1d_btd(const float *x, const float *W, const float *b, float *y, int B, int T, int D, int K, int stride,
+                   int pad) {
+    return vqf_conv(x, W, b, y, B, T, D, K, stride, pad, 0, NULL);
+}
+
 static int vqf_gn(const float *x, float *y, int B, int T, int D) {
     void *a[] = {&x, &y, &T, &D};
     return ncm_launch_named("vqf_groupnorm", (unsigned)B * 8u, 1, 1, 64, a);

@@ -16,7 +16,7 @@ REPO = os.path.dirname(HERE)
 LIB_PATH = os.path.join(HERE, "libncmhip.so")
 HEADER = os.path.join(REPO, "include", "ncm_hip.h")
 
-ACT = {"none": 0, "silu": 1, "gelu": 2, "gelu_tanh": 3}
+ACT = {"none": 0, "silu": 1, "gelu": 2, "gelu_tanh": 3, "relu2": 4}
 
 c_float_p = ctypes.POINTER(ctypes.c_float)
 vp = ctypes.c_void_p
@@ -150,6 +150,17 @@ _SIGS = {
     "ncm_hip_sample_flag": (ci, []),
     "sample_topkp_dev": (None, [vp, ci, ctypes.c_float, ci, ctypes.c_float, vp, vp, vp]),
     "vq_load": (vp, [vp, vp, ctypes.c_char_p]),
+    "ncp_load": (vp, [vp, vp, vp]),
+    "ncp_free": (None, [vp]),
+    "ncp_forward": (None, [vp, vp, vp, vp, ci]),
+    "ncp_P": (ci, [vp]),
+    "ncp_T": (ci, [vp]),
+    "ncp_ntgt": (ci, [vp]),
+    "ncp_lvlfirst": (ci, [vp]),
+    "ncp_rope_cos": (vp, [vp]),
+    "ncp_rope_sin": (vp, [vp]),
+    "ncp_rope_gen_cos": (vp, [vp, ci]),
+    "ncp_rope_gen_sin": (vp, [vp, ci]),
     "vq_free": (None, [vp]),
     "vq_total_codes": (ci, [vp]),
     "vq_nlevels": (ci, [vp]),
@@ -524,3 +535,34 @@ class NcpConfig(ctypes.Structure):
     _fields_ = [("n_layer", ctypes.c_int), ("n_embd", ctypes.c_int), ("n_head", ctypes.c_int),
                 ("n_kv", ctypes.c_int), ("n_inner", ctypes.c_int), ("vocab", ctypes.c_int),
                 ("rope_base", ctypes.c_int)]
+
+
+def weight_store(named):
+    """A WeightStore of device tensors for {name: array}; returns (store,
+    keep-alive list)."""
+    items = (NamedTensor * len(named))()
+    keep = [items]
+    for j, (k, arr) in enumerate(named.items()):
+        buf = DeviceBuffer.from_numpy(np.ascontiguousarray(arr, np.float32))
+        t = TensorS()
+        t.data = buf.ptr
+        for a, d in enumerate(arr.shape):
+            t.shape[a] = d
+        t.ndim, t.n = arr.ndim, int(arr.size)
+        items[j].name = k.encode()
+        items[j].t = ctypes.pointer(t)
+        keep += [buf, t]
+    return WeightStore(items, len(named)), keep
+
+
+def ncm_config(**fields):
+    """An NCMConfig with the given fields set (lists fill the array fields)."""
+    c = NCMConfig()
+    for k, v in fields.items():
+        if isinstance(v, (list, tuple)):
+            arr = getattr(c, k)
+            for i, x in enumerate(v):
+                arr[i] = x
+        else:
+            setattr(c, k, v)
+    return c

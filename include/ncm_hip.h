@@ -350,6 +350,11 @@ void ncm_t_rope(NcmTape *t, const float *xq, const float *xk, float *yq, float *
                 const float *sin, int B, int H, int Hkv, int T, int hd);
 void ncm_t_sdpa(NcmTape *t, const float *q, const float *k, const float *v, const float *mask, float *o,
                 int B, int H, int Hkv, int Tq, int Tkv, int hd);
+/* extension: ncm_t_sdpa with the causal mask generated in the kernels (query t
+ * sees keys <= t + Tkv - Tq), replacing the T x T -1e9 mask the reference's
+ * callers build and upload (train_gpt2.c:112-121) */
+void ncm_t_sdpa_causal(NcmTape *t, const float *q, const float *k, const float *v, float *o, int B, int H, int Hkv,
+                       int Tq, int Tkv, int hd);
 void ncm_t_qkvsplit(NcmTape *t, const float *in, float *qq, float *kk, float *vv, int B, int T, int C, int H, int hd,
                     int K, int rep);
 void ncm_t_headmerge(NcmTape *t, const float *ctx, float *out, int B, int T, int C, int H, int hd);

@@ -61,8 +61,7 @@ static float *A(int64_t n) {
 }
 
 /* train_gpt2.c:42-103 */
-static float *gpt2_block(NcmTape *tp, const NcmGpt2Config *c, float *const *P, int li, float *x, int B, int T,
-                         const float *mask) {
+static float *gpt2_block(NcmTape *tp, const NcmGpt2Config *c, float *const *P, int li, float *x, int B, int T) {
     const int C = c->n_embd, H = c->n_head, hd = C / H, I = 4 * C;
     const int64_t R = (int64_t)B * T;
     float *const *w = P + 2 + PER_LAYER * li;
@@ -74,7 +73,7 @@ static float *gpt2_block(NcmTape *tp, const NcmGpt2Config *c, float *const *P, i
     ncm_t_layernorm_eps(tp, x, w[0], w[1], ln, R, C, GPT2_LN_EPS);
     ncm_t_linear(tp, ln, w[2], w[3], qkv, R, 3 * C, C);
     ncm_t_qkvsplit(tp, qkv, qq, kk, vv, B, T, C, H, hd, H, 1);
-    ncm_t_sdpa(tp, qq, kk, vv, mask, ctx, B, H, H, T, T, hd);
+    ncm_t_sdpa_causal(tp, qq, kk, vv, ctx, B, H, H, T, T, hd);   /* the -1e9 causal mask, generated */
     ncm_t_headmerge(tp, ctx, mo, B, T, C, H, hd);
     ncm_t_linear(tp, mo, w[4], w[5], ao, R, C, C);
     ncm_t_add(tp, x, ao, x1, R * C);
@@ -92,13 +91,11 @@ float *ncm_gpt2_forward(NcmTape *tp, const NcmGpt2Config *c, float *const *P, co
     if (ncm_ready()) return NULL;
     const int C = c->n_embd, V = c->vocab;
     const int64_t R = (int64_t)B * T;
-    float *h = A(R * C), *xe = A(R * C), *pe = A(R * C), *mask = A((int64_t)T * T);
+    float *h = A(R * C), *xe = A(R * C), *pe = A(R * C);
     int *ph = (int *)malloc((size_t)R * sizeof(int));
-    float *hm = (float *)malloc((size_t)T * T * sizeof(float));
-    if (!mask || !ph || !hm) {
+    if (!pe || !ph) {
         free(ph);
-        free(hm);
-        if (mask) ncm_fail(NCM_E_OOM, "gpt2: host buffers");
+        if (pe) ncm_fail(NCM_E_OOM, "gpt2: host buffers");
         return NULL;
     }
     ncm_t_embed(tp, P[0], ids, V, xe, R, C);
@@ -107,11 +104,9 @@ float *ncm_gpt2_forward(NcmTape *tp, const NcmGpt2Config *c, float *const *P, co
     ncm_t_embed(tp, P[1], ph, c->n_pos, pe, R, C);
     free(ph);
     ncm_t_add(tp, xe, pe, h, R * C);
-    for (int tq = 0; tq < T; tq++)
-        for (int tk = 0; tk < T; tk++) hm[(size_t)tq * T + tk] = tk <= tq ? 0.0f : -1e9f;
-    mem_h2d(mask, hm, (size_t)T * T * sizeof(float));
-    free(hm);
-    for (int li = 0; li < c->n_layer && h; li++) h = gpt2_block(tp, c, P, li, h, B, T, mask);
+    /* the causal -1e9 mask of train_gpt2.c:112-121 is generated in the SDPA
+     * kernels (exactly zero probability for every later key, as -1e9 gives) */
+    for (int li = 0; li < c->n_layer && h; li++) h = gpt2_block(tp, c, P, li, h, B, T);
     if (!h) return NULL;
     const int n = ncm_gpt2_param_count(c);
     float *lnf = A(R * C), *logits = A(R * V);

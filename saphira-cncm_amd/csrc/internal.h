@@ -54,6 +54,16 @@ void ncm_adamw_update_clear(float *p, float *g, float *m, float *v, int64_t n, d
  * W [D][D][K]; launches only. */
 int ncm_conv1d_btd(const float *x, const float *W, const float *b, float *y, int B, int T, int D, int K, int stride,
                    int pad);
+/* SDPA forward (hd 64, 16-byte aligned operands) that also writes each
+ * query row's softmax (max, sum) to stats [B][Hq][Tq][2]; causal generates
+ * the mask (query t sees keys <= t + Tkv - Tq) instead of reading one. */
+void ncm_sdpa_fwd_stats(const float *q, const float *k, const float *v, const float *mask, float *out, float *stats,
+                        int B, int Hq, int Hkv, int Tq, int Tkv, int hd, int causal);
+/* SDPA backward that recomputes the probabilities from q, k and the row
+ * statistics of ncm_sdpa_fwd_stats (no stored P); gradients accumulate. */
+void ncm_sdpa_bwd_flash(const float *q, const float *k, const float *v, const float *o, const float *stats,
+                        const float *mask, int causal, const float *dO, float *dq, float *dk, float *dv, int B, int H,
+                        int Hkv, int Tq, int Tkv, int hd);
 /* Compute units of the selected device. */
 int ncm_cu_count(void);
 void *ncm_workspace(int slot, size_t bytes);

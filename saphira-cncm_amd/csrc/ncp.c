@@ -63,6 +63,8 @@ int ncm_ncp_rope_tables(int S, int hd, int base, float *cos_host, float *sin_hos
     return 0;
 }
 
+static int rope_upload(const int *pos, int n, int hd, int base, float **cd, float **sd);
+
 static float *A(int64_t n) {
     float *p = arena_alloc((size_t)n);
     if (!p) ncm_fail(NCM_E_OOM, "ncp: arena");
@@ -87,31 +89,52 @@ float *ncm_ncp_forward(const NcmNcpConfig *c, float *const *P, const int *ids, i
     const int C = c->n_embd, H = c->n_head, Kv = c->n_kv, hd = C / H, I = c->n_inner, V = c->vocab;
     const int QKV = C + 2 * Kv * hd, rep = H / Kv;
     const int64_t R = (int64_t)B * S;
-    float *cosd = A((int64_t)S * hd), *sind = A((int64_t)S * hd), *x = A(R * C);
+    float *x = A(R * C);
     int *bids = (int *)A(R);
-    float *hc = (float *)malloc((size_t)S * hd * sizeof(float)), *hs = (float *)malloc((size_t)S * hd * sizeof(float));
-    if (!bids || !hc || !hs) {
-        free(hc);
-        free(hs);
-        if (bids) ncm_fail(NCM_E_OOM, "ncp: host tables");
-        return NULL;
+    if (!bids) return NULL;
+    /* RoPE tables for positions 0..S-1 (ncp.c:80-92): built once per (S, hd,
+     * base) and kept on the device */
+    static float *tab_cos = NULL, *tab_sin = NULL;
+    static int tab_S = 0, tab_hd = 0, tab_base = 0;
+    if (!tab_cos || tab_S != S || tab_hd != hd || tab_base != c->rope_base) {
+        ncm_hip_free(tab_cos);
+        ncm_hip_free(tab_sin);
+        tab_cos = tab_sin = NULL;
+        int *pos = (int *)malloc((size_t)S * sizeof(int));
+        if (!pos) {
+            ncm_fail(NCM_E_OOM, "ncp: positions");
+            return NULL;
+        }
+        for (int t = 0; t < S; t++) pos[t] = t;
+        int rc = rope_upload(pos, S, hd, c->rope_base, &tab_cos, &tab_sin);
+        free(pos);
+        if (rc) return NULL;
+        tab_S = S;
+        tab_hd = hd;
+        tab_base = c->rope_base;
     }
-    ncm_ncp_rope_tables(S, hd, c->rope_base, hc, hs);
-    mem_h2d(cosd, hc, (size_t)S * hd * sizeof(float));
-    mem_h2d(sind, hs, (size_t)S * hd * sizeof(float));
-    free(hc);
-    free(hs);
+    const float *cosd = tab_cos, *sind = tab_sin;
     mem_h2d(bids, ids, (size_t)R * sizeof(int));
     embedding_fwd_v(P[0], V, bids, x, R, C);
-    float *ln = A(R * C), *qkv = A(R * QKV), *qq = A(R * C), *kk = A(R * C), *vv = A(R * C),
-          *mo = A(R * C), *g = A(R * I);
+    /* K and V at their kv-head count when the fused split applies (hd <= 64),
+     * else replicated to every query head as ncp.c:213-236 does */
+    const int fused = hd <= 64, hk = fused ? Kv : H;
+    float *ln = A(R * C), *qkv = A(R * QKV), *qq = A(R * C), *kk = A((int64_t)B * hk * S * hd),
+          *vv = A((int64_t)B * hk * S * hd), *mo = A(R * C), *g = A(R * I);
     if (!g) return NULL;
     for (int li = 0; li < c->n_layer; li++) {
         float *const *w = P + 1 + NCP_PER_LAYER * li;
         norm(c, x, w[0], w[1], ln, R);
         linear_fwd(ln, w[2], w[3], qkv, R, QKV, C);
-        qkv_split_rope_fwd(qkv, qq, kk, vv, cosd, sind, B, S, C, H, hd, Kv, rep);   /* split, then RoPE */
-        sdpa_fwd_gqa_merged(qq, kk, vv, NULL, mo, B, H, H, S, S, hd);               /* heads merged on output */
+        if (fused) {   /* split + RoPE, kv heads kept */
+            const float *nul = NULL;
+            int Bi = B, Si = S, Hi = H, Ki = Kv, hdi = hd;
+            void *a[] = {&qkv, &qq, &kk, &vv, &nul, &nul, &cosd, &sind, &Bi, &Si, &Hi, &Ki, &hdi};
+            if (ncm_launch_named("ncp_qkv_k", (unsigned)((R * (H + 2 * Kv) + 3) / 4), 1, 1, 256, a)) return NULL;
+        } else {
+            qkv_split_rope_fwd(qkv, qq, kk, vv, cosd, sind, B, S, C, H, hd, Kv, rep);   /* split, then RoPE */
+        }
+        sdpa_fwd_gqa_merged(qq, kk, vv, NULL, mo, B, H, hk, S, S, hd);              /* heads merged on output */
         linear_fwd_ep(mo, w[4], w[5], x, x, R, C, C, NCM_ACT_NONE);      /* x += c_proj(.) */
         norm(c, x, w[6], w[7], ln, R);
         linear_fwd_gated(ln, w[8], w[9], w[10], w[11], g, R, I, C, NCM_ACT_SILU);   /* silu(w_gate(.)) * w_up(.) */

@@ -170,7 +170,7 @@ void embedding_fwd(const float *W, const int *idx, float *y, int64_t n, int D) {
 /* ---- SDPA (kernels.c:364-507) ---- */
 /* out [B][Hq][Tq][hd], or [B][Tq][Hq * hd] (the heads merged) when merged */
 static void sdpa_any(const char *fn, const float *q, const float *k, const float *v, const float *mask, float *out,
-                     int B, int Hq, int Hkv, int Tq, int Tkv, int hd, int causal, int merged) {
+                     int B, int Hq, int Hkv, int Tq, int Tkv, int hd, int causal, int merged, float *stats) {
     if (B < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || Tq < 0 || Tkv <= 0 || hd <= 0 || hd > 256) {
         ncm_fail(NCM_E_ARG, "%s: bad shape B=%d Hq=%d Hkv=%d Tq=%d Tkv=%d hd=%d", fn, B, Hq, Hkv, Tq, Tkv, hd);
         return;
@@ -185,8 +185,10 @@ static void sdpa_any(const char *fn, const float *q, const float *k, const float
     if (ncm_ready()) return;
     float scale = 1.0f / sqrtf((float)hd);
     if (hd == 64 && is_aligned16(q) && is_aligned16(k) && is_aligned16(v) && is_aligned16(out)) {
-        void *a[] = {&q, &k, &v, &mask, &out, &Hq, &Hkv, &Tq, &Tkv, &scale, &causal, &merged};
+        void *a[] = {&q, &k, &v, &mask, &out, &Hq, &Hkv, &Tq, &Tkv, &scale, &causal, &merged, &stats};
         ncm_launch_named("sdpa_hd64", (unsigned)((Tq + 63) / 64), (unsigned)Hq, (unsigned)B, 256, a);
+    } else if (stats) {
+        ncm_fail(NCM_E_ARG, "%s: row statistics need hd = 64 and 16-byte aligned operands", fn);
     } else {
         int64_t rows = (int64_t)B * Hq * Tq;
         void *a[] = {&q, &k, &v, &mask, &out, &B, &Hq, &Hkv, &Tq, &Tkv, &hd, &scale, &causal, &merged};
@@ -196,20 +198,25 @@ static void sdpa_any(const char *fn, const float *q, const float *k, const float
 
 void sdpa_fwd_gqa(const float *q, const float *k, const float *v, const float *mask, float *out, int B, int Hq,
                   int Hkv, int Tq, int Tkv, int hd) {
-    sdpa_any("sdpa_fwd_gqa", q, k, v, mask, out, B, Hq, Hkv, Tq, Tkv, hd, 0, 0);
+    sdpa_any("sdpa_fwd_gqa", q, k, v, mask, out, B, Hq, Hkv, Tq, Tkv, hd, 0, 0, NULL);
 }
 
 void sdpa_fwd(const float *q, const float *k, const float *v, const float *mask, float *out, int B, int H, int Tq,
               int Tkv, int hd) {
-    sdpa_any("sdpa_fwd", q, k, v, mask, out, B, H, H, Tq, Tkv, hd, 0, 0);
+    sdpa_any("sdpa_fwd", q, k, v, mask, out, B, H, H, Tq, Tkv, hd, 0, 0, NULL);
 }
 
 void sdpa_fwd_gqa_merged(const float *q, const float *k, const float *v, const float *mask, float *out, int B,
                          int Hq, int Hkv, int Tq, int Tkv, int hd) {
-    sdpa_any("sdpa_fwd_gqa_merged", q, k, v, mask, out, B, Hq, Hkv, Tq, Tkv, hd, 0, 1);
+    sdpa_any("sdpa_fwd_gqa_merged", q, k, v, mask, out, B, Hq, Hkv, Tq, Tkv, hd, 0, 1, NULL);
 }
 
 void sdpa_fwd_gqa_causal(const float *q, const float *k, const float *v, float *out, int B, int Hq, int Hkv, int Tq,
                          int Tkv, int hd) {
-    sdpa_any("sdpa_fwd_gqa_causal", q, k, v, NULL, out, B, Hq, Hkv, Tq, Tkv, hd, 1, 0);
+    sdpa_any("sdpa_fwd_gqa_causal", q, k, v, NULL, out, B, Hq, Hkv, Tq, Tkv, hd, 1, 0, NULL);
+}
+
+void ncm_sdpa_fwd_stats(const float *q, const float *k, const float *v, const float *mask, float *out, float *stats,
+                        int B, int Hq, int Hkv, int Tq, int Tkv, int hd, int causal) {
+    sdpa_any("ncm_sdpa_fwd_stats", q, k, v, mask, out, B, Hq, Hkv, Tq, Tkv, hd, causal, 0, stats);
 }

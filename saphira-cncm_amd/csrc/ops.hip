@@ -225,7 +225,7 @@ eltwise_k(const float *a, const float *b, float *y, float s, int64_t n, int op) 
 extern "C" __global__ void __launch_bounds__(256)
 sdpa_hd64(const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
           const float *__restrict__ mask, float *__restrict__ out, int Hq, int Hkv, int Tq, int Tkv,
-          float scale, int causal, int merged) {
+          float scale, int causal, int merged, float *__restrict__ stats) {
     __shared__ __attribute__((aligned(16))) float sK[SD_T * SD_LD];
     __shared__ __attribute__((aligned(16))) float sV[SD_T * SD_LD];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -253,23 +253,35 @@ sdpa_hd64(const float *__restrict__ q, const float *__restrict__ k, const float 
     const int coff = Tkv - Tq;   // causal offset of the query positions
     int kend = Tkv;
     if (causal) kend = min(Tkv, q0 + 64 + coff);
-    for (int k0 = 0; k0 < kend; k0 += SD_T) {
-        __syncthreads();
-        // stage K and V tiles (64 keys x 64 d), rows beyond Tkv as zero
+    // K and V tiles (64 keys x 64 d, rows beyond Tkv as zero): the next tile
+    // is loaded into registers while the current one is used from LDS
+    f4 pk[4], pv[4];
+    auto load_tile = [&](int k0) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int f = tid + j * 256;
             const int r = f >> 4, c = (f & 15) * 4;
             const int key = k0 + r;
-            f4 kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
+            pk[j] = f4{0.f, 0.f, 0.f, 0.f};
+            pv[j] = f4{0.f, 0.f, 0.f, 0.f};
             if (key < Tkv) {
-                kv = *(const f4 *)(kb + (int64_t)key * 64 + c);
-                vv = *(const f4 *)(vb + (int64_t)key * 64 + c);
+                pk[j] = *(const f4 *)(kb + (int64_t)key * 64 + c);
+                pv[j] = *(const f4 *)(vb + (int64_t)key * 64 + c);
             }
-            *(f4 *)(sK + r * SD_LD + c) = kv;
-            *(f4 *)(sV + r * SD_LD + c) = vv;
+        }
+    };
+    if (kend > 0) load_tile(0);
+    for (int k0 = 0; k0 < kend; k0 += SD_T) {
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int f = tid + j * 256;
+            const int r = f >> 4, c = (f & 15) * 4;
+            *(f4 *)(sK + r * SD_LD + c) = pk[j];
+            *(f4 *)(sV + r * SD_LD + c) = pv[j];
         }
         __syncthreads();
+        if (k0 + SD_T < kend) load_tile(k0 + SD_T);
 
         // S^T[c]: keys k0 + 16c + 4lg + r, query my_q
         f4 s[4];
@@ -332,6 +344,12 @@ sdpa_hd64(const float *__restrict__ q, const float *__restrict__ k, const float 
             }
     }
 
+    // the row statistics a recomputing backward needs: (max, sum) of query my_q
+    if (stats && lg == 0 && my_q < Tq) {
+        float *st = stats + (((int64_t)b * Hq + h) * Tq + my_q) * 2;
+        st[0] = m_run;
+        st[1] = l_run;
+    }
     // normalise by l of query qw + 4lg + r and store float4 along d
 #pragma unroll
     for (int r = 0; r < 4; ++r) {

@@ -84,7 +84,8 @@ typedef struct {
     NtKind op;
     const float *a, *b, *c;
     float *y;
-    float *aux;                 /* SDPA: P; CE: dlogits */
+    float *aux;                 /* SDPA: P, or the row statistics (p6 & 1); CE: dlogits */
+    const float *mask;          /* SDPA: the additive mask (may be NULL) */
     int *ids;                   /* EMBED: host copy of the ids */
     const float *cos_t, *sin_t; /* ROPE tables */
     int64_t n;
@@ -286,16 +287,51 @@ void ncm_t_rope(NcmTape *t, const float *xq, const float *xk, float *yq, float *
     r->n = B; r->p1 = H; r->p2 = T; r->p3 = hd; r->p4 = Hkv;
 }
 
+/* The forward of an SDPA record.  hd = 64 with aligned operands (the MFMA
+ * path): the forward also keeps each query row's softmax (max, sum), and the
+ * backward rebuilds P from them (p6 bit 0; bit 1 = causal); otherwise P is
+ * stored, as the reference's t_sdpa keeps it (train_tape.c:289-313). */
+static void t_sdpa_any(NcmTape *t, const float *q, const float *k, const float *v, const float *mask, int causal,
+                       float *o, int B, int H, int Hkv, int Tq, int Tkv, int hd) {
+    if (Hkv < 1 || H % Hkv) { ncm_fail(NCM_E_ARG, "ncm_t_sdpa: H=%d Hkv=%d", H, Hkv); return; }
+    const int flash = hd == 64 && Tkv % 4 == 0 && is_aligned16(q) && is_aligned16(k) && is_aligned16(v) &&
+                      is_aligned16(o);
+    float *aux;
+    if (flash) {
+        aux = (float *)pool_alloc(&t->rec, (size_t)B * H * Tq * 2 * sizeof(float));
+        if (!aux) { ncm_fail(NCM_E_OOM, "ncm_t_sdpa: row statistics"); return; }
+        ncm_sdpa_fwd_stats(q, k, v, mask, o, aux, B, H, Hkv, Tq, Tkv, hd, causal);
+    } else {
+        float *m = NULL;
+        if (causal) {   /* the -1e9 causal mask of the reference's callers */
+            m = (float *)pool_alloc(&t->rec, (size_t)Tq * Tkv * sizeof(float));
+            float *hm = (float *)malloc((size_t)Tq * Tkv * sizeof(float));
+            if (!m || !hm) { free(hm); ncm_fail(NCM_E_OOM, "ncm_t_sdpa: mask"); return; }
+            for (int i = 0; i < Tq; i++)
+                for (int j = 0; j < Tkv; j++) hm[(size_t)i * Tkv + j] = j <= i + (Tkv - Tq) ? 0.0f : -1e9f;
+            mem_h2d(m, hm, (size_t)Tq * Tkv * sizeof(float));
+            free(hm);
+            mask = m;
+        }
+        sdpa_fwd_gqa(q, k, v, mask, o, B, H, Hkv, Tq, Tkv, hd);
+        aux = (float *)pool_alloc(&t->rec, (size_t)B * H * Tq * Tkv * sizeof(float));
+        if (!aux) { ncm_fail(NCM_E_OOM, "ncm_t_sdpa: probabilities"); return; }
+        sdpa_probs_gqa(q, k, mask, aux, B, H, Hkv, Tq, Tkv, hd);
+    }
+    REC_OR_RETURN(r, t, NT_SDPA);
+    r->a = q; r->b = k; r->c = v; r->y = o; r->aux = aux; r->mask = mask;
+    r->n = B; r->p1 = H; r->p2 = Hkv; r->p3 = Tq; r->p4 = Tkv; r->p5 = hd; r->p6 = flash | (causal ? 2 : 0);
+}
+
 void ncm_t_sdpa(NcmTape *t, const float *q, const float *k, const float *v, const float *mask, float *o, int B,
                 int H, int Hkv, int Tq, int Tkv, int hd) {
-    if (Hkv < 1 || H % Hkv) { ncm_fail(NCM_E_ARG, "ncm_t_sdpa: H=%d Hkv=%d", H, Hkv); return; }
-    sdpa_fwd_gqa(q, k, v, mask, o, B, H, Hkv, Tq, Tkv, hd);
-    float *P = (float *)pool_alloc(&t->rec, (size_t)B * H * Tq * Tkv * sizeof(float));
-    if (!P) { ncm_fail(NCM_E_OOM, "ncm_t_sdpa: probabilities"); return; }
-    sdpa_probs_gqa(q, k, mask, P, B, H, Hkv, Tq, Tkv, hd);
-    REC_OR_RETURN(r, t, NT_SDPA);
-    r->a = q; r->b = k; r->c = v; r->y = o; r->aux = P;
-    r->n = B; r->p1 = H; r->p2 = Hkv; r->p3 = Tq; r->p4 = Tkv; r->p5 = hd;
+    t_sdpa_any(t, q, k, v, mask, 0, o, B, H, Hkv, Tq, Tkv, hd);
+}
+
+void ncm_t_sdpa_causal(NcmTape *t, const float *q, const float *k, const float *v, float *o, int B, int H, int Hkv,
+                       int Tq, int Tkv, int hd) {
+    if (Tq > Tkv) { ncm_fail(NCM_E_ARG, "ncm_t_sdpa_causal: Tq %d > Tkv %d", Tq, Tkv); return; }
+    t_sdpa_any(t, q, k, v, NULL, 1, o, B, H, Hkv, Tq, Tkv, hd);
 }
 
 void ncm_t_qkvsplit(NcmTape *t, const float *in, float *qq, float *kk, float *vv, int B, int T, int C, int H, int hd,
@@ -418,9 +454,13 @@ void ncm_tape_backward(NcmTape *t, const NcmPMap *pm) {
         }
         case NT_SDPA: {
             int B = (int)r->n, H = r->p1, Hkv = r->p2, Tq = r->p3, Tkv = r->p4, hd = r->p5;
-            sdpa_bwd_gqa(r->a, r->b, r->c, r->aux, dy, gmap_get(t, r->a, (int64_t)B * H * Tq * hd),
-                         gmap_get(t, r->b, (int64_t)B * Hkv * Tkv * hd), gmap_get(t, r->c, (int64_t)B * Hkv * Tkv * hd),
-                         B, H, Hkv, Tq, Tkv, hd);
+            float *gq = gmap_get(t, r->a, (int64_t)B * H * Tq * hd);
+            float *gk = gmap_get(t, r->b, (int64_t)B * Hkv * Tkv * hd), *gv = gmap_get(t, r->c, (int64_t)B * Hkv * Tkv * hd);
+            if (r->p6 & 1)
+                ncm_sdpa_bwd_flash(r->a, r->b, r->c, r->y, r->aux, r->mask, (r->p6 >> 1) & 1, dy, gq, gk, gv, B, H,
+                                   Hkv, Tq, Tkv, hd);
+            else
+                sdpa_bwd_gqa(r->a, r->b, r->c, r->aux, dy, gq, gk, gv, B, H, Hkv, Tq, Tkv, hd);
             break;
         }
         case NT_SPLIT: {

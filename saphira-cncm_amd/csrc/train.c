@@ -170,6 +170,39 @@ void sdpa_bwd_gqa(const float *q, const float *k, const float *v, const float *P
     }
 }
 
+/* The recomputing backward of the tape's SDPA records (hd 64, aligned): D =
+ * rowsum(dO o O), then the dq and dk/dv kernels rebuild P tile by tile from
+ * the forward's row statistics.  Gradients accumulate. */
+void ncm_sdpa_bwd_flash(const float *q, const float *k, const float *v, const float *o, const float *stats,
+                        const float *mask, int causal, const float *dO, float *dq, float *dk, float *dv, int B, int H,
+                        int Hkv, int Tq, int Tkv, int hd) {
+    if (attn_check("ncm_sdpa_bwd_flash", B, H, Hkv, Tq, Tkv, hd)) return;
+    if ((int64_t)B * Tq == 0 || (!dq && !dk && !dv)) return;
+    if (hd != 64 || !q || !k || !v || !o || !stats || !dO) {
+        ncm_fail(NCM_E_ARG, "ncm_sdpa_bwd_flash: hd %d (64 only) or null input", hd);
+        return;
+    }
+    if (causal && Tq > Tkv) {
+        ncm_fail(NCM_E_ARG, "ncm_sdpa_bwd_flash: causal attention needs Tq <= Tkv");
+        return;
+    }
+    if (ncm_ready()) return;
+    const int64_t rows = (int64_t)B * H * Tq;
+    float *D = (float *)ncm_workspace(WS_TRAIN, (size_t)rows * sizeof(float));
+    if (!D) return;
+    float scale = 1.0f / sqrtf((float)hd);
+    void *a0[] = {&dO, &o, &D, (void *)&rows, &hd};
+    if (ncm_launch_named("sdpa_bwd_rowdot", blocks_of(rows, 4), 1, 1, 256, a0)) return;
+    if (dq) {
+        void *a[] = {&q, &k, &v, &mask, &stats, &D, &dO, &dq, &H, &Hkv, &Tq, &Tkv, &scale, &causal};
+        if (ncm_launch_named("sdpa_fbwd_dq_hd64", blocks_of(Tq, 64), (unsigned)H, (unsigned)B, 256, a)) return;
+    }
+    if (dk || dv) {
+        void *a[] = {&q, &k, &v, &mask, &stats, &D, &dO, &dk, &dv, &H, &Hkv, &Tq, &Tkv, &scale, &causal};
+        ncm_launch_named("sdpa_fbwd_dkdv_hd64", blocks_of(Tkv, 64), (unsigned)Hkv, (unsigned)B, 256, a);
+    }
+}
+
 /* ---- optimizer (train.c:51-64, 102-145, 172-178; train_gpt2.c:160-173) ---- */
 static void adamw_any(float *p, float *g, float *m, float *v, int64_t n, double lr, double b1, double b2,
                       double b1t, double b2t, double eps, double wd, int clear_g) {

@@ -898,3 +898,301 @@ axpy_k(float *__restrict__ dx, const float *__restrict__ dy, float s, int64_t n)
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i < n) dx[i] = dx[i] + dy[i] * s;
 }
+
+// ---------------------------------------------------------------- recomputing (flash) backward
+// The SDPA backward of the tape without stored probabilities: P is rebuilt
+// tile by tile from q, k and each query row's softmax (max m, sum l) saved by
+// the forward, P = exp(s scale + mask - m) / l, with the forward's own
+// arithmetic.  D = rowsum(P o dP) is formed as rowsum(dO o O), its equal
+// (sum_k P dP = sum_k P (dO . v_k) = dO . sum_k P v_k = dO . O).
+
+// D[row] = sum_d dO[row][d] O[row][d] (fp64 sum), one wave per row, hd <= 64
+extern "C" __global__ void __launch_bounds__(256)
+sdpa_bwd_rowdot(const float *__restrict__ dO, const float *__restrict__ O, float *__restrict__ D, int64_t rows,
+                int hd) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    double s = lane < hd ? (double)dO[row * hd + lane] * (double)O[row * hd + lane] : 0.0;
+    s = wave_sum_d(s);
+    if (lane == 0) D[row] = (float)s;
+}
+
+// dq: 64 queries of one (b, h) per workgroup, wave w the queries q0 + 16w + li.
+// Per key tile: S^T = K Q^T and dP^T = V dO^T in the layout (key 16c + 4g + r,
+// query li), P and dS^T = P^T o (dP^T - D) in place, dq += dS K with dS^T as the
+// A operand (as sdpa_bwd_dq_hd64's second sweep).  Causal: key tiles past the
+// tile's last query are skipped (their P is exactly 0).
+extern "C" __global__ void __launch_bounds__(256)
+sdpa_fbwd_dq_hd64(const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+                  const float *__restrict__ mask, const float *__restrict__ stats, const float *__restrict__ D,
+                  const float *__restrict__ dO, float *__restrict__ dq, int H, int Hkv, int Tq, int Tkv, float scale,
+                  int causal) {
+    __shared__ __attribute__((aligned(16))) float sK[64 * SB_LD];
+    __shared__ __attribute__((aligned(16))) float sV[64 * SB_LD];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4;
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int kvh = h / (H / Hkv);
+    const int q0 = blockIdx.x * 64, qw = q0 + wave * 16;
+    const int my_q = qw + li;
+    const int64_t rbase = ((int64_t)b * H + h) * Tq;
+    const float *kb = k + ((int64_t)b * Hkv + kvh) * Tkv * 64;
+    const float *vb = v + ((int64_t)b * Hkv + kvh) * Tkv * 64;
+    const bool qok = my_q < Tq;
+
+    f4 qf[4], gf[4];   // Q^T and dO^T fragments: query my_q, d = 16kc + 4g .. +3
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+        qf[kc] = qok ? *(const f4 *)(q + (rbase + my_q) * 64 + kc * 16 + 4 * lg) : f4{0.f, 0.f, 0.f, 0.f};
+        gf[kc] = qok ? *(const f4 *)(dO + (rbase + my_q) * 64 + kc * 16 + 4 * lg) : f4{0.f, 0.f, 0.f, 0.f};
+    }
+    const float mq = qok ? stats[(rbase + my_q) * 2] : 0.f;
+    const float il = qok ? 1.0f / stats[(rbase + my_q) * 2 + 1] : 0.f;
+    const float dq_d = qok ? D[rbase + my_q] : 0.f;
+    f4 acc[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[u] = f4{0.f, 0.f, 0.f, 0.f};
+
+    const int coff = Tkv - Tq;
+    int kend = Tkv;
+    if (causal) kend = min(Tkv, q0 + 64 + coff);
+    // the next tile's K and V rows are loaded into registers while the
+    // current tile is computed from LDS
+    f4 pk[4], pv[4];
+    auto load_tile = [&](int k0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int f = tid + j * 256;
+            const int r = f >> 4, c = (f & 15) * 4;
+            const int key = k0 + r;
+            pv[j] = f4{0.f, 0.f, 0.f, 0.f};
+            pk[j] = f4{0.f, 0.f, 0.f, 0.f};
+            if (key < Tkv) {
+                pv[j] = *(const f4 *)(vb + (int64_t)key * 64 + c);
+                pk[j] = *(const f4 *)(kb + (int64_t)key * 64 + c);
+            }
+        }
+    };
+    if (kend > 0) load_tile(0);
+    for (int k0 = 0; k0 < kend; k0 += 64) {
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int f = tid + j * 256;
+            const int r = f >> 4, c = (f & 15) * 4;
+            *(f4 *)(sV + r * SB_LD + c) = pv[j];
+            *(f4 *)(sK + r * SB_LD + c) = pk[j];
+        }
+        __syncthreads();
+        if (k0 + 64 < kend) load_tile(k0 + 64);
+        f4 s[4], dp[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            s[c] = f4{0.f, 0.f, 0.f, 0.f};
+            dp[c] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kc = 0; kc < 4; ++kc) {
+                const f4 kf = *(const f4 *)(sK + (16 * c + li) * SB_LD + kc * 16 + 4 * lg);
+                const f4 vf = *(const f4 *)(sV + (16 * c + li) * SB_LD + kc * 16 + 4 * lg);
+#pragma unroll
+                for (int st = 0; st < 4; ++st) {
+                    s[c] = mfma4(kf[st], qf[kc][st], s[c]);
+                    dp[c] = mfma4(vf[st], gf[kc][st], dp[c]);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int key = k0 + 16 * c + 4 * lg + r;
+                float x = s[c][r] * scale;
+                if (mask && key < Tkv && qok) x += mask[(int64_t)my_q * Tkv + key];
+                if (key >= Tkv || (causal && key > my_q + coff)) x = -INFINITY;
+                const float p = qok ? __expf(x - mq) * il : 0.f;
+                dp[c][r] = p * (dp[c][r] - dq_d);
+            }
+        }
+        // dq[query qw + 4g + r][d = 4li + u] += dS[query][key] K[key][d]
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const f4 kf = *(const f4 *)(sK + (16 * c + 4 * lg + st) * SB_LD + 4 * li);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) acc[u] = mfma4(dp[c][st], kf[u], acc[u]);
+            }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int qi = qw + 4 * lg + r;
+        if (qi < Tq) {
+            f4 *o = (f4 *)(dq + (rbase + qi) * 64 + 4 * li);
+            f4 cur = *o;
+            cur[0] += scale * acc[0][r];
+            cur[1] += scale * acc[1][r];
+            cur[2] += scale * acc[2][r];
+            cur[3] += scale * acc[3][r];
+            *o = cur;
+        }
+    }
+}
+
+// dk / dv: 64 keys of one (b, kv head) per workgroup, wave w the keys
+// k0 + 16w + li.  For every query head of the group and query tile: S = Q K^T
+// and dP = dO V^T in the layout (query 16c + 4g + r, key li), P and dS in
+// registers (no transposed copy of P), dV += P^T dO, dK += dS^T Q.  Causal:
+// query tiles before the first query that sees this key tile are skipped.
+extern "C" __global__ void __launch_bounds__(256)
+sdpa_fbwd_dkdv_hd64(const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+                    const float *__restrict__ mask, const float *__restrict__ stats, const float *__restrict__ D,
+                    const float *__restrict__ dO, float *__restrict__ dk, float *__restrict__ dv, int H, int Hkv,
+                    int Tq, int Tkv, float scale, int causal) {
+    __shared__ __attribute__((aligned(16))) float sG[64 * SB_LD];   // dO tile [query][d]
+    __shared__ __attribute__((aligned(16))) float sQ[64 * SB_LD];   // Q tile  [query][d]
+    __shared__ __attribute__((aligned(16))) float sM[64];
+    __shared__ __attribute__((aligned(16))) float sL[64];
+    __shared__ __attribute__((aligned(16))) float sD[64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4;
+    const int kvh = blockIdx.y, b = blockIdx.z;
+    const int rep = H / Hkv;
+    const int k0 = blockIdx.x * 64;
+    const int kl = wave * 16 + li;
+    const int my_k = k0 + kl;
+    const bool kok = my_k < Tkv;
+    const int64_t kbase = ((int64_t)b * Hkv + kvh) * Tkv;
+
+    f4 vf[4], kf[4];   // V and K fragments: key my_k, d = 16kc + 4g .. +3
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+        vf[kc] = kok ? *(const f4 *)(v + (kbase + my_k) * 64 + kc * 16 + 4 * lg) : f4{0.f, 0.f, 0.f, 0.f};
+        kf[kc] = kok ? *(const f4 *)(k + (kbase + my_k) * 64 + kc * 16 + 4 * lg) : f4{0.f, 0.f, 0.f, 0.f};
+    }
+    f4 ak[4], av[4];   // [u][r]: key k0 + 16w + 4g + r, d = 4li + u
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        ak[u] = f4{0.f, 0.f, 0.f, 0.f};
+        av[u] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+    const int coff = Tkv - Tq;
+    int qstart = 0;
+    if (causal) {   // the first query that sees key k0 is k0 - coff
+        const int first = k0 - coff;
+        qstart = first > 0 ? (first / 64) * 64 : 0;
+    }
+    // the (query head, query tile) pairs in order; the next pair's dO and Q
+    // rows and row statistics are loaded into registers while the current one
+    // is computed from LDS
+    const int nq = qstart < Tq ? (Tq - qstart + 63) / 64 : 0, niter = rep * nq;
+    f4 pg[4], pq[4];
+    float pm = 0.f, pl = 0.f, pd = 0.f;
+    auto load_tile = [&](int it) {
+        const int h = kvh * rep + it / nq, q0 = qstart + (it % nq) * 64;
+        const int64_t rbase = ((int64_t)b * H + h) * Tq;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int f = tid + j * 256;
+            const int r = f >> 4, c = (f & 15) * 4;
+            const int qi = q0 + r;
+            pg[j] = f4{0.f, 0.f, 0.f, 0.f};
+            pq[j] = f4{0.f, 0.f, 0.f, 0.f};
+            if (qi < Tq) {
+                pg[j] = *(const f4 *)(dO + (rbase + qi) * 64 + c);
+                pq[j] = *(const f4 *)(q + (rbase + qi) * 64 + c);
+            }
+        }
+        if (tid < 64) {
+            const int qi = q0 + tid;
+            const bool ok = qi < Tq;
+            pm = ok ? stats[(rbase + qi) * 2] : 0.f;
+            pl = ok ? 1.0f / stats[(rbase + qi) * 2 + 1] : 0.f;
+            pd = ok ? D[rbase + qi] : 0.f;
+        }
+    };
+    if (niter > 0) load_tile(0);
+    for (int it = 0; it < niter; ++it) {
+        const int q0 = qstart + (it % nq) * 64;
+        {
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int f = tid + j * 256;
+                const int r = f >> 4, c = (f & 15) * 4;
+                *(f4 *)(sG + r * SB_LD + c) = pg[j];
+                *(f4 *)(sQ + r * SB_LD + c) = pq[j];
+            }
+            if (tid < 64) {
+                sM[tid] = pm;
+                sL[tid] = pl;
+                sD[tid] = pd;
+            }
+            __syncthreads();
+            if (it + 1 < niter) load_tile(it + 1);
+            f4 dp[4], pf[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                dp[c] = f4{0.f, 0.f, 0.f, 0.f};
+                f4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kc = 0; kc < 4; ++kc) {
+                    const f4 gfr = *(const f4 *)(sG + (16 * c + li) * SB_LD + kc * 16 + 4 * lg);
+                    const f4 qfr = *(const f4 *)(sQ + (16 * c + li) * SB_LD + kc * 16 + 4 * lg);
+#pragma unroll
+                    for (int st = 0; st < 4; ++st) {
+                        dp[c] = mfma4(gfr[st], vf[kc][st], dp[c]);
+                        s = mfma4(qfr[st], kf[kc][st], s);
+                    }
+                }
+                const f4 mm = *(const f4 *)(sM + 16 * c + 4 * lg);
+                const f4 ll = *(const f4 *)(sL + 16 * c + 4 * lg);
+                const f4 dd = *(const f4 *)(sD + 16 * c + 4 * lg);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int qi = q0 + 16 * c + 4 * lg + r;
+                    float x = s[r] * scale;
+                    if (mask && qi < Tq && kok) x += mask[(int64_t)qi * Tkv + my_k];
+                    if (!kok || (causal && my_k > qi + coff)) x = -INFINITY;
+                    const float p = qi < Tq ? __expf(x - mm[r]) * ll[r] : 0.f;
+                    pf[c][r] = p;
+                    dp[c][r] = p * (dp[c][r] - dd[r]);
+                }
+            }
+            // dV += P^T dO, dK += dS^T Q
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int st = 0; st < 4; ++st) {
+                    const f4 gfr = *(const f4 *)(sG + (16 * c + 4 * lg + st) * SB_LD + 4 * li);
+                    const f4 qfr = *(const f4 *)(sQ + (16 * c + 4 * lg + st) * SB_LD + 4 * li);
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        av[u] = mfma4(pf[c][st], gfr[u], av[u]);
+                        ak[u] = mfma4(dp[c][st], qfr[u], ak[u]);
+                    }
+                }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int key = k0 + wave * 16 + 4 * lg + r;
+        if (key < Tkv) {
+            if (dk) {
+                f4 *o = (f4 *)(dk + (kbase + key) * 64 + 4 * li);
+                f4 cur = *o;
+                cur[0] += scale * ak[0][r];
+                cur[1] += scale * ak[1][r];
+                cur[2] += scale * ak[2][r];
+                cur[3] += scale * ak[3][r];
+                *o = cur;
+            }
+            if (dv) {
+                f4 *o = (f4 *)(dv + (kbase + key) * 64 + 4 * li);
+                f4 cur = *o;
+                cur[0] += av[0][r];
+                cur[1] += av[1][r];
+                cur[2] += av[2][r];
+                cur[3] += av[3][r];
+                *o = cur;
+            }
+        }
+    }
+}

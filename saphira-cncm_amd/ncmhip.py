@@ -121,6 +121,7 @@ _SIGS = {
     "ncm_t_scale": (None, [vp, vp, ctypes.c_float, vp, i64]),
     "ncm_t_rope": (None, [vp] * 7 + [ci] * 5),
     "ncm_t_sdpa": (None, [vp] * 6 + [ci] * 6),
+    "ncm_t_sdpa_causal": (None, [vp] * 5 + [ci] * 6),
     "ncm_t_qkvsplit": (None, [vp] * 5 + [ci] * 7),
     "ncm_t_headmerge": (None, [vp] * 3 + [ci] * 5),
     "ncm_t_headsplit": (None, [vp] * 3 + [ci] * 5),

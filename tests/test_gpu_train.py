@@ -252,3 +252,57 @@ def test_split_merge_bwd(B, T, C, H, hd, K, rep):
     dxs = up(x0)
     ncmhip.call("heads_transpose_bwd", up(dys), dxs, B, T, C, H, hd)
     assert bits_equal(dxs.numpy(), O.heads_transpose_bwd(dys, B, T, C, H, hd, x0))
+
+
+# ---------------------------------------------------------------- the tape's recomputing SDPA backward
+class _PMap(ctypes.Structure):
+    _fields_ = [("params", ctypes.c_void_p), ("grads", ctypes.c_void_p), ("sizes", ctypes.c_void_p),
+                ("n", ctypes.c_int)]
+
+
+@pytest.mark.parametrize("B,H,Hkv,Tq,Tkv,hd,kind", [
+    (2, 12, 12, 512, 512, 64, "causal"),    # config 5 heads and length, the generated causal mask
+    (2, 12, 12, 512, 512, 64, "mask"),      # the same with the reference's -1e9 mask read from memory
+    (1, 14, 2, 100, 164, 64, "causal"),     # GQA, Tq < Tkv (bottom-right causal), ragged tiles
+    (1, 4, 2, 96, 96, 64, "random"),        # an arbitrary additive mask
+    (1, 4, 2, 81, 81, 64, "causal"),        # Tkv % 4 != 0: stored probabilities, as the reference
+    (2, 6, 3, 33, 33, 32, "causal"),        # hd != 64: stored probabilities
+])
+def test_tape_sdpa_backward(B, H, Hkv, Tq, Tkv, hd, kind):
+    """One SDPA record on the device tape (ncm_t_sdpa / ncm_t_sdpa_causal) and
+    its backward against the oracle's restatement of t_sdpa + its backward
+    case (train_tape.c:289-313, 936-1051), upstream gradient dO."""
+    lib = ncmhip.load()
+    q, k, v = rnd(60, B, H, Tq, hd), rnd(61, B, Hkv, Tkv, hd), rnd(62, B, Hkv, Tkv, hd)
+    dO = rnd(63, B, H, Tq, hd)
+    if kind == "random":
+        mask = np.where(np.random.default_rng(64).random((Tq, Tkv)) < 0.3, -1e9, 0.0).astype(np.float32)
+        mask[:, 0] = 0.0
+    else:
+        mask = causal(Tq, Tkv)
+    P = O.sdpa_probs(q, k, mask)
+    rdq, rdk, rdv = O.sdpa_bwd(q, k, v, P, dO)
+    qd, kd, vd, od = up(q), up(k), up(v), D.empty(q.shape)
+    gq, gk, gv, go = (D.from_numpy(np.zeros_like(a)) for a in (q, k, v, dO))
+    go.upload(dO)
+    md = up(mask)
+    tape = lib.ncm_tape_new()
+    try:
+        if kind == "causal":
+            lib.ncm_t_sdpa_causal(tape, qd.ptr, kd.ptr, vd.ptr, od.ptr, B, H, Hkv, Tq, Tkv, hd)
+        else:
+            lib.ncm_t_sdpa(tape, qd.ptr, kd.ptr, vd.ptr, md.ptr, od.ptr, B, H, Hkv, Tq, Tkv, hd)
+        ncmhip.check()
+        assert np.max(np.abs(od.numpy() - O.sdpa_gqa(q, k, v, mask))) <= 1e-5
+        ptrs = (ctypes.c_void_p * 4)(od.ptr, qd.ptr, kd.ptr, vd.ptr)
+        grads = (ctypes.c_void_p * 4)(go.ptr, gq.ptr, gk.ptr, gv.ptr)
+        sizes = (ctypes.c_int64 * 4)(dO.size, q.size, k.size, v.size)
+        pm = _PMap(ctypes.cast(ptrs, ctypes.c_void_p), ctypes.cast(grads, ctypes.c_void_p),
+                   ctypes.cast(sizes, ctypes.c_void_p), 4)
+        lib.ncm_tape_backward(tape, ctypes.byref(pm))
+        ncmhip.check()
+        for got, ref in ((gq, rdq), (gk, rdk), (gv, rdv)):
+            g = got.numpy()
+            assert np.max(np.abs(g - ref)) <= 1e-4 and maxrel(g, ref) <= 1e-4, (kind, float(np.max(np.abs(g - ref))))
+    finally:
+        lib.ncm_tape_free(tape)

@@ -41,22 +41,23 @@ PEAK_HBM_GBS = 8000.0
 SHAPES = [(768, 2304), (768, 3072), (3072, 768), (896, 4864), (4864, 896)]  # (K, N)
 MS = [1, 64, 512, 4096]
 CPU_MS = [1, 64, 512]
-# HBM bytes per launch of the roofline kernel over its standalone launches,
-# measured with two rocprofv3 counter passes (FETCH_SIZE, then WRITE_SIZE) of
-# "bench.py --steps 2 --warmup 1 --no-cpu --no-extras --copy-calibration",
-# each scaled by what the counter reads for the run's 256 MiB copies; valid
-# while the same kernel and launches are the roofline.
-TRAFFIC = {("gemm_64x64_dx_v", ("dX M=4096 3072->768", "dX M=4096 4864->896", "dX M=4096 768->2304",
-                                "dX M=4096 768->3072")): 211.4e6}
+# HBM bytes per launch of the roofline kernel are measured in each run by two
+# rocprofv3 counter passes (FETCH_SIZE, then WRITE_SIZE) over a child process
+# that repeats the roofline kernel's own launches (measure_traffic below).
+TRAFFIC_REPS = 3
 
 
-def build_workload(ncmhip, seed=0):
+def build_workload(ncmhip, seed=0, only=None):
+    """The sweep's 80 calls (or those whose label is in `only`), with their
+    operands on the device: (kernel, flops, label, call, single-kernel call?)."""
     D = ncmhip.DeviceBuffer
     rng = np.random.default_rng(seed)
     calls = []
     keep = []
     for M in MS:
         for K, N in SHAPES:
+            if only is not None and not any(l.endswith(f" M={M} {K}->{N}") for l in only):
+                continue
             x = D.from_numpy(rng.standard_normal((M, K), dtype=np.float32))
             W = D.from_numpy((rng.standard_normal((N, K), dtype=np.float32) / np.float32(np.sqrt(K))))
             b = D.from_numpy((rng.standard_normal(N, dtype=np.float32) * np.float32(0.02)))
@@ -82,7 +83,85 @@ def build_workload(ncmhip, seed=0):
             calls.append(("colsum_partial_v", 0.0, f"db M={M} {K}->{N}",
                           lambda x=x, W=W, dy=dy, db=db, M=M, N=N, K=K:
                           ncmhip.linear_bwd(x, W, dy, None, None, db, M, N, K), False))
+    if only is not None:
+        calls = [c for c in calls if c[2] in only]
     return calls, keep
+
+
+def algo_bytes(labels):
+    """Mean algorithmic HBM bytes per call over sweep labels ("fwd|dX|dW M=m
+    k->n"): each operand read once, each output written once, and the
+    accumulated gradient (dX or dW) also read once."""
+    tot = 0.0
+    for lab in labels:
+        op, m, kn = lab.split()
+        M = int(m[2:])
+        K, N = (int(v) for v in kn.split("->"))
+        if op == "fwd":
+            b = M * K + N * K + N + M * N
+        elif op == "dX":
+            b = M * N + N * K + 2 * M * K
+        else:
+            b = M * N + M * K + 2 * N * K
+        tot += 4.0 * b
+    return tot / len(labels)
+
+
+def traffic_child(labels, reps):
+    """Counter-pass child: three 256 MiB device copies (the known-size
+    calibration) and `reps` rounds of the given sweep calls."""
+    import ncmhip
+    ncmhip.init(0)
+    src, dst = ncmhip.DeviceBuffer(256 << 20), ncmhip.DeviceBuffer(256 << 20)
+    for _ in range(3):
+        ncmhip.load().mem_d2d(dst.ptr, src.ptr, 256 << 20)
+    ncmhip.check()
+    del src, dst
+    calls, keep = build_workload(ncmhip, only=set(labels))
+    for _ in range(reps):
+        for c in calls:
+            c[3]()
+    ncmhip.sync()
+    ncmhip.check()
+
+
+def measure_traffic(kernel, labels, reps=TRAFFIC_REPS):
+    """HBM bytes per launch of `kernel` over the sweep calls `labels`: one
+    rocprofv3 --pmc pass per counter (FETCH_SIZE, WRITE_SIZE) of a child that
+    repeats those calls, each counter scaled by what it reads for the child's
+    256 MiB copies.  Returns (bytes or None, note)."""
+    import csv
+    import glob
+    import shutil
+    import tempfile
+    prof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(prof):
+        return None, "rocprofv3 not found"
+    total, parts = 0.0, []
+    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = tempfile.mkdtemp(prefix="ncm_traffic_", dir="/tmp")
+        cmd = ["timeout", "-s", "KILL", "120", prof, "--pmc", ctr, "--output-format", "csv", "-d", d, "-o", "t",
+               "--", sys.executable, os.path.abspath(__file__), "--traffic-child", ";".join(labels),
+               "--traffic-reps", str(reps)]
+        try:
+            subprocess.run(cmd, check=True, capture_output=True, text=True, timeout=180, cwd="/tmp",
+                           env=dict(os.environ, TMPDIR="/tmp"))
+            files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+            rows = [r for f in files for r in csv.DictReader(open(f))]
+        except Exception as e:  # reported, never fatal for the GPU number
+            return None, f"{ctr} pass failed: {e}"
+        finally:
+            shutil.rmtree(d, ignore_errors=True)
+        cal = [float(r["Counter_Value"]) for r in rows
+               if r["Kernel_Name"].startswith("__amd_rocclr_copyBuffer") and float(r["Counter_Value"]) > 1e5]
+        vals = [float(r["Counter_Value"]) for r in rows if r["Kernel_Name"].split("(")[0].strip() == kernel]
+        if not cal or not vals:
+            return None, f"{ctr} pass: no calibration copies or no {kernel} dispatches in the counters"
+        factor = (sum(cal) / len(cal)) / 262144.0          # counter KiB per KiB copied
+        per = sum(vals) / len(vals) * 1024.0 / factor
+        total += per
+        parts.append(f"{ctr} {per / 1e6:.1f} MB (x{1 / factor:.3f}, {len(vals)} dispatches)")
+    return total, "measured in this run: " + "; ".join(parts)
 
 
 def timed(ncmhip, fn, reps, warm=1):
@@ -464,9 +543,16 @@ def main():
     ap.add_argument("--qwen-steps", type=int, default=256,
                     help="decode steps of config 4 (256; fewer only to keep profiler runs short)")
     ap.add_argument("--cpu-baseline-child", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the two rocprofv3 counter passes that measure roofline.traffic")
+    ap.add_argument("--traffic-child", default=None, help=argparse.SUPPRESS)
+    ap.add_argument("--traffic-reps", type=int, default=TRAFFIC_REPS, help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.cpu_baseline_child:
         cpu_baseline_child()
+        return
+    if args.traffic_child is not None:
+        traffic_child(args.traffic_child.split(";"), args.traffic_reps)
         return
     global QWEN_STEPS
     QWEN_STEPS = max(2, args.qwen_steps)
@@ -535,6 +621,12 @@ def main():
     dom = max((k for k in solo if solo[k][1] > 0), key=lambda k: solo[k][0])
     dms, dfl, dn, dlabels = solo[dom]
     achieved = dfl / (dms / 1e3) / 1e12
+    # the same kernel over every call whose main launch it is (split calls
+    # include their fixup launch in the event bracket)
+    top = max((k for k in per_kernel if per_kernel[k][1] > 0), key=lambda k: per_kernel[k][0])
+    tms, tfl, tn = per_kernel[top]
+    traffic, traffic_note = (None, "skipped (--no-traffic)") if args.no_traffic else \
+        measure_traffic(dom, sorted(dlabels))
 
     result = {
         "metric": METRIC,
@@ -558,7 +650,12 @@ def main():
                      "peak": PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_TFLOPS, 4),
                      "avg_launch_us": round(dms / dn * 1e3, 3), "launches_per_step": dn // args.steps,
                      "launches": sorted(dlabels),
-                     "traffic": TRAFFIC.get((dom, tuple(sorted(dlabels))))},
+                     "traffic": None if traffic is None else round(traffic), "traffic_note": traffic_note,
+                     "traffic_over_algorithmic": None if traffic is None else
+                     round(traffic / algo_bytes(dlabels), 3),
+                     "all_launches": {"kernel": top, "achieved": round(tfl / (tms / 1e3) / 1e12, 3),
+                                      "frac": round(tfl / (tms / 1e3) / 1e12 / PEAK_TFLOPS, 4),
+                                      "calls_per_step": tn // args.steps}},
         "kernels": {k: {"ms_per_step": round(v[0] / args.steps, 4),
                         "tflops": round(v[1] / (v[0] / 1e3) / 1e12, 3) if v[1] else None}
                     for k, v in sorted(per_kernel.items(), key=lambda kv: -kv[1][0])},

@@ -557,7 +557,6 @@ struct DecGemvArgs {
     int ld;
 };
 
-#define DEC_KMAX 8192
 
 // row (in the concatenated row space) of the i-th dot product of this wave
 __device__ __forceinline__ void dec_rows(const DecGemvArgs &p, int unit, int i, int &m, int &row) {
@@ -583,7 +582,9 @@ __device__ __forceinline__ void dec_rows(const DecGemvArgs &p, int unit, int i, 
 template <int RW, int PRE, int DOTS, int XPT>
 __device__ __forceinline__ void dec_gemv_body(const DecGemvArgs &p) {
 #pragma clang fp contract(off)
-    __shared__ __attribute__((aligned(16))) float xs[DEC_KMAX];
+    // the staged input: K <= 1024 XPT floats (LDS sized to it, so that short
+    // rows do not reserve the 32 KB of the longest)
+    __shared__ __attribute__((aligned(16))) float xs[1024 * XPT];
     __shared__ double red[4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int K = p.K, K4 = K >> 2;

@@ -275,8 +275,7 @@ static int dec_launch(DecGemvArgs *a) {
             k = a->K <= 5120 ? "dec_gemv_d1_r1_p20_x5" : "dec_gemv_d1_r1_p8_x8";
         }
     } else if (a->K <= 1024) {
-        if (units >= 4096) { k = "dec_gemv_d2_r2_p4_x1"; rw = 2; }
-        else k = "dec_gemv_d2_r1_p4_x1";
+        k = "dec_gemv_d2_r1_p4_x1";
     } else {
         k = "dec_gemv_d2_r1_p8_x8";
     }

@@ -32,6 +32,7 @@ void argmax_rows(const float *x, int *idx, int64_t rows, int n) {
 }
 
 static unsigned grid_of(int64_t n, int per_block) { return (unsigned)((n + per_block - 1) / per_block); }
+static int aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 static int ops_ready(const char *fn, int64_t n, int nptr, const void *p0, const void *p1) {
     if (n < 0) return ncm_fail(NCM_E_ARG, "%s: negative size", fn);
@@ -69,6 +70,12 @@ void layernorm_eps_fwd(const float *x, const float *w, const float *b, float *y,
 static void eltwise(const char *fn, const float *a, const float *b, float *y, float s, int64_t n, int op) {
     if (ops_ready(fn, n, 2, a, y)) return;
     if ((op == 0 || op == 1) && !b) { ncm_fail(NCM_E_ARG, "%s: null operand", fn); return; }
+    if (n % 4 == 0 && aligned16(a) && aligned16(y) && (!b || aligned16(b))) {
+        int64_t n4 = n / 4;
+        void *args[] = {&a, &b, &y, &s, &n4, &op};
+        ncm_launch_named("eltwise4_k", grid_of(n4, 256), 1, 1, 256, args);
+        return;
+    }
     void *args[] = {&a, &b, &y, &s, &n, &op};
     ncm_launch_named("eltwise_k", grid_of(n, 256), 1, 1, 256, args);
 }

@@ -187,21 +187,40 @@ embedding_k(const float *__restrict__ W, const int *__restrict__ idx, float *__r
 // ---------------------------------------------------------------- elementwise
 // op: 0 add (a+b), 1 mul (a*b), 2 scale (a*s), 3 add_inplace (y += a),
 //     4 silu, 5 gelu, 6 gelu_tanh   (kernels.c:167-226, 829-874)
+__device__ __forceinline__ float elt_op(float v, float w, float yv, float s, int op) {
+#pragma clang fp contract(off)
+    switch (op) {
+    case 0: return v + w;
+    case 1: return v * w;
+    case 2: return v * s;
+    case 3: return yv + v;
+    case 4: return ncm_act(v, ACT_SILU);
+    case 5: return ncm_act(v, ACT_GELU);
+    default: return ncm_act(v, ACT_GELU_TANH);
+    }
+}
+
 extern "C" __global__ void __launch_bounds__(256)
 eltwise_k(const float *a, const float *b, float *y, float s, int64_t n, int op) {
-#pragma clang fp contract(off)
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
-    const float v = a[i];
-    switch (op) {
-    case 0: y[i] = v + b[i]; break;
-    case 1: y[i] = v * b[i]; break;
-    case 2: y[i] = v * s; break;
-    case 3: y[i] = y[i] + v; break;
-    case 4: y[i] = ncm_act(v, ACT_SILU); break;
-    case 5: y[i] = ncm_act(v, ACT_GELU); break;
-    default: y[i] = ncm_act(v, ACT_GELU_TANH); break;
-    }
+    y[i] = elt_op(a[i], (op == 0 || op == 1) ? b[i] : 0.f, op == 3 ? y[i] : 0.f, s, op);
+}
+
+// The same on float4 groups (n4 = n / 4, 16-byte aligned operands): each
+// element gets the scalar kernel's float operations; a, b and y may alias
+// (each element is read before it is written, by the same thread).
+extern "C" __global__ void __launch_bounds__(256)
+eltwise4_k(const float *a, const float *b, float *y, float s, int64_t n4, int op) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;
+    const f4 v = ((const f4 *)a)[i];
+    const f4 w = (op == 0 || op == 1) ? ((const f4 *)b)[i] : f4{0.f, 0.f, 0.f, 0.f};
+    const f4 yv = op == 3 ? ((const f4 *)y)[i] : f4{0.f, 0.f, 0.f, 0.f};
+    f4 r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = elt_op(v[e], w[e], yv[e], s, op);
+    ((f4 *)y)[i] = r;
 }
 
 // ---------------------------------------------------------------- SDPA
@@ -222,7 +241,7 @@ eltwise_k(const float *a, const float *b, float *y, float s, int64_t n, int op) 
 #define SD_T 64
 #define SD_LD (64 + 8)
 
-extern "C" __global__ void __launch_bounds__(256)
+extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4)))
 sdpa_hd64(const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
           const float *__restrict__ mask, float *__restrict__ out, int Hq, int Hkv, int Tq, int Tkv,
           float scale, int causal, int merged, float *__restrict__ stats) {
@@ -253,35 +272,25 @@ sdpa_hd64(const float *__restrict__ q, const float *__restrict__ k, const float 
     const int coff = Tkv - Tq;   // causal offset of the query positions
     int kend = Tkv;
     if (causal) kend = min(Tkv, q0 + 64 + coff);
-    // K and V tiles (64 keys x 64 d, rows beyond Tkv as zero): the next tile
-    // is loaded into registers while the current one is used from LDS
-    f4 pk[4], pv[4];
-    auto load_tile = [&](int k0) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int f = tid + j * 256;
-            const int r = f >> 4, c = (f & 15) * 4;
-            const int key = k0 + r;
-            pk[j] = f4{0.f, 0.f, 0.f, 0.f};
-            pv[j] = f4{0.f, 0.f, 0.f, 0.f};
-            if (key < Tkv) {
-                pk[j] = *(const f4 *)(kb + (int64_t)key * 64 + c);
-                pv[j] = *(const f4 *)(vb + (int64_t)key * 64 + c);
-            }
-        }
-    };
-    if (kend > 0) load_tile(0);
+    // K and V tiles (64 keys x 64 d, rows beyond Tkv as zero), staged through
+    // LDS; no register prefetch of the next tile, so the kernel stays under
+    // 128 registers and four workgroups share a CU
     for (int k0 = 0; k0 < kend; k0 += SD_T) {
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int f = tid + j * 256;
             const int r = f >> 4, c = (f & 15) * 4;
-            *(f4 *)(sK + r * SD_LD + c) = pk[j];
-            *(f4 *)(sV + r * SD_LD + c) = pv[j];
+            const int key = k0 + r;
+            f4 kk = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
+            if (key < Tkv) {
+                kk = *(const f4 *)(kb + (int64_t)key * 64 + c);
+                vv = *(const f4 *)(vb + (int64_t)key * 64 + c);
+            }
+            *(f4 *)(sK + r * SD_LD + c) = kk;
+            *(f4 *)(sV + r * SD_LD + c) = vv;
         }
         __syncthreads();
-        if (k0 + SD_T < kend) load_tile(k0 + SD_T);
 
         // S^T[c]: keys k0 + 16c + 4lg + r, query my_q
         f4 s[4];

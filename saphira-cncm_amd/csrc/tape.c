@@ -29,7 +29,26 @@ typedef struct {
     size_t *size;
     int n, cap, cur;
     size_t off;
+    /* zeroing pools (the gradient pool): per chunk, the extent cleared since
+     * the last reset and the largest extent used by an earlier cycle.  The
+     * first allocation in a chunk clears that earlier extent with one memset,
+     * so a step's gradient buffers cost one clear per chunk, not one each. */
+    int zeroing;
+    size_t *zeroed, *high;
 } Pool;
+
+/* Zeroing pools: makes [0, p->off) of the current chunk zero.  This
+ * cycle's allocations are contiguous from 0 and [0, zeroed) was cleared after
+ * the last reset and, past p->off before this allocation, not handed out
+ * since, so clearing [zeroed, max(off, high)) suffices. */
+static int pool_zero(Pool *p) {
+    const int c = p->cur;
+    if (p->off <= p->zeroed[c]) return 0;
+    const size_t to = p->off > p->high[c] ? p->off : p->high[c];
+    if (ncm_zero_async(p->chunk[c] + p->zeroed[c], to - p->zeroed[c])) return -1;
+    p->zeroed[c] = to;
+    return 0;
+}
 
 static void *pool_alloc(Pool *p, size_t bytes) {
     bytes = (bytes + 255) & ~(size_t)255;
@@ -38,6 +57,7 @@ static void *pool_alloc(Pool *p, size_t bytes) {
         if (p->off + bytes <= p->size[p->cur]) {
             void *r = p->chunk[p->cur] + p->off;
             p->off += bytes;
+            if (p->zeroing && pool_zero(p)) return NULL;
             return r;
         }
         p->cur++;
@@ -51,6 +71,12 @@ static void *pool_alloc(Pool *p, size_t bytes) {
         size_t *s = (size_t *)realloc(p->size, (size_t)cap * sizeof(size_t));
         if (!s) return NULL;
         p->size = s;
+        size_t *z = (size_t *)realloc(p->zeroed, (size_t)cap * sizeof(size_t));
+        if (!z) return NULL;
+        p->zeroed = z;
+        size_t *h = (size_t *)realloc(p->high, (size_t)cap * sizeof(size_t));
+        if (!h) return NULL;
+        p->high = h;
         p->cap = cap;
     }
     size_t sz = bytes > POOL_CHUNK ? bytes : POOL_CHUNK;
@@ -58,12 +84,19 @@ static void *pool_alloc(Pool *p, size_t bytes) {
     if (!m) return NULL;
     p->chunk[p->n] = (char *)m;
     p->size[p->n] = sz;
+    p->zeroed[p->n] = 0;
+    p->high[p->n] = 0;
     p->cur = p->n++;
     p->off = bytes;
+    if (p->zeroing && pool_zero(p)) return NULL;
     return m;
 }
 
 static void pool_reset(Pool *p) {
+    for (int i = 0; i < p->n; i++) {
+        if (p->zeroed[i] > p->high[i]) p->high[i] = p->zeroed[i];
+        p->zeroed[i] = 0;
+    }
     p->cur = 0;
     p->off = 0;
 }
@@ -72,6 +105,8 @@ static void pool_free(Pool *p) {
     for (int i = 0; i < p->n; i++) ncm_hip_free(p->chunk[i]);
     free(p->chunk);
     free(p->size);
+    free(p->zeroed);
+    free(p->high);
     memset(p, 0, sizeof(*p));
 }
 
@@ -106,7 +141,11 @@ struct NcmTape {
     int gn, gcap;
 };
 
-NcmTape *ncm_tape_new(void) { return (NcmTape *)calloc(1, sizeof(NcmTape)); }
+NcmTape *ncm_tape_new(void) {
+    NcmTape *t = (NcmTape *)calloc(1, sizeof(NcmTape));
+    if (t) t->grad.zeroing = 1;   /* gradient buffers start at zero */
+    return t;
+}
 
 static void free_recs(NcmTape *t) {
     for (int i = 0; i < t->n; i++) free(t->r[i].ids);
@@ -178,12 +217,12 @@ static float *gmap_get(NcmTape *t, const float *key, int64_t n) {
     if (!key) return NULL;
     float *g = gmap_find(t, key);
     if (g) return g;
-    g = (float *)pool_alloc(&t->grad, (size_t)n * sizeof(float));
+    g = (float *)pool_alloc(&t->grad, (size_t)n * sizeof(float));   /* zeroed by the pool */
     if (!g) {
         ncm_fail(NCM_E_OOM, "tape: gradient buffer of %lld floats", (long long)n);
         return NULL;
     }
-    if (ncm_zero_async(g, (size_t)n * sizeof(float)) || gmap_put(t, key, g)) return NULL;
+    if (gmap_put(t, key, g)) return NULL;
     return g;
 }
 

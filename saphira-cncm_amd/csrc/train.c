@@ -377,6 +377,12 @@ static int elt_check(const char *fn, int64_t n, const void *a, const void *b) {
 
 static void act_bwd(const char *fn, const float *x, const float *dy, float *dx, int64_t n, int kind) {
     if (elt_check(fn, n, x, dy) || !dx) return;
+    if (n % 4 == 0 && (((uintptr_t)x | (uintptr_t)dy | (uintptr_t)dx) & 15) == 0) {
+        int64_t n4 = n / 4;
+        void *a[] = {&x, &dy, &dx, &n4, &kind};
+        ncm_launch_named("act_bwd4_k", blocks_of(n4, 256), 1, 1, 256, a);
+        return;
+    }
     void *a[] = {&x, &dy, &dx, &n, &kind};
     ncm_launch_named("act_bwd_k", blocks_of(n, 256), 1, 1, 256, a);
 }

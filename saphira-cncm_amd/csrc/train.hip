@@ -767,15 +767,11 @@ sdpa_probs_rows(const float *__restrict__ q, const float *__restrict__ k, const 
     }
 }
 
-// ---------------------------------------------------------------- elementwise backward
-// train_tape.c:830-873: dx += (float)(dy * g(x)), g in fp64.
-// kind 0 gelu (erf), 1 silu, 2 gelu_tanh (gelu_new).
-extern "C" __global__ void __launch_bounds__(256)
-act_bwd_k(const float *__restrict__ x, const float *__restrict__ dy, float *__restrict__ dx, int64_t n, int kind) {
+// dy * act'(x) in fp64, rounded to float (the reference's activation
+// backward): kind 0 GELU (erf), 1 SiLU, 2 GELU (tanh form)
+__device__ __forceinline__ float act_bwd_one(float xf, float dyf, int kind) {
 #pragma clang fp contract(off)
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= n) return;
-    const double xv = (double)x[i];
+    const double xv = (double)xf;
     double g;
     if (kind == 0) {
         const double e = erf(xv / 1.4142135623730951);
@@ -785,10 +781,33 @@ act_bwd_k(const float *__restrict__ x, const float *__restrict__ dy, float *__re
         g = s * (1 + xv * (1 - s));
     } else {
         const double c0 = 0.7978845608028654, c1 = 0.044715;
-        const double th = tanh(c0 * (xv + c1 * xv * xv * xv));
+        const double th = ncm_tanh_d(c0 * (xv + c1 * xv * xv * xv));
         g = 0.5 * (1.0 + th) + 0.5 * xv * (1.0 - th * th) * c0 * (1.0 + 3.0 * c1 * xv * xv);
     }
-    dx[i] += (float)((double)dy[i] * g);
+    return (float)((double)dyf * g);
+}
+
+// ---------------------------------------------------------------- elementwise backward
+// train_tape.c:830-873: dx += (float)(dy * g(x)), g in fp64.
+// kind 0 gelu (erf), 1 silu, 2 gelu_tanh (gelu_new).
+extern "C" __global__ void __launch_bounds__(256)
+act_bwd_k(const float *__restrict__ x, const float *__restrict__ dy, float *__restrict__ dx, int64_t n, int kind) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    dx[i] += act_bwd_one(x[i], dy[i], kind);
+}
+
+// The same on float4 groups (n4 = n / 4, 16-byte aligned): four independent
+// fp64 evaluations per thread.
+extern "C" __global__ void __launch_bounds__(256)
+act_bwd4_k(const float *__restrict__ x, const float *__restrict__ dy, float *__restrict__ dx, int64_t n4, int kind) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;
+    const f4 xv = ((const f4 *)x)[i], g = ((const f4 *)dy)[i];
+    f4 d = ((const f4 *)dx)[i];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) d[e] += act_bwd_one(xv[e], g[e], kind);
+    ((f4 *)dx)[i] = d;
 }
 
 // train_tape.c:1254-1268: da += dy*b, db += dy*a (float products)
@@ -921,9 +940,11 @@ sdpa_bwd_rowdot(const float *__restrict__ dO, const float *__restrict__ O, float
 // dq: 64 queries of one (b, h) per workgroup, wave w the queries q0 + 16w + li.
 // Per key tile: S^T = K Q^T and dP^T = V dO^T in the layout (key 16c + 4g + r,
 // query li), P and dS^T = P^T o (dP^T - D) in place, dq += dS K with dS^T as the
-// A operand (as sdpa_bwd_dq_hd64's second sweep).  Causal: key tiles past the
-// tile's last query are skipped (their P is exactly 0).
-extern "C" __global__ void __launch_bounds__(256)
+// A operand (as sdpa_bwd_dq_hd64's second sweep), one block of 16 keys at a
+// time.  Causal: key tiles past the tile's last query are skipped (their P is
+// exactly 0).  Under 128 registers (no prefetch of the next tile): four
+// workgroups share a CU.
+extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4)))
 sdpa_fbwd_dq_hd64(const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
                   const float *__restrict__ mask, const float *__restrict__ stats, const float *__restrict__ D,
                   const float *__restrict__ dO, float *__restrict__ dq, int H, int Hkv, int Tq, int Tkv, float scale,
@@ -957,69 +978,52 @@ sdpa_fbwd_dq_hd64(const float *__restrict__ q, const float *__restrict__ k, cons
     const int coff = Tkv - Tq;
     int kend = Tkv;
     if (causal) kend = min(Tkv, q0 + 64 + coff);
-    // the next tile's K and V rows are loaded into registers while the
-    // current tile is computed from LDS
-    f4 pk[4], pv[4];
-    auto load_tile = [&](int k0) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int f = tid + j * 256;
-            const int r = f >> 4, c = (f & 15) * 4;
-            const int key = k0 + r;
-            pv[j] = f4{0.f, 0.f, 0.f, 0.f};
-            pk[j] = f4{0.f, 0.f, 0.f, 0.f};
-            if (key < Tkv) {
-                pv[j] = *(const f4 *)(vb + (int64_t)key * 64 + c);
-                pk[j] = *(const f4 *)(kb + (int64_t)key * 64 + c);
-            }
-        }
-    };
-    if (kend > 0) load_tile(0);
     for (int k0 = 0; k0 < kend; k0 += 64) {
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int f = tid + j * 256;
             const int r = f >> 4, c = (f & 15) * 4;
-            *(f4 *)(sV + r * SB_LD + c) = pv[j];
-            *(f4 *)(sK + r * SB_LD + c) = pk[j];
+            const int key = k0 + r;
+            f4 vv = {0.f, 0.f, 0.f, 0.f}, kk = {0.f, 0.f, 0.f, 0.f};
+            if (key < Tkv) {
+                vv = *(const f4 *)(vb + (int64_t)key * 64 + c);
+                kk = *(const f4 *)(kb + (int64_t)key * 64 + c);
+            }
+            *(f4 *)(sV + r * SB_LD + c) = vv;
+            *(f4 *)(sK + r * SB_LD + c) = kk;
         }
         __syncthreads();
-        if (k0 + 64 < kend) load_tile(k0 + 64);
-        f4 s[4], dp[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            s[c] = f4{0.f, 0.f, 0.f, 0.f};
-            dp[c] = f4{0.f, 0.f, 0.f, 0.f};
+            f4 s = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kc = 0; kc < 4; ++kc) {
                 const f4 kf = *(const f4 *)(sK + (16 * c + li) * SB_LD + kc * 16 + 4 * lg);
                 const f4 vf = *(const f4 *)(sV + (16 * c + li) * SB_LD + kc * 16 + 4 * lg);
 #pragma unroll
                 for (int st = 0; st < 4; ++st) {
-                    s[c] = mfma4(kf[st], qf[kc][st], s[c]);
-                    dp[c] = mfma4(vf[st], gf[kc][st], dp[c]);
+                    s = mfma4(kf[st], qf[kc][st], s);
+                    dp = mfma4(vf[st], gf[kc][st], dp);
                 }
             }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int key = k0 + 16 * c + 4 * lg + r;
-                float x = s[c][r] * scale;
+                float x = s[r] * scale;
                 if (mask && key < Tkv && qok) x += mask[(int64_t)my_q * Tkv + key];
                 if (key >= Tkv || (causal && key > my_q + coff)) x = -INFINITY;
                 const float p = qok ? __expf(x - mq) * il : 0.f;
-                dp[c][r] = p * (dp[c][r] - dq_d);
+                dp[r] = p * (dp[r] - dq_d);
             }
-        }
-        // dq[query qw + 4g + r][d = 4li + u] += dS[query][key] K[key][d]
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
+            // dq[query qw + 4g + r][d = 4li + u] += dS[query][key] K[key][d] over this block's keys
 #pragma unroll
             for (int st = 0; st < 4; ++st) {
                 const f4 kf = *(const f4 *)(sK + (16 * c + 4 * lg + st) * SB_LD + 4 * li);
 #pragma unroll
-                for (int u = 0; u < 4; ++u) acc[u] = mfma4(dp[c][st], kf[u], acc[u]);
+                for (int u = 0; u < 4; ++u) acc[u] = mfma4(dp[st], kf[u], acc[u]);
             }
+        }
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -1037,11 +1041,14 @@ sdpa_fbwd_dq_hd64(const float *__restrict__ q, const float *__restrict__ k, cons
 }
 
 // dk / dv: 64 keys of one (b, kv head) per workgroup, wave w the keys
-// k0 + 16w + li.  For every query head of the group and query tile: S = Q K^T
-// and dP = dO V^T in the layout (query 16c + 4g + r, key li), P and dS in
-// registers (no transposed copy of P), dV += P^T dO, dK += dS^T Q.  Causal:
-// query tiles before the first query that sees this key tile are skipped.
-extern "C" __global__ void __launch_bounds__(256)
+// k0 + 16w + li.  For every query head of the group and query tile, per block
+// of 16 queries c: S = Q K^T and dP = dO V^T in the layout (query 16c + 4g +
+// r, key li), P and dS in registers (no transposed copy of P), then at once
+// dV += P^T dO and dK += dS^T Q for that block, so only one block's P and dS
+// are live.  Causal: query tiles before the first query that sees this key
+// tile are skipped.  No register prefetch of the next tile: the registers
+// stay under 128, so four workgroups share a CU and hide each other's loads.
+extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4)))
 sdpa_fbwd_dkdv_hd64(const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
                     const float *__restrict__ mask, const float *__restrict__ stats, const float *__restrict__ D,
                     const float *__restrict__ dO, float *__restrict__ dk, float *__restrict__ dv, int H, int Hkv,
@@ -1079,96 +1086,71 @@ sdpa_fbwd_dkdv_hd64(const float *__restrict__ q, const float *__restrict__ k, co
         const int first = k0 - coff;
         qstart = first > 0 ? (first / 64) * 64 : 0;
     }
-    // the (query head, query tile) pairs in order; the next pair's dO and Q
-    // rows and row statistics are loaded into registers while the current one
-    // is computed from LDS
+    // the (query head, query tile) pairs in order
     const int nq = qstart < Tq ? (Tq - qstart + 63) / 64 : 0, niter = rep * nq;
-    f4 pg[4], pq[4];
-    float pm = 0.f, pl = 0.f, pd = 0.f;
-    auto load_tile = [&](int it) {
+    for (int it = 0; it < niter; ++it) {
         const int h = kvh * rep + it / nq, q0 = qstart + (it % nq) * 64;
         const int64_t rbase = ((int64_t)b * H + h) * Tq;
+        __syncthreads();
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int f = tid + j * 256;
             const int r = f >> 4, c = (f & 15) * 4;
             const int qi = q0 + r;
-            pg[j] = f4{0.f, 0.f, 0.f, 0.f};
-            pq[j] = f4{0.f, 0.f, 0.f, 0.f};
+            f4 g = {0.f, 0.f, 0.f, 0.f}, qq = {0.f, 0.f, 0.f, 0.f};
             if (qi < Tq) {
-                pg[j] = *(const f4 *)(dO + (rbase + qi) * 64 + c);
-                pq[j] = *(const f4 *)(q + (rbase + qi) * 64 + c);
+                g = *(const f4 *)(dO + (rbase + qi) * 64 + c);
+                qq = *(const f4 *)(q + (rbase + qi) * 64 + c);
             }
+            *(f4 *)(sG + r * SB_LD + c) = g;
+            *(f4 *)(sQ + r * SB_LD + c) = qq;
         }
         if (tid < 64) {
             const int qi = q0 + tid;
             const bool ok = qi < Tq;
-            pm = ok ? stats[(rbase + qi) * 2] : 0.f;
-            pl = ok ? 1.0f / stats[(rbase + qi) * 2 + 1] : 0.f;
-            pd = ok ? D[rbase + qi] : 0.f;
+            sM[tid] = ok ? stats[(rbase + qi) * 2] : 0.f;
+            sL[tid] = ok ? 1.0f / stats[(rbase + qi) * 2 + 1] : 0.f;
+            sD[tid] = ok ? D[rbase + qi] : 0.f;
         }
-    };
-    if (niter > 0) load_tile(0);
-    for (int it = 0; it < niter; ++it) {
-        const int q0 = qstart + (it % nq) * 64;
-        {
-            __syncthreads();
+        __syncthreads();
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int f = tid + j * 256;
-                const int r = f >> 4, c = (f & 15) * 4;
-                *(f4 *)(sG + r * SB_LD + c) = pg[j];
-                *(f4 *)(sQ + r * SB_LD + c) = pq[j];
-            }
-            if (tid < 64) {
-                sM[tid] = pm;
-                sL[tid] = pl;
-                sD[tid] = pd;
-            }
-            __syncthreads();
-            if (it + 1 < niter) load_tile(it + 1);
-            f4 dp[4], pf[4];
+        for (int c = 0; c < 4; ++c) {
+            f4 dp = {0.f, 0.f, 0.f, 0.f}, s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                dp[c] = f4{0.f, 0.f, 0.f, 0.f};
-                f4 s = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int kc = 0; kc < 4; ++kc) {
-                    const f4 gfr = *(const f4 *)(sG + (16 * c + li) * SB_LD + kc * 16 + 4 * lg);
-                    const f4 qfr = *(const f4 *)(sQ + (16 * c + li) * SB_LD + kc * 16 + 4 * lg);
-#pragma unroll
-                    for (int st = 0; st < 4; ++st) {
-                        dp[c] = mfma4(gfr[st], vf[kc][st], dp[c]);
-                        s = mfma4(qfr[st], kf[kc][st], s);
-                    }
-                }
-                const f4 mm = *(const f4 *)(sM + 16 * c + 4 * lg);
-                const f4 ll = *(const f4 *)(sL + 16 * c + 4 * lg);
-                const f4 dd = *(const f4 *)(sD + 16 * c + 4 * lg);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int qi = q0 + 16 * c + 4 * lg + r;
-                    float x = s[r] * scale;
-                    if (mask && qi < Tq && kok) x += mask[(int64_t)qi * Tkv + my_k];
-                    if (!kok || (causal && my_k > qi + coff)) x = -INFINITY;
-                    const float p = qi < Tq ? __expf(x - mm[r]) * ll[r] : 0.f;
-                    pf[c][r] = p;
-                    dp[c][r] = p * (dp[c][r] - dd[r]);
-                }
-            }
-            // dV += P^T dO, dK += dS^T Q
-#pragma unroll
-            for (int c = 0; c < 4; ++c)
+            for (int kc = 0; kc < 4; ++kc) {
+                const f4 gfr = *(const f4 *)(sG + (16 * c + li) * SB_LD + kc * 16 + 4 * lg);
+                const f4 qfr = *(const f4 *)(sQ + (16 * c + li) * SB_LD + kc * 16 + 4 * lg);
 #pragma unroll
                 for (int st = 0; st < 4; ++st) {
-                    const f4 gfr = *(const f4 *)(sG + (16 * c + 4 * lg + st) * SB_LD + 4 * li);
-                    const f4 qfr = *(const f4 *)(sQ + (16 * c + 4 * lg + st) * SB_LD + 4 * li);
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) {
-                        av[u] = mfma4(pf[c][st], gfr[u], av[u]);
-                        ak[u] = mfma4(dp[c][st], qfr[u], ak[u]);
-                    }
+                    dp = mfma4(gfr[st], vf[kc][st], dp);
+                    s = mfma4(qfr[st], kf[kc][st], s);
                 }
+            }
+            const f4 mm = *(const f4 *)(sM + 16 * c + 4 * lg);
+            const f4 ll = *(const f4 *)(sL + 16 * c + 4 * lg);
+            const f4 dd = *(const f4 *)(sD + 16 * c + 4 * lg);
+            f4 pf;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int qi = q0 + 16 * c + 4 * lg + r;
+                float x = s[r] * scale;
+                if (mask && qi < Tq && kok) x += mask[(int64_t)qi * Tkv + my_k];
+                if (!kok || (causal && my_k > qi + coff)) x = -INFINITY;
+                const float p = qi < Tq ? __expf(x - mm[r]) * ll[r] : 0.f;
+                pf[r] = p;
+                dp[r] = p * (dp[r] - dd[r]);
+            }
+            // dV += P^T dO, dK += dS^T Q over this block's 16 queries
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const f4 gfr = *(const f4 *)(sG + (16 * c + 4 * lg + st) * SB_LD + 4 * li);
+                const f4 qfr = *(const f4 *)(sQ + (16 * c + 4 * lg + st) * SB_LD + 4 * li);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    av[u] = mfma4(pf[st], gfr[u], av[u]);
+                    ak[u] = mfma4(dp[st], qfr[u], ak[u]);
+                }
+            }
         }
     }
 #pragma unroll

@@ -51,6 +51,16 @@ __device__ __forceinline__ double wave_sum_d(double v) {
     return v;
 }
 
+// Column swizzle of the SDPA kernels' 64 x 64 LDS tiles (row pitch 72
+// floats): float column c of row r is stored at c ^ 16 when bits 2 and 3 of r
+// differ.  Both fragment reads of those kernels -- lane (li, g) reading row
+// 16c + li at columns 16kc + 4g, and reading row 16c + 4g + s at columns 4li
+// -- then touch 64 distinct banks in every group of 16 lanes that
+// ds_read_b128 serves per cycle on gfx950 ({0-3, 12-15, 20-23, 24-27},
+// {4-7, 8-11, 16-19, 28-31} and the same + 32); unswizzled, the second read
+// was 2-way conflicted.
+#define LDS_SWZ(r, c) ((c) ^ (((((r) >> 2) ^ ((r) >> 3)) & 1) << 4))
+
 // One 16x16x4 fp32 MFMA: lane l supplies A[l%16][l/16] and B[l/16][l%16];
 // the result holds D[4*(l/16)+r][l%16] in component r.
 __device__ __forceinline__ f4 mfma4(float a, float b, f4 c) {

@@ -277,18 +277,24 @@ sdpa_hd64(const float *__restrict__ q, const float *__restrict__ k, const float 
     // 128 registers and four workgroups share a CU
     for (int k0 = 0; k0 < kend; k0 += SD_T) {
         __syncthreads();
+        // all eight loads in flight at once (keys past Tkv read key Tkv - 1 and
+        // are stored as zero), then the LDS stores.  Thread tid stages rows
+        // tid / 16 + 16 j, columns 4 (tid % 16): the swizzle depends on bits 2
+        // and 3 of the row only, so one LDS offset serves all four rows.
+        f4 kk[4], vv[4];
+        const int r0 = tid >> 4, c0 = (tid & 15) * 4;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int f = tid + j * 256;
-            const int r = f >> 4, c = (f & 15) * 4;
-            const int key = k0 + r;
-            f4 kk = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
-            if (key < Tkv) {
-                kk = *(const f4 *)(kb + (int64_t)key * 64 + c);
-                vv = *(const f4 *)(vb + (int64_t)key * 64 + c);
-            }
-            *(f4 *)(sK + r * SD_LD + c) = kk;
-            *(f4 *)(sV + r * SD_LD + c) = vv;
+            const int64_t key = min(k0 + r0 + 16 * j, Tkv - 1);
+            kk[j] = *(const f4 *)(kb + key * 64 + c0);
+            vv[j] = *(const f4 *)(vb + key * 64 + c0);
+        }
+        const int so = r0 * SD_LD + LDS_SWZ(r0, c0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const bool ok = k0 + r0 + 16 * j < Tkv;
+            *(f4 *)(sK + so + 16 * j * SD_LD) = ok ? kk[j] : f4{0.f, 0.f, 0.f, 0.f};
+            *(f4 *)(sV + so + 16 * j * SD_LD) = ok ? vv[j] : f4{0.f, 0.f, 0.f, 0.f};
         }
         __syncthreads();
 
@@ -299,7 +305,7 @@ sdpa_hd64(const float *__restrict__ q, const float *__restrict__ k, const float 
             s[c] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kc = 0; kc < 4; ++kc) {
-                const f4 kf = *(const f4 *)(sK + (16 * c + li) * SD_LD + kc * 16 + 4 * lg);
+                const f4 kf = *(const f4 *)(sK + (16 * c + li) * SD_LD + LDS_SWZ((16 * c + li), kc * 16 + 4 * lg));
 #pragma unroll
                 for (int st = 0; st < 4; ++st) s[c] = mfma4(kf[st], qf[kc][st], s[c]);
             }
@@ -347,7 +353,7 @@ sdpa_hd64(const float *__restrict__ q, const float *__restrict__ k, const float 
         for (int c = 0; c < 4; ++c)
 #pragma unroll
             for (int st = 0; st < 4; ++st) {
-                const f4 vf = *(const f4 *)(sV + (16 * c + 4 * lg + st) * SD_LD + 4 * li);
+                const f4 vf = *(const f4 *)(sV + (16 * c + 4 * lg + st) * SD_LD + LDS_SWZ((16 * c + 4 * lg + st), 4 * li));
 #pragma unroll
                 for (int u = 0; u < 4; ++u) o[u] = mfma4(s[c][st], vf[u], o[u]);
             }

@@ -438,8 +438,8 @@ sdpa_bwd_dq_hd64(const float *__restrict__ k, const float *__restrict__ v, const
                     vv = *(const f4 *)(vb + (int64_t)key * 64 + c);
                     if (sweep) kv = *(const f4 *)(kb + (int64_t)key * 64 + c);
                 }
-                *(f4 *)(sV + r * SB_LD + c) = vv;
-                if (sweep) *(f4 *)(sK + r * SB_LD + c) = kv;
+                *(f4 *)(sV + r * SB_LD + LDS_SWZ(r, c)) = vv;
+                if (sweep) *(f4 *)(sK + r * SB_LD + LDS_SWZ(r, c)) = kv;
             }
             __syncthreads();
             // dP^T[c]: keys k0 + 16c + 4g + r, query my_q
@@ -449,7 +449,7 @@ sdpa_bwd_dq_hd64(const float *__restrict__ k, const float *__restrict__ v, const
                 dp[c] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int kc = 0; kc < 4; ++kc) {
-                    const f4 vf = *(const f4 *)(sV + (16 * c + li) * SB_LD + kc * 16 + 4 * lg);
+                    const f4 vf = *(const f4 *)(sV + (16 * c + li) * SB_LD + LDS_SWZ((16 * c + li), kc * 16 + 4 * lg));
 #pragma unroll
                     for (int st = 0; st < 4; ++st) dp[c] = mfma4(vf[st], gf[kc][st], dp[c]);
                 }
@@ -471,7 +471,7 @@ sdpa_bwd_dq_hd64(const float *__restrict__ k, const float *__restrict__ v, const
                 for (int c = 0; c < 4; ++c)
 #pragma unroll
                     for (int st = 0; st < 4; ++st) {
-                        const f4 kf = *(const f4 *)(sK + (16 * c + 4 * lg + st) * SB_LD + 4 * li);
+                        const f4 kf = *(const f4 *)(sK + (16 * c + 4 * lg + st) * SB_LD + LDS_SWZ((16 * c + 4 * lg + st), 4 * li));
 #pragma unroll
                         for (int u = 0; u < 4; ++u) acc[u] = mfma4(dp[c][st], kf[u], acc[u]);
                     }
@@ -549,8 +549,8 @@ sdpa_bwd_dkdv_hd64(const float *__restrict__ q, const float *__restrict__ v, con
                     gv = *(const f4 *)(dO + (rbase + qi) * 64 + c);
                     qv = *(const f4 *)(q + (rbase + qi) * 64 + c);
                 }
-                *(f4 *)(sG + r * SB_LD + c) = gv;
-                *(f4 *)(sQ + r * SB_LD + c) = qv;
+                *(f4 *)(sG + r * SB_LD + LDS_SWZ(r, c)) = gv;
+                *(f4 *)(sQ + r * SB_LD + LDS_SWZ(r, c)) = qv;
                 // P rows (query r2, keys 4c2 .. +3) stored transposed
                 const int r2 = f & 63, c2 = f >> 6;
                 const int qj = q0 + r2, key = k0 + 4 * c2;
@@ -572,7 +572,7 @@ sdpa_bwd_dkdv_hd64(const float *__restrict__ q, const float *__restrict__ v, con
                 dp[c] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int kc = 0; kc < 4; ++kc) {
-                    const f4 gfr = *(const f4 *)(sG + (16 * c + li) * SB_LD + kc * 16 + 4 * lg);
+                    const f4 gfr = *(const f4 *)(sG + (16 * c + li) * SB_LD + LDS_SWZ((16 * c + li), kc * 16 + 4 * lg));
 #pragma unroll
                     for (int st = 0; st < 4; ++st) dp[c] = mfma4(gfr[st], vf[kc][st], dp[c]);
                 }
@@ -586,8 +586,8 @@ sdpa_bwd_dkdv_hd64(const float *__restrict__ q, const float *__restrict__ v, con
             for (int c = 0; c < 4; ++c)
 #pragma unroll
                 for (int st = 0; st < 4; ++st) {
-                    const f4 gfr = *(const f4 *)(sG + (16 * c + 4 * lg + st) * SB_LD + 4 * li);
-                    const f4 qfr = *(const f4 *)(sQ + (16 * c + 4 * lg + st) * SB_LD + 4 * li);
+                    const f4 gfr = *(const f4 *)(sG + (16 * c + 4 * lg + st) * SB_LD + LDS_SWZ((16 * c + 4 * lg + st), 4 * li));
+                    const f4 qfr = *(const f4 *)(sQ + (16 * c + 4 * lg + st) * SB_LD + LDS_SWZ((16 * c + 4 * lg + st), 4 * li));
 #pragma unroll
                     for (int u = 0; u < 4; ++u) {
                         av[u] = mfma4(pf[c][st], gfr[u], av[u]);
@@ -652,7 +652,7 @@ sdpa_probs_hd64(const float *__restrict__ q, const float *__restrict__ k, const 
                 const int f = tid + j * 256;
                 const int r = f >> 4, c = (f & 15) * 4;
                 const int key = k0 + r;
-                *(f4 *)(sK + r * SB_LD + c) = key < Tkv ? *(const f4 *)(kb + (int64_t)key * 64 + c)
+                *(f4 *)(sK + r * SB_LD + LDS_SWZ(r, c)) = key < Tkv ? *(const f4 *)(kb + (int64_t)key * 64 + c)
                                                         : f4{0.f, 0.f, 0.f, 0.f};
             }
             __syncthreads();
@@ -662,7 +662,7 @@ sdpa_probs_hd64(const float *__restrict__ q, const float *__restrict__ k, const 
                 s[c] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int kc = 0; kc < 4; ++kc) {
-                    const f4 kf = *(const f4 *)(sK + (16 * c + li) * SB_LD + kc * 16 + 4 * lg);
+                    const f4 kf = *(const f4 *)(sK + (16 * c + li) * SB_LD + LDS_SWZ((16 * c + li), kc * 16 + 4 * lg));
 #pragma unroll
                     for (int st = 0; st < 4; ++st) s[c] = mfma4(kf[st], qf[kc][st], s[c]);
                 }
@@ -980,18 +980,23 @@ sdpa_fbwd_dq_hd64(const float *__restrict__ q, const float *__restrict__ k, cons
     if (causal) kend = min(Tkv, q0 + 64 + coff);
     for (int k0 = 0; k0 < kend; k0 += 64) {
         __syncthreads();
+        // all eight loads in flight at once (keys past Tkv read key Tkv - 1 and
+        // are stored as zero), then the LDS stores (one LDS offset for the
+        // thread's four rows, as in the dk / dv kernel)
+        f4 vv[4], kk[4];
+        const int r0 = tid >> 4, c0 = (tid & 15) * 4;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int f = tid + j * 256;
-            const int r = f >> 4, c = (f & 15) * 4;
-            const int key = k0 + r;
-            f4 vv = {0.f, 0.f, 0.f, 0.f}, kk = {0.f, 0.f, 0.f, 0.f};
-            if (key < Tkv) {
-                vv = *(const f4 *)(vb + (int64_t)key * 64 + c);
-                kk = *(const f4 *)(kb + (int64_t)key * 64 + c);
-            }
-            *(f4 *)(sV + r * SB_LD + c) = vv;
-            *(f4 *)(sK + r * SB_LD + c) = kk;
+            const int64_t key = min(k0 + r0 + 16 * j, Tkv - 1);
+            vv[j] = *(const f4 *)(vb + key * 64 + c0);
+            kk[j] = *(const f4 *)(kb + key * 64 + c0);
+        }
+        const int so = r0 * SB_LD + LDS_SWZ(r0, c0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const bool ok = k0 + r0 + 16 * j < Tkv;
+            *(f4 *)(sV + so + 16 * j * SB_LD) = ok ? vv[j] : f4{0.f, 0.f, 0.f, 0.f};
+            *(f4 *)(sK + so + 16 * j * SB_LD) = ok ? kk[j] : f4{0.f, 0.f, 0.f, 0.f};
         }
         __syncthreads();
 #pragma unroll
@@ -999,8 +1004,8 @@ sdpa_fbwd_dq_hd64(const float *__restrict__ q, const float *__restrict__ k, cons
             f4 s = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kc = 0; kc < 4; ++kc) {
-                const f4 kf = *(const f4 *)(sK + (16 * c + li) * SB_LD + kc * 16 + 4 * lg);
-                const f4 vf = *(const f4 *)(sV + (16 * c + li) * SB_LD + kc * 16 + 4 * lg);
+                const f4 kf = *(const f4 *)(sK + (16 * c + li) * SB_LD + LDS_SWZ((16 * c + li), kc * 16 + 4 * lg));
+                const f4 vf = *(const f4 *)(sV + (16 * c + li) * SB_LD + LDS_SWZ((16 * c + li), kc * 16 + 4 * lg));
 #pragma unroll
                 for (int st = 0; st < 4; ++st) {
                     s = mfma4(kf[st], qf[kc][st], s);
@@ -1019,7 +1024,7 @@ sdpa_fbwd_dq_hd64(const float *__restrict__ q, const float *__restrict__ k, cons
             // dq[query qw + 4g + r][d = 4li + u] += dS[query][key] K[key][d] over this block's keys
 #pragma unroll
             for (int st = 0; st < 4; ++st) {
-                const f4 kf = *(const f4 *)(sK + (16 * c + 4 * lg + st) * SB_LD + 4 * li);
+                const f4 kf = *(const f4 *)(sK + (16 * c + 4 * lg + st) * SB_LD + LDS_SWZ((16 * c + 4 * lg + st), 4 * li));
 #pragma unroll
                 for (int u = 0; u < 4; ++u) acc[u] = mfma4(dp[st], kf[u], acc[u]);
             }
@@ -1092,18 +1097,24 @@ sdpa_fbwd_dkdv_hd64(const float *__restrict__ q, const float *__restrict__ k, co
         const int h = kvh * rep + it / nq, q0 = qstart + (it % nq) * 64;
         const int64_t rbase = ((int64_t)b * H + h) * Tq;
         __syncthreads();
+        // all eight loads in flight at once (rows past Tq read row Tq - 1 and
+        // are stored as zero), then the LDS stores.  Thread tid stages rows
+        // tid / 16 + 16 j, columns 4 (tid % 16): the swizzle depends on bits 2
+        // and 3 of the row only, so one LDS offset serves all four rows.
+        f4 g[4], qq[4];
+        const int r0 = tid >> 4, c0 = (tid & 15) * 4;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int f = tid + j * 256;
-            const int r = f >> 4, c = (f & 15) * 4;
-            const int qi = q0 + r;
-            f4 g = {0.f, 0.f, 0.f, 0.f}, qq = {0.f, 0.f, 0.f, 0.f};
-            if (qi < Tq) {
-                g = *(const f4 *)(dO + (rbase + qi) * 64 + c);
-                qq = *(const f4 *)(q + (rbase + qi) * 64 + c);
-            }
-            *(f4 *)(sG + r * SB_LD + c) = g;
-            *(f4 *)(sQ + r * SB_LD + c) = qq;
+            const int64_t qr = rbase + min(q0 + r0 + 16 * j, Tq - 1);
+            g[j] = *(const f4 *)(dO + qr * 64 + c0);
+            qq[j] = *(const f4 *)(q + qr * 64 + c0);
+        }
+        const int so = r0 * SB_LD + LDS_SWZ(r0, c0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const bool ok = q0 + r0 + 16 * j < Tq;
+            *(f4 *)(sG + so + 16 * j * SB_LD) = ok ? g[j] : f4{0.f, 0.f, 0.f, 0.f};
+            *(f4 *)(sQ + so + 16 * j * SB_LD) = ok ? qq[j] : f4{0.f, 0.f, 0.f, 0.f};
         }
         if (tid < 64) {
             const int qi = q0 + tid;
@@ -1118,8 +1129,8 @@ sdpa_fbwd_dkdv_hd64(const float *__restrict__ q, const float *__restrict__ k, co
             f4 dp = {0.f, 0.f, 0.f, 0.f}, s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kc = 0; kc < 4; ++kc) {
-                const f4 gfr = *(const f4 *)(sG + (16 * c + li) * SB_LD + kc * 16 + 4 * lg);
-                const f4 qfr = *(const f4 *)(sQ + (16 * c + li) * SB_LD + kc * 16 + 4 * lg);
+                const f4 gfr = *(const f4 *)(sG + (16 * c + li) * SB_LD + LDS_SWZ((16 * c + li), kc * 16 + 4 * lg));
+                const f4 qfr = *(const f4 *)(sQ + (16 * c + li) * SB_LD + LDS_SWZ((16 * c + li), kc * 16 + 4 * lg));
 #pragma unroll
                 for (int st = 0; st < 4; ++st) {
                     dp = mfma4(gfr[st], vf[kc][st], dp);
@@ -1143,8 +1154,8 @@ sdpa_fbwd_dkdv_hd64(const float *__restrict__ q, const float *__restrict__ k, co
             // dV += P^T dO, dK += dS^T Q over this block's 16 queries
 #pragma unroll
             for (int st = 0; st < 4; ++st) {
-                const f4 gfr = *(const f4 *)(sG + (16 * c + 4 * lg + st) * SB_LD + 4 * li);
-                const f4 qfr = *(const f4 *)(sQ + (16 * c + 4 * lg + st) * SB_LD + 4 * li);
+                const f4 gfr = *(const f4 *)(sG + (16 * c + 4 * lg + st) * SB_LD + LDS_SWZ((16 * c + 4 * lg + st), 4 * li));
+                const f4 qfr = *(const f4 *)(sQ + (16 * c + 4 * lg + st) * SB_LD + LDS_SWZ((16 * c + 4 * lg + st), 4 * li));
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     av[u] = mfma4(pf[st], gfr[u], av[u]);

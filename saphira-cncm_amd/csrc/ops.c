@@ -188,12 +188,12 @@ static void sdpa_any(const char *fn, const float *q, const float *k, const float
     }
     if ((int64_t)B * Tq == 0) return;
     if (!q || !k || !v || !out) { ncm_fail(NCM_E_ARG, "%s: null pointer", fn); return; }
-    if (B > 65535 || Hq > 65535) { ncm_fail(NCM_E_ARG, "%s: grid too large", fn); return; }
+    if (B > 65535 || Hq > 65535 || (Tq + 63) / 64 > 65535) { ncm_fail(NCM_E_ARG, "%s: grid too large", fn); return; }
     if (ncm_ready()) return;
     float scale = 1.0f / sqrtf((float)hd);
     if (hd == 64 && is_aligned16(q) && is_aligned16(k) && is_aligned16(v) && is_aligned16(out)) {
         void *a[] = {&q, &k, &v, &mask, &out, &Hq, &Hkv, &Tq, &Tkv, &scale, &causal, &merged, &stats};
-        ncm_launch_named("sdpa_hd64", (unsigned)((Tq + 63) / 64), (unsigned)Hq, (unsigned)B, 256, a);
+        ncm_launch_named("sdpa_hd64", (unsigned)Hq, (unsigned)B, (unsigned)((Tq + 63) / 64), 256, a);
     } else if (stats) {
         ncm_fail(NCM_E_ARG, "%s: row statistics need hd = 64 and 16-byte aligned operands", fn);
     } else {

@@ -249,9 +249,12 @@ sdpa_hd64(const float *__restrict__ q, const float *__restrict__ k, const float 
     __shared__ __attribute__((aligned(16))) float sV[SD_T * SD_LD];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
-    const int h = blockIdx.y, b = blockIdx.z;
+    // grid (Hq, B, query tiles), the last query tile first: under a causal
+    // mask it has the most key tiles, and dispatching the heaviest workgroups
+    // first keeps the chip busy to the end (longest-first order)
+    const int h = blockIdx.x, b = blockIdx.y;
     const int kvh = h / (Hq / Hkv);
-    const int q0 = blockIdx.x * 64, qw = q0 + wave * 16;
+    const int q0 = (gridDim.z - 1 - blockIdx.z) * 64, qw = q0 + wave * 16;
     const float *qb = q + ((int64_t)b * Hq + h) * Tq * 64;
     const float *kb = k + ((int64_t)b * Hkv + kvh) * Tkv * 64;
     const float *vb = v + ((int64_t)b * Hkv + kvh) * Tkv * 64;

@@ -186,6 +186,10 @@ void ncm_sdpa_bwd_flash(const float *q, const float *k, const float *v, const fl
         ncm_fail(NCM_E_ARG, "ncm_sdpa_bwd_flash: causal attention needs Tq <= Tkv");
         return;
     }
+    if ((Tq + 63) / 64 > 65535 || (Tkv + 63) / 64 > 65535) {   /* tiles are the grid's z dimension */
+        ncm_fail(NCM_E_ARG, "ncm_sdpa_bwd_flash: grid too large");
+        return;
+    }
     if (ncm_ready()) return;
     const int64_t rows = (int64_t)B * H * Tq;
     float *D = (float *)ncm_workspace(WS_TRAIN, (size_t)rows * sizeof(float));
@@ -195,11 +199,11 @@ void ncm_sdpa_bwd_flash(const float *q, const float *k, const float *v, const fl
     if (ncm_launch_named("sdpa_bwd_rowdot", blocks_of(rows, 4), 1, 1, 256, a0)) return;
     if (dq) {
         void *a[] = {&q, &k, &v, &mask, &stats, &D, &dO, &dq, &H, &Hkv, &Tq, &Tkv, &scale, &causal};
-        if (ncm_launch_named("sdpa_fbwd_dq_hd64", blocks_of(Tq, 64), (unsigned)H, (unsigned)B, 256, a)) return;
+        if (ncm_launch_named("sdpa_fbwd_dq_hd64", (unsigned)H, (unsigned)B, blocks_of(Tq, 64), 256, a)) return;
     }
     if (dk || dv) {
         void *a[] = {&q, &k, &v, &mask, &stats, &D, &dO, &dk, &dv, &H, &Hkv, &Tq, &Tkv, &scale, &causal};
-        ncm_launch_named("sdpa_fbwd_dkdv_hd64", blocks_of(Tkv, 64), (unsigned)Hkv, (unsigned)B, 256, a);
+        ncm_launch_named("sdpa_fbwd_dkdv_hd64", (unsigned)Hkv, (unsigned)B, blocks_of(Tkv, 64), 256, a);
     }
 }
 

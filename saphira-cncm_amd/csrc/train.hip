@@ -953,9 +953,12 @@ sdpa_fbwd_dq_hd64(const float *__restrict__ q, const float *__restrict__ k, cons
     __shared__ __attribute__((aligned(16))) float sV[64 * SB_LD];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
-    const int h = blockIdx.y, b = blockIdx.z;
+    // grid (H, B, query tiles), the last query tile first: under a causal mask
+    // it has the most key tiles, and dispatching the heaviest workgroups first
+    // keeps the chip busy to the end (longest-first order)
+    const int h = blockIdx.x, b = blockIdx.y;
     const int kvh = h / (H / Hkv);
-    const int q0 = blockIdx.x * 64, qw = q0 + wave * 16;
+    const int q0 = (gridDim.z - 1 - blockIdx.z) * 64, qw = q0 + wave * 16;
     const int my_q = qw + li;
     const int64_t rbase = ((int64_t)b * H + h) * Tq;
     const float *kb = k + ((int64_t)b * Hkv + kvh) * Tkv * 64;
@@ -1065,9 +1068,12 @@ sdpa_fbwd_dkdv_hd64(const float *__restrict__ q, const float *__restrict__ k, co
     __shared__ __attribute__((aligned(16))) float sD[64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
-    const int kvh = blockIdx.y, b = blockIdx.z;
+    // grid (Hkv, B, key tiles), the first key tile first: under a causal mask
+    // it meets the most query tiles, and dispatching the heaviest workgroups
+    // first keeps the chip busy to the end (longest-first order)
+    const int kvh = blockIdx.x, b = blockIdx.y;
     const int rep = H / Hkv;
-    const int k0 = blockIdx.x * 64;
+    const int k0 = blockIdx.z * 64;
     const int kl = wave * 16 + li;
     const int my_k = k0 + kl;
     const bool kok = my_k < Tkv;

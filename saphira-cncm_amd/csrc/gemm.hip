@@ -127,6 +127,40 @@ colsum_partial_s(const float *__restrict__ dy, int64_t rows, int N, double *__re
     part[(int64_t)blockIdx.y * N + col] = s;
 }
 
+// The same sum in one launch for rows <= COLSUM_SMALL_ROWS: a workgroup of 16
+// waves owns 64 columns (one per lane, so any N and alignment), wave w sums
+// rows w, w + 16, ... in fp64 with all of its loads in flight, and wave 0
+// adds the 16 partials in wave order.  Two launches of ~4 us each were the
+// whole cost of a small-batch bias gradient.
+#define COLSUM_SMALL_ROWS 512
+extern "C" __global__ void __launch_bounds__(1024)
+colsum_small(const float *__restrict__ dy, int rows, int N, float *db) {
+    __shared__ double red[16][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = blockIdx.x * 64 + lane;
+    double s = 0.0;
+    if (col < N) {
+        // unconditional loads of a clamped row (a guarded load would be a
+        // branch with a wait after it), rows past the end then count zero
+        float v[COLSUM_SMALL_ROWS / 16];
+        const float *p = dy + col;
+#pragma unroll
+        for (int j = 0; j < COLSUM_SMALL_ROWS / 16; ++j)
+            v[j] = p[(int64_t)min(wave + 16 * j, rows - 1) * N];
+#pragma unroll
+        for (int j = 0; j < COLSUM_SMALL_ROWS / 16; ++j)
+            if (wave + 16 * j < rows) s += (double)v[j];
+    }
+    red[wave][lane] = s;
+    __syncthreads();
+    if (wave == 0 && col < N) {
+        double t = red[0][lane];
+#pragma unroll
+        for (int w = 1; w < 16; ++w) t += red[w][lane];
+        db[col] += (float)t;
+    }
+}
+
 extern "C" __global__ void __launch_bounds__(256)
 colsum_final(const double *__restrict__ part, int chunks, int N, float *db) {
     int col = blockIdx.x * 256 + threadIdx.x;

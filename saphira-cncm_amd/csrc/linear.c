@@ -333,6 +333,7 @@ static const char *dxt_name(int nb) {
 }
 #define DXT_ROWS 32
 #define COLSUM_ROWS 64
+#define COLSUM_SMALL_ROWS 512   /* colsum_small covers up to this many rows */
 
 static int run_dxt(const float *dy, const float *W, float *dx, int nb, int M, int K) {
     int r0 = 0;
@@ -390,6 +391,11 @@ void linear_bwd(const float *x, const float *W, const float *dy, float *dx, floa
         if (rc) return;
     }
     if (db) {
+        if (nb <= COLSUM_SMALL_ROWS) {   /* one launch: a workgroup per 64 columns sums every row */
+            void *a[] = {&dy, &nb, &M, &db};
+            ncm_launch_named("colsum_small", (unsigned)((M + 63) / 64), 1, 1, 1024, a);
+            return;
+        }
         int chunks = (nb + COLSUM_ROWS - 1) / COLSUM_ROWS;
         double *part = (double *)ncm_workspace(WS_COLSUM, (size_t)chunks * M * sizeof(double));
         if (!part) return;

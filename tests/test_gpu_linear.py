@@ -175,6 +175,26 @@ def test_exact_integer_products():
         assert bits_equal(db, dy.astype(np.int64).sum(0).astype(np.float32))
 
 
+def test_bias_gradient_batch_sizes():
+    """db over batch sizes on both sides of the one-launch column sum's limits
+    (16 waves, 512 rows) and column counts that are not whole 64-column
+    blocks or 16-byte aligned rows; accumulated onto a non-zero db."""
+    rng = np.random.default_rng(23)
+    for rows in (1, 15, 16, 17, 100, 511, 512, 513, 1100):
+        for N in (1, 63, 130, 2304):
+            K = 8
+            x = rng.standard_normal((rows, K)).astype(np.float32)
+            W = rng.standard_normal((N, K)).astype(np.float32)
+            db0 = rng.standard_normal(N).astype(np.float32)
+            dyi = rng.integers(-4, 5, (rows, N)).astype(np.float32)
+            _, _, db = gpu_bwd(x, W, dyi, None, None, np.zeros(N, np.float32))
+            assert bits_equal(db, dyi.astype(np.int64).sum(0).astype(np.float32)), (rows, N)
+            dy = rng.standard_normal((rows, N)).astype(np.float32)
+            _, _, db = gpu_bwd(x, W, dy, None, None, db0)
+            _, _, ref = O.linear_bwd(x, W, dy, db=db0, want=("db",))
+            assert maxrel(db, ref) <= TOL, (rows, N)
+
+
 def test_run_to_run_determinism():
     rng, x, W, b = sweep_inputs(3, 512, 3072, 768)
     a = gpu_fwd(x, W, b)

@@ -43,9 +43,23 @@ static int ops_ready(const char *fn, int64_t n, int nptr, const void *p0, const 
 }
 
 /* ---- norms (kernels.c:101-162) ---- */
+/* The register-resident norm kernels take rows of C <= 1024 floats,
+ * C % 4 == 0, 16-byte aligned. */
+static int norm4_ok(const float *x, const float *w, const float *b, const float *y, int C) {
+    return C % 4 == 0 && C <= 1024 && aligned16(x) && aligned16(w) && aligned16(b) && aligned16(y);
+}
+
 void rmsnorm_fwd(const float *x, const float *w, float *y, int64_t rows, int C) {
     if (C <= 0) { ncm_fail(NCM_E_ARG, "rmsnorm_fwd: C=%d", C); return; }
     if (ops_ready("rmsnorm_fwd", rows, 2, x, y)) return;
+    if (norm4_ok(x, w, NULL, y, C)) {
+        static const char *const k[4] = {"rmsnorm4_1", "rmsnorm4_2", "rmsnorm4_3", "rmsnorm4_4"};
+        const float *none = NULL;
+        double eps = 0.0;
+        void *a[] = {&x, &w, &none, &y, &rows, &C, &eps};
+        ncm_launch_named(k[(C + 255) / 256 - 1], grid_of(rows, 4), 1, 1, 256, a);
+        return;
+    }
     void *a[] = {&x, &w, &y, &rows, &C};
     ncm_launch_named("rmsnorm_k", grid_of(rows, 4), 1, 1, 256, a);
 }
@@ -55,6 +69,11 @@ static void layernorm_any(const char *fn, const float *x, const float *w, const 
     if (C <= 0) { ncm_fail(NCM_E_ARG, "%s: C=%d", fn, C); return; }
     if (ops_ready(fn, rows, 2, x, y)) return;
     void *a[] = {&x, &w, &b, &y, &rows, &C, &eps};
+    if (norm4_ok(x, w, b, y, C)) {
+        static const char *const k[4] = {"layernorm4_1", "layernorm4_2", "layernorm4_3", "layernorm4_4"};
+        ncm_launch_named(k[(C + 255) / 256 - 1], grid_of(rows, 4), 1, 1, 256, a);
+        return;
+    }
     ncm_launch_named("layernorm_k", grid_of(rows, 4), 1, 1, 256, a);
 }
 
@@ -115,6 +134,12 @@ void heads_transpose_fwd_b(const float *in, float *out, int B, int64_t T, int H,
     int64_t n = (int64_t)B * T * H * hd;
     if (B < 0 || T < 0 || H < 0 || hd < 0) { ncm_fail(NCM_E_ARG, "heads_transpose_fwd: bad shape"); return; }
     if (ops_ready("heads_transpose_fwd", n, 2, in, out)) return;
+    if (hd % 4 == 0 && (int64_t)B * T <= INT_MAX && T <= INT_MAX && aligned16(in) && aligned16(out)) {
+        int Ti = (int)T;
+        void *a[] = {&in, &out, &Ti, &H, &hd};
+        ncm_launch_named("heads_transpose_rows_k", (unsigned)(B * T), 1, 1, 256, a);
+        return;
+    }
     void *a[] = {&in, &out, &B, &T, &H, &hd};
     ncm_launch_named("heads_transpose_k", grid_of(n, 256), 1, 1, 256, a);
 }
@@ -133,6 +158,12 @@ void qkv_split_fwd(const float *in, float *qq, float *kk, float *vv, int B, int 
     }
     if (ops_ready("qkv_split_fwd", n, 2, in, qq)) return;
     if (!kk || !vv) { ncm_fail(NCM_E_ARG, "qkv_split_fwd: null pointer"); return; }
+    if (hd % 4 == 0 && C % 4 == 0 && (int64_t)B * T <= INT_MAX && (int64_t)C + 2 * K * hd <= INT_MAX &&
+        aligned16(in) && aligned16(qq) && aligned16(kk) && aligned16(vv)) {
+        void *a[] = {&in, &qq, &kk, &vv, &T, &C, &H, &hd, &K, &rep};
+        ncm_launch_named("qkv_split_rows_k", (unsigned)((int64_t)B * T), 1, 1, 256, a);
+        return;
+    }
     void *a[] = {&in, &qq, &kk, &vv, &B, &T, &C, &H, &hd, &K, &rep};
     ncm_launch_named("qkv_split_k", grid_of(n, 256), 1, 1, 256, a);
 }
@@ -158,6 +189,11 @@ void head_merge_fwd(const float *ctx, float *out, int B, int T, int C, int H, in
         return;
     }
     if (ops_ready("head_merge_fwd", n, 2, ctx, out)) return;
+    if (hd % 4 == 0 && C % 4 == 0 && (int64_t)B * T <= INT_MAX && aligned16(ctx) && aligned16(out)) {
+        void *a[] = {&ctx, &out, &T, &C, &H, &hd};
+        ncm_launch_named("head_merge_rows_k", (unsigned)((int64_t)B * T), 1, 1, 256, a);
+        return;
+    }
     void *a[] = {&ctx, &out, &B, &T, &C, &H, &hd};
     ncm_launch_named("head_merge_k", grid_of(n, 256), 1, 1, 256, a);
 }

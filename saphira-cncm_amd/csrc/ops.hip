@@ -78,6 +78,90 @@ layernorm_k(const float *__restrict__ x, const float *__restrict__ w, const floa
         yr[c] = (float)(((double)xr[c] - mean) * inv) * (w ? w[c] : 1.0f) + (b ? b[c] : 0.0f);
 }
 
+// Register-resident forms of rmsnorm_k (KIND 1) and layernorm_k (KIND 0) for
+// C <= 256 * NPL, C % 4 == 0 and 16-byte aligned rows: the wave reads its row
+// once as float4 groups (group q = lane + 64 j) with every load in flight,
+// and the statistics and the output come from those registers, with the
+// kernels' arithmetic per element.  In place (y == x) is allowed: a row is
+// read whole before it is written.
+template <int KIND, int NPL>
+__device__ __forceinline__ void norm_rows4(const float *x, const float *__restrict__ w, const float *__restrict__ b,
+                                           float *y, int64_t rows, int C, double eps) {
+#pragma clang fp contract(off)
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    f4 v[NPL];
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+        const int c = 4 * (lane + 64 * j);
+        v[j] = c < C ? *(const f4 *)(x + row * C + c) : f4{0.f, 0.f, 0.f, 0.f};
+    }
+    if (KIND == 0) {
+        double mean = 0.0;
+#pragma unroll
+        for (int j = 0; j < NPL; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) mean += (double)v[j][e];
+        mean = wave_sum_d(mean) / C;
+        double var = 0.0;
+#pragma unroll
+        for (int j = 0; j < NPL; ++j)
+            if (4 * (lane + 64 * j) < C)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const double d = (double)v[j][e] - mean;
+                    var += d * d;
+                }
+        var = wave_sum_d(var) / C;
+        const double inv = 1.0 / sqrt(var + eps);
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) {
+            const int c = 4 * (lane + 64 * j);
+            if (c >= C) continue;
+            const f4 wv = w ? *(const f4 *)(w + c) : f4{1.f, 1.f, 1.f, 1.f};
+            const f4 bv = b ? *(const f4 *)(b + c) : f4{0.f, 0.f, 0.f, 0.f};
+            f4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = (float)(((double)v[j][e] - mean) * inv) * wv[e] + bv[e];
+            *(f4 *)(y + row * C + c) = o;
+        }
+    } else {
+        double ms = 0.0;
+#pragma unroll
+        for (int j = 0; j < NPL; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) ms += (double)v[j][e] * (double)v[j][e];
+        ms = wave_sum_d(ms) / C;
+        const float s = (float)(1.0 / sqrt(ms + 1e-6));
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) {
+            const int c = 4 * (lane + 64 * j);
+            if (c >= C) continue;
+            const f4 wv = w ? *(const f4 *)(w + c) : f4{1.f, 1.f, 1.f, 1.f};
+            f4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = v[j][e] * s * wv[e];
+            *(f4 *)(y + row * C + c) = o;
+        }
+    }
+}
+
+#define NORM_ROWS4(name, KIND, NPL)                                                                            \
+    extern "C" __global__ void __launch_bounds__(256)                                                         \
+        name(const float *x, const float *__restrict__ w, const float *__restrict__ b, float *y, int64_t rows, \
+             int C, double eps) {                                                                             \
+        norm_rows4<KIND, NPL>(x, w, b, y, rows, C, eps);                                                      \
+    }
+NORM_ROWS4(layernorm4_1, 0, 1)
+NORM_ROWS4(layernorm4_2, 0, 2)
+NORM_ROWS4(layernorm4_3, 0, 3)
+NORM_ROWS4(layernorm4_4, 0, 4)
+NORM_ROWS4(rmsnorm4_1, 1, 1)
+NORM_ROWS4(rmsnorm4_2, 1, 2)
+NORM_ROWS4(rmsnorm4_3, 1, 3)
+NORM_ROWS4(rmsnorm4_4, 1, 4)
+
 // ---------------------------------------------------------------- RoPE
 // Rotate-half RoPE in place (kernels.c:249-264): rows of hd, position
 // row % T, y[d] = a*c[d] + (-b)*s[d], y[d+h] = b*c[d+h] + a*s[d+h] with the
@@ -171,6 +255,68 @@ head_merge_k(const float *__restrict__ ctx, float *__restrict__ out, int B, int 
     const int t = (int)((i / C) % T);
     const int b = (int)(i / ((int64_t)T * C));
     out[i] = ctx[(((int64_t)b * H + hh) * T + t) * hd + dd];
+}
+
+// Row-blocked forms of the three layout kernels above, for hd and C multiples
+// of 4 and 16-byte aligned operands: one workgroup per (b, t) row and one
+// float4 per thread and pass, so the row's index arithmetic is done once per
+// workgroup in 32-bit (the per-element forms spend most of their time in
+// 64-bit division) and every access is 16 bytes inside a run of hd floats.
+// Head h of row (b, t) in a [B][H][T][hd] tensor starts at base + h * hs.
+__device__ __forceinline__ void row_bt(int T, int H, int hd, int &bt, int64_t &base, int64_t &hs) {
+    bt = blockIdx.x;
+    const int b = bt / T, t = bt - b * T;
+    hs = (int64_t)T * hd;
+    base = ((int64_t)b * H * T + t) * hd;
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+qkv_split_rows_k(const float *__restrict__ in, float *__restrict__ qq, float *__restrict__ kk,
+                 float *__restrict__ vv, int T, int C, int H, int hd, int K, int rep) {
+    int bt;
+    int64_t base, hs;
+    row_bt(T, H, hd, bt, base, hs);
+    const int rl = C + 2 * K * hd;
+    const f4 *row = (const f4 *)(in + (int64_t)bt * rl);
+    for (int f = threadIdx.x; f < rl / 4; f += 256) {
+        const int c = 4 * f;
+        const f4 v = row[f];
+        if (c < C) {
+            const int h = c / hd;
+            if (h < H) *(f4 *)(qq + base + h * hs + (c - h * hd)) = v;
+        } else {
+            // kv head kvh feeds query heads kvh * rep .. kvh * rep + rep - 1
+            const int kc = c - C;
+            float *dst = kc < K * hd ? kk : vv;
+            const int k2 = kc < K * hd ? kc : kc - K * hd;
+            const int kvh = k2 / hd, d = k2 - kvh * hd;
+            for (int h = kvh * rep; h < (kvh + 1) * rep && h < H; ++h) *(f4 *)(dst + base + h * hs + d) = v;
+        }
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+head_merge_rows_k(const float *__restrict__ ctx, float *__restrict__ out, int T, int C, int H, int hd) {
+    int bt;
+    int64_t base, hs;
+    row_bt(T, H, hd, bt, base, hs);
+    f4 *orow = (f4 *)(out + (int64_t)bt * C);
+    for (int f = threadIdx.x; f < C / 4; f += 256) {
+        const int c = 4 * f, h = c / hd;
+        orow[f] = *(const f4 *)(ctx + base + h * hs + (c - h * hd));
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+heads_transpose_rows_k(const float *__restrict__ in, float *__restrict__ out, int T, int H, int hd) {
+    int bt;
+    int64_t base, hs;
+    row_bt(T, H, hd, bt, base, hs);
+    const f4 *irow = (const f4 *)(in + (int64_t)bt * H * hd);
+    for (int f = threadIdx.x; f < H * hd / 4; f += 256) {
+        const int c = 4 * f, h = c / hd;
+        *(f4 *)(out + base + h * hs + (c - h * hd)) = irow[f];
+    }
 }
 
 // embedding_fwd (kernels.c:59-74): y[i,:] = W[idx[i],:]; ids outside [0, V)

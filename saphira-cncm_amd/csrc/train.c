@@ -13,6 +13,7 @@
 #include <stdlib.h>
 
 #define NORM_ROWS 128
+#define NBF_ROWS 32   /* rows per workgroup of the fused norm backward */
 
 static unsigned blocks_of(int64_t n, int per) { return (unsigned)((n + per - 1) / per); }
 
@@ -29,8 +30,28 @@ static void norm_bwd(const char *fn, int kind, const float *x, const float *w, c
     if (rows == 0) return;
     if (!x || !dy) { ncm_fail(NCM_E_ARG, "%s: null input", fn); return; }
     if (ncm_ready()) return;
-    const int chunks = (int)((rows + NORM_ROWS - 1) / NORM_ROWS);
     const int want_param = dw || db;
+    if (C % 4 == 0 && C <= 1024 && is_aligned16(x) && is_aligned16(dy) && (!dx || is_aligned16(dx)) &&
+        (!w || is_aligned16(w)) && (rows + NBF_ROWS - 1) / NBF_ROWS <= INT_MAX) {
+        /* one pass: rows in registers, dx and the parameter partials together */
+        static const char *const names[2][4] = {{"ln_bwd_fused_1", "ln_bwd_fused_2", "ln_bwd_fused_3", "ln_bwd_fused_4"},
+                                                {"rmsn_bwd_fused_1", "rmsn_bwd_fused_2", "rmsn_bwd_fused_3",
+                                                 "rmsn_bwd_fused_4"}};
+        const int chunks = (int)((rows + NBF_ROWS - 1) / NBF_ROWS);
+        double *part = NULL;
+        if (want_param) {
+            part = (double *)ncm_workspace(WS_TRAIN, (size_t)chunks * C * 2 * sizeof(double));
+            if (!part) return;
+        }
+        void *a[] = {&x, &w, &dy, &dx, &part, &rows, &C, &eps};
+        if (ncm_launch_named(names[kind][(C + 255) / 256 - 1], (unsigned)chunks, 1, 1, 256, a)) return;
+        if (!want_param) return;
+        float *dbk = kind == 0 ? db : NULL;
+        void *a2[] = {&part, &dw, &dbk, (void *)&chunks, &C};
+        ncm_launch_named("norm_param_sum", blocks_of(C, 64), 1, 1, 1024, a2);
+        return;
+    }
+    const int chunks = (int)((rows + NORM_ROWS - 1) / NORM_ROWS);
     if (chunks > 65535 && want_param) { ncm_fail(NCM_E_ARG, "%s: too many rows", fn); return; }
     size_t stats_bytes = (size_t)rows * 2 * sizeof(double);
     size_t part_bytes = want_param ? (size_t)chunks * C * 2 * sizeof(double) : 0;
@@ -487,6 +508,12 @@ void qkv_split_bwd(const float *gq, const float *gk, const float *gv, float *dx,
     int64_t n = (int64_t)B * T * ((int64_t)C + 2 * K * hd);
     if (elt_check("qkv_split_bwd", n, dx, dx)) return;
     if (!gq && !gk && !gv) return;
+    if (hd % 4 == 0 && C % 4 == 0 && (int64_t)B * T <= INT_MAX && (int64_t)C + 2 * K * hd <= INT_MAX &&
+        is_aligned16(gq) && is_aligned16(gk) && is_aligned16(gv) && is_aligned16(dx)) {
+        void *a[] = {&gq, &gk, &gv, &dx, &T, &C, &H, &hd, &K, &rep};
+        ncm_launch_named("qkv_split_bwd_rows_k", (unsigned)((int64_t)B * T), 1, 1, 256, a);
+        return;
+    }
     void *a[] = {&gq, &gk, &gv, &dx, &B, &T, &C, &H, &hd, &K, &rep};
     ncm_launch_named("qkv_split_bwd_k", blocks_of(n, 256), 1, 1, 256, a);
 }
@@ -498,6 +525,11 @@ static void heads_bwd(const char *fn, const float *dy, float *dx, int B, int T, 
     }
     int64_t n = dir == 0 ? (int64_t)B * H * T * hd : (int64_t)B * T * C;
     if (elt_check(fn, n, dy, dx)) return;
+    if (hd % 4 == 0 && C % 4 == 0 && (int64_t)B * T <= INT_MAX && is_aligned16(dy) && is_aligned16(dx)) {
+        void *a[] = {&dy, &dx, &T, &C, &H, &hd, &dir};
+        ncm_launch_named("heads_bwd_rows_k", (unsigned)((int64_t)B * T), 1, 1, 256, a);
+        return;
+    }
     void *a[] = {&dy, &dx, &B, &T, &C, &H, &hd, &dir};
     ncm_launch_named("heads_bwd_k", blocks_of(n, 256), 1, 1, 256, a);
 }

@@ -115,6 +115,243 @@ norm_param_final(const double *__restrict__ part, float *__restrict__ dw, float 
     if (db) db[c] += (float)sb;
 }
 
+// Fused norm backward for C <= 256 * NPL, C % 4 == 0 and 16-byte aligned rows:
+// a workgroup owns NBF_ROWS consecutive rows, NBF_ROWS / 4 per wave in
+// ascending order.  A row is read once into registers (float4 column group
+// q = lane + 64 j of each operand) and the next row's loads are in flight
+// while it is reduced: the row statistics, dx (the arithmetic of ln_bwd_rows /
+// rmsn_bwd_rows) and the column partials of the parameter gradients (that of
+// norm_param_partial) all come from those registers.  The four waves' column
+// partials are added in wave order into part[chunk][C][2]; norm_param_sum adds
+// the chunks in order.  x and dy are read once instead of twice and the row
+// loop keeps its loads in flight instead of one scalar load per pass.
+#define NBF_ROWS 32
+template <int KIND, int NPL>
+__device__ __forceinline__ void nbf_load(const float *__restrict__ p, int64_t row, int C, int lane, f4 (&v)[NPL]) {
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+        const int c = 4 * (lane + 64 * j);
+        v[j] = c < C ? *(const f4 *)(p + row * C + c) : f4{0.f, 0.f, 0.f, 0.f};
+    }
+}
+
+template <int KIND, int NPL>
+__device__ __forceinline__ void norm_bwd_fused_body(const float *__restrict__ x, const float *__restrict__ w,
+                                                    const float *__restrict__ dy, float *__restrict__ dx,
+                                                    double *__restrict__ part, int64_t rows, int C, double eps) {
+#pragma clang fp contract(off)
+    constexpr int NP = KIND == 0 ? 2 : 1;   // parameter gradients: (dw, db) or dw
+    __shared__ double red[3][64 * NPL][4][NP];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t rbeg = (int64_t)blockIdx.x * NBF_ROWS + wave * (NBF_ROWS / 4);
+    const int64_t rend = min(rows, rbeg + NBF_ROWS / 4);
+    f4 wv[NPL];
+    if (w) nbf_load<KIND, NPL>(w, 0, C, lane, wv);
+#pragma unroll
+    for (int j = 0; j < NPL; ++j)
+        if (!w) wv[j] = f4{1.f, 1.f, 1.f, 1.f};
+    double sp[NPL][4][NP];
+#pragma unroll
+    for (int j = 0; j < NPL; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int k = 0; k < NP; ++k) sp[j][e][k] = 0.0;
+    f4 xa[NPL], ga[NPL];
+    if (rbeg < rend) {
+        nbf_load<KIND, NPL>(x, rbeg, C, lane, xa);
+        nbf_load<KIND, NPL>(dy, rbeg, C, lane, ga);
+    }
+    for (int64_t r = rbeg; r < rend; ++r) {
+        f4 xn[NPL], gn[NPL];
+        if (r + 1 < rend) {
+            nbf_load<KIND, NPL>(x, r + 1, C, lane, xn);
+            nbf_load<KIND, NPL>(dy, r + 1, C, lane, gn);
+        }
+        if (KIND == 0) {
+            double mean = 0.0;
+#pragma unroll
+            for (int j = 0; j < NPL; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) mean += (double)xa[j][e];
+            mean = wave_sum_d(mean) / C;
+            double var = 0.0;
+#pragma unroll
+            for (int j = 0; j < NPL; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (4 * (lane + 64 * j) < C) {
+                        const double d = (double)xa[j][e] - mean;
+                        var += d * d;
+                    }
+            var = wave_sum_d(var) / C;
+            const double inv = 1.0 / sqrt(var + eps);
+            if (dx) {
+                double dmean = 0.0, dvar = 0.0;
+#pragma unroll
+                for (int j = 0; j < NPL; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (4 * (lane + 64 * j) < C) {
+                            const double d = (double)ga[j][e] * (double)wv[j][e];
+                            dmean += d;
+                            dvar += d * ((double)xa[j][e] - mean);
+                        }
+                dmean = wave_sum_d(dmean) / C;
+                dvar = wave_sum_d(dvar) * (-0.5 * inv * inv * inv / C);
+#pragma unroll
+                for (int j = 0; j < NPL; ++j) {
+                    const int c = 4 * (lane + 64 * j);
+                    if (c < C) {
+                        f4 *o = (f4 *)(dx + r * C + c);
+                        f4 v = *o;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const double d = (double)ga[j][e] * (double)wv[j][e];
+                            v[e] += (float)((d - dmean) * inv + 2 * ((double)xa[j][e] - mean) * dvar);
+                        }
+                        *o = v;
+                    }
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < NPL; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    sp[j][e][0] += (double)ga[j][e] * (((double)xa[j][e] - mean) * inv);
+                    sp[j][e][NP - 1] += (double)ga[j][e];
+                }
+        } else {
+            double ms = 0.0;
+#pragma unroll
+            for (int j = 0; j < NPL; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) ms += (double)xa[j][e] * (double)xa[j][e];
+            ms = wave_sum_d(ms) / C;
+            const double inv = 1.0 / sqrt(ms + 1e-6);
+            if (dx) {
+                double dot = 0.0;
+#pragma unroll
+                for (int j = 0; j < NPL; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) dot += (double)ga[j][e] * (double)wv[j][e] * (double)xa[j][e];
+                dot = wave_sum_d(dot) / C;
+#pragma unroll
+                for (int j = 0; j < NPL; ++j) {
+                    const int c = 4 * (lane + 64 * j);
+                    if (c < C) {
+                        f4 *o = (f4 *)(dx + r * C + c);
+                        f4 v = *o;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            v[e] += (float)(((double)ga[j][e] * (double)wv[j][e] -
+                                             dot * (double)xa[j][e] * inv * inv) * inv);
+                        *o = v;
+                    }
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < NPL; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float gx = ga[j][e] * xa[j][e];
+                    sp[j][e][0] += (double)gx * inv;
+                }
+        }
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) {
+            xa[j] = xn[j];
+            ga[j] = gn[j];
+        }
+    }
+    if (!part) return;
+    if (wave > 0) {
+#pragma unroll
+        for (int j = 0; j < NPL; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int k = 0; k < NP; ++k) red[wave - 1][lane + 64 * j][e][k] = sp[j][e][k];
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) {
+            const int c = 4 * (lane + 64 * j);
+            if (c >= C) continue;
+            double *o = part + ((int64_t)blockIdx.x * C + c) * 2;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                double s0 = sp[j][e][0], s1 = sp[j][e][NP - 1];
+#pragma unroll
+                for (int v = 0; v < 3; ++v) {
+                    s0 += red[v][lane + 64 * j][e][0];
+                    s1 += red[v][lane + 64 * j][e][NP - 1];
+                }
+                o[2 * e] = s0;
+                o[2 * e + 1] = KIND == 0 ? s1 : 0.0;
+            }
+        }
+    }
+}
+
+#define NORM_BWD_FUSED(name, KIND, NPL)                                                                      \
+    extern "C" __global__ void __launch_bounds__(256)                                                       \
+        name(const float *__restrict__ x, const float *__restrict__ w, const float *__restrict__ dy,        \
+             float *__restrict__ dx, double *__restrict__ part, int64_t rows, int C, double eps) {           \
+        norm_bwd_fused_body<KIND, NPL>(x, w, dy, dx, part, rows, C, eps);                                   \
+    }
+NORM_BWD_FUSED(ln_bwd_fused_1, 0, 1)
+NORM_BWD_FUSED(ln_bwd_fused_2, 0, 2)
+NORM_BWD_FUSED(ln_bwd_fused_3, 0, 3)
+NORM_BWD_FUSED(ln_bwd_fused_4, 0, 4)
+NORM_BWD_FUSED(rmsn_bwd_fused_1, 1, 1)
+NORM_BWD_FUSED(rmsn_bwd_fused_2, 1, 2)
+NORM_BWD_FUSED(rmsn_bwd_fused_3, 1, 3)
+NORM_BWD_FUSED(rmsn_bwd_fused_4, 1, 4)
+
+// dw[c] += (float) sum_k part[k][c][0], db[c] += (float) sum_k part[k][c][1],
+// the chunks added in order: a workgroup of 16 waves per 64 columns, wave v
+// sums chunks v, v + 16, ... (32 loads in flight per batch), then wave 0 adds
+// the 16 wave sums in wave order.
+extern "C" __global__ void __launch_bounds__(1024)
+norm_param_sum(const double *__restrict__ part, float *__restrict__ dw, float *__restrict__ db, int chunks, int C) {
+    __shared__ double red[16][64][2];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c = blockIdx.x * 64 + lane;
+    double s0 = 0.0, s1 = 0.0;
+    if (c < C) {
+        const double *p = part + (int64_t)c * 2;
+        for (int k0 = wave; k0 < chunks; k0 += 16 * 16) {
+            double2 v[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const int k = min(k0 + 16 * u, chunks - 1);
+                v[u] = *(const double2 *)(p + (int64_t)k * C * 2);
+            }
+#pragma unroll
+            for (int u = 0; u < 16; ++u)
+                if (k0 + 16 * u < chunks) {
+                    s0 += v[u].x;
+                    s1 += v[u].y;
+                }
+        }
+    }
+    red[wave][lane][0] = s0;
+    red[wave][lane][1] = s1;
+    __syncthreads();
+    if (wave == 0 && c < C) {
+        double t0 = red[0][lane][0], t1 = red[0][lane][1];
+#pragma unroll
+        for (int v = 1; v < 16; ++v) {
+            t0 += red[v][lane][0];
+            t1 += red[v][lane][1];
+        }
+        if (dw) dw[c] += (float)t0;
+        if (db) db[c] += (float)t1;
+    }
+}
+
 // ---------------------------------------------------------------- cross-entropy
 // One wave per row (train_tape.c:452-465): float max, fp64 exp and sum,
 // p = (float)e / (float)den, nll = w * -log(p[tgt] + 1e-30).
@@ -884,6 +1121,58 @@ qkv_split_bwd_k(const float *__restrict__ gq, const float *__restrict__ gk, cons
     float s = 0.f;
     for (int h = kvh * rep; h < (kvh + 1) * rep && h < H; ++h) s += g[(((int64_t)b * H + h) * T + t) * hd + d];
     dx[i] += s;
+}
+
+// Row-blocked forms of qkv_split_bwd_k and heads_bwd_k (the same float
+// operations per element) for hd and C multiples of 4 and 16-byte aligned
+// operands: one workgroup per (b, t) row, one float4 per thread and pass,
+// the row's indices computed once in 32-bit.
+__device__ __forceinline__ void rows_bt(int T, int H, int hd, int &bt, int64_t &base, int64_t &hs) {
+    bt = blockIdx.x;
+    const int b = bt / T, t = bt - b * T;
+    hs = (int64_t)T * hd;
+    base = ((int64_t)b * H * T + t) * hd;
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+qkv_split_bwd_rows_k(const float *__restrict__ gq, const float *__restrict__ gk, const float *__restrict__ gv,
+                     float *__restrict__ dx, int T, int C, int H, int hd, int K, int rep) {
+#pragma clang fp contract(off)
+    int bt;
+    int64_t base, hs;
+    rows_bt(T, H, hd, bt, base, hs);
+    const int rl = C + 2 * K * hd;
+    f4 *row = (f4 *)(dx + (int64_t)bt * rl);
+    for (int f = threadIdx.x; f < rl / 4; f += 256) {
+        const int c = 4 * f;
+        if (c < C) {
+            const int h = c / hd;
+            if (gq && h < H) row[f] += *(const f4 *)(gq + base + h * hs + (c - h * hd));
+            continue;
+        }
+        const int kc = c - C;
+        const float *g = kc < K * hd ? gk : gv;
+        if (!g) continue;
+        const int k2 = kc < K * hd ? kc : kc - K * hd;
+        const int kvh = k2 / hd, d = k2 - kvh * hd;
+        f4 s = {0.f, 0.f, 0.f, 0.f};
+        for (int h = kvh * rep; h < (kvh + 1) * rep && h < H; ++h) s += *(const f4 *)(g + base + h * hs + d);
+        row[f] += s;
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+heads_bwd_rows_k(const float *__restrict__ dy, float *__restrict__ dx, int T, int C, int H, int hd, int dir) {
+#pragma clang fp contract(off)
+    int bt;
+    int64_t base, hs;
+    rows_bt(T, H, hd, bt, base, hs);
+    for (int f = threadIdx.x; f < C / 4; f += 256) {
+        const int c = 4 * f, h = c / hd;
+        const int64_t o = base + h * hs + (c - h * hd);
+        if (dir == 0) *(f4 *)(dx + o) += *(const f4 *)(dy + (int64_t)bt * C + c);
+        else *(f4 *)(dx + (int64_t)bt * C + c) += *(const f4 *)(dy + o);
+    }
 }
 
 // TOP_MERGE (train_tape.c:1329-1338): dctx[b,h,t,d] += dy[b,t,h*hd+d];

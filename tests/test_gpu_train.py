@@ -39,7 +39,7 @@ def up(a):
 
 
 # ---------------------------------------------------------------- norms
-@pytest.mark.parametrize("rows,C", [(1, 1), (37, 96), (300, 65), (4096, 768), (129, 896)])
+@pytest.mark.parametrize("rows,C", [(1, 1), (37, 96), (300, 65), (4096, 768), (129, 896), (70, 1024), (33, 1028)])
 @pytest.mark.parametrize("eps,affine", [(1e-6, True), (1e-5, True), (1e-6, False)])
 def test_layernorm_bwd(rows, C, eps, affine):
     x, dy = rnd(1, rows, C) * 2 + 0.3, rnd(2, rows, C)
@@ -54,7 +54,7 @@ def test_layernorm_bwd(rows, C, eps, affine):
         assert maxrel(dw.numpy(), rdw) <= 1e-5 and maxrel(db.numpy(), rdb) <= 1e-5
 
 
-@pytest.mark.parametrize("rows,C", [(1, 1), (29, 128), (5184, 256), (2048, 896)])
+@pytest.mark.parametrize("rows,C", [(1, 1), (29, 128), (5184, 256), (2048, 896), (45, 1024)])
 @pytest.mark.parametrize("weighted", [True, False])
 def test_rmsnorm_bwd(rows, C, weighted):
     x, dy = rnd(7, rows, C), rnd(8, rows, C)
@@ -252,6 +252,24 @@ def test_split_merge_bwd(B, T, C, H, hd, K, rep):
     dxs = up(x0)
     ncmhip.call("heads_transpose_bwd", up(dys), dxs, B, T, C, H, hd)
     assert bits_equal(dxs.numpy(), O.heads_transpose_bwd(dys, B, T, C, H, hd, x0))
+
+
+def test_layout_rows_partial_heads():
+    """A qkv row whose q part is wider than H*hd (its tail unused) on the
+    row-blocked layout path, with a missing q gradient.  (Merged rows are
+    exactly H*hd wide: the reference's head_merge_fwd writes H*hd columns.)"""
+    B, T, H, hd, K, rep = 2, 5, 4, 16, 2, 2
+    C = 80
+    x = rnd(130, B, T, C + 2 * K * hd)
+    outs = [D.empty((B, H, T, hd)) for _ in range(3)]
+    ncmhip.call("qkv_split_fwd", up(x), *outs, B, T, C, H, hd, K, rep)
+    for g, r in zip(outs, O.qkv_split(x, B, T, C, H, hd, K, rep)):
+        assert bits_equal(g.numpy(), r)
+    gk, gv = rnd(131, B, H, T, hd), rnd(132, B, H, T, hd)
+    dx0 = rnd(133, B, T, C + 2 * K * hd)
+    dx = up(dx0)
+    ncmhip.call("qkv_split_bwd", None, up(gk), up(gv), dx, B, T, C, H, hd, K, rep)
+    assert bits_equal(dx.numpy(), O.qkv_split_bwd(None, gk, gv, B, T, C, H, hd, K, rep, dx0))
 
 
 # ---------------------------------------------------------------- the tape's recomputing SDPA backward

@@ -171,6 +171,36 @@ colsum_final(const double *__restrict__ part, int chunks, int N, float *db) {
     db[col] += (float)s;
 }
 
+// Stage 2 over many chunks: a workgroup of 16 waves per 64 columns, wave v
+// adds chunks v, v + 16, ... in order with 16 loads in flight per pass, then
+// wave 0 adds the 16 wave sums in wave order (colsum_final walks every chunk
+// of a column in one thread, one round trip per 16 chunks).
+extern "C" __global__ void __launch_bounds__(1024)
+colsum_final_w(const double *__restrict__ part, int chunks, int N, float *db) {
+    __shared__ double red[16][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = blockIdx.x * 64 + lane;
+    double s = 0.0;
+    if (col < N) {
+        for (int k0 = wave; k0 < chunks; k0 += 256) {
+            double v[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) v[u] = part[(int64_t)min(k0 + 16 * u, chunks - 1) * N + col];
+#pragma unroll
+            for (int u = 0; u < 16; ++u)
+                if (k0 + 16 * u < chunks) s += v[u];
+        }
+    }
+    red[wave][lane] = s;
+    __syncthreads();
+    if (wave == 0 && col < N) {
+        double t = red[0][lane];
+#pragma unroll
+        for (int w = 1; w < 16; ++w) t += red[w][lane];
+        db[col] += (float)t;
+    }
+}
+
 // ---- small-batch backward (batch <= 8 rows of dy) ----
 // dW[n,k] += sum_r dy[r,n] x[r,k]: the reference's per-output fp64 sum over
 // r ascending, rounded to float and added through a zeroed temporary

@@ -406,7 +406,10 @@ void linear_bwd(const float *x, const float *W, const float *dy, float *dx, floa
                              (unsigned)chunks, 1, 256, a1))
             return;
         void *a2[] = {&part, &chunks, &M, &db};
-        ncm_launch_named("colsum_final", (unsigned)((M + 255) / 256), 1, 1, 256, a2);
+        if (chunks > 16)   /* many chunks: 16 waves per 64 columns */
+            ncm_launch_named("colsum_final_w", (unsigned)((M + 63) / 64), 1, 1, 1024, a2);
+        else
+            ncm_launch_named("colsum_final", (unsigned)((M + 255) / 256), 1, 1, 256, a2);
     }
 }
 

@@ -608,18 +608,27 @@ sdpa_decode_partial(const float *__restrict__ q, const float *__restrict__ kc, c
     const int k0 = chunk * DEC_CH;
     if (k0 >= Tkv) return;    // chunk past the current length (grid sized for n_ctx)
     const int nk = min(DEC_CH, Tkv - k0);
-    for (int i = tid; i < rep * 16; i += 256) *(f4 *)(sQ + 4 * i) = *(const f4 *)(q + (int64_t)h0 * 64 + 4 * i);
+    // every load issued before the first LDS store, unconditionally (clamped
+    // rows, zeroed afterwards): one memory round trip instead of one per row
+    // group (a guarded load is a branch with a wait after it)
+    const int nq = rep * 16;   // float4 of the group's queries (rep <= 16)
+    const f4 qv = *(const f4 *)(q + (int64_t)h0 * 64 + 4 * min(tid, nq - 1));
     const float *kb = kc + ((int64_t)kvh * ld + k0) * 64, *vb = vc + ((int64_t)kvh * ld + k0) * 64;
+    f4 kr[4], vr[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int f = tid + 256 * j, r = min(f >> 4, nk - 1), c = (f & 15) * 4;
+        kr[j] = *(const f4 *)(kb + r * 64 + c);
+        vr[j] = *(const f4 *)(vb + r * 64 + c);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (tid < nq) *(f4 *)(sQ + 4 * tid) = qv;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int f = tid + 256 * j, r = f >> 4, c = (f & 15) * 4;
-        f4 kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
-        if (r < nk) {
-            kv = *(const f4 *)(kb + r * 64 + c);
-            vv = *(const f4 *)(vb + r * 64 + c);
-        }
-        *(f4 *)(sK + r * DEC_LD + c) = kv;
-        *(f4 *)(sV + r * 64 + c) = vv;
+        const f4 z = {0.f, 0.f, 0.f, 0.f};
+        *(f4 *)(sK + r * DEC_LD + c) = r < nk ? kr[j] : z;
+        *(f4 *)(sV + r * 64 + c) = r < nk ? vr[j] : z;
     }
     __syncthreads();
     // scores: wave w, queries j = w, w+4, ... (lane = key)
@@ -664,6 +673,27 @@ sdpa_decode_combine(const float *__restrict__ part_o, const float *__restrict__ 
     const int h = blockIdx.x, lane = threadIdx.x;
     const int nchunk = (*posp + DEC_CH) / DEC_CH;
     const float *ml = part_ml + (int64_t)h * stride * 2, *po = part_o + (int64_t)h * stride * 64;
+    if (nchunk <= 64) {
+        // one round trip: every chunk's (max, sum) and output loaded before
+        // the first use (clamped index, weight 0 past the last chunk); the
+        // same operations in the same order as the loop below
+        const int cl = min(lane, nchunk - 1);
+        const float mc = ml[2 * cl], lcv = ml[2 * cl + 1];
+        float pv[64];
+#pragma unroll
+        for (int t = 0; t < 64; ++t) pv[t] = po[(int64_t)min(t, nchunk - 1) * 64 + lane];
+        float m = lane < nchunk ? mc : -INFINITY;
+#pragma unroll
+        for (int s = 32; s > 0; s >>= 1) m = fmaxf(m, __shfl_xor(m, s, 64));
+        const float w = (lane < nchunk && mc != -INFINITY) ? __expf(mc - m) : 0.f;
+        float l = lane < nchunk ? lcv * w : 0.f, o = 0.f;
+#pragma unroll
+        for (int t = 0; t < 64; ++t) o += pv[t] * __shfl(w, t, 64);
+#pragma unroll
+        for (int s = 32; s > 0; s >>= 1) l += __shfl_xor(l, s, 64);
+        out[(int64_t)h * 64 + lane] = o / l;
+        return;
+    }
     float m = -INFINITY;
     for (int c = lane; c < nchunk; c += 64) m = fmaxf(m, ml[2 * c]);
 #pragma unroll
@@ -696,8 +726,9 @@ sdpa_decode_combine(const float *__restrict__ part_o, const float *__restrict__ 
 // waves), the input staged once per workgroup in LDS -- optionally RMS-
 // normalised on the way (rmsnorm_fwd's arithmetic: fp64 sum of squares,
 // s = (float)(1/sqrt(ms/K + 1e-6)), xn = (x*s)*nw).  Each wave issues the
-// loads of its first PRE float4 per lane and row before the input prologue,
-// so the weight stream overlaps the staging.
+// small loads and the input first, then its first PRE float4 per lane and
+// row, so the normalisation and staging run while the weight stream is in
+// flight.
 //   mode 0: rows index the concatenation of up to three matrices; res (one
 //           matrix) is added last.
 //   mode 1: row n pairs W0 and W1: y0[n] = silu(W0 x + b0)[n] * (W1 x + b1)[n]
@@ -721,6 +752,14 @@ struct DecGemvArgs {
     int ld;
 };
 
+
+// Member m of a 3-pointer argument array, by selects: indexing the array with
+// a run-time m makes the compiler read the pointer from the argument block
+// in memory, and that load queues behind the weight loads already in flight.
+template <typename T>
+__device__ __forceinline__ T sel3(const T (&a)[3], int m) {
+    return m == 0 ? a[0] : (m == 1 ? a[1] : a[2]);
+}
 
 // row (in the concatenated row space) of the i-th dot product of this wave
 __device__ __forceinline__ void dec_rows(const DecGemvArgs &p, int unit, int i, int &m, int &row) {
@@ -767,26 +806,76 @@ __device__ __forceinline__ void dec_gemv_body(const DecGemvArgs &p) {
             if (p.mode == 1) row = min(u0 + r, units - 1);
             um[r][i] = m;
             urow[r][i] = row;
-            wr[r][i] = p.W[m] + (int64_t)row * K;
+            wr[r][i] = sel3(p.W, m) + (int64_t)row * K;
         }
+    // Load order.  A wave's loads complete in issue order, so what is needed
+    // first is issued first: the position, the epilogue's bias and residual
+    // values and the input, then the weight rows (the bulk), then the RoPE
+    // table values (their address needs the position).  The input is
+    // normalised and staged while the weight rows stream in, and the
+    // epilogue reads nothing from memory.
+    // Every load is unconditional (a clamped index, or a valid stand-in for
+    // an absent operand, with the value selected afterwards): a load under a
+    // branch makes the compiler wait for all loads in flight where the
+    // branches join, which would serialise the stream.
+    const int *pp = p.mode == 2 ? p.posp : (const int *)p.x;
+    const int pos = p.mode == 2 ? *pp : 0;
+    float eb[RW][DOTS], er[RW];
+    bool hb[RW][DOTS];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+#pragma unroll
+        for (int i = 0; i < DOTS; ++i) {
+            const float *bm = sel3(p.b, um[r][i]);
+            hb[r][i] = bm != nullptr;
+            eb[r][i] = *(bm ? bm + urow[r][i] : p.x);
+        }
+        const bool hr = p.mode == 0 && p.res;
+        er[r] = *(hr ? p.res + urow[r][0] : p.x);
+    }
+    // (raw values here; lanes past the row end hold a duplicate of its last
+    // group and are zeroed where the values are used, after the waits)
+    f4 xv4[XPT], nv4[XPT];
+    const float *nwp = p.nw ? p.nw : p.x;
+#pragma unroll
+    for (int e = 0; e < XPT; ++e) {
+        const int cc = min(tid + 256 * e, K4 - 1);
+        xv4[e] = *(const f4 *)(p.x + 4 * cc);
+        if (p.nw) nv4[e] = *(const f4 *)(nwp + 4 * cc);
+    }
+    __builtin_amdgcn_sched_barrier(0);   // keep the issue order: the small loads first
     f4 pw[RW][DOTS][PRE];
 #pragma unroll
     for (int r = 0; r < RW; ++r)
 #pragma unroll
         for (int i = 0; i < DOTS; ++i)
 #pragma unroll
-            for (int e = 0; e < PRE; ++e) {
-                const int c = lane + 64 * e;
-                pw[r][i][e] = c < K4 ? __builtin_nontemporal_load((const f4 *)wr[r][i] + c) : f4{0.f, 0.f, 0.f, 0.f};
-            }
-    // input: all of this thread's float4 loads issued together (K <= 1024 XPT)
-    f4 xv4[XPT], nv4[XPT];
+            for (int e = 0; e < PRE; ++e)
+                pw[r][i][e] = __builtin_nontemporal_load((const f4 *)wr[r][i] + min(lane + 64 * e, K4 - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    // RoPE: the rotation pair (d, d + 32) of a q or k head (d = row & 31).
+    // Loaded unconditionally, from the input row when there is no table (a
+    // branch around the loads makes the compiler wait for every load in
+    // flight where the branches join).
+    float rc0[RW], rs0[RW], rc1[RW], rs1[RW];
+    {
+        const bool rope = p.mode == 2;
+        const float *co = rope ? p.cos_t + (int64_t)pos * 64 : p.x;
+        const float *si = rope ? p.sin_t + (int64_t)pos * 64 : p.x;
 #pragma unroll
-    for (int e = 0; e < XPT; ++e) {
-        const int c = tid + 256 * e;
-        xv4[e] = c < K4 ? *(const f4 *)(p.x + 4 * c) : f4{0.f, 0.f, 0.f, 0.f};
-        nv4[e] = (p.nw && c < K4) ? *(const f4 *)(p.nw + 4 * c) : f4{1.f, 1.f, 1.f, 1.f};
+        for (int r = 0; r < RW; ++r) {
+            const int d = urow[r][0] & 31;
+            const int d0 = rope ? d : min(d, K - 1), d1 = rope ? d + 32 : min(d + 32, K - 1);
+            rc0[r] = co[d0];
+            rs0[r] = si[d0];
+            rc1[r] = co[d1];
+            rs1[r] = si[d1];
+        }
     }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int e = 0; e < XPT; ++e)
+        if (tid + 256 * e >= K4) xv4[e] = f4{0.f, 0.f, 0.f, 0.f};
     if (p.nw) {
         double ss = 0.0;
 #pragma unroll
@@ -817,7 +906,7 @@ __device__ __forceinline__ void dec_gemv_body(const DecGemvArgs &p) {
 #pragma unroll
     for (int e = 0; e < PRE; ++e) {
         const int c = lane + 64 * e;
-        if (c < K4) {
+        if (c < K4) {   // (lanes past the row end loaded a duplicate: skipped here)
             const f4 xv = *(const f4 *)(xs + 4 * c);
 #pragma unroll
             for (int r = 0; r < RW; ++r)
@@ -845,26 +934,24 @@ __device__ __forceinline__ void dec_gemv_body(const DecGemvArgs &p) {
         if (lane != 0 || unit >= units) continue;
         if (p.mode == 0) {
             const int m = um[r][0], row = urow[r][0];
-            float v = p.b[m] ? a0 + p.b[m][row] : a0;
-            if (p.res) v = p.res[row] + v;
-            p.y[m][row] = v;
+            float v = hb[r][0] ? a0 + eb[r][0] : a0;
+            if (p.res) v = er[r] + v;
+            sel3(p.y, m)[row] = v;
         } else if (p.mode == 1) {
-            const float g = p.b[0] ? a0 + p.b[0][unit] : a0;
-            const float u = p.b[1] ? a1 + p.b[1][unit] : a1;
+            const float g = hb[r][0] ? a0 + eb[r][0] : a0;
+            const float u = hb[r][DOTS - 1] ? a1 + eb[r][DOTS - 1] : a1;
             p.y[0][unit] = ncm_act(g, ACT_SILU) * u;
         } else {
-            const int pos = *p.posp;
-            const int m0 = um[r][0], row0 = urow[r][0], m1 = um[r][DOTS - 1], row1 = urow[r][DOTS - 1];
-            const float v0 = p.b[m0] ? a0 + p.b[m0][row0] : a0;
-            const float v1 = p.b[m1] ? a1 + p.b[m1][row1] : a1;
+            const int m0 = um[r][0], row0 = urow[r][0], row1 = urow[r][DOTS - 1];
+            const float v0 = hb[r][0] ? a0 + eb[r][0] : a0;
+            const float v1 = hb[r][DOTS - 1] ? a1 + eb[r][DOTS - 1] : a1;
             if (m0 == 2) {      // v rows: plain append
                 p.vc[((int64_t)(row0 >> 6) * p.ld + pos) * 64 + (row0 & 63)] = v0;
                 p.vc[((int64_t)(row1 >> 6) * p.ld + pos) * 64 + (row1 & 63)] = v1;
             } else {
                 const int d = row0 & 63;          // 0..31; row1 = row0 + 32
-                const float *co = p.cos_t + (int64_t)pos * 64, *si = p.sin_t + (int64_t)pos * 64;
-                const float y0 = v0 * co[d] + (-v1) * si[d];
-                const float y1 = v1 * co[d + 32] + v0 * si[d + 32];
+                const float y0 = v0 * rc0[r] + (-v1) * rs0[r];
+                const float y1 = v1 * rc1[r] + v0 * rs1[r];
                 float *dst = m0 == 0 ? p.y[0] + (row0 & ~63)
                                      : p.kc + ((int64_t)(row0 >> 6) * p.ld + pos) * 64;
                 dst[d] = y0;

@@ -503,17 +503,45 @@ struct GSlab {
     }
 };
 
-template <int ACT, int EPI>
-__device__ __forceinline__ void g_out(const GemmArgs &p, int i, int j, float v) {
-    if (i >= p.Mo || j >= p.No) return;
-    float *c = p.C + (int64_t)i * p.ldc + j;
-    if (EPI == EPI_ACCUM) {
-        *c = *c + v;
-    } else {
-        if (p.bias) v += p.bias[j];
-        v = ncm_act(v, ACT);
-        if (p.res) v = p.res_mul ? v * p.res[(int64_t)i * p.ldc + j] : p.res[(int64_t)i * p.ldc + j] + v;
-        *c = v;
+// The epilogue of N output elements (ii[n], jj[n], v[n]) of one thread, in two
+// phases: every operand the elements need -- the old C of an accumulation,
+// the bias, the residual -- is loaded first, unconditionally, from clamped
+// coordinates (an absent bias reads C[0] in its place, an absent residual
+// the bias address, so neither costs a stream); then the in-bounds elements
+// are computed and stored: C += v (ACCUM), or C = res + act(v + bias) /
+// act(v + bias) * res (STORE).  One guarded element at a time made each
+// element a memory round trip (load, wait, store).
+template <int N, int ACT, int EPI>
+__device__ __forceinline__ void g_out_n(const GemmArgs &p, const int (&ii)[N], const int (&jj)[N],
+                                        const float (&v)[N]) {
+#pragma clang fp contract(off)
+    const bool hb = p.bias != nullptr, hr = p.res != nullptr;
+    float o1[N], o2[N];
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+        const int i = min(ii[n], p.Mo - 1), j = min(jj[n], p.No - 1);
+        const int64_t e = (int64_t)i * p.ldc + j;
+        if (EPI == EPI_ACCUM) {
+            o1[n] = p.C[e];
+        } else {
+            const float *bq = hb ? p.bias + j : p.C;
+            o1[n] = *bq;
+            o2[n] = *(hr ? p.res + e : bq);
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+        if (ii[n] >= p.Mo || jj[n] >= p.No) continue;
+        float *c = p.C + (int64_t)ii[n] * p.ldc + jj[n];
+        float x = v[n];
+        if (EPI == EPI_ACCUM) {
+            *c = o1[n] + x;
+        } else {
+            if (hb) x += o1[n];
+            x = ncm_act(x, ACT);
+            if (hr) x = p.res_mul ? x * o2[n] : o2[n] + x;
+            *c = x;
+        }
     }
 }
 
@@ -527,16 +555,23 @@ __device__ __forceinline__ void g_epilogue_act(const GemmArgs &p, const f4 (&tot
                                                int tid) {
     const int lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
     const int li = lane & 15, lg = lane >> 4;
+    constexpr int N = (BM / 32) * (BN / 32) * 4;
+    int ii[N], jj[N];
+    float v[N];
 #pragma unroll
     for (int a = 0; a < BM / 32; ++a)
 #pragma unroll
         for (int b = 0; b < BN / 32; ++b)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
+                const int n = (a * (BN / 32) + b) * 4 + r;
                 const int row = IA ? wm * 32 + 2 * (4 * lg + r) + a : wm * (BM / 2) + a * 16 + 4 * lg + r;
                 const int col = IB ? wn * 32 + 2 * li + b : wn * (BN / 2) + b * 16 + li;
-                g_out<ACT, EPI>(p, i0 + row, j0 + col, tot[a][b][r]);
+                ii[n] = i0 + row;
+                jj[n] = j0 + col;
+                v[n] = tot[a][b][r];
             }
+    g_out_n<N, ACT, EPI>(p, ii, jj, v);
 }
 
 template <int BM, int BN, int EPI, bool IA = false, bool IB = false>
@@ -689,12 +724,17 @@ __device__ __forceinline__ void g_epilogue_blk_act(const GemmArgs &p, const f4 &
                                                    int tid) {
     const int lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
     const int li = lane & 15, lg = lane >> 4;
+    int ii[4], jj[4];
+    float vv[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int row = IA ? wm * 32 + 2 * (4 * lg + r) + a : wm * 32 + a * 16 + 4 * lg + r;
         const int col = IB ? wn * 32 + 2 * li + b : wn * 32 + b * 16 + li;
-        g_out<ACT, EPI>(p, i0 + row, j0 + col, v[r]);
+        ii[r] = i0 + row;
+        jj[r] = j0 + col;
+        vv[r] = v[r];
     }
+    g_out_n<4, ACT, EPI>(p, ii, jj, vv);
 }
 
 // Sum of the segment partials of one MFMA block of a split 64x64 tile
@@ -710,14 +750,14 @@ __device__ __forceinline__ void gemm_tile_fixup_body(const GemmArgs &p) {
     int tm, tn;
     tile_rc<8>(p.dp_tiles + tail, p.tiles_m, p.tiles_n, tm, tn);
     const float *first = p.ws + (int64_t)tail * p.segs * 4096 + (blk * GEMM_NT + tid) * 4;
+    // unconditional loads (a segment index clamped to the last one, the extra
+    // values not added): a guarded load is a branch with a wait after it
     f4 part[FIXUP_MAX_SEGS];
 #pragma unroll
-    for (int s = 0; s < FIXUP_MAX_SEGS; ++s)
-        if (s < p.segs) part[s] = *(const f4 *)(first + (int64_t)s * 4096);
+    for (int s = 0; s < FIXUP_MAX_SEGS; ++s) part[s] = *(const f4 *)(first + (int64_t)min(s, p.segs - 1) * 4096);
     f4 tot = part[0];
 #pragma unroll
-    for (int s = 1; s < FIXUP_MAX_SEGS; ++s)
-        if (s < p.segs) tot += part[s];
+    for (int s = 1; s < FIXUP_MAX_SEGS; ++s) tot = s < p.segs ? tot + part[s] : tot;
     const int a = blk >> 1, b = blk & 1, i0 = tm * 64, j0 = tn * 64;
     if (EPI == EPI_ACCUM) { g_epilogue_blk_act<EPI, ACT_NONE, IA, IB>(p, tot, a, b, i0, j0, tid); return; }
     switch (p.act) {
@@ -735,6 +775,16 @@ __device__ __forceinline__ void gemm_tile_fixup_body(const GemmArgs &p) {
 template <int ACT>
 __device__ __forceinline__ void g_gated_out(const GemmArgs &p, const f4 (&g)[2][2], const f4 (&u)[2][2], int r0,
                                             int j0, int li, int lg) {
+    // the biases of the thread's 4 columns loaded first (a stand-in address
+    // when absent), then the in-bounds elements computed and stored
+    const bool hb = p.bias != nullptr, hb2 = p.bias2 != nullptr;
+    float bg[2], bu[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        const int j = min(j0 + b * 16 + li, p.No - 1);
+        bg[b] = *(hb ? p.bias + j : p.C);
+        bu[b] = *(hb2 ? p.bias2 + j : p.C);
+    }
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
@@ -744,9 +794,9 @@ __device__ __forceinline__ void g_gated_out(const GemmArgs &p, const f4 (&g)[2][
                 const int i = r0 + a * 16 + 4 * lg + r, j = j0 + b * 16 + li;
                 if (i >= p.Mo || j >= p.No) continue;
                 float vg = g[a][b][r], vu = u[a][b][r];
-                if (p.bias) vg += p.bias[j];
+                if (hb) vg += bg[b];
                 vg = ncm_act(vg, ACT);
-                if (p.bias2) vu += p.bias2[j];
+                if (hb2) vu += bu[b];
                 p.C[(int64_t)i * p.ldc + j] = vg * vu;
             }
 }

@@ -142,15 +142,24 @@ float ncm_gpt2_train_step(NcmTape *tp, const NcmGpt2Config *c, float *const *P, 
         ncm_t_ce(tp, logits, xout, NULL, loss, NULL, R, c->vocab, 1.0);
         NcmPMap pm = {(float **)P, (float **)G, sizes, n};
         ncm_tape_backward(tp, &pm);
-        double gnorm = grad_clip_global(G, sizes, n, 1.0);
-        if (gnorm_out) *gnorm_out = gnorm;
-        mem_d2h(&lh, loss, sizeof(float));
         const double b1 = 0.9, b2 = 0.95, eps = 1e-8;
         const double lr = base_lr * sched_cosine_warmup(step, warmup, total);
         const double b1t = 1.0 - pow(b1, (double)step), b2t = 1.0 - pow(b2, (double)step);
-        for (int i = 0; i < n; i++) {
-            /* the update also clears the gradient for the next step */
-            ncm_adamw_update_clear(P[i], G[i], M[i], Vm[i], sizes[i], lr, b1, b2, b1t, b2t, eps, wd);
+        const double *g2_dev = NULL;
+        if (ncm_clip_adamw_multi(P, G, M, Vm, sizes, n, 1.0, lr, b1, b2, b1t, b2t, eps, wd, 1, &g2_dev) == 0) {
+            /* clip + update in three launches; loss and norm read back once, at the end */
+            double g2 = 0.0;
+            mem_d2h(&lh, loss, sizeof(float));
+            mem_d2h(&g2, g2_dev, sizeof(double));
+            if (gnorm_out) *gnorm_out = sqrt(g2);
+        } else if (!ncm_ready()) {
+            double gnorm = grad_clip_global(G, sizes, n, 1.0);
+            if (gnorm_out) *gnorm_out = gnorm;
+            mem_d2h(&lh, loss, sizeof(float));
+            for (int i = 0; i < n; i++) {
+                /* the update also clears the gradient for the next step */
+                ncm_adamw_update_clear(P[i], G[i], M[i], Vm[i], sizes[i], lr, b1, b2, b1t, b2t, eps, wd);
+            }
         }
     }
     free(sizes);

@@ -49,6 +49,14 @@ size_t ncm_sample_ws_bytes(int V);
  * step; the gradient is consumed and the next step accumulates from zero). */
 void ncm_adamw_update_clear(float *p, float *g, float *m, float *v, int64_t n, double lr, double b1, double b2,
                             double b1t, double b2t, double eps, double wd);
+/* grad_clip_global(G, sizes, count, max_norm) followed by
+ * ncm_adamw_update_clear (clear_g) or adamw_update on every tensor, in three
+ * launches with no host synchronisation; *g2_dev gets the device address of
+ * the gradients' sum of squares before clipping.  Returns -1 (nothing
+ * launched) for lists this path does not take (over 2048 tensors). */
+int ncm_clip_adamw_multi(float *const *P, float *const *G, float *const *M, float *const *V, const int64_t *sizes,
+                         int count, double max_norm, double lr, double b1, double b2, double b1t, double b2t,
+                         double eps, double wd, int clear_g, const double **g2_dev);
 /* conv1d_fwd (kernels.c:546-566, bit-exact) on [B][T][D] rows with D input
  * and D output channels: y [B][To][D], To = (T + 2 pad - K) / stride + 1;
  * W [D][D][K]; launches only. */

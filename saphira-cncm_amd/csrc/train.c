@@ -11,6 +11,7 @@
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
+#include <string.h>
 
 #define NORM_ROWS 128
 #define NBF_ROWS 32   /* rows per workgroup of the fused norm backward */
@@ -390,6 +391,123 @@ double grad_clip_global(float *const *grads, const int64_t *sizes, int count, do
         }
     }
     return gnorm;
+}
+
+/* ---- clip + AdamW over a tensor list in three launches (multi-tensor) ----
+ * grad_clip_global followed by ncm_adamw_update_clear on every tensor, with
+ * no host synchronisation in between: sumsq_multi (the same per-tensor
+ * partials as sumsq_partial), clip_final (the norm and the clip scale on the
+ * device) and adamw_multi (the gradient times the scale, the adamw_k update,
+ * the gradient cleared).  The tensor tables live on the device and are
+ * rebuilt only when the list (pointers, sizes, multipliers) changes. */
+typedef struct {   /* must match struct MtTensor in train.hip */
+    float *p, *g, *m, *v;
+    int64_t n;
+    double lr_mul;
+} MtTensor;
+#define MT_MAX 2048       /* tensors per list (the kernels' LDS table) */
+#define MT_CHUNK 16384    /* elements per adamw_multi workgroup */
+
+static struct {
+    int count, nparts, nchunks;
+    MtTensor *tt;         /* host copy of the device table */
+    char *dev;            /* tt | boff | chunks | partials | g2 | scale */
+    size_t bytes;
+} g_mt;
+
+static size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+/* Device tables for the list; returns 0, or -1 when the list does not fit
+ * (the caller then takes the per-tensor path). */
+static int mt_prepare(float *const *P, float *const *G, float *const *M, float *const *V, const int64_t *sizes,
+                      const double *lr_mul, int count) {
+    if (count < 1 || count > MT_MAX) return -1;
+    MtTensor *tt = (MtTensor *)malloc((size_t)count * sizeof(MtTensor));
+    int *boff = (int *)malloc((size_t)(count + 1) * sizeof(int));
+    if (!tt || !boff) { free(tt); free(boff); return -1; }
+    int64_t nparts = 0, nchunks = 0;
+    for (int i = 0; i < count; i++) {
+        tt[i].p = P[i]; tt[i].g = G[i]; tt[i].m = M[i]; tt[i].v = V[i];
+        tt[i].n = sizes[i];
+        tt[i].lr_mul = lr_mul ? lr_mul[i] : 1.0;
+        boff[i] = (int)nparts;
+        if (sizes[i] > 0) {
+            const int64_t b = (sizes[i] + 255) / 256;
+            nparts += b < CLIP_MAX_BLOCKS ? b : CLIP_MAX_BLOCKS;
+            nchunks += (sizes[i] + MT_CHUNK - 1) / MT_CHUNK;
+        }
+    }
+    boff[count] = (int)nparts;
+    if (nparts == 0 || nparts > INT_MAX / 2 || nchunks > INT_MAX / 2) { free(tt); free(boff); return -1; }
+    if (g_mt.dev && g_mt.count == count && memcmp(g_mt.tt, tt, (size_t)count * sizeof(MtTensor)) == 0) {
+        free(tt);
+        free(boff);
+        return 0;
+    }
+    const size_t b_tt = al256((size_t)count * sizeof(MtTensor)), b_bo = al256((size_t)(count + 1) * sizeof(int)),
+                 b_ch = al256((size_t)nchunks * 2 * sizeof(int)), b_pa = al256((size_t)nparts * sizeof(double));
+    const size_t bytes = b_tt + b_bo + b_ch + b_pa + 256 + 256;
+    int *ch = (int *)malloc((size_t)nchunks * 2 * sizeof(int));
+    if (!ch) { free(tt); free(boff); return -1; }
+    int64_t c = 0;
+    for (int i = 0; i < count; i++)
+        for (int64_t k = 0; sizes[i] > 0 && k < (sizes[i] + MT_CHUNK - 1) / MT_CHUNK; k++) {
+            ch[2 * c] = i;
+            ch[2 * c + 1] = (int)k;
+            c++;
+        }
+    if (g_mt.bytes < bytes) {
+        if (g_mt.dev) { ncm_hip_sync(); ncm_hip_free(g_mt.dev); }
+        g_mt.dev = (char *)ncm_hip_malloc(bytes);
+        g_mt.bytes = g_mt.dev ? bytes : 0;
+    }
+    int rc = -1;
+    if (g_mt.dev) {
+        mem_h2d(g_mt.dev, tt, (size_t)count * sizeof(MtTensor));
+        mem_h2d(g_mt.dev + b_tt, boff, (size_t)(count + 1) * sizeof(int));
+        mem_h2d(g_mt.dev + b_tt + b_bo, ch, (size_t)nchunks * 2 * sizeof(int));
+        free(g_mt.tt);
+        g_mt.tt = tt;
+        tt = NULL;
+        g_mt.count = count;
+        g_mt.nparts = (int)nparts;
+        g_mt.nchunks = (int)nchunks;
+        rc = ncm_ready() ? -1 : 0;
+    }
+    free(tt);
+    free(boff);
+    free(ch);
+    return rc;
+}
+
+/* Launches the clip and the update; *g2_dev gets the device address of the
+ * sum of squares of the gradients (before clipping). */
+static int mt_clip_adamw(double max_norm, double lr, double b1, double b2, double b1t, double b2t, double eps,
+                         double wd, int clear_g, const double **g2_dev) {
+    const int count = g_mt.count;
+    const size_t b_tt = al256((size_t)count * sizeof(MtTensor)), b_bo = al256((size_t)(count + 1) * sizeof(int)),
+                 b_ch = al256((size_t)g_mt.nchunks * 2 * sizeof(int)), b_pa = al256((size_t)g_mt.nparts * sizeof(double));
+    const MtTensor *tt = (const MtTensor *)g_mt.dev;
+    const int *boff = (const int *)(g_mt.dev + b_tt), *chs = (const int *)(g_mt.dev + b_tt + b_bo);
+    double *part = (double *)(g_mt.dev + b_tt + b_bo + b_ch), *g2 = (double *)(g_mt.dev + b_tt + b_bo + b_ch + b_pa);
+    float *scale = (float *)(g_mt.dev + b_tt + b_bo + b_ch + b_pa + 256);
+    int np = g_mt.nparts, len = MT_CHUNK;
+    void *a1[] = {&tt, &boff, (void *)&count, &part};
+    if (ncm_launch_named("sumsq_multi", (unsigned)np, 1, 1, 256, a1)) return -1;
+    void *a2[] = {&part, &np, &g2, &scale, &max_norm};
+    if (ncm_launch_named("clip_final", 1, 1, 1, 64, a2)) return -1;
+    void *a3[] = {&tt, &chs, &len, &scale, &lr, &b1, &b2, &b1t, &b2t, &eps, &wd, &clear_g};
+    if (ncm_launch_named("adamw_multi", (unsigned)g_mt.nchunks, 1, 1, 256, a3)) return -1;
+    *g2_dev = g2;
+    return 0;
+}
+
+int ncm_clip_adamw_multi(float *const *P, float *const *G, float *const *M, float *const *V, const int64_t *sizes,
+                         int count, double max_norm, double lr, double b1, double b2, double b1t, double b2t,
+                         double eps, double wd, int clear_g, const double **g2_dev) {
+    if (ncm_ready()) return -1;
+    if (mt_prepare(P, G, M, V, sizes, NULL, count)) return -1;
+    return mt_clip_adamw(max_norm, lr, b1, b2, b1t, b2t, eps, wd, clear_g, g2_dev);
 }
 
 /* ---- remaining tape backward cases ---- */

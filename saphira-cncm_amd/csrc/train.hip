@@ -501,6 +501,120 @@ sumsq_final(const double *__restrict__ part, int count, double *__restrict__ out
     if (threadIdx.x == 0) out[0] = s;
 }
 
+// ---- multi-tensor forms (one launch over a list of tensors) ----
+// A tensor of the list: parameter, gradient, moments, size, learning-rate
+// multiplier.  Must match struct MtTensor in train.c.
+struct MtTensor {
+    float *p, *g, *m, *v;
+    int64_t n;
+    double lr_mul;
+};
+
+// sumsq_partial over every tensor of the list in one launch, with the same
+// partials: tensor i owns blocks [boff[i], boff[i+1]) (min(ceil(n/256), 1024)
+// of them), and its block j sums elements j*256 + t, stepping by its own
+// block count * 256, as sumsq_partial does with that grid.  The block's tensor
+// is found by a binary search over boff staged in LDS (count <= MT_MAX).
+#define MT_MAX 2048
+extern "C" __global__ void __launch_bounds__(256)
+sumsq_multi(const MtTensor *__restrict__ tt, const int *__restrict__ boff, int count, double *__restrict__ part) {
+    __shared__ int so[MT_MAX + 1];
+    __shared__ double ws[4];
+    for (int i = threadIdx.x; i <= count; i += 256) so[i] = boff[i];
+    __syncthreads();
+    const int b = blockIdx.x;
+    int lo = 0, hi = count - 1;   // last i with so[i] <= b
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (so[mid] <= b) lo = mid;
+        else hi = mid - 1;
+    }
+    const int64_t nb = so[lo + 1] - so[lo], j = b - so[lo], n = tt[lo].n;
+    const float *g = tt[lo].g;
+    const int64_t st = nb * 256;
+    double s = 0.0;
+    // four loads in flight per pass (clamped index), added in element order
+    for (int64_t i0 = j * 256 + threadIdx.x; i0 < n; i0 += 4 * st) {
+        float x[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) x[u] = g[min(i0 + u * st, n - 1)];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (i0 + u * st < n) s += (double)x[u] * (double)x[u];
+    }
+    s = wave_sum_d(s);
+    if ((threadIdx.x & 63) == 0) ws[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) part[b] = ((ws[0] + ws[1]) + ws[2]) + ws[3];
+}
+
+// sumsq_final, then the clip decision on the device: out[0] = sum of
+// squares, scale[0] = (float)(1 / norm) when norm > max_norm, else 1 (a
+// multiplication by 1.0f leaves every float as it is).
+extern "C" __global__ void __launch_bounds__(64)
+clip_final(const double *__restrict__ part, int count, double *__restrict__ out, float *__restrict__ scale,
+           double max_norm) {
+    double s = 0.0;
+    // lane l adds partials l, l + 64, ... in order, 16 loads in flight per pass
+    for (int i0 = threadIdx.x; i0 < count; i0 += 64 * 16) {
+        double x[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) x[u] = part[min(i0 + 64 * u, count - 1)];
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+            if (i0 + 64 * u < count) s += x[u];
+    }
+    s = wave_sum_d(s);
+    if (threadIdx.x == 0) {
+        out[0] = s;
+        const double gn = sqrt(s);
+        scale[0] = gn > max_norm ? (float)(1.0 / gn) : 1.0f;
+    }
+}
+
+// adamw_k over every tensor of the list in one launch: block b updates
+// elements [start, start + len) of tensor ch[b].x (start = ch[b].y * len),
+// reading the gradient times *scale (the in-place clip of the gradient
+// followed by adamw_k, without writing the scaled gradient back) and, with
+// clear_g, leaving the gradient zero.  lr of tensor i = lr * lr_mul.
+extern "C" __global__ void __launch_bounds__(256)
+adamw_multi(const MtTensor *__restrict__ tt, const int2 *__restrict__ ch, int len, const float *__restrict__ scale,
+            double lr0, double b1, double b2, double b1t, double b2t, double eps, double wd, int clear_g) {
+#pragma clang fp contract(off)
+    const int2 c = ch[blockIdx.x];
+    const MtTensor t = tt[c.x];
+    const int64_t start = (int64_t)c.y * len, end = min(t.n, start + len);
+    const float s = *scale;
+    const double lr = lr0 * t.lr_mul;
+    // four elements per pass, their loads issued together (clamped index)
+    for (int64_t k0 = start + threadIdx.x; k0 < end; k0 += 1024) {
+        float g4[4], p4[4], m4[4], v4[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t k = min(k0 + 256 * u, end - 1);
+            g4[u] = t.g[k];
+            p4[u] = t.p[k];
+            m4[u] = t.m[k];
+            v4[u] = t.v[k];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t k = k0 + 256 * u;
+            if (k >= end) continue;
+            const float gk = g4[u] * s;
+            if (clear_g) t.g[k] = 0.0f;
+            float pk = p4[u];
+            pk = pk - (float)(lr * wd * (double)pk);
+            const float mk = (float)(b1 * (double)m4[u] + (1.0 - b1) * (double)gk);
+            const float vk = (float)(b2 * (double)v4[u] + (1.0 - b2) * (double)gk * (double)gk);
+            t.m[k] = mk;
+            t.v[k] = vk;
+            const double mh = (double)mk / b1t, vh = (double)vk / b2t;
+            t.p[k] = pk - (float)(lr * mh / (sqrt(vh) + eps));
+        }
+    }
+}
+
 extern "C" __global__ void __launch_bounds__(256)
 scale_inplace_k(float *__restrict__ g, int64_t n, float s) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;

@@ -67,6 +67,8 @@ struct GemmArgs {
     unsigned a_bytes, b_bytes;  // extents of A and B for the buffer descriptors
     const float *B2;     // GATED: the up-projection weight (B is the gate's)
     const float *bias2;  // GATED: its bias or null
+    int beta;            // ACCUM: 1 C += acc; 0 C = 0.0f + acc, the first write of a gradient (the bits of an
+                         // accumulation into zeros, without reading C or clearing it first)
 };
 
 // Grouped raster: GROUP_M tile rows advance together along N so that the B
@@ -522,7 +524,7 @@ __device__ __forceinline__ void g_out_n(const GemmArgs &p, const int (&ii)[N], c
         const int i = min(ii[n], p.Mo - 1), j = min(jj[n], p.No - 1);
         const int64_t e = (int64_t)i * p.ldc + j;
         if (EPI == EPI_ACCUM) {
-            o1[n] = p.C[e];
+            o1[n] = p.beta ? p.C[e] : 0.0f;
         } else {
             const float *bq = hb ? p.bias + j : p.C;
             o1[n] = *bq;

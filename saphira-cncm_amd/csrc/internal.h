@@ -49,6 +49,24 @@ size_t ncm_sample_ws_bytes(int V);
  * step; the gradient is consumed and the next step accumulates from zero). */
 void ncm_adamw_update_clear(float *p, float *g, float *m, float *v, int64_t n, double lr, double b1, double b2,
                             double b1t, double b2t, double eps, double wd);
+/* Backward ops with a first-write form: beta 1 accumulates (the public
+ * functions' contract), beta 0 writes 0.0f + the gradient -- the bits of an
+ * accumulation into zeros -- so the output needs no clearing and is not read.
+ * Where a path cannot write every element it clears the output first. */
+void ncm_linear_bwd_ex(const float *x, const float *W, const float *dy, float *dx, float *dW, float *db,
+                       int64_t batch, int M, int K, int dx_beta);
+void ncm_layernorm_bwd_ex(const float *x, const float *w, const float *dy, float *dx, float *dw, float *db,
+                          int64_t rows, int C, double eps, int beta);
+void ncm_rmsnorm_bwd_ex(const float *x, const float *w, const float *dy, float *dx, float *dw, int64_t rows, int C,
+                        int beta);
+void ncm_act_bwd_ex(int kind, const float *x, const float *dy, float *dx, int64_t n, int beta);
+void ncm_add_inplace_ex(float *y, const float *x, int64_t n, int beta);
+void ncm_sdpa_bwd_flash_ex(const float *q, const float *k, const float *v, const float *o, const float *stats,
+                           const float *mask, int causal, const float *dO, float *dq, float *dk, float *dv, int B,
+                           int H, int Hkv, int Tq, int Tkv, int hd, int beta);
+void ncm_qkv_split_bwd_ex(const float *gq, const float *gk, const float *gv, float *dx, int B, int T, int C, int H,
+                          int hd, int K, int rep, int beta);
+void ncm_heads_bwd_ex(const float *dy, float *dx, int B, int T, int C, int H, int hd, int dir, int beta);
 /* grad_clip_global(G, sizes, count, max_norm) followed by
  * ncm_adamw_update_clear (clear_g) or adamw_update on every tensor, in three
  * launches with no host synchronisation; *g2_dev gets the device address of

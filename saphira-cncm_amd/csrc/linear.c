@@ -35,6 +35,7 @@ typedef struct {
     unsigned a_bytes, b_bytes;
     const float *B2;
     const float *bias2;
+    int beta;
 } GemmArgs;
 
 /* Must match struct GemvArgs in gemm.hip. */
@@ -173,9 +174,10 @@ static int64_t extent(int64_t rows, int64_t cols, int64_t ld) { return ((rows - 
 #define TILE_M 64
 #define TILE_N 64
 
+/* beta (accumulating kinds): 1 C += A.B, 0 C = 0.0f + A.B (C is not read). */
 static int run_gemm(int kind, const float *A, const float *B, float *C, const float *bias,
                     const float *res, int res_mul, int Mo, int No, int Kred, int lda, int ldb, int ldc,
-                    int act, int vec) {
+                    int act, int vec, int beta) {
     if (Mo <= 0 || No <= 0) return 0;
     const int bm = TILE_M, bn = TILE_N;
     if ((int64_t)((Mo + bm - 1) / bm) * ((No + bn - 1) / bn) > INT_MAX / 4)
@@ -192,7 +194,7 @@ static int run_gemm(int kind, const float *A, const float *B, float *C, const fl
         return ncm_fail(NCM_E_ARG, "linear: operand of %lld / %lld bytes exceeds the 2 GiB buffer range",
                         (long long)ab, (long long)bb);
     GemmArgs p = {A, B, C, bias, res, NULL, Mo, No, Kred, lda, ldb, ldc, act, 0,
-                  g.tiles_m, g.tiles_n, g.iters, g.dp_tiles, g.segs, (unsigned)ab, (unsigned)bb, NULL, NULL};
+                  g.tiles_m, g.tiles_n, g.iters, g.dp_tiles, g.segs, (unsigned)ab, (unsigned)bb, NULL, NULL, beta};
     p.res_mul = res_mul;
     int split_tiles = g.tiles_m * g.tiles_n - g.dp_tiles;
     if (g.segs > 1) {
@@ -270,7 +272,7 @@ static void linear_forward(const char *fn, const float *x, const float *W, const
     } else if (batch <= 8)
         run_gemv(x, W, b, res, y, (int)batch, M, K, act, vec);
     else
-        run_gemm(L_FWD, x, W, y, b, res, res_mul, (int)batch, M, K, K, K, M, act, vec);
+        run_gemm(L_FWD, x, W, y, b, res, res_mul, (int)batch, M, K, K, K, M, act, vec, 1);
 }
 
 void linear_fwd(const float *x, const float *W, const float *b, float *y, int64_t batch, int M,
@@ -313,7 +315,7 @@ void linear_fwd_gated(const float *x, const float *Wg, const float *bg, const fl
         if (ab < MAX_BUFFER_BYTES && bb < MAX_BUFFER_BYTES) {
             const int groups = (K + 4 * BK - 1) / (4 * BK);
             GemmArgs p = {x, Wg, y, bg, NULL, NULL, (int)batch, M, K, K, K, M, act, 0,
-                          tiles_m, tiles_n, 4 * groups, tiles_m * tiles_n, 1, (unsigned)ab, (unsigned)bb, Wu, bu};
+                          tiles_m, tiles_n, 4 * groups, tiles_m * tiles_n, 1, (unsigned)ab, (unsigned)bb, Wu, bu, 1};
             void *args[] = {&p};
             ncm_launch_named("gemm_64x64_gated_v", (unsigned)(tiles_m * tiles_n), 1, 1, 256, args);
             return;
@@ -356,8 +358,11 @@ static int run_dxt(const float *dy, const float *W, float *dx, int nb, int M, in
     return 0;
 }
 
-void linear_bwd(const float *x, const float *W, const float *dy, float *dx, float *dW, float *db,
-                int64_t batch, int M, int K) {
+/* linear_bwd with dx_beta = 0: dx is written (0.0f + the product, the bits of
+ * accumulating into zeros) instead of accumulated, so its buffer needs no
+ * clearing; dW and db always accumulate. */
+void ncm_linear_bwd_ex(const float *x, const float *W, const float *dy, float *dx, float *dW, float *db,
+                       int64_t batch, int M, int K, int dx_beta) {
     if (check_dims("linear_bwd", batch, M, K)) return;
     if (batch == 0) return;
     if (!dy || (dx && !W) || (dW && !x)) {
@@ -368,11 +373,12 @@ void linear_bwd(const float *x, const float *W, const float *dy, float *dx, floa
     int nb = (int)batch;
     if (dx) {
         int rc;
-        if (nb <= 8 && K % 4 == 0 && is_aligned16(W))
+        if (nb <= 8 && K % 4 == 0 && is_aligned16(W)) {
+            if (!dx_beta && ncm_zero_async(dx, (size_t)nb * K * sizeof(float))) return;
             rc = run_dxt(dy, W, dx, nb, M, K);
-        else {
+        } else {
             int vec = (M % 4 == 0) && (K % 4 == 0) && is_aligned16(dy) && is_aligned16(W);
-            rc = run_gemm(L_DX, dy, W, dx, NULL, NULL, 0, nb, K, M, M, K, K, 0, vec);
+            rc = run_gemm(L_DX, dy, W, dx, NULL, NULL, 0, nb, K, M, M, K, K, 0, vec, dx_beta);
         }
         if (rc) return;
     }
@@ -386,7 +392,7 @@ void linear_bwd(const float *x, const float *W, const float *dy, float *dx, floa
             rc = ncm_launch_named(vec ? "dw_rank_v" : "dw_rank_s", (unsigned)((n + 255) / 256), 1, 1, 256, a);
         } else {
             int vec = (M % 4 == 0) && (K % 4 == 0) && is_aligned16(dy) && is_aligned16(x);
-            rc = run_gemm(L_DW, dy, x, dW, NULL, NULL, 0, M, K, nb, M, K, K, 0, vec);
+            rc = run_gemm(L_DW, dy, x, dW, NULL, NULL, 0, M, K, nb, M, K, K, 0, vec, 1);
         }
         if (rc) return;
     }
@@ -411,6 +417,11 @@ void linear_bwd(const float *x, const float *W, const float *dy, float *dx, floa
         else
             ncm_launch_named("colsum_final", (unsigned)((M + 255) / 256), 1, 1, 256, a2);
     }
+}
+
+void linear_bwd(const float *x, const float *W, const float *dy, float *dx, float *dW, float *db,
+                int64_t batch, int M, int K) {
+    ncm_linear_bwd_ex(x, W, dy, dx, dW, db, batch, M, K, 1);
 }
 
 int ncm_hip_linear_plan(int op, int64_t batch, int M, int K, char *kernel, size_t cap) {

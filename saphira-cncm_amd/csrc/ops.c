@@ -102,6 +102,9 @@ void add_fwd(const float *a, const float *b, float *y, int64_t n) { eltwise("add
 void mul_fwd(const float *a, const float *b, float *y, int64_t n) { eltwise("mul_fwd", a, b, y, 0.f, n, 1); }
 void scale_fwd(const float *x, float s, float *y, int64_t n) { eltwise("scale_fwd", x, NULL, y, s, n, 2); }
 void add_inplace_fwd(float *y, const float *x, int64_t n) { eltwise("add_inplace_fwd", x, NULL, y, 0.f, n, 3); }
+void ncm_add_inplace_ex(float *y, const float *x, int64_t n, int beta) {
+    eltwise("add_inplace_fwd", x, NULL, y, 0.f, n, beta ? 3 : 7);
+}
 void silu_fwd(const float *x, float *y, int64_t n) { eltwise("silu_fwd", x, NULL, y, 0.f, n, 4); }
 void gelu_fwd(const float *x, float *y, int64_t n) { eltwise("gelu_fwd", x, NULL, y, 0.f, n, 5); }
 void gelu_tanh_fwd(const float *x, float *y, int64_t n) { eltwise("gelu_tanh_fwd", x, NULL, y, 0.f, n, 6); }

@@ -332,7 +332,9 @@ embedding_k(const float *__restrict__ W, const int *__restrict__ idx, float *__r
 
 // ---------------------------------------------------------------- elementwise
 // op: 0 add (a+b), 1 mul (a*b), 2 scale (a*s), 3 add_inplace (y += a),
-//     4 silu, 5 gelu, 6 gelu_tanh   (kernels.c:167-226, 829-874)
+//     4 silu, 5 gelu, 6 gelu_tanh   (kernels.c:167-226, 829-874),
+//     7 y = 0.0f + a (add_inplace into a fresh gradient: the bits of
+//       accumulating into zeros, without reading or clearing y)
 __device__ __forceinline__ float elt_op(float v, float w, float yv, float s, int op) {
 #pragma clang fp contract(off)
     switch (op) {
@@ -340,6 +342,7 @@ __device__ __forceinline__ float elt_op(float v, float w, float yv, float s, int
     case 1: return v * w;
     case 2: return v * s;
     case 3: return yv + v;
+    case 7: return 0.0f + v;
     case 4: return ncm_act(v, ACT_SILU);
     case 5: return ncm_act(v, ACT_GELU);
     default: return ncm_act(v, ACT_GELU_TANH);

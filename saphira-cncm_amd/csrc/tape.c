@@ -136,7 +136,7 @@ typedef struct {
 struct NcmTape {
     NtRec *r;
     int n, cap;
-    Pool rec, grad;
+    Pool rec, grad, gradw;   /* gradw: gradients whose first writer overwrites (not cleared) */
     GEnt *gm;
     int gn, gcap;
 };
@@ -157,6 +157,7 @@ void ncm_tape_clear(NcmTape *t) {
     free_recs(t);
     pool_reset(&t->rec);
     pool_reset(&t->grad);
+    pool_reset(&t->gradw);
     t->gn = 0;
 }
 
@@ -166,6 +167,7 @@ void ncm_tape_free(NcmTape *t) {
     free_recs(t);
     pool_free(&t->rec);
     pool_free(&t->grad);
+    pool_free(&t->gradw);
     free(t->r);
     free(t->gm);
     free(t);
@@ -223,6 +225,25 @@ static float *gmap_get(NcmTape *t, const float *key, int64_t n) {
         return NULL;
     }
     if (gmap_put(t, key, g)) return NULL;
+    return g;
+}
+
+/* The gradient buffer of `key` for an op that can write its first gradient
+ * instead of accumulating it: an existing buffer is returned with *beta = 1
+ * (accumulate); a new one comes from the pool that is not cleared, with
+ * *beta = 0, and the op must write every element of it. */
+static float *gmap_get_fresh(NcmTape *t, const float *key, int64_t n, int *beta) {
+    *beta = 1;
+    if (!key) return NULL;
+    float *g = gmap_find(t, key);
+    if (g) return g;
+    g = (float *)pool_alloc(&t->gradw, (size_t)n * sizeof(float));
+    if (!g) {
+        ncm_fail(NCM_E_OOM, "tape: gradient buffer of %lld floats", (long long)n);
+        return NULL;
+    }
+    if (gmap_put(t, key, g)) return NULL;
+    *beta = 0;
     return g;
 }
 
@@ -418,6 +439,7 @@ void ncm_tape_backward(NcmTape *t, const NcmPMap *pm) {
     if (!t || ncm_ready()) return;
     t->gn = 0;
     pool_reset(&t->grad);
+    pool_reset(&t->gradw);
     if (pm)
         for (int i = 0; i < pm->n; i++)
             if (pm->params[i] && pm->grads[i] && gmap_put(t, pm->params[i], pm->grads[i])) return;
@@ -443,36 +465,45 @@ void ncm_tape_backward(NcmTape *t, const NcmPMap *pm) {
         switch (r->op) {
         case NT_LINEAR: {
             int64_t batch = r->n;
-            int M = r->p1, K = r->p2;
-            linear_bwd(r->a, r->b, dy, gmap_get(t, r->a, batch * K), gmap_get(t, r->b, (int64_t)M * K),
-                       r->c ? gmap_get(t, r->c, M) : NULL, batch, M, K);
+            int M = r->p1, K = r->p2, bx;
+            float *dx = gmap_get_fresh(t, r->a, batch * K, &bx);
+            ncm_linear_bwd_ex(r->a, r->b, dy, dx, gmap_get(t, r->b, (int64_t)M * K),
+                              r->c ? gmap_get(t, r->c, M) : NULL, batch, M, K, bx);
             break;
         }
         case NT_EMBED:
             embedding_bwd(dy, r->ids, r->n, r->p1, gmap_get(t, r->a, (int64_t)r->p2 * r->p1), r->p2);
             break;
-        case NT_LN:
-            layernorm_bwd(r->a, r->b, dy, gmap_get(t, r->a, r->n * r->p1), r->b ? gmap_get(t, r->b, r->p1) : NULL,
-                          r->c ? gmap_get(t, r->c, r->p1) : NULL, r->n, r->p1, r->s);
+        case NT_LN: {
+            int bx;
+            float *dx = gmap_get_fresh(t, r->a, r->n * r->p1, &bx);
+            ncm_layernorm_bwd_ex(r->a, r->b, dy, dx, r->b ? gmap_get(t, r->b, r->p1) : NULL,
+                                 r->c ? gmap_get(t, r->c, r->p1) : NULL, r->n, r->p1, r->s, bx);
             break;
-        case NT_RMSN:
-            rmsnorm_bwd(r->a, r->b, dy, gmap_get(t, r->a, r->n * r->p1), r->b ? gmap_get(t, r->b, r->p1) : NULL,
-                        r->n, r->p1);
+        }
+        case NT_RMSN: {
+            int bx;
+            float *dx = gmap_get_fresh(t, r->a, r->n * r->p1, &bx);
+            ncm_rmsnorm_bwd_ex(r->a, r->b, dy, dx, r->b ? gmap_get(t, r->b, r->p1) : NULL, r->n, r->p1, bx);
             break;
+        }
         case NT_ACT: {
-            float *dx = gmap_get(t, r->a, r->n);
-            if (r->p1 == 0) gelu_bwd(r->a, dy, dx, r->n);
-            else if (r->p1 == 1) silu_bwd(r->a, dy, dx, r->n);
-            else gelu_tanh_bwd(r->a, dy, dx, r->n);
+            int bx;
+            float *dx = gmap_get_fresh(t, r->a, r->n, &bx);
+            ncm_act_bwd_ex(r->p1, r->a, dy, dx, r->n, bx);
             break;
         }
         case NT_MUL:
             mul_bwd(r->a, r->b, dy, gmap_get(t, r->a, r->n), gmap_get(t, r->b, r->n), r->n);
             break;
-        case NT_ADD:
-            add_inplace_fwd(gmap_get(t, r->a, r->n), dy, r->n);
-            add_inplace_fwd(gmap_get(t, r->b, r->n), dy, r->n);
+        case NT_ADD: {
+            int ba, bb;
+            float *ga = gmap_get_fresh(t, r->a, r->n, &ba);
+            if (ga) ncm_add_inplace_ex(ga, dy, r->n, ba);
+            float *gb = gmap_get_fresh(t, r->b, r->n, &bb);   /* after a's write: b may be a */
+            if (gb) ncm_add_inplace_ex(gb, dy, r->n, bb);
             break;
+        }
         case NT_SCALE: {
             float *dx = gmap_get(t, r->a, r->n);
             float s = (float)r->s;
@@ -493,29 +524,45 @@ void ncm_tape_backward(NcmTape *t, const NcmPMap *pm) {
         }
         case NT_SDPA: {
             int B = (int)r->n, H = r->p1, Hkv = r->p2, Tq = r->p3, Tkv = r->p4, hd = r->p5;
-            float *gq = gmap_get(t, r->a, (int64_t)B * H * Tq * hd);
-            float *gk = gmap_get(t, r->b, (int64_t)B * Hkv * Tkv * hd), *gv = gmap_get(t, r->c, (int64_t)B * Hkv * Tkv * hd);
+            const int64_t nq = (int64_t)B * H * Tq * hd, nk = (int64_t)B * Hkv * Tkv * hd;
+            int fq, fk, fv;
+            float *gq = gmap_get_fresh(t, r->a, nq, &fq);
+            float *gk = gmap_get_fresh(t, r->b, nk, &fk), *gv = gmap_get_fresh(t, r->c, nk, &fv);
+            /* one flag for the three outputs: written only when all three are
+             * new and distinct (the flash kernels give every element one
+             * writer); otherwise the new ones are cleared and accumulated */
+            int beta = 1;
+            if ((r->p6 & 1) && !fq && !fk && !fv && gq != gk && gq != gv && gk != gv) {
+                beta = 0;
+            } else {
+                if (!fq && gq && ncm_zero_async(gq, (size_t)nq * sizeof(float))) return;
+                if (!fk && gk && gk != gq && ncm_zero_async(gk, (size_t)nk * sizeof(float))) return;
+                if (!fv && gv && gv != gq && gv != gk && ncm_zero_async(gv, (size_t)nk * sizeof(float))) return;
+            }
             if (r->p6 & 1)
-                ncm_sdpa_bwd_flash(r->a, r->b, r->c, r->y, r->aux, r->mask, (r->p6 >> 1) & 1, dy, gq, gk, gv, B, H,
-                                   Hkv, Tq, Tkv, hd);
+                ncm_sdpa_bwd_flash_ex(r->a, r->b, r->c, r->y, r->aux, r->mask, (r->p6 >> 1) & 1, dy, gq, gk, gv, B,
+                                      H, Hkv, Tq, Tkv, hd, beta);
             else
                 sdpa_bwd_gqa(r->a, r->b, r->c, r->aux, dy, gq, gk, gv, B, H, Hkv, Tq, Tkv, hd);
             break;
         }
         case NT_SPLIT: {
-            int B = (int)r->n, T = r->p1, C = r->p2, H = r->p3, hd = r->p4, K = r->p5, rep = r->p6;
-            qkv_split_bwd(gmap_find(t, r->b), gmap_find(t, r->c), gmap_find(t, r->y),
-                          gmap_get(t, r->a, (int64_t)B * T * ((int64_t)C + 2 * K * hd)), B, T, C, H, hd, K, rep);
+            int B = (int)r->n, T = r->p1, C = r->p2, H = r->p3, hd = r->p4, K = r->p5, rep = r->p6, bx;
+            float *dx = gmap_get_fresh(t, r->a, (int64_t)B * T * ((int64_t)C + 2 * K * hd), &bx);
+            ncm_qkv_split_bwd_ex(gmap_find(t, r->b), gmap_find(t, r->c), gmap_find(t, r->y), dx, B, T, C, H, hd, K,
+                                 rep, bx);
             break;
         }
         case NT_MERGE: {
-            int B = (int)r->n, T = r->p1, C = r->p2, H = r->p3, hd = r->p4;
-            head_merge_bwd(dy, gmap_get(t, r->a, (int64_t)B * H * T * hd), B, T, C, H, hd);
+            int B = (int)r->n, T = r->p1, C = r->p2, H = r->p3, hd = r->p4, bx;
+            float *dx = gmap_get_fresh(t, r->a, (int64_t)B * H * T * hd, &bx);
+            ncm_heads_bwd_ex(dy, dx, B, T, C, H, hd, 0, bx);
             break;
         }
         case NT_HEADSPLIT: {
-            int B = (int)r->n, T = r->p1, C = r->p2, H = r->p3, hd = r->p4;
-            heads_transpose_bwd(dy, gmap_get(t, r->a, (int64_t)B * T * C), B, T, C, H, hd);
+            int B = (int)r->n, T = r->p1, C = r->p2, H = r->p3, hd = r->p4, bx;
+            float *dx = gmap_get_fresh(t, r->a, (int64_t)B * T * C, &bx);
+            ncm_heads_bwd_ex(dy, dx, B, T, C, H, hd, 1, bx);
             break;
         }
         case NT_CE:

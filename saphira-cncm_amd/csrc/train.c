@@ -25,8 +25,9 @@ static int shape_ok(const char *fn, int64_t rows, int C) {
 }
 
 /* ---- LayerNorm / RMSNorm backward (train_tape.c:569-634, 748-792) ---- */
+/* beta 0: dx is written (0.0f + the gradient) instead of accumulated. */
 static void norm_bwd(const char *fn, int kind, const float *x, const float *w, const float *dy, float *dx,
-                     float *dw, float *db, int64_t rows, int C, double eps) {
+                     float *dw, float *db, int64_t rows, int C, double eps, int beta) {
     if (shape_ok(fn, rows, C)) return;
     if (rows == 0) return;
     if (!x || !dy) { ncm_fail(NCM_E_ARG, "%s: null input", fn); return; }
@@ -44,7 +45,7 @@ static void norm_bwd(const char *fn, int kind, const float *x, const float *w, c
             part = (double *)ncm_workspace(WS_TRAIN, (size_t)chunks * C * 2 * sizeof(double));
             if (!part) return;
         }
-        void *a[] = {&x, &w, &dy, &dx, &part, &rows, &C, &eps};
+        void *a[] = {&x, &w, &dy, &dx, &part, &rows, &C, &eps, &beta};
         if (ncm_launch_named(names[kind][(C + 255) / 256 - 1], (unsigned)chunks, 1, 1, 256, a)) return;
         if (!want_param) return;
         float *dbk = kind == 0 ? db : NULL;
@@ -54,6 +55,7 @@ static void norm_bwd(const char *fn, int kind, const float *x, const float *w, c
     }
     const int chunks = (int)((rows + NORM_ROWS - 1) / NORM_ROWS);
     if (chunks > 65535 && want_param) { ncm_fail(NCM_E_ARG, "%s: too many rows", fn); return; }
+    if (dx && !beta && ncm_zero_async(dx, (size_t)rows * C * sizeof(float))) return;
     size_t stats_bytes = (size_t)rows * 2 * sizeof(double);
     size_t part_bytes = want_param ? (size_t)chunks * C * 2 * sizeof(double) : 0;
     char *ws = (char *)ncm_workspace(WS_TRAIN, stats_bytes + part_bytes);
@@ -76,11 +78,21 @@ static void norm_bwd(const char *fn, int kind, const float *x, const float *w, c
 
 void layernorm_bwd(const float *x, const float *w, const float *dy, float *dx, float *dw, float *db, int64_t rows,
                    int C, double eps) {
-    norm_bwd("layernorm_bwd", 0, x, w, dy, dx, dw, db, rows, C, eps);
+    norm_bwd("layernorm_bwd", 0, x, w, dy, dx, dw, db, rows, C, eps, 1);
 }
 
 void rmsnorm_bwd(const float *x, const float *w, const float *dy, float *dx, float *dw, int64_t rows, int C) {
-    norm_bwd("rmsnorm_bwd", 1, x, w, dy, dx, dw, NULL, rows, C, 1e-6);
+    norm_bwd("rmsnorm_bwd", 1, x, w, dy, dx, dw, NULL, rows, C, 1e-6, 1);
+}
+
+void ncm_layernorm_bwd_ex(const float *x, const float *w, const float *dy, float *dx, float *dw, float *db,
+                          int64_t rows, int C, double eps, int beta) {
+    norm_bwd("layernorm_bwd", 0, x, w, dy, dx, dw, db, rows, C, eps, beta);
+}
+
+void ncm_rmsnorm_bwd_ex(const float *x, const float *w, const float *dy, float *dx, float *dw, int64_t rows, int C,
+                        int beta) {
+    norm_bwd("rmsnorm_bwd", 1, x, w, dy, dx, dw, NULL, rows, C, 1e-6, beta);
 }
 
 /* ---- softmax cross-entropy (train_tape.c:442-481, 657-679, 1801-1810) ---- */
@@ -195,9 +207,9 @@ void sdpa_bwd_gqa(const float *q, const float *k, const float *v, const float *P
 /* The recomputing backward of the tape's SDPA records (hd 64, aligned): D =
  * rowsum(dO o O), then the dq and dk/dv kernels rebuild P tile by tile from
  * the forward's row statistics.  Gradients accumulate. */
-void ncm_sdpa_bwd_flash(const float *q, const float *k, const float *v, const float *o, const float *stats,
-                        const float *mask, int causal, const float *dO, float *dq, float *dk, float *dv, int B, int H,
-                        int Hkv, int Tq, int Tkv, int hd) {
+static void sdpa_bwd_flash_any(const float *q, const float *k, const float *v, const float *o, const float *stats,
+                               const float *mask, int causal, const float *dO, float *dq, float *dk, float *dv, int B,
+                               int H, int Hkv, int Tq, int Tkv, int hd, int beta) {
     if (attn_check("ncm_sdpa_bwd_flash", B, H, Hkv, Tq, Tkv, hd)) return;
     if ((int64_t)B * Tq == 0 || (!dq && !dk && !dv)) return;
     if (hd != 64 || !q || !k || !v || !o || !stats || !dO) {
@@ -220,13 +232,27 @@ void ncm_sdpa_bwd_flash(const float *q, const float *k, const float *v, const fl
     void *a0[] = {&dO, &o, &D, (void *)&rows, &hd};
     if (ncm_launch_named("sdpa_bwd_rowdot", blocks_of(rows, 4), 1, 1, 256, a0)) return;
     if (dq) {
-        void *a[] = {&q, &k, &v, &mask, &stats, &D, &dO, &dq, &H, &Hkv, &Tq, &Tkv, &scale, &causal};
+        void *a[] = {&q, &k, &v, &mask, &stats, &D, &dO, &dq, &H, &Hkv, &Tq, &Tkv, &scale, &causal, &beta};
         if (ncm_launch_named("sdpa_fbwd_dq_hd64", (unsigned)H, (unsigned)B, blocks_of(Tq, 64), 256, a)) return;
     }
     if (dk || dv) {
-        void *a[] = {&q, &k, &v, &mask, &stats, &D, &dO, &dk, &dv, &H, &Hkv, &Tq, &Tkv, &scale, &causal};
+        void *a[] = {&q, &k, &v, &mask, &stats, &D, &dO, &dk, &dv, &H, &Hkv, &Tq, &Tkv, &scale, &causal, &beta};
         ncm_launch_named("sdpa_fbwd_dkdv_hd64", (unsigned)Hkv, (unsigned)B, blocks_of(Tkv, 64), 256, a);
     }
+}
+
+void ncm_sdpa_bwd_flash(const float *q, const float *k, const float *v, const float *o, const float *stats,
+                        const float *mask, int causal, const float *dO, float *dq, float *dk, float *dv, int B, int H,
+                        int Hkv, int Tq, int Tkv, int hd) {
+    sdpa_bwd_flash_any(q, k, v, o, stats, mask, causal, dO, dq, dk, dv, B, H, Hkv, Tq, Tkv, hd, 1);
+}
+
+/* beta 0: dq, dk and dv are written (every element has one writer in the
+ * kernels) instead of accumulated. */
+void ncm_sdpa_bwd_flash_ex(const float *q, const float *k, const float *v, const float *o, const float *stats,
+                           const float *mask, int causal, const float *dO, float *dq, float *dk, float *dv, int B,
+                           int H, int Hkv, int Tq, int Tkv, int hd, int beta) {
+    sdpa_bwd_flash_any(q, k, v, o, stats, mask, causal, dO, dq, dk, dv, B, H, Hkv, Tq, Tkv, hd, beta);
 }
 
 /* ---- optimizer (train.c:51-64, 102-145, 172-178; train_gpt2.c:160-173) ---- */
@@ -518,21 +544,27 @@ static int elt_check(const char *fn, int64_t n, const void *a, const void *b) {
     return ncm_ready();
 }
 
-static void act_bwd(const char *fn, const float *x, const float *dy, float *dx, int64_t n, int kind) {
+static void act_bwd(const char *fn, const float *x, const float *dy, float *dx, int64_t n, int kind, int beta) {
     if (elt_check(fn, n, x, dy) || !dx) return;
     if (n % 4 == 0 && (((uintptr_t)x | (uintptr_t)dy | (uintptr_t)dx) & 15) == 0) {
         int64_t n4 = n / 4;
-        void *a[] = {&x, &dy, &dx, &n4, &kind};
+        void *a[] = {&x, &dy, &dx, &n4, &kind, &beta};
         ncm_launch_named("act_bwd4_k", blocks_of(n4, 256), 1, 1, 256, a);
         return;
     }
+    if (!beta && ncm_zero_async(dx, (size_t)n * sizeof(float))) return;
     void *a[] = {&x, &dy, &dx, &n, &kind};
     ncm_launch_named("act_bwd_k", blocks_of(n, 256), 1, 1, 256, a);
 }
-void gelu_bwd(const float *x, const float *dy, float *dx, int64_t n) { act_bwd("gelu_bwd", x, dy, dx, n, 0); }
-void silu_bwd(const float *x, const float *dy, float *dx, int64_t n) { act_bwd("silu_bwd", x, dy, dx, n, 1); }
+void gelu_bwd(const float *x, const float *dy, float *dx, int64_t n) { act_bwd("gelu_bwd", x, dy, dx, n, 0, 1); }
+void silu_bwd(const float *x, const float *dy, float *dx, int64_t n) { act_bwd("silu_bwd", x, dy, dx, n, 1, 1); }
 void gelu_tanh_bwd(const float *x, const float *dy, float *dx, int64_t n) {
-    act_bwd("gelu_tanh_bwd", x, dy, dx, n, 2);
+    act_bwd("gelu_tanh_bwd", x, dy, dx, n, 2, 1);
+}
+void ncm_act_bwd_ex(int kind, const float *x, const float *dy, float *dx, int64_t n, int beta) {
+    static const char *const fn[3] = {"gelu_bwd", "silu_bwd", "gelu_tanh_bwd"};
+    const int k = kind == 0 || kind == 1 ? kind : 2;   /* the tape's act codes: 0 gelu, 1 silu, else gelu_tanh */
+    act_bwd(fn[k], x, dy, dx, n, k, beta);
 }
 
 void mul_bwd(const float *a, const float *b, const float *dy, float *da, float *db, int64_t n) {
@@ -616,8 +648,11 @@ void embedding_bwd(const float *dy, const int *idx, int64_t n, int D, float *dW,
     }
 }
 
-void qkv_split_bwd(const float *gq, const float *gk, const float *gv, float *dx, int B, int T, int C, int H, int hd,
-                   int K, int rep) {
+/* beta 0: dx is fresh (not cleared): the row kernel writes it when every
+ * element has a source (q, k and v gradients, C == H hd); otherwise it is
+ * cleared first and accumulated. */
+static void qkv_split_bwd_any(const float *gq, const float *gk, const float *gv, float *dx, int B, int T, int C,
+                              int H, int hd, int K, int rep, int beta) {
     if (B < 0 || T < 0 || C < 0 || H <= 0 || hd <= 0 || K <= 0 || rep <= 0 || (H - 1) / rep >= K ||
         (int64_t)H * hd > C) {
         ncm_fail(NCM_E_ARG, "qkv_split_bwd: bad shape");
@@ -625,10 +660,16 @@ void qkv_split_bwd(const float *gq, const float *gk, const float *gv, float *dx,
     }
     int64_t n = (int64_t)B * T * ((int64_t)C + 2 * K * hd);
     if (elt_check("qkv_split_bwd", n, dx, dx)) return;
+    const int rows_path = hd % 4 == 0 && C % 4 == 0 && (int64_t)B * T <= INT_MAX &&
+                          (int64_t)C + 2 * K * hd <= INT_MAX && is_aligned16(gq) && is_aligned16(gk) &&
+                          is_aligned16(gv) && is_aligned16(dx);
+    if (!beta && !(rows_path && gq && gk && gv && C == H * hd)) {
+        if (ncm_zero_async(dx, (size_t)n * sizeof(float))) return;
+        beta = 1;
+    }
     if (!gq && !gk && !gv) return;
-    if (hd % 4 == 0 && C % 4 == 0 && (int64_t)B * T <= INT_MAX && (int64_t)C + 2 * K * hd <= INT_MAX &&
-        is_aligned16(gq) && is_aligned16(gk) && is_aligned16(gv) && is_aligned16(dx)) {
-        void *a[] = {&gq, &gk, &gv, &dx, &T, &C, &H, &hd, &K, &rep};
+    if (rows_path) {
+        void *a[] = {&gq, &gk, &gv, &dx, &T, &C, &H, &hd, &K, &rep, &beta};
         ncm_launch_named("qkv_split_bwd_rows_k", (unsigned)((int64_t)B * T), 1, 1, 256, a);
         return;
     }
@@ -636,15 +677,34 @@ void qkv_split_bwd(const float *gq, const float *gk, const float *gv, float *dx,
     ncm_launch_named("qkv_split_bwd_k", blocks_of(n, 256), 1, 1, 256, a);
 }
 
-static void heads_bwd(const char *fn, const float *dy, float *dx, int B, int T, int C, int H, int hd, int dir) {
+void qkv_split_bwd(const float *gq, const float *gk, const float *gv, float *dx, int B, int T, int C, int H, int hd,
+                   int K, int rep) {
+    qkv_split_bwd_any(gq, gk, gv, dx, B, T, C, H, hd, K, rep, 1);
+}
+
+void ncm_qkv_split_bwd_ex(const float *gq, const float *gk, const float *gv, float *dx, int B, int T, int C, int H,
+                          int hd, int K, int rep, int beta) {
+    qkv_split_bwd_any(gq, gk, gv, dx, B, T, C, H, hd, K, rep, beta);
+}
+
+/* beta 0: dx is fresh; the row kernel writes every element when the rows are
+ * whole heads (C == H hd), otherwise dx is cleared first. */
+static void heads_bwd(const char *fn, const float *dy, float *dx, int B, int T, int C, int H, int hd, int dir,
+                      int beta) {
     if (B < 0 || T < 0 || C < 0 || H <= 0 || hd <= 0 || C > (int64_t)H * hd) {
         ncm_fail(NCM_E_ARG, "%s: bad shape", fn);
         return;
     }
     int64_t n = dir == 0 ? (int64_t)B * H * T * hd : (int64_t)B * T * C;
     if (elt_check(fn, n, dy, dx)) return;
-    if (hd % 4 == 0 && C % 4 == 0 && (int64_t)B * T <= INT_MAX && is_aligned16(dy) && is_aligned16(dx)) {
-        void *a[] = {&dy, &dx, &T, &C, &H, &hd, &dir};
+    const int rows_path = hd % 4 == 0 && C % 4 == 0 && (int64_t)B * T <= INT_MAX && is_aligned16(dy) &&
+                          is_aligned16(dx);
+    if (!beta && !(rows_path && (dir == 1 || C == H * hd))) {
+        if (ncm_zero_async(dx, (size_t)n * sizeof(float))) return;
+        beta = 1;
+    }
+    if (rows_path) {
+        void *a[] = {&dy, &dx, &T, &C, &H, &hd, &dir, &beta};
         ncm_launch_named("heads_bwd_rows_k", (unsigned)((int64_t)B * T), 1, 1, 256, a);
         return;
     }
@@ -653,9 +713,13 @@ static void heads_bwd(const char *fn, const float *dy, float *dx, int B, int T, 
 }
 
 void head_merge_bwd(const float *dy, float *dctx, int B, int T, int C, int H, int hd) {
-    heads_bwd("head_merge_bwd", dy, dctx, B, T, C, H, hd, 0);
+    heads_bwd("head_merge_bwd", dy, dctx, B, T, C, H, hd, 0, 1);
 }
 
 void heads_transpose_bwd(const float *dy, float *dx, int B, int T, int C, int H, int hd) {
-    heads_bwd("heads_transpose_bwd", dy, dx, B, T, C, H, hd, 1);
+    heads_bwd("heads_transpose_bwd", dy, dx, B, T, C, H, hd, 1, 1);
+}
+
+void ncm_heads_bwd_ex(const float *dy, float *dx, int B, int T, int C, int H, int hd, int dir, int beta) {
+    heads_bwd(dir == 0 ? "head_merge_bwd" : "heads_transpose_bwd", dy, dx, B, T, C, H, hd, dir, beta);
 }

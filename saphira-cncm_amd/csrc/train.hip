@@ -138,7 +138,8 @@ __device__ __forceinline__ void nbf_load(const float *__restrict__ p, int64_t ro
 template <int KIND, int NPL>
 __device__ __forceinline__ void norm_bwd_fused_body(const float *__restrict__ x, const float *__restrict__ w,
                                                     const float *__restrict__ dy, float *__restrict__ dx,
-                                                    double *__restrict__ part, int64_t rows, int C, double eps) {
+                                                    double *__restrict__ part, int64_t rows, int C, double eps,
+                                                    int beta) {
 #pragma clang fp contract(off)
     constexpr int NP = KIND == 0 ? 2 : 1;   // parameter gradients: (dw, db) or dw
     __shared__ double red[3][64 * NPL][4][NP];
@@ -204,7 +205,7 @@ __device__ __forceinline__ void norm_bwd_fused_body(const float *__restrict__ x,
                     const int c = 4 * (lane + 64 * j);
                     if (c < C) {
                         f4 *o = (f4 *)(dx + r * C + c);
-                        f4 v = *o;
+                        f4 v = beta ? *o : f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const double d = (double)ga[j][e] * (double)wv[j][e];
@@ -241,7 +242,7 @@ __device__ __forceinline__ void norm_bwd_fused_body(const float *__restrict__ x,
                     const int c = 4 * (lane + 64 * j);
                     if (c < C) {
                         f4 *o = (f4 *)(dx + r * C + c);
-                        f4 v = *o;
+                        f4 v = beta ? *o : f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
                             v[e] += (float)(((double)ga[j][e] * (double)wv[j][e] -
@@ -298,8 +299,8 @@ __device__ __forceinline__ void norm_bwd_fused_body(const float *__restrict__ x,
 #define NORM_BWD_FUSED(name, KIND, NPL)                                                                      \
     extern "C" __global__ void __launch_bounds__(256)                                                       \
         name(const float *__restrict__ x, const float *__restrict__ w, const float *__restrict__ dy,        \
-             float *__restrict__ dx, double *__restrict__ part, int64_t rows, int C, double eps) {           \
-        norm_bwd_fused_body<KIND, NPL>(x, w, dy, dx, part, rows, C, eps);                                   \
+             float *__restrict__ dx, double *__restrict__ part, int64_t rows, int C, double eps, int beta) { \
+        norm_bwd_fused_body<KIND, NPL>(x, w, dy, dx, part, rows, C, eps, beta);                             \
     }
 NORM_BWD_FUSED(ln_bwd_fused_1, 0, 1)
 NORM_BWD_FUSED(ln_bwd_fused_2, 0, 2)
@@ -1151,11 +1152,12 @@ act_bwd_k(const float *__restrict__ x, const float *__restrict__ dy, float *__re
 // The same on float4 groups (n4 = n / 4, 16-byte aligned): four independent
 // fp64 evaluations per thread.
 extern "C" __global__ void __launch_bounds__(256)
-act_bwd4_k(const float *__restrict__ x, const float *__restrict__ dy, float *__restrict__ dx, int64_t n4, int kind) {
+act_bwd4_k(const float *__restrict__ x, const float *__restrict__ dy, float *__restrict__ dx, int64_t n4, int kind,
+           int beta) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n4) return;
     const f4 xv = ((const f4 *)x)[i], g = ((const f4 *)dy)[i];
-    f4 d = ((const f4 *)dx)[i];
+    f4 d = beta ? ((const f4 *)dx)[i] : f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int e = 0; e < 4; ++e) d[e] += act_bwd_one(xv[e], g[e], kind);
     ((f4 *)dx)[i] = d;
@@ -1250,7 +1252,7 @@ __device__ __forceinline__ void rows_bt(int T, int H, int hd, int &bt, int64_t &
 
 extern "C" __global__ void __launch_bounds__(256)
 qkv_split_bwd_rows_k(const float *__restrict__ gq, const float *__restrict__ gk, const float *__restrict__ gv,
-                     float *__restrict__ dx, int T, int C, int H, int hd, int K, int rep) {
+                     float *__restrict__ dx, int T, int C, int H, int hd, int K, int rep, int beta) {
 #pragma clang fp contract(off)
     int bt;
     int64_t base, hs;
@@ -1259,9 +1261,10 @@ qkv_split_bwd_rows_k(const float *__restrict__ gq, const float *__restrict__ gk,
     f4 *row = (f4 *)(dx + (int64_t)bt * rl);
     for (int f = threadIdx.x; f < rl / 4; f += 256) {
         const int c = 4 * f;
+        const f4 z = {0.f, 0.f, 0.f, 0.f};
         if (c < C) {
             const int h = c / hd;
-            if (gq && h < H) row[f] += *(const f4 *)(gq + base + h * hs + (c - h * hd));
+            if (gq && h < H) row[f] = (beta ? row[f] : z) + *(const f4 *)(gq + base + h * hs + (c - h * hd));
             continue;
         }
         const int kc = c - C;
@@ -1271,12 +1274,13 @@ qkv_split_bwd_rows_k(const float *__restrict__ gq, const float *__restrict__ gk,
         const int kvh = k2 / hd, d = k2 - kvh * hd;
         f4 s = {0.f, 0.f, 0.f, 0.f};
         for (int h = kvh * rep; h < (kvh + 1) * rep && h < H; ++h) s += *(const f4 *)(g + base + h * hs + d);
-        row[f] += s;
+        row[f] = (beta ? row[f] : z) + s;
     }
 }
 
 extern "C" __global__ void __launch_bounds__(256)
-heads_bwd_rows_k(const float *__restrict__ dy, float *__restrict__ dx, int T, int C, int H, int hd, int dir) {
+heads_bwd_rows_k(const float *__restrict__ dy, float *__restrict__ dx, int T, int C, int H, int hd, int dir,
+                 int beta) {
 #pragma clang fp contract(off)
     int bt;
     int64_t base, hs;
@@ -1284,8 +1288,10 @@ heads_bwd_rows_k(const float *__restrict__ dy, float *__restrict__ dx, int T, in
     for (int f = threadIdx.x; f < C / 4; f += 256) {
         const int c = 4 * f, h = c / hd;
         const int64_t o = base + h * hs + (c - h * hd);
-        if (dir == 0) *(f4 *)(dx + o) += *(const f4 *)(dy + (int64_t)bt * C + c);
-        else *(f4 *)(dx + (int64_t)bt * C + c) += *(const f4 *)(dy + o);
+        const f4 z = {0.f, 0.f, 0.f, 0.f};
+        f4 *dst = (f4 *)(dx + (dir == 0 ? o : (int64_t)bt * C + c));
+        const f4 src = *(const f4 *)(dy + (dir == 0 ? (int64_t)bt * C + c : o));
+        *dst = (beta ? *dst : z) + src;
     }
 }
 
@@ -1351,7 +1357,7 @@ extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_pe
 sdpa_fbwd_dq_hd64(const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
                   const float *__restrict__ mask, const float *__restrict__ stats, const float *__restrict__ D,
                   const float *__restrict__ dO, float *__restrict__ dq, int H, int Hkv, int Tq, int Tkv, float scale,
-                  int causal) {
+                  int causal, int beta) {
     __shared__ __attribute__((aligned(16))) float sK[64 * SB_LD];
     __shared__ __attribute__((aligned(16))) float sV[64 * SB_LD];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1441,7 +1447,7 @@ sdpa_fbwd_dq_hd64(const float *__restrict__ q, const float *__restrict__ k, cons
         const int qi = qw + 4 * lg + r;
         if (qi < Tq) {
             f4 *o = (f4 *)(dq + (rbase + qi) * 64 + 4 * li);
-            f4 cur = *o;
+            f4 cur = beta ? *o : f4{0.f, 0.f, 0.f, 0.f};
             cur[0] += scale * acc[0][r];
             cur[1] += scale * acc[1][r];
             cur[2] += scale * acc[2][r];
@@ -1463,7 +1469,7 @@ extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_pe
 sdpa_fbwd_dkdv_hd64(const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
                     const float *__restrict__ mask, const float *__restrict__ stats, const float *__restrict__ D,
                     const float *__restrict__ dO, float *__restrict__ dk, float *__restrict__ dv, int H, int Hkv,
-                    int Tq, int Tkv, float scale, int causal) {
+                    int Tq, int Tkv, float scale, int causal, int beta) {
     __shared__ __attribute__((aligned(16))) float sG[64 * SB_LD];   // dO tile [query][d]
     __shared__ __attribute__((aligned(16))) float sQ[64 * SB_LD];   // Q tile  [query][d]
     __shared__ __attribute__((aligned(16))) float sM[64];
@@ -1579,7 +1585,7 @@ sdpa_fbwd_dkdv_hd64(const float *__restrict__ q, const float *__restrict__ k, co
         if (key < Tkv) {
             if (dk) {
                 f4 *o = (f4 *)(dk + (kbase + key) * 64 + 4 * li);
-                f4 cur = *o;
+                f4 cur = beta ? *o : f4{0.f, 0.f, 0.f, 0.f};
                 cur[0] += scale * ak[0][r];
                 cur[1] += scale * ak[1][r];
                 cur[2] += scale * ak[2][r];
@@ -1588,7 +1594,7 @@ sdpa_fbwd_dkdv_hd64(const float *__restrict__ q, const float *__restrict__ k, co
             }
             if (dv) {
                 f4 *o = (f4 *)(dv + (kbase + key) * 64 + 4 * li);
-                f4 cur = *o;
+                f4 cur = beta ? *o : f4{0.f, 0.f, 0.f, 0.f};
                 cur[0] += av[0][r];
                 cur[1] += av[1][r];
                 cur[2] += av[2][r];

@@ -89,6 +89,38 @@ def test_gpt2_grads(n_layer, C, H, V, npos, B, T):
         lib.ncm_tape_free(tape)
 
 
+@pytest.mark.parametrize("n_layer,C,H,V,npos,B,T", CASES)
+def test_gpt2_grads_reused_tape(n_layer, C, H, V, npos, B, T):
+    """The backward writes most activation gradients instead of accumulating
+    them into cleared buffers, and reuses those buffers across steps: a step
+    on other ids in between must not leak into the next step's gradients
+    (bit for bit equal to the first run on the same ids)."""
+    lib = ncmhip.load()
+    params, ids, tgt = case(13, n_layer, C, H, V, npos, B, T)
+    _, ids2, tgt2 = case(14, n_layer, C, H, V, npos, B, T)
+    cfg = ncmhip.Gpt2Config(n_layer, C, H, V, npos)
+    P = [D.from_numpy(p) for p in params]
+    sizes = (ctypes.c_int64 * len(P))(*[p.size for p in params])
+    tape = lib.ncm_tape_new()
+    try:
+        runs = []
+        for x, y in ((ids, tgt), (ids2, tgt2), (ids, tgt)):
+            G = [D.from_numpy(np.zeros_like(p)) for p in params]
+            lib.ncm_tape_clear(tape)
+            lib.arena_reset()
+            logits = lib.ncm_gpt2_forward(tape, ctypes.byref(cfg), ncmhip.ptr_array(P), x.ctypes.data, B, T)
+            loss = D.empty(1)
+            lib.ncm_t_ce(tape, logits, y.ctypes.data, None, loss.ptr, None, B * T, V, 1.0)
+            lib.ncm_tape_backward(tape, ctypes.byref(PMap(ncmhip.ptr_array(P), ncmhip.ptr_array(G), sizes, len(P))))
+            ncmhip.check()
+            runs.append([g.numpy() for g in G])
+        for i, (a, c) in enumerate(zip(runs[0], runs[2])):
+            assert np.array_equal(a.view(np.uint32), c.view(np.uint32)), i
+        assert any(not np.array_equal(a, b) for a, b in zip(runs[0], runs[1]))
+    finally:
+        lib.ncm_tape_free(tape)
+
+
 def test_gpt2_train_steps():
     lib = ncmhip.load()
     n_layer, C, H, V, npos, B, T = 1, 256, 4, 512, 64, 2, 64

@@ -3,6 +3,7 @@
 
 #include <limits.h>
 #include <math.h>
+#include <stdlib.h>
 
 /* kernels.c:731-735, on a HOST row, as the reference: strict '>' from index 0. */
 int argmax_row(const float *x, int n) {
@@ -215,6 +216,110 @@ void embedding_fwd(const float *W, const int *idx, float *y, int64_t n, int D) {
 
 /* ---- SDPA (kernels.c:364-507) ---- */
 /* out [B][Hq][Tq][hd], or [B][Tq][Hq * hd] (the heads merged) when merged */
+/* Key-split attention for grids that cannot fill the chip (few (b, h) pairs
+ * and long rows, e.g. a single-sequence prefill): each query tile's key range
+ * is cut into parts of at most P key blocks, sized for about four workgroups
+ * per CU, and sdpa_hd64_combine merges the parts of the tiles that were cut.
+ * The work and tile lists depend only on the shape and are built once per
+ * shape (a few cached) on the device.  Returns 0 when launched, 1 when the
+ * unsplit kernel should run (the grid already fills the chip, or no tile is
+ * long enough to cut). */
+#define SPLIT_MAXP 8
+typedef struct { int B, Hq, Tq, Tkv, causal; int4 *work; int2 *tiles; int nwork, nsplit, nslots; } SplitPlan;
+static SplitPlan g_split[4];
+static int g_split_next;
+
+static int sdpa_split(const float *q, const float *k, const float *v, const float *mask, float *out, int B, int Hq,
+                      int Hkv, int Tq, int Tkv, float scale, int causal, int merged) {
+    const int ntiles = (Tq + 63) / 64, C = ncm_cu_count();
+    const int64_t BH = (int64_t)B * Hq;
+    if (BH * ntiles >= 2 * (int64_t)C || BH > INT_MAX / 4096) return 1;
+    SplitPlan *sp = NULL;
+    for (int i = 0; i < 4; i++)
+        if (g_split[i].work && g_split[i].B == B && g_split[i].Hq == Hq && g_split[i].Tq == Tq &&
+            g_split[i].Tkv == Tkv && g_split[i].causal == causal)
+            sp = &g_split[i];
+    if (!sp) {
+        int *nkb = (int *)malloc((size_t)ntiles * sizeof(int));
+        if (!nkb) return 1;
+        int64_t units = 0;
+        int maxb = 0;
+        for (int t = 0; t < ntiles; t++) {
+            const int kend = causal ? (t * 64 + 64 + (Tkv - Tq) < Tkv ? t * 64 + 64 + (Tkv - Tq) : Tkv) : Tkv;
+            nkb[t] = (kend + 63) / 64;
+            units += nkb[t];
+            if (nkb[t] > maxb) maxb = nkb[t];
+        }
+        int P = (int)((BH * units + 4 * (int64_t)C - 1) / (4 * (int64_t)C));
+        if (P < (maxb + SPLIT_MAXP - 1) / SPLIT_MAXP) P = (maxb + SPLIT_MAXP - 1) / SPLIT_MAXP;
+        if (P < 2) P = 2;
+        if (P >= maxb) { free(nkb); return 1; }
+        int nwork = 0, nsplit = 0, nslots = 0;
+        for (int t = 0; t < ntiles; t++) {
+            const int np = (nkb[t] + P - 1) / P;
+            nwork += np;
+            if (np > 1) { nsplit++; nslots += np; }
+        }
+        int4 *work = (int4 *)malloc((size_t)nwork * sizeof(int4));
+        int2 *tiles = (int2 *)malloc((size_t)(nsplit + 1) * sizeof(int2));
+        if (!work || !tiles) { free(nkb); free(work); free(tiles); return 1; }
+        int w = 0, st = 0, slot = 0;
+        /* longest parts first: part lengths P, P - 1, ..., 1 in turn */
+        for (int len = P; len >= 1; len--)
+            for (int t = ntiles - 1; t >= 0; t--) {
+                const int np = (nkb[t] + P - 1) / P;
+                for (int p = 0; p < np; p++) {
+                    const int l = nkb[t] - p * P < P ? nkb[t] - p * P : P;
+                    if (l != len) continue;
+                    work[w].x = t; work[w].y = p * P; work[w].z = l; work[w].w = -1;
+                    w++;
+                }
+            }
+        for (int t = 0; t < ntiles; t++) {   /* slots of the cut tiles, in tile order */
+            const int np = (nkb[t] + P - 1) / P;
+            if (np < 2) continue;
+            tiles[st].x = t; tiles[st].y = slot;
+            for (int i = 0; i < nwork; i++)
+                if (work[i].x == t) work[i].w = slot + work[i].y / P;
+            slot += np;
+            st++;
+        }
+        tiles[nsplit].x = 0; tiles[nsplit].y = nslots;
+        free(nkb);
+        sp = &g_split[g_split_next];
+        g_split_next = (g_split_next + 1) % 4;
+        if (sp->work) { ncm_hip_sync(); ncm_hip_free(sp->work); ncm_hip_free(sp->tiles); }
+        sp->work = (int4 *)ncm_hip_malloc((size_t)nwork * sizeof(int4));
+        sp->tiles = (int2 *)ncm_hip_malloc((size_t)(nsplit + 1) * sizeof(int2));
+        if (!sp->work || !sp->tiles) {
+            free(work); free(tiles);
+            if (sp->work) ncm_hip_free(sp->work);
+            if (sp->tiles) ncm_hip_free(sp->tiles);
+            sp->work = NULL; sp->tiles = NULL;
+            return 1;
+        }
+        mem_h2d(sp->work, work, (size_t)nwork * sizeof(int4));
+        mem_h2d(sp->tiles, tiles, (size_t)(nsplit + 1) * sizeof(int2));
+        free(work);
+        free(tiles);
+        sp->B = B; sp->Hq = Hq; sp->Tq = Tq; sp->Tkv = Tkv; sp->causal = causal;
+        sp->nwork = nwork; sp->nsplit = nsplit; sp->nslots = nslots;
+    }
+    if ((int64_t)sp->nwork * BH > INT_MAX) return 1;
+    float *part = (float *)ncm_workspace(WS_ATTN, (size_t)BH * sp->nslots * 64 * 66 * sizeof(float));
+    if (!part) return -1;
+    float *part_o = part, *part_ml = part + (size_t)BH * sp->nslots * 64 * 64;
+    int bh = (int)BH, nslots = sp->nslots;
+    void *a[] = {&q, &k, &v, &mask, &out, &Hq, &Hkv, &Tq, &Tkv, &scale, &causal, &merged, &sp->work, &bh, &nslots,
+                 &part_o, &part_ml};
+    if (ncm_launch_named("sdpa_hd64_split", (unsigned)(sp->nwork * BH), 1, 1, 256, a)) return -1;
+    if (sp->nsplit > 0) {
+        void *a2[] = {&sp->tiles, &part_o, &part_ml, &out, &Hq, &Tq, &merged, &nslots};
+        if (ncm_launch_named("sdpa_hd64_combine", (unsigned)sp->nsplit, (unsigned)BH, 1, 256, a2)) return -1;
+    }
+    return 0;
+}
+
 static void sdpa_any(const char *fn, const float *q, const float *k, const float *v, const float *mask, float *out,
                      int B, int Hq, int Hkv, int Tq, int Tkv, int hd, int causal, int merged, float *stats) {
     if (B < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || Tq < 0 || Tkv <= 0 || hd <= 0 || hd > 256) {
@@ -231,6 +336,7 @@ static void sdpa_any(const char *fn, const float *q, const float *k, const float
     if (ncm_ready()) return;
     float scale = 1.0f / sqrtf((float)hd);
     if (hd == 64 && is_aligned16(q) && is_aligned16(k) && is_aligned16(v) && is_aligned16(out)) {
+        if (!stats && sdpa_split(q, k, v, mask, out, B, Hq, Hkv, Tq, Tkv, scale, causal, merged) <= 0) return;
         void *a[] = {&q, &k, &v, &mask, &out, &Hq, &Hkv, &Tq, &Tkv, &scale, &causal, &merged, &stats};
         ncm_launch_named("sdpa_hd64", (unsigned)Hq, (unsigned)B, (unsigned)((Tq + 63) / 64), 256, a);
     } else if (stats) {

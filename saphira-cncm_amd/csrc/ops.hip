@@ -390,20 +390,24 @@ eltwise4_k(const float *a, const float *b, float *y, float s, int64_t n4, int op
 #define SD_T 64
 #define SD_LD (64 + 8)
 
-extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4)))
-sdpa_hd64(const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
-          const float *__restrict__ mask, float *__restrict__ out, int Hq, int Hkv, int Tq, int Tkv,
-          float scale, int causal, int merged, float *__restrict__ stats) {
+// The loop of one workgroup: queries q0 .. q0 + 63 of (b, h) over the key
+// blocks [kb_lo, kb_hi) (64 keys each) of the range the query tile sees.
+// part_o == nullptr: the whole range -- the output is normalised and stored
+// (and the row statistics when asked for); otherwise a part of a split range:
+// the unnormalised O rows and each query's (max, sum) go to the part's slot
+// for sdpa_hd64_combine.
+__device__ __forceinline__ void sdpa_hd64_body(const float *__restrict__ q, const float *__restrict__ k,
+                                               const float *__restrict__ v, const float *__restrict__ mask,
+                                               float *__restrict__ out, int Hq, int Hkv, int Tq, int Tkv,
+                                               float scale, int causal, int merged, float *__restrict__ stats,
+                                               int h, int b, int q0, int kb_lo, int kb_hi,
+                                               float *__restrict__ part_o, float *__restrict__ part_ml) {
     __shared__ __attribute__((aligned(16))) float sK[SD_T * SD_LD];
     __shared__ __attribute__((aligned(16))) float sV[SD_T * SD_LD];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
-    // grid (Hq, B, query tiles), the last query tile first: under a causal
-    // mask it has the most key tiles, and dispatching the heaviest workgroups
-    // first keeps the chip busy to the end (longest-first order)
-    const int h = blockIdx.x, b = blockIdx.y;
     const int kvh = h / (Hq / Hkv);
-    const int q0 = (gridDim.z - 1 - blockIdx.z) * 64, qw = q0 + wave * 16;
+    const int qw = q0 + wave * 16;
     const float *qb = q + ((int64_t)b * Hq + h) * Tq * 64;
     const float *kb = k + ((int64_t)b * Hkv + kvh) * Tkv * 64;
     const float *vb = v + ((int64_t)b * Hkv + kvh) * Tkv * 64;
@@ -427,7 +431,8 @@ sdpa_hd64(const float *__restrict__ q, const float *__restrict__ k, const float 
     // K and V tiles (64 keys x 64 d, rows beyond Tkv as zero), staged through
     // LDS; no register prefetch of the next tile, so the kernel stays under
     // 128 registers and four workgroups share a CU
-    for (int k0 = 0; k0 < kend; k0 += SD_T) {
+    kend = min(kend, kb_hi * SD_T);
+    for (int k0 = kb_lo * SD_T; k0 < kend; k0 += SD_T) {
         __syncthreads();
         // all eight loads in flight at once (keys past Tkv read key Tkv - 1 and
         // are stored as zero), then the LDS stores.  Thread tid stages rows
@@ -511,6 +516,19 @@ sdpa_hd64(const float *__restrict__ q, const float *__restrict__ k, const float 
             }
     }
 
+    if (part_o) {   // a part of a split range: unnormalised rows and (max, sum)
+        if (lg == 0 && my_q < Tq) {
+            part_ml[(wave * 16 + li) * 2] = m_run;
+            part_ml[(wave * 16 + li) * 2 + 1] = l_run;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = wave * 16 + 4 * lg + r;
+            f4 val = {o[0][r], o[1][r], o[2][r], o[3][r]};
+            *(f4 *)(part_o + row * 64 + 4 * li) = val;
+        }
+        return;
+    }
     // the row statistics a recomputing backward needs: (max, sum) of query my_q
     if (stats && lg == 0 && my_q < Tq) {
         float *st = stats + (((int64_t)b * Hq + h) * Tq + my_q) * 2;
@@ -529,6 +547,88 @@ sdpa_hd64(const float *__restrict__ q, const float *__restrict__ k, const float 
                     4 * li) = val;
         }
     }
+}
+
+extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4)))
+sdpa_hd64(const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+          const float *__restrict__ mask, float *__restrict__ out, int Hq, int Hkv, int Tq, int Tkv,
+          float scale, int causal, int merged, float *__restrict__ stats) {
+    // grid (Hq, B, query tiles), the last query tile first: under a causal
+    // mask it has the most key tiles, and dispatching the heaviest workgroups
+    // first keeps the chip busy to the end (longest-first order)
+    sdpa_hd64_body(q, k, v, mask, out, Hq, Hkv, Tq, Tkv, scale, causal, merged, stats, blockIdx.x, blockIdx.y,
+                   (gridDim.z - 1 - blockIdx.z) * 64, 0, (Tkv + SD_T - 1) / SD_T, nullptr, nullptr);
+}
+
+// The same over a work list, for grids too small to fill the chip (few (b, h)
+// pairs, long rows): a query tile's key range is cut into parts of at most
+// a fixed number of key blocks.  work[i] = (query tile, first key block, key
+// blocks, slot): slot < 0 -- the tile's only part, stored as sdpa_hd64 does;
+// otherwise the part's unnormalised rows go to part_o[bh][slot][64][64] and
+// its (max, sum) to part_ml[bh][slot][64][2].  Workgroup x: work item x / BH,
+// (b, h) pair x % BH, BH = B * Hq (the list is sorted longest part first).
+extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4)))
+sdpa_hd64_split(const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+                const float *__restrict__ mask, float *__restrict__ out, int Hq, int Hkv, int Tq, int Tkv,
+                float scale, int causal, int merged, const int4 *__restrict__ work, int BH, int nslots,
+                float *__restrict__ part_o, float *__restrict__ part_ml) {
+    const int bh = blockIdx.x % BH;
+    const int4 w = work[blockIdx.x / BH];
+    const int h = bh % Hq, b = bh / Hq;
+    float *po = w.w < 0 ? nullptr : part_o + ((int64_t)bh * nslots + w.w) * 64 * 64;
+    float *pm = w.w < 0 ? nullptr : part_ml + ((int64_t)bh * nslots + w.w) * 64 * 2;
+    sdpa_hd64_body(q, k, v, mask, out, Hq, Hkv, Tq, Tkv, scale, causal, merged, nullptr, h, b, w.x * 64, w.y,
+                   w.y + w.z, po, pm);
+}
+
+// Merge of the parts of a split query tile: workgroup (tile x of the list
+// tiles[], (b, h) pair y); thread = (query tid / 4, d = 16 (tid % 4) .. +15).
+// m = max m_p, w_p = e^(m_p - m) (0 for a part whose keys were all masked),
+// out = sum_p w_p o_p / sum_p w_p l_p.  A tile has at most SPLIT_MAXP parts;
+// every part's loads are issued before the first use (clamped part index,
+// weight 0 past the last part).
+#define SPLIT_MAXP 8
+extern "C" __global__ void __launch_bounds__(256)
+sdpa_hd64_combine(const int2 *__restrict__ tiles, const float *__restrict__ part_o, const float *__restrict__ part_ml,
+                  float *__restrict__ out, int Hq, int Tq, int merged, int nslots) {
+    const int2 t = tiles[blockIdx.x];   // (query tile, first slot); parts = next entry's slot - this one's
+    const int np = tiles[blockIdx.x + 1].y - t.y;
+    const int bh = blockIdx.y, h = bh % Hq, b = bh / Hq;
+    const int r = threadIdx.x >> 2, d0 = (threadIdx.x & 3) * 16;
+    const int qi = t.x * 64 + r;
+    if (qi >= Tq) return;
+    const float *ml = part_ml + ((int64_t)bh * nslots + t.y) * 64 * 2 + r * 2;
+    const float *po = part_o + ((int64_t)bh * nslots + t.y) * 64 * 64 + r * 64 + d0;
+    float mp[SPLIT_MAXP], lp[SPLIT_MAXP];
+    f4 op[SPLIT_MAXP][4];
+#pragma unroll
+    for (int p = 0; p < SPLIT_MAXP; ++p) {
+        const int pc = min(p, np - 1);
+        mp[p] = ml[(int64_t)pc * 64 * 2];
+        lp[p] = ml[(int64_t)pc * 64 * 2 + 1];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) op[p][u] = *(const f4 *)(po + (int64_t)pc * 64 * 64 + 4 * u);
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int p = 0; p < SPLIT_MAXP; ++p)
+        if (p < np) m = fmaxf(m, mp[p]);
+    float l = 0.f;
+    f4 acc[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[u] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int p = 0; p < SPLIT_MAXP; ++p) {
+        if (p >= np) continue;
+        const float wp = mp[p] == -INFINITY ? 0.f : __expf(mp[p] - m);
+        l += lp[p] * wp;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[u] += op[p][u] * wp;
+    }
+    const float inv = 1.0f / l;
+    float *o = out + (merged ? ((int64_t)b * Tq + qi) * Hq + h : ((int64_t)b * Hq + h) * Tq + qi) * 64 + d0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) *(f4 *)(o + 4 * u) = acc[u] * inv;
 }
 
 // Generic SDPA for any hd <= 256: one wave per query row, online softmax in

@@ -210,6 +210,27 @@ def test_sdpa_causal(B, Hq, Hkv, Tq, Tkv, hd):
     check_sdpa(gpu_sdpa(q, k, v, causal=True), ref)
 
 
+def test_sdpa_key_split():
+    """Grids that cannot fill the chip cut each query tile's keys into parts
+    merged afterwards: a causal 1024-token single sequence (up to 8 parts per
+    tile), and a masked long-key case where whole parts are masked out (their
+    max is -inf and they must weigh nothing), head-major and merged output."""
+    B, Hq, Hkv, T = 1, 4, 2, 1024
+    q, k, v = rnd(40, B, Hq, T, 64), rnd(41, B, Hkv, T, 64), rnd(42, B, Hkv, T, 64)
+    check_sdpa(gpu_sdpa(q, k, v, causal=True), O.sdpa_gqa(q, k, v, causal_mask(T, T)))
+    Tq, Tkv = 100, 700
+    q, k, v = rnd(43, 1, 2, Tq, 64), rnd(44, 1, 1, Tkv, 64), rnd(45, 1, 1, Tkv, 64)
+    m = np.zeros((Tq, Tkv), np.float32)
+    m[:, 128:384] = -np.inf
+    m[::3, 500:] = -np.inf
+    ref = O.sdpa_gqa(q, k, v, m)
+    check_sdpa(gpu_sdpa(q, k, v, mask=m), ref)
+    out = D.empty((1, Tq, 2 * 64))
+    ncmhip.call("sdpa_fwd_gqa_merged", D.from_numpy(q), D.from_numpy(k), D.from_numpy(v), D.from_numpy(m), out, 1,
+                2, 1, Tq, Tkv, 64)
+    check_sdpa(out.numpy().reshape(1, Tq, 2, 64).transpose(0, 2, 1, 3), ref)
+
+
 def test_sdpa_additive_mask_and_large_scores():
     B, Hq, Hkv, Tq, Tkv, hd = 1, 4, 2, 70, 90, 64
     q, k, v = rnd(7, B, Hq, Tq, hd, scale=4.0), rnd(8, B, Hkv, Tkv, hd, scale=4.0), rnd(9, B, Hkv, Tkv, hd)

@@ -319,6 +319,46 @@ heads_transpose_rows_k(const float *__restrict__ in, float *__restrict__ out, in
     }
 }
 
+// A prefill's q, k, v rows (from their GEMMs, [T][H hd] and [T][K hd]) to
+// attention layout with RoPE, and k, v into the KV cache: one workgroup per
+// position t, one rotation pair (d, d + hd/2) per thread and pass.  The
+// operations are heads_transpose_fwd's copies and rope_k's float operations
+// (y[d] = a c[d] + (-b) s[d], y[d + h] = b c[d + h] + a s[d + h]); qq
+// [H][T][hd], kk / vv [K][T][hd], kc / vc [K][ld][hd] at row t.
+extern "C" __global__ void __launch_bounds__(256)
+qkv_rope_cache_k(const float *__restrict__ ql, const float *__restrict__ kl, const float *__restrict__ vl,
+                 float *__restrict__ qq, float *__restrict__ kk, float *__restrict__ vv, float *__restrict__ kc,
+                 float *__restrict__ vc, const float *__restrict__ cos_t, const float *__restrict__ sin_t, int T,
+                 int H, int K, int hd, int ld) {
+#pragma clang fp contract(off)
+    const int t = blockIdx.x, h2 = hd >> 1;
+    const float *co = cos_t + (int64_t)t * hd, *si = sin_t + (int64_t)t * hd;
+    // q and k rotation pairs: H + K heads of h2 pairs; then v: K heads of hd
+    for (int i = threadIdx.x; i < (H + K) * h2; i += 256) {
+        const int hh = i / h2, d = i - hh * h2;
+        const bool isq = hh < H;
+        const int head = isq ? hh : hh - H;
+        const float *src = isq ? ql + ((int64_t)t * H + head) * hd : kl + ((int64_t)t * K + head) * hd;
+        const float a = src[d], b = src[d + h2];
+        const float y0 = a * co[d] + (-b) * si[d];
+        const float y1 = b * co[d + h2] + a * si[d + h2];
+        float *dst = isq ? qq + ((int64_t)head * T + t) * hd : kk + ((int64_t)head * T + t) * hd;
+        dst[d] = y0;
+        dst[d + h2] = y1;
+        if (!isq) {
+            float *c = kc + ((int64_t)head * ld + t) * hd;
+            c[d] = y0;
+            c[d + h2] = y1;
+        }
+    }
+    for (int i = threadIdx.x; i < K * hd; i += 256) {
+        const int head = i / hd, d = i - head * hd;
+        const float x = vl[((int64_t)t * K + head) * hd + d];
+        vv[((int64_t)head * T + t) * hd + d] = x;
+        vc[((int64_t)head * ld + t) * hd + d] = x;
+    }
+}
+
 // embedding_fwd (kernels.c:59-74): y[i,:] = W[idx[i],:]; ids outside [0, V)
 // read row 0 (the reference would read out of bounds).
 extern "C" __global__ void __launch_bounds__(256)

@@ -212,16 +212,16 @@ float *ncm_qwen_forward(NcmQwen *m, const int *ids, int T, int last_only) {
         linear_fwd(h1, w[1], w[2], ql, T, C, C);
         linear_fwd(h1, w[3], w[4], kl, T, K * hd, C);
         linear_fwd(h1, w[5], w[6], vl, T, K * hd, C);
-        heads_transpose_fwd(ql, qq, T, H, hd);
-        heads_transpose_fwd(kl, kk, T, K, hd);
-        heads_transpose_fwd(vl, vv, T, K, hd);
-        rope_apply_gqa(qq, kk, m->cos_t, m->sin_t, 1, H, K, T, hd);
-        sdpa_fwd_gqa_causal(qq, kk, vv, ctx, 1, H, K, T, T, hd);
-        /* keep k, v for the cached decode: [K][T][hd] -> cache [K][n_ctx][hd] */
-        const size_t pitch = (size_t)c->n_ctx * hd * sizeof(float), row = (size_t)T * hd * sizeof(float);
+        /* heads to [H][T][hd] with RoPE, and k, v also into the KV cache for
+         * the cached decode: [K][T][hd] at rows 0..T-1 of [K][n_ctx][hd] */
         float *kc = m->kcache + (size_t)li * K * c->n_ctx * hd, *vc = m->vcache + (size_t)li * K * c->n_ctx * hd;
-        HIP_TRY_NULL(hipMemcpy2DAsync(kc, pitch, kk, row, row, K, hipMemcpyDeviceToDevice, ncm_stream()));
-        HIP_TRY_NULL(hipMemcpy2DAsync(vc, pitch, vv, row, row, K, hipMemcpyDeviceToDevice, ncm_stream()));
+        {
+            int ld = c->n_ctx;
+            void *a[] = {&ql, &kl, &vl, &qq, &kk, &vv, &kc, &vc, &m->cos_t, &m->sin_t, &T, (void *)&H, (void *)&K,
+                         (void *)&hd, &ld};
+            if (ncm_launch_named("qkv_rope_cache_k", (unsigned)T, 1, 1, 256, a)) return NULL;
+        }
+        sdpa_fwd_gqa_causal(qq, kk, vv, ctx, 1, H, K, T, T, hd);
         head_merge_fwd(ctx, mo, 1, T, C, H, hd);
         linear_fwd_ep(mo, w[7], NULL, h, x1, T, C, C, NCM_ACT_NONE);   /* x1 = h + mo W^T */
         rmsnorm_fwd(x1, w[8], h2, T, C);

@@ -5,7 +5,9 @@ Workload (the configuration the headline metric "linear
 GEMM TFLOP/s" is quoted on): Y = X W^T + b, dX = dY W, dW = dY^T X, db for
 M in {1, 64, 512, 4096} x (K -> N) in {768->2304, 768->3072, 3072->768,
 896->4864, 4864->896}; X ~ N(0,1), W ~ N(0,1/K), b ~ N(0,0.02), dY ~ N(0,1).
-One step = all 20 shapes x {forward, dX, dW, db} (80 library calls).  Every
+One step = all 20 shapes x {forward, dX, dW with db} (60 library calls: dW
+and db are requested by one linear_bwd call, as a layer's backward asks for
+them, and for batches above 8 one GEMM launch computes both).  Every
 (shape, M) owns its own buffers (~1.3 GB in total, far above the 256 MB
 Infinity Cache), so each call starts cold, as the M=1 GEMV rule requires.
 
@@ -73,7 +75,7 @@ def build_workload(ncmhip, seed=0, only=None):
             flops = 2.0 * M * N * K
             fwd_k, fwd_s = ncmhip.linear_plan("fwd", M, N, K)
             dx_k, dx_s = ncmhip.linear_plan("dx", M, N, K)
-            dw_k, dw_s = ncmhip.linear_plan("dw", M, N, K)
+            dw_k, dw_s = ncmhip.linear_plan("dwdb", M, N, K)
             # (kernel, flops, label, call, single-kernel call?)
             calls.append((fwd_k, flops, f"fwd M={M} {K}->{N}",
                           lambda x=x, W=W, b=b, y=y, M=M, N=N, K=K: ncmhip.linear_fwd(x, W, b, y, M, N, K),
@@ -81,21 +83,20 @@ def build_workload(ncmhip, seed=0, only=None):
             calls.append((dx_k, flops, f"dX M={M} {K}->{N}",
                           lambda x=x, W=W, dy=dy, dx=dx, M=M, N=N, K=K:
                           ncmhip.linear_bwd(x, W, dy, dx, None, None, M, N, K), dx_s == 1 and M > 8))
-            calls.append((dw_k, flops, f"dW M={M} {K}->{N}",
-                          lambda x=x, W=W, dy=dy, dW=dW, M=M, N=N, K=K:
-                          ncmhip.linear_bwd(x, W, dy, None, dW, None, M, N, K), dw_s == 1))
-            calls.append(("colsum_small" if M <= 512 else "colsum_partial_v", 0.0, f"db M={M} {K}->{N}",
-                          lambda x=x, W=W, dy=dy, db=db, M=M, N=N, K=K:
-                          ncmhip.linear_bwd(x, W, dy, None, None, db, M, N, K), False))
+            # dW and db from one linear_bwd call (for batches above 8 one GEMM
+            # launch sums both); a batch of at most 8 adds the column-sum launch
+            calls.append((dw_k, flops, f"dW+db M={M} {K}->{N}",
+                          lambda x=x, W=W, dy=dy, dW=dW, db=db, M=M, N=N, K=K:
+                          ncmhip.linear_bwd(x, W, dy, None, dW, db, M, N, K), dw_s == 1 and M > 8))
     if only is not None:
         calls = [c for c in calls if c[2] in only]
     return calls, keep
 
 
 def algo_bytes(labels):
-    """Mean algorithmic HBM bytes per call over sweep labels ("fwd|dX|dW M=m
-    k->n"): each operand read once, each output written once, and the
-    accumulated gradient (dX or dW) also read once."""
+    """Mean algorithmic HBM bytes per call over sweep labels ("fwd|dX|dW+db
+    M=m k->n"): each operand read once, each output written once, and the
+    accumulated gradients (dX, or dW and db) also read once."""
     tot = 0.0
     for lab in labels:
         op, m, kn = lab.split()
@@ -106,7 +107,7 @@ def algo_bytes(labels):
         elif op == "dX":
             b = M * N + N * K + 2 * M * K
         else:
-            b = M * N + M * K + 2 * N * K
+            b = M * N + M * K + 2 * N * K + 2 * N
         tot += 4.0 * b
     return tot / len(labels)
 

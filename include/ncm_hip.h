@@ -136,9 +136,10 @@ void linear_bwd(const float *x, const float *W, const float *dy,
                 float *dx, float *dW, float *db, int64_t batch, int M, int K);
 
 /* extension: which kernel a linear call launches (op 0 = linear_fwd,
- * 1 = dX of linear_bwd, 2 = dW of linear_bwd) for 16-byte aligned operands,
- * written to `kernel`; returns the number of K splits (>= 1; a split
- * count above 1 adds a splitk_reduce launch), -1 on bad arguments. */
+ * 1 = dX of linear_bwd, 2 = dW of linear_bwd, 3 = dW and db of one
+ * linear_bwd call: the dW GEMM then also sums db) for 16-byte aligned
+ * operands, written to `kernel`; returns the number of K splits (>= 1; a
+ * split count above 1 adds a fixup launch), -1 on bad arguments. */
 int ncm_hip_linear_plan(int op, int64_t batch, int M, int K, char *kernel, size_t cap);
 
 /* ------------------------------------------------------------------ */

@@ -69,6 +69,9 @@ struct GemmArgs {
     const float *bias2;  // GATED: its bias or null
     int beta;            // ACCUM: 1 C += acc; 0 C = 0.0f + acc, the first write of a gradient (the bits of an
                          // accumulation into zeros, without reading C or clearing it first)
+    float *db;           // dW (vectorised kernel) or null: db[i] += 0.0f + (float)(fp64 sum over k of A(i,k)),
+                         // the bias gradient, from the A slabs of the tiles in tile column 0
+    double *dbpart;      // its per-segment fp64 partials of split tiles [units][64]
 };
 
 // Grouped raster: GROUP_M tile rows advance together along N so that the B
@@ -746,7 +749,7 @@ __device__ __forceinline__ void g_epilogue_blk_act(const GemmArgs &p, const f4 &
 // of a thread's segment loads are issued before the first add: the launch
 // is one round trip of latency, not one per segment.
 #define FIXUP_MAX_SEGS 16
-template <int EPI, bool IA, bool IB>
+template <int EPI, bool IA, bool IB, bool DB>
 __device__ __forceinline__ void gemm_tile_fixup_body(const GemmArgs &p) {
     const int tid = threadIdx.x, tail = blockIdx.x >> 2, blk = blockIdx.x & 3;
     int tm, tn;
@@ -761,7 +764,24 @@ __device__ __forceinline__ void gemm_tile_fixup_body(const GemmArgs &p) {
 #pragma unroll
     for (int s = 1; s < FIXUP_MAX_SEGS; ++s) tot = s < p.segs ? tot + part[s] : tot;
     const int a = blk >> 1, b = blk & 1, i0 = tm * 64, j0 = tn * 64;
-    if (EPI == EPI_ACCUM) { g_epilogue_blk_act<EPI, ACT_NONE, IA, IB>(p, tot, a, b, i0, j0, tid); return; }
+    if (EPI == EPI_ACCUM) {
+        g_epilogue_blk_act<EPI, ACT_NONE, IA, IB>(p, tot, a, b, i0, j0, tid);
+        // dW: the bias gradient of a split tile in tile column 0, from its
+        // segments' fp64 partials in segment order
+        if (DB && p.db != nullptr && tn == 0 && blk == 0 && tid < 64) {
+            const double *q = p.dbpart + (int64_t)tail * p.segs * 64 + tid;
+            double dp[FIXUP_MAX_SEGS];
+#pragma unroll
+            for (int s = 0; s < FIXUP_MAX_SEGS; ++s) dp[s] = q[(int64_t)min(s, p.segs - 1) * 64];
+            const int i = min(i0 + tid, p.Mo - 1);
+            const float old = p.db[i];
+            double sum = dp[0];
+#pragma unroll
+            for (int s = 1; s < FIXUP_MAX_SEGS; ++s) sum = s < p.segs ? sum + dp[s] : sum;
+            if (i0 + tid < p.Mo) p.db[i] = old + (0.0f + (float)sum);
+        }
+        return;
+    }
     switch (p.act) {
     case ACT_SILU: g_epilogue_blk_act<EPI, ACT_SILU, IA, IB>(p, tot, a, b, i0, j0, tid); break;
     case ACT_GELU: g_epilogue_blk_act<EPI, ACT_GELU, IA, IB>(p, tot, a, b, i0, j0, tid); break;
@@ -809,7 +829,13 @@ __device__ __forceinline__ void g_gated_out(const GemmArgs &p, const f4 (&g)[2][
 // slab, barrier (every wave's loads have landed and every read of the
 // current stage is done), fragment reads of the next slab's chunk 0, loads of
 // the slab after next into the current stage, MFMAs of chunk 1.
-template <bool AKC, bool BKC, int EPI>
+template <bool V>
+struct BoolTag {
+    static constexpr bool value = V;
+};
+
+// DB: the dW kernel that also sums the bias gradient (p.db)
+template <bool AKC, bool BKC, int EPI, bool DB = false>
 __device__ __forceinline__ void gemm_dma_body(const GemmArgs &p) {
     __shared__ __attribute__((aligned(16))) float sm[2 * 2 * D_SLAB];   // [stage][A | B]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -860,6 +886,19 @@ __device__ __forceinline__ void gemm_dma_body(const GemmArgs &p) {
 #pragma unroll
                 for (int b = 0; b < 2; ++b) acc[a][b] = mfma4(fa[a][s], fb[b][s], acc[a][b]);
     };
+    // dW with the bias gradient (DB kernels): A(i,k) = dy[k][i], so the
+    // tiles of tile column 0 also sum their A fragments over k, in fp64, for
+    // the column sums of dy.  Lane (li, lg) of wave (wm, wn) holds rows
+    // wm 32 + 2 li and 2 li + 1 (blocks t = 0, 1) and, of every 16-wide k
+    // chunk, k rows 4 lg .. 4 lg + 3 (steps s); both waves of a wm read the
+    // same fragments, so wave wn sums block t = wn, into one accumulator per
+    // step (no dependent chain inside a chunk).  The fragments of slabs past
+    // the segment's (or the matrix's) end are zeros.  Those tiles run their
+    // own copy of the k loop, so no other tile (and no other kernel) carries
+    // the work or a branch in it.
+    const bool dsum = DB && p.db != nullptr && tn == 0;
+    const bool wodd = __builtin_amdgcn_readfirstlane(wn) != 0;
+    double ds[4] = {0.0, 0.0, 0.0, 0.0};
     float *const sA0 = sm, *const sB0 = sm + D_SLAB, *const sA1 = sm + 2 * D_SLAB, *const sB1 = sm + 3 * D_SLAB;
 
     float f0a[2][4], f0b[2][4], f1a[2][4], f1b[2][4];
@@ -871,38 +910,67 @@ __device__ __forceinline__ void gemm_dma_body(const GemmArgs &p) {
     d_frags<BKC>(sB0, wn, li, lg, 0, f0b);
     la.load(ra, sA1, wave, (it0 + 1) * GEMM_BK, p.lda);
     lb.load(rb, sB1, wave, (it0 + 1) * GEMM_BK, p.ldb);
-    for (int kt = it0; kt < it1; kt += 4) {
+    auto kloop = [&](auto ds_tag) {
+        constexpr bool DS = decltype(ds_tag)::value;
+        auto colsum = [&](const float (&fa)[2][4]) {
+            if constexpr (DS) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            // it0 is a multiple of 4: slab kt+u lives in stage u & 1
-            float *const ca = (u & 1) ? sA1 : sA0, *const cb = (u & 1) ? sB1 : sB0;
-            float *const na = (u & 1) ? sA0 : sA1, *const nb = (u & 1) ? sB0 : sB1;
-            d_frags<AKC>(ca, wm, li, lg, 1, f1a);
-            d_frags<BKC>(cb, wn, li, lg, 1, f1b);
-            __builtin_amdgcn_sched_barrier(0);
-            mfmas(f0a, f0b);
-            __builtin_amdgcn_sched_barrier(0);
-            __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's loads of slab kt+u+1
-            __syncthreads();
-            d_frags<AKC>(na, wm, li, lg, 0, f0a);
-            d_frags<BKC>(nb, wn, li, lg, 0, f0b);
-            __builtin_amdgcn_sched_barrier(0);
-            la.load(ra, ca, wave, (kt + u + 2) * GEMM_BK, p.lda);
-            lb.load(rb, cb, wave, (kt + u + 2) * GEMM_BK, p.ldb);
-            __builtin_amdgcn_sched_barrier(0);
-            mfmas(f1a, f1b);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-#pragma unroll
-        for (int a = 0; a < 2; ++a)
-#pragma unroll
-            for (int b = 0; b < 2; ++b) {
-                tot[a][b] += acc[a][b];
-                acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
+                for (int s = 0; s < 4; ++s) ds[s] += (double)(wodd ? fa[1][s] : fa[0][s]);
             }
-    }
+        };
+        for (int kt = it0; kt < it1; kt += 4) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                // it0 is a multiple of 4: slab kt+u lives in stage u & 1
+                float *const ca = (u & 1) ? sA1 : sA0, *const cb = (u & 1) ? sB1 : sB0;
+                float *const na = (u & 1) ? sA0 : sA1, *const nb = (u & 1) ? sB0 : sB1;
+                d_frags<AKC>(ca, wm, li, lg, 1, f1a);
+                d_frags<BKC>(cb, wn, li, lg, 1, f1b);
+                __builtin_amdgcn_sched_barrier(0);
+                mfmas(f0a, f0b);
+                colsum(f0a);
+                __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's loads of slab kt+u+1
+                __syncthreads();
+                d_frags<AKC>(na, wm, li, lg, 0, f0a);
+                d_frags<BKC>(nb, wn, li, lg, 0, f0b);
+                __builtin_amdgcn_sched_barrier(0);
+                la.load(ra, ca, wave, (kt + u + 2) * GEMM_BK, p.lda);
+                lb.load(rb, cb, wave, (kt + u + 2) * GEMM_BK, p.ldb);
+                __builtin_amdgcn_sched_barrier(0);
+                mfmas(f1a, f1b);
+                colsum(f1a);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int a = 0; a < 2; ++a)
+#pragma unroll
+                for (int b = 0; b < 2; ++b) {
+                    tot[a][b] += acc[a][b];
+                    acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
+                }
+        }
+    };
+    if (dsum)
+        kloop(BoolTag<DB>{});
+    else
+        kloop(BoolTag<false>{});
     // No load may still be writing LDS when the workgroup ends.
     __builtin_amdgcn_s_waitcnt(0x0f70);
+    if (dsum) {
+        double d = (ds[0] + ds[1]) + (ds[2] + ds[3]);
+        d += __shfl_xor(d, 16);
+        d += __shfl_xor(d, 32);
+        const int r = wm * 32 + 2 * li + wn;
+        if (unit >= 0) {
+            if (lg == 0) p.dbpart[(int64_t)unit * 64 + r] = d;
+        } else if (lg == 0) {
+            // a row past Mo reads the clamped address and writes nothing
+            const int i = min(i0 + r, p.Mo - 1);
+            const float old = p.db[i];
+            if (i0 + r < p.Mo) p.db[i] = old + (0.0f + (float)d);
+        }
+    }
     if (unit >= 0) {
         float *mine = p.ws + (int64_t)unit * 4096;
 #pragma unroll
@@ -950,23 +1018,25 @@ __device__ __forceinline__ void gemm_dma_body(const GemmArgs &p) {
         __attribute__((amdgpu_waves_per_eu(BM * BN <= 4096 ? 4 : 1))) name(GemmArgs p) {          \
         gemm_tile_body<BM, BN, AKC, BKC, EPI, VEC>(p);                                               \
     }
-#define GEMM_DMA_KERNEL(name, AKC, BKC, EPI)                                                           \
+#define GEMM_DMA_KERNEL(name, AKC, BKC, EPI, DB)                                                       \
     extern "C" __global__ void __launch_bounds__(GEMM_NT) __attribute__((amdgpu_waves_per_eu(4)))      \
         name(GemmArgs p) {                                                                             \
-        gemm_dma_body<AKC, BKC, EPI>(p);                                                               \
+        gemm_dma_body<AKC, BKC, EPI, DB>(p);                                                           \
     }
-#define GEMM_TILE_FIXUP(name, EPI, IA, IB) \
-    extern "C" __global__ void __launch_bounds__(GEMM_NT) name(GemmArgs p) { gemm_tile_fixup_body<EPI, IA, IB>(p); }
-GEMM_DMA_KERNEL(gemm_64x64_fwd_v, true, true, EPI_STORE)
-GEMM_DMA_KERNEL(gemm_64x64_dx_v, true, false, EPI_ACCUM)
-GEMM_DMA_KERNEL(gemm_64x64_dw_v, false, false, EPI_ACCUM)
-GEMM_DMA_KERNEL(gemm_64x64_gated_v, true, true, EPI_GATED)
+#define GEMM_TILE_FIXUP(name, EPI, IA, IB, DB) \
+    extern "C" __global__ void __launch_bounds__(GEMM_NT) name(GemmArgs p) { gemm_tile_fixup_body<EPI, IA, IB, DB>(p); }
+GEMM_DMA_KERNEL(gemm_64x64_fwd_v, true, true, EPI_STORE, false)
+GEMM_DMA_KERNEL(gemm_64x64_dx_v, true, false, EPI_ACCUM, false)
+GEMM_DMA_KERNEL(gemm_64x64_dw_v, false, false, EPI_ACCUM, false)
+GEMM_DMA_KERNEL(gemm_64x64_dwb_v, false, false, EPI_ACCUM, true)   // dW + db
+GEMM_DMA_KERNEL(gemm_64x64_gated_v, true, true, EPI_GATED, false)
 GEMM_TILE_KERNEL(gemm_64x64_fwd_s, 64, 64, true, true, EPI_STORE, false)
 GEMM_TILE_KERNEL(gemm_64x64_dx_s, 64, 64, true, false, EPI_ACCUM, false)
 GEMM_TILE_KERNEL(gemm_64x64_dw_s, 64, 64, false, false, EPI_ACCUM, false)
-GEMM_TILE_FIXUP(gemm_64x64_fixup_fwd_v, EPI_STORE, false, false)
-GEMM_TILE_FIXUP(gemm_64x64_fixup_dx_v, EPI_ACCUM, false, true)
-GEMM_TILE_FIXUP(gemm_64x64_fixup_dw_v, EPI_ACCUM, true, true)
-GEMM_TILE_FIXUP(gemm_64x64_fixup_fwd_s, EPI_STORE, false, false)
-GEMM_TILE_FIXUP(gemm_64x64_fixup_dx_s, EPI_ACCUM, false, false)
-GEMM_TILE_FIXUP(gemm_64x64_fixup_dw_s, EPI_ACCUM, false, false)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_fwd_v, EPI_STORE, false, false, false)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_dx_v, EPI_ACCUM, false, true, false)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_dw_v, EPI_ACCUM, true, true, false)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_dwb_v, EPI_ACCUM, true, true, true)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_fwd_s, EPI_STORE, false, false, false)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_dx_s, EPI_ACCUM, false, false, false)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_dw_s, EPI_ACCUM, false, false, false)

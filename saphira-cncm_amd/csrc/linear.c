@@ -36,6 +36,8 @@ typedef struct {
     const float *B2;
     const float *bias2;
     int beta;
+    float *db;
+    double *dbpart;
 } GemmArgs;
 
 /* Must match struct GemvArgs in gemm.hip. */
@@ -174,16 +176,19 @@ static int64_t extent(int64_t rows, int64_t cols, int64_t ld) { return ((rows - 
 #define TILE_M 64
 #define TILE_N 64
 
-/* beta (accumulating kinds): 1 C += A.B, 0 C = 0.0f + A.B (C is not read). */
+/* beta (accumulating kinds): 1 C += A.B, 0 C = 0.0f + A.B (C is not read).
+ * db (L_DW with vec only, else NULL): the bias gradient db[i] += sum_k A(i,k)
+ * is summed by the same launch. */
 static int run_gemm(int kind, const float *A, const float *B, float *C, const float *bias,
                     const float *res, int res_mul, int Mo, int No, int Kred, int lda, int ldb, int ldc,
-                    int act, int vec, int beta) {
+                    int act, int vec, int beta, float *db) {
     if (Mo <= 0 || No <= 0) return 0;
     const int bm = TILE_M, bn = TILE_N;
     if ((int64_t)((Mo + bm - 1) / bm) * ((No + bn - 1) / bn) > INT_MAX / 4)
         return ncm_fail(NCM_E_ARG, "linear: %d x %d output has too many tiles", Mo, No);
     char name[48], fix[48];
     gemm_name(bm, bn, kind, vec, name, sizeof name);
+    if (db) snprintf(name, sizeof name, "gemm_%dx%d_dwb_v", bm, bn);   /* the dW kernel that also sums db */
     int slots = gemm_slots(name);
     if (slots < 0) return NCM_E_INIT;
     GemmPlan g = plan_gemm(Mo, No, Kred, slots, bm, bn);
@@ -194,17 +199,21 @@ static int run_gemm(int kind, const float *A, const float *B, float *C, const fl
         return ncm_fail(NCM_E_ARG, "linear: operand of %lld / %lld bytes exceeds the 2 GiB buffer range",
                         (long long)ab, (long long)bb);
     GemmArgs p = {A, B, C, bias, res, NULL, Mo, No, Kred, lda, ldb, ldc, act, 0,
-                  g.tiles_m, g.tiles_n, g.iters, g.dp_tiles, g.segs, (unsigned)ab, (unsigned)bb, NULL, NULL, beta};
+                  g.tiles_m, g.tiles_n, g.iters, g.dp_tiles, g.segs, (unsigned)ab, (unsigned)bb, NULL, NULL, beta,
+                  db, NULL};
     p.res_mul = res_mul;
     int split_tiles = g.tiles_m * g.tiles_n - g.dp_tiles;
     if (g.segs > 1) {
-        p.ws = (float *)ncm_workspace(WS_SPLITK, (size_t)split_tiles * g.segs * bm * bn * sizeof(float));
+        /* partial tiles [units][64 * 64] floats, then the bias partials [units][64] doubles */
+        size_t units = (size_t)split_tiles * g.segs;
+        p.ws = (float *)ncm_workspace(WS_SPLITK, units * (bm * bn * sizeof(float) + (db ? 64 * sizeof(double) : 0)));
         if (!p.ws) return NCM_E_OOM;
+        if (db) p.dbpart = (double *)(p.ws + units * bm * bn);
     }
     void *args[] = {&p};
     int rc = ncm_launch(ncm_kernel(name), (unsigned)g.blocks, 1, 1, 256, args);
     if (rc || g.segs == 1) return rc;
-    snprintf(fix, sizeof fix, "gemm_%dx%d_fixup_%s_%c", bm, bn, kind_names[kind], vec ? 'v' : 's');
+    snprintf(fix, sizeof fix, "gemm_%dx%d_fixup_%s_%c", bm, bn, db ? "dwb" : kind_names[kind], vec ? 'v' : 's');
     return ncm_launch_named(fix, (unsigned)split_tiles * 4u, 1, 1, 256, args);  /* one workgroup per MFMA block */
 }
 
@@ -272,7 +281,7 @@ static void linear_forward(const char *fn, const float *x, const float *W, const
     } else if (batch <= 8)
         run_gemv(x, W, b, res, y, (int)batch, M, K, act, vec);
     else
-        run_gemm(L_FWD, x, W, y, b, res, res_mul, (int)batch, M, K, K, K, M, act, vec, 1);
+        run_gemm(L_FWD, x, W, y, b, res, res_mul, (int)batch, M, K, K, K, M, act, vec, 1, NULL);
 }
 
 void linear_fwd(const float *x, const float *W, const float *b, float *y, int64_t batch, int M,
@@ -315,7 +324,7 @@ void linear_fwd_gated(const float *x, const float *Wg, const float *bg, const fl
         if (ab < MAX_BUFFER_BYTES && bb < MAX_BUFFER_BYTES) {
             const int groups = (K + 4 * BK - 1) / (4 * BK);
             GemmArgs p = {x, Wg, y, bg, NULL, NULL, (int)batch, M, K, K, K, M, act, 0,
-                          tiles_m, tiles_n, 4 * groups, tiles_m * tiles_n, 1, (unsigned)ab, (unsigned)bb, Wu, bu, 1};
+                          tiles_m, tiles_n, 4 * groups, tiles_m * tiles_n, 1, (unsigned)ab, (unsigned)bb, Wu, bu, 1, NULL, NULL};
             void *args[] = {&p};
             ncm_launch_named("gemm_64x64_gated_v", (unsigned)(tiles_m * tiles_n), 1, 1, 256, args);
             return;
@@ -378,7 +387,7 @@ void ncm_linear_bwd_ex(const float *x, const float *W, const float *dy, float *d
             rc = run_dxt(dy, W, dx, nb, M, K);
         } else {
             int vec = (M % 4 == 0) && (K % 4 == 0) && is_aligned16(dy) && is_aligned16(W);
-            rc = run_gemm(L_DX, dy, W, dx, NULL, NULL, 0, nb, K, M, M, K, K, 0, vec, dx_beta);
+            rc = run_gemm(L_DX, dy, W, dx, NULL, NULL, 0, nb, K, M, M, K, K, 0, vec, dx_beta, NULL);
         }
         if (rc) return;
     }
@@ -392,7 +401,9 @@ void ncm_linear_bwd_ex(const float *x, const float *W, const float *dy, float *d
             rc = ncm_launch_named(vec ? "dw_rank_v" : "dw_rank_s", (unsigned)((n + 255) / 256), 1, 1, 256, a);
         } else {
             int vec = (M % 4 == 0) && (K % 4 == 0) && is_aligned16(dy) && is_aligned16(x);
-            rc = run_gemm(L_DW, dy, x, dW, NULL, NULL, 0, M, K, nb, M, K, K, 0, vec, 1);
+            /* the vectorised dW kernel also sums db (from the dy slabs it loads anyway) */
+            rc = run_gemm(L_DW, dy, x, dW, NULL, NULL, 0, M, K, nb, M, K, K, 0, vec, 1, vec ? db : NULL);
+            if (vec) db = NULL;
         }
         if (rc) return;
     }
@@ -425,9 +436,10 @@ void linear_bwd(const float *x, const float *W, const float *dy, float *dx, floa
 }
 
 int ncm_hip_linear_plan(int op, int64_t batch, int M, int K, char *kernel, size_t cap) {
-    if (op < 0 || op > 2 || batch <= 0 || batch > INT_MAX || M <= 0 || K <= 0 || !kernel || !cap)
+    if (op < 0 || op > 3 || batch <= 0 || batch > INT_MAX || M <= 0 || K <= 0 || !kernel || !cap)
         return ncm_fail(NCM_E_ARG, "ncm_hip_linear_plan: bad arguments"), -1;
-    int nb = (int)batch;
+    int nb = (int)batch, with_db = op == 3;
+    if (with_db) op = L_DW;
     if (op == L_FWD && nb <= 8) {
         gemv_name(nb >= 8 ? 8 : nb >= 4 ? 4 : nb >= 2 ? 2 : 1, M, K % 4 == 0, kernel, cap);
         return 1;
@@ -444,6 +456,7 @@ int ncm_hip_linear_plan(int op, int64_t batch, int M, int K, char *kernel, size_
     int vec = op == L_FWD ? K % 4 == 0 : (M % 4 == 0 && K % 4 == 0);
     const int bm = TILE_M, bn = TILE_N;
     gemm_name(bm, bn, op, vec, kernel, cap);
+    if (with_db && vec) snprintf(kernel, cap, "gemm_%dx%d_dwb_v", bm, bn);
     if ((int64_t)((Mo + bm - 1) / bm) * ((No + bn - 1) / bn) > INT_MAX / 4)
         return ncm_fail(NCM_E_ARG, "ncm_hip_linear_plan: %d x %d output has too many tiles", Mo, No), -1;
     int slots = gemm_slots(kernel);

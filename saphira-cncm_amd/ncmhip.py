@@ -331,9 +331,10 @@ def linear_bwd(x, W, dy, dx, dW, db, batch, M, K):
 
 
 def linear_plan(op, batch, M, K):
-    """(kernel name, split count) a linear call launches; op in fwd/dx/dw."""
+    """(kernel name, split count) a linear call launches; op in fwd/dx/dw, or
+    dwdb for dW and db requested by one linear_bwd call."""
     buf = ctypes.create_string_buffer(64)
-    s = load().ncm_hip_linear_plan({"fwd": 0, "dx": 1, "dw": 2}[op], batch, M, K, buf, 64)
+    s = load().ncm_hip_linear_plan({"fwd": 0, "dx": 1, "dw": 2, "dwdb": 3}[op], batch, M, K, buf, 64)
     check()
     return buf.value.decode(), s
 

@@ -195,6 +195,36 @@ def test_bias_gradient_batch_sizes():
             assert maxrel(db, ref) <= TOL, (rows, N)
 
 
+def test_bias_gradient_inside_dw():
+    """With dW requested (aligned rows), db is summed by the dW GEMM itself
+    from the dy slabs of its first tile column: whole tiles write it, split
+    tiles leave fp64 partials per segment that the fixup adds in segment
+    order.  Row counts that are not whole slabs, 4-aligned column counts that
+    are not whole 64-row tiles, both plans; accumulated onto a non-zero db.
+    Integer data: every sum is exact, so db and dW are compared bit for bit."""
+    rng = np.random.default_rng(29)
+    segs_seen = set()
+    for rows, N, K in ((9, 68, 8), (100, 132, 64), (513, 2304, 768), (4096, 132, 8), (1100, 200, 256),
+                       (16384, 200, 64)):
+        kernel, segs = ncmhip.linear_plan("dwdb", rows, N, K)
+        assert kernel == "gemm_64x64_dwb_v"
+        segs_seen.add(segs > 1)
+        x = rng.integers(-4, 5, (rows, K)).astype(np.float32)
+        W = rng.integers(-4, 5, (N, K)).astype(np.float32)
+        dy = rng.integers(-4, 5, (rows, N)).astype(np.float32)
+        db0 = rng.integers(-50, 51, N).astype(np.float32)
+        _, dW, db = gpu_bwd(x, W, dy, None, np.zeros((N, K), np.float32), db0)
+        assert bits_equal(db, (db0.astype(np.int64) + dy.astype(np.int64).sum(0)).astype(np.float32)), (rows, N)
+        assert bits_equal(dW, (dy.T.astype(np.int64) @ x.astype(np.int64)).astype(np.float32)), (rows, N)
+        if rows <= 1100:
+            dyf = rng.standard_normal((rows, N)).astype(np.float32)
+            dbf = rng.standard_normal(N).astype(np.float32)
+            _, _, got = gpu_bwd(x, W, dyf, None, np.zeros((N, K), np.float32), dbf)
+            _, _, ref = O.linear_bwd(x, W, dyf, db=dbf, want=("db",))
+            assert maxrel(got, ref) <= TOL, (rows, N)
+    assert segs_seen == {False, True}
+
+
 def test_run_to_run_determinism():
     rng, x, W, b = sweep_inputs(3, 512, 3072, 768)
     a = gpu_fwd(x, W, b)

@@ -351,6 +351,17 @@ void ncm_t_rope(NcmTape *t, const float *xq, const float *xk, float *yq, float *
                 const float *sin, int B, int H, int Hkv, int T, int hd);
 void ncm_t_sdpa(NcmTape *t, const float *q, const float *k, const float *v, const float *mask, float *o,
                 int B, int H, int Hkv, int Tq, int Tkv, int hd);
+/* extension: ncm_t_linear (x -> pre) followed by the activation (pre -> y;
+ * kind 0 GELU, 1 SiLU, 2 GELU tanh form, as ncm_t_gelu / ncm_t_silu /
+ * ncm_t_gelu_tanh) with one GEMM writing both outputs, bit for bit the two
+ * calls (train_gpt2.c:87-89) */
+void ncm_t_linear_act(NcmTape *t, const float *x, const float *W, const float *b, float *pre, float *y,
+                      int64_t batch, int M, int K, int kind);
+/* extension: ncm_t_linear then ncm_t_add(res, linear output -> y) with the sum
+ * in the GEMM epilogue and the linear output never stored (train_gpt2.c:72-74,
+ * 95-97); res must not be y */
+void ncm_t_linear_res(NcmTape *t, const float *x, const float *W, const float *b, const float *res, float *y,
+                      int64_t batch, int M, int K);
 /* extension: ncm_t_sdpa with the causal mask generated in the kernels (query t
  * sees keys <= t + Tkv - Tq), replacing the T x T -1e9 mask the reference's
  * callers build and upload (train_gpt2.c:112-121) */

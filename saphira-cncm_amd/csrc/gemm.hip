@@ -72,6 +72,7 @@ struct GemmArgs {
     float *db;           // dW (vectorised kernel) or null: db[i] += 0.0f + (float)(fp64 sum over k of A(i,k)),
                          // the bias gradient, from the A slabs of the tiles in tile column 0
     double *dbpart;      // its per-segment fp64 partials of split tiles [units][64]
+    float *pre;          // STORE or null: also stores acc + bias (before the activation) at the same index
 };
 
 // Grouped raster: GROUP_M tile rows advance together along N so that the B
@@ -543,6 +544,7 @@ __device__ __forceinline__ void g_out_n(const GemmArgs &p, const int (&ii)[N], c
             *c = o1[n] + x;
         } else {
             if (hb) x += o1[n];
+            if (p.pre) p.pre[(int64_t)ii[n] * p.ldc + jj[n]] = x;
             x = ncm_act(x, ACT);
             if (hr) x = p.res_mul ? x * o2[n] : o2[n] + x;
             *c = x;

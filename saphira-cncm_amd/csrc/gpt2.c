@@ -67,21 +67,18 @@ static float *gpt2_block(NcmTape *tp, const NcmGpt2Config *c, float *const *P, i
     float *const *w = P + 2 + PER_LAYER * li;
     float *ln = A(R * C), *qkv = A(R * 3 * C);
     float *qq = A(R * C), *kk = A(R * C), *vv = A(R * C), *ctx = A(R * C);
-    float *mo = A(R * C), *ao = A(R * C), *x1 = A(R * C), *mn = A(R * C);
-    float *mm = A(R * I), *m2 = A(R * I), *mlpo = A(R * C), *out = A(R * C);
+    float *mo = A(R * C), *x1 = A(R * C), *mn = A(R * C);
+    float *mm = A(R * I), *m2 = A(R * I), *out = A(R * C);
     if (!out) return NULL;
     ncm_t_layernorm_eps(tp, x, w[0], w[1], ln, R, C, GPT2_LN_EPS);
     ncm_t_linear(tp, ln, w[2], w[3], qkv, R, 3 * C, C);
     ncm_t_qkvsplit(tp, qkv, qq, kk, vv, B, T, C, H, hd, H, 1);
     ncm_t_sdpa_causal(tp, qq, kk, vv, ctx, B, H, H, T, T, hd);   /* the -1e9 causal mask, generated */
     ncm_t_headmerge(tp, ctx, mo, B, T, C, H, hd);
-    ncm_t_linear(tp, mo, w[4], w[5], ao, R, C, C);
-    ncm_t_add(tp, x, ao, x1, R * C);
+    ncm_t_linear_res(tp, mo, w[4], w[5], x, x1, R, C, C);   /* x1 = x + attn proj */
     ncm_t_layernorm_eps(tp, x1, w[6], w[7], mn, R, C, GPT2_LN_EPS);
-    ncm_t_linear(tp, mn, w[8], w[9], mm, R, I, C);
-    ncm_t_gelu_tanh(tp, mm, m2, R * I);
-    ncm_t_linear(tp, m2, w[10], w[11], mlpo, R, C, I);
-    ncm_t_add(tp, x1, mlpo, out, R * C);
+    ncm_t_linear_act(tp, mn, w[8], w[9], mm, m2, R, I, C, 2);   /* m2 = gelu_tanh(mm) */
+    ncm_t_linear_res(tp, m2, w[10], w[11], x1, out, R, C, I);  /* out = x1 + mlp proj */
     return out;
 }
 

@@ -49,6 +49,10 @@ size_t ncm_sample_ws_bytes(int V);
  * step; the gradient is consumed and the next step accumulates from zero). */
 void ncm_adamw_update_clear(float *p, float *g, float *m, float *v, int64_t n, double lr, double b1, double b2,
                             double b1t, double b2t, double eps, double wd);
+/* pre = x W^T + b and y = act(pre) for act SILU / GELU / GELU_TANH, bit for
+ * bit linear_fwd followed by the elementwise activation (linear.c). */
+void ncm_linear_fwd_pre(const float *x, const float *W, const float *b, float *pre, float *y, int64_t batch,
+                        int M, int K, int act);
 /* Backward ops with a first-write form: beta 1 accumulates (the public
  * functions' contract), beta 0 writes 0.0f + the gradient -- the bits of an
  * accumulation into zeros -- so the output needs no clearing and is not read.

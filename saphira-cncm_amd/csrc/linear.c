@@ -38,6 +38,7 @@ typedef struct {
     int beta;
     float *db;
     double *dbpart;
+    float *pre;
 } GemmArgs;
 
 /* Must match struct GemvArgs in gemm.hip. */
@@ -179,9 +180,9 @@ static int64_t extent(int64_t rows, int64_t cols, int64_t ld) { return ((rows - 
 /* beta (accumulating kinds): 1 C += A.B, 0 C = 0.0f + A.B (C is not read).
  * db (L_DW with vec only, else NULL): the bias gradient db[i] += sum_k A(i,k)
  * is summed by the same launch. */
-static int run_gemm(int kind, const float *A, const float *B, float *C, const float *bias,
-                    const float *res, int res_mul, int Mo, int No, int Kred, int lda, int ldb, int ldc,
-                    int act, int vec, int beta, float *db) {
+static int run_gemm_pre(int kind, const float *A, const float *B, float *C, const float *bias,
+                        const float *res, int res_mul, int Mo, int No, int Kred, int lda, int ldb, int ldc,
+                        int act, int vec, int beta, float *db, float *pre) {
     if (Mo <= 0 || No <= 0) return 0;
     const int bm = TILE_M, bn = TILE_N;
     if ((int64_t)((Mo + bm - 1) / bm) * ((No + bn - 1) / bn) > INT_MAX / 4)
@@ -200,7 +201,7 @@ static int run_gemm(int kind, const float *A, const float *B, float *C, const fl
                         (long long)ab, (long long)bb);
     GemmArgs p = {A, B, C, bias, res, NULL, Mo, No, Kred, lda, ldb, ldc, act, 0,
                   g.tiles_m, g.tiles_n, g.iters, g.dp_tiles, g.segs, (unsigned)ab, (unsigned)bb, NULL, NULL, beta,
-                  db, NULL};
+                  db, NULL, pre};
     p.res_mul = res_mul;
     int split_tiles = g.tiles_m * g.tiles_n - g.dp_tiles;
     if (g.segs > 1) {
@@ -215,6 +216,12 @@ static int run_gemm(int kind, const float *A, const float *B, float *C, const fl
     if (rc || g.segs == 1) return rc;
     snprintf(fix, sizeof fix, "gemm_%dx%d_fixup_%s_%c", bm, bn, db ? "dwb" : kind_names[kind], vec ? 'v' : 's');
     return ncm_launch_named(fix, (unsigned)split_tiles * 4u, 1, 1, 256, args);  /* one workgroup per MFMA block */
+}
+
+static int run_gemm(int kind, const float *A, const float *B, float *C, const float *bias,
+                    const float *res, int res_mul, int Mo, int No, int Kred, int lda, int ldb, int ldc,
+                    int act, int vec, int beta, float *db) {
+    return run_gemm_pre(kind, A, B, C, bias, res, res_mul, Mo, No, Kred, lda, ldb, ldc, act, vec, beta, db, NULL);
 }
 
 /* GEMV kernel for a chunk of nb <= 8 batch rows; returns rows per workgroup. */
@@ -299,6 +306,36 @@ void linear_fwd_glu(const float *x, const float *W, const float *b, const float 
     linear_forward("linear_fwd_glu", x, W, b, mul, 1, y, batch, M, K, act);
 }
 
+/* pre = x W^T + b and y = act(pre): the outputs of linear_fwd followed by
+ * silu_fwd / gelu_fwd / gelu_tanh_fwd, bit for bit (the GEMM epilogue applies
+ * the elementwise kernels' activation function to the same float), in one
+ * GEMM launch for batches above 8; otherwise those two calls. */
+void ncm_linear_fwd_pre(const float *x, const float *W, const float *b, float *pre, float *y, int64_t batch,
+                        int M, int K, int act) {
+    const char *fn = "ncm_linear_fwd_pre";
+    if (check_dims(fn, batch, M, K)) return;
+    if (act != NCM_ACT_SILU && act != NCM_ACT_GELU && act != NCM_ACT_GELU_TANH) {
+        ncm_fail(NCM_E_ARG, "%s: activation %d has no elementwise form", fn, act);
+        return;
+    }
+    if (batch == 0) return;
+    if (!x || !W || !y || !pre || pre == y) {
+        ncm_fail(NCM_E_ARG, "%s: null x/W/y/pre or pre == y", fn);
+        return;
+    }
+    if (ncm_ready()) return;
+    if (batch <= 8) {
+        linear_forward(fn, x, W, b, NULL, 0, pre, batch, M, K, NCM_ACT_NONE);
+        int64_t n = batch * M;
+        if (act == NCM_ACT_SILU) silu_fwd(pre, y, n);
+        else if (act == NCM_ACT_GELU) gelu_fwd(pre, y, n);
+        else gelu_tanh_fwd(pre, y, n);
+        return;
+    }
+    int vec = (K % 4 == 0) && is_aligned16(x) && is_aligned16(W);
+    run_gemm_pre(L_FWD, x, W, y, b, NULL, 0, (int)batch, M, K, K, K, M, act, vec, 1, NULL, pre);
+}
+
 /* Both products of a gated unit in one GEMM launch when its tiles (64 rows x
  * 32 output columns of each product) fill the CUs; otherwise the up product
  * into a workspace, then the gate product with the multiply epilogue. */
@@ -324,7 +361,7 @@ void linear_fwd_gated(const float *x, const float *Wg, const float *bg, const fl
         if (ab < MAX_BUFFER_BYTES && bb < MAX_BUFFER_BYTES) {
             const int groups = (K + 4 * BK - 1) / (4 * BK);
             GemmArgs p = {x, Wg, y, bg, NULL, NULL, (int)batch, M, K, K, K, M, act, 0,
-                          tiles_m, tiles_n, 4 * groups, tiles_m * tiles_n, 1, (unsigned)ab, (unsigned)bb, Wu, bu, 1, NULL, NULL};
+                          tiles_m, tiles_n, 4 * groups, tiles_m * tiles_n, 1, (unsigned)ab, (unsigned)bb, Wu, bu, 1, NULL, NULL, NULL};
             void *args[] = {&p};
             ncm_launch_named("gemm_64x64_gated_v", (unsigned)(tiles_m * tiles_n), 1, 1, 256, args);
             return;

@@ -315,6 +315,35 @@ void ncm_t_gelu_tanh(NcmTape *t, const float *x, float *y, int64_t n) {
     rec_act(t, x, y, n, 2);
 }
 
+/* ncm_t_linear (x -> pre) then the activation (pre -> y), the GEMM writing
+ * both outputs; the same two records. */
+void ncm_t_linear_act(NcmTape *t, const float *x, const float *W, const float *b, float *pre, float *y,
+                      int64_t batch, int M, int K, int kind) {
+    static const int acts[3] = {NCM_ACT_GELU, NCM_ACT_SILU, NCM_ACT_GELU_TANH};
+    if (kind < 0 || kind > 2) { ncm_fail(NCM_E_ARG, "ncm_t_linear_act: unknown activation %d", kind); return; }
+    ncm_linear_fwd_pre(x, W, b, pre, y, batch, M, K, acts[kind]);
+    REC_OR_RETURN(r, t, NT_LINEAR);
+    r->a = x; r->b = W; r->c = b; r->y = pre;
+    r->n = batch; r->p1 = M; r->p2 = K;
+    rec_act(t, pre, y, batch * M, kind);
+}
+
+/* y = res + (x W^T + b) in one GEMM launch: the records of ncm_t_linear and
+ * ncm_t_add without the linear output in between -- the linear record's
+ * output is y itself (the add passes y's gradient through unchanged) and
+ * the add record carries only res. */
+void ncm_t_linear_res(NcmTape *t, const float *x, const float *W, const float *b, const float *res, float *y,
+                      int64_t batch, int M, int K) {
+    if (!res || res == y) { ncm_fail(NCM_E_ARG, "ncm_t_linear_res: res must be a buffer other than y"); return; }
+    linear_fwd_ep(x, W, b, res, y, batch, M, K, NCM_ACT_NONE);
+    NtRec *r = emit(t, NT_LINEAR);
+    if (!r) return;
+    r->a = x; r->b = W; r->c = b; r->y = y;
+    r->n = batch; r->p1 = M; r->p2 = K;
+    REC_OR_RETURN(ra, t, NT_ADD);
+    ra->a = res; ra->b = NULL; ra->y = y; ra->n = batch * M;
+}
+
 void ncm_t_mul(NcmTape *t, const float *a, const float *b, float *y, int64_t n) {
     mul_fwd(a, b, y, n);
     REC_OR_RETURN(r, t, NT_MUL);
@@ -500,7 +529,7 @@ void ncm_tape_backward(NcmTape *t, const NcmPMap *pm) {
             int ba, bb;
             float *ga = gmap_get_fresh(t, r->a, r->n, &ba);
             if (ga) ncm_add_inplace_ex(ga, dy, r->n, ba);
-            float *gb = gmap_get_fresh(t, r->b, r->n, &bb);   /* after a's write: b may be a */
+            float *gb = r->b ? gmap_get_fresh(t, r->b, r->n, &bb) : NULL;   /* after a's write: b may be a */
             if (gb) ncm_add_inplace_ex(gb, dy, r->n, bb);
             break;
         }

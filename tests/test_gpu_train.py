@@ -324,3 +324,66 @@ def test_tape_sdpa_backward(B, H, Hkv, Tq, Tkv, hd, kind):
             assert np.max(np.abs(g - ref)) <= 1e-4 and maxrel(g, ref) <= 1e-4, (kind, float(np.max(np.abs(g - ref))))
     finally:
         lib.ncm_tape_free(tape)
+
+
+# ---------------------------------------------------------------- fused linear records
+@pytest.mark.parametrize("R,K,M", [(300, 96, 128), (130, 768, 3072), (6, 64, 96)])
+def test_tape_fused_linear_records(R, K, M):
+    """ncm_t_linear_act (the GEMM also writing the pre-activation) and
+    ncm_t_linear_res (the residual summed in the GEMM epilogue, the linear
+    output never stored) against the unfused records ncm_t_linear +
+    ncm_t_gelu_tanh and ncm_t_linear + ncm_t_add: outputs and every gradient
+    bit for bit, from one seeded output gradient.  Shapes: whole GEMM tiles,
+    a split-K forward (fixup epilogue), and a batch of at most 8 (the GEMV
+    path)."""
+    lib = ncmhip.load()
+    x, W, b, res, g = rnd(70, R, K), rnd(71, M, K), rnd(72, M), rnd(73, R, M), rnd(74, R, M)
+
+    def run(records, outs, inputs):
+        """records(tape, bufs); the seeded gradient goes to outs[-1]; returns
+        the outputs and the gradients of the inputs."""
+        bufs = {n: up(a) for n, a in inputs.items()}
+        for n, shape in outs:
+            bufs[n] = D.empty(shape)
+        grads = {n: D.from_numpy(np.zeros_like(a)) for n, a in inputs.items()}
+        gy = up(g)
+        tape = lib.ncm_tape_new()
+        try:
+            records(tape, bufs)
+            ncmhip.check()
+            names = list(inputs) + [outs[-1][0]]
+            ptrs = (ctypes.c_void_p * len(names))(*[bufs[n].ptr for n in names])
+            gp = (ctypes.c_void_p * len(names))(*[grads[n].ptr for n in inputs] + [gy.ptr])
+            sizes = (ctypes.c_int64 * len(names))(*[inputs[n].size for n in inputs] + [g.size])
+            pm = _PMap(ctypes.cast(ptrs, ctypes.c_void_p), ctypes.cast(gp, ctypes.c_void_p),
+                       ctypes.cast(sizes, ctypes.c_void_p), len(names))
+            lib.ncm_tape_backward(tape, ctypes.byref(pm))
+            ncmhip.check()
+            return {n: bufs[n].numpy() for n, _ in outs}, {n: grads[n].numpy() for n in inputs}
+        finally:
+            lib.ncm_tape_free(tape)
+
+    ins = {"x": x, "W": W, "b": b}
+    o1, g1 = run(lambda t, f: (lib.ncm_t_linear(t, f["x"].ptr, f["W"].ptr, f["b"].ptr, f["pre"].ptr, R, M, K),
+                               lib.ncm_t_gelu_tanh(t, f["pre"].ptr, f["y"].ptr, R * M)),
+                 [("pre", (R, M)), ("y", (R, M))], ins)
+    o2, g2 = run(lambda t, f: lib.ncm_t_linear_act(t, f["x"].ptr, f["W"].ptr, f["b"].ptr, f["pre"].ptr,
+                                                   f["y"].ptr, R, M, K, 2),
+                 [("pre", (R, M)), ("y", (R, M))], ins)
+    for n in o1:
+        assert bits_equal(o1[n], o2[n]), n
+    for n in g1:
+        assert bits_equal(g1[n], g2[n]), n
+    assert np.any(g1["x"])
+
+    ins = {"x": x, "W": W, "b": b, "res": res}
+    o1, g1 = run(lambda t, f: (lib.ncm_t_linear(t, f["x"].ptr, f["W"].ptr, f["b"].ptr, f["ao"].ptr, R, M, K),
+                               lib.ncm_t_add(t, f["res"].ptr, f["ao"].ptr, f["y"].ptr, R * M)),
+                 [("ao", (R, M)), ("y", (R, M))], ins)
+    o2, g2 = run(lambda t, f: lib.ncm_t_linear_res(t, f["x"].ptr, f["W"].ptr, f["b"].ptr, f["res"].ptr,
+                                                   f["y"].ptr, R, M, K),
+                 [("y", (R, M))], ins)
+    assert bits_equal(o1["y"], o2["y"])
+    for n in g1:
+        assert bits_equal(g1[n], g2[n]), n
+    assert bits_equal(g1["res"], g)

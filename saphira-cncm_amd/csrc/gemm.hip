@@ -44,10 +44,13 @@
 //
 // Epilogues: STORE  C = res + act(acc + bias) (or act(acc + bias) * res, the
 // gated-unit product);  ACCUM  C += acc;  GATED  C = act(x B^T + bias) *
-// (x B2^T + bias2), both products in one tile (gemm_64x64_gated_v).
+// (x B2^T + bias2), both products in one tile (gemm_64x64_gated_v);
+// ACT_BWD  C += act'(bwd_x) (0.0f + acc): the dX product written as a fresh
+// gradient and passed back through the activation that produced the layer's
+// input, without storing it (gemm_64x64_dxa_v).
 #include "mfma_slab.h"
 
-enum { EPI_STORE = 0, EPI_ACCUM = 1, EPI_GATED = 2 };
+enum { EPI_STORE = 0, EPI_ACCUM = 1, EPI_GATED = 2, EPI_ACT_BWD = 3 };
 
 struct GemmArgs {
     const float *A;
@@ -73,6 +76,8 @@ struct GemmArgs {
                          // the bias gradient, from the A slabs of the tiles in tile column 0
     double *dbpart;      // its per-segment fp64 partials of split tiles [units][64]
     float *pre;          // STORE or null: also stores acc + bias (before the activation) at the same index
+    const float *bwd_x;  // ACT_BWD: the activation's input, indexed like C
+    int bwd_kind;        // ACT_BWD: 0 GELU (erf), 1 SiLU, 2 GELU (tanh form)
 };
 
 // Grouped raster: GROUP_M tile rows advance together along N so that the B
@@ -527,8 +532,9 @@ __device__ __forceinline__ void g_out_n(const GemmArgs &p, const int (&ii)[N], c
     for (int n = 0; n < N; ++n) {
         const int i = min(ii[n], p.Mo - 1), j = min(jj[n], p.No - 1);
         const int64_t e = (int64_t)i * p.ldc + j;
-        if (EPI == EPI_ACCUM) {
+        if (EPI == EPI_ACCUM || EPI == EPI_ACT_BWD) {
             o1[n] = p.beta ? p.C[e] : 0.0f;
+            if (EPI == EPI_ACT_BWD) o2[n] = p.bwd_x[e];
         } else {
             const float *bq = hb ? p.bias + j : p.C;
             o1[n] = *bq;
@@ -542,6 +548,8 @@ __device__ __forceinline__ void g_out_n(const GemmArgs &p, const int (&ii)[N], c
         float x = v[n];
         if (EPI == EPI_ACCUM) {
             *c = o1[n] + x;
+        } else if (EPI == EPI_ACT_BWD) {
+            *c = o1[n] + act_bwd_one(o2[n], 0.0f + x, p.bwd_kind);
         } else {
             if (hb) x += o1[n];
             if (p.pre) p.pre[(int64_t)ii[n] * p.ldc + jj[n]] = x;
@@ -584,7 +592,10 @@ __device__ __forceinline__ void g_epilogue_act(const GemmArgs &p, const f4 (&tot
 template <int BM, int BN, int EPI, bool IA = false, bool IB = false>
 __device__ __forceinline__ void g_epilogue(const GemmArgs &p, const f4 (&tot)[BM / 32][BN / 32], int i0, int j0,
                                            int tid) {
-    if (EPI == EPI_ACCUM) { g_epilogue_act<BM, BN, EPI, ACT_NONE, IA, IB>(p, tot, i0, j0, tid); return; }
+    if (EPI == EPI_ACCUM || EPI == EPI_ACT_BWD) {
+        g_epilogue_act<BM, BN, EPI, ACT_NONE, IA, IB>(p, tot, i0, j0, tid);
+        return;
+    }
     switch (p.act) {
     case ACT_SILU: g_epilogue_act<BM, BN, EPI, ACT_SILU, IA, IB>(p, tot, i0, j0, tid); break;
     case ACT_GELU: g_epilogue_act<BM, BN, EPI, ACT_GELU, IA, IB>(p, tot, i0, j0, tid); break;
@@ -766,7 +777,7 @@ __device__ __forceinline__ void gemm_tile_fixup_body(const GemmArgs &p) {
 #pragma unroll
     for (int s = 1; s < FIXUP_MAX_SEGS; ++s) tot = s < p.segs ? tot + part[s] : tot;
     const int a = blk >> 1, b = blk & 1, i0 = tm * 64, j0 = tn * 64;
-    if (EPI == EPI_ACCUM) {
+    if (EPI == EPI_ACCUM || EPI == EPI_ACT_BWD) {
         g_epilogue_blk_act<EPI, ACT_NONE, IA, IB>(p, tot, a, b, i0, j0, tid);
         // dW: the bias gradient of a split tile in tile column 0, from its
         // segments' fp64 partials in segment order
@@ -1031,6 +1042,7 @@ GEMM_DMA_KERNEL(gemm_64x64_fwd_v, true, true, EPI_STORE, false)
 GEMM_DMA_KERNEL(gemm_64x64_dx_v, true, false, EPI_ACCUM, false)
 GEMM_DMA_KERNEL(gemm_64x64_dw_v, false, false, EPI_ACCUM, false)
 GEMM_DMA_KERNEL(gemm_64x64_dwb_v, false, false, EPI_ACCUM, true)   // dW + db
+GEMM_DMA_KERNEL(gemm_64x64_dxa_v, true, false, EPI_ACT_BWD, false) // dX through the activation backward
 GEMM_DMA_KERNEL(gemm_64x64_gated_v, true, true, EPI_GATED, false)
 GEMM_TILE_KERNEL(gemm_64x64_fwd_s, 64, 64, true, true, EPI_STORE, false)
 GEMM_TILE_KERNEL(gemm_64x64_dx_s, 64, 64, true, false, EPI_ACCUM, false)
@@ -1039,6 +1051,7 @@ GEMM_TILE_FIXUP(gemm_64x64_fixup_fwd_v, EPI_STORE, false, false, false)
 GEMM_TILE_FIXUP(gemm_64x64_fixup_dx_v, EPI_ACCUM, false, true, false)
 GEMM_TILE_FIXUP(gemm_64x64_fixup_dw_v, EPI_ACCUM, true, true, false)
 GEMM_TILE_FIXUP(gemm_64x64_fixup_dwb_v, EPI_ACCUM, true, true, true)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_dxa_v, EPI_ACT_BWD, false, true, false)
 GEMM_TILE_FIXUP(gemm_64x64_fixup_fwd_s, EPI_STORE, false, false, false)
 GEMM_TILE_FIXUP(gemm_64x64_fixup_dx_s, EPI_ACCUM, false, false, false)
 GEMM_TILE_FIXUP(gemm_64x64_fixup_dw_s, EPI_ACCUM, false, false, false)

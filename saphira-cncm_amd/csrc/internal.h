@@ -53,6 +53,15 @@ void ncm_adamw_update_clear(float *p, float *g, float *m, float *v, int64_t n, d
  * bit linear_fwd followed by the elementwise activation (linear.c). */
 void ncm_linear_fwd_pre(const float *x, const float *W, const float *b, float *pre, float *y, int64_t batch,
                         int M, int K, int act);
+/* 1 when linear_bwd's dX runs as one vectorised GEMM (batch > 8, M and K
+ * multiples of 4, dy and W 16-byte aligned): then ncm_linear_bwd_act applies. */
+int ncm_linear_dx_fusable(int64_t batch, int M, int K, const float *dy, const float *W);
+/* linear_bwd whose dX goes back through the activation (kind 0 GELU, 1 SiLU,
+ * 2 GELU tanh form) that produced x from ax: dxa (+)= act'(ax) (0.0f + dy W)
+ * (beta 1 accumulates, 0 writes), bit for bit the fresh dX followed by
+ * ncm_act_bwd_ex, the dX itself never stored; dW / db accumulate. */
+void ncm_linear_bwd_act(const float *x, const float *W, const float *dy, float *dxa, const float *ax, int kind,
+                        int beta, float *dW, float *db, int64_t batch, int M, int K);
 /* Backward ops with a first-write form: beta 1 accumulates (the public
  * functions' contract), beta 0 writes 0.0f + the gradient -- the bits of an
  * accumulation into zeros -- so the output needs no clearing and is not read.

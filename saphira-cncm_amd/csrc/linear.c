@@ -39,6 +39,8 @@ typedef struct {
     float *db;
     double *dbpart;
     float *pre;
+    const float *bwd_x;
+    int bwd_kind;
 } GemmArgs;
 
 /* Must match struct GemvArgs in gemm.hip. */
@@ -177,19 +179,30 @@ static int64_t extent(int64_t rows, int64_t cols, int64_t ld) { return ((rows - 
 #define TILE_M 64
 #define TILE_N 64
 
-/* beta (accumulating kinds): 1 C += A.B, 0 C = 0.0f + A.B (C is not read).
- * db (L_DW with vec only, else NULL): the bias gradient db[i] += sum_k A(i,k)
- * is summed by the same launch. */
-static int run_gemm_pre(int kind, const float *A, const float *B, float *C, const float *bias,
-                        const float *res, int res_mul, int Mo, int No, int Kred, int lda, int ldb, int ldc,
-                        int act, int vec, int beta, float *db, float *pre) {
+/* Optional parts of a GEMM launch (NULL for a plain one; vectorised kernels
+ * only). */
+typedef struct {
+    float *db;           /* L_DW: the bias gradient db[i] += sum_k A(i,k), summed by the same launch */
+    float *pre;          /* L_FWD: also stores acc + bias before the activation */
+    const float *bwd_x;  /* L_DX: C (+)= act'(bwd_x) (0.0f + A.B), the activation backward of bwd_kind */
+    int bwd_kind;
+} GemmExtra;
+
+/* beta (accumulating kinds): 1 C += A.B, 0 C = 0.0f + A.B (C is not read). */
+static int run_gemm_x(int kind, const float *A, const float *B, float *C, const float *bias,
+                      const float *res, int res_mul, int Mo, int No, int Kred, int lda, int ldb, int ldc,
+                      int act, int vec, int beta, const GemmExtra *ex) {
+    static const GemmExtra none = {NULL, NULL, NULL, 0};
+    if (!ex) ex = &none;
+    float *db = ex->db;
     if (Mo <= 0 || No <= 0) return 0;
     const int bm = TILE_M, bn = TILE_N;
     if ((int64_t)((Mo + bm - 1) / bm) * ((No + bn - 1) / bn) > INT_MAX / 4)
         return ncm_fail(NCM_E_ARG, "linear: %d x %d output has too many tiles", Mo, No);
     char name[48], fix[48];
-    gemm_name(bm, bn, kind, vec, name, sizeof name);
-    if (db) snprintf(name, sizeof name, "gemm_%dx%d_dwb_v", bm, bn);   /* the dW kernel that also sums db */
+    /* dwb: the dW kernel that also sums db; dxa: dX through the activation backward */
+    const char *op = db ? "dwb" : ex->bwd_x ? "dxa" : kind_names[kind];
+    snprintf(name, sizeof name, "gemm_%dx%d_%s_%c", bm, bn, op, vec ? 'v' : 's');
     int slots = gemm_slots(name);
     if (slots < 0) return NCM_E_INIT;
     GemmPlan g = plan_gemm(Mo, No, Kred, slots, bm, bn);
@@ -201,7 +214,7 @@ static int run_gemm_pre(int kind, const float *A, const float *B, float *C, cons
                         (long long)ab, (long long)bb);
     GemmArgs p = {A, B, C, bias, res, NULL, Mo, No, Kred, lda, ldb, ldc, act, 0,
                   g.tiles_m, g.tiles_n, g.iters, g.dp_tiles, g.segs, (unsigned)ab, (unsigned)bb, NULL, NULL, beta,
-                  db, NULL, pre};
+                  db, NULL, ex->pre, ex->bwd_x, ex->bwd_kind};
     p.res_mul = res_mul;
     int split_tiles = g.tiles_m * g.tiles_n - g.dp_tiles;
     if (g.segs > 1) {
@@ -214,14 +227,15 @@ static int run_gemm_pre(int kind, const float *A, const float *B, float *C, cons
     void *args[] = {&p};
     int rc = ncm_launch(ncm_kernel(name), (unsigned)g.blocks, 1, 1, 256, args);
     if (rc || g.segs == 1) return rc;
-    snprintf(fix, sizeof fix, "gemm_%dx%d_fixup_%s_%c", bm, bn, db ? "dwb" : kind_names[kind], vec ? 'v' : 's');
+    snprintf(fix, sizeof fix, "gemm_%dx%d_fixup_%s_%c", bm, bn, op, vec ? 'v' : 's');
     return ncm_launch_named(fix, (unsigned)split_tiles * 4u, 1, 1, 256, args);  /* one workgroup per MFMA block */
 }
 
 static int run_gemm(int kind, const float *A, const float *B, float *C, const float *bias,
                     const float *res, int res_mul, int Mo, int No, int Kred, int lda, int ldb, int ldc,
                     int act, int vec, int beta, float *db) {
-    return run_gemm_pre(kind, A, B, C, bias, res, res_mul, Mo, No, Kred, lda, ldb, ldc, act, vec, beta, db, NULL);
+    GemmExtra ex = {db, NULL, NULL, 0};
+    return run_gemm_x(kind, A, B, C, bias, res, res_mul, Mo, No, Kred, lda, ldb, ldc, act, vec, beta, &ex);
 }
 
 /* GEMV kernel for a chunk of nb <= 8 batch rows; returns rows per workgroup. */
@@ -333,7 +347,8 @@ void ncm_linear_fwd_pre(const float *x, const float *W, const float *b, float *p
         return;
     }
     int vec = (K % 4 == 0) && is_aligned16(x) && is_aligned16(W);
-    run_gemm_pre(L_FWD, x, W, y, b, NULL, 0, (int)batch, M, K, K, K, M, act, vec, 1, NULL, pre);
+    GemmExtra ex = {NULL, pre, NULL, 0};
+    run_gemm_x(L_FWD, x, W, y, b, NULL, 0, (int)batch, M, K, K, K, M, act, vec, 1, &ex);
 }
 
 /* Both products of a gated unit in one GEMM launch when its tiles (64 rows x
@@ -361,7 +376,7 @@ void linear_fwd_gated(const float *x, const float *Wg, const float *bg, const fl
         if (ab < MAX_BUFFER_BYTES && bb < MAX_BUFFER_BYTES) {
             const int groups = (K + 4 * BK - 1) / (4 * BK);
             GemmArgs p = {x, Wg, y, bg, NULL, NULL, (int)batch, M, K, K, K, M, act, 0,
-                          tiles_m, tiles_n, 4 * groups, tiles_m * tiles_n, 1, (unsigned)ab, (unsigned)bb, Wu, bu, 1, NULL, NULL, NULL};
+                          tiles_m, tiles_n, 4 * groups, tiles_m * tiles_n, 1, (unsigned)ab, (unsigned)bb, Wu, bu, 1, NULL, NULL, NULL, NULL, 0};
             void *args[] = {&p};
             ncm_launch_named("gemm_64x64_gated_v", (unsigned)(tiles_m * tiles_n), 1, 1, 256, args);
             return;
@@ -465,6 +480,28 @@ void ncm_linear_bwd_ex(const float *x, const float *W, const float *dy, float *d
         else
             ncm_launch_named("colsum_final", (unsigned)((M + 255) / 256), 1, 1, 256, a2);
     }
+}
+
+int ncm_linear_dx_fusable(int64_t batch, int M, int K, const float *dy, const float *W) {
+    return batch > 8 && batch <= INT_MAX && M > 0 && K > 0 && M % 4 == 0 && K % 4 == 0 && is_aligned16(dy) &&
+           is_aligned16(W);
+}
+
+/* linear_bwd with the dX product passed back through the activation that
+ * produced x: dxa (+)= act'(ax) (0.0f + dy W), i.e. ncm_linear_bwd_ex's fresh
+ * dX followed by ncm_act_bwd_ex(kind, ax, dX, dxa, beta) bit for bit, with dX
+ * never stored; dW and db as linear_bwd. */
+void ncm_linear_bwd_act(const float *x, const float *W, const float *dy, float *dxa, const float *ax, int kind,
+                        int beta, float *dW, float *db, int64_t batch, int M, int K) {
+    if (check_dims("ncm_linear_bwd_act", batch, M, K)) return;
+    if (!ncm_linear_dx_fusable(batch, M, K, dy, W) || !dxa || !ax || (dW && !x)) {
+        ncm_fail(NCM_E_ARG, "ncm_linear_bwd_act: shape or operands not supported");
+        return;
+    }
+    if (ncm_ready()) return;
+    GemmExtra ex = {NULL, NULL, ax, kind == 0 || kind == 1 ? kind : 2};
+    if (run_gemm_x(L_DX, dy, W, dxa, NULL, NULL, 0, (int)batch, K, M, M, K, K, 0, 1, beta, &ex)) return;
+    ncm_linear_bwd_ex(x, W, dy, NULL, dW, db, batch, M, K, 1);
 }
 
 void linear_bwd(const float *x, const float *W, const float *dy, float *dx, float *dW, float *db,

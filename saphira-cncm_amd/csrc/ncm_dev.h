@@ -39,6 +39,26 @@ __device__ __forceinline__ float ncm_act(float v, int act) {
     }
 }
 
+// dy * act'(x) in fp64, rounded to float (the reference's activation
+// backward): kind 0 GELU (erf), 1 SiLU, 2 GELU (tanh form)
+__device__ __forceinline__ float act_bwd_one(float xf, float dyf, int kind) {
+#pragma clang fp contract(off)
+    const double xv = (double)xf;
+    double g;
+    if (kind == 0) {
+        const double e = erf(xv / 1.4142135623730951);
+        g = 0.5 * (1 + e) + xv * exp(-0.5 * xv * xv) * 0.3989422804014327;
+    } else if (kind == 1) {
+        const double s = 1.0 / (1.0 + exp(-xv));
+        g = s * (1 + xv * (1 - s));
+    } else {
+        const double c0 = 0.7978845608028654, c1 = 0.044715;
+        const double th = ncm_tanh_d(c0 * (xv + c1 * xv * xv * xv));
+        g = 0.5 * (1.0 + th) + 0.5 * xv * (1.0 - th * th) * c0 * (1.0 + 3.0 * c1 * xv * xv);
+    }
+    return (float)((double)dyf * g);
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);

@@ -495,6 +495,20 @@ void ncm_tape_backward(NcmTape *t, const NcmPMap *pm) {
         case NT_LINEAR: {
             int64_t batch = r->n;
             int M = r->p1, K = r->p2, bx;
+            const NtRec *ra = i > 0 ? &t->r[i - 1] : NULL;
+            if (ra && ra->op == NT_ACT && ra->y == r->a && ra->n == batch * K && !gmap_find(t, r->a) &&
+                ncm_linear_dx_fusable(batch, M, K, dy, r->b)) {
+                /* the record right before is the activation that produced this
+                 * linear's input, and nothing else reads that input: its
+                 * backward runs in the dX GEMM's epilogue, the input's gradient
+                 * is never stored, and the activation record is done too */
+                float *dxa = gmap_get_fresh(t, ra->a, ra->n, &bx);
+                if (!dxa) return;
+                ncm_linear_bwd_act(r->a, r->b, dy, dxa, ra->a, ra->p1, bx, gmap_get(t, r->b, (int64_t)M * K),
+                                   r->c ? gmap_get(t, r->c, M) : NULL, batch, M, K);
+                i--;
+                break;
+            }
             float *dx = gmap_get_fresh(t, r->a, batch * K, &bx);
             ncm_linear_bwd_ex(r->a, r->b, dy, dx, gmap_get(t, r->b, (int64_t)M * K),
                               r->c ? gmap_get(t, r->c, M) : NULL, batch, M, K, bx);

@@ -1119,26 +1119,6 @@ sdpa_probs_rows(const float *__restrict__ q, const float *__restrict__ k, const 
     }
 }
 
-// dy * act'(x) in fp64, rounded to float (the reference's activation
-// backward): kind 0 GELU (erf), 1 SiLU, 2 GELU (tanh form)
-__device__ __forceinline__ float act_bwd_one(float xf, float dyf, int kind) {
-#pragma clang fp contract(off)
-    const double xv = (double)xf;
-    double g;
-    if (kind == 0) {
-        const double e = erf(xv / 1.4142135623730951);
-        g = 0.5 * (1 + e) + xv * exp(-0.5 * xv * xv) * 0.3989422804014327;
-    } else if (kind == 1) {
-        const double s = 1.0 / (1.0 + exp(-xv));
-        g = s * (1 + xv * (1 - s));
-    } else {
-        const double c0 = 0.7978845608028654, c1 = 0.044715;
-        const double th = ncm_tanh_d(c0 * (xv + c1 * xv * xv * xv));
-        g = 0.5 * (1.0 + th) + 0.5 * xv * (1.0 - th * th) * c0 * (1.0 + 3.0 * c1 * xv * xv);
-    }
-    return (float)((double)dyf * g);
-}
-
 // ---------------------------------------------------------------- elementwise backward
 // train_tape.c:830-873: dx += (float)(dy * g(x)), g in fp64.
 // kind 0 gelu (erf), 1 silu, 2 gelu_tanh (gelu_new).

@@ -9,7 +9,8 @@ makes exact:
   train_gpt2.c:42-147 does) gives the same loss and the same gradients, bit
   for bit, as the library's ncm_gpt2_forward driver;
 - c_fc and mlp.c_proj of the first and last block: dW and db rows (sums over
-  all 16384 rows) and dx rows;
+  all 16384 rows) and dx rows (for c_proj, passed back through the GELU,
+  which its dX GEMM does in the epilogue);
 - SDPA backward (causal, T = 512) on sampled (batch, head) slices: dq, dk, dv;
 - softmax cross-entropy: the loss over all rows and dlogits on sampled rows;
 - the tied head's dx rows and ln_f's dw, db (over all rows) and dx rows.
@@ -169,8 +170,14 @@ def test_mlp_linears_full_rows(step, li):
         assert maxrel(gb[ms], db) <= 1e-4, (which, "db", maxrel(gb[ms], db))
         rs = sample(R, 30, li * 11 + wi)
         dx, _, _ = O.linear_bwd(x[rs], W, dy[rs], want=("dx",))
-        # mn feeds only c_fc and m2 only c_proj: their gradients are these products' dx
-        got_dx = host(step["grad"](keep[xkey]), (R, K))[rs]
+        if which == "c_fc":   # mn feeds only c_fc: its gradient is this product's dx
+            got_dx = host(step["grad"](keep[xkey]), (R, K))[rs]
+        else:
+            # m2 = gelu_tanh(mm) feeds only c_proj, so c_proj's dX GEMM applies
+            # the GELU backward in its epilogue and m2's gradient is never
+            # stored: check mm's gradient (mm feeds only the GELU)
+            dx = O.act_bwd("gelu_tanh", host(keep["mm"], (R, I))[rs], dx)
+            got_dx = host(step["grad"](keep["mm"]), (R, I))[rs]
         assert maxrel(got_dx, dx) <= 1e-4, (which, "dx", maxrel(got_dx, dx))
 
 

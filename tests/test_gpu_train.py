@@ -387,3 +387,52 @@ def test_tape_fused_linear_records(R, K, M):
     for n in g1:
         assert bits_equal(g1[n], g2[n]), n
     assert bits_equal(g1["res"], g)
+
+
+@pytest.mark.parametrize("kind", [0, 1, 2])
+@pytest.mark.parametrize("R,K0,K1,M", [(300, 64, 96, 128), (130, 768, 3072, 768), (33, 20, 36, 52), (6, 32, 64, 48)])
+def test_tape_activation_backward_in_dx_gemm(kind, R, K0, K1, M):
+    """linear -> activation -> linear on the tape: when nothing else reads the
+    activation's output, the second linear's dX GEMM applies the activation
+    backward in its epilogue and that gradient is never stored.  Against the
+    same tape with the activation output's gradient requested (which keeps the
+    two records apart): every gradient bit for bit, including the
+    pre-activation's.  Shapes: whole tiles, the GPT-2 MLP widths (split-K
+    fixup), ragged tiles, and a batch of at most 8 (no fusion)."""
+    lib = ncmhip.load()
+    x, W1, b1 = rnd(80, R, K0), rnd(81, K1, K0, scale=0.2), rnd(82, K1)
+    W2, b2, g = rnd(83, M, K1, scale=0.2), rnd(84, M), rnd(85, R, M)
+    act = (lib.ncm_t_gelu, lib.ncm_t_silu, lib.ncm_t_gelu_tanh)[kind]
+
+    def run(keep_h):
+        ins = {"x": x, "W1": W1, "b1": b1, "W2": W2, "b2": b2}
+        bufs = {n: up(a) for n, a in ins.items()}
+        pre, h, y = D.empty((R, K1)), D.empty((R, K1)), D.empty((R, M))
+        grads = {n: D.from_numpy(np.zeros_like(a)) for n, a in ins.items()}
+        gy, gh = up(g), D.from_numpy(np.zeros((R, K1), np.float32))
+        tape = lib.ncm_tape_new()
+        try:
+            lib.ncm_t_linear(tape, bufs["x"].ptr, bufs["W1"].ptr, bufs["b1"].ptr, pre.ptr, R, K1, K0)
+            act(tape, pre.ptr, h.ptr, R * K1)
+            lib.ncm_t_linear(tape, h.ptr, bufs["W2"].ptr, bufs["b2"].ptr, y.ptr, R, M, K1)
+            ncmhip.check()
+            keys = [bufs[n].ptr for n in ins] + [y.ptr] + ([h.ptr] if keep_h else [])
+            gps = [grads[n].ptr for n in ins] + [gy.ptr] + ([gh.ptr] if keep_h else [])
+            sz = [a.size for a in ins.values()] + [g.size] + ([R * K1] if keep_h else [])
+            n = len(keys)
+            pm = _PMap(ctypes.cast((ctypes.c_void_p * n)(*keys), ctypes.c_void_p),
+                       ctypes.cast((ctypes.c_void_p * n)(*gps), ctypes.c_void_p),
+                       ctypes.cast((ctypes.c_int64 * n)(*sz), ctypes.c_void_p), n)
+            lib.ncm_tape_backward(tape, ctypes.byref(pm))
+            ncmhip.check()
+            gpre = np.empty((R, K1), np.float32)
+            lib.mem_d2h(gpre.ctypes.data, lib.ncm_tape_grad(tape, pre.ptr), gpre.nbytes)
+            ncmhip.check()
+            return {n: grads[n].numpy() for n in ins} | {"pre": gpre}
+        finally:
+            lib.ncm_tape_free(tape)
+
+    fused, apart = run(False), run(True)
+    for n in apart:
+        assert bits_equal(fused[n], apart[n]), n
+    assert np.any(apart["pre"]) and np.any(apart["x"])

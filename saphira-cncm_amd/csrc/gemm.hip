@@ -78,7 +78,32 @@ struct GemmArgs {
     float *pre;          // STORE or null: also stores acc + bias (before the activation) at the same index
     const float *bwd_x;  // ACT_BWD: the activation's input, indexed like C
     int bwd_kind;        // ACT_BWD: 0 GELU (erf), 1 SiLU, 2 GELU (tanh form)
+    // F3 kernels (gemm_64x64_fwd3_v): up to three products of the same A side by
+    // side, product g owning n3[g] output columns (a multiple of 64 but the
+    // last) with its own B (extent b3_bytes[g]), bias and output [Mo][n3[g]]
+    const float *B3[3];
+    const float *bias3[3];
+    float *C3[3];
+    int n3[3];
+    unsigned b3_bytes[3];
 };
+
+// F3: the product that output column jt (a tile's first) belongs to, written
+// into q (a copy of the arguments) as a plain GEMM's B, bias, output and
+// width; returns the product's first column.  The tables are read from the
+// kernel's own arguments: selecting from the copy's arrays would index them
+// at run time and keep the copy in scratch memory.
+__device__ __forceinline__ int f3_select(const GemmArgs &src, GemmArgs &q, int jt) {
+    const int n0 = src.n3[0], n01 = n0 + src.n3[1];
+    const int g = jt < n0 ? 0 : jt < n01 ? 1 : 2;
+    q.B = g == 0 ? src.B3[0] : g == 1 ? src.B3[1] : src.B3[2];
+    q.bias = g == 0 ? src.bias3[0] : g == 1 ? src.bias3[1] : src.bias3[2];
+    q.C = g == 0 ? src.C3[0] : g == 1 ? src.C3[1] : src.C3[2];
+    q.No = g == 0 ? n0 : g == 1 ? src.n3[1] : src.n3[2];
+    q.ldc = q.No;
+    q.b_bytes = g == 0 ? src.b3_bytes[0] : g == 1 ? src.b3_bytes[1] : src.b3_bytes[2];
+    return g == 0 ? 0 : g == 1 ? n0 : n01;
+}
 
 // Grouped raster: GROUP_M tile rows advance together along N so that the B
 // panels they share stay in L2.
@@ -762,11 +787,14 @@ __device__ __forceinline__ void g_epilogue_blk_act(const GemmArgs &p, const f4 &
 // of a thread's segment loads are issued before the first add: the launch
 // is one round trip of latency, not one per segment.
 #define FIXUP_MAX_SEGS 16
-template <int EPI, bool IA, bool IB, bool DB>
-__device__ __forceinline__ void gemm_tile_fixup_body(const GemmArgs &p) {
+template <int EPI, bool IA, bool IB, bool DB, bool F3 = false>
+__device__ __forceinline__ void gemm_tile_fixup_body(const GemmArgs &pa) {
     const int tid = threadIdx.x, tail = blockIdx.x >> 2, blk = blockIdx.x & 3;
     int tm, tn;
-    tile_rc<8>(p.dp_tiles + tail, p.tiles_m, p.tiles_n, tm, tn);
+    tile_rc<8>(pa.dp_tiles + tail, pa.tiles_m, pa.tiles_n, tm, tn);
+    GemmArgs pl = pa;
+    const int jb = F3 ? f3_select(pa, pl, tn * 64) : 0;
+    const GemmArgs &p = F3 ? pl : pa;
     const float *first = p.ws + (int64_t)tail * p.segs * 4096 + (blk * GEMM_NT + tid) * 4;
     // unconditional loads (a segment index clamped to the last one, the extra
     // values not added): a guarded load is a branch with a wait after it
@@ -776,7 +804,7 @@ __device__ __forceinline__ void gemm_tile_fixup_body(const GemmArgs &p) {
     f4 tot = part[0];
 #pragma unroll
     for (int s = 1; s < FIXUP_MAX_SEGS; ++s) tot = s < p.segs ? tot + part[s] : tot;
-    const int a = blk >> 1, b = blk & 1, i0 = tm * 64, j0 = tn * 64;
+    const int a = blk >> 1, b = blk & 1, i0 = tm * 64, j0 = tn * 64 - jb;
     if (EPI == EPI_ACCUM || EPI == EPI_ACT_BWD) {
         g_epilogue_blk_act<EPI, ACT_NONE, IA, IB>(p, tot, a, b, i0, j0, tid);
         // dW: the bias gradient of a split tile in tile column 0, from its
@@ -847,9 +875,10 @@ struct BoolTag {
     static constexpr bool value = V;
 };
 
-// DB: the dW kernel that also sums the bias gradient (p.db)
-template <bool AKC, bool BKC, int EPI, bool DB = false>
-__device__ __forceinline__ void gemm_dma_body(const GemmArgs &p) {
+// DB: the dW kernel that also sums the bias gradient (p.db); F3: the
+// forward of up to three products side by side (f3_select)
+template <bool AKC, bool BKC, int EPI, bool DB = false, bool F3 = false>
+__device__ __forceinline__ void gemm_dma_body(const GemmArgs &pa) {
     __shared__ __attribute__((aligned(16))) float sm[2 * 2 * D_SLAB];   // [stage][A | B]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1, li = lane & 15, lg = lane >> 4;
@@ -857,28 +886,31 @@ __device__ __forceinline__ void gemm_dma_body(const GemmArgs &p) {
     int tile, it0, it1, unit = -1;
     {
         const int b = blockIdx.x;
-        if (b < p.dp_tiles) {
-            tile = xcd_remap(b, p.dp_tiles);
+        if (b < pa.dp_tiles) {
+            tile = xcd_remap(b, pa.dp_tiles);
             it0 = 0;
-            it1 = p.iters;
+            it1 = pa.iters;
         } else {
-            const int ntail = (p.tiles_m * p.tiles_n - p.dp_tiles) * p.segs;
-            const int j = b - p.dp_tiles;
-            unit = ((p.dp_tiles & 7) == 0) ? xcd_remap(j, ntail) : j;
-            const int tail = unit / p.segs, seg = unit - tail * p.segs;
-            tile = p.dp_tiles + tail;
-            const int q4 = p.iters >> 2;
-            it0 = (int)((int64_t)seg * q4 / p.segs) * 4;
-            it1 = (int)((int64_t)(seg + 1) * q4 / p.segs) * 4;
+            const int ntail = (pa.tiles_m * pa.tiles_n - pa.dp_tiles) * pa.segs;
+            const int j = b - pa.dp_tiles;
+            unit = ((pa.dp_tiles & 7) == 0) ? xcd_remap(j, ntail) : j;
+            const int tail = unit / pa.segs, seg = unit - tail * pa.segs;
+            tile = pa.dp_tiles + tail;
+            const int q4 = pa.iters >> 2;
+            it0 = (int)((int64_t)seg * q4 / pa.segs) * 4;
+            it1 = (int)((int64_t)(seg + 1) * q4 / pa.segs) * 4;
         }
     }
     int tm, tn;
-    tile_rc<8>(tile, p.tiles_m, p.tiles_n, tm, tn);
+    tile_rc<8>(tile, pa.tiles_m, pa.tiles_n, tm, tn);
+    GemmArgs pl = pa;
+    const int jb = F3 ? f3_select(pa, pl, tn * 64) : 0;
+    const GemmArgs &p = F3 ? pl : pa;
     // GATED: tile columns 0-31 are output columns j0 .. j0 + 31 of the gate
     // product, 32-63 the same columns of the up product; waves 0-1 load the
     // gate's B rows, waves 2-3 the up projection's
     const bool up_rows = EPI == EPI_GATED && wave >= 2;
-    const int i0 = tm * 64, j0 = tn * (EPI == EPI_GATED ? 32 : 64);
+    const int i0 = tm * 64, j0 = tn * (EPI == EPI_GATED ? 32 : 64) - jb;
     const int kend = min(p.K, it1 * GEMM_BK);
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, p.a_bytes), rb = make_rsrc(up_rows ? p.B2 : p.B, p.b_bytes);
     DSlab<AKC> la;
@@ -1031,27 +1063,29 @@ __device__ __forceinline__ void gemm_dma_body(const GemmArgs &p) {
         __attribute__((amdgpu_waves_per_eu(BM * BN <= 4096 ? 4 : 1))) name(GemmArgs p) {          \
         gemm_tile_body<BM, BN, AKC, BKC, EPI, VEC>(p);                                               \
     }
-#define GEMM_DMA_KERNEL(name, AKC, BKC, EPI, DB)                                                       \
+#define GEMM_DMA_KERNEL(name, AKC, BKC, EPI, DB, F3)                                                   \
     extern "C" __global__ void __launch_bounds__(GEMM_NT) __attribute__((amdgpu_waves_per_eu(4)))      \
         name(GemmArgs p) {                                                                             \
-        gemm_dma_body<AKC, BKC, EPI, DB>(p);                                                           \
+        gemm_dma_body<AKC, BKC, EPI, DB, F3>(p);                                                       \
     }
-#define GEMM_TILE_FIXUP(name, EPI, IA, IB, DB) \
-    extern "C" __global__ void __launch_bounds__(GEMM_NT) name(GemmArgs p) { gemm_tile_fixup_body<EPI, IA, IB, DB>(p); }
-GEMM_DMA_KERNEL(gemm_64x64_fwd_v, true, true, EPI_STORE, false)
-GEMM_DMA_KERNEL(gemm_64x64_dx_v, true, false, EPI_ACCUM, false)
-GEMM_DMA_KERNEL(gemm_64x64_dw_v, false, false, EPI_ACCUM, false)
-GEMM_DMA_KERNEL(gemm_64x64_dwb_v, false, false, EPI_ACCUM, true)   // dW + db
-GEMM_DMA_KERNEL(gemm_64x64_dxa_v, true, false, EPI_ACT_BWD, false) // dX through the activation backward
-GEMM_DMA_KERNEL(gemm_64x64_gated_v, true, true, EPI_GATED, false)
+#define GEMM_TILE_FIXUP(name, EPI, IA, IB, DB, F3) \
+    extern "C" __global__ void __launch_bounds__(GEMM_NT) name(GemmArgs p) { gemm_tile_fixup_body<EPI, IA, IB, DB, F3>(p); }
+GEMM_DMA_KERNEL(gemm_64x64_fwd_v, true, true, EPI_STORE, false, false)
+GEMM_DMA_KERNEL(gemm_64x64_fwd3_v, true, true, EPI_STORE, false, true)   // products side by side
+GEMM_DMA_KERNEL(gemm_64x64_dx_v, true, false, EPI_ACCUM, false, false)
+GEMM_DMA_KERNEL(gemm_64x64_dw_v, false, false, EPI_ACCUM, false, false)
+GEMM_DMA_KERNEL(gemm_64x64_dwb_v, false, false, EPI_ACCUM, true, false)   // dW + db
+GEMM_DMA_KERNEL(gemm_64x64_dxa_v, true, false, EPI_ACT_BWD, false, false) // dX through the activation backward
+GEMM_DMA_KERNEL(gemm_64x64_gated_v, true, true, EPI_GATED, false, false)
 GEMM_TILE_KERNEL(gemm_64x64_fwd_s, 64, 64, true, true, EPI_STORE, false)
 GEMM_TILE_KERNEL(gemm_64x64_dx_s, 64, 64, true, false, EPI_ACCUM, false)
 GEMM_TILE_KERNEL(gemm_64x64_dw_s, 64, 64, false, false, EPI_ACCUM, false)
-GEMM_TILE_FIXUP(gemm_64x64_fixup_fwd_v, EPI_STORE, false, false, false)
-GEMM_TILE_FIXUP(gemm_64x64_fixup_dx_v, EPI_ACCUM, false, true, false)
-GEMM_TILE_FIXUP(gemm_64x64_fixup_dw_v, EPI_ACCUM, true, true, false)
-GEMM_TILE_FIXUP(gemm_64x64_fixup_dwb_v, EPI_ACCUM, true, true, true)
-GEMM_TILE_FIXUP(gemm_64x64_fixup_dxa_v, EPI_ACT_BWD, false, true, false)
-GEMM_TILE_FIXUP(gemm_64x64_fixup_fwd_s, EPI_STORE, false, false, false)
-GEMM_TILE_FIXUP(gemm_64x64_fixup_dx_s, EPI_ACCUM, false, false, false)
-GEMM_TILE_FIXUP(gemm_64x64_fixup_dw_s, EPI_ACCUM, false, false, false)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_fwd_v, EPI_STORE, false, false, false, false)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_fwd3_v, EPI_STORE, false, false, false, true)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_dx_v, EPI_ACCUM, false, true, false, false)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_dw_v, EPI_ACCUM, true, true, false, false)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_dwb_v, EPI_ACCUM, true, true, true, false)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_dxa_v, EPI_ACT_BWD, false, true, false, false)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_fwd_s, EPI_STORE, false, false, false, false)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_dx_s, EPI_ACCUM, false, false, false, false)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_dw_s, EPI_ACCUM, false, false, false, false)

@@ -53,6 +53,9 @@ void ncm_adamw_update_clear(float *p, float *g, float *m, float *v, int64_t n, d
  * bit linear_fwd followed by the elementwise activation (linear.c). */
 void ncm_linear_fwd_pre(const float *x, const float *W, const float *b, float *pre, float *y, int64_t batch,
                         int M, int K, int act);
+/* Three linear_fwd products of the same x in one GEMM launch (linear.c). */
+void ncm_linear_fwd3(const float *x, const float *const W[3], const float *const b[3], float *const y[3],
+                     const int N[3], int64_t batch, int K);
 /* 1 when linear_bwd's dX runs as one vectorised GEMM (batch > 8, M and K
  * multiples of 4, dy and W 16-byte aligned): then ncm_linear_bwd_act applies. */
 int ncm_linear_dx_fusable(int64_t batch, int M, int K, const float *dy, const float *W);
@@ -93,6 +96,10 @@ int ncm_clip_adamw_multi(float *const *P, float *const *G, float *const *M, floa
  * W [D][D][K]; launches only. */
 int ncm_conv1d_btd(const float *x, const float *W, const float *b, float *y, int B, int T, int D, int K, int stride,
                    int pad);
+/* sdpa_fwd_gqa_causal with the heads merged on output: out [B][Tq][Hq * hd]
+ * (the values of sdpa_fwd_gqa_causal followed by head_merge_fwd). */
+void ncm_sdpa_fwd_causal_merged(const float *q, const float *k, const float *v, float *out, int B, int Hq, int Hkv,
+                                int Tq, int Tkv, int hd);
 /* SDPA forward (hd 64, 16-byte aligned operands) that also writes each
  * query row's softmax (max, sum) to stats [B][Hq][Tq][2]; causal generates
  * the mask (query t sees keys <= t + Tkv - Tq) instead of reading one. */

@@ -41,6 +41,11 @@ typedef struct {
     float *pre;
     const float *bwd_x;
     int bwd_kind;
+    const float *B3[3];
+    const float *bias3[3];
+    float *C3[3];
+    int n3[3];
+    unsigned b3_bytes[3];
 } GemmArgs;
 
 /* Must match struct GemvArgs in gemm.hip. */
@@ -186,13 +191,17 @@ typedef struct {
     float *pre;          /* L_FWD: also stores acc + bias before the activation */
     const float *bwd_x;  /* L_DX: C (+)= act'(bwd_x) (0.0f + A.B), the activation backward of bwd_kind */
     int bwd_kind;
+    const float *const *W3;   /* L_FWD: three products side by side (B, bias, output, width each) */
+    const float *const *b3;
+    float *const *y3;
+    const int *n3;
 } GemmExtra;
 
 /* beta (accumulating kinds): 1 C += A.B, 0 C = 0.0f + A.B (C is not read). */
 static int run_gemm_x(int kind, const float *A, const float *B, float *C, const float *bias,
                       const float *res, int res_mul, int Mo, int No, int Kred, int lda, int ldb, int ldc,
                       int act, int vec, int beta, const GemmExtra *ex) {
-    static const GemmExtra none = {NULL, NULL, NULL, 0};
+    static const GemmExtra none = {NULL, NULL, NULL, 0, NULL, NULL, NULL, NULL};
     if (!ex) ex = &none;
     float *db = ex->db;
     if (Mo <= 0 || No <= 0) return 0;
@@ -201,7 +210,7 @@ static int run_gemm_x(int kind, const float *A, const float *B, float *C, const 
         return ncm_fail(NCM_E_ARG, "linear: %d x %d output has too many tiles", Mo, No);
     char name[48], fix[48];
     /* dwb: the dW kernel that also sums db; dxa: dX through the activation backward */
-    const char *op = db ? "dwb" : ex->bwd_x ? "dxa" : kind_names[kind];
+    const char *op = db ? "dwb" : ex->bwd_x ? "dxa" : ex->W3 ? "fwd3" : kind_names[kind];
     snprintf(name, sizeof name, "gemm_%dx%d_%s_%c", bm, bn, op, vec ? 'v' : 's');
     int slots = gemm_slots(name);
     if (slots < 0) return NCM_E_INIT;
@@ -214,8 +223,16 @@ static int run_gemm_x(int kind, const float *A, const float *B, float *C, const 
                         (long long)ab, (long long)bb);
     GemmArgs p = {A, B, C, bias, res, NULL, Mo, No, Kred, lda, ldb, ldc, act, 0,
                   g.tiles_m, g.tiles_n, g.iters, g.dp_tiles, g.segs, (unsigned)ab, (unsigned)bb, NULL, NULL, beta,
-                  db, NULL, ex->pre, ex->bwd_x, ex->bwd_kind};
+                  db, NULL, ex->pre, ex->bwd_x, ex->bwd_kind, {NULL}, {NULL}, {NULL}, {0}, {0}};
     p.res_mul = res_mul;
+    if (ex->W3)
+        for (int g = 0; g < 3; g++) {
+            p.B3[g] = ex->W3[g];
+            p.bias3[g] = ex->b3[g];
+            p.C3[g] = ex->y3[g];
+            p.n3[g] = ex->n3[g];
+            p.b3_bytes[g] = (unsigned)extent(ex->n3[g], Kred, ldb);
+        }
     int split_tiles = g.tiles_m * g.tiles_n - g.dp_tiles;
     if (g.segs > 1) {
         /* partial tiles [units][64 * 64] floats, then the bias partials [units][64] doubles */
@@ -234,7 +251,7 @@ static int run_gemm_x(int kind, const float *A, const float *B, float *C, const 
 static int run_gemm(int kind, const float *A, const float *B, float *C, const float *bias,
                     const float *res, int res_mul, int Mo, int No, int Kred, int lda, int ldb, int ldc,
                     int act, int vec, int beta, float *db) {
-    GemmExtra ex = {db, NULL, NULL, 0};
+    GemmExtra ex = {db, NULL, NULL, 0, NULL, NULL, NULL, NULL};
     return run_gemm_x(kind, A, B, C, bias, res, res_mul, Mo, No, Kred, lda, ldb, ldc, act, vec, beta, &ex);
 }
 
@@ -347,7 +364,7 @@ void ncm_linear_fwd_pre(const float *x, const float *W, const float *b, float *p
         return;
     }
     int vec = (K % 4 == 0) && is_aligned16(x) && is_aligned16(W);
-    GemmExtra ex = {NULL, pre, NULL, 0};
+    GemmExtra ex = {NULL, pre, NULL, 0, NULL, NULL, NULL, NULL};
     run_gemm_x(L_FWD, x, W, y, b, NULL, 0, (int)batch, M, K, K, K, M, act, vec, 1, &ex);
 }
 
@@ -376,7 +393,8 @@ void linear_fwd_gated(const float *x, const float *Wg, const float *bg, const fl
         if (ab < MAX_BUFFER_BYTES && bb < MAX_BUFFER_BYTES) {
             const int groups = (K + 4 * BK - 1) / (4 * BK);
             GemmArgs p = {x, Wg, y, bg, NULL, NULL, (int)batch, M, K, K, K, M, act, 0,
-                          tiles_m, tiles_n, 4 * groups, tiles_m * tiles_n, 1, (unsigned)ab, (unsigned)bb, Wu, bu, 1, NULL, NULL, NULL, NULL, 0};
+                          tiles_m, tiles_n, 4 * groups, tiles_m * tiles_n, 1, (unsigned)ab, (unsigned)bb, Wu, bu, 1, NULL, NULL, NULL, NULL, 0,
+                          {NULL}, {NULL}, {NULL}, {0}, {0}};
             void *args[] = {&p};
             ncm_launch_named("gemm_64x64_gated_v", (unsigned)(tiles_m * tiles_n), 1, 1, 256, args);
             return;
@@ -482,6 +500,39 @@ void ncm_linear_bwd_ex(const float *x, const float *W, const float *dy, float *d
     }
 }
 
+/* Three linear_fwd products of the same x (y_g = x W_g^T + b_g, W_g
+ * [N_g][K]) in one GEMM launch, the q | k | v projections; N_0 and N_1 must be
+ * multiples of 64 (a tile column never straddles two products), else, for
+ * batches of at most 8 or unaligned operands, the three calls. */
+void ncm_linear_fwd3(const float *x, const float *const W[3], const float *const b[3], float *const y[3],
+                     const int N[3], int64_t batch, int K) {
+    const char *fn = "ncm_linear_fwd3";
+    for (int g = 0; g < 3; g++)
+        if (check_dims(fn, batch, N[g], K)) return;
+    if (batch == 0) return;
+    int whole = N[0] % 64 == 0 && N[1] % 64 == 0 && batch > 8 && K % 4 == 0 && is_aligned16(x);
+    for (int g = 0; g < 3; g++) {
+        if (!W[g] || !y[g]) {
+            ncm_fail(NCM_E_ARG, "%s: null W/y", fn);
+            return;
+        }
+        whole = whole && is_aligned16(W[g]);
+    }
+    if (!x) {
+        ncm_fail(NCM_E_ARG, "%s: null x", fn);
+        return;
+    }
+    if (ncm_ready()) return;
+    const int64_t Nt = (int64_t)N[0] + N[1] + N[2];
+    if (!whole || Nt > INT_MAX) {
+        for (int g = 0; g < 3; g++) linear_fwd(x, W[g], b[g], y[g], batch, N[g], K);
+        return;
+    }
+    GemmExtra ex = {NULL, NULL, NULL, 0, W, b, y, N};
+    run_gemm_x(L_FWD, x, W[0], y[0], NULL, NULL, 0, (int)batch, (int)Nt, K, K, K, (int)Nt, NCM_ACT_NONE, 1, 1,
+               &ex);
+}
+
 int ncm_linear_dx_fusable(int64_t batch, int M, int K, const float *dy, const float *W) {
     return batch > 8 && batch <= INT_MAX && M > 0 && K > 0 && M % 4 == 0 && K % 4 == 0 && is_aligned16(dy) &&
            is_aligned16(W);
@@ -499,7 +550,7 @@ void ncm_linear_bwd_act(const float *x, const float *W, const float *dy, float *
         return;
     }
     if (ncm_ready()) return;
-    GemmExtra ex = {NULL, NULL, ax, kind == 0 || kind == 1 ? kind : 2};
+    GemmExtra ex = {NULL, NULL, ax, kind == 0 || kind == 1 ? kind : 2, NULL, NULL, NULL, NULL};
     if (run_gemm_x(L_DX, dy, W, dxa, NULL, NULL, 0, (int)batch, K, M, M, K, K, 0, 1, beta, &ex)) return;
     ncm_linear_bwd_ex(x, W, dy, NULL, dW, db, batch, M, K, 1);
 }

@@ -204,14 +204,17 @@ float *ncm_qwen_forward(NcmQwen *m, const int *ids, int T, int last_only) {
         float *const *w = P + 1 + QW_PER_LAYER * li;
         float *h1 = A((int64_t)T * C), *ql = A((int64_t)T * C), *kl = A((int64_t)T * K * hd),
               *vl = A((int64_t)T * K * hd), *qq = A((int64_t)T * C), *kk = A((int64_t)T * K * hd),
-              *vv = A((int64_t)T * K * hd), *ctx = A((int64_t)T * C), *mo = A((int64_t)T * C),
+              *vv = A((int64_t)T * K * hd), *mo = A((int64_t)T * C),
               *x1 = A((int64_t)T * C), *h2 = A((int64_t)T * C),
               *gu = A((int64_t)T * I), *out = A((int64_t)T * C);
         if (!out) return NULL;
         rmsnorm_fwd(h, w[0], h1, T, C);
-        linear_fwd(h1, w[1], w[2], ql, T, C, C);
-        linear_fwd(h1, w[3], w[4], kl, T, K * hd, C);
-        linear_fwd(h1, w[5], w[6], vl, T, K * hd, C);
+        {   /* q | k | v in one launch */
+            const float *const W3[3] = {w[1], w[3], w[5]}, *const b3[3] = {w[2], w[4], w[6]};
+            float *const y3[3] = {ql, kl, vl};
+            const int n3[3] = {C, K * hd, K * hd};
+            ncm_linear_fwd3(h1, W3, b3, y3, n3, T, C);
+        }
         /* heads to [H][T][hd] with RoPE, and k, v also into the KV cache for
          * the cached decode: [K][T][hd] at rows 0..T-1 of [K][n_ctx][hd] */
         float *kc = m->kcache + (size_t)li * K * c->n_ctx * hd, *vc = m->vcache + (size_t)li * K * c->n_ctx * hd;
@@ -221,8 +224,7 @@ float *ncm_qwen_forward(NcmQwen *m, const int *ids, int T, int last_only) {
                          (void *)&hd, &ld};
             if (ncm_launch_named("qkv_rope_cache_k", (unsigned)T, 1, 1, 256, a)) return NULL;
         }
-        sdpa_fwd_gqa_causal(qq, kk, vv, ctx, 1, H, K, T, T, hd);
-        head_merge_fwd(ctx, mo, 1, T, C, H, hd);
+        ncm_sdpa_fwd_causal_merged(qq, kk, vv, mo, 1, H, K, T, T, hd);   /* heads merged: mo [T][C] */
         linear_fwd_ep(mo, w[7], NULL, h, x1, T, C, C, NCM_ACT_NONE);   /* x1 = h + mo W^T */
         rmsnorm_fwd(x1, w[8], h2, T, C);
         linear_fwd_gated(h2, w[9], NULL, w[10], NULL, gu, T, I, C, NCM_ACT_SILU);   /* silu(gate) * up */

@@ -230,3 +230,31 @@ def test_run_to_run_determinism():
     a = gpu_fwd(x, W, b)
     c = gpu_fwd(x, W, b)
     assert bits_equal(a, c)
+
+
+@pytest.mark.parametrize("batch,K,ns", [(2048, 896, (896, 128, 128)), (100, 64, (64, 128, 40)),
+                                        (300, 256, (128, 64, 64)), (6, 32, (64, 64, 8)), (50, 36, (60, 64, 64))])
+def test_three_products_one_launch(batch, K, ns):
+    """ncm_linear_fwd3 (the Qwen prefill's q | k | v projections): three
+    products of the same x in one GEMM launch, each tile column inside one
+    product, against the oracle per product; a ragged last product, a product
+    without bias, and the fallbacks (a batch of at most 8, a first width that
+    is not whole tiles)."""
+    import ctypes
+    lib = ncmhip.load()
+    rng = np.random.default_rng(batch + K)
+    x = rng.standard_normal((batch, K)).astype(np.float32)
+    Ws = [(rng.standard_normal((n, K)) / np.sqrt(K)).astype(np.float32) for n in ns]
+    bs = [(rng.standard_normal(n) * 0.1).astype(np.float32) if g != 1 else None for g, n in enumerate(ns)]
+    xd, Wd = D.from_numpy(x), [D.from_numpy(W) for W in Ws]
+    bd = [None if b is None else D.from_numpy(b) for b in bs]
+    yd = [D.empty((batch, n)) for n in ns]
+    P3 = ctypes.c_void_p * 3
+    fn = lib.ncm_linear_fwd3
+    fn.restype = None
+    fn.argtypes = [ctypes.c_void_p, P3, P3, P3, ctypes.c_int * 3, ctypes.c_int64, ctypes.c_int]
+    fn(xd.ptr, P3(*[w.ptr for w in Wd]), P3(*[None if b is None else b.ptr for b in bd]),
+       P3(*[y.ptr for y in yd]), (ctypes.c_int * 3)(*ns), batch, K)
+    ncmhip.check()
+    for g in range(3):
+        assert maxrel(yd[g].numpy(), O.linear_fwd(x, Ws[g], bs[g])) <= TOL, g

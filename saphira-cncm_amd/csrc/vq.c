@@ -78,12 +78,13 @@ static int vq_search(const float *X, const float *E, int *idx, int rows, int V, 
     void *a0[] = {&s.counters};
     if ((rc = ncm_launch_named("vq_init", 1, 1, 1, 64, a0))) return rc;
     unsigned *cmax = s.counters + 1;
-    void *a1[] = {&E, &V, &D, &s.cn, &cmax};
-    if ((rc = ncm_launch_named("vq_prep_codebook", (unsigned)((V + 255) / 256), 1, 1, 256, a1))) return rc;
+    int vec = (D % 4 == 0) && is_aligned16(X) && is_aligned16(E);
+    void *a1[] = {&E, &V, &D, &vec, &s.cn, &cmax};
+    unsigned pgrid = (unsigned)((V + 3) / 4) < 256u ? (unsigned)((V + 3) / 4) : 256u;
+    if ((rc = ncm_launch_named("vq_prep_codebook_w", pgrid, 1, 1, 256, a1))) return rc;
     void *a2[] = {&X, &rows, &D, &s.xn};
     if ((rc = ncm_launch_named("vq_rownorm", (unsigned)((rows + 3) / 4), 1, 1, 256, a2))) return rc;
 
-    int vec = (D % 4 == 0) && is_aligned16(X) && is_aligned16(E);
     VqArgs p = {X, E, s.cn, s.xn, cmax, idx, s.flags, (int *)s.counters,
                 s.pairs, (int *)s.counters + 2, s.keys, s.done, rows, V, D, L, total, off};
     void *a3[] = {&p};
@@ -177,7 +178,12 @@ void vq_quantize_multiscale(const float *z, const float *const *E, const int *vo
         int first = lv == 0;
         int64_t n = (int64_t)rows * D;
         void *args[] = {&El, &idx, &rows, &V, &D, &L, &total, &off, &first, &z_hat, &z_rest};
-        if (ncm_launch_named("vq_residual", (unsigned)((n + 255) / 256), 1, 1, 256, args)) return;
+        if (D % 4 == 0 && n / 4 <= UINT32_MAX - 256 && is_aligned16(El) && is_aligned16(z_hat) &&
+            is_aligned16(z_rest)) {
+            if (ncm_launch_named("vq_residual4", (unsigned)((n / 4 + 255) / 256), 1, 1, 256, args)) return;
+        } else if (ncm_launch_named("vq_residual", (unsigned)((n + 255) / 256), 1, 1, 256, args)) {
+            return;
+        }
     }
 }
 

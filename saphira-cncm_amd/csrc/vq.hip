@@ -85,22 +85,37 @@ extern "C" __global__ void vq_init(unsigned *counters) {
 }
 
 // cn[j] = (float) sum_c E[j,c]^2 (fp64); cmax = upper bound of max_j |E_j|.
+// One wave per codeword at a time (lanes over c, float4 loads when vec), so
+// the rows are read coalesced and the fp64 sums run 64 wide; cn differs from
+// a serial sum only in the fp64 rounding order, far inside the screen's bound
+// for the rounding of |E_j|^2.  Waves stride over the codebook so that at
+// most gridDim.x (<= 256) atomics meet on cmax: one per codeword group of 4
+// had serialised there.
 extern "C" __global__ void __launch_bounds__(256)
-vq_prep_codebook(const float *__restrict__ E, int V, int D, float *__restrict__ cn, unsigned *cmax_bits) {
-    int j = blockIdx.x * 256 + threadIdx.x;
+vq_prep_codebook_w(const float *__restrict__ E, int V, int D, int vec, float *__restrict__ cn,
+                   unsigned *cmax_bits) {
+    const int lane = threadIdx.x & 63;
     float nrm = 0.f;
-    if (j < V) {
+    for (int j = blockIdx.x * 4 + (threadIdx.x >> 6); j < V; j += gridDim.x * 4) {
         const float *e = E + (int64_t)j * D;
         double s = 0.0;
-        for (int c = 0; c < D; ++c) s += (double)e[c] * (double)e[c];
-        cn[j] = (float)s;
-        nrm = (float)sqrt(s) * (1.0f + 1e-6f);
-        if (!(nrm <= FLT_MAX)) nrm = __int_as_float(0x7f800000);  // NaN/inf -> +inf
+        if (vec) {
+            for (int c = 4 * lane; c < D; c += 256) {
+                const f4 v = *(const f4 *)(e + c);
+                s += ((double)v.x * (double)v.x + (double)v.y * (double)v.y) +
+                     ((double)v.z * (double)v.z + (double)v.w * (double)v.w);
+            }
+        } else {
+            for (int c = lane; c < D; c += 64) s += (double)e[c] * (double)e[c];
+        }
+        s = wave_sum_d(s);
+        if (lane == 0) cn[j] = (float)s;
+        float n = (float)sqrt(s) * (1.0f + 1e-6f);
+        if (!(n <= FLT_MAX)) n = __int_as_float(0x7f800000);  // NaN/inf -> +inf
+        nrm = fmaxf(nrm, n);
     }
-    // block max, then one atomic per block (non-negative floats order as uints)
     __shared__ float red[4];
-    for (int o = 32; o > 0; o >>= 1) nrm = fmaxf(nrm, __shfl_xor(nrm, o, 64));
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = nrm;
+    if (lane == 0) red[threadIdx.x >> 6] = nrm;
     __syncthreads();
     if (threadIdx.x == 0) {
         float m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
@@ -116,7 +131,15 @@ vq_rownorm(const float *__restrict__ X, int rows, int D, float *__restrict__ xn)
     if (row >= rows) return;
     const float *x = X + (int64_t)row * D;
     double s = 0.0;
-    for (int c = lane; c < D; c += 64) s += (double)x[c] * (double)x[c];
+    if ((D & 3) == 0 && ((uintptr_t)X & 15) == 0) {   // float4 loads
+        for (int c = 4 * lane; c < D; c += 256) {
+            const f4 v = *(const f4 *)(x + c);
+            s += ((double)v.x * (double)v.x + (double)v.y * (double)v.y) +
+                 ((double)v.z * (double)v.z + (double)v.w * (double)v.w);
+        }
+    } else {
+        for (int c = lane; c < D; c += 64) s += (double)x[c] * (double)x[c];
+    }
     s = wave_sum_d(s);
     if (lane == 0) {
         float v = (float)sqrt(s) * (1.0f + 1e-6f);
@@ -525,6 +548,27 @@ vq_residual(const float *__restrict__ E, const int *__restrict__ idx, int rows, 
     float h = first ? 0.0f : z_hat[i];
     z_hat[i] = h + q;
     z_rest[i] = z_rest[i] - q;
+}
+
+// The same on float4 groups (D % 4 == 0, 16-byte aligned E, z_hat, z_rest):
+// the same float operations per element, the row and code found once per
+// float4 in 32-bit arithmetic (the per-element kernel's 64-bit division and
+// modulo were most of its time).
+extern "C" __global__ void __launch_bounds__(256)
+vq_residual4(const float *__restrict__ E, const int *__restrict__ idx, int rows, int V, int D, int L, int total,
+             int off, int first, float *z_hat, float *z_rest) {
+#pragma clang fp contract(off)
+    const int per = D >> 2;
+    const unsigned i4 = blockIdx.x * 256u + threadIdx.x;
+    if (i4 >= (unsigned)rows * (unsigned)per) return;
+    const int row = (int)(i4 / (unsigned)per), c = (int)(i4 - (unsigned)row * per) * 4;
+    int code = idx[code_slot(row, L, total, off)];
+    if ((unsigned)code >= (unsigned)V) code = 0;  // never read outside E
+    const f4 q = *(const f4 *)(E + (int64_t)code * D + c);
+    f4 *zh = (f4 *)(z_hat + (int64_t)row * D + c), *zr = (f4 *)(z_rest + (int64_t)row * D + c);
+    const f4 h = first ? f4{0.f, 0.f, 0.f, 0.f} : *zh, r = *zr;
+    *zh = h + q;
+    *zr = r - q;
 }
 
 // ---------------------------------------------------------------- the full quantizer

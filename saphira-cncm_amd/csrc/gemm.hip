@@ -47,10 +47,11 @@
 // (x B2^T + bias2), both products in one tile (gemm_64x64_gated_v);
 // ACT_BWD  C += act'(bwd_x) (0.0f + acc): the dX product written as a fresh
 // gradient and passed back through the activation that produced the layer's
-// input, without storing it (gemm_64x64_dxa_v).
+// input, without storing it (gemm_64x64_dxa_v); HEADS  STORE into the
+// attention's head-major layout (gemm_64x64_fwdh_v).
 #include "mfma_slab.h"
 
-enum { EPI_STORE = 0, EPI_ACCUM = 1, EPI_GATED = 2, EPI_ACT_BWD = 3 };
+enum { EPI_STORE = 0, EPI_ACCUM = 1, EPI_GATED = 2, EPI_ACT_BWD = 3, EPI_HEADS = 4 };
 
 struct GemmArgs {
     const float *A;
@@ -86,7 +87,23 @@ struct GemmArgs {
     float *C3[3];
     int n3[3];
     unsigned b3_bytes[3];
+    // HEADS (gemm_64x64_fwdh_v): the output row i = b T + t of a [q | k | v]
+    // product (part widths n3[], heads of 64) goes to C3[part] as
+    // [B][n3[part] / 64][T][64]; hm_T = T
+    int hm_T;
 };
+
+// HEADS: the address of output element (i, j).  Every tile column lies in one
+// head of one part (the widths are multiples of 64), so the part is uniform.
+__device__ __forceinline__ float *heads_addr(const GemmArgs &p, int i, int j) {
+    const int n0 = p.n3[0], n01 = n0 + p.n3[1];
+    const int g = __builtin_amdgcn_readfirstlane(j < n0 ? 0 : j < n01 ? 1 : 2);
+    const int jl = j - (g == 0 ? 0 : g == 1 ? n0 : n01);
+    const int hw = (g == 0 ? n0 : g == 1 ? p.n3[1] : p.n3[2]) >> 6;
+    float *const base = g == 0 ? p.C3[0] : g == 1 ? p.C3[1] : p.C3[2];
+    const int b = i / p.hm_T, t = i - b * p.hm_T;
+    return base + (((int64_t)b * hw + (jl >> 6)) * p.hm_T + t) * 64 + (jl & 63);
+}
 
 // F3: the product that output column jt (a tile's first) belongs to, written
 // into q (a copy of the arguments) as a plain GEMM's B, bias, output and
@@ -569,7 +586,7 @@ __device__ __forceinline__ void g_out_n(const GemmArgs &p, const int (&ii)[N], c
 #pragma unroll
     for (int n = 0; n < N; ++n) {
         if (ii[n] >= p.Mo || jj[n] >= p.No) continue;
-        float *c = p.C + (int64_t)ii[n] * p.ldc + jj[n];
+        float *c = EPI == EPI_HEADS ? heads_addr(p, ii[n], jj[n]) : p.C + (int64_t)ii[n] * p.ldc + jj[n];
         float x = v[n];
         if (EPI == EPI_ACCUM) {
             *c = o1[n] + x;
@@ -1072,6 +1089,7 @@ __device__ __forceinline__ void gemm_dma_body(const GemmArgs &pa) {
     extern "C" __global__ void __launch_bounds__(GEMM_NT) name(GemmArgs p) { gemm_tile_fixup_body<EPI, IA, IB, DB, F3>(p); }
 GEMM_DMA_KERNEL(gemm_64x64_fwd_v, true, true, EPI_STORE, false, false)
 GEMM_DMA_KERNEL(gemm_64x64_fwd3_v, true, true, EPI_STORE, false, true)   // products side by side
+GEMM_DMA_KERNEL(gemm_64x64_fwdh_v, true, true, EPI_HEADS, false, false)  // q | k | v to head-major
 GEMM_DMA_KERNEL(gemm_64x64_dx_v, true, false, EPI_ACCUM, false, false)
 GEMM_DMA_KERNEL(gemm_64x64_dw_v, false, false, EPI_ACCUM, false, false)
 GEMM_DMA_KERNEL(gemm_64x64_dwb_v, false, false, EPI_ACCUM, true, false)   // dW + db
@@ -1082,6 +1100,7 @@ GEMM_TILE_KERNEL(gemm_64x64_dx_s, 64, 64, true, false, EPI_ACCUM, false)
 GEMM_TILE_KERNEL(gemm_64x64_dw_s, 64, 64, false, false, EPI_ACCUM, false)
 GEMM_TILE_FIXUP(gemm_64x64_fixup_fwd_v, EPI_STORE, false, false, false, false)
 GEMM_TILE_FIXUP(gemm_64x64_fixup_fwd3_v, EPI_STORE, false, false, false, true)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_fwdh_v, EPI_HEADS, false, false, false, false)
 GEMM_TILE_FIXUP(gemm_64x64_fixup_dx_v, EPI_ACCUM, false, true, false, false)
 GEMM_TILE_FIXUP(gemm_64x64_fixup_dw_v, EPI_ACCUM, true, true, false, false)
 GEMM_TILE_FIXUP(gemm_64x64_fixup_dwb_v, EPI_ACCUM, true, true, true, false)

@@ -71,8 +71,7 @@ static float *gpt2_block(NcmTape *tp, const NcmGpt2Config *c, float *const *P, i
     float *mm = A(R * I), *m2 = A(R * I), *out = A(R * C);
     if (!out) return NULL;
     ncm_t_layernorm_eps(tp, x, w[0], w[1], ln, R, C, GPT2_LN_EPS);
-    ncm_t_linear(tp, ln, w[2], w[3], qkv, R, 3 * C, C);
-    ncm_t_qkvsplit(tp, qkv, qq, kk, vv, B, T, C, H, hd, H, 1);
+    ncm_t_linear_qkvsplit(tp, ln, w[2], w[3], qkv, qq, kk, vv, B, T, C, H, hd, H, 1);   /* GEMM to heads */
     ncm_t_sdpa_causal(tp, qq, kk, vv, ctx, B, H, H, T, T, hd);   /* the -1e9 causal mask, generated */
     ncm_t_headmerge(tp, ctx, mo, B, T, C, H, hd);
     ncm_t_linear_res(tp, mo, w[4], w[5], x, x1, R, C, C);   /* x1 = x + attn proj */

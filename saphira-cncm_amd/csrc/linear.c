@@ -46,6 +46,7 @@ typedef struct {
     float *C3[3];
     int n3[3];
     unsigned b3_bytes[3];
+    int hm_T;
 } GemmArgs;
 
 /* Must match struct GemvArgs in gemm.hip. */
@@ -195,13 +196,15 @@ typedef struct {
     const float *const *b3;
     float *const *y3;
     const int *n3;
+    float *const *heads;      /* L_FWD: q | k | v parts of the output to head-major [B][n/64][T][64] */
+    int hm_T;
 } GemmExtra;
 
 /* beta (accumulating kinds): 1 C += A.B, 0 C = 0.0f + A.B (C is not read). */
 static int run_gemm_x(int kind, const float *A, const float *B, float *C, const float *bias,
                       const float *res, int res_mul, int Mo, int No, int Kred, int lda, int ldb, int ldc,
                       int act, int vec, int beta, const GemmExtra *ex) {
-    static const GemmExtra none = {NULL, NULL, NULL, 0, NULL, NULL, NULL, NULL};
+    static const GemmExtra none = {NULL, NULL, NULL, 0, NULL, NULL, NULL, NULL, NULL, 0};
     if (!ex) ex = &none;
     float *db = ex->db;
     if (Mo <= 0 || No <= 0) return 0;
@@ -210,7 +213,7 @@ static int run_gemm_x(int kind, const float *A, const float *B, float *C, const 
         return ncm_fail(NCM_E_ARG, "linear: %d x %d output has too many tiles", Mo, No);
     char name[48], fix[48];
     /* dwb: the dW kernel that also sums db; dxa: dX through the activation backward */
-    const char *op = db ? "dwb" : ex->bwd_x ? "dxa" : ex->W3 ? "fwd3" : kind_names[kind];
+    const char *op = db ? "dwb" : ex->bwd_x ? "dxa" : ex->W3 ? "fwd3" : ex->heads ? "fwdh" : kind_names[kind];
     snprintf(name, sizeof name, "gemm_%dx%d_%s_%c", bm, bn, op, vec ? 'v' : 's');
     int slots = gemm_slots(name);
     if (slots < 0) return NCM_E_INIT;
@@ -223,7 +226,7 @@ static int run_gemm_x(int kind, const float *A, const float *B, float *C, const 
                         (long long)ab, (long long)bb);
     GemmArgs p = {A, B, C, bias, res, NULL, Mo, No, Kred, lda, ldb, ldc, act, 0,
                   g.tiles_m, g.tiles_n, g.iters, g.dp_tiles, g.segs, (unsigned)ab, (unsigned)bb, NULL, NULL, beta,
-                  db, NULL, ex->pre, ex->bwd_x, ex->bwd_kind, {NULL}, {NULL}, {NULL}, {0}, {0}};
+                  db, NULL, ex->pre, ex->bwd_x, ex->bwd_kind, {NULL}, {NULL}, {NULL}, {0}, {0}, ex->hm_T};
     p.res_mul = res_mul;
     if (ex->W3)
         for (int g = 0; g < 3; g++) {
@@ -232,6 +235,11 @@ static int run_gemm_x(int kind, const float *A, const float *B, float *C, const 
             p.C3[g] = ex->y3[g];
             p.n3[g] = ex->n3[g];
             p.b3_bytes[g] = (unsigned)extent(ex->n3[g], Kred, ldb);
+        }
+    if (ex->heads)
+        for (int g = 0; g < 3; g++) {
+            p.C3[g] = ex->heads[g];
+            p.n3[g] = ex->n3[g];
         }
     int split_tiles = g.tiles_m * g.tiles_n - g.dp_tiles;
     if (g.segs > 1) {
@@ -251,7 +259,7 @@ static int run_gemm_x(int kind, const float *A, const float *B, float *C, const 
 static int run_gemm(int kind, const float *A, const float *B, float *C, const float *bias,
                     const float *res, int res_mul, int Mo, int No, int Kred, int lda, int ldb, int ldc,
                     int act, int vec, int beta, float *db) {
-    GemmExtra ex = {db, NULL, NULL, 0, NULL, NULL, NULL, NULL};
+    GemmExtra ex = {db, NULL, NULL, 0, NULL, NULL, NULL, NULL, NULL, 0};
     return run_gemm_x(kind, A, B, C, bias, res, res_mul, Mo, No, Kred, lda, ldb, ldc, act, vec, beta, &ex);
 }
 
@@ -364,7 +372,7 @@ void ncm_linear_fwd_pre(const float *x, const float *W, const float *b, float *p
         return;
     }
     int vec = (K % 4 == 0) && is_aligned16(x) && is_aligned16(W);
-    GemmExtra ex = {NULL, pre, NULL, 0, NULL, NULL, NULL, NULL};
+    GemmExtra ex = {NULL, pre, NULL, 0, NULL, NULL, NULL, NULL, NULL, 0};
     run_gemm_x(L_FWD, x, W, y, b, NULL, 0, (int)batch, M, K, K, K, M, act, vec, 1, &ex);
 }
 
@@ -394,7 +402,7 @@ void linear_fwd_gated(const float *x, const float *Wg, const float *bg, const fl
             const int groups = (K + 4 * BK - 1) / (4 * BK);
             GemmArgs p = {x, Wg, y, bg, NULL, NULL, (int)batch, M, K, K, K, M, act, 0,
                           tiles_m, tiles_n, 4 * groups, tiles_m * tiles_n, 1, (unsigned)ab, (unsigned)bb, Wu, bu, 1, NULL, NULL, NULL, NULL, 0,
-                          {NULL}, {NULL}, {NULL}, {0}, {0}};
+                          {NULL}, {NULL}, {NULL}, {0}, {0}, 0};
             void *args[] = {&p};
             ncm_launch_named("gemm_64x64_gated_v", (unsigned)(tiles_m * tiles_n), 1, 1, 256, args);
             return;
@@ -528,9 +536,35 @@ void ncm_linear_fwd3(const float *x, const float *const W[3], const float *const
         for (int g = 0; g < 3; g++) linear_fwd(x, W[g], b[g], y[g], batch, N[g], K);
         return;
     }
-    GemmExtra ex = {NULL, NULL, NULL, 0, W, b, y, N};
+    GemmExtra ex = {NULL, NULL, NULL, 0, W, b, y, N, NULL, 0};
     run_gemm_x(L_FWD, x, W[0], y[0], NULL, NULL, 0, (int)batch, (int)Nt, K, K, K, (int)Nt, NCM_ACT_NONE, 1, 1,
                &ex);
+}
+
+/* linear_fwd into qkv [B*T][C + 2 K hd] followed by qkv_split_fwd(qkv, qq, kk,
+ * vv, B, T, C, H, hd, K, rep): for hd = 64, C = H hd, one kv head per query
+ * head (K = H, rep = 1: the split copies each kv head once) and aligned
+ * operands the GEMM writes qq, kk and vv [B][H][T][hd] from its epilogue (the
+ * same values) and qkv is not written; otherwise the two calls. */
+void ncm_linear_fwd_qkv_heads(const float *x, const float *W, const float *b, float *qkv, float *qq, float *kk,
+                              float *vv, int B, int T, int C, int H, int hd, int K, int rep) {
+    const int64_t rows = (int64_t)B * T, N = (int64_t)C + 2LL * K * hd;
+    if (B < 0 || T < 0 || N > INT_MAX || rows > INT_MAX) {
+        ncm_fail(NCM_E_ARG, "ncm_linear_fwd_qkv_heads: bad shape");
+        return;
+    }
+    int whole = hd == 64 && C == H * hd && C % 64 == 0 && K == H && rep == 1 && rows > 8 &&
+                C % 4 == 0 && x && W && qq && kk && vv && is_aligned16(x) && is_aligned16(W);
+    if (!whole) {
+        linear_fwd(x, W, b, qkv, rows, (int)N, C);
+        qkv_split_fwd(qkv, qq, kk, vv, B, T, C, H, hd, K, rep);
+        return;
+    }
+    if (check_dims("ncm_linear_fwd_qkv_heads", rows, (int)N, C) || ncm_ready()) return;
+    float *const heads[3] = {qq, kk, vv};
+    const int n3[3] = {C, K * hd, K * hd};
+    GemmExtra ex = {NULL, NULL, NULL, 0, NULL, NULL, NULL, n3, heads, T};
+    run_gemm_x(L_FWD, x, W, qq, b, NULL, 0, (int)rows, (int)N, C, C, C, (int)N, NCM_ACT_NONE, 1, 1, &ex);
 }
 
 int ncm_linear_dx_fusable(int64_t batch, int M, int K, const float *dy, const float *W) {
@@ -550,7 +584,7 @@ void ncm_linear_bwd_act(const float *x, const float *W, const float *dy, float *
         return;
     }
     if (ncm_ready()) return;
-    GemmExtra ex = {NULL, NULL, ax, kind == 0 || kind == 1 ? kind : 2, NULL, NULL, NULL, NULL};
+    GemmExtra ex = {NULL, NULL, ax, kind == 0 || kind == 1 ? kind : 2, NULL, NULL, NULL, NULL, NULL, 0};
     if (run_gemm_x(L_DX, dy, W, dxa, NULL, NULL, 0, (int)batch, K, M, M, K, K, 0, 1, beta, &ex)) return;
     ncm_linear_bwd_ex(x, W, dy, NULL, dW, db, batch, M, K, 1);
 }

@@ -431,6 +431,21 @@ void ncm_t_qkvsplit(NcmTape *t, const float *in, float *qq, float *kk, float *vv
     r->n = B; r->p1 = T; r->p2 = C; r->p3 = H; r->p4 = hd; r->p5 = K; r->p6 = rep;
 }
 
+/* ncm_t_linear (x -> qkv) then ncm_t_qkvsplit (qkv -> qq, kk, vv) with the
+ * split done by the GEMM's epilogue: the same two records, qkv serving as
+ * the key of its gradient (its values are never read by the backward). */
+void ncm_t_linear_qkvsplit(NcmTape *t, const float *x, const float *W, const float *b, float *qkv, float *qq,
+                           float *kk, float *vv, int B, int T, int C, int H, int hd, int K, int rep) {
+    ncm_linear_fwd_qkv_heads(x, W, b, qkv, qq, kk, vv, B, T, C, H, hd, K, rep);
+    NtRec *r = emit(t, NT_LINEAR);
+    if (!r) return;
+    r->a = x; r->b = W; r->c = b; r->y = qkv;
+    r->n = (int64_t)B * T; r->p1 = C + 2 * K * hd; r->p2 = C;
+    REC_OR_RETURN(rs, t, NT_SPLIT);
+    rs->a = qkv; rs->b = qq; rs->c = kk; rs->y = vv;
+    rs->n = B; rs->p1 = T; rs->p2 = C; rs->p3 = H; rs->p4 = hd; rs->p5 = K; rs->p6 = rep;
+}
+
 void ncm_t_headmerge(NcmTape *t, const float *ctx, float *out, int B, int T, int C, int H, int hd) {
     head_merge_fwd(ctx, out, B, T, C, H, hd);
     REC_OR_RETURN(r, t, NT_MERGE);

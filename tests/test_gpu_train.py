@@ -436,3 +436,53 @@ def test_tape_activation_backward_in_dx_gemm(kind, R, K0, K1, M):
     for n in apart:
         assert bits_equal(fused[n], apart[n]), n
     assert np.any(apart["pre"]) and np.any(apart["x"])
+
+
+@pytest.mark.parametrize("B,T,C,H,hd,K", [(2, 100, 128, 2, 64, 2), (2, 70, 256, 4, 64, 2), (3, 33, 192, 3, 64, 3),
+                                          (2, 40, 128, 4, 32, 4), (1, 6, 128, 2, 64, 2)])
+def test_tape_qkv_projection_to_heads(B, T, C, H, hd, K):
+    """ncm_t_linear_qkvsplit (the c_attn GEMM storing q, k, v in the
+    attention's head-major layout from its epilogue) against ncm_t_linear +
+    ncm_t_qkvsplit: q, k, v and the gradients of x, W and b bit for bit, from
+    seeded q, k, v gradients.  Shapes: whole tiles, rows of a tile in two
+    sequences (T = 33, 70), and the fallbacks (GQA, whose split repeats each kv
+    head for its query heads; hd 32; 6 rows).  q, k and v are [B][H][T][hd]."""
+    lib = ncmhip.load()
+    R, N = B * T, C + 2 * K * hd
+    x, W, b = rnd(90, R, C), rnd(91, N, C, scale=0.1), rnd(92, N)
+    gq, gk, gv = rnd(93, B, H, T, hd), rnd(94, B, H, T, hd), rnd(95, B, H, T, hd)
+
+    def run(fused):
+        ins = {"x": x, "W": W, "b": b}
+        bufs = {n: up(a) for n, a in ins.items()}
+        qkv, qq, kk, vv = D.empty((R, N)), D.empty((B, H, T, hd)), D.empty((B, H, T, hd)), D.empty((B, H, T, hd))
+        grads = {n: D.from_numpy(np.zeros_like(a)) for n, a in ins.items()}
+        gbuf = [up(gq), up(gk), up(gv)]
+        tape = lib.ncm_tape_new()
+        try:
+            if fused:
+                lib.ncm_t_linear_qkvsplit(tape, bufs["x"].ptr, bufs["W"].ptr, bufs["b"].ptr, qkv.ptr, qq.ptr, kk.ptr,
+                                          vv.ptr, B, T, C, H, hd, K, H // K)
+            else:
+                lib.ncm_t_linear(tape, bufs["x"].ptr, bufs["W"].ptr, bufs["b"].ptr, qkv.ptr, R, N, C)
+                lib.ncm_t_qkvsplit(tape, qkv.ptr, qq.ptr, kk.ptr, vv.ptr, B, T, C, H, hd, K, H // K)
+            ncmhip.check()
+            keys = [bufs[n].ptr for n in ins] + [qq.ptr, kk.ptr, vv.ptr]
+            gps = [grads[n].ptr for n in ins] + [g.ptr for g in gbuf]
+            sz = [a.size for a in ins.values()] + [gq.size, gk.size, gv.size]
+            n = len(keys)
+            pm = _PMap(ctypes.cast((ctypes.c_void_p * n)(*keys), ctypes.c_void_p),
+                       ctypes.cast((ctypes.c_void_p * n)(*gps), ctypes.c_void_p),
+                       ctypes.cast((ctypes.c_int64 * n)(*sz), ctypes.c_void_p), n)
+            lib.ncm_tape_backward(tape, ctypes.byref(pm))
+            ncmhip.check()
+            return [qq.numpy(), kk.numpy(), vv.numpy()], {n: grads[n].numpy() for n in ins}
+        finally:
+            lib.ncm_tape_free(tape)
+
+    (o1, g1), (o2, g2) = run(False), run(True)
+    for a, c in zip(o1, o2):
+        assert bits_equal(a, c)
+    for n in g1:
+        assert bits_equal(g1[n], g2[n]), n
+    assert np.any(o1[0]) and np.any(g1["x"])

@@ -65,6 +65,19 @@ int ncm_ncp_rope_tables(int S, int hd, int base, float *cos_host, float *sin_hos
 
 static int rope_upload(const int *pos, int n, int hd, int base, float **cd, float **sd);
 
+/* q [B][H][S][hd], k and v [B][nkv][S][hd] from qkv rows (ncp.c:206-244: split,
+ * optional qk-norm, optional RoPE); one wave per row when hd = 64 and a row
+ * holds at most 16 heads, else one wave per head. */
+static int ncp_qkv_launch(const float *qkv, float *q, float *k, float *v, const float *qn, const float *kn,
+                          const float *cs, const float *sn, int B, int S, int H, int nkv, int hd) {
+    if (hd == 64 && H + 2 * nkv <= 16 && (int64_t)B * S <= INT32_MAX - 3) {
+        void *a[] = {&qkv, &q, &k, &v, &qn, &kn, &cs, &sn, &B, &S, &H, &nkv};
+        return ncm_launch_named("ncp_qkv_rows_k", (unsigned)(((int64_t)B * S + 3) / 4), 1, 1, 256, a);
+    }
+    void *a[] = {&qkv, &q, &k, &v, &qn, &kn, &cs, &sn, &B, &S, &H, &nkv, &hd};
+    return ncm_launch_named("ncp_qkv_k", (unsigned)(((int64_t)B * (H + 2 * nkv) * S + 3) / 4), 1, 1, 256, a);
+}
+
 static float *A(int64_t n) {
     float *p = arena_alloc((size_t)n);
     if (!p) ncm_fail(NCM_E_OOM, "ncp: arena");
@@ -127,10 +140,7 @@ float *ncm_ncp_forward(const NcmNcpConfig *c, float *const *P, const int *ids, i
         norm(c, x, w[0], w[1], ln, R);
         linear_fwd(ln, w[2], w[3], qkv, R, QKV, C);
         if (fused) {   /* split + RoPE, kv heads kept */
-            const float *nul = NULL;
-            int Bi = B, Si = S, Hi = H, Ki = Kv, hdi = hd;
-            void *a[] = {&qkv, &qq, &kk, &vv, &nul, &nul, &cosd, &sind, &Bi, &Si, &Hi, &Ki, &hdi};
-            if (ncm_launch_named("ncp_qkv_k", (unsigned)((R * (H + 2 * Kv) + 3) / 4), 1, 1, 256, a)) return NULL;
+            if (ncp_qkv_launch(qkv, qq, kk, vv, NULL, NULL, cosd, sind, B, S, H, Kv, hd)) return NULL;
         } else {
             qkv_split_rope_fwd(qkv, qq, kk, vv, cosd, sind, B, S, C, H, hd, Kv, rep);   /* split, then RoPE */
         }
@@ -522,10 +532,7 @@ static int ncp_block_dev(NCPState *m, const NcpLayer *L, float *x, int nb, const
     linear_fwd(ln, L->attw, L->attb, qkv, R, (int)QKV, C);
     const float *cs = c->use_rope ? m->rope_cos : NULL, *sn = c->use_rope ? m->rope_sin : NULL;
     if (fused) {
-        int Bi = nb, Si = S, Hi = H, Ki = nkv, hdi = hd;
-        const float *qn = L->qn, *kn = L->kn;
-        void *a[] = {&qkv, &q, &k, &v, &qn, &kn, &cs, &sn, &Bi, &Si, &Hi, &Ki, &hdi};
-        int rc = ncm_launch_named("ncp_qkv_k", (unsigned)(((int64_t)nb * (H + 2 * nkv) * S + 3) / 4), 1, 1, 256, a);
+        int rc = ncp_qkv_launch(qkv, q, k, v, L->qn, L->kn, cs, sn, nb, S, H, nkv, hd);
         if (rc) return rc;
     } else {
         /* the reference's own sequence: split with the kv heads replicated,

@@ -57,6 +57,54 @@ ncp_qkv_k(const float *__restrict__ qkv, float *__restrict__ q, float *__restric
     if (act) dst[lane] = x;
 }
 
+// The same for hd = 64 and H + 2 nkv <= 16 heads per row: one wave per qkv
+// row (lane = d), the row's head loads all issued first (the slot index
+// clamped; absent norm weights and tables read a stand-in address and are not
+// used), row and head indices in 32-bit.  The per-head kernel's 64-bit
+// division and one guarded round trip per head were most of its time.
+extern "C" __global__ void __launch_bounds__(256)
+ncp_qkv_rows_k(const float *__restrict__ qkv, float *__restrict__ q, float *__restrict__ k, float *__restrict__ v,
+               const float *__restrict__ qn, const float *__restrict__ kn, const float *__restrict__ cos_t,
+               const float *__restrict__ sin_t, int B, int S, int H, int nkv) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);   // row = b S + s
+    if (row >= B * S) return;
+    const int b = row / S, s = row - b * S, slots = H + 2 * nkv;
+    const float *src = qkv + (int64_t)row * slots * 64 + lane;
+    float xv[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) xv[j] = src[min(j, slots - 1) * 64];
+    const float wq = *(qn ? qn + lane : src), wk = *(kn ? kn + lane : src);
+    const float c = *(cos_t ? cos_t + (int64_t)s * 64 + lane : src);
+    const float sn = *(cos_t ? sin_t + (int64_t)s * 64 + lane : src);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        if (j >= slots) continue;
+        float x = xv[j];
+        float *dst;
+        if (j < H) {
+            dst = q + (((int64_t)b * H + j) * S + s) * 64;
+        } else if (j < H + nkv) {
+            dst = k + (((int64_t)b * nkv + (j - H)) * S + s) * 64;
+        } else {
+            dst = v + (((int64_t)b * nkv + (j - H - nkv)) * S + s) * 64;
+        }
+        if (j < H + nkv) {
+            const bool isq = j < H;
+            if (isq ? qn != nullptr : kn != nullptr) {
+                double ms = wave_sum_d((double)x * (double)x) / 64;
+                const float sc = (float)(1.0 / sqrt(ms + 1e-6));
+                x = x * sc * (isq ? wq : wk);
+            }
+            if (cos_t) {
+                const float other = __shfl(x, lane < 32 ? lane + 32 : lane - 32, 64);
+                x = lane < 32 ? x * c + (-other) * sn : x * c + other * sn;
+            }
+        }
+        dst[lane] = x;
+    }
+}
+
 // The additive mask of build_full_mask (ncp.c:361-386) for one board:
 // prefix rows see only the prefix, target rows see the prefix and the
 // target levels the pattern allows (block_diag: its own level; else levels

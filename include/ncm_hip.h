@@ -364,7 +364,8 @@ void ncm_t_linear_res(NcmTape *t, const float *x, const float *W, const float *b
                       int64_t batch, int M, int K);
 /* extension: ncm_t_linear (x -> qkv, [B*T][C + 2 K hd]) then ncm_t_qkvsplit
  * (qkv -> qq, kk, vv) with the split done by the GEMM's epilogue when hd = 64,
- * C = H hd and K = H (qkv is then not written; it still keys its gradient),
+ * C = H hd, K = H and T % 64 == 0 (qkv is then not written; it still keys its
+ * gradient),
  * bit for bit the two calls (train_gpt2.c:58-62) */
 void ncm_t_linear_qkvsplit(NcmTape *t, const float *x, const float *W, const float *b, float *qkv, float *qq,
                            float *kk, float *vv, int B, int T, int C, int H, int hd, int K, int rep);

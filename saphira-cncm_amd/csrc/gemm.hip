@@ -47,11 +47,13 @@
 // (x B2^T + bias2), both products in one tile (gemm_64x64_gated_v);
 // ACT_BWD  C += act'(bwd_x) (0.0f + acc): the dX product written as a fresh
 // gradient and passed back through the activation that produced the layer's
-// input, without storing it (gemm_64x64_dxa_v); HEADS  STORE into the
-// attention's head-major layout (gemm_64x64_fwdh_v).
+// input, without storing it (gemm_64x64_dxa_v).
 #include "mfma_slab.h"
 
-enum { EPI_STORE = 0, EPI_ACCUM = 1, EPI_GATED = 2, EPI_ACT_BWD = 3, EPI_HEADS = 4 };
+enum { EPI_STORE = 0, EPI_ACCUM = 1, EPI_GATED = 2, EPI_ACT_BWD = 3 };
+// Per-tile output selection of the forward kernels: SEL_F3 (gemm_64x64_fwd3_v,
+// f3_select) and SEL_HEADS (gemm_64x64_fwdh_v, heads_select).
+enum { SEL_NONE = 0, SEL_F3 = 1, SEL_HEADS = 2 };
 
 struct GemmArgs {
     const float *A;
@@ -87,22 +89,27 @@ struct GemmArgs {
     float *C3[3];
     int n3[3];
     unsigned b3_bytes[3];
-    // HEADS (gemm_64x64_fwdh_v): the output row i = b T + t of a [q | k | v]
-    // product (part widths n3[], heads of 64) goes to C3[part] as
-    // [B][n3[part] / 64][T][64]; hm_T = T
+    // SEL_HEADS (gemm_64x64_fwdh_v): output row i = b T + t of a [q | k | v]
+    // product (part widths n3[], heads of 64 columns) goes to C3[part] as
+    // [B][n3[part] / 64][T][64]; hm_T = T, a multiple of 64
     int hm_T;
 };
 
-// HEADS: the address of output element (i, j).  Every tile column lies in one
-// head of one part (the widths are multiples of 64), so the part is uniform.
-__device__ __forceinline__ float *heads_addr(const GemmArgs &p, int i, int j) {
-    const int n0 = p.n3[0], n01 = n0 + p.n3[1];
-    const int g = __builtin_amdgcn_readfirstlane(j < n0 ? 0 : j < n01 ? 1 : 2);
-    const int jl = j - (g == 0 ? 0 : g == 1 ? n0 : n01);
-    const int hw = (g == 0 ? n0 : g == 1 ? p.n3[1] : p.n3[2]) >> 6;
-    float *const base = g == 0 ? p.C3[0] : g == 1 ? p.C3[1] : p.C3[2];
-    const int b = i / p.hm_T, t = i - b * p.hm_T;
-    return base + (((int64_t)b * hw + (jl >> 6)) * p.hm_T + t) * 64 + (jl & 63);
+// SEL_HEADS: the tile at (i0, j0) lies in one head of one part and, T being a
+// multiple of 64, in one sequence b; in the head-major layout its 64 rows are
+// one contiguous [64][64] block.  So the tile is stored as a plain row-major
+// tile through q.C, offset so that C + i * 64 + j (ldc 64) lands in that
+// block for every (i, j) of the tile.
+__device__ __forceinline__ void heads_select(const GemmArgs &src, GemmArgs &q, int i0, int j0) {
+    const int n0 = src.n3[0], n01 = n0 + src.n3[1];
+    const int g = j0 < n0 ? 0 : j0 < n01 ? 1 : 2;
+    const int jl = j0 - (g == 0 ? 0 : g == 1 ? n0 : n01);
+    const int hw = (g == 0 ? n0 : g == 1 ? src.n3[1] : src.n3[2]) >> 6;
+    float *const base = g == 0 ? src.C3[0] : g == 1 ? src.C3[1] : src.C3[2];
+    const int b = i0 / src.hm_T, t0 = i0 - b * src.hm_T;
+    float *const blk = base + (((int64_t)b * hw + (jl >> 6)) * src.hm_T + t0) * 64;
+    q.C = blk - (int64_t)i0 * 64 - j0;
+    q.ldc = 64;
 }
 
 // F3: the product that output column jt (a tile's first) belongs to, written
@@ -578,7 +585,7 @@ __device__ __forceinline__ void g_out_n(const GemmArgs &p, const int (&ii)[N], c
             o1[n] = p.beta ? p.C[e] : 0.0f;
             if (EPI == EPI_ACT_BWD) o2[n] = p.bwd_x[e];
         } else {
-            const float *bq = hb ? p.bias + j : p.C;
+            const float *bq = hb ? p.bias + j : p.A;   // an absent bias reads a valid stand-in
             o1[n] = *bq;
             o2[n] = *(hr ? p.res + e : bq);
         }
@@ -586,7 +593,7 @@ __device__ __forceinline__ void g_out_n(const GemmArgs &p, const int (&ii)[N], c
 #pragma unroll
     for (int n = 0; n < N; ++n) {
         if (ii[n] >= p.Mo || jj[n] >= p.No) continue;
-        float *c = EPI == EPI_HEADS ? heads_addr(p, ii[n], jj[n]) : p.C + (int64_t)ii[n] * p.ldc + jj[n];
+        float *c = p.C + (int64_t)ii[n] * p.ldc + jj[n];
         float x = v[n];
         if (EPI == EPI_ACCUM) {
             *c = o1[n] + x;
@@ -804,14 +811,15 @@ __device__ __forceinline__ void g_epilogue_blk_act(const GemmArgs &p, const f4 &
 // of a thread's segment loads are issued before the first add: the launch
 // is one round trip of latency, not one per segment.
 #define FIXUP_MAX_SEGS 16
-template <int EPI, bool IA, bool IB, bool DB, bool F3 = false>
+template <int EPI, bool IA, bool IB, bool DB, int SEL = SEL_NONE>
 __device__ __forceinline__ void gemm_tile_fixup_body(const GemmArgs &pa) {
     const int tid = threadIdx.x, tail = blockIdx.x >> 2, blk = blockIdx.x & 3;
     int tm, tn;
     tile_rc<8>(pa.dp_tiles + tail, pa.tiles_m, pa.tiles_n, tm, tn);
     GemmArgs pl = pa;
-    const int jb = F3 ? f3_select(pa, pl, tn * 64) : 0;
-    const GemmArgs &p = F3 ? pl : pa;
+    const int jb = SEL == SEL_F3 ? f3_select(pa, pl, tn * 64) : 0;
+    if (SEL == SEL_HEADS) heads_select(pa, pl, tm * 64, tn * 64);
+    const GemmArgs &p = SEL != SEL_NONE ? pl : pa;
     const float *first = p.ws + (int64_t)tail * p.segs * 4096 + (blk * GEMM_NT + tid) * 4;
     // unconditional loads (a segment index clamped to the last one, the extra
     // values not added): a guarded load is a branch with a wait after it
@@ -892,9 +900,9 @@ struct BoolTag {
     static constexpr bool value = V;
 };
 
-// DB: the dW kernel that also sums the bias gradient (p.db); F3: the
-// forward of up to three products side by side (f3_select)
-template <bool AKC, bool BKC, int EPI, bool DB = false, bool F3 = false>
+// DB: the dW kernel that also sums the bias gradient (p.db); SEL: per-tile
+// output selection (f3_select, heads_select)
+template <bool AKC, bool BKC, int EPI, bool DB = false, int SEL = SEL_NONE>
 __device__ __forceinline__ void gemm_dma_body(const GemmArgs &pa) {
     __shared__ __attribute__((aligned(16))) float sm[2 * 2 * D_SLAB];   // [stage][A | B]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -921,8 +929,9 @@ __device__ __forceinline__ void gemm_dma_body(const GemmArgs &pa) {
     int tm, tn;
     tile_rc<8>(tile, pa.tiles_m, pa.tiles_n, tm, tn);
     GemmArgs pl = pa;
-    const int jb = F3 ? f3_select(pa, pl, tn * 64) : 0;
-    const GemmArgs &p = F3 ? pl : pa;
+    const int jb = SEL == SEL_F3 ? f3_select(pa, pl, tn * 64) : 0;
+    if (SEL == SEL_HEADS) heads_select(pa, pl, tm * 64, tn * 64);
+    const GemmArgs &p = SEL != SEL_NONE ? pl : pa;
     // GATED: tile columns 0-31 are output columns j0 .. j0 + 31 of the gate
     // product, 32-63 the same columns of the up product; waves 0-1 load the
     // gate's B rows, waves 2-3 the up projection's
@@ -1080,31 +1089,31 @@ __device__ __forceinline__ void gemm_dma_body(const GemmArgs &pa) {
         __attribute__((amdgpu_waves_per_eu(BM * BN <= 4096 ? 4 : 1))) name(GemmArgs p) {          \
         gemm_tile_body<BM, BN, AKC, BKC, EPI, VEC>(p);                                               \
     }
-#define GEMM_DMA_KERNEL(name, AKC, BKC, EPI, DB, F3)                                                   \
+#define GEMM_DMA_KERNEL(name, AKC, BKC, EPI, DB, SEL)                                                   \
     extern "C" __global__ void __launch_bounds__(GEMM_NT) __attribute__((amdgpu_waves_per_eu(4)))      \
         name(GemmArgs p) {                                                                             \
-        gemm_dma_body<AKC, BKC, EPI, DB, F3>(p);                                                       \
+        gemm_dma_body<AKC, BKC, EPI, DB, SEL>(p);                                                      \
     }
-#define GEMM_TILE_FIXUP(name, EPI, IA, IB, DB, F3) \
-    extern "C" __global__ void __launch_bounds__(GEMM_NT) name(GemmArgs p) { gemm_tile_fixup_body<EPI, IA, IB, DB, F3>(p); }
-GEMM_DMA_KERNEL(gemm_64x64_fwd_v, true, true, EPI_STORE, false, false)
-GEMM_DMA_KERNEL(gemm_64x64_fwd3_v, true, true, EPI_STORE, false, true)   // products side by side
-GEMM_DMA_KERNEL(gemm_64x64_fwdh_v, true, true, EPI_HEADS, false, false)  // q | k | v to head-major
-GEMM_DMA_KERNEL(gemm_64x64_dx_v, true, false, EPI_ACCUM, false, false)
-GEMM_DMA_KERNEL(gemm_64x64_dw_v, false, false, EPI_ACCUM, false, false)
-GEMM_DMA_KERNEL(gemm_64x64_dwb_v, false, false, EPI_ACCUM, true, false)   // dW + db
-GEMM_DMA_KERNEL(gemm_64x64_dxa_v, true, false, EPI_ACT_BWD, false, false) // dX through the activation backward
-GEMM_DMA_KERNEL(gemm_64x64_gated_v, true, true, EPI_GATED, false, false)
+#define GEMM_TILE_FIXUP(name, EPI, IA, IB, DB, SEL) \
+    extern "C" __global__ void __launch_bounds__(GEMM_NT) name(GemmArgs p) { gemm_tile_fixup_body<EPI, IA, IB, DB, SEL>(p); }
+GEMM_DMA_KERNEL(gemm_64x64_fwd_v, true, true, EPI_STORE, false, SEL_NONE)
+GEMM_DMA_KERNEL(gemm_64x64_fwd3_v, true, true, EPI_STORE, false, SEL_F3)   // products side by side
+GEMM_DMA_KERNEL(gemm_64x64_fwdh_v, true, true, EPI_STORE, false, SEL_HEADS)  // q | k | v to head-major
+GEMM_DMA_KERNEL(gemm_64x64_dx_v, true, false, EPI_ACCUM, false, SEL_NONE)
+GEMM_DMA_KERNEL(gemm_64x64_dw_v, false, false, EPI_ACCUM, false, SEL_NONE)
+GEMM_DMA_KERNEL(gemm_64x64_dwb_v, false, false, EPI_ACCUM, true, SEL_NONE)   // dW + db
+GEMM_DMA_KERNEL(gemm_64x64_dxa_v, true, false, EPI_ACT_BWD, false, SEL_NONE) // dX through the activation backward
+GEMM_DMA_KERNEL(gemm_64x64_gated_v, true, true, EPI_GATED, false, SEL_NONE)
 GEMM_TILE_KERNEL(gemm_64x64_fwd_s, 64, 64, true, true, EPI_STORE, false)
 GEMM_TILE_KERNEL(gemm_64x64_dx_s, 64, 64, true, false, EPI_ACCUM, false)
 GEMM_TILE_KERNEL(gemm_64x64_dw_s, 64, 64, false, false, EPI_ACCUM, false)
-GEMM_TILE_FIXUP(gemm_64x64_fixup_fwd_v, EPI_STORE, false, false, false, false)
-GEMM_TILE_FIXUP(gemm_64x64_fixup_fwd3_v, EPI_STORE, false, false, false, true)
-GEMM_TILE_FIXUP(gemm_64x64_fixup_fwdh_v, EPI_HEADS, false, false, false, false)
-GEMM_TILE_FIXUP(gemm_64x64_fixup_dx_v, EPI_ACCUM, false, true, false, false)
-GEMM_TILE_FIXUP(gemm_64x64_fixup_dw_v, EPI_ACCUM, true, true, false, false)
-GEMM_TILE_FIXUP(gemm_64x64_fixup_dwb_v, EPI_ACCUM, true, true, true, false)
-GEMM_TILE_FIXUP(gemm_64x64_fixup_dxa_v, EPI_ACT_BWD, false, true, false, false)
-GEMM_TILE_FIXUP(gemm_64x64_fixup_fwd_s, EPI_STORE, false, false, false, false)
-GEMM_TILE_FIXUP(gemm_64x64_fixup_dx_s, EPI_ACCUM, false, false, false, false)
-GEMM_TILE_FIXUP(gemm_64x64_fixup_dw_s, EPI_ACCUM, false, false, false, false)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_fwd_v, EPI_STORE, false, false, false, SEL_NONE)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_fwd3_v, EPI_STORE, false, false, false, SEL_F3)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_fwdh_v, EPI_STORE, false, false, false, SEL_HEADS)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_dx_v, EPI_ACCUM, false, true, false, SEL_NONE)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_dw_v, EPI_ACCUM, true, true, false, SEL_NONE)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_dwb_v, EPI_ACCUM, true, true, true, SEL_NONE)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_dxa_v, EPI_ACT_BWD, false, true, false, SEL_NONE)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_fwd_s, EPI_STORE, false, false, false, SEL_NONE)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_dx_s, EPI_ACCUM, false, false, false, SEL_NONE)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_dw_s, EPI_ACCUM, false, false, false, SEL_NONE)

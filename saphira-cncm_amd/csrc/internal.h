@@ -57,7 +57,7 @@ void ncm_linear_fwd_pre(const float *x, const float *W, const float *b, float *p
 void ncm_linear_fwd3(const float *x, const float *const W[3], const float *const b[3], float *const y[3],
                      const int N[3], int64_t batch, int K);
 /* linear_fwd into qkv then qkv_split_fwd, with the split done by the GEMM's
- * epilogue (qkv not written) when hd = 64, C = H hd and K = H (linear.c). */
+ * epilogue (qkv not written) when hd = 64, C = H hd, K = H and 64 | T (linear.c). */
 void ncm_linear_fwd_qkv_heads(const float *x, const float *W, const float *b, float *qkv, float *qq, float *kk,
                               float *vv, int B, int T, int C, int H, int hd, int K, int rep);
 /* 1 when linear_bwd's dX runs as one vectorised GEMM (batch > 8, M and K

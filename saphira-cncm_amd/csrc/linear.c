@@ -543,8 +543,9 @@ void ncm_linear_fwd3(const float *x, const float *const W[3], const float *const
 
 /* linear_fwd into qkv [B*T][C + 2 K hd] followed by qkv_split_fwd(qkv, qq, kk,
  * vv, B, T, C, H, hd, K, rep): for hd = 64, C = H hd, one kv head per query
- * head (K = H, rep = 1: the split copies each kv head once) and aligned
- * operands the GEMM writes qq, kk and vv [B][H][T][hd] from its epilogue (the
+ * head (K = H, rep = 1: the split copies each kv head once), T a multiple of
+ * 64 (a tile's rows stay in one sequence) and aligned operands, the GEMM
+ * stores each tile straight into its [64 t][64 d] block of qq, kk or vv (the
  * same values) and qkv is not written; otherwise the two calls. */
 void ncm_linear_fwd_qkv_heads(const float *x, const float *W, const float *b, float *qkv, float *qq, float *kk,
                               float *vv, int B, int T, int C, int H, int hd, int K, int rep) {
@@ -553,7 +554,7 @@ void ncm_linear_fwd_qkv_heads(const float *x, const float *W, const float *b, fl
         ncm_fail(NCM_E_ARG, "ncm_linear_fwd_qkv_heads: bad shape");
         return;
     }
-    int whole = hd == 64 && C == H * hd && C % 64 == 0 && K == H && rep == 1 && rows > 8 &&
+    int whole = hd == 64 && C == H * hd && C % 64 == 0 && K == H && rep == 1 && rows > 8 && T % 64 == 0 &&
                 C % 4 == 0 && x && W && qq && kk && vv && is_aligned16(x) && is_aligned16(W);
     if (!whole) {
         linear_fwd(x, W, b, qkv, rows, (int)N, C);

@@ -438,15 +438,16 @@ def test_tape_activation_backward_in_dx_gemm(kind, R, K0, K1, M):
     assert np.any(apart["pre"]) and np.any(apart["x"])
 
 
-@pytest.mark.parametrize("B,T,C,H,hd,K", [(2, 100, 128, 2, 64, 2), (2, 70, 256, 4, 64, 2), (3, 33, 192, 3, 64, 3),
-                                          (2, 40, 128, 4, 32, 4), (1, 6, 128, 2, 64, 2)])
+@pytest.mark.parametrize("B,T,C,H,hd,K", [(2, 128, 128, 2, 64, 2), (3, 64, 192, 3, 64, 3), (2, 192, 256, 4, 64, 2),
+                                          (2, 70, 128, 2, 64, 2), (2, 40, 128, 4, 32, 4), (1, 6, 128, 2, 64, 2)])
 def test_tape_qkv_projection_to_heads(B, T, C, H, hd, K):
     """ncm_t_linear_qkvsplit (the c_attn GEMM storing q, k, v in the
     attention's head-major layout from its epilogue) against ncm_t_linear +
     ncm_t_qkvsplit: q, k, v and the gradients of x, W and b bit for bit, from
-    seeded q, k, v gradients.  Shapes: whole tiles, rows of a tile in two
-    sequences (T = 33, 70), and the fallbacks (GQA, whose split repeats each kv
-    head for its query heads; hd 32; 6 rows).  q, k and v are [B][H][T][hd]."""
+    seeded q, k, v gradients.  Shapes: sequences of 128 and 64 tokens (every
+    tile one [64 t][64 d] block of q, k or v), and the fallbacks (GQA, whose
+    split repeats each kv head for its query heads; T = 70, whose tiles would
+    span two sequences; hd 32; 6 rows).  q, k and v are [B][H][T][hd]."""
     lib = ncmhip.load()
     R, N = B * T, C + 2 * K * hd
     x, W, b = rnd(90, R, C), rnd(91, N, C, scale=0.1), rnd(92, N)

@@ -127,7 +127,7 @@ float *ncm_ncp_forward(const NcmNcpConfig *c, float *const *P, const int *ids, i
         tab_base = c->rope_base;
     }
     const float *cosd = tab_cos, *sind = tab_sin;
-    mem_h2d(bids, ids, (size_t)R * sizeof(int));
+    if (ncm_h2d_async(bids, ids, (size_t)R * sizeof(int))) return NULL;
     embedding_fwd_v(P[0], V, bids, x, R, C);
     /* K and V at their kv-head count when the fused split applies (hd <= 64),
      * else replicated to every query head as ncp.c:213-236 does */

@@ -198,7 +198,7 @@ float *ncm_qwen_forward(NcmQwen *m, const int *ids, int T, int last_only) {
     int *bids = (int *)A(T);
     float *h = A((int64_t)T * C);
     if (!h) return NULL;
-    mem_h2d(bids, ids, (size_t)T * sizeof(int));
+    if (ncm_h2d_async(bids, ids, (size_t)T * sizeof(int))) return NULL;
     embedding_fwd_v(P[0], V, bids, h, T, C);
     for (int li = 0; li < c->n_layer; li++) {
         float *const *w = P + 1 + QW_PER_LAYER * li;

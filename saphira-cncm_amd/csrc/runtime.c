@@ -235,6 +235,41 @@ void mem_h2d(void *d, const void *h, size_t n) {
     if (e != hipSuccess) ncm_fail(NCM_E_HIP, "mem_h2d(%zu): %s", n, hipGetErrorString(e));
 }
 
+/* Small host-to-device uploads (token ids, targets) without a host
+ * synchronisation: the bytes are copied into one of a ring of pinned staging
+ * slots and sent by an asynchronous copy on the library stream; a slot is
+ * reused only once the event recorded behind its last copy has completed.
+ * Larger uploads, or a device other than the one the ring was made on, take
+ * mem_h2d. */
+#define H2D_SLOTS 8
+#define H2D_SLOT_BYTES ((size_t)256 << 10)
+static unsigned char *g_h2d_pin = NULL;
+static hipEvent_t g_h2d_ev[H2D_SLOTS];
+static int g_h2d_used[H2D_SLOTS], g_h2d_next = 0, g_h2d_dev = -1;
+
+int ncm_h2d_async(void *d, const void *h, size_t n) {
+    int rc = ncm_ready();
+    if (rc || n == 0) return rc;
+    if (n > H2D_SLOT_BYTES || (g_h2d_pin && g_h2d_dev != ncm_device())) {
+        mem_h2d(d, h, n);
+        return ncm_ready();
+    }
+    if (!g_h2d_pin) {
+        HIP_TRY(hipHostMalloc((void **)&g_h2d_pin, H2D_SLOTS * H2D_SLOT_BYTES, hipHostMallocDefault));
+        for (int i = 0; i < H2D_SLOTS; i++) HIP_TRY(hipEventCreateWithFlags(&g_h2d_ev[i], hipEventDisableTiming));
+        g_h2d_dev = ncm_device();
+    }
+    const int s = g_h2d_next;
+    g_h2d_next = (s + 1) % H2D_SLOTS;
+    if (g_h2d_used[s]) HIP_TRY(hipEventSynchronize(g_h2d_ev[s]));
+    unsigned char *slot = g_h2d_pin + (size_t)s * H2D_SLOT_BYTES;
+    memcpy(slot, h, n);
+    HIP_TRY(hipMemcpyAsync(d, slot, n, hipMemcpyHostToDevice, g_stream));
+    HIP_TRY(hipEventRecord(g_h2d_ev[s], g_stream));
+    g_h2d_used[s] = 1;
+    return 0;
+}
+
 void mem_d2d(void *d, const void *s, size_t n) {
     if (ncm_ready() || n == 0) return;
     hipError_t e = hipMemcpyAsync(d, s, n, hipMemcpyDeviceToDevice, g_stream);

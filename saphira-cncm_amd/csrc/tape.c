@@ -270,7 +270,10 @@ void ncm_t_embed(NcmTape *t, const float *W, const int *idx, int V, float *y, in
         return;
     }
     memcpy(hcopy, idx, (size_t)n * sizeof(int));
-    mem_h2d(dcopy, idx, (size_t)n * sizeof(int));
+    if (ncm_h2d_async(dcopy, idx, (size_t)n * sizeof(int))) {
+        free(hcopy);
+        return;
+    }
     embedding_fwd_v(W, V, dcopy, y, n, D);
     NtRec *r = emit(t, NT_EMBED);
     if (!r) { free(hcopy); return; }
@@ -468,8 +471,8 @@ void ncm_t_ce(NcmTape *t, const float *logits, const int *tgt, const float *wmas
     float *dw = wmask ? (float *)pool_alloc(&t->rec, (size_t)rows * sizeof(float)) : NULL;
     float *dl = (float *)pool_alloc(&t->rec, (size_t)rows * V * sizeof(float));
     if (!dt || (wmask && !dw) || !dl) { ncm_fail(NCM_E_OOM, "ncm_t_ce: buffers"); return; }
-    mem_h2d(dt, tgt, (size_t)rows * sizeof(int));
-    if (wmask) mem_h2d(dw, wmask, (size_t)rows * sizeof(float));
+    if (ncm_h2d_async(dt, tgt, (size_t)rows * sizeof(int))) return;
+    if (wmask && ncm_h2d_async(dw, wmask, (size_t)rows * sizeof(float))) return;
     if (ncm_zero_async(dl, (size_t)rows * V * sizeof(float))) return;
     if (probs) ce_fwd(logits, dt, dw, loss, probs, rows, V);
     ce_fwd_bwd(logits, dt, dw, loss, dl, rows, V, weight);

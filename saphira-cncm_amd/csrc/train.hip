@@ -126,20 +126,23 @@ norm_param_final(const double *__restrict__ part, float *__restrict__ dw, float 
 // the chunks in order.  x and dy are read once instead of twice and the row
 // loop keeps its loads in flight instead of one scalar load per pass.
 #define NBF_ROWS 32
+// A row's float4 groups: every load unconditional (a column past C reads the
+// row's last group and counts zero), so that a wave's loads of the next row
+// stay in flight: a guarded load is a branch with a full wait at the join.
 template <int KIND, int NPL>
 __device__ __forceinline__ void nbf_load(const float *__restrict__ p, int64_t row, int C, int lane, f4 (&v)[NPL]) {
 #pragma unroll
     for (int j = 0; j < NPL; ++j) {
         const int c = 4 * (lane + 64 * j);
-        v[j] = c < C ? *(const f4 *)(p + row * C + c) : f4{0.f, 0.f, 0.f, 0.f};
+        const f4 t = *(const f4 *)(p + row * C + min(c, C - 4));
+        v[j] = c < C ? t : f4{0.f, 0.f, 0.f, 0.f};
     }
 }
 
-template <int KIND, int NPL>
+template <int KIND, int NPL, bool BETA>
 __device__ __forceinline__ void norm_bwd_fused_body(const float *__restrict__ x, const float *__restrict__ w,
                                                     const float *__restrict__ dy, float *__restrict__ dx,
-                                                    double *__restrict__ part, int64_t rows, int C, double eps,
-                                                    int beta) {
+                                                    double *__restrict__ part, int64_t rows, int C, double eps) {
 #pragma clang fp contract(off)
     constexpr int NP = KIND == 0 ? 2 : 1;   // parameter gradients: (dw, db) or dw
     __shared__ double red[3][64 * NPL][4][NP];
@@ -159,16 +162,15 @@ __device__ __forceinline__ void norm_bwd_fused_body(const float *__restrict__ x,
 #pragma unroll
             for (int k = 0; k < NP; ++k) sp[j][e][k] = 0.0;
     f4 xa[NPL], ga[NPL];
-    if (rbeg < rend) {
-        nbf_load<KIND, NPL>(x, rbeg, C, lane, xa);
-        nbf_load<KIND, NPL>(dy, rbeg, C, lane, ga);
-    }
+    const int64_t r0 = min(rbeg, rows - 1);   // a wave past the last row loads a valid row and skips the loop
+    nbf_load<KIND, NPL>(x, r0, C, lane, xa);
+    nbf_load<KIND, NPL>(dy, r0, C, lane, ga);
     for (int64_t r = rbeg; r < rend; ++r) {
+        // the next row's loads (the last row again at the end), unconditionally
         f4 xn[NPL], gn[NPL];
-        if (r + 1 < rend) {
-            nbf_load<KIND, NPL>(x, r + 1, C, lane, xn);
-            nbf_load<KIND, NPL>(dy, r + 1, C, lane, gn);
-        }
+        const int64_t rn = r + 1 < rend ? r + 1 : r;
+        nbf_load<KIND, NPL>(x, rn, C, lane, xn);
+        nbf_load<KIND, NPL>(dy, rn, C, lane, gn);
         if (KIND == 0) {
             double mean = 0.0;
 #pragma unroll
@@ -205,7 +207,8 @@ __device__ __forceinline__ void norm_bwd_fused_body(const float *__restrict__ x,
                     const int c = 4 * (lane + 64 * j);
                     if (c < C) {
                         f4 *o = (f4 *)(dx + r * C + c);
-                        f4 v = beta ? *o : f4{0.f, 0.f, 0.f, 0.f};
+                        f4 v = f4{0.f, 0.f, 0.f, 0.f};
+                        if constexpr (BETA) v = *o;
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const double d = (double)ga[j][e] * (double)wv[j][e];
@@ -242,7 +245,8 @@ __device__ __forceinline__ void norm_bwd_fused_body(const float *__restrict__ x,
                     const int c = 4 * (lane + 64 * j);
                     if (c < C) {
                         f4 *o = (f4 *)(dx + r * C + c);
-                        f4 v = beta ? *o : f4{0.f, 0.f, 0.f, 0.f};
+                        f4 v = f4{0.f, 0.f, 0.f, 0.f};
+                        if constexpr (BETA) v = *o;
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
                             v[e] += (float)(((double)ga[j][e] * (double)wv[j][e] -
@@ -300,7 +304,10 @@ __device__ __forceinline__ void norm_bwd_fused_body(const float *__restrict__ x,
     extern "C" __global__ void __launch_bounds__(256)                                                       \
         name(const float *__restrict__ x, const float *__restrict__ w, const float *__restrict__ dy,        \
              float *__restrict__ dx, double *__restrict__ part, int64_t rows, int C, double eps, int beta) { \
-        norm_bwd_fused_body<KIND, NPL>(x, w, dy, dx, part, rows, C, eps, beta);                             \
+        if (beta)                                                                                           \
+            norm_bwd_fused_body<KIND, NPL, true>(x, w, dy, dx, part, rows, C, eps);                         \
+        else                                                                                                \
+            norm_bwd_fused_body<KIND, NPL, false>(x, w, dy, dx, part, rows, C, eps);                        \
     }
 NORM_BWD_FUSED(ln_bwd_fused_1, 0, 1)
 NORM_BWD_FUSED(ln_bwd_fused_2, 0, 2)

@@ -88,6 +88,13 @@ void ncm_add_inplace_ex(float *y, const float *x, int64_t n, int beta);
 void ncm_sdpa_bwd_flash_ex(const float *q, const float *k, const float *v, const float *o, const float *stats,
                            const float *mask, int causal, const float *dO, float *dq, float *dk, float *dv, int B,
                            int H, int Hkv, int Tq, int Tkv, int hd, int beta);
+/* ncm_sdpa_bwd_flash_ex with the three gradients written into the q | k | v
+ * rows' gradient dqkv [B*T][(H + 2 Hkv) hd] (q at column 0, k at H hd, v at
+ * (H + Hkv) hd): the gradient qkv_split_bwd would form from them, when q, k
+ * and v came from such rows by a split with one kv head per kv head. */
+void ncm_sdpa_bwd_flash_rows(const float *q, const float *k, const float *v, const float *o, const float *stats,
+                             const float *mask, int causal, const float *dO, float *dqkv, int B, int H, int Hkv,
+                             int Tq, int Tkv, int hd, int beta);
 void ncm_qkv_split_bwd_ex(const float *gq, const float *gk, const float *gv, float *dx, int B, int T, int C, int H,
                           int hd, int K, int rep, int beta);
 void ncm_heads_bwd_ex(const float *dy, float *dx, int B, int T, int C, int H, int hd, int dir, int beta);

@@ -586,6 +586,24 @@ void ncm_tape_backward(NcmTape *t, const NcmPMap *pm) {
         case NT_SDPA: {
             int B = (int)r->n, H = r->p1, Hkv = r->p2, Tq = r->p3, Tkv = r->p4, hd = r->p5;
             const int64_t nq = (int64_t)B * H * Tq * hd, nk = (int64_t)B * Hkv * Tkv * hd;
+            const NtRec *rs = i > 0 ? &t->r[i - 1] : NULL;
+            if ((r->p6 & 1) && rs && rs->op == NT_SPLIT && rs->b == r->a && rs->c == r->b && rs->y == r->c &&
+                rs->n == B && rs->p1 == Tq && Tq == Tkv && rs->p3 == H && rs->p4 == hd && rs->p5 == Hkv &&
+                Hkv == H && rs->p6 == 1 && rs->p2 == H * hd && !gmap_find(t, r->a) && !gmap_find(t, r->b) &&
+                !gmap_find(t, r->c)) {
+                /* the record right before is the split that produced q, k and v
+                 * from rows [B*T][3 C], one kv head per query head, and only
+                 * the attention reads them: its gradients go straight into the
+                 * rows' gradient (what the split's backward would form), and
+                 * the split record is done too */
+                int bx;
+                float *gx = gmap_get_fresh(t, rs->a, (int64_t)B * Tq * 3 * H * hd, &bx);
+                if (!gx) return;
+                ncm_sdpa_bwd_flash_rows(r->a, r->b, r->c, r->y, r->aux, r->mask, (r->p6 >> 1) & 1, dy, gx, B, H, Hkv,
+                                        Tq, Tkv, hd, bx);
+                i--;
+                break;
+            }
             int fq, fk, fv;
             float *gq = gmap_get_fresh(t, r->a, nq, &fq);
             float *gk = gmap_get_fresh(t, r->b, nk, &fk), *gv = gmap_get_fresh(t, r->c, nk, &fv);

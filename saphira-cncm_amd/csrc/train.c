@@ -207,9 +207,11 @@ void sdpa_bwd_gqa(const float *q, const float *k, const float *v, const float *P
 /* The recomputing backward of the tape's SDPA records (hd 64, aligned): D =
  * rowsum(dO o O), then the dq and dk/dv kernels rebuild P tile by tile from
  * the forward's row statistics.  Gradients accumulate. */
+/* ldo 0: dq, dk, dv as [B][heads][T][hd]; ldo > 0: rows (b, t) of stride ldo
+ * floats with head h at column h hd (the layout of the q | k | v rows). */
 static void sdpa_bwd_flash_any(const float *q, const float *k, const float *v, const float *o, const float *stats,
                                const float *mask, int causal, const float *dO, float *dq, float *dk, float *dv, int B,
-                               int H, int Hkv, int Tq, int Tkv, int hd, int beta) {
+                               int H, int Hkv, int Tq, int Tkv, int hd, int beta, int ldo) {
     if (attn_check("ncm_sdpa_bwd_flash", B, H, Hkv, Tq, Tkv, hd)) return;
     if ((int64_t)B * Tq == 0 || (!dq && !dk && !dv)) return;
     if (hd != 64 || !q || !k || !v || !o || !stats || !dO) {
@@ -232,11 +234,12 @@ static void sdpa_bwd_flash_any(const float *q, const float *k, const float *v, c
     void *a0[] = {&dO, &o, &D, (void *)&rows, &hd};
     if (ncm_launch_named("sdpa_bwd_rowdot", blocks_of(rows, 4), 1, 1, 256, a0)) return;
     if (dq) {
-        void *a[] = {&q, &k, &v, &mask, &stats, &D, &dO, &dq, &H, &Hkv, &Tq, &Tkv, &scale, &causal, &beta};
+        void *a[] = {&q, &k, &v, &mask, &stats, &D, &dO, &dq, &H, &Hkv, &Tq, &Tkv, &scale, &causal, &beta, &ldo};
         if (ncm_launch_named("sdpa_fbwd_dq_hd64", (unsigned)H, (unsigned)B, blocks_of(Tq, 64), 256, a)) return;
     }
     if (dk || dv) {
-        void *a[] = {&q, &k, &v, &mask, &stats, &D, &dO, &dk, &dv, &H, &Hkv, &Tq, &Tkv, &scale, &causal, &beta};
+        void *a[] = {&q, &k, &v, &mask, &stats, &D, &dO, &dk, &dv, &H, &Hkv, &Tq, &Tkv, &scale, &causal, &beta,
+                     &ldo};
         ncm_launch_named("sdpa_fbwd_dkdv_hd64", (unsigned)Hkv, (unsigned)B, blocks_of(Tkv, 64), 256, a);
     }
 }
@@ -244,7 +247,7 @@ static void sdpa_bwd_flash_any(const float *q, const float *k, const float *v, c
 void ncm_sdpa_bwd_flash(const float *q, const float *k, const float *v, const float *o, const float *stats,
                         const float *mask, int causal, const float *dO, float *dq, float *dk, float *dv, int B, int H,
                         int Hkv, int Tq, int Tkv, int hd) {
-    sdpa_bwd_flash_any(q, k, v, o, stats, mask, causal, dO, dq, dk, dv, B, H, Hkv, Tq, Tkv, hd, 1);
+    sdpa_bwd_flash_any(q, k, v, o, stats, mask, causal, dO, dq, dk, dv, B, H, Hkv, Tq, Tkv, hd, 1, 0);
 }
 
 /* beta 0: dq, dk and dv are written (every element has one writer in the
@@ -252,7 +255,19 @@ void ncm_sdpa_bwd_flash(const float *q, const float *k, const float *v, const fl
 void ncm_sdpa_bwd_flash_ex(const float *q, const float *k, const float *v, const float *o, const float *stats,
                            const float *mask, int causal, const float *dO, float *dq, float *dk, float *dv, int B,
                            int H, int Hkv, int Tq, int Tkv, int hd, int beta) {
-    sdpa_bwd_flash_any(q, k, v, o, stats, mask, causal, dO, dq, dk, dv, B, H, Hkv, Tq, Tkv, hd, beta);
+    sdpa_bwd_flash_any(q, k, v, o, stats, mask, causal, dO, dq, dk, dv, B, H, Hkv, Tq, Tkv, hd, beta, 0);
+}
+
+void ncm_sdpa_bwd_flash_rows(const float *q, const float *k, const float *v, const float *o, const float *stats,
+                             const float *mask, int causal, const float *dO, float *dqkv, int B, int H, int Hkv,
+                             int Tq, int Tkv, int hd, int beta) {
+    const int64_t ld = (int64_t)(H + 2 * Hkv) * hd;
+    if (Tq != Tkv || ld > INT_MAX || !dqkv) {
+        ncm_fail(NCM_E_ARG, "ncm_sdpa_bwd_flash_rows: needs Tq == Tkv and a gradient buffer");
+        return;
+    }
+    float *dq = dqkv, *dk = dqkv + (int64_t)H * hd, *dv = dk + (int64_t)Hkv * hd;
+    sdpa_bwd_flash_any(q, k, v, o, stats, mask, causal, dO, dq, dk, dv, B, H, Hkv, Tq, Tkv, hd, beta, (int)ld);
 }
 
 /* ---- optimizer (train.c:51-64, 102-145, 172-178; train_gpt2.c:160-173) ---- */

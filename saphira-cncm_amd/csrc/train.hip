@@ -1344,7 +1344,7 @@ extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_pe
 sdpa_fbwd_dq_hd64(const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
                   const float *__restrict__ mask, const float *__restrict__ stats, const float *__restrict__ D,
                   const float *__restrict__ dO, float *__restrict__ dq, int H, int Hkv, int Tq, int Tkv, float scale,
-                  int causal, int beta) {
+                  int causal, int beta, int ldo) {
     __shared__ __attribute__((aligned(16))) float sK[64 * SB_LD];
     __shared__ __attribute__((aligned(16))) float sV[64 * SB_LD];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1433,7 +1433,8 @@ sdpa_fbwd_dq_hd64(const float *__restrict__ q, const float *__restrict__ k, cons
     for (int r = 0; r < 4; ++r) {
         const int qi = qw + 4 * lg + r;
         if (qi < Tq) {
-            f4 *o = (f4 *)(dq + (rbase + qi) * 64 + 4 * li);
+            // ldo > 0: rows (b, query) of stride ldo, head h at column 64 h
+            f4 *o = (f4 *)(dq + (ldo ? ((int64_t)b * Tq + qi) * ldo + h * 64 : (rbase + qi) * 64) + 4 * li);
             f4 cur = beta ? *o : f4{0.f, 0.f, 0.f, 0.f};
             cur[0] += scale * acc[0][r];
             cur[1] += scale * acc[1][r];
@@ -1456,7 +1457,7 @@ extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_pe
 sdpa_fbwd_dkdv_hd64(const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
                     const float *__restrict__ mask, const float *__restrict__ stats, const float *__restrict__ D,
                     const float *__restrict__ dO, float *__restrict__ dk, float *__restrict__ dv, int H, int Hkv,
-                    int Tq, int Tkv, float scale, int causal, int beta) {
+                    int Tq, int Tkv, float scale, int causal, int beta, int ldo) {
     __shared__ __attribute__((aligned(16))) float sG[64 * SB_LD];   // dO tile [query][d]
     __shared__ __attribute__((aligned(16))) float sQ[64 * SB_LD];   // Q tile  [query][d]
     __shared__ __attribute__((aligned(16))) float sM[64];
@@ -1570,8 +1571,10 @@ sdpa_fbwd_dkdv_hd64(const float *__restrict__ q, const float *__restrict__ k, co
     for (int r = 0; r < 4; ++r) {
         const int key = k0 + wave * 16 + 4 * lg + r;
         if (key < Tkv) {
+            // ldo > 0: rows (b, key) of stride ldo, kv head kvh at column 64 kvh
+            const int64_t oe = (ldo ? ((int64_t)b * Tkv + key) * ldo + kvh * 64 : (kbase + key) * 64) + 4 * li;
             if (dk) {
-                f4 *o = (f4 *)(dk + (kbase + key) * 64 + 4 * li);
+                f4 *o = (f4 *)(dk + oe);
                 f4 cur = beta ? *o : f4{0.f, 0.f, 0.f, 0.f};
                 cur[0] += scale * ak[0][r];
                 cur[1] += scale * ak[1][r];
@@ -1580,7 +1583,7 @@ sdpa_fbwd_dkdv_hd64(const float *__restrict__ q, const float *__restrict__ k, co
                 *o = cur;
             }
             if (dv) {
-                f4 *o = (f4 *)(dv + (kbase + key) * 64 + 4 * li);
+                f4 *o = (f4 *)(dv + oe);
                 f4 cur = beta ? *o : f4{0.f, 0.f, 0.f, 0.f};
                 cur[0] += av[0][r];
                 cur[1] += av[1][r];

@@ -126,7 +126,7 @@ def step():
         lib.ncm_t_gelu_tanh(tp, mm, m2, R * I)
         lib.ncm_t_linear(tp, m2, w[10], w[11], mlpo, R, C, I)
         lib.ncm_t_add(tp, x1, mlpo, out, R * C)
-        keep[li] = dict(qq=qq, kk=kk, vv=vv, ctx=ctx, mn=mn, mm=mm, m2=m2, mlpo=mlpo)
+        keep[li] = dict(qkv=qkv, qq=qq, kk=kk, vv=vv, ctx=ctx, mn=mn, mm=mm, m2=m2, mlpo=mlpo)
         h = out
     ncmhip.check()
     n = len(P)
@@ -186,7 +186,11 @@ def test_sdpa_backward_t512_slices(step, li):
     keep = step["keep"][li]
     q, k, v = (host(keep[n], (B, H, T, HD)) for n in ("qq", "kk", "vv"))
     dO = host(step["grad"](keep["ctx"]), (B, H, T, HD))
-    gq, gk, gv = (host(step["grad"](keep[n]), (B, H, T, HD)) for n in ("qq", "kk", "vv"))
+    # q, k and v feed only the attention, and the split that made them stands
+    # right before it: the attention's backward writes their gradients straight
+    # into the qkv rows' gradient [R][3C] (q | k | v, head h at columns 64 h)
+    gqkv = host(step["grad"](keep["qkv"]), (B, T, 3, H, HD))
+    gq, gk, gv = (np.ascontiguousarray(gqkv[:, :, j].transpose(0, 2, 1, 3)) for j in range(3))
     mask = np.where(np.arange(T)[None, :] <= np.arange(T)[:, None], 0.0, -1e9).astype(np.float32)
     for b, hh in ((0, 0), (B - 1, H - 1), (13, 5)):
         sl = np.s_[b:b + 1, hh:hh + 1]

@@ -487,3 +487,53 @@ def test_tape_qkv_projection_to_heads(B, T, C, H, hd, K):
     for n in g1:
         assert bits_equal(g1[n], g2[n]), n
     assert np.any(o1[0]) and np.any(g1["x"])
+
+
+@pytest.mark.parametrize("B,T,C,H,causal", [(2, 128, 128, 2, 1), (2, 96, 192, 3, 0), (1, 70, 128, 2, 1)])
+def test_tape_attention_gradients_into_qkv_rows(B, T, C, H, causal):
+    """split -> attention on the tape with nothing else reading q, k and v:
+    the attention's backward writes its gradients straight into the qkv rows'
+    gradient (the split's backward is skipped).  Against the same tape with
+    q's gradient requested, which keeps the two records apart: the gradients
+    of x, W and b bit for bit (ctx's gradient seeded)."""
+    lib = ncmhip.load()
+    hd, R = 64, B * T
+    N = 3 * C
+    x, W, b = rnd(100, R, C), rnd(101, N, C, scale=0.1), rnd(102, N)
+    g = rnd(103, B, H, T, hd)
+    mask = np.where(np.arange(T)[None, :] <= np.arange(T)[:, None], 0.0, -1e9).astype(np.float32)
+
+    def run(keep_q):
+        ins = {"x": x, "W": W, "b": b}
+        bufs = {n: up(a) for n, a in ins.items()}
+        qkv, qq, kk, vv, ctx = (D.empty((R, N)), D.empty((B, H, T, hd)), D.empty((B, H, T, hd)),
+                                D.empty((B, H, T, hd)), D.empty((B, H, T, hd)))
+        md = up(mask)
+        grads = {n: D.from_numpy(np.zeros_like(a)) for n, a in ins.items()}
+        gctx, gqb = up(g), D.from_numpy(np.zeros((B, H, T, hd), np.float32))
+        tape = lib.ncm_tape_new()
+        try:
+            lib.ncm_t_linear(tape, bufs["x"].ptr, bufs["W"].ptr, bufs["b"].ptr, qkv.ptr, R, N, C)
+            lib.ncm_t_qkvsplit(tape, qkv.ptr, qq.ptr, kk.ptr, vv.ptr, B, T, C, H, hd, H, 1)
+            if causal:
+                lib.ncm_t_sdpa_causal(tape, qq.ptr, kk.ptr, vv.ptr, ctx.ptr, B, H, H, T, T, hd)
+            else:
+                lib.ncm_t_sdpa(tape, qq.ptr, kk.ptr, vv.ptr, md.ptr, ctx.ptr, B, H, H, T, T, hd)
+            ncmhip.check()
+            keys = [bufs[n].ptr for n in ins] + [ctx.ptr] + ([qq.ptr] if keep_q else [])
+            gps = [grads[n].ptr for n in ins] + [gctx.ptr] + ([gqb.ptr] if keep_q else [])
+            sz = [a.size for a in ins.values()] + [g.size] + ([g.size] if keep_q else [])
+            n = len(keys)
+            pm = _PMap(ctypes.cast((ctypes.c_void_p * n)(*keys), ctypes.c_void_p),
+                       ctypes.cast((ctypes.c_void_p * n)(*gps), ctypes.c_void_p),
+                       ctypes.cast((ctypes.c_int64 * n)(*sz), ctypes.c_void_p), n)
+            lib.ncm_tape_backward(tape, ctypes.byref(pm))
+            ncmhip.check()
+            return {n: grads[n].numpy() for n in ins}
+        finally:
+            lib.ncm_tape_free(tape)
+
+    fused, apart = run(False), run(True)
+    for n in apart:
+        assert bits_equal(fused[n], apart[n]), n
+    assert np.any(apart["x"])

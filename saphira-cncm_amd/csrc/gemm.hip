@@ -51,8 +51,8 @@
 #include "mfma_slab.h"
 
 enum { EPI_STORE = 0, EPI_ACCUM = 1, EPI_GATED = 2, EPI_ACT_BWD = 3 };
-// Per-tile output selection of the forward kernels: SEL_F3 (gemm_64x64_fwd3_v,
-// f3_select) and SEL_HEADS (gemm_64x64_fwdh_v, heads_select).
+// Per-tile output selection: SEL_F3 (gemm_64x64_fwd3_v, f3_select) and
+// SEL_HEADS (gemm_64x64_fwdh_v, gemm_64x64_dxh_v: heads_select).
 enum { SEL_NONE = 0, SEL_F3 = 1, SEL_HEADS = 2 };
 
 struct GemmArgs {
@@ -1103,6 +1103,7 @@ GEMM_DMA_KERNEL(gemm_64x64_dx_v, true, false, EPI_ACCUM, false, SEL_NONE)
 GEMM_DMA_KERNEL(gemm_64x64_dw_v, false, false, EPI_ACCUM, false, SEL_NONE)
 GEMM_DMA_KERNEL(gemm_64x64_dwb_v, false, false, EPI_ACCUM, true, SEL_NONE)   // dW + db
 GEMM_DMA_KERNEL(gemm_64x64_dxa_v, true, false, EPI_ACT_BWD, false, SEL_NONE) // dX through the activation backward
+GEMM_DMA_KERNEL(gemm_64x64_dxh_v, true, false, EPI_ACCUM, false, SEL_HEADS)  // dX to head-major
 GEMM_DMA_KERNEL(gemm_64x64_gated_v, true, true, EPI_GATED, false, SEL_NONE)
 GEMM_TILE_KERNEL(gemm_64x64_fwd_s, 64, 64, true, true, EPI_STORE, false)
 GEMM_TILE_KERNEL(gemm_64x64_dx_s, 64, 64, true, false, EPI_ACCUM, false)
@@ -1114,6 +1115,7 @@ GEMM_TILE_FIXUP(gemm_64x64_fixup_dx_v, EPI_ACCUM, false, true, false, SEL_NONE)
 GEMM_TILE_FIXUP(gemm_64x64_fixup_dw_v, EPI_ACCUM, true, true, false, SEL_NONE)
 GEMM_TILE_FIXUP(gemm_64x64_fixup_dwb_v, EPI_ACCUM, true, true, true, SEL_NONE)
 GEMM_TILE_FIXUP(gemm_64x64_fixup_dxa_v, EPI_ACT_BWD, false, true, false, SEL_NONE)
+GEMM_TILE_FIXUP(gemm_64x64_fixup_dxh_v, EPI_ACCUM, false, true, false, SEL_HEADS)
 GEMM_TILE_FIXUP(gemm_64x64_fixup_fwd_s, EPI_STORE, false, false, false, SEL_NONE)
 GEMM_TILE_FIXUP(gemm_64x64_fixup_dx_s, EPI_ACCUM, false, false, false, SEL_NONE)
 GEMM_TILE_FIXUP(gemm_64x64_fixup_dw_s, EPI_ACCUM, false, false, false, SEL_NONE)

@@ -73,6 +73,11 @@ int ncm_linear_dx_fusable(int64_t batch, int M, int K, const float *dy, const fl
  * ncm_act_bwd_ex, the dX itself never stored; dW / db accumulate. */
 void ncm_linear_bwd_act(const float *x, const float *W, const float *dy, float *dxa, const float *ax, int kind,
                         int beta, float *dW, float *db, int64_t batch, int M, int K);
+/* linear_bwd whose x [B*T][64 H] is the head merge of ctx [B][H][T][64]: dX
+ * written (beta 0) or added into ctx's gradient directly (T % 64 == 0; the
+ * merge's backward bit for bit); dW / db accumulate. */
+void ncm_linear_bwd_heads(const float *x, const float *W, const float *dy, float *dctx, int beta, float *dW,
+                          float *db, int B, int T, int M, int H);
 /* Backward ops with a first-write form: beta 1 accumulates (the public
  * functions' contract), beta 0 writes 0.0f + the gradient -- the bits of an
  * accumulation into zeros -- so the output needs no clearing and is not read.

@@ -213,7 +213,11 @@ static int run_gemm_x(int kind, const float *A, const float *B, float *C, const 
         return ncm_fail(NCM_E_ARG, "linear: %d x %d output has too many tiles", Mo, No);
     char name[48], fix[48];
     /* dwb: the dW kernel that also sums db; dxa: dX through the activation backward */
-    const char *op = db ? "dwb" : ex->bwd_x ? "dxa" : ex->W3 ? "fwd3" : ex->heads ? "fwdh" : kind_names[kind];
+    const char *op = db           ? "dwb"
+                     : ex->bwd_x  ? "dxa"
+                     : ex->W3     ? "fwd3"
+                     : ex->heads  ? (kind == L_DX ? "dxh" : "fwdh")
+                                  : kind_names[kind];
     snprintf(name, sizeof name, "gemm_%dx%d_%s_%c", bm, bn, op, vec ? 'v' : 's');
     int slots = gemm_slots(name);
     if (slots < 0) return NCM_E_INIT;
@@ -566,6 +570,28 @@ void ncm_linear_fwd_qkv_heads(const float *x, const float *W, const float *b, fl
     const int n3[3] = {C, K * hd, K * hd};
     GemmExtra ex = {NULL, NULL, NULL, 0, NULL, NULL, NULL, n3, heads, T};
     run_gemm_x(L_FWD, x, W, qq, b, NULL, 0, (int)rows, (int)N, C, C, C, (int)N, NCM_ACT_NONE, 1, 1, &ex);
+}
+
+/* linear_bwd whose x is the head merge of ctx [B][H][T][64] (x = rows (b, t)
+ * of C = 64 H): the dX product is written (beta 0) or added (beta 1) straight
+ * into ctx's gradient dctx, each tile one [64 t][64 d] block of a head, which
+ * is linear_bwd's dX followed by the merge's backward, bit for bit; dW and db
+ * as linear_bwd.  Needs ncm_linear_dx_fusable, T % 64 == 0. */
+void ncm_linear_bwd_heads(const float *x, const float *W, const float *dy, float *dctx, int beta, float *dW,
+                          float *db, int B, int T, int M, int H) {
+    const int64_t batch = (int64_t)B * T;
+    const int K = 64 * H;
+    if (check_dims("ncm_linear_bwd_heads", batch, M, K)) return;
+    if (!ncm_linear_dx_fusable(batch, M, K, dy, W) || T % 64 != 0 || !dctx || (dW && !x)) {
+        ncm_fail(NCM_E_ARG, "ncm_linear_bwd_heads: shape or operands not supported");
+        return;
+    }
+    if (ncm_ready()) return;
+    float *const heads[3] = {dctx, NULL, NULL};
+    const int n3[3] = {K, 0, 0};
+    GemmExtra ex = {NULL, NULL, NULL, 0, NULL, NULL, NULL, n3, heads, T};
+    if (run_gemm_x(L_DX, dy, W, dctx, NULL, NULL, 0, (int)batch, K, M, M, K, K, 0, 1, beta, &ex)) return;
+    ncm_linear_bwd_ex(x, W, dy, NULL, dW, db, batch, M, K, 1);
 }
 
 int ncm_linear_dx_fusable(int64_t batch, int M, int K, const float *dy, const float *W) {

@@ -527,6 +527,20 @@ void ncm_tape_backward(NcmTape *t, const NcmPMap *pm) {
                 i--;
                 break;
             }
+            if (ra && ra->op == NT_MERGE && ra->y == r->a && ra->p4 == 64 && ra->p2 == ra->p3 * 64 && K == ra->p2 &&
+                (int64_t)ra->n * ra->p1 == batch && ra->p1 % 64 == 0 && !gmap_find(t, r->a) &&
+                ncm_linear_dx_fusable(batch, M, K, dy, r->b)) {
+                /* the record right before merged the attention heads into this
+                 * linear's input, and nothing else reads it: the dX GEMM writes
+                 * the heads' gradient directly (the merged rows' gradient is
+                 * never stored), and the merge record is done too */
+                float *dctx = gmap_get_fresh(t, ra->a, batch * K, &bx);
+                if (!dctx) return;
+                ncm_linear_bwd_heads(r->a, r->b, dy, dctx, bx, gmap_get(t, r->b, (int64_t)M * K),
+                                     r->c ? gmap_get(t, r->c, M) : NULL, (int)ra->n, ra->p1, M, ra->p3);
+                i--;
+                break;
+            }
             float *dx = gmap_get_fresh(t, r->a, batch * K, &bx);
             ncm_linear_bwd_ex(r->a, r->b, dy, dx, gmap_get(t, r->b, (int64_t)M * K),
                               r->c ? gmap_get(t, r->c, M) : NULL, batch, M, K, bx);

@@ -537,3 +537,44 @@ def test_tape_attention_gradients_into_qkv_rows(B, T, C, H, causal):
     for n in apart:
         assert bits_equal(fused[n], apart[n]), n
     assert np.any(apart["x"])
+
+
+@pytest.mark.parametrize("B,T,H,M", [(2, 128, 2, 96), (3, 64, 4, 256), (1, 70, 2, 64)])
+def test_tape_merge_then_linear_dx_to_heads(B, T, H, M):
+    """head merge -> linear on the tape with nothing else reading the merged
+    rows: the linear's dX GEMM writes the heads' gradient directly (the merge's
+    backward is skipped).  Against the same tape with the merged rows'
+    gradient requested (which keeps the records apart): the gradients of ctx,
+    W and b bit for bit.  T = 70: rows of a tile in two sequences (no fusion)."""
+    lib = ncmhip.load()
+    hd, R, C = 64, B * T, 64 * H
+    ctx, W, b, g = rnd(110, B, H, T, hd), rnd(111, M, C, scale=0.1), rnd(112, M), rnd(113, R, M)
+
+    def run(keep_mo):
+        ins = {"ctx": ctx, "W": W, "b": b}
+        bufs = {n: up(a) for n, a in ins.items()}
+        mo, y = D.empty((R, C)), D.empty((R, M))
+        grads = {n: D.from_numpy(np.zeros_like(a)) for n, a in ins.items()}
+        gy, gmo = up(g), D.from_numpy(np.zeros((R, C), np.float32))
+        tape = lib.ncm_tape_new()
+        try:
+            lib.ncm_t_headmerge(tape, bufs["ctx"].ptr, mo.ptr, B, T, C, H, hd)
+            lib.ncm_t_linear(tape, mo.ptr, bufs["W"].ptr, bufs["b"].ptr, y.ptr, R, M, C)
+            ncmhip.check()
+            keys = [bufs[n].ptr for n in ins] + [y.ptr] + ([mo.ptr] if keep_mo else [])
+            gps = [grads[n].ptr for n in ins] + [gy.ptr] + ([gmo.ptr] if keep_mo else [])
+            sz = [a.size for a in ins.values()] + [g.size] + ([R * C] if keep_mo else [])
+            n = len(keys)
+            pm = _PMap(ctypes.cast((ctypes.c_void_p * n)(*keys), ctypes.c_void_p),
+                       ctypes.cast((ctypes.c_void_p * n)(*gps), ctypes.c_void_p),
+                       ctypes.cast((ctypes.c_int64 * n)(*sz), ctypes.c_void_p), n)
+            lib.ncm_tape_backward(tape, ctypes.byref(pm))
+            ncmhip.check()
+            return {n: grads[n].numpy() for n in ins}
+        finally:
+            lib.ncm_tape_free(tape)
+
+    fused, apart = run(False), run(True)
+    for n in apart:
+        assert bits_equal(fused[n], apart[n]), n
+    assert np.any(apart["ctx"])

@@ -369,6 +369,12 @@ void ncm_t_linear_res(NcmTape *t, const float *x, const float *W, const float *b
  * bit for bit the two calls (train_gpt2.c:58-62) */
 void ncm_t_linear_qkvsplit(NcmTape *t, const float *x, const float *W, const float *b, float *qkv, float *qq,
                            float *kk, float *vv, int B, int T, int C, int H, int hd, int K, int rep);
+/* extension: ncm_t_sdpa_causal (q, k, v -> ctx [B][H][T][hd]) then
+ * ncm_t_headmerge (ctx -> out [B*T][H hd]) with the attention writing the
+ * merged rows itself (hd 64: ctx is then not written; it still keys its
+ * gradient), bit for bit the two calls (train_gpt2.c:64-66) */
+void ncm_t_sdpa_causal_merge(NcmTape *t, const float *q, const float *k, const float *v, float *ctx, float *out,
+                             int B, int H, int Hkv, int T, int hd);
 /* extension: ncm_t_sdpa with the causal mask generated in the kernels (query t
  * sees keys <= t + Tkv - Tq), replacing the T x T -1e9 mask the reference's
  * callers build and upload (train_gpt2.c:112-121) */

@@ -72,8 +72,7 @@ static float *gpt2_block(NcmTape *tp, const NcmGpt2Config *c, float *const *P, i
     if (!out) return NULL;
     ncm_t_layernorm_eps(tp, x, w[0], w[1], ln, R, C, GPT2_LN_EPS);
     ncm_t_linear_qkvsplit(tp, ln, w[2], w[3], qkv, qq, kk, vv, B, T, C, H, hd, H, 1);   /* GEMM to heads */
-    ncm_t_sdpa_causal(tp, qq, kk, vv, ctx, B, H, H, T, T, hd);   /* the -1e9 causal mask, generated */
-    ncm_t_headmerge(tp, ctx, mo, B, T, C, H, hd);
+    ncm_t_sdpa_causal_merge(tp, qq, kk, vv, ctx, mo, B, H, H, T, hd);   /* causal mask generated, heads merged */
     ncm_t_linear_res(tp, mo, w[4], w[5], x, x1, R, C, C);   /* x1 = x + attn proj */
     ncm_t_layernorm_eps(tp, x1, w[6], w[7], mn, R, C, GPT2_LN_EPS);
     ncm_t_linear_act(tp, mn, w[8], w[9], mm, m2, R, I, C, 2);   /* m2 = gelu_tanh(mm) */

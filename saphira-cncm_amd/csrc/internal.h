@@ -90,16 +90,17 @@ void ncm_rmsnorm_bwd_ex(const float *x, const float *w, const float *dy, float *
                         int beta);
 void ncm_act_bwd_ex(int kind, const float *x, const float *dy, float *dx, int64_t n, int beta);
 void ncm_add_inplace_ex(float *y, const float *x, int64_t n, int beta);
+/* (o_ld > 0: o stored with the heads merged, rows (b, t) of stride o_ld) */
 void ncm_sdpa_bwd_flash_ex(const float *q, const float *k, const float *v, const float *o, const float *stats,
                            const float *mask, int causal, const float *dO, float *dq, float *dk, float *dv, int B,
-                           int H, int Hkv, int Tq, int Tkv, int hd, int beta);
+                           int H, int Hkv, int Tq, int Tkv, int hd, int beta, int o_ld);
 /* ncm_sdpa_bwd_flash_ex with the three gradients written into the q | k | v
  * rows' gradient dqkv [B*T][(H + 2 Hkv) hd] (q at column 0, k at H hd, v at
  * (H + Hkv) hd): the gradient qkv_split_bwd would form from them, when q, k
  * and v came from such rows by a split with one kv head per kv head. */
 void ncm_sdpa_bwd_flash_rows(const float *q, const float *k, const float *v, const float *o, const float *stats,
                              const float *mask, int causal, const float *dO, float *dqkv, int B, int H, int Hkv,
-                             int Tq, int Tkv, int hd, int beta);
+                             int Tq, int Tkv, int hd, int beta, int o_ld);
 void ncm_qkv_split_bwd_ex(const float *gq, const float *gk, const float *gv, float *dx, int B, int T, int C, int H,
                           int hd, int K, int rep, int beta);
 void ncm_heads_bwd_ex(const float *dy, float *dx, int B, int T, int C, int H, int hd, int dir, int beta);
@@ -120,6 +121,9 @@ int ncm_conv1d_btd(const float *x, const float *W, const float *b, float *y, int
  * (the values of sdpa_fwd_gqa_causal followed by head_merge_fwd). */
 void ncm_sdpa_fwd_causal_merged(const float *q, const float *k, const float *v, float *out, int B, int Hq, int Hkv,
                                 int Tq, int Tkv, int hd);
+/* ncm_sdpa_fwd_stats with the heads merged on output: out [B][Tq][Hq hd]. */
+void ncm_sdpa_fwd_stats_merged(const float *q, const float *k, const float *v, const float *mask, float *out,
+                               float *stats, int B, int Hq, int Hkv, int Tq, int Tkv, int hd, int causal);
 /* SDPA forward (hd 64, 16-byte aligned operands) that also writes each
  * query row's softmax (max, sum) to stats [B][Hq][Tq][2]; causal generates
  * the mask (query t sees keys <= t + Tkv - Tq) instead of reading one. */

@@ -373,6 +373,11 @@ void ncm_sdpa_fwd_causal_merged(const float *q, const float *k, const float *v, 
     sdpa_any("ncm_sdpa_fwd_causal_merged", q, k, v, NULL, out, B, Hq, Hkv, Tq, Tkv, hd, 1, 1, NULL);
 }
 
+void ncm_sdpa_fwd_stats_merged(const float *q, const float *k, const float *v, const float *mask, float *out,
+                               float *stats, int B, int Hq, int Hkv, int Tq, int Tkv, int hd, int causal) {
+    sdpa_any("ncm_sdpa_fwd_stats_merged", q, k, v, mask, out, B, Hq, Hkv, Tq, Tkv, hd, causal, 1, stats);
+}
+
 void ncm_sdpa_fwd_stats(const float *q, const float *k, const float *v, const float *mask, float *out, float *stats,
                         int B, int Hq, int Hkv, int Tq, int Tkv, int hd, int causal) {
     sdpa_any("ncm_sdpa_fwd_stats", q, k, v, mask, out, B, Hq, Hkv, Tq, Tkv, hd, causal, 0, stats);

@@ -123,6 +123,8 @@ typedef struct {
     const float *mask;          /* SDPA: the additive mask (may be NULL) */
     int *ids;                   /* EMBED: host copy of the ids */
     const float *cos_t, *sin_t; /* ROPE tables */
+    const float *orow;          /* SDPA: the output's values with the heads merged (y only keys the gradient) */
+    int o_ld;                   /* SDPA: orow's row stride */
     int64_t n;
     int p1, p2, p3, p4, p5, p6;
     double s;
@@ -426,6 +428,33 @@ void ncm_t_sdpa_causal(NcmTape *t, const float *q, const float *k, const float *
     t_sdpa_any(t, q, k, v, NULL, 1, o, B, H, Hkv, Tq, Tkv, hd);
 }
 
+/* ncm_t_sdpa_causal (q, k, v -> ctx) then ncm_t_headmerge (ctx -> out) with
+ * the attention writing the merged rows itself: the same records, ctx keying
+ * its gradient while the attention record reads its output values from out
+ * (flash path; otherwise the two calls). */
+void ncm_t_sdpa_causal_merge(NcmTape *t, const float *q, const float *k, const float *v, float *ctx, float *out,
+                             int B, int H, int Hkv, int T, int hd) {
+    const int C = H * hd;
+    const int flash = hd == 64 && T % 4 == 0 && Hkv >= 1 && H % Hkv == 0 && is_aligned16(q) && is_aligned16(k) &&
+                      is_aligned16(v) && is_aligned16(out);
+    if (!flash) {
+        ncm_t_sdpa_causal(t, q, k, v, ctx, B, H, Hkv, T, T, hd);
+        ncm_t_headmerge(t, ctx, out, B, T, C, H, hd);
+        return;
+    }
+    float *aux = (float *)pool_alloc(&t->rec, (size_t)B * H * T * 2 * sizeof(float));
+    if (!aux) { ncm_fail(NCM_E_OOM, "ncm_t_sdpa_causal_merge: row statistics"); return; }
+    ncm_sdpa_fwd_stats_merged(q, k, v, NULL, out, aux, B, H, Hkv, T, T, hd, 1);
+    NtRec *r = emit(t, NT_SDPA);
+    if (!r) return;
+    r->a = q; r->b = k; r->c = v; r->y = ctx; r->aux = aux; r->mask = NULL;
+    r->orow = out; r->o_ld = C;
+    r->n = B; r->p1 = H; r->p2 = Hkv; r->p3 = T; r->p4 = T; r->p5 = hd; r->p6 = 1 | 2;
+    REC_OR_RETURN(rm, t, NT_MERGE);
+    rm->a = ctx; rm->y = out;
+    rm->n = B; rm->p1 = T; rm->p2 = C; rm->p3 = H; rm->p4 = hd;
+}
+
 void ncm_t_qkvsplit(NcmTape *t, const float *in, float *qq, float *kk, float *vv, int B, int T, int C, int H, int hd,
                     int K, int rep) {
     qkv_split_fwd(in, qq, kk, vv, B, T, C, H, hd, K, rep);
@@ -613,8 +642,8 @@ void ncm_tape_backward(NcmTape *t, const NcmPMap *pm) {
                 int bx;
                 float *gx = gmap_get_fresh(t, rs->a, (int64_t)B * Tq * 3 * H * hd, &bx);
                 if (!gx) return;
-                ncm_sdpa_bwd_flash_rows(r->a, r->b, r->c, r->y, r->aux, r->mask, (r->p6 >> 1) & 1, dy, gx, B, H, Hkv,
-                                        Tq, Tkv, hd, bx);
+                ncm_sdpa_bwd_flash_rows(r->a, r->b, r->c, r->orow ? r->orow : r->y, r->aux, r->mask, (r->p6 >> 1) & 1,
+                                        dy, gx, B, H, Hkv, Tq, Tkv, hd, bx, r->orow ? r->o_ld : 0);
                 i--;
                 break;
             }
@@ -633,8 +662,8 @@ void ncm_tape_backward(NcmTape *t, const NcmPMap *pm) {
                 if (!fv && gv && gv != gq && gv != gk && ncm_zero_async(gv, (size_t)nk * sizeof(float))) return;
             }
             if (r->p6 & 1)
-                ncm_sdpa_bwd_flash_ex(r->a, r->b, r->c, r->y, r->aux, r->mask, (r->p6 >> 1) & 1, dy, gq, gk, gv, B,
-                                      H, Hkv, Tq, Tkv, hd, beta);
+                ncm_sdpa_bwd_flash_ex(r->a, r->b, r->c, r->orow ? r->orow : r->y, r->aux, r->mask, (r->p6 >> 1) & 1,
+                                      dy, gq, gk, gv, B, H, Hkv, Tq, Tkv, hd, beta, r->orow ? r->o_ld : 0);
             else
                 sdpa_bwd_gqa(r->a, r->b, r->c, r->aux, dy, gq, gk, gv, B, H, Hkv, Tq, Tkv, hd);
             break;

@@ -208,10 +208,12 @@ void sdpa_bwd_gqa(const float *q, const float *k, const float *v, const float *P
  * rowsum(dO o O), then the dq and dk/dv kernels rebuild P tile by tile from
  * the forward's row statistics.  Gradients accumulate. */
 /* ldo 0: dq, dk, dv as [B][heads][T][hd]; ldo > 0: rows (b, t) of stride ldo
- * floats with head h at column h hd (the layout of the q | k | v rows). */
+ * floats with head h at column h hd (the layout of the q | k | v rows).
+ * o_ld 0: o as [B][H][Tq][hd]; o_ld > 0: o with the heads merged, rows of
+ * stride o_ld. */
 static void sdpa_bwd_flash_any(const float *q, const float *k, const float *v, const float *o, const float *stats,
                                const float *mask, int causal, const float *dO, float *dq, float *dk, float *dv, int B,
-                               int H, int Hkv, int Tq, int Tkv, int hd, int beta, int ldo) {
+                               int H, int Hkv, int Tq, int Tkv, int hd, int beta, int ldo, int o_ld) {
     if (attn_check("ncm_sdpa_bwd_flash", B, H, Hkv, Tq, Tkv, hd)) return;
     if ((int64_t)B * Tq == 0 || (!dq && !dk && !dv)) return;
     if (hd != 64 || !q || !k || !v || !o || !stats || !dO) {
@@ -231,7 +233,7 @@ static void sdpa_bwd_flash_any(const float *q, const float *k, const float *v, c
     float *D = (float *)ncm_workspace(WS_TRAIN, (size_t)rows * sizeof(float));
     if (!D) return;
     float scale = 1.0f / sqrtf((float)hd);
-    void *a0[] = {&dO, &o, &D, (void *)&rows, &hd};
+    void *a0[] = {&dO, &o, &D, (void *)&rows, &hd, &H, &Tq, &o_ld};
     if (ncm_launch_named("sdpa_bwd_rowdot", blocks_of(rows, 4), 1, 1, 256, a0)) return;
     if (dq) {
         void *a[] = {&q, &k, &v, &mask, &stats, &D, &dO, &dq, &H, &Hkv, &Tq, &Tkv, &scale, &causal, &beta, &ldo};
@@ -247,27 +249,27 @@ static void sdpa_bwd_flash_any(const float *q, const float *k, const float *v, c
 void ncm_sdpa_bwd_flash(const float *q, const float *k, const float *v, const float *o, const float *stats,
                         const float *mask, int causal, const float *dO, float *dq, float *dk, float *dv, int B, int H,
                         int Hkv, int Tq, int Tkv, int hd) {
-    sdpa_bwd_flash_any(q, k, v, o, stats, mask, causal, dO, dq, dk, dv, B, H, Hkv, Tq, Tkv, hd, 1, 0);
+    sdpa_bwd_flash_any(q, k, v, o, stats, mask, causal, dO, dq, dk, dv, B, H, Hkv, Tq, Tkv, hd, 1, 0, 0);
 }
 
 /* beta 0: dq, dk and dv are written (every element has one writer in the
  * kernels) instead of accumulated. */
 void ncm_sdpa_bwd_flash_ex(const float *q, const float *k, const float *v, const float *o, const float *stats,
                            const float *mask, int causal, const float *dO, float *dq, float *dk, float *dv, int B,
-                           int H, int Hkv, int Tq, int Tkv, int hd, int beta) {
-    sdpa_bwd_flash_any(q, k, v, o, stats, mask, causal, dO, dq, dk, dv, B, H, Hkv, Tq, Tkv, hd, beta, 0);
+                           int H, int Hkv, int Tq, int Tkv, int hd, int beta, int o_ld) {
+    sdpa_bwd_flash_any(q, k, v, o, stats, mask, causal, dO, dq, dk, dv, B, H, Hkv, Tq, Tkv, hd, beta, 0, o_ld);
 }
 
 void ncm_sdpa_bwd_flash_rows(const float *q, const float *k, const float *v, const float *o, const float *stats,
                              const float *mask, int causal, const float *dO, float *dqkv, int B, int H, int Hkv,
-                             int Tq, int Tkv, int hd, int beta) {
+                             int Tq, int Tkv, int hd, int beta, int o_ld) {
     const int64_t ld = (int64_t)(H + 2 * Hkv) * hd;
     if (Tq != Tkv || ld > INT_MAX || !dqkv) {
         ncm_fail(NCM_E_ARG, "ncm_sdpa_bwd_flash_rows: needs Tq == Tkv and a gradient buffer");
         return;
     }
     float *dq = dqkv, *dk = dqkv + (int64_t)H * hd, *dv = dk + (int64_t)Hkv * hd;
-    sdpa_bwd_flash_any(q, k, v, o, stats, mask, causal, dO, dq, dk, dv, B, H, Hkv, Tq, Tkv, hd, beta, (int)ld);
+    sdpa_bwd_flash_any(q, k, v, o, stats, mask, causal, dO, dq, dk, dv, B, H, Hkv, Tq, Tkv, hd, beta, (int)ld, o_ld);
 }
 
 /* ---- optimizer (train.c:51-64, 102-145, 172-178; train_gpt2.c:160-173) ---- */

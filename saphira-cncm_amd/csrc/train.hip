@@ -1321,14 +1321,21 @@ axpy_k(float *__restrict__ dx, const float *__restrict__ dy, float s, int64_t n)
 // arithmetic.  D = rowsum(P o dP) is formed as rowsum(dO o O), its equal
 // (sum_k P dP = sum_k P (dO . v_k) = dO . sum_k P v_k = dO . O).
 
-// D[row] = sum_d dO[row][d] O[row][d] (fp64 sum), one wave per row, hd <= 64
+// D[row] = sum_d dO[row][d] O[row][d] (fp64 sum), one wave per row, hd <= 64;
+// row = (b H + h) T + t.  ldO > 0: O is stored with the heads merged, rows
+// (b, t) of stride ldO and head h at column h hd.
 extern "C" __global__ void __launch_bounds__(256)
 sdpa_bwd_rowdot(const float *__restrict__ dO, const float *__restrict__ O, float *__restrict__ D, int64_t rows,
-                int hd) {
+                int hd, int H, int T, int ldO) {
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= rows) return;
-    double s = lane < hd ? (double)dO[row * hd + lane] * (double)O[row * hd + lane] : 0.0;
+    int64_t oe = row * hd;
+    if (ldO) {
+        const int64_t bh = row / T, t = row - bh * T, b = bh / H, h = bh - b * H;
+        oe = (b * T + t) * ldO + h * hd;
+    }
+    double s = lane < hd ? (double)dO[row * hd + lane] * (double)O[oe + lane] : 0.0;
     s = wave_sum_d(s);
     if (lane == 0) D[row] = (float)s;
 }

@@ -125,6 +125,7 @@ _SIGS = {
     "ncm_t_linear_act": (None, [vp] * 6 + [i64, ci, ci, ci]),
     "ncm_t_linear_res": (None, [vp] * 6 + [i64, ci, ci]),
     "ncm_t_linear_qkvsplit": (None, [vp] * 8 + [ci] * 7),
+    "ncm_t_sdpa_causal_merge": (None, [vp] * 6 + [ci] * 5),
     "ncm_t_qkvsplit": (None, [vp] * 5 + [ci] * 7),
     "ncm_t_headmerge": (None, [vp] * 3 + [ci] * 5),
     "ncm_t_headsplit": (None, [vp] * 3 + [ci] * 5),

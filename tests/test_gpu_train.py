@@ -578,3 +578,48 @@ def test_tape_merge_then_linear_dx_to_heads(B, T, H, M):
     for n in apart:
         assert bits_equal(fused[n], apart[n]), n
     assert np.any(apart["ctx"])
+
+
+@pytest.mark.parametrize("B,H,T", [(2, 3, 128), (1, 4, 100), (2, 2, 36)])
+def test_tape_attention_writing_merged_rows(B, H, T):
+    """ncm_t_sdpa_causal_merge (the attention writing the merged rows itself,
+    its backward reading them as O) against ncm_t_sdpa_causal +
+    ncm_t_headmerge: the merged output and the q, k, v gradients bit for bit
+    from a seeded gradient of the merged rows."""
+    lib = ncmhip.load()
+    hd = 64
+    q, k, v, g = rnd(120, B, H, T, hd), rnd(121, B, H, T, hd), rnd(122, B, H, T, hd), rnd(123, B * T, H * hd)
+
+    def run(fused):
+        ins = {"q": q, "k": k, "v": v}
+        bufs = {n: up(a) for n, a in ins.items()}
+        ctx, mo = D.empty((B, H, T, hd)), D.empty((B * T, H * hd))
+        grads = {n: D.from_numpy(np.zeros_like(a)) for n, a in ins.items()}
+        gmo = up(g)
+        tape = lib.ncm_tape_new()
+        try:
+            if fused:
+                lib.ncm_t_sdpa_causal_merge(tape, bufs["q"].ptr, bufs["k"].ptr, bufs["v"].ptr, ctx.ptr, mo.ptr, B, H,
+                                            H, T, hd)
+            else:
+                lib.ncm_t_sdpa_causal(tape, bufs["q"].ptr, bufs["k"].ptr, bufs["v"].ptr, ctx.ptr, B, H, H, T, T, hd)
+                lib.ncm_t_headmerge(tape, ctx.ptr, mo.ptr, B, T, H * hd, H, hd)
+            ncmhip.check()
+            keys = [bufs[n].ptr for n in ins] + [mo.ptr]
+            gps = [grads[n].ptr for n in ins] + [gmo.ptr]
+            sz = [a.size for a in ins.values()] + [g.size]
+            n = len(keys)
+            pm = _PMap(ctypes.cast((ctypes.c_void_p * n)(*keys), ctypes.c_void_p),
+                       ctypes.cast((ctypes.c_void_p * n)(*gps), ctypes.c_void_p),
+                       ctypes.cast((ctypes.c_int64 * n)(*sz), ctypes.c_void_p), n)
+            lib.ncm_tape_backward(tape, ctypes.byref(pm))
+            ncmhip.check()
+            return mo.numpy(), {n: grads[n].numpy() for n in ins}
+        finally:
+            lib.ncm_tape_free(tape)
+
+    (o1, g1), (o2, g2) = run(False), run(True)
+    assert bits_equal(o1, o2)
+    for n in g1:
+        assert bits_equal(g1[n], g2[n]), n
+    assert np.any(g1["q"])

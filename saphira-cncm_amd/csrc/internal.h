@@ -88,6 +88,12 @@ void ncm_layernorm_bwd_ex(const float *x, const float *w, const float *dy, float
                           int64_t rows, int C, double eps, int beta);
 void ncm_rmsnorm_bwd_ex(const float *x, const float *w, const float *dy, float *dx, float *dw, int64_t rows, int C,
                         int beta);
+/* norm backward writing dx = (0.0f + base) + the norm's gradient: a residual
+ * gradient's first write and the norm's accumulation onto it, in one pass */
+void ncm_layernorm_bwd_base(const float *x, const float *w, const float *dy, float *dx, float *dw, float *db,
+                            int64_t rows, int C, double eps, const float *base);
+void ncm_rmsnorm_bwd_base(const float *x, const float *w, const float *dy, float *dx, float *dw, int64_t rows, int C,
+                          const float *base);
 void ncm_act_bwd_ex(int kind, const float *x, const float *dy, float *dx, int64_t n, int beta);
 void ncm_add_inplace_ex(float *y, const float *x, int64_t n, int beta);
 /* (o_ld > 0: o stored with the heads merged, rows (b, t) of stride o_ld) */

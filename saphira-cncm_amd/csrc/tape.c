@@ -135,13 +135,43 @@ typedef struct {
     float *g;
 } GEnt;
 
+#define PEND_MAX 8
 struct NcmTape {
     NtRec *r;
     int n, cap;
     Pool rec, grad, gradw;   /* gradw: gradients whose first writer overwrites (not cleared) */
     GEnt *gm;
     int gn, gcap;
+    /* residual gradients passed through (backward): the gradient of key, not
+     * yet written, is 0.0f + base, to be written by the norm that reads key */
+    const float *pend_key[PEND_MAX];
+    const float *pend_base[PEND_MAX];
+    int64_t pend_n[PEND_MAX];
+    int npend;
 };
+
+/* The first record at or before index j (the backward visits them in that
+ * order) that names key as an operand or output, or NULL. */
+static const NtRec *next_use(const NcmTape *t, int j, const float *key) {
+    for (; j >= 0; j--) {
+        const NtRec *q = &t->r[j];
+        if (q->a == key || q->b == key || q->c == key || q->y == key) return q;
+    }
+    return NULL;
+}
+
+static const float *pend_take(NcmTape *t, const float *key) {
+    for (int k = 0; k < t->npend; k++)
+        if (t->pend_key[k] == key) {
+            const float *b = t->pend_base[k];
+            t->pend_key[k] = t->pend_key[t->npend - 1];
+            t->pend_base[k] = t->pend_base[t->npend - 1];
+            t->pend_n[k] = t->pend_n[t->npend - 1];
+            t->npend--;
+            return b;
+        }
+    return NULL;
+}
 
 NcmTape *ncm_tape_new(void) {
     NcmTape *t = (NcmTape *)calloc(1, sizeof(NcmTape));
@@ -514,6 +544,7 @@ void ncm_t_ce(NcmTape *t, const float *logits, const int *tgt, const float *wmas
 void ncm_tape_backward(NcmTape *t, const NcmPMap *pm) {
     if (!t || ncm_ready()) return;
     t->gn = 0;
+    t->npend = 0;
     pool_reset(&t->grad);
     pool_reset(&t->gradw);
     if (pm)
@@ -535,6 +566,10 @@ void ncm_tape_backward(NcmTape *t, const NcmPMap *pm) {
                 /* only the q output carries a gradient */
             } else if (r->op == NT_SPLIT && (gmap_find(t, r->b) || gmap_find(t, r->c))) {
             } else {
+                /* a norm left with nothing to add still owes the pending first
+                 * write of its input's gradient */
+                const float *base = t->npend && (r->op == NT_LN || r->op == NT_RMSN) ? pend_take(t, r->a) : NULL;
+                if (base) ncm_add_inplace_ex(gmap_find(t, r->a), base, r->n * r->p1, 0);
                 continue;
             }
         }
@@ -581,14 +616,23 @@ void ncm_tape_backward(NcmTape *t, const NcmPMap *pm) {
         case NT_LN: {
             int bx;
             float *dx = gmap_get_fresh(t, r->a, r->n * r->p1, &bx);
-            ncm_layernorm_bwd_ex(r->a, r->b, dy, dx, r->b ? gmap_get(t, r->b, r->p1) : NULL,
-                                 r->c ? gmap_get(t, r->c, r->p1) : NULL, r->n, r->p1, r->s, bx);
+            const float *base = pend_take(t, r->a);
+            if (base)
+                ncm_layernorm_bwd_base(r->a, r->b, dy, dx, r->b ? gmap_get(t, r->b, r->p1) : NULL,
+                                       r->c ? gmap_get(t, r->c, r->p1) : NULL, r->n, r->p1, r->s, base);
+            else
+                ncm_layernorm_bwd_ex(r->a, r->b, dy, dx, r->b ? gmap_get(t, r->b, r->p1) : NULL,
+                                     r->c ? gmap_get(t, r->c, r->p1) : NULL, r->n, r->p1, r->s, bx);
             break;
         }
         case NT_RMSN: {
             int bx;
             float *dx = gmap_get_fresh(t, r->a, r->n * r->p1, &bx);
-            ncm_rmsnorm_bwd_ex(r->a, r->b, dy, dx, r->b ? gmap_get(t, r->b, r->p1) : NULL, r->n, r->p1, bx);
+            const float *base = pend_take(t, r->a);
+            if (base)
+                ncm_rmsnorm_bwd_base(r->a, r->b, dy, dx, r->b ? gmap_get(t, r->b, r->p1) : NULL, r->n, r->p1, base);
+            else
+                ncm_rmsnorm_bwd_ex(r->a, r->b, dy, dx, r->b ? gmap_get(t, r->b, r->p1) : NULL, r->n, r->p1, bx);
             break;
         }
         case NT_ACT: {
@@ -603,7 +647,21 @@ void ncm_tape_backward(NcmTape *t, const NcmPMap *pm) {
         case NT_ADD: {
             int ba, bb;
             float *ga = gmap_get_fresh(t, r->a, r->n, &ba);
-            if (ga) ncm_add_inplace_ex(ga, dy, r->n, ba);
+            const NtRec *nu = ga && !ba && !r->b && t->npend < PEND_MAX ? next_use(t, i - 1, r->a) : NULL;
+            if (nu && (nu->op == NT_LN || nu->op == NT_RMSN) && nu->a == r->a && nu->n * nu->p1 == r->n) {
+                /* a residual input whose gradient is new and whose next use
+                 * (in backward order) is the norm that reads it: its first
+                 * write, 0.0f + dy, is left to that norm's backward, which
+                 * writes (0.0f + dy) + its own gradient in one pass; dy is not
+                 * written again before then (its writers ran before this
+                 * record) */
+                t->pend_key[t->npend] = r->a;
+                t->pend_base[t->npend] = dy;
+                t->pend_n[t->npend] = r->n;
+                t->npend++;
+            } else if (ga) {
+                ncm_add_inplace_ex(ga, dy, r->n, ba);
+            }
             float *gb = r->b ? gmap_get_fresh(t, r->b, r->n, &bb) : NULL;   /* after a's write: b may be a */
             if (gb) ncm_add_inplace_ex(gb, dy, r->n, bb);
             break;
@@ -691,6 +749,13 @@ void ncm_tape_backward(NcmTape *t, const NcmPMap *pm) {
             break;
         }
         if (ncm_ready()) return;
+    }
+    /* (every pending write is taken by its norm record; none is left unless
+     * that record was never visited) */
+    while (t->npend > 0) {
+        const int k = t->npend - 1;
+        ncm_add_inplace_ex(gmap_find(t, t->pend_key[k]), t->pend_base[k], t->pend_n[k], 0);
+        t->npend--;
     }
 }
 

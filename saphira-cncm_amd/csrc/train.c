@@ -26,15 +26,18 @@ static int shape_ok(const char *fn, int64_t rows, int C) {
 
 /* ---- LayerNorm / RMSNorm backward (train_tape.c:569-634, 748-792) ---- */
 /* beta 0: dx is written (0.0f + the gradient) instead of accumulated. */
+/* base (with dx): dx = (0.0f + base) + the gradient, written (a residual
+ * gradient passed through, then the norm's own accumulated onto it) */
 static void norm_bwd(const char *fn, int kind, const float *x, const float *w, const float *dy, float *dx,
-                     float *dw, float *db, int64_t rows, int C, double eps, int beta) {
+                     float *dw, float *db, int64_t rows, int C, double eps, int beta, const float *base) {
     if (shape_ok(fn, rows, C)) return;
     if (rows == 0) return;
     if (!x || !dy) { ncm_fail(NCM_E_ARG, "%s: null input", fn); return; }
     if (ncm_ready()) return;
+    if (!dx) base = NULL;
     const int want_param = dw || db;
     if (C % 4 == 0 && C <= 1024 && is_aligned16(x) && is_aligned16(dy) && (!dx || is_aligned16(dx)) &&
-        (!w || is_aligned16(w)) && (rows + NBF_ROWS - 1) / NBF_ROWS <= INT_MAX) {
+        (!w || is_aligned16(w)) && (!base || is_aligned16(base)) && (rows + NBF_ROWS - 1) / NBF_ROWS <= INT_MAX) {
         /* one pass: rows in registers, dx and the parameter partials together */
         static const char *const names[2][4] = {{"ln_bwd_fused_1", "ln_bwd_fused_2", "ln_bwd_fused_3", "ln_bwd_fused_4"},
                                                 {"rmsn_bwd_fused_1", "rmsn_bwd_fused_2", "rmsn_bwd_fused_3",
@@ -45,7 +48,7 @@ static void norm_bwd(const char *fn, int kind, const float *x, const float *w, c
             part = (double *)ncm_workspace(WS_TRAIN, (size_t)chunks * C * 2 * sizeof(double));
             if (!part) return;
         }
-        void *a[] = {&x, &w, &dy, &dx, &part, &rows, &C, &eps, &beta};
+        void *a[] = {&x, &w, &dy, &dx, &part, &rows, &C, &eps, &beta, &base};
         if (ncm_launch_named(names[kind][(C + 255) / 256 - 1], (unsigned)chunks, 1, 1, 256, a)) return;
         if (!want_param) return;
         float *dbk = kind == 0 ? db : NULL;
@@ -55,6 +58,10 @@ static void norm_bwd(const char *fn, int kind, const float *x, const float *w, c
     }
     const int chunks = (int)((rows + NORM_ROWS - 1) / NORM_ROWS);
     if (chunks > 65535 && want_param) { ncm_fail(NCM_E_ARG, "%s: too many rows", fn); return; }
+    if (base) {   /* dx = 0.0f + base, then the norm's gradient accumulated */
+        ncm_add_inplace_ex(dx, base, rows * C, 0);
+        beta = 1;
+    }
     if (dx && !beta && ncm_zero_async(dx, (size_t)rows * C * sizeof(float))) return;
     size_t stats_bytes = (size_t)rows * 2 * sizeof(double);
     size_t part_bytes = want_param ? (size_t)chunks * C * 2 * sizeof(double) : 0;
@@ -78,21 +85,31 @@ static void norm_bwd(const char *fn, int kind, const float *x, const float *w, c
 
 void layernorm_bwd(const float *x, const float *w, const float *dy, float *dx, float *dw, float *db, int64_t rows,
                    int C, double eps) {
-    norm_bwd("layernorm_bwd", 0, x, w, dy, dx, dw, db, rows, C, eps, 1);
+    norm_bwd("layernorm_bwd", 0, x, w, dy, dx, dw, db, rows, C, eps, 1, NULL);
 }
 
 void rmsnorm_bwd(const float *x, const float *w, const float *dy, float *dx, float *dw, int64_t rows, int C) {
-    norm_bwd("rmsnorm_bwd", 1, x, w, dy, dx, dw, NULL, rows, C, 1e-6, 1);
+    norm_bwd("rmsnorm_bwd", 1, x, w, dy, dx, dw, NULL, rows, C, 1e-6, 1, NULL);
 }
 
 void ncm_layernorm_bwd_ex(const float *x, const float *w, const float *dy, float *dx, float *dw, float *db,
                           int64_t rows, int C, double eps, int beta) {
-    norm_bwd("layernorm_bwd", 0, x, w, dy, dx, dw, db, rows, C, eps, beta);
+    norm_bwd("layernorm_bwd", 0, x, w, dy, dx, dw, db, rows, C, eps, beta, NULL);
+}
+
+void ncm_layernorm_bwd_base(const float *x, const float *w, const float *dy, float *dx, float *dw, float *db,
+                            int64_t rows, int C, double eps, const float *base) {
+    norm_bwd("layernorm_bwd", 0, x, w, dy, dx, dw, db, rows, C, eps, 0, base);
 }
 
 void ncm_rmsnorm_bwd_ex(const float *x, const float *w, const float *dy, float *dx, float *dw, int64_t rows, int C,
                         int beta) {
-    norm_bwd("rmsnorm_bwd", 1, x, w, dy, dx, dw, NULL, rows, C, 1e-6, beta);
+    norm_bwd("rmsnorm_bwd", 1, x, w, dy, dx, dw, NULL, rows, C, 1e-6, beta, NULL);
+}
+
+void ncm_rmsnorm_bwd_base(const float *x, const float *w, const float *dy, float *dx, float *dw, int64_t rows, int C,
+                          const float *base) {
+    norm_bwd("rmsnorm_bwd", 1, x, w, dy, dx, dw, NULL, rows, C, 1e-6, 0, base);
 }
 
 /* ---- softmax cross-entropy (train_tape.c:442-481, 657-679, 1801-1810) ---- */

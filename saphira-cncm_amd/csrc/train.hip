@@ -139,10 +139,14 @@ __device__ __forceinline__ void nbf_load(const float *__restrict__ p, int64_t ro
     }
 }
 
-template <int KIND, int NPL, bool BETA>
+// MODE 0: dx = 0.0f + the gradient (a first write); 1: dx += the gradient;
+// 2: dx = (0.0f + base) + the gradient, the bits of a first write of base
+// followed by the accumulation (base: a residual gradient passed through)
+template <int KIND, int NPL, int MODE>
 __device__ __forceinline__ void norm_bwd_fused_body(const float *__restrict__ x, const float *__restrict__ w,
                                                     const float *__restrict__ dy, float *__restrict__ dx,
-                                                    double *__restrict__ part, int64_t rows, int C, double eps) {
+                                                    double *__restrict__ part, int64_t rows, int C, double eps,
+                                                    const float *__restrict__ base) {
 #pragma clang fp contract(off)
     constexpr int NP = KIND == 0 ? 2 : 1;   // parameter gradients: (dw, db) or dw
     __shared__ double red[3][64 * NPL][4][NP];
@@ -208,7 +212,11 @@ __device__ __forceinline__ void norm_bwd_fused_body(const float *__restrict__ x,
                     if (c < C) {
                         f4 *o = (f4 *)(dx + r * C + c);
                         f4 v = f4{0.f, 0.f, 0.f, 0.f};
-                        if constexpr (BETA) v = *o;
+                        if constexpr (MODE == 1) v = *o;
+                        if constexpr (MODE == 2) {
+                            const f4 bv = *(const f4 *)(base + r * C + c);
+                            v = f4{0.0f + bv.x, 0.0f + bv.y, 0.0f + bv.z, 0.0f + bv.w};
+                        }
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const double d = (double)ga[j][e] * (double)wv[j][e];
@@ -246,7 +254,11 @@ __device__ __forceinline__ void norm_bwd_fused_body(const float *__restrict__ x,
                     if (c < C) {
                         f4 *o = (f4 *)(dx + r * C + c);
                         f4 v = f4{0.f, 0.f, 0.f, 0.f};
-                        if constexpr (BETA) v = *o;
+                        if constexpr (MODE == 1) v = *o;
+                        if constexpr (MODE == 2) {
+                            const f4 bv = *(const f4 *)(base + r * C + c);
+                            v = f4{0.0f + bv.x, 0.0f + bv.y, 0.0f + bv.z, 0.0f + bv.w};
+                        }
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
                             v[e] += (float)(((double)ga[j][e] * (double)wv[j][e] -
@@ -303,11 +315,14 @@ __device__ __forceinline__ void norm_bwd_fused_body(const float *__restrict__ x,
 #define NORM_BWD_FUSED(name, KIND, NPL)                                                                      \
     extern "C" __global__ void __launch_bounds__(256)                                                       \
         name(const float *__restrict__ x, const float *__restrict__ w, const float *__restrict__ dy,        \
-             float *__restrict__ dx, double *__restrict__ part, int64_t rows, int C, double eps, int beta) { \
-        if (beta)                                                                                           \
-            norm_bwd_fused_body<KIND, NPL, true>(x, w, dy, dx, part, rows, C, eps);                         \
+             float *__restrict__ dx, double *__restrict__ part, int64_t rows, int C, double eps, int beta,    \
+             const float *__restrict__ base) {                                                              \
+        if (base)                                                                                           \
+            norm_bwd_fused_body<KIND, NPL, 2>(x, w, dy, dx, part, rows, C, eps, base);                      \
+        else if (beta)                                                                                      \
+            norm_bwd_fused_body<KIND, NPL, 1>(x, w, dy, dx, part, rows, C, eps, base);                      \
         else                                                                                                \
-            norm_bwd_fused_body<KIND, NPL, false>(x, w, dy, dx, part, rows, C, eps);                        \
+            norm_bwd_fused_body<KIND, NPL, 0>(x, w, dy, dx, part, rows, C, eps, base);                      \
     }
 NORM_BWD_FUSED(ln_bwd_fused_1, 0, 1)
 NORM_BWD_FUSED(ln_bwd_fused_2, 0, 2)

@@ -623,3 +623,70 @@ def test_tape_attention_writing_merged_rows(B, H, T):
     for n in g1:
         assert bits_equal(g1[n], g2[n]), n
     assert np.any(g1["q"])
+
+
+@pytest.mark.parametrize("norm", ["ln", "rms"])
+@pytest.mark.parametrize("R,C", [(300, 128), (130, 768), (33, 52), (7, 1040)])
+@pytest.mark.parametrize("shape", ["read", "unread", "shared"])
+def test_tape_residual_gradient_into_norm(norm, R, C, shape):
+    """The residual gradient of ncm_t_linear_res whose next reader (backward
+    order) is the norm of that residual: its first write is folded into the
+    norm's dX pass.  Against ncm_t_linear + ncm_t_add (two operands, never
+    deferred): output and every gradient bit for bit.  s = 1.5 x is the
+    residual (an intermediate, so its gradient is new at the add).  Shapes:
+    the norm output feeding the linear ("read"), the norm output unread (the
+    norm record is skipped and still owes the write), s also scaled into the
+    linear's input between the norm and the add ("shared": no deferral).
+    C 52 and 1040 take the unfused norm backward."""
+    lib = ncmhip.load()
+    x, W, b = rnd(130, R, C), rnd(131, C, C), rnd(132, C)
+    lw, lb, x2, g = rnd(133, C) + 1.0, rnd(134, C), rnd(135, R, C), rnd(136, R, C)
+
+    def run(fused):
+        ins = {"x": x, "W": W, "b": b, "lw": lw, "x2": x2}
+        if norm == "ln":
+            ins["lb"] = lb
+        bufs = {n: up(a) for n, a in ins.items()}
+        s, h, t2, ao, y = (D.empty((R, C)) for _ in range(5))
+        grads = {n: D.from_numpy(np.zeros_like(a)) for n, a in ins.items()}
+        gy = up(g)
+        tape = lib.ncm_tape_new()
+        try:
+            lib.ncm_t_scale(tape, bufs["x"].ptr, 1.5, s.ptr, R * C)
+            if norm == "ln":
+                lib.ncm_t_layernorm(tape, s.ptr, bufs["lw"].ptr, bufs["lb"].ptr, h.ptr, R, C)
+            else:
+                lib.ncm_t_rmsnorm(tape, s.ptr, bufs["lw"].ptr, h.ptr, R, C)
+            if shape == "read":
+                lin_in = h
+            elif shape == "unread":
+                lin_in = bufs["x2"]
+            else:
+                lib.ncm_t_scale(tape, s.ptr, 0.5, t2.ptr, R * C)
+                lib.ncm_t_add(tape, h.ptr, t2.ptr, ao.ptr, R * C)
+                lin_in = ao
+                ao = D.empty((R, C))
+            if fused:
+                lib.ncm_t_linear_res(tape, lin_in.ptr, bufs["W"].ptr, bufs["b"].ptr, s.ptr, y.ptr, R, C, C)
+            else:
+                lib.ncm_t_linear(tape, lin_in.ptr, bufs["W"].ptr, bufs["b"].ptr, ao.ptr, R, C, C)
+                lib.ncm_t_add(tape, s.ptr, ao.ptr, y.ptr, R * C)
+            ncmhip.check()
+            keys = [bufs[n].ptr for n in ins] + [y.ptr]
+            gps = [grads[n].ptr for n in ins] + [gy.ptr]
+            sz = [a.size for a in ins.values()] + [g.size]
+            n = len(keys)
+            pm = _PMap(ctypes.cast((ctypes.c_void_p * n)(*keys), ctypes.c_void_p),
+                       ctypes.cast((ctypes.c_void_p * n)(*gps), ctypes.c_void_p),
+                       ctypes.cast((ctypes.c_int64 * n)(*sz), ctypes.c_void_p), n)
+            lib.ncm_tape_backward(tape, ctypes.byref(pm))
+            ncmhip.check()
+            return y.numpy(), {n: grads[n].numpy() for n in ins}
+        finally:
+            lib.ncm_tape_free(tape)
+
+    (o1, g1), (o2, g2) = run(False), run(True)
+    assert bits_equal(o1, o2)
+    for n in g1:
+        assert bits_equal(g1[n], g2[n]), n
+    assert np.any(g1["x"]) and np.any(g1["W"])

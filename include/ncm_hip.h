@@ -634,6 +634,13 @@ int  vq_Ddim(const VQState *vq);
  * z [B][L][D] device, idx [B][total] HOST level-major codes, as the
  * reference's caller receives them.  Codes bit-exact with the CPU path. */
 void vq_z_to_idx(VQState *vq, const float *z, int B, int *idx);
+/* replaces vq_z_to_idx_soft, ncm.h:214, vq.c:388-437 (training: levels below
+ * soft_levels draw from the tempered softmax over code distances, one
+ * xorshift64 step of *rng (host memory) per drawn row, rows in order; idx is
+ * host memory as in vq_z_to_idx; soft_levels <= 0, soft_tau <= 0 or rng NULL
+ * is vq_z_to_idx) */
+void vq_z_to_idx_soft(VQState *vq, const float *z, int B, int *idx, int soft_levels, double soft_tau,
+                      unsigned long long *rng);
 /* extension: vq_z_to_idx with device codes, and the final z_hat / z_rest
  * [B][L][D] (device, may be NULL); asynchronous on the library stream. */
 void vq_z_to_idx_dev(VQState *vq, const float *z, int B, int *idx, float *z_hat, float *z_rest);

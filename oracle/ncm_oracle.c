@@ -487,6 +487,80 @@ static void orc_level_up(const OrcVq *q, const int *idx, int B, int lv, int base
     orc_level_up_at(q, idx, total, B, lv, base, up);
 }
 
+/* vq.c:402-431: one row's soft draw.  m = mean of the row's distances (double,
+ * in index order); m <= 0 returns -1 (the caller takes the argmin, the rng is
+ * not advanced).  Else T = tau * m, bv = the row minimum, w_j = exp(-(d_j -
+ * bv) / T), one xorshift64 (13, 7, 17) step, draw = (rng >> 11) * 2^-53 *
+ * sum w, and the first j whose running sum of w exceeds the draw (V - 1 if
+ * none). */
+int orc_soft_pick(const float *d, int V, double tau, unsigned long long *rng) {
+    double m = 0;
+    for (int j = 0; j < V; j++) m += d[j];
+    m /= V;
+    if (!(m > 0)) return -1;
+    const double T = tau * m;
+    double bv = d[0];
+    for (int j = 1; j < V; j++)
+        if (d[j] < bv) bv = d[j];
+    double acc = 0;
+    for (int j = 0; j < V; j++) acc += exp(-(d[j] - bv) / T);
+    unsigned long long x = *rng;
+    x ^= x << 13;
+    x ^= x >> 7;
+    x ^= x << 17;
+    *rng = x;
+    const double draw = ((double)(x >> 11) * (1.0 / 9007199254740992.0)) * acc;
+    double csum = 0;
+    for (int j = 0; j < V; j++) {
+        csum += exp(-(d[j] - bv) / T);
+        if (draw < csum) return j;
+    }
+    return V - 1;
+}
+
+/* vq.c:388-500 vq_z_to_idx_soft: levels below soft_levels draw from the
+ * tempered softmax over the row's distances (orc_soft_pick, rows in order,
+ * one rng state), the rest take the argmin; soft_levels <= 0, tau <= 0 or no
+ * rng is vq_z_to_idx. */
+void orc_vq_z_to_idx_soft(const OrcVq *q, const float *z, int B, int *idx, float *z_hat, float *z_rest,
+                          int soft_levels, double tau, unsigned long long *rng) {
+    const int D = q->D, L = q->levels[q->n_levels - 1];
+    const size_t n = (size_t)B * L * D;
+    int total = 0;
+    for (int k = 0; k < q->n_levels; k++) total += q->levels[k];
+    float *zr = (float *)malloc(n * sizeof(float)), *zh = (float *)calloc(n, sizeof(float));
+    float *down = (float *)malloc(n * sizeof(float)), *up = (float *)malloc(n * sizeof(float));
+    memcpy(zr, z, n * sizeof(float));
+    int off = 0;
+    for (int lv = 0; lv < q->n_levels; lv++) {
+        const int tl = q->levels[lv], V = q->vocabs[lv];
+        orc_down(q, zr, B, lv, down);
+        int *codes = (int *)malloc((size_t)B * tl * sizeof(int));
+        orc_vq_argmin(down, q->E[lv], codes, (int64_t)B * tl, V, D);
+        if (rng && lv < soft_levels && tau > 0) {
+            float *dd = (float *)malloc((size_t)V * sizeof(float));
+            for (int r = 0; r < B * tl; r++) {
+                orc_l2sq(down + (size_t)r * D, q->E[lv], dd, 1, V, D);
+                const int j = orc_soft_pick(dd, V, tau, rng);
+                if (j >= 0) codes[r] = j;
+            }
+            free(dd);
+        }
+        for (int r = 0; r < B * tl; r++) idx[(int64_t)(r / tl) * total + off + r % tl] = codes[r];
+        free(codes);
+        orc_level_up(q, idx, B, lv, off, up);
+        off += tl;
+        for (size_t i = 0; i < n; i++) zh[i] += up[i];
+        for (size_t i = 0; i < n; i++) zr[i] -= up[i];
+    }
+    if (z_hat) memcpy(z_hat, zh, n * sizeof(float));
+    if (z_rest) memcpy(z_rest, zr, n * sizeof(float));
+    free(zr);
+    free(zh);
+    free(down);
+    free(up);
+}
+
 /* vq.c:378-500 vq_z_to_idx (argmin at every level) */
 void orc_vq_z_to_idx(const OrcVq *q, const float *z, int B, int *idx, float *z_hat, float *z_rest) {
     const int D = q->D, L = q->levels[q->n_levels - 1];

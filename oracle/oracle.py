@@ -46,6 +46,8 @@ def lib():
             "orc_argmax_row": (ci, [vp, ci]),
             "orc_sample_topkp": (ci, [vp, ci, ctypes.c_float, ci, ctypes.c_float, ctypes.POINTER(ctypes.c_uint64)]),
             "orc_vq_z_to_idx": (None, [vp, vp, ci, vp, vp, vp]),
+            "orc_vq_z_to_idx_soft": (None, [vp, vp, ci, vp, vp, vp, ci, ctypes.c_double, vp]),
+            "orc_soft_pick": (ci, [vp, ci, ctypes.c_double, vp]),
             "orc_vq_idx_to_zhats": (None, [vp, vp, ci, vp]),
             "orc_vq_next_input": (None, [vp, vp, ci, vp, vp, ci]),
             "orc_vq_idx_to_ncm_input": (None, [vp, vp, ci, vp]),
@@ -247,6 +249,28 @@ def vq_z_to_idx(cfg, weights, z, B):
     zh, zr = np.empty((B, L, D), np.float32), np.empty((B, L, D), np.float32)
     lib().orc_vq_z_to_idx(ctypes.byref(d), _ptr(z), B, _ptr(idx), _ptr(zh), _ptr(zr))
     return idx, zh, zr
+
+
+def vq_z_to_idx_soft(cfg, weights, z, B, soft_levels, tau, seed):
+    """vq_load + vq_z_to_idx_soft (vq.c:388-500) from rng state `seed`;
+    returns (idx, z_hat, z_rest, the rng state after)."""
+    d, keep = vq_desc(cfg, weights)
+    n, L, D = cfg["n_qlevels"], cfg["levels"][cfg["n_qlevels"] - 1], cfg["vq_embed_dim"]
+    z = _f32(z)
+    idx = np.zeros((B, sum(cfg["levels"][:n])), np.int32)
+    zh, zr = np.empty((B, L, D), np.float32), np.empty((B, L, D), np.float32)
+    rng = ctypes.c_ulonglong(seed)
+    lib().orc_vq_z_to_idx_soft(ctypes.byref(d), _ptr(z), B, _ptr(idx), _ptr(zh), _ptr(zr), soft_levels, tau,
+                               ctypes.byref(rng))
+    return idx, zh, zr, rng.value
+
+
+def soft_pick(d, tau, seed):
+    """One row's soft draw (vq.c:402-431): (index or -1, rng state after)."""
+    d = _f32(d)
+    rng = ctypes.c_ulonglong(seed)
+    j = lib().orc_soft_pick(_ptr(d), d.size, tau, ctypes.byref(rng))
+    return j, rng.value
 
 
 def vq_idx_to_zhats(cfg, weights, idx, B):

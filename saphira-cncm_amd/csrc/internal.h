@@ -33,7 +33,7 @@ int ncm_launch_named(const char *name, unsigned gx, unsigned gy, unsigned gz, un
 
 /* Library-owned device workspaces (grown on demand, stream-synchronised
  * before a grow).  Slot ids keep independent users apart. */
-enum { WS_SPLITK = 0, WS_COLSUM = 1, WS_VQ = 2, WS_DXT = 3, WS_TRAIN = 4, WS_SAMPLE = 5, WS_VQF = 6, WS_GATED = 7, WS_ATTN = 8, WS_COUNT = 9 };
+enum { WS_SPLITK = 0, WS_COLSUM = 1, WS_VQ = 2, WS_DXT = 3, WS_TRAIN = 4, WS_SAMPLE = 5, WS_VQF = 6, WS_GATED = 7, WS_ATTN = 8, WS_VQSOFT = 9, WS_COUNT = 10 };
 /* Host-to-device copy of at most 256 KB through pinned staging, ordered on
  * the library stream, returning without waiting for it (the host buffer is
  * free on return); larger copies synchronise as mem_h2d. */

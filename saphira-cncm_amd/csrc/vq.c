@@ -521,10 +521,57 @@ static int vqf_check(const VQState *vq, const float *z, int B, const char *fn) {
     return ncm_ready();
 }
 
-void vq_z_to_idx_dev(VQState *vq, const float *z, int B, int *idx, float *z_hat, float *z_rest) {
-    if (vqf_check(vq, z, B, "vq_z_to_idx_dev") || B == 0) return;
+/* vq.c:400-431: the soft draws of one level's rows (B * tl of them, codes
+ * into idx [B][total] at column off + t).  The distances are the reference's
+ * rowwise_l2sq values; a kernel takes each row's mean, minimum and weight sum
+ * (fp64, in index order, as the reference's serial loops), the host steps the
+ * xorshift64 state once per row whose mean is positive, in row order, and a
+ * second kernel draws (or takes the argmin where the mean is not positive). */
+static int vqf_soft(const float *down, const float *E, int *idx, int rows, int V, int D, int tl, int total, int off,
+                    double tau, unsigned long long *rng) {
+    const size_t dd_b = al256((size_t)rows * V * sizeof(float)), st_b = al256((size_t)rows * 3 * sizeof(double));
+    const size_t u_b = al256((size_t)rows * sizeof(double));
+    char *base = (char *)ncm_workspace(WS_VQSOFT, dd_b + st_b + u_b + (size_t)rows);
+    if (!base) return NCM_E_OOM;
+    float *dd = (float *)base;
+    double *st = (double *)(base + dd_b), *u = (double *)(base + dd_b + st_b);
+    unsigned char *flag = (unsigned char *)(base + dd_b + st_b + u_b);
+    rowwise_l2sq(down, E, dd, rows, V, D);
+    void *a[] = {&dd, &rows, &V, &tau, &st, &flag};
+    if (ncm_ready() || ncm_launch_named("vq_soft_stats", grid256(rows), 1, 1, 256, a)) return ncm_ready();
+    unsigned char *fh = (unsigned char *)malloc((size_t)rows);
+    double *uh = (double *)malloc((size_t)rows * sizeof(double));
+    if (!fh || !uh) {
+        free(fh);
+        free(uh);
+        return ncm_fail(NCM_E_OOM, "vq_z_to_idx_soft: host draws of %d rows", rows);
+    }
+    mem_d2h(fh, flag, (size_t)rows);
+    unsigned long long x = *rng;
+    for (int r = 0; r < rows; r++) {
+        if (!fh[r]) {
+            uh[r] = -1.0;
+            continue;
+        }
+        x ^= x << 13;
+        x ^= x >> 7;
+        x ^= x << 17;
+        uh[r] = (double)(x >> 11) * (1.0 / 9007199254740992.0);
+    }
+    if (!ncm_ready()) *rng = x;
+    mem_h2d(u, uh, (size_t)rows * sizeof(double));
+    free(fh);
+    free(uh);
+    void *b[] = {&dd, &rows, &V, &st, &u, &idx, &tl, &total, &off};
+    if (ncm_ready() || ncm_launch_named("vq_soft_pick", grid256(rows), 1, 1, 256, b)) return ncm_ready();
+    return 0;
+}
+
+static void vqf_run(VQState *vq, const float *z, int B, int *idx, float *z_hat, float *z_rest, int soft_levels,
+                    double tau, unsigned long long *rng, const char *fn) {
+    if (vqf_check(vq, z, B, fn) || B == 0) return;
     if (!idx) {
-        ncm_fail(NCM_E_ARG, "vq_z_to_idx_dev: null idx");
+        ncm_fail(NCM_E_ARG, "%s: null idx", fn);
         return;
     }
     VqfWs w;
@@ -544,7 +591,11 @@ void vq_z_to_idx_dev(VQState *vq, const float *z, int B, int *idx, float *z_hat,
         if (vq->has_all && lv >= 1 && lv <= vq->n_levels - 2 && vq->drefW[lv] &&
             vqf_refine(vq, w.down, vq->drefW[lv], vq->drefB[lv], w.t1, B, tl))
             return;
-        if (vq_search(w.down, vq->E[lv], idx, B * tl, vq->vocabs[lv], D, tl, vq->total, off, NULL)) return;
+        if (rng && lv < soft_levels && tau > 0) {
+            if (vqf_soft(w.down, vq->E[lv], idx, B * tl, vq->vocabs[lv], D, tl, vq->total, off, tau, rng)) return;
+        } else if (vq_search(w.down, vq->E[lv], idx, B * tl, vq->vocabs[lv], D, tl, vq->total, off, NULL)) {
+            return;
+        }
         if (vqf_level_up(vq, idx, B, lv, off, &w)) return;
         int init = lv == 0;
         void *ua[] = {&w.zh, &w.zr, &w.up, (void *)&nL, &init};
@@ -553,6 +604,23 @@ void vq_z_to_idx_dev(VQState *vq, const float *z, int B, int *idx, float *z_hat,
     }
     if (z_hat && ncm_copy_async(z_hat, w.zh, (size_t)nL * sizeof(float))) return;
     if (z_rest) ncm_copy_async(z_rest, w.zr, (size_t)nL * sizeof(float));
+}
+
+void vq_z_to_idx_dev(VQState *vq, const float *z, int B, int *idx, float *z_hat, float *z_rest) {
+    vqf_run(vq, z, B, idx, z_hat, z_rest, 0, 0.0, NULL, "vq_z_to_idx_dev");
+}
+
+void vq_z_to_idx_soft(VQState *vq, const float *z, int B, int *idx, int soft_levels, double soft_tau,
+                      unsigned long long *rng) {
+    if (vqf_check(vq, z, B, "vq_z_to_idx_soft") || B == 0) return;
+    if (!idx) {
+        ncm_fail(NCM_E_ARG, "vq_z_to_idx_soft: null idx");
+        return;
+    }
+    VqfWs w;
+    if (vqf_ws(vq, B, &w)) return;
+    vqf_run(vq, z, B, w.idx, NULL, NULL, soft_levels, soft_tau, rng, "vq_z_to_idx_soft");
+    mem_d2h(idx, w.idx, (size_t)B * vq->total * sizeof(int));
 }
 
 void vq_z_to_idx(VQState *vq, const float *z, int B, int *idx) {

@@ -533,6 +533,72 @@ l2sq_exact(const float *__restrict__ a, const float *__restrict__ b, float *__re
     d2[i] = exact_d2<false>(a + r * C, b + j * C, C);
 }
 
+// Soft assignment (vq.c:400-431), step 1, one thread per row of the distance
+// matrix dd [rows][V]: m = mean of the row (fp64, index order, as the
+// reference's serial loop); m > 0 gives T = tau * m, bv = the row minimum and
+// acc = sum_j exp(-(d_j - bv) / T) (index order) in st[3r..3r+2] and flag 1;
+// otherwise flag 0 (argmin, no draw).
+extern "C" __global__ void __launch_bounds__(256)
+vq_soft_stats(const float *__restrict__ dd, int rows, int V, double tau, double *__restrict__ st,
+              unsigned char *__restrict__ flag) {
+#pragma clang fp contract(off)
+    const int r = blockIdx.x * 256 + threadIdx.x;
+    if (r >= rows) return;
+    const float *d = dd + (int64_t)r * V;
+    double m = 0;
+    for (int j = 0; j < V; j++) m += (double)d[j];
+    m /= V;
+    if (!(m > 0)) {
+        flag[r] = 0;
+        return;
+    }
+    const double T = tau * m;
+    double bv = d[0];
+    for (int j = 1; j < V; j++)
+        if ((double)d[j] < bv) bv = d[j];
+    double acc = 0;
+    for (int j = 0; j < V; j++) acc += exp(-((double)d[j] - bv) / T);
+    st[3 * r] = T;
+    st[3 * r + 1] = bv;
+    st[3 * r + 2] = acc;
+    flag[r] = 1;
+}
+
+// Step 2: u[r] >= 0 is the row's uniform draw (rng >> 11) * 2^-53: the code
+// is the first j whose running sum of exp(-(d_j - bv) / T) exceeds u * acc
+// (V - 1 if none); u[r] < 0 takes the argmin (first minimum).  The code goes to
+// idx[(r / tl) * total + off + r % tl].
+extern "C" __global__ void __launch_bounds__(256)
+vq_soft_pick(const float *__restrict__ dd, int rows, int V, const double *__restrict__ st,
+             const double *__restrict__ u, int *__restrict__ idx, int tl, int total, int off) {
+#pragma clang fp contract(off)
+    const int r = blockIdx.x * 256 + threadIdx.x;
+    if (r >= rows) return;
+    const float *d = dd + (int64_t)r * V;
+    const double ur = u[r];
+    int bi = 0;
+    if (ur < 0) {
+        float bv = d[0];
+        for (int j = 1; j < V; j++)
+            if (d[j] < bv) {
+                bv = d[j];
+                bi = j;
+            }
+    } else {
+        const double T = st[3 * r], bv = st[3 * r + 1], draw = ur * st[3 * r + 2];
+        double csum = 0;
+        bi = V - 1;
+        for (int j = 0; j < V; j++) {
+            csum += exp(-((double)d[j] - bv) / T);
+            if (draw < csum) {
+                bi = j;
+                break;
+            }
+        }
+    }
+    idx[(int64_t)(r / tl) * total + off + r % tl] = bi;
+}
+
 // Residual update of one level (vq.c:476-498 with identity resampling):
 // q = E[code]; z_hat += q; z_rest -= q, in float.  On the first level z_hat
 // starts from +0.0 as the reference's memset does, so z_hat = 0.0f + q.

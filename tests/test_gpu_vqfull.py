@@ -169,3 +169,49 @@ def test_next_input_refuses_the_last_level():
             q.next_input(np.zeros((2, 16), np.int32), 2, z, 2, 16)
     finally:
         q.close()
+
+
+@pytest.mark.parametrize("name,kw", [CASES[0], CASES[2], CASES[5], CASES[8]],
+                         ids=[CASES[i][0] for i in (0, 2, 5, 8)])
+@pytest.mark.parametrize("soft_levels,tau", [(2, 0.5), (5, 0.05), (9, 2.0), (0, 0.5)])
+def test_soft_assignment_matches_oracle(name, kw, soft_levels, tau):
+    """vq_z_to_idx_soft (vq.c:388-437) through the drop-in entry point: codes
+    and the rng state after equal to the oracle's (which equals the
+    reference's own from the same seed).  soft_levels 0 is vq_z_to_idx with
+    the rng untouched."""
+    cfg, w, z = make_case(7, **kw)
+    B, seed = kw["B"], 0x9E3779B97F4A7C15
+    print(f"[gpu] vq soft case {name} levels {soft_levels} tau {tau}", flush=True)
+    want_idx, _, _, want_rng = O.vq_z_to_idx_soft(cfg, w, z, B, soft_levels, tau, seed)
+    q = DevVq(cfg, w)
+    try:
+        zd = D_.from_numpy(z)
+        idx = np.zeros((B, q.total), np.int32)
+        rng = ctypes.c_ulonglong(seed)
+        q.lib.vq_z_to_idx_soft(q.vq, zd.ptr, B, idx.ctypes.data, soft_levels, tau, ctypes.byref(rng))
+        ncmhip.check()
+        assert np.array_equal(idx, want_idx)
+        assert rng.value == want_rng
+        if soft_levels == 0:
+            assert rng.value == seed and np.array_equal(idx, O.vq_z_to_idx(cfg, w, z, B)[0])
+    finally:
+        q.close()
+
+
+def test_soft_assignment_larger_rows():
+    """2048 rows at the last level, 512 codes: every row drawn on the device,
+    the same codes and rng state as the oracle."""
+    cfg, w, z = make_case(11, B=128, levels=[1, 2, 4, 8, 16], V=512, D=64)
+    seed = 88172645463325252
+    print("[gpu] vq soft larger case", flush=True)
+    want_idx, _, _, want_rng = O.vq_z_to_idx_soft(cfg, w, z, 128, 5, 0.3, seed)
+    q = DevVq(cfg, w)
+    try:
+        zd = D_.from_numpy(z)
+        idx = np.zeros((128, q.total), np.int32)
+        rng = ctypes.c_ulonglong(seed)
+        q.lib.vq_z_to_idx_soft(q.vq, zd.ptr, 128, idx.ctypes.data, 5, 0.3, ctypes.byref(rng))
+        ncmhip.check()
+        assert np.array_equal(idx, want_idx) and rng.value == want_rng
+    finally:
+        q.close()

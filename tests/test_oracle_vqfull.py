@@ -28,6 +28,56 @@ def test_oracle_matches_reference(name, kw):
 
 
 @needs_ref
+@pytest.mark.parametrize("name,kw", [CASES[0], CASES[2], CASES[5], CASES[8]],
+                         ids=[CASES[i][0] for i in (0, 2, 5, 8)])
+@pytest.mark.parametrize("soft_levels,tau", [(2, 0.5), (5, 0.05), (9, 2.0)])
+def test_soft_assignment_matches_reference(name, kw, soft_levels, tau):
+    """vq_z_to_idx_soft (vq.c:388-437): codes, every level's z_hat and the rng
+    state after, equal to the reference's own from the same seed; the levels
+    at and above soft_levels keep the argmin codes of the same residual."""
+    cfg, w, z = make_case(7, **kw)
+    B, seed = kw["B"], 0x9E3779B97F4A7C15
+    idx, zh, zr, rng = O.vq_z_to_idx_soft(cfg, w, z, B, soft_levels, tau, seed)
+    ridx, rzh, rrng = ref_vq(cfg, w, z, B, soft=(soft_levels, tau, seed))
+    assert np.array_equal(idx, ridx) and rng == rrng
+    assert bits_equal(O.vq_idx_to_zhats(cfg, w, idx, B), rzh)
+    hard, _, _ = O.vq_z_to_idx(cfg, w, z, B)
+    n_soft = sum(cfg["levels"][:min(soft_levels, cfg["n_qlevels"])])
+    assert rng != seed and not np.array_equal(idx[:, :n_soft], hard[:, :n_soft])
+    if soft_levels < cfg["n_qlevels"]:   # the first hard level reads a residual the draws changed
+        assert idx.shape == hard.shape
+
+
+def test_soft_pick_closed_forms():
+    """One row's draw: the xorshift64 (13, 7, 17) step against its definition
+    on a known state, the two-code case against the explicit threshold, a row
+    of zeros (m = 0: no draw, rng untouched), and the empirical frequencies of
+    many draws against the tempered softmax."""
+    s = 0x0123456789ABCDEF
+    x = s
+    for sh in (13, -7, 17):
+        x = (x ^ (x << sh if sh > 0 else x >> -sh)) & (2**64 - 1)
+    d = np.array([1.0, 3.0], np.float32)
+    j, s1 = O.soft_pick(d, 0.5, s)
+    assert s1 == x
+    T = 0.5 * 2.0
+    p0 = 1.0 / (1.0 + np.exp(-2.0 / T))
+    u = (x >> 11) * 2.0**-53
+    assert j == (0 if u < p0 else 1)
+    assert O.soft_pick(np.zeros(5, np.float32), 0.5, s) == (-1, s)
+    rng = np.random.default_rng(3)
+    d = (rng.random(6) * 4).astype(np.float32)
+    T = 0.7 * float(np.mean(d.astype(np.float64)))
+    p = np.exp(-(d - d.min()) / T)
+    p /= p.sum()
+    counts, st = np.zeros(6), 12345
+    for _ in range(20000):
+        j, st = O.soft_pick(d, 0.7, st)
+        counts[j] += 1
+    assert np.allclose(counts / 20000, p, atol=0.015)
+
+
+@needs_ref
 @pytest.mark.parametrize("name,kw", CASES, ids=[c[0] for c in CASES])
 def test_next_input_and_ncm_input_match_reference(name, kw):
     cfg, w, z = make_case(7, **kw)

@@ -87,15 +87,19 @@ def host_tensor(a):
 _ref_ready = False
 
 
-def ref_vq(cfg, w, z, B):
+def ref_vq(cfg, w, z, B, soft=None):
     """The reference's own vq_load + vq_z_to_idx + vq_idx_to_zhats (CPU build):
-    returns (idx, zhats [n_levels][B][L][D])."""
+    returns (idx, zhats [n_levels][B][L][D]).  soft = (soft_levels, tau,
+    seed): the codes come from its vq_z_to_idx_soft instead, and the rng
+    state after is returned third."""
     global _ref_ready
     R = O.ref()
     if not _ref_ready:
         R.vq_load.restype = ctypes.c_void_p
         R.vq_load.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_char_p]
         R.vq_z_to_idx.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+        R.vq_z_to_idx_soft.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
+                                       ctypes.c_double, ctypes.c_void_p]
         R.vq_idx_to_zhats.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
         R.vq_free.argtypes = [ctypes.c_void_p]
         R.arena_init.argtypes = [ctypes.c_size_t]
@@ -110,13 +114,17 @@ def ref_vq(cfg, w, z, B):
     z = np.ascontiguousarray(z, np.float32)
     idx = np.zeros((B, sum(cfg["levels"][:n])), np.int32)
     R.arena_reset()
-    R.vq_z_to_idx(vq, z.ctypes.data, B, idx.ctypes.data)
+    rng = ctypes.c_ulonglong(soft[2] if soft else 0)
+    if soft:
+        R.vq_z_to_idx_soft(vq, z.ctypes.data, B, idx.ctypes.data, soft[0], soft[1], ctypes.byref(rng))
+    else:
+        R.vq_z_to_idx(vq, z.ctypes.data, B, idx.ctypes.data)
     zh = np.empty((n, B, L, D), np.float32)
     ptrs = (ctypes.c_void_p * n)(*[zh[i].ctypes.data for i in range(n)])
     R.arena_reset()
     R.vq_idx_to_zhats(vq, idx.ctypes.data, B, ptrs)
     R.vq_free(vq)
-    return idx, zh
+    return (idx, zh, rng.value) if soft else (idx, zh)
 
 
 def ref_inputs(cfg, w, idx, B):

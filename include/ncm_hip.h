@@ -641,6 +641,12 @@ void vq_z_to_idx(VQState *vq, const float *z, int B, int *idx);
  * is vq_z_to_idx) */
 void vq_z_to_idx_soft(VQState *vq, const float *z, int B, int *idx, int soft_levels, double soft_tau,
                       unsigned long long *rng);
+/* replaces vq_ema_init / vq_ema_update, ncm.h:228-229, vq.c:677-790 (training:
+ * EMA codebook maintenance; z device memory, codes host memory [B][total]; the
+ * codebooks vq_load bound are rewritten in place, as the reference's are;
+ * a code outside its level's [0, V) is NCM_E_ARG) */
+void vq_ema_init(VQState *vq);
+void vq_ema_update(VQState *vq, const float *z, const int *codes, int B, double decay, double eps);
 /* extension: vq_z_to_idx with device codes, and the final z_hat / z_rest
  * [B][L][D] (device, may be NULL); asynchronous on the library stream. */
 void vq_z_to_idx_dev(VQState *vq, const float *z, int B, int *idx, float *z_hat, float *z_rest);

@@ -561,6 +561,57 @@ void orc_vq_z_to_idx_soft(const OrcVq *q, const float *z, int B, int *idx, float
     free(up);
 }
 
+/* vq.c:697-790 vq_ema_update with the EMA state passed in (vq_ema_init,
+ * vq.c:677-695: cs[lv] = 1, w[lv] = E[lv]); codes [B][total] level-major.  Per
+ * level: the level's input rows (down-sampled z_rest), count[v] and the fp64
+ * sum over the rows holding code v, in row order; cs = (float)(decay cs + (1 -
+ * decay) count), w = (float)(decay w + (1 - decay) sum); the codebook E
+ * (rewritten in place) = (float)(w / ((cs + eps) / (n + V eps) n)), n = the
+ * sum of cs; then the residual advances with the new codebook as in
+ * vq_z_to_idx. */
+void orc_vq_ema_update(const OrcVq *q, float *const *cs, float *const *w, const float *z, const int *codes, int B,
+                       double decay, double eps) {
+    const int D = q->D, L = q->levels[q->n_levels - 1];
+    const size_t n = (size_t)B * L * D;
+    int total = 0;
+    for (int k = 0; k < q->n_levels; k++) total += q->levels[k];
+    float *zr = (float *)malloc(n * sizeof(float)), *zh = (float *)calloc(n, sizeof(float));
+    float *down = (float *)malloc(n * sizeof(float)), *up = (float *)malloc(n * sizeof(float));
+    memcpy(zr, z, n * sizeof(float));
+    int off = 0;
+    for (int lv = 0; lv < q->n_levels; lv++) {
+        const int tl = q->levels[lv], V = q->vocabs[lv], rows = B * tl;
+        orc_down(q, zr, B, lv, down);
+        double *cnt = (double *)calloc((size_t)V, sizeof(double));
+        for (int r = 0; r < rows; r++) cnt[codes[(size_t)(r / tl) * total + off + r % tl]] += 1.0;
+        for (int v = 0; v < V; v++) {
+            cs[lv][v] = (float)(decay * cs[lv][v] + (1 - decay) * cnt[v]);
+            for (int d = 0; d < D; d++) {
+                double sum = 0;
+                for (int r = 0; r < rows; r++)
+                    if (codes[(size_t)(r / tl) * total + off + r % tl] == v) sum += down[(size_t)r * D + d];
+                w[lv][(size_t)v * D + d] = (float)(decay * w[lv][(size_t)v * D + d] + (1 - decay) * sum);
+            }
+        }
+        free(cnt);
+        double nsum = 0;
+        for (int v = 0; v < V; v++) nsum += cs[lv][v];
+        float *E = (float *)q->E[lv];
+        for (int v = 0; v < V; v++) {
+            const double sm = (cs[lv][v] + eps) / (nsum + V * eps) * nsum;
+            for (int d = 0; d < D; d++) E[(size_t)v * D + d] = (float)(w[lv][(size_t)v * D + d] / sm);
+        }
+        orc_level_up(q, codes, B, lv, off, up);
+        off += tl;
+        for (size_t i = 0; i < n; i++) zh[i] += up[i];
+        for (size_t i = 0; i < n; i++) zr[i] -= up[i];
+    }
+    free(zr);
+    free(zh);
+    free(down);
+    free(up);
+}
+
 /* vq.c:378-500 vq_z_to_idx (argmin at every level) */
 void orc_vq_z_to_idx(const OrcVq *q, const float *z, int B, int *idx, float *z_hat, float *z_rest) {
     const int D = q->D, L = q->levels[q->n_levels - 1];

@@ -132,6 +132,8 @@ void orc_vq_z_to_idx(const OrcVq *q, const float *z, int B, int *idx, float *z_h
 void orc_vq_z_to_idx_soft(const OrcVq *q, const float *z, int B, int *idx, float *z_hat, float *z_rest,
                           int soft_levels, double tau, unsigned long long *rng);
 int orc_soft_pick(const float *d, int V, double tau, unsigned long long *rng);
+void orc_vq_ema_update(const OrcVq *q, float *const *cs, float *const *w, const float *z, const int *codes, int B,
+                       double decay, double eps);
 /* zhats [n_levels][B][L][D]: z_hat after each level */
 void orc_vq_idx_to_zhats(const OrcVq *q, const int *idx, int B, float *zhats);
 void orc_vq_next_input(const OrcVq *q, const int *codes, int lv, float *z_hat, float *x_out, int B);

@@ -48,6 +48,7 @@ def lib():
             "orc_vq_z_to_idx": (None, [vp, vp, ci, vp, vp, vp]),
             "orc_vq_z_to_idx_soft": (None, [vp, vp, ci, vp, vp, vp, ci, ctypes.c_double, vp]),
             "orc_soft_pick": (ci, [vp, ci, ctypes.c_double, vp]),
+            "orc_vq_ema_update": (None, [vp, vp, vp, vp, vp, ci, ctypes.c_double, ctypes.c_double]),
             "orc_vq_idx_to_zhats": (None, [vp, vp, ci, vp]),
             "orc_vq_next_input": (None, [vp, vp, ci, vp, vp, ci]),
             "orc_vq_idx_to_ncm_input": (None, [vp, vp, ci, vp]),
@@ -263,6 +264,24 @@ def vq_z_to_idx_soft(cfg, weights, z, B, soft_levels, tau, seed):
     lib().orc_vq_z_to_idx_soft(ctypes.byref(d), _ptr(z), B, _ptr(idx), _ptr(zh), _ptr(zr), soft_levels, tau,
                                ctypes.byref(rng))
     return idx, zh, zr, rng.value
+
+
+def vq_ema_update(cfg, weights, z, codes, B, decay, eps, steps=1):
+    """vq_ema_init + `steps` calls of vq_ema_update (vq.c:677-790) with the
+    same z and codes; returns (codebooks after, [n_levels] arrays), the EMA
+    counts and sums after."""
+    n = cfg["n_qlevels"]
+    w2 = {k: np.array(v, np.float32, copy=True) for k, v in weights.items()}
+    d, keep = vq_desc(cfg, w2)
+    cs = [np.ones(cfg["vq_vocab"][i], np.float32) for i in range(n)]
+    ws = [np.array(w2[f"embeddings.{i}.weight"], np.float32, copy=True) for i in range(n)]
+    csp = (vp * n)(*[a.ctypes.data for a in cs])
+    wsp = (vp * n)(*[a.ctypes.data for a in ws])
+    z = _f32(z)
+    codes = np.ascontiguousarray(codes, np.int32)
+    for _ in range(steps):
+        lib().orc_vq_ema_update(ctypes.byref(d), csp, wsp, _ptr(z), _ptr(codes), B, decay, eps)
+    return [w2[f"embeddings.{i}.weight"] for i in range(n)], cs, ws
 
 
 def soft_pick(d, tau, seed):

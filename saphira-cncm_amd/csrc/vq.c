@@ -233,6 +233,8 @@ struct VQState {
     int l1_norm, l1_norm_final;
     int has_all;
     const float *drefW[NCM_MAX_LEVELS], *drefB[NCM_MAX_LEVELS], *urefW[NCM_MAX_LEVELS], *urefB[NCM_MAX_LEVELS];
+    float *ema_cs[NCM_MAX_LEVELS];   /* host [V]: EMA code counts (vq_ema_init) */
+    float *ema_w[NCM_MAX_LEVELS];    /* device [V][D]: EMA code sums */
 };
 
 static Tensor *vq_weight(WeightStore *ws, const char *prefix, const char *name) {
@@ -373,7 +375,14 @@ fail:
     return NULL;
 }
 
-void vq_free(VQState *vq) { free(vq); }
+void vq_free(VQState *vq) {
+    if (!vq) return;
+    for (int i = 0; i < NCM_MAX_LEVELS; i++) {
+        free(vq->ema_cs[i]);
+        if (vq->ema_w[i]) ncm_hip_free(vq->ema_w[i]);
+    }
+    free(vq);
+}
 int vq_total_codes(const VQState *vq) { return vq ? vq->total : 0; }
 int vq_nlevels(const VQState *vq) { return vq ? vq->n_levels : 0; }
 int vq_level_len(const VQState *vq, int k) { return vq && k >= 0 && k < vq->n_levels ? vq->levels[k] : 0; }
@@ -567,6 +576,20 @@ static int vqf_soft(const float *down, const float *E, int *idx, int rows, int V
     return 0;
 }
 
+/* z_rest down-sampled to level lv's length into w->down (vq.c:280-330) */
+static int vqf_down(const VQState *vq, VqfWs *w, int B, int lv) {
+    const int tl = vq->levels[lv];
+    if (lv == 0 && vq->n_down > 0) {
+        if (vqf_cascade(vq, w->zr, w->down, w, B, vq->L, 0)) return 1;
+    } else {
+        if (vqf_area(w->zr, w->down, B, vq->L, tl, vq->D, tl, 0)) return 1;
+    }
+    if (vq->has_all && lv >= 1 && lv <= vq->n_levels - 2 && vq->drefW[lv] &&
+        vqf_refine(vq, w->down, vq->drefW[lv], vq->drefB[lv], w->t1, B, tl))
+        return 1;
+    return 0;
+}
+
 static void vqf_run(VQState *vq, const float *z, int B, int *idx, float *z_hat, float *z_rest, int soft_levels,
                     double tau, unsigned long long *rng, const char *fn) {
     if (vqf_check(vq, z, B, fn) || B == 0) return;
@@ -582,15 +605,7 @@ static void vqf_run(VQState *vq, const float *z, int B, int *idx, float *z_hat, 
     int off = 0;
     for (int lv = 0; lv < vq->n_levels; lv++) {
         const int tl = vq->levels[lv];
-        /* down-sample z_rest to this level (vq.c:280-330) */
-        if (lv == 0 && vq->n_down > 0) {
-            if (vqf_cascade(vq, w.zr, w.down, &w, B, L, 0)) return;
-        } else {
-            if (vqf_area(w.zr, w.down, B, L, tl, D, tl, 0)) return;
-        }
-        if (vq->has_all && lv >= 1 && lv <= vq->n_levels - 2 && vq->drefW[lv] &&
-            vqf_refine(vq, w.down, vq->drefW[lv], vq->drefB[lv], w.t1, B, tl))
-            return;
+        if (vqf_down(vq, &w, B, lv)) return;
         if (rng && lv < soft_levels && tau > 0) {
             if (vqf_soft(w.down, vq->E[lv], idx, B * tl, vq->vocabs[lv], D, tl, vq->total, off, tau, rng)) return;
         } else if (vq_search(w.down, vq->E[lv], idx, B * tl, vq->vocabs[lv], D, tl, vq->total, off, NULL)) {
@@ -621,6 +636,108 @@ void vq_z_to_idx_soft(VQState *vq, const float *z, int B, int *idx, int soft_lev
     if (vqf_ws(vq, B, &w)) return;
     vqf_run(vq, z, B, w.idx, NULL, NULL, soft_levels, soft_tau, rng, "vq_z_to_idx_soft");
     mem_d2h(idx, w.idx, (size_t)B * vq->total * sizeof(int));
+}
+
+/* vq.c:677-695: EMA counts 1 (host), EMA sums = the codebooks (device), once */
+void vq_ema_init(VQState *vq) {
+    if (!vq || ncm_ready() || vq->ema_cs[0]) return;
+    for (int i = 0; i < vq->n_levels; i++) {
+        const int V = vq->vocabs[i];
+        vq->ema_cs[i] = (float *)malloc((size_t)V * sizeof(float));
+        vq->ema_w[i] = (float *)ncm_hip_malloc((size_t)V * vq->D * sizeof(float));
+        if (!vq->ema_cs[i] || !vq->ema_w[i]) {
+            ncm_fail(NCM_E_OOM, "vq_ema_init: level %d", i);
+            return;
+        }
+        for (int v = 0; v < V; v++) vq->ema_cs[i][v] = 1.0f;
+        if (ncm_copy_async(vq->ema_w[i], vq->E[i], (size_t)V * vq->D * sizeof(float))) return;
+    }
+}
+
+/* vq.c:697-790.  codes: host [B][total] level-major, as the reference's.  Per
+ * level the host does the counts (serial, fp64), the EMA counts and the
+ * smoothing divisor per code, and lists each code's rows in row order; a
+ * kernel per (code, d) sums the code's rows in that order (fp64, the
+ * reference's order) into the EMA sums and rewrites the codebook the state
+ * was loaded with; the residual then advances with the new codebook as in
+ * vq_z_to_idx. */
+void vq_ema_update(VQState *vq, const float *z, const int *codes, int B, double decay, double eps) {
+    if (vqf_check(vq, z, B, "vq_ema_update") || B == 0) return;
+    if (!codes) {
+        ncm_fail(NCM_E_ARG, "vq_ema_update: null codes");
+        return;
+    }
+    const int total = vq->total, D = vq->D;
+    for (int lv = 0, off = 0; lv < vq->n_levels; off += vq->levels[lv], lv++)
+        for (int b = 0; b < B; b++)
+            for (int t = 0; t < vq->levels[lv]; t++) {
+                const int c = codes[(size_t)b * total + off + t];
+                if (c < 0 || c >= vq->vocabs[lv]) {
+                    ncm_fail(NCM_E_ARG, "vq_ema_update: code %d outside [0, %d) at level %d", c, vq->vocabs[lv], lv);
+                    return;
+                }
+            }
+    vq_ema_init(vq);
+    VqfWs w;
+    if (ncm_ready() || vqf_ws(vq, B, &w)) return;
+    const int64_t nL = (int64_t)B * vq->L * D;
+    mem_h2d(w.idx, codes, (size_t)B * total * sizeof(int));
+    if (ncm_ready() || ncm_copy_async(w.zr, z, (size_t)nL * sizeof(float))) return;
+    int maxV = 0;
+    for (int lv = 0; lv < vq->n_levels; lv++) maxV = vq->vocabs[lv] > maxV ? vq->vocabs[lv] : maxV;
+    const int maxrows = B * vq->L;
+    const size_t sm_b = al256((size_t)maxV * sizeof(double)), st_b = al256((size_t)(maxV + 1) * sizeof(int));
+    char *base = (char *)ncm_workspace(WS_VQSOFT, sm_b + st_b + (size_t)maxrows * sizeof(int));
+    double *smh = (double *)malloc(sm_b);
+    int *sth = (int *)malloc(st_b), *lsh = (int *)malloc((size_t)maxrows * sizeof(int));
+    double *cnt = (double *)malloc((size_t)maxV * sizeof(double));
+    if (!base || !smh || !sth || !lsh || !cnt) {
+        ncm_fail(NCM_E_OOM, "vq_ema_update: staging");
+        goto done;
+    }
+    double *smd = (double *)base;
+    int *std_ = (int *)(base + sm_b), *lsd = (int *)(base + sm_b + st_b);
+    for (int lv = 0, off = 0; lv < vq->n_levels; off += vq->levels[lv], lv++) {
+        const int tl = vq->levels[lv], V = vq->vocabs[lv], rows = B * tl;
+        if (vqf_down(vq, &w, B, lv)) goto done;
+        for (int v = 0; v < V; v++) cnt[v] = 0;
+        for (int r = 0; r < rows; r++) cnt[codes[(size_t)(r / tl) * total + off + r % tl]] += 1.0;
+        sth[0] = 0;
+        for (int v = 0; v < V; v++) sth[v + 1] = sth[v] + (int)cnt[v];
+        for (int v = 0; v < V; v++) smh[v] = sth[v];   /* fill cursors */
+        for (int r = 0; r < rows; r++) {
+            const int c = codes[(size_t)(r / tl) * total + off + r % tl];
+            lsh[(int)smh[c]] = r;
+            smh[c] += 1;
+        }
+        float *cs = vq->ema_cs[lv];
+        double nsum = 0;
+        for (int v = 0; v < V; v++) {
+            const double keep = decay * cs[v], add = (1 - decay) * cnt[v];
+            cs[v] = (float)(keep + add);
+            nsum += cs[v];
+        }
+        for (int v = 0; v < V; v++) {
+            const double a = cs[v] + eps, den = nsum + V * eps;
+            smh[v] = a / den * nsum;
+        }
+        mem_h2d(smd, smh, (size_t)V * sizeof(double));
+        mem_h2d(std_, sth, (size_t)(V + 1) * sizeof(int));
+        mem_h2d(lsd, lsh, (size_t)rows * sizeof(int));
+        float *E = (float *)vq->E[lv], *ew = vq->ema_w[lv];
+        const int64_t n = (int64_t)V * D;
+        void *a[] = {&w.down, &std_, &lsd, &smd, &ew, &E, (void *)&V, (void *)&D, &decay};
+        if (ncm_ready() || ncm_launch_named("vq_ema_codebook", grid256(n), 1, 1, 256, a)) goto done;
+        if (vqf_level_up(vq, w.idx, B, lv, off, &w)) goto done;
+        int init = lv == 0;
+        void *ua[] = {&w.zh, &w.zr, &w.up, (void *)&nL, &init};
+        if (ncm_launch_named("vqf_update", grid256(nL), 1, 1, 256, ua)) goto done;
+    }
+done:   /* (every upload above is synchronous: the host staging is free to go) */
+    free(smh);
+    free(sth);
+    free(lsh);
+    free(cnt);
 }
 
 void vq_z_to_idx(VQState *vq, const float *z, int B, int *idx) {

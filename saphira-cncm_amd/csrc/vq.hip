@@ -599,6 +599,26 @@ vq_soft_pick(const float *__restrict__ dd, int rows, int V, const double *__rest
     idx[(int64_t)(r / tl) * total + off + r % tl] = bi;
 }
 
+// EMA codebook step (vq.c:717-745), one thread per (code v, column d): the
+// fp64 sum of the level's input rows holding code v (rows listed in row order,
+// list[start[v] .. start[v + 1])), w = (float)(decay w + (1 - decay) sum), and
+// the codebook E = (float)(w / sm[v]).
+extern "C" __global__ void __launch_bounds__(256)
+vq_ema_codebook(const float *__restrict__ x, const int *__restrict__ start, const int *__restrict__ list,
+                const double *__restrict__ sm, float *__restrict__ w, float *__restrict__ E, int V, int D,
+                double decay) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)V * D) return;
+    const int v = (int)(i / D), d = (int)(i - (int64_t)v * D);
+    double sum = 0;
+    for (int k = start[v]; k < start[v + 1]; k++) sum += (double)x[(int64_t)list[k] * D + d];
+    const double keep = decay * (double)w[i], add = (1 - decay) * sum;
+    const float nw = (float)(keep + add);
+    w[i] = nw;
+    E[i] = (float)((double)nw / sm[v]);
+}
+
 // Residual update of one level (vq.c:476-498 with identity resampling):
 // q = E[code]; z_hat += q; z_rest -= q, in float.  On the first level z_hat
 // starts from +0.0 as the reference's memset does, so z_hat = 0.0f + q.

@@ -175,6 +175,8 @@ _SIGS = {
     "vq_Ddim": (ci, [vp]),
     "vq_z_to_idx": (None, [vp, vp, ci, vp]),
     "vq_z_to_idx_soft": (None, [vp, vp, ci, vp, ci, ctypes.c_double, vp]),
+    "vq_ema_init": (None, [vp]),
+    "vq_ema_update": (None, [vp, vp, vp, ci, ctypes.c_double, ctypes.c_double]),
     "vq_z_to_idx_dev": (None, [vp, vp, ci, vp, vp, vp]),
     "vq_idx_to_zhats": (None, [vp, vp, ci, ctypes.POINTER(vp)]),
     "vq_next_input": (None, [vp, vp, ci, vp, vp, ci]),

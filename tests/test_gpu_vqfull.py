@@ -215,3 +215,53 @@ def test_soft_assignment_larger_rows():
         assert np.array_equal(idx, want_idx) and rng.value == want_rng
     finally:
         q.close()
+
+
+@pytest.mark.parametrize("name,kw", [CASES[0], CASES[1], CASES[3], CASES[5], CASES[8]],
+                         ids=[CASES[i][0] for i in (0, 1, 3, 5, 8)])
+def test_ema_update_matches_oracle(name, kw):
+    """vq_ema_update (vq.c:677-790) twice in a row through the drop-in entry
+    point: every codebook the state was loaded with, rewritten in place, bit
+    for bit with the oracle's (which equals the reference's own); the codes
+    are the argmin codes of the same input."""
+    cfg, w, z = make_case(7, **kw)
+    B = kw["B"]
+    print(f"[gpu] vq ema case {name}", flush=True)
+    idx, _, _ = O.vq_z_to_idx(cfg, w, z, B)
+    want, _, _ = O.vq_ema_update(cfg, w, z, idx, B, 0.9, 1e-5, steps=2)
+    q = DevVq(cfg, w)
+    try:
+        zd = D_.from_numpy(z)
+        codes = np.ascontiguousarray(idx, np.int32)
+        for _ in range(2):
+            q.lib.vq_ema_update(q.vq, zd.ptr, codes.ctypes.data, B, 0.9, 1e-5)
+            ncmhip.check()
+        bufs = dict(zip([k for k, _ in q.tens], q.bufs))
+        for lv in range(q.n):
+            assert bits_equal(bufs[f"embeddings.{lv}.weight"].numpy(), want[lv]), lv
+        bad = codes.copy()
+        bad[0, 0] = cfg["vq_vocab"][0]
+        with pytest.raises(ncmhip.NcmError, match="vq_ema_update"):
+            q.lib.vq_ema_update(q.vq, zd.ptr, bad.ctypes.data, B, 0.9, 1e-5)
+            ncmhip.check()
+    finally:
+        q.close()
+
+
+def test_ema_update_larger_rows():
+    """128 sequences (2048 rows at the last level), 512 codes, D 64: the
+    codebooks after one update equal the oracle's."""
+    cfg, w, z = make_case(13, B=128, levels=[1, 2, 4, 8, 16], V=512, D=64)
+    print("[gpu] vq ema larger case", flush=True)
+    idx, _, _ = O.vq_z_to_idx(cfg, w, z, 128)
+    want, _, _ = O.vq_ema_update(cfg, w, z, idx, 128, 0.99, 1e-5)
+    q = DevVq(cfg, w)
+    try:
+        zd = D_.from_numpy(z)
+        q.lib.vq_ema_update(q.vq, zd.ptr, np.ascontiguousarray(idx, np.int32).ctypes.data, 128, 0.99, 1e-5)
+        ncmhip.check()
+        bufs = dict(zip([k for k, _ in q.tens], q.bufs))
+        for lv in range(q.n):
+            assert bits_equal(bufs[f"embeddings.{lv}.weight"].numpy(), want[lv]), lv
+    finally:
+        q.close()

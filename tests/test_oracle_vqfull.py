@@ -9,7 +9,7 @@ import pytest
 
 import oracle as O
 from conftest import bits_equal
-from vqfull_cases import CASES, make_case, ref_inputs, ref_vq
+from vqfull_cases import CASES, make_case, ref_inputs, ref_vq, ref_vq_ema
 
 needs_ref = pytest.mark.skipif(not O.ref_available(), reason="reference not compiled here")
 
@@ -46,6 +46,36 @@ def test_soft_assignment_matches_reference(name, kw, soft_levels, tau):
     assert rng != seed and not np.array_equal(idx[:, :n_soft], hard[:, :n_soft])
     if soft_levels < cfg["n_qlevels"]:   # the first hard level reads a residual the draws changed
         assert idx.shape == hard.shape
+
+
+@needs_ref
+@pytest.mark.parametrize("name,kw", [CASES[0], CASES[1], CASES[3], CASES[5], CASES[8]],
+                         ids=[CASES[i][0] for i in (0, 1, 3, 5, 8)])
+def test_ema_update_matches_reference(name, kw):
+    """vq_ema_init + vq_ema_update (vq.c:677-790), two calls in a row: every
+    codebook after, bit for bit with the reference's own."""
+    cfg, w, z = make_case(7, **kw)
+    B = kw["B"]
+    idx, _, _ = O.vq_z_to_idx(cfg, w, z, B)
+    want = ref_vq_ema(cfg, w, z, idx, B, 0.9, 1e-5, steps=2)
+    got, cs, _ = O.vq_ema_update(cfg, w, z, idx, B, 0.9, 1e-5, steps=2)
+    for lv in range(cfg["n_qlevels"]):
+        assert bits_equal(got[lv], want[lv]), lv
+        assert not np.array_equal(got[lv], w[f"embeddings.{lv}.weight"])
+    # counts: cs = 0.81 * 1 + 0.19 * count over the two decays (fp32 rounding twice)
+    cnt = np.bincount(idx[:, :cfg["levels"][0]].ravel(), minlength=cs[0].size)
+    c1 = np.float32(0.9 * 1.0 + 0.1 * cnt)
+    assert bits_equal(cs[0], (0.9 * c1.astype(np.float64) + 0.1 * cnt).astype(np.float32))
+
+
+def test_ema_update_decay_one_keeps_codebooks():
+    """decay 1: the sums and counts keep their cold start (w = E, cs = 1), so
+    each code becomes E / ((1 + eps) / (V + V eps) V) = E exactly."""
+    cfg, w, z = make_case(5, B=3, levels=[1, 2, 4, 8, 16], V=32, D=16)
+    idx, _, _ = O.vq_z_to_idx(cfg, w, z, 3)
+    got, _, _ = O.vq_ema_update(cfg, w, z, idx, 3, 1.0, 1e-5)
+    for lv in range(cfg["n_qlevels"]):
+        assert bits_equal(got[lv], w[f"embeddings.{lv}.weight"])
 
 
 def test_soft_pick_closed_forms():

@@ -127,6 +127,28 @@ def ref_vq(cfg, w, z, B, soft=None):
     return (idx, zh, rng.value) if soft else (idx, zh)
 
 
+def ref_vq_ema(cfg, w, z, codes, B, decay, eps, steps=1):
+    """The reference's own vq_ema_update (vq.c:697-790), `steps` calls with the
+    same z and codes, on copies of the weights: returns the codebooks after
+    (its vq_load binds them in place, vq.c:90)."""
+    ref_vq(cfg, w, z, B)   # argtypes and arena
+    R = O.ref()
+    R.vq_ema_update.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_double,
+                                ctypes.c_double]
+    arrays = {k: np.array(v, np.float32, copy=True) for k, v in w.items()}
+    tens = [(k, host_tensor(a)) for k, a in arrays.items()]
+    ws, keep = weight_store(tens)
+    c = ncm_config(cfg)
+    vq = R.vq_load(ctypes.byref(c), ctypes.byref(ws), b"")
+    z = np.ascontiguousarray(z, np.float32)
+    codes = np.ascontiguousarray(codes, np.int32)
+    for _ in range(steps):
+        R.arena_reset()
+        R.vq_ema_update(vq, z.ctypes.data, codes.ctypes.data, B, decay, eps)
+    R.vq_free(vq)
+    return [arrays[f"embeddings.{i}.weight"] for i in range(cfg["n_qlevels"])]
+
+
 def ref_inputs(cfg, w, idx, B):
     """The reference's own vq_idx_to_ncm_input and, level by level from a zero
     z_hat, vq_next_input over the same codes: returns (x [B][T][D],

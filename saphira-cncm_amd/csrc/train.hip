@@ -169,12 +169,16 @@ __device__ __forceinline__ void norm_bwd_fused_body(const float *__restrict__ x,
     const int64_t r0 = min(rbeg, rows - 1);   // a wave past the last row loads a valid row and skips the loop
     nbf_load<KIND, NPL>(x, r0, C, lane, xa);
     nbf_load<KIND, NPL>(dy, r0, C, lane, ga);
+    f4 ba[NPL];   // MODE 2: the base rows, loaded with x and dy one row ahead
+    if constexpr (MODE == 2) nbf_load<KIND, NPL>(base, r0, C, lane, ba);
     for (int64_t r = rbeg; r < rend; ++r) {
         // the next row's loads (the last row again at the end), unconditionally
         f4 xn[NPL], gn[NPL];
         const int64_t rn = r + 1 < rend ? r + 1 : r;
         nbf_load<KIND, NPL>(x, rn, C, lane, xn);
         nbf_load<KIND, NPL>(dy, rn, C, lane, gn);
+        f4 bn[NPL];
+        if constexpr (MODE == 2) nbf_load<KIND, NPL>(base, rn, C, lane, bn);
         if (KIND == 0) {
             double mean = 0.0;
 #pragma unroll
@@ -214,8 +218,7 @@ __device__ __forceinline__ void norm_bwd_fused_body(const float *__restrict__ x,
                         f4 v = f4{0.f, 0.f, 0.f, 0.f};
                         if constexpr (MODE == 1) v = *o;
                         if constexpr (MODE == 2) {
-                            const f4 bv = *(const f4 *)(base + r * C + c);
-                            v = f4{0.0f + bv.x, 0.0f + bv.y, 0.0f + bv.z, 0.0f + bv.w};
+                            v = f4{0.0f + ba[j].x, 0.0f + ba[j].y, 0.0f + ba[j].z, 0.0f + ba[j].w};
                         }
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
@@ -256,8 +259,7 @@ __device__ __forceinline__ void norm_bwd_fused_body(const float *__restrict__ x,
                         f4 v = f4{0.f, 0.f, 0.f, 0.f};
                         if constexpr (MODE == 1) v = *o;
                         if constexpr (MODE == 2) {
-                            const f4 bv = *(const f4 *)(base + r * C + c);
-                            v = f4{0.0f + bv.x, 0.0f + bv.y, 0.0f + bv.z, 0.0f + bv.w};
+                            v = f4{0.0f + ba[j].x, 0.0f + ba[j].y, 0.0f + ba[j].z, 0.0f + ba[j].w};
                         }
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
@@ -279,6 +281,7 @@ __device__ __forceinline__ void norm_bwd_fused_body(const float *__restrict__ x,
         for (int j = 0; j < NPL; ++j) {
             xa[j] = xn[j];
             ga[j] = gn[j];
+            if constexpr (MODE == 2) ba[j] = bn[j];
         }
     }
     if (!part) return;

@@ -50,6 +50,11 @@ void *ncm_hip_stream(void);
 /* Device allocation helpers for callers that do not use Tensor/arenas. */
 void *ncm_hip_malloc(size_t bytes);
 void  ncm_hip_free(void *p);
+/* Test hook (no counterpart in the reference): after n more successful
+ * ncm_hip_malloc calls, the next ones fail with NCM_E_OOM as if the device
+ * memory were exhausted; n < 0 (the default) turns it off.  Lets the tests
+ * drive the library's allocation-failure paths. */
+void  ncm_hip_fail_alloc_after(long n);
 
 /* ------------------------------------------------------------------ */
 /* tensor + memory substrate -- replaces src/tensor.c (ncm.h:27-56)     */
@@ -157,6 +162,13 @@ void rowwise_l2sq(const float *a, const float *b, float *d2,
  * Bit-exact with that reference sequence; never materialises the rows x V
  * distance matrix.  idx is a device int32 array. */
 void vq_argmin(const float *a, const float *E, int *idx, int64_t rows, int V, int D);
+/* extension for tests and profiling: with counting on, every search (of
+ * vq_argmin, vq_quantize_multiscale and the quantiser) waits for its rescore
+ * and adds up the rows the fp32 screen could not certify: those decided
+ * between two tracked codewords (pairs) and those rescored against every
+ * codeword (full).  Turning counting on or off clears the totals. */
+void ncm_vq_count_rescores(int on);
+void ncm_vq_rescore_counts(long long *pairs, long long *full);
 
 /* extension with no counterpart in the reference: vq_argmin for callers that
  * cannot allocate device memory (code under HIP graph capture, serving loops,
@@ -500,10 +512,14 @@ unsigned long long rng_next(unsigned long long *state);
 /* replaces sample_topkp, ncm.h:197-198, kernels.c:782-825: temperature,
  * top-k (0 = all) and nucleus sampling of one row.  HOST logits and rng, as
  * the reference's callers pass them (qwen.c:220-223, gpt2.c:194); the row is
- * copied to the device and sampled there (sample_topkp_dev).  temp <= 0
+ * copied to the device and sampled there (sample_topkp_dev).  When the device
+ * cannot certify its draw (flag 1 or 2 below), the draw is made again on the
+ * host from the same row and starting rng state with the reference's own
+ * steps, so the returned id and *rng are always the reference's.  temp <= 0
  * returns argmax_row and leaves *rng as it is.  V <= 262144, top_p >= 0. */
 int sample_topkp(const float *logits, int V, float temp, int top_k, float top_p, unsigned long long *rng);
-/* flag of the last sample_topkp call (see sample_topkp_dev) */
+/* device flag of the last sample_topkp call (see sample_topkp_dev); not 0
+ * means its id came from the host redraw */
 int ncm_hip_sample_flag(void);
 
 /* extension: sample_topkp on the device.  logits [V], rng (the xorshift64*
@@ -641,6 +657,10 @@ void vq_z_to_idx(VQState *vq, const float *z, int B, int *idx);
  * is vq_z_to_idx) */
 void vq_z_to_idx_soft(VQState *vq, const float *z, int B, int *idx, int soft_levels, double soft_tau,
                       unsigned long long *rng);
+/* extension: rows of the last vq_z_to_idx_soft call whose draw lay within the
+ * rounding bound of the device exp against glibc's and was therefore decided
+ * again on the host with the reference's loop and libm exp */
+int ncm_vq_soft_host_rows(void);
 /* replaces vq_ema_init / vq_ema_update, ncm.h:228-229, vq.c:677-790 (training:
  * EMA codebook maintenance; z device memory, codes host memory [B][total]; the
  * codebooks vq_load bound are rewritten in place, as the reference's are;

@@ -169,8 +169,19 @@ void *ncm_workspace(int slot, size_t bytes) {
 int ncm_cu_count(void) { return g_cus > 0 ? g_cus : 1; }
 
 /* ---- plain device allocation ---- */
+/* Test hook: after this many more successful allocations, ncm_hip_malloc
+ * fails as if the device were out of memory (< 0: never). */
+static long g_alloc_fail_after = -1;
+
+void ncm_hip_fail_alloc_after(long n) { g_alloc_fail_after = n; }
+
 void *ncm_hip_malloc(size_t bytes) {
     if (ncm_ready()) return NULL;
+    if (g_alloc_fail_after == 0) {
+        ncm_fail(NCM_E_OOM, "hipMalloc(%zu): failure injected by ncm_hip_fail_alloc_after", bytes);
+        return NULL;
+    }
+    if (g_alloc_fail_after > 0) g_alloc_fail_after--;
     void *p = NULL;
     hipError_t e = hipMalloc(&p, bytes ? bytes : 16);
     if (e != hipSuccess) {

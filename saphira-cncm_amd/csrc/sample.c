@@ -3,10 +3,13 @@
  * device.  Launch sequence per row: 4 radix passes (a digit histogram, then
  * a scatter that forms its own offsets from it), the probabilities, and the
  * one-workgroup finish: 10 launches. */
+#define _GNU_SOURCE /* qsort_r */
 #include "internal.h"
 
 #include <limits.h>
+#include <math.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #define SMP_NT 1024
@@ -177,6 +180,78 @@ static int g_last_flag = 0;
 
 int ncm_hip_sample_flag(void) { return g_last_flag; }
 
+/* Descending order of the scaled logits, comparing values only: equal values
+ * (and any pair involving a NaN) compare equal, as the reference's comparator
+ * does (kernels.c:784-789); glibc's qsort is a stable merge sort, so equal
+ * values keep their index order. */
+static int smp_cmp_desc(const void *a, const void *b, void *ctx) {
+    const float *w = (const float *)ctx;
+    const float va = w[*(const int *)a], vb = w[*(const int *)b];
+    return (va < vb) - (va > vb);
+}
+
+/* The reference's draw, recomputed on the host from the caller's row and the
+ * rng state before the device draw (kernels.c:794-825): the row divided by
+ * temp in float, the index order sorted by glibc's qsort with the comparator
+ * above, fp64 exponentials relative to the maximum over the first keep ranks
+ * and their serial sum, the nucleus cut at the first rank whose preceding
+ * mass minus its own exceeds top_p, then u = U * (the kept mass, summed
+ * again) against the running sum, U from one xorshift64* step.  Used when
+ * the device cannot certify its draw equal to this one.  Returns the id, or
+ * -1 (error recorded) when host memory runs out. */
+static int smp_host_draw(const float *logits, int V, float temp, int top_k, float top_p,
+                         unsigned long long *rng) {
+    float *w = (float *)malloc((size_t)V * sizeof *w);
+    int *ord = (int *)malloc((size_t)V * sizeof *ord);
+    double *q = (double *)malloc((size_t)V * sizeof *q);
+    if (!w || !ord || !q) {
+        free(w);
+        free(ord);
+        free(q);
+        ncm_fail(NCM_E_OOM, "sample_topkp: no host memory for the exact draw (V = %d)", V);
+        return -1;
+    }
+    for (int i = 0; i < V; i++) {
+        w[i] = logits[i] / temp;
+        ord[i] = i;
+    }
+    qsort_r(ord, (size_t)V, sizeof *ord, smp_cmp_desc, w);
+    const int keep = top_k > 0 && top_k < V ? top_k : V;
+    const double top = w[ord[0]];
+    double total = 0.0;
+    for (int r = 0; r < keep; r++) {
+        q[r] = exp((double)w[ord[r]] - top);
+        total += q[r];
+    }
+    for (int r = 0; r < keep; r++) q[r] /= total;
+    int cut = keep;
+    double before = 0.0;
+    for (int r = 0; r < keep; r++) {
+        if (before - q[r] > top_p) {
+            cut = r;
+            break;
+        }
+        before += q[r];
+    }
+    /* top_p >= 0 (checked by the caller), so rank 0 is always kept */
+    double mass = 0.0;
+    for (int r = 0; r < cut; r++) mass += q[r];
+    const double u = (double)(rng_next(rng) >> 11) * (1.0 / 9007199254740992.0) * mass;
+    int pick = ord[cut - 1];
+    double run = 0.0;
+    for (int r = 0; r < cut; r++) {
+        run += q[r];
+        if (u <= run) {
+            pick = ord[r];
+            break;
+        }
+    }
+    free(w);
+    free(ord);
+    free(q);
+    return pick;
+}
+
 int sample_topkp(const float *logits, int V, float temp, int top_k, float top_p, unsigned long long *rng) {
     g_last_flag = 0;
     if (!logits || V < 1) {
@@ -192,6 +267,7 @@ int sample_topkp(const float *logits, int V, float temp, int top_k, float top_p,
     SmpWs w;
     if (smp_ws(V, &w)) return 0;
     hipStream_t s = ncm_stream();
+    const unsigned long long rng0 = *rng;
     int res[2] = {0, 0};
     if (hipMemcpyAsync(w.row, logits, (size_t)V * 4, hipMemcpyHostToDevice, s) != hipSuccess ||
         hipMemcpyAsync(w.rng, rng, 8, hipMemcpyHostToDevice, s) != hipSuccess) {
@@ -208,12 +284,16 @@ int sample_topkp(const float *logits, int V, float temp, int top_k, float top_p,
     }
     g_last_flag = res[1];
     if (res[1] != 0) {
-        /* not certified equal to the reference's draw (a draw within the
-         * rounding bound, about 1e-10 of draws, or non-finite logits): say so
-         * instead of diverging silently; the flag stays readable through
-         * ncm_hip_sample_flag */
-        fprintf(stderr, "ncmhip: sample_topkp: draw %d not certified against the CPU reference (flag %d)\n",
-                res[0], res[1]);
+        /* the device draw is not certified equal to the reference's (u within
+         * the rounding bound of a cumulative sum, or non-finite logits): the
+         * row is host memory here, so draw again exactly as the reference
+         * does from the state the call started with (one rng step either
+         * way); the flag stays readable through ncm_hip_sample_flag */
+        unsigned long long st = rng0;
+        const int pick = smp_host_draw(logits, V, temp, top_k, top_p, &st);
+        if (pick < 0) return 0;
+        *rng = st;
+        return pick;
     }
     return res[0];
 }

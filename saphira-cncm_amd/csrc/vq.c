@@ -69,6 +69,21 @@ static int vq_scratch(VqScratch *s, int rows, int V, unsigned char *base) {
     return 0;
 }
 
+/* Rescore counting for the tests: when on, every search waits for its
+ * rescore and adds the rows that took the pair rescore and the full rescore. */
+static int g_count_rescores = 0;
+static long long g_rescore_pairs = 0, g_rescore_full = 0;
+
+void ncm_vq_count_rescores(int on) {
+    g_count_rescores = on;
+    g_rescore_pairs = g_rescore_full = 0;
+}
+
+void ncm_vq_rescore_counts(long long *pairs, long long *full) {
+    if (pairs) *pairs = g_rescore_pairs;
+    if (full) *full = g_rescore_full;
+}
+
 /* codes of `rows` rows of X against E, written at idx[(row/L)*total + off + row%L] */
 static int vq_search(const float *X, const float *E, int *idx, int rows, int V, int D, int L,
                      int total, int off, unsigned char *scratch) {
@@ -93,7 +108,12 @@ static int vq_search(const float *X, const float *E, int *idx, int rows, int V, 
         return rc;
     const unsigned *cnt = s.counters;
     void *a4[] = {&X, &E, &V, &D, &vec, &s.flags, &s.pairs, &cnt, &s.keys, &s.done, &idx, &L, &total, &off};
-    return ncm_launch_named("vq_rescore", RESCORE_GRID, 1, 1, 256, a4);
+    if ((rc = ncm_launch_named("vq_rescore", RESCORE_GRID, 1, 1, 256, a4)) || !g_count_rescores) return rc;
+    unsigned c[3];
+    mem_d2h(c, s.counters, sizeof c);
+    g_rescore_full += c[0];
+    g_rescore_pairs += c[2];
+    return ncm_ready();
 }
 
 static int vq_check(const char *fn, int64_t rows, int V, int D) {
@@ -375,12 +395,11 @@ fail:
     return NULL;
 }
 
+static void vq_ema_release(VQState *vq);
+
 void vq_free(VQState *vq) {
     if (!vq) return;
-    for (int i = 0; i < NCM_MAX_LEVELS; i++) {
-        free(vq->ema_cs[i]);
-        if (vq->ema_w[i]) ncm_hip_free(vq->ema_w[i]);
-    }
+    vq_ema_release(vq);
     free(vq);
 }
 int vq_total_codes(const VQState *vq) { return vq ? vq->total : 0; }
@@ -530,30 +549,39 @@ static int vqf_check(const VQState *vq, const float *z, int B, const char *fn) {
     return ncm_ready();
 }
 
+static int g_soft_host_rows = 0;
+
+int ncm_vq_soft_host_rows(void) { return g_soft_host_rows; }
+
 /* vq.c:400-431: the soft draws of one level's rows (B * tl of them, codes
  * into idx [B][total] at column off + t).  The distances are the reference's
  * rowwise_l2sq values; a kernel takes each row's mean, minimum and weight sum
  * (fp64, in index order, as the reference's serial loops), the host steps the
  * xorshift64 state once per row whose mean is positive, in row order, and a
- * second kernel draws (or takes the argmin where the mean is not positive). */
+ * second kernel draws (or takes the argmin where the mean is not positive).
+ * A draw the device's exp could have decided differently from glibc's (the
+ * pick kernel marks it) is decided again here with the reference's loop and
+ * libm exp, from the row's distances and the device's row statistics (the
+ * same fp64 operations as the reference's, so the same values). */
 static int vqf_soft(const float *down, const float *E, int *idx, int rows, int V, int D, int tl, int total, int off,
                     double tau, unsigned long long *rng) {
     const size_t dd_b = al256((size_t)rows * V * sizeof(float)), st_b = al256((size_t)rows * 3 * sizeof(double));
-    const size_t u_b = al256((size_t)rows * sizeof(double));
-    char *base = (char *)ncm_workspace(WS_VQSOFT, dd_b + st_b + u_b + (size_t)rows);
+    const size_t u_b = al256((size_t)rows * sizeof(double)), f_b = al256((size_t)rows);
+    char *base = (char *)ncm_workspace(WS_VQSOFT, dd_b + st_b + u_b + 2 * f_b);
     if (!base) return NCM_E_OOM;
     float *dd = (float *)base;
     double *st = (double *)(base + dd_b), *u = (double *)(base + dd_b + st_b);
-    unsigned char *flag = (unsigned char *)(base + dd_b + st_b + u_b);
+    unsigned char *flag = (unsigned char *)(base + dd_b + st_b + u_b), *near = flag + f_b;
     rowwise_l2sq(down, E, dd, rows, V, D);
     void *a[] = {&dd, &rows, &V, &tau, &st, &flag};
     if (ncm_ready() || ncm_launch_named("vq_soft_stats", grid256(rows), 1, 1, 256, a)) return ncm_ready();
     unsigned char *fh = (unsigned char *)malloc((size_t)rows);
     double *uh = (double *)malloc((size_t)rows * sizeof(double));
-    if (!fh || !uh) {
-        free(fh);
-        free(uh);
-        return ncm_fail(NCM_E_OOM, "vq_z_to_idx_soft: host draws of %d rows", rows);
+    float *row = (float *)malloc((size_t)V * sizeof(float));
+    int rc = 0;
+    if (!fh || !uh || !row) {
+        rc = ncm_fail(NCM_E_OOM, "vq_z_to_idx_soft: host draws of %d rows", rows);
+        goto done;
     }
     mem_d2h(fh, flag, (size_t)rows);
     unsigned long long x = *rng;
@@ -569,11 +597,34 @@ static int vqf_soft(const float *down, const float *E, int *idx, int rows, int V
     }
     if (!ncm_ready()) *rng = x;
     mem_h2d(u, uh, (size_t)rows * sizeof(double));
+    void *b[] = {&dd, &rows, &V, &st, &u, &idx, &tl, &total, &off, &near};
+    if ((rc = ncm_ready()) || (rc = ncm_launch_named("vq_soft_pick", grid256(rows), 1, 1, 256, b))) goto done;
+    mem_d2h(fh, near, (size_t)rows);
+    for (int r = 0; r < rows && !(rc = ncm_ready()); r++) {
+        if (!fh[r]) continue;
+        double s3[3];
+        mem_d2h(s3, st + 3 * (size_t)r, sizeof s3);
+        mem_d2h(row, dd + (size_t)r * V, (size_t)V * sizeof(float));
+        const double T = s3[0], bv = s3[1];
+        double acc = 0, csum = 0;
+        for (int j = 0; j < V; j++) acc += exp(-(row[j] - bv) / T);
+        const double draw = uh[r] * acc;
+        int bi = V - 1;
+        for (int j = 0; j < V; j++) {
+            csum += exp(-(row[j] - bv) / T);
+            if (draw < csum) {
+                bi = j;
+                break;
+            }
+        }
+        mem_h2d(idx + (size_t)(r / tl) * total + off + r % tl, &bi, sizeof bi);
+        g_soft_host_rows++;
+    }
+done:
     free(fh);
     free(uh);
-    void *b[] = {&dd, &rows, &V, &st, &u, &idx, &tl, &total, &off};
-    if (ncm_ready() || ncm_launch_named("vq_soft_pick", grid256(rows), 1, 1, 256, b)) return ncm_ready();
-    return 0;
+    free(row);
+    return rc;
 }
 
 /* z_rest down-sampled to level lv's length into w->down (vq.c:280-330) */
@@ -627,6 +678,7 @@ void vq_z_to_idx_dev(VQState *vq, const float *z, int B, int *idx, float *z_hat,
 
 void vq_z_to_idx_soft(VQState *vq, const float *z, int B, int *idx, int soft_levels, double soft_tau,
                       unsigned long long *rng) {
+    g_soft_host_rows = 0;
     if (vqf_check(vq, z, B, "vq_z_to_idx_soft") || B == 0) return;
     if (!idx) {
         ncm_fail(NCM_E_ARG, "vq_z_to_idx_soft: null idx");
@@ -638,20 +690,52 @@ void vq_z_to_idx_soft(VQState *vq, const float *z, int B, int *idx, int soft_lev
     mem_d2h(idx, w.idx, (size_t)B * vq->total * sizeof(int));
 }
 
-/* vq.c:677-695: EMA counts 1 (host), EMA sums = the codebooks (device), once */
-void vq_ema_init(VQState *vq) {
-    if (!vq || ncm_ready() || vq->ema_cs[0]) return;
+/* Frees the EMA state of every level and clears the pointers. */
+static void vq_ema_release(VQState *vq) {
+    for (int i = 0; i < NCM_MAX_LEVELS; i++) {
+        free(vq->ema_cs[i]);
+        vq->ema_cs[i] = NULL;
+        if (vq->ema_w[i]) ncm_hip_free(vq->ema_w[i]);
+        vq->ema_w[i] = NULL;
+    }
+}
+
+/* Non-zero unless every level holds its EMA counts and sums. */
+static int vq_ema_missing(const VQState *vq) {
+    for (int i = 0; i < vq->n_levels; i++)
+        if (!vq->ema_cs[i] || !vq->ema_w[i]) return 1;
+    return 0;
+}
+
+/* vq.c:677-695: EMA counts 1 (host), EMA sums = the codebooks (device), once.
+ * All or nothing: a failure at any level (allocation or copy) releases every
+ * level, so the state is either whole or absent and a later call starts
+ * again. */
+static int vq_ema_prepare(VQState *vq) {
+    int rc;
+    if ((rc = ncm_ready())) return rc;
+    if (!vq_ema_missing(vq)) return 0;
+    vq_ema_release(vq);
     for (int i = 0; i < vq->n_levels; i++) {
         const int V = vq->vocabs[i];
         vq->ema_cs[i] = (float *)malloc((size_t)V * sizeof(float));
         vq->ema_w[i] = (float *)ncm_hip_malloc((size_t)V * vq->D * sizeof(float));
         if (!vq->ema_cs[i] || !vq->ema_w[i]) {
-            ncm_fail(NCM_E_OOM, "vq_ema_init: level %d", i);
-            return;
+            rc = ncm_fail(NCM_E_OOM, "vq_ema_init: level %d", i);
+            vq_ema_release(vq);
+            return rc;
         }
         for (int v = 0; v < V; v++) vq->ema_cs[i][v] = 1.0f;
-        if (ncm_copy_async(vq->ema_w[i], vq->E[i], (size_t)V * vq->D * sizeof(float))) return;
+        if ((rc = ncm_copy_async(vq->ema_w[i], vq->E[i], (size_t)V * vq->D * sizeof(float)))) {
+            vq_ema_release(vq);
+            return rc;
+        }
     }
+    return 0;
+}
+
+void vq_ema_init(VQState *vq) {
+    if (vq) vq_ema_prepare(vq);
 }
 
 /* vq.c:697-790.  codes: host [B][total] level-major, as the reference's.  Per
@@ -677,9 +761,8 @@ void vq_ema_update(VQState *vq, const float *z, const int *codes, int B, double 
                     return;
                 }
             }
-    vq_ema_init(vq);
     VqfWs w;
-    if (ncm_ready() || vqf_ws(vq, B, &w)) return;
+    if (vq_ema_prepare(vq) || vq_ema_missing(vq) || vqf_ws(vq, B, &w)) return;
     const int64_t nL = (int64_t)B * vq->L * D;
     mem_h2d(w.idx, codes, (size_t)B * total * sizeof(int));
     if (ncm_ready() || ncm_copy_async(w.zr, z, (size_t)nL * sizeof(float))) return;

@@ -567,16 +567,24 @@ vq_soft_stats(const float *__restrict__ dd, int rows, int V, double tau, double 
 // Step 2: u[r] >= 0 is the row's uniform draw (rng >> 11) * 2^-53: the code
 // is the first j whose running sum of exp(-(d_j - bv) / T) exceeds u * acc
 // (V - 1 if none); u[r] < 0 takes the argmin (first minimum).  The code goes to
-// idx[(r / tl) * total + off + r % tl].
+// idx[(r / tl) * total + off + r % tl].  The host's exp (glibc, which the
+// reference calls) and the device's may differ by an ulp or two per term, so
+// the sums the draw is compared with are known to within
+// eta = (V + 4) 2^-50 acc (two ulps per term plus one rounding per addition,
+// doubled); near[r] = 1 marks a draw within eta of the running sum it was
+// decided on (the chosen code's or the one before), which the host then
+// decides again with its own exp.
 extern "C" __global__ void __launch_bounds__(256)
 vq_soft_pick(const float *__restrict__ dd, int rows, int V, const double *__restrict__ st,
-             const double *__restrict__ u, int *__restrict__ idx, int tl, int total, int off) {
+             const double *__restrict__ u, int *__restrict__ idx, int tl, int total, int off,
+             unsigned char *__restrict__ near) {
 #pragma clang fp contract(off)
     const int r = blockIdx.x * 256 + threadIdx.x;
     if (r >= rows) return;
     const float *d = dd + (int64_t)r * V;
     const double ur = u[r];
     int bi = 0;
+    unsigned char nr = 0;
     if (ur < 0) {
         float bv = d[0];
         for (int j = 1; j < V; j++)
@@ -585,18 +593,22 @@ vq_soft_pick(const float *__restrict__ dd, int rows, int V, const double *__rest
                 bi = j;
             }
     } else {
-        const double T = st[3 * r], bv = st[3 * r + 1], draw = ur * st[3 * r + 2];
-        double csum = 0;
+        const double T = st[3 * r], bv = st[3 * r + 1], acc = st[3 * r + 2], draw = ur * acc;
+        const double eta = (double)(V + 4) * 0x1p-50 * acc;
+        double csum = 0, prev = 0;
         bi = V - 1;
         for (int j = 0; j < V; j++) {
+            prev = csum;
             csum += exp(-((double)d[j] - bv) / T);
             if (draw < csum) {
                 bi = j;
                 break;
             }
         }
+        nr = fabs(draw - csum) <= eta || (bi > 0 && fabs(draw - prev) <= eta);
     }
     idx[(int64_t)(r / tl) * total + off + r % tl] = bi;
+    near[r] = nr;
 }
 
 // EMA codebook step (vq.c:717-745), one thread per (code v, column d): the

@@ -137,3 +137,46 @@ NCP_CASES = {
                                         query_level0=1, vocab_size=[32, 40, 48, 56]),
     "tied_codebook_puc_mha": ncp_cfg(tie_heads_to_codebook=1, puc_enabled=1, puc_kernel=3, n_kv_heads=4),
 }
+
+
+# Config 5 (BASELINE): the GPT-2-style training step, 12 layers, d 768, 12
+# heads, vocab 4096, learned positions (512), batch 32 x 512 tokens.
+C5 = dict(n_layer=12, C=768, H=12, V=4096, npos=512)
+C5_B, C5_T = 32, 512
+
+
+def gpt2_c5_weights(seed=51):
+    """Parameters in oracle.gpt2_shapes order, N(0, 0.02^2) float32 draws with
+    1.0 added to the LayerNorm gains (and to ln_f's last tensor), then token
+    ids and shifted targets uniform in [0, V)."""
+    rng = np.random.default_rng(seed)
+    shapes = O.gpt2_shapes(C5["n_layer"], C5["C"], C5["V"], C5["npos"])
+    ps = [(rng.standard_normal(s, dtype=np.float32) * np.float32(0.02)) for s in shapes]
+    for i, s in enumerate(shapes):
+        if len(s) == 1 and s[0] == C5["C"] and (i >= len(ps) - 2 or (i - 2) % 12 in (0, 6)):
+            ps[i] = ps[i] + np.float32(1.0)
+    ids = rng.integers(0, C5["V"], (C5_B, C5_T)).astype(np.int32)
+    tgt = rng.integers(0, C5["V"], (C5_B, C5_T)).astype(np.int32)
+    return ps, ids, tgt
+
+
+def grad_probe_signs(n, seed):
+    """A seeded +-1 vector of length n (float64): the probe direction of a
+    full-tensor gradient checksum sum(g * s)."""
+    rng = np.random.default_rng(seed)
+    return np.where(rng.integers(0, 2, n) == 1, 1.0, -1.0)
+
+
+# Config 3 (BASELINE): 65536 encoder vectors of dim 256, 4 residual scales of
+# 4096 codes each.
+C3 = dict(R=65536, D=256, V=4096, S=4)
+
+
+def vq_c3_inputs(seed=2026):
+    """z ~ N(0, 1) [R][D] and S codebooks ~ N(0, 1) / sqrt(D) [V][D], float32,
+    drawn in that order from one generator."""
+    rng = np.random.default_rng(seed)
+    R, D, V, S = C3["R"], C3["D"], C3["V"], C3["S"]
+    z = rng.standard_normal((R, D)).astype(np.float32)
+    Es = [(rng.standard_normal((V, D)) / np.sqrt(D)).astype(np.float32) for _ in range(S)]
+    return z, Es

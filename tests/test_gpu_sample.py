@@ -99,3 +99,63 @@ def test_non_finite_rows_are_flagged():
     x[17] = np.inf
     j, st, fl = DevSampler(x).draw(1.0, 0, 1.0, 5)
     assert fl == 2 and 0 <= j < 3000
+
+
+M64 = (1 << 64) - 1
+XS_MUL = 0x2545F4914F6CDD1D
+
+
+def state_drawing_half():
+    """An xorshift64* state whose next draw gives U = 0.5 exactly (output
+    2^63): the multiplier is inverted mod 2^64 and the three xorshift steps
+    undone in reverse order."""
+    y = (1 << 63) * pow(XS_MUL, -1, 1 << 64) & M64
+    y ^= (y >> 27) ^ (y >> 54)                                      # x ^= x >> 27
+    y = (y ^ (y << 25) ^ (y << 50)) & M64                           # x ^= x << 25
+    y ^= (y >> 12) ^ (y >> 24) ^ (y >> 36) ^ (y >> 48) ^ (y >> 60)  # x ^= x >> 12
+    return y
+
+
+def reference_draw(x, temp, k, p, st):
+    if O.ref_available():
+        return O.ref_sample_topkp(x, temp, k, p, st)
+    pytest.skip("oracle/_ref/libref.so (the reference's sampler) is not built here")
+
+
+def test_host_entry_redraws_on_a_cumulative_boundary():
+    """u lands exactly on a cumulative sum (four equal logits, U = 0.5): the
+    device cannot certify such a draw, and the host entry point must return
+    the reference's own pick and rng state."""
+    st = state_drawing_half()
+    assert (O.sample_topkp(np.zeros(4, np.float32), 1.0, 0, 1.0, st)[1] * XS_MUL & M64) >> 11 == 1 << 52
+    for V, hot in ((4, [0, 1, 2, 3]), (151936, [5, 77, 140000, 151935])):
+        x = np.full(V, -1e4, np.float32)
+        x[hot] = 3.0
+        for temp, k, p in ((1.0, 0, 1.0), (0.7, 0, 0.99), (1.0, 4, 1.0), (1.0, 1000, 0.9)):
+            want = reference_draw(x, temp, k, p, st)
+            j, s2, fl = DevSampler(x).draw(temp, k, p, st)
+            assert fl == 1 and s2 == want[1], (V, temp, k, p, fl)
+            got = ncmhip.sample_topkp(x, temp, k, p, st)
+            print(f"[gpu] boundary V={V} temp={temp} k={k} p={p}: device {j}, host entry {got[0]}, "
+                  f"reference {want[0]}", flush=True)
+            assert got == (want[0], want[1], 1), (V, temp, k, p, got, want)
+
+
+@pytest.mark.parametrize("kind", ["inf", "nan", "neg_inf_mix", "all_nan"])
+def test_host_entry_non_finite_rows_match_reference(kind):
+    rng = np.random.default_rng(17)
+    x = rng.standard_normal(3000).astype(np.float32)
+    if kind == "inf":
+        x[[17, 2500]] = np.inf
+    elif kind == "nan":
+        x[[3, 900, 2999]] = np.nan
+    elif kind == "neg_inf_mix":
+        x[[0, 1, 2]] = -np.inf
+        x[1500] = np.inf
+        x[10] = np.nan
+    else:
+        x[:] = np.nan
+    for temp, k, p, st in ((1.0, 0, 1.0, 5), (0.5, 40, 0.9, 12345), (2.0, 0, 0.0, 99)):
+        want = reference_draw(x, temp, k, p, st)
+        got = ncmhip.sample_topkp(x, temp, k, p, st)
+        assert got[:2] == want and got[2] == 2, (kind, temp, k, p, got, want)

@@ -10,7 +10,7 @@ import pytest
 import ncmhip
 import oracle as O
 from conftest import bits_equal
-from vqfull_cases import CASES, make_case, ncm_config, weight_store
+from vqfull_cases import CASES, make_case, ncm_config, ref_vq, weight_store
 
 pytestmark = pytest.mark.gpu
 D_ = ncmhip.DeviceBuffer
@@ -263,5 +263,90 @@ def test_ema_update_larger_rows():
         bufs = dict(zip([k for k, _ in q.tens], q.bufs))
         for lv in range(q.n):
             assert bits_equal(bufs[f"embeddings.{lv}.weight"].numpy(), want[lv]), lv
+    finally:
+        q.close()
+
+
+def test_ema_init_failure_leaves_no_half_state():
+    """An allocation failure at the second level of the EMA set-up releases
+    the first level too: the update reports it and changes nothing, and the
+    next update (allocations working again) builds the state whole and gives
+    the oracle's codebooks."""
+    name, kw = CASES[0]
+    cfg, w, z = make_case(7, **kw)
+    B = kw["B"]
+    print(f"[gpu] vq ema rollback on case {name}", flush=True)
+    idx, _, _ = O.vq_z_to_idx(cfg, w, z, B)
+    want, _, _ = O.vq_ema_update(cfg, w, z, idx, B, 0.9, 1e-5)
+    q = DevVq(cfg, w)
+    assert q.n >= 2
+    try:
+        zd = D_.from_numpy(z)
+        codes = np.ascontiguousarray(idx, np.int32)
+        bufs = dict(zip([k for k, _ in q.tens], q.bufs))
+        before = [bufs[f"embeddings.{lv}.weight"].numpy() for lv in range(q.n)]
+        q.lib.ncm_hip_fail_alloc_after(1)
+        try:
+            with pytest.raises(ncmhip.NcmError, match="vq_ema_init: level 1"):
+                q.lib.vq_ema_update(q.vq, zd.ptr, codes.ctypes.data, B, 0.9, 1e-5)
+                ncmhip.check()
+        finally:
+            q.lib.ncm_hip_fail_alloc_after(-1)
+        for lv in range(q.n):
+            assert bits_equal(bufs[f"embeddings.{lv}.weight"].numpy(), before[lv]), lv
+        q.lib.vq_ema_update(q.vq, zd.ptr, codes.ctypes.data, B, 0.9, 1e-5)
+        ncmhip.check()
+        for lv in range(q.n):
+            assert bits_equal(bufs[f"embeddings.{lv}.weight"].numpy(), want[lv]), lv
+    finally:
+        q.close()
+
+
+def _soft_state_drawing_half():
+    """A xorshift64 state (vq.c:425's 13/7/17 form) whose next step gives
+    u = (x >> 11) 2^-53 = 0.5 exactly: the three steps undone in reverse."""
+    m = (1 << 64) - 1
+    y = 1 << 63
+    y = (y ^ (y << 17) ^ (y << 34) ^ (y << 51)) & m
+    t = y
+    for s in range(7, 64, 7):
+        t ^= y >> s
+    y = t
+    y = (y ^ (y << 13) ^ (y << 26) ^ (y << 39) ^ (y << 52)) & m
+    x = y
+    x ^= (x << 13) & m
+    x ^= x >> 7
+    x ^= (x << 17) & m
+    assert x >> 11 == 1 << 52
+    return y
+
+
+def test_soft_draw_on_a_running_sum_is_decided_on_the_host():
+    """Codewords e_j (one-hot) and z = 0 make every level-0 distance 1.0, so
+    every weight is exp(0) = 1 and the first row's draw 0.5 * V lands exactly
+    on a running sum: the device marks it, the host decides it with glibc's
+    exp, and codes and rng state equal the oracle's and the reference's."""
+    V, D, B, levels = 16, 32, 4, [1, 2, 4]
+    cfg, w, _ = make_case(3, B=B, levels=levels, V=V, D=D)
+    w["embeddings.0.weight"] = np.eye(V, D, dtype=np.float32)
+    z = np.zeros((B, levels[-1], D), np.float32)
+    seed = _soft_state_drawing_half()
+    print("[gpu] vq soft draw on a running sum", flush=True)
+    want_idx, _, _, want_rng = O.vq_z_to_idx_soft(cfg, w, z, B, 3, 0.5, seed)
+    assert want_idx[0, 0] == V // 2
+    q = DevVq(cfg, w)
+    try:
+        zd = D_.from_numpy(z)
+        idx = np.zeros((B, q.total), np.int32)
+        rng = ctypes.c_ulonglong(seed)
+        q.lib.vq_z_to_idx_soft(q.vq, zd.ptr, B, idx.ctypes.data, 3, 0.5, ctypes.byref(rng))
+        ncmhip.check()
+        host_rows = q.lib.ncm_vq_soft_host_rows()
+        print(f"[gpu] rows decided on the host: {host_rows}", flush=True)
+        assert host_rows >= 1
+        assert np.array_equal(idx, want_idx) and rng.value == want_rng
+        if O.ref_available():
+            ridx, _, rrng = ref_vq(cfg, w, z, B, soft=(3, 0.5, seed))
+            assert np.array_equal(idx, ridx) and rng.value == rrng
     finally:
         q.close()

@@ -146,6 +146,10 @@ void linear_bwd(const float *x, const float *W, const float *dy,
  * operands, written to `kernel`; returns the number of K splits (>= 1; a
  * split count above 1 adds a fixup launch), -1 on bad arguments. */
 int ncm_hip_linear_plan(int op, int64_t batch, int M, int K, char *kernel, size_t cap);
+/* extension for tuning and tests: 64 or 128 runs every GEMM that has a
+ * kernel of that tile size (128 x 128: the vectorised ones, whole tiles) on
+ * it; 0 (the default) lets the library's cost model choose per call. */
+void ncm_hip_set_gemm_tiles(int mode);
 
 /* ------------------------------------------------------------------ */
 /* VQ nearest-codeword search                                          */

@@ -612,8 +612,9 @@ __device__ __forceinline__ void g_out_n(const GemmArgs &p, const int (&ii)[N], c
 // tot[a][b][r] holds MFMA output row 4*lg + r, column li of block (a, b).
 // Blocks of 16 consecutive rows / columns: row wm*(BM/2) + a*16 + 4*lg + r,
 // column wn*(BN/2) + b*16 + li.  Interleaved (IA / IB, the operand read from
-// an i/j-contiguous LDS slab with ds_read_b64): block a takes the rows
-// wm*32 + 2*i + a, block b the columns wn*32 + 2*j + b (64x64 tiles only).
+// an i/j-contiguous LDS slab, one read feeding every block of the wave):
+// block a takes the rows wm*(BM/2) + (BM/32)*i + a, block b the columns
+// wn*(BN/2) + (BN/32)*j + b.
 template <int BM, int BN, int EPI, int ACT, bool IA, bool IB>
 __device__ __forceinline__ void g_epilogue_act(const GemmArgs &p, const f4 (&tot)[BM / 32][BN / 32], int i0, int j0,
                                                int tid) {
@@ -629,8 +630,8 @@ __device__ __forceinline__ void g_epilogue_act(const GemmArgs &p, const f4 (&tot
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int n = (a * (BN / 32) + b) * 4 + r;
-                const int row = IA ? wm * 32 + 2 * (4 * lg + r) + a : wm * (BM / 2) + a * 16 + 4 * lg + r;
-                const int col = IB ? wn * 32 + 2 * li + b : wn * (BN / 2) + b * 16 + li;
+                const int row = IA ? wm * (BM / 2) + (BM / 32) * (4 * lg + r) + a : wm * (BM / 2) + a * 16 + 4 * lg + r;
+                const int col = IB ? wn * (BN / 2) + (BN / 32) * li + b : wn * (BN / 2) + b * 16 + li;
                 ii[n] = i0 + row;
                 jj[n] = j0 + col;
                 v[n] = tot[a][b][r];
@@ -1119,3 +1120,256 @@ GEMM_TILE_FIXUP(gemm_64x64_fixup_dxh_v, EPI_ACCUM, false, true, false, SEL_HEADS
 GEMM_TILE_FIXUP(gemm_64x64_fixup_fwd_s, EPI_STORE, false, false, false, SEL_NONE)
 GEMM_TILE_FIXUP(gemm_64x64_fixup_dx_s, EPI_ACCUM, false, false, false, SEL_NONE)
 GEMM_TILE_FIXUP(gemm_64x64_fixup_dw_s, EPI_ACCUM, false, false, false, SEL_NONE)
+
+// ---------------------------------------------------------------- GEMM, 128 x 128 tiles
+// The direct-to-LDS pipeline of gemm_dma_body on 128 x 128 tiles: each wave
+// owns a 64 x 64 sub-tile of 4 x 4 MFMA blocks, so a 16-wide chunk costs the
+// wave 8 fragment reads for 64 MFMAs (4 for 16 on 64 x 64 tiles) and the
+// operand traffic from L2 per FLOP halves.  Two stages of 32 KB: two
+// workgroups share a CU.  Used where whole tiles fill the CUs (no split-K).
+//
+// Slabs: k-contiguous [128 rows][32 k] as the 64-row slabs (pitch 32 floats,
+// float4 group g of row r in slot g ^ (r & 7)); i/j-contiguous [32 k][128
+// cols] at pitch 128 with no swizzle: a wave's fragment read at (k-row kr,
+// columns wn*64 + 4 li .. + 3) is one ds_read_b128 that feeds its four MFMA
+// blocks (block b takes column wn*64 + 4 j + b), and the 16 lanes of a
+// gfx950 ds_read_b128 service group -- {0-3, 12-15, 20-23, 24-27} or {4-7,
+// 8-11, 16-19, 28-31}, lane = 16 lg + li -- then cover the 64 banks once
+// (rows 4 lg apart start at bank 0, columns 4 li span 16 banks per lane
+// quad).
+#define BIG 128
+#define D_SLAB_BIG (BIG * GEMM_BK)
+
+template <bool KC>
+struct DSlabBig {
+    // The wave issues loads 4 * wave + e (e = 0..3) of the slab's sixteen.
+    // k-contiguous: rows 8 q .. 8 q + 7 (8 lanes per row), a row bound per
+    // load; i/j-contiguous: k-rows 2 q, 2 q + 1 (32 lanes per row), one column
+    // bound for all four loads, which sit 2 e k-rows after load 0 (so only
+    // load 0's offset and k bound are kept: registers are scarce here).
+    unsigned voff[KC ? 4 : 1];
+    int klim[KC ? 4 : 1];
+    __device__ __forceinline__ void init(int wave, int lane, int ld, int fix0, int fix_lim, int k_lim) {
+        if (KC) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = 8 * (4 * wave + e) + (lane >> 3), g = (lane & 7) ^ (r & 7);
+                voff[e] = fix0 + r < fix_lim ? (unsigned)((fix0 + r) * ld + 4 * g) * 4u : OOB_OFFSET;
+                klim[e] = k_lim - 4 * g;
+            }
+        } else {
+            const int kr = 8 * wave + (lane >> 5), c = lane & 31;
+            voff[0] = fix0 + 4 * c < fix_lim ? (unsigned)(kr * ld + fix0 + 4 * c) * 4u : OOB_OFFSET;
+            klim[0] = k_lim - kr;
+        }
+    }
+    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, float *slab, int wave, int k0, int ld) const {
+        const unsigned dk = KC ? (unsigned)k0 * 4u : (unsigned)k0 * (unsigned)ld * 4u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            unsigned off;
+            if (KC)
+                off = k0 < klim[e] ? voff[e] + dk : OOB_OFFSET;
+            else   // an out-of-range column stays beyond the buffer after the k-row step
+                off = k0 + 2 * e < klim[0] && voff[0] != OOB_OFFSET ? voff[0] + dk + (unsigned)(2 * e * ld) * 4u
+                                                                   : OOB_OFFSET;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rs, (__attribute__((address_space(3))) void *)(slab + (4 * wave + e) * 256), 16, off, 0, 0, 0);
+        }
+    }
+};
+
+// f[t][s]: the operand value of MFMA block t at step s of chunk kc, for the
+// wave's 64 rows / columns starting at w * 64.
+template <bool KC>
+__device__ __forceinline__ void d_frags_big(const float *slab, int w, int li, int lg, int kc, float (&f)[4][4]) {
+    if (KC) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int r = w * 64 + 16 * t + li;
+            const f4 v = *(const f4 *)(slab + r * GEMM_BK + 4 * ((4 * kc + lg) ^ (r & 7)));
+#pragma unroll
+            for (int s = 0; s < 4; ++s) f[t][s] = v[s];
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int kr = 16 * kc + 4 * lg + s;
+            const f4 v = *(const f4 *)(slab + kr * BIG + w * 64 + 4 * li);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) f[t][s] = v[t];
+        }
+    }
+}
+
+// The epilogue of a 128 x 128 tile, one row of MFMA blocks (16 outputs per
+// thread) at a time, so that the loaded operands of all 64 outputs are not
+// live at once.
+template <int EPI, int ACT, bool IA, bool IB>
+__device__ __forceinline__ void g_epilogue_big_act(const GemmArgs &p, const f4 (&tot)[4][4], int i0, int j0,
+                                                   int tid) {
+    const int lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
+    const int li = lane & 15, lg = lane >> 4;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+        int ii[16], jj[16];
+        float v[16];
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int n = b * 4 + r;
+                ii[n] = i0 + (IA ? wm * 64 + 4 * (4 * lg + r) + a : wm * 64 + a * 16 + 4 * lg + r);
+                jj[n] = j0 + (IB ? wn * 64 + 4 * li + b : wn * 64 + b * 16 + li);
+                v[n] = tot[a][b][r];
+            }
+        g_out_n<16, ACT, EPI>(p, ii, jj, v);
+    }
+}
+
+template <int EPI, bool IA, bool IB>
+__device__ __forceinline__ void g_epilogue_big(const GemmArgs &p, const f4 (&tot)[4][4], int i0, int j0, int tid) {
+    if (EPI == EPI_ACCUM || EPI == EPI_ACT_BWD) {
+        g_epilogue_big_act<EPI, ACT_NONE, IA, IB>(p, tot, i0, j0, tid);
+        return;
+    }
+    switch (p.act) {
+    case ACT_SILU: g_epilogue_big_act<EPI, ACT_SILU, IA, IB>(p, tot, i0, j0, tid); break;
+    case ACT_GELU: g_epilogue_big_act<EPI, ACT_GELU, IA, IB>(p, tot, i0, j0, tid); break;
+    case ACT_GELU_TANH: g_epilogue_big_act<EPI, ACT_GELU_TANH, IA, IB>(p, tot, i0, j0, tid); break;
+    case ACT_RELU2: g_epilogue_big_act<EPI, ACT_RELU2, IA, IB>(p, tot, i0, j0, tid); break;
+    default: g_epilogue_big_act<EPI, ACT_NONE, IA, IB>(p, tot, i0, j0, tid); break;
+    }
+}
+
+// Whole 128 x 128 tiles (blockIdx.x = tile; dp_tiles = all tiles).  DB: the
+// dW kernel that also sums the bias gradient; SEL_HEADS: each wave's 64
+// output columns lie in one head and its 128 rows in one sequence (T a
+// multiple of 128), so the wave stores into that head's [128 t][64 d] block.
+template <bool AKC, bool BKC, int EPI, bool DB = false, int SEL = SEL_NONE>
+__device__ __forceinline__ void gemm_big_body(const GemmArgs &pa) {
+    __shared__ __attribute__((aligned(16))) float sm[2 * 2 * D_SLAB_BIG];   // [stage][A | B]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1, li = lane & 15, lg = lane >> 4;
+    const int tile = xcd_remap(blockIdx.x, pa.tiles_m * pa.tiles_n);
+    int tm, tn;
+    tile_rc<8>(tile, pa.tiles_m, pa.tiles_n, tm, tn);
+    const int i0 = tm * BIG, j0 = tn * BIG;
+    GemmArgs pl = pa;
+    if (SEL == SEL_HEADS) heads_select(pa, pl, i0, j0 + wn * 64);
+    const GemmArgs &p = SEL != SEL_NONE ? pl : pa;
+    const int kend = p.K;
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, p.a_bytes), rb = make_rsrc(p.B, p.b_bytes);
+    DSlabBig<AKC> la;
+    DSlabBig<BKC> lb;
+    la.init(wave, lane, p.lda, i0, p.Mo, kend);
+    lb.init(wave, lane, p.ldb, j0, p.No, kend);
+
+    f4 acc[4][4], tot[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = tot[a][b] = f4{0.f, 0.f, 0.f, 0.f};
+    auto mfmas = [&](const float (&fa)[4][4], const float (&fb)[4][4]) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int b = 0; b < 4; ++b) acc[a][b] = mfma4(fa[a][s], fb[b][s], acc[a][b]);
+    };
+    // dW with the bias gradient: A(i,k) = dy[k][i], so the tiles of tile
+    // column 0 also sum each A slab over k in fp64, straight from LDS while
+    // the slab is current: thread t takes tile row t & 127 and the slab's k
+    // rows 16 (t >> 7) .. + 15 (consecutive lanes, consecutive banks); the
+    // two halves are added at the end.  (Summing the MFMA fragments in
+    // registers, as the 64 x 64 kernel does, spilled at this tile size.)
+    const bool dsum = DB && p.db != nullptr && tn == 0;
+    double ds = 0.0;
+    float *const sA0 = sm, *const sB0 = sm + D_SLAB_BIG, *const sA1 = sm + 2 * D_SLAB_BIG,
+                 *const sB1 = sm + 3 * D_SLAB_BIG;
+    const int iters = p.iters;
+
+    float f0a[4][4], f0b[4][4], f1a[4][4], f1b[4][4];
+    la.load(ra, sA0, wave, 0, p.lda);
+    lb.load(rb, sB0, wave, 0, p.ldb);
+    __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
+    __syncthreads();
+    d_frags_big<AKC>(sA0, wm, li, lg, 0, f0a);
+    d_frags_big<BKC>(sB0, wn, li, lg, 0, f0b);
+    la.load(ra, sA1, wave, GEMM_BK, p.lda);
+    lb.load(rb, sB1, wave, GEMM_BK, p.ldb);
+    auto kloop = [&](auto ds_tag) {
+        constexpr bool DS = decltype(ds_tag)::value;
+        auto colsum = [&](const float *slab) {
+            if constexpr (DS) {
+                const float *q = slab + 16 * (tid >> 7) * BIG + (tid & 127);
+#pragma unroll
+                for (int k = 0; k < 16; ++k) ds += (double)q[k * BIG];
+            }
+        };
+        for (int kt = 0; kt < iters; kt += 4) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                float *const ca = (u & 1) ? sA1 : sA0, *const cb = (u & 1) ? sB1 : sB0;
+                float *const na = (u & 1) ? sA0 : sA1, *const nb = (u & 1) ? sB0 : sB1;
+                d_frags_big<AKC>(ca, wm, li, lg, 1, f1a);
+                d_frags_big<BKC>(cb, wn, li, lg, 1, f1b);
+                colsum(ca);
+                __builtin_amdgcn_sched_barrier(0);
+                mfmas(f0a, f0b);
+                __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's loads of slab kt+u+1
+                __syncthreads();
+                d_frags_big<AKC>(na, wm, li, lg, 0, f0a);
+                d_frags_big<BKC>(nb, wn, li, lg, 0, f0b);
+                __builtin_amdgcn_sched_barrier(0);
+                la.load(ra, ca, wave, (kt + u + 2) * GEMM_BK, p.lda);
+                lb.load(rb, cb, wave, (kt + u + 2) * GEMM_BK, p.ldb);
+                __builtin_amdgcn_sched_barrier(0);
+                mfmas(f1a, f1b);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    tot[a][b] += acc[a][b];
+                    acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
+                }
+        }
+    };
+    if (dsum)
+        kloop(BoolTag<DB>{});
+    else
+        kloop(BoolTag<false>{});
+    // No load may still be writing LDS when the workgroup ends.
+    __builtin_amdgcn_s_waitcnt(0x0f70);
+    if (dsum) {
+        __syncthreads();   // every wave is done with the slabs: reuse the LDS
+        double *half = (double *)sm;
+        if (tid >= 128) half[tid - 128] = ds;
+        __syncthreads();
+        if (tid < 128) {
+            // a row past Mo reads the clamped address and writes nothing
+            const double d = ds + half[tid];
+            const int i = min(i0 + tid, p.Mo - 1);
+            const float old = p.db[i];
+            if (i0 + tid < p.Mo) p.db[i] = old + (0.0f + (float)d);
+        }
+    }
+    g_epilogue_big<EPI, !AKC, !BKC>(p, tot, i0, j0, tid);
+}
+
+#define GEMM_BIG_KERNEL(name, AKC, BKC, EPI, DB, SEL)                                                   \
+    extern "C" __global__ void __launch_bounds__(GEMM_NT) __attribute__((amdgpu_waves_per_eu(2)))      \
+        name(GemmArgs p) {                                                                             \
+        gemm_big_body<AKC, BKC, EPI, DB, SEL>(p);                                                      \
+    }
+GEMM_BIG_KERNEL(gemm_128x128_fwd_v, true, true, EPI_STORE, false, SEL_NONE)
+GEMM_BIG_KERNEL(gemm_128x128_fwdh_v, true, true, EPI_STORE, false, SEL_HEADS)
+GEMM_BIG_KERNEL(gemm_128x128_dx_v, true, false, EPI_ACCUM, false, SEL_NONE)
+GEMM_BIG_KERNEL(gemm_128x128_dw_v, false, false, EPI_ACCUM, false, SEL_NONE)
+GEMM_BIG_KERNEL(gemm_128x128_dwb_v, false, false, EPI_ACCUM, true, SEL_NONE)
+GEMM_BIG_KERNEL(gemm_128x128_dxa_v, true, false, EPI_ACT_BWD, false, SEL_NONE)
+GEMM_BIG_KERNEL(gemm_128x128_dxh_v, true, false, EPI_ACCUM, false, SEL_HEADS)

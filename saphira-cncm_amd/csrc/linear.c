@@ -77,6 +77,7 @@ static void gemm_name(int bm, int bn, int kind, int vec, char *out, size_t cap) 
  * groups of 4 slabs) whose partial tiles a fixup launch sums. */
 typedef struct {
     int tiles_m, tiles_n, iters, dp_tiles, segs, blocks;
+    double cost;   /* the cost model's makespan, in slabs of a 64 x 64 tile */
 } GemmPlan;
 
 /* CU makespan, in slabs, of list-scheduling dp units of I slabs and then n2
@@ -138,6 +139,7 @@ static GemmPlan plan_gemm_uncached(int Mo, int No, int Kred, int slots, int bm, 
         }
     }
     g.blocks = g.dp_tiles + (T - g.dp_tiles) * g.segs;
+    g.cost = best;
     return g;
 }
 
@@ -181,9 +183,64 @@ static int gemm_slots(const char *name) {
 /* Bytes spanned by a rows x cols row-major operand with row stride ld. */
 static int64_t extent(int64_t rows, int64_t cols, int64_t ld) { return ((rows - 1) * ld + cols) * 4; }
 
-/* Tile shape of every GEMM: 64 x 64 (gemm.hip instantiates only this one). */
+/* Tile shapes: 64 x 64 (every kernel, split-K capable) and 128 x 128 (whole
+ * tiles only, the vectorised plain / dW+db / dX-through-activation / head-major
+ * kernels), chosen per call by the cost model below. */
 #define TILE_M 64
 #define TILE_N 64
+#define BIG_TILE 128
+/* Timing model of the two tile sizes on MI355X, fitted to forward launches
+ * of 8192 x 1024 outputs (512 tiles of 128 x 128: one pair per CU) at K =
+ * 256 .. 4096 with operands rotated through three copies: a 64 x 64 plan's
+ * cost-model slabs take ~0.586 us each plus ~22 us per launch; a pair of
+ * 128 x 128 tiles of W slab units each (one unit = one slab of 64 x 64 work)
+ * takes 2 W 0.434 + 71.6 us -- near the MFMA peak per slab, but with a large
+ * fixed cost per tile (start-up and epilogue are not hidden behind other
+ * workgroups at two per CU) -- and a tile alone on its CU (one workgroup per
+ * CU) is taken as W 0.6 + 60 us.  So the big tiles pay only for long K (about
+ * K >= 2048) with CUs holding whole pairs; in the training step's context
+ * (cold operands, activation epilogues) they measured 3-12% slower at K = 768
+ * .. 3072. */
+#define U64_US 0.586
+#define U64_FIXED_US 22.0
+#define PAIR_US 0.434
+#define PAIR_FIXED_US 71.6
+#define SINGLE_US 0.6
+#define SINGLE_FIXED_US 60.0
+/* 0: cost model; 64 / 128: that tile wherever it applies.  The environment
+ * variable NCM_GEMM_TILES sets the starting mode (for tuning runs). */
+static int g_tile_mode = -1;
+
+void ncm_hip_set_gemm_tiles(int mode) { g_tile_mode = mode == 64 || mode == 128 ? mode : 0; }
+
+static int tile_mode(void) {
+    if (g_tile_mode < 0) {
+        const char *e = getenv("NCM_GEMM_TILES");
+        ncm_hip_set_gemm_tiles(e ? atoi(e) : 0);
+    }
+    return g_tile_mode;
+}
+
+/* Whether the 128 x 128 kernel of op runs this GEMM: it exists for the
+ * vectorised plain, dwb, dxa and head-major products, needs whole rows of
+ * tiles within one sequence for the head-major ones, and is chosen when its
+ * whole-tile makespan beats the 64 x 64 plan's (or when forced). */
+static int use_big(const char *op, int vec, int Mo, int No, int Kred, int hm_T, double cost64, int slots64) {
+    const int mode = tile_mode();
+    if (!vec || mode == 64 || strcmp(op, "fwd3") == 0) return 0;
+    if ((strcmp(op, "fwdh") == 0 || strcmp(op, "dxh") == 0) && hm_T % BIG_TILE != 0) return 0;
+    const int64_t T = (int64_t)((Mo + BIG_TILE - 1) / BIG_TILE) * ((No + BIG_TILE - 1) / BIG_TILE);
+    if (T > INT_MAX / 4) return 0;
+    if (mode == 128) return 1;
+    (void)slots64;
+    const int groups = Kred > 0 ? (Kred + 4 * BK - 1) / (4 * BK) : 1;
+    const int C = ncm_cu_count();
+    const int64_t n = (T + C - 1) / C;             /* tiles on the busiest CU */
+    const double W = 16.0 * groups;                /* 64 x 64 slab units per 128 x 128 tile */
+    const double big_us = (double)(n / 2) * (2 * W * PAIR_US + PAIR_FIXED_US) +
+                          (double)(n % 2) * (W * SINGLE_US + SINGLE_FIXED_US);
+    return big_us < 0.92 * (cost64 * U64_US + U64_FIXED_US);   /* only a clear win */
+}
 
 /* Optional parts of a GEMM launch (NULL for a plain one; vectorised kernels
  * only). */
@@ -222,6 +279,14 @@ static int run_gemm_x(int kind, const float *A, const float *B, float *C, const 
     int slots = gemm_slots(name);
     if (slots < 0) return NCM_E_INIT;
     GemmPlan g = plan_gemm(Mo, No, Kred, slots, bm, bn);
+    int big = use_big(op, vec, Mo, No, Kred, ex->hm_T, g.cost, slots);
+    if (big) {
+        snprintf(name, sizeof name, "gemm_%dx%d_%s_v", BIG_TILE, BIG_TILE, op);
+        g.tiles_m = (Mo + BIG_TILE - 1) / BIG_TILE;
+        g.tiles_n = (No + BIG_TILE - 1) / BIG_TILE;
+        g.dp_tiles = g.blocks = g.tiles_m * g.tiles_n;
+        g.segs = 1;
+    }
     /* operand extents as stored: A is [Mo][Kred] (k-contiguous) or [Kred][Mo] */
     int64_t ab = kind == L_DW ? extent(Kred, Mo, lda) : extent(Mo, Kred, lda);
     int64_t bb = kind == L_FWD ? extent(No, Kred, ldb) : extent(Kred, No, ldb);
@@ -648,5 +713,10 @@ int ncm_hip_linear_plan(int op, int64_t batch, int M, int K, char *kernel, size_
     int slots = gemm_slots(kernel);
     if (slots < 0) return -1;
     GemmPlan g = plan_gemm(Mo, No, Kred, slots, bm, bn);
+    const char *op_name = with_db && vec ? "dwb" : kind_names[op];
+    if (use_big(op_name, vec, Mo, No, Kred, 0, g.cost, slots)) {
+        snprintf(kernel, cap, "gemm_%dx%d_%s_v", BIG_TILE, BIG_TILE, op_name);
+        return 1;
+    }
     return g.segs;
 }

@@ -800,10 +800,13 @@ sdpa_decode_partial(const float *__restrict__ q, const float *__restrict__ kc, c
     __syncthreads();
     // o[j][d] = sum_key p[j][key] v[key][d]: wave w, queries w, w+4, ...; lane = d
     for (int j = wave; j < rep; j += 4) {
-        float o = 0.f;
-#pragma unroll 8
-        for (int t = 0; t < DEC_CH; ++t) o += sP[j * DEC_CH + t] * sV[t * 64 + lane];
-        part_o[((int64_t)(h0 + j) * nchunk + chunk) * 64 + lane] = o;
+        // four independent chains (keys t = 4 i + u), added at the end
+        float o4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+        for (int t = 0; t < DEC_CH; t += 4)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) o4[u] += sP[j * DEC_CH + t + u] * sV[(t + u) * 64 + lane];
+        part_o[((int64_t)(h0 + j) * nchunk + chunk) * 64 + lane] = (o4[0] + o4[1]) + (o4[2] + o4[3]);
     }
 }
 
@@ -1115,6 +1118,67 @@ DEC_GEMV(dec_gemv_d1_r1_p8_x8, 1, 8, 1, 8)
 DEC_GEMV(dec_gemv_d2_r1_p4_x1, 1, 4, 2, 1)
 DEC_GEMV(dec_gemv_d2_r2_p4_x1, 2, 4, 2, 1)
 DEC_GEMV(dec_gemv_d2_r1_p8_x8, 1, 8, 2, 8)
+
+// ---------------------------------------------------------------- decode GEMV, workgroup per row pair
+// For the decode products with too few rows to give every CU a wave per row
+// (the o-projection and the down projection: 896 rows of 896 or 4864), a
+// workgroup owns R rows and its 256 threads split K: thread t holds float4
+// t + 256 e of the input in registers and multiplies it with the same float4
+// of each of its rows; the 256 partial dot products are added by a wave
+// reduction and then, across the four waves in order, through LDS.  The
+// input never goes through LDS, and all of a thread's loads are issued
+// before the first wait (input, weight rows, then the epilogue's bias and
+// residual).  y[n] = res[n] + (W x)[n] (+ bias), dec_gemv's mode 0 over one
+// matrix.  K % 4 == 0, K <= 1024 XPT.  (A wave per row, as dec_gemv_body
+// streams it, leaves a quarter of the CUs idle at 896 rows.)
+template <int R, int XPT>
+__device__ __forceinline__ void dec_wg_body(const DecGemvArgs &p) {
+#pragma clang fp contract(off)
+    __shared__ float red[4][R];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int K = p.K, K4 = K >> 2, N = p.N[0];
+    const int n0 = blockIdx.x * R;
+    f4 xv[XPT];
+#pragma unroll
+    for (int e = 0; e < XPT; ++e) xv[e] = *(const f4 *)(p.x + 4 * min(tid + 256 * e, K4 - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    f4 w[R][XPT];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int e = 0; e < XPT; ++e)
+            w[r][e] = __builtin_nontemporal_load((const f4 *)(p.W[0] + (int64_t)min(n0 + r, N - 1) * K) +
+                                                 min(tid + 256 * e, K4 - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    // the epilogue's values (used by threads r < R; a stand-in address when absent)
+    const int nr = min(n0 + min(tid, R - 1), N - 1);
+    const float eb = *(p.b[0] ? p.b[0] + nr : p.x), er = *(p.res ? p.res + nr : p.x);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int e = 0; e < XPT; ++e)
+        if (tid + 256 * e >= K4) xv[e] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float a = 0.f;
+#pragma unroll
+        for (int e = 0; e < XPT; ++e)
+            a += (w[r][e].x * xv[e].x + w[r][e].y * xv[e].y) + (w[r][e].z * xv[e].z + w[r][e].w * xv[e].w);
+        a = wave_sum(a);
+        if (lane == 0) red[wave][r] = a;
+    }
+    __syncthreads();
+    if (tid >= R || n0 + tid >= N) return;
+    float v = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
+    if (p.b[0]) v += eb;
+    if (p.res) v = er + v;
+    p.y[0][n0 + tid] = v;
+}
+
+// r<R> rows per workgroup, x<XPT> input float4 per thread (K <= 1024 XPT)
+#define DEC_WG(name, R, XPT) \
+    extern "C" __global__ void __launch_bounds__(256) name(DecGemvArgs p) { dec_wg_body<R, XPT>(p); }
+DEC_WG(dec_wg_plain_r2_x1, 2, 1)   // o-projection + residual (K <= 1024)
+DEC_WG(dec_wg_plain_r2_x5, 2, 5)   // down projection + residual (K <= 5120)
 
 // Position-driven pieces of a decode step, so that the step's launches do
 // not change from one token to the next (it can be replayed as one graph):

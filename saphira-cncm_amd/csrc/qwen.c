@@ -330,7 +330,15 @@ static int decode_core(NcmQwen *m) {
             void *a2[] = {&m->part_o, &m->part_ml, &m->ctx, &stride, &m->pos_dev};
             if (ncm_launch_named("sdpa_decode_combine", (unsigned)H, 1, 1, 64, a2)) return -1;
         }
-        {   /* x1 = x + o_proj(ctx)   (ctx [H][hd] is the merged row) */
+        if (C <= 1024) {   /* x1 = x + o_proj(ctx) (ctx [H][hd] is the merged row): a workgroup per
+                            * two rows, K split over its threads */
+            DecGemvArgs a;
+            memset(&a, 0, sizeof(a));
+            a.x = m->ctx; a.res = m->x; a.K = C; a.mode = 0;
+            a.W[0] = w[7]; a.y[0] = m->x1; a.N[0] = C;
+            void *args[] = {&a};
+            if (ncm_launch_named("dec_wg_plain_r2_x1", (unsigned)((C + 1) / 2), 1, 1, 256, args)) return -1;
+        } else {
             const float *W[1] = {w[7]}, *b[1] = {NULL};
             float *y[1] = {m->x1};
             int N[1] = {C};
@@ -342,7 +350,14 @@ static int decode_core(NcmQwen *m) {
             int N[2] = {I, I};
             if (dec_gemv(m->x1, w[8], NULL, 2, W, b, y, N, C, 1)) return -1;
         }
-        {   /* x = x1 + down(gu) */
+        if (I <= 5120) {   /* x = x1 + down(gu): a workgroup per two rows, K split over its threads */
+            DecGemvArgs a;
+            memset(&a, 0, sizeof(a));
+            a.x = m->up; a.res = m->x1; a.K = I; a.mode = 0;
+            a.W[0] = w[11]; a.y[0] = m->x; a.N[0] = C;
+            void *args[] = {&a};
+            if (ncm_launch_named("dec_wg_plain_r2_x5", (unsigned)((C + 1) / 2), 1, 1, 256, args)) return -1;
+        } else {
             const float *W[1] = {w[11]}, *b[1] = {NULL};
             float *y[1] = {m->x};
             int N[1] = {C};

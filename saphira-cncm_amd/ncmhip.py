@@ -35,6 +35,7 @@ _SIGS = {
     "ncm_hip_free": (None, [vp]),
     "ncm_hip_fail_alloc_after": (None, [ctypes.c_long]),
     "ncm_vq_soft_host_rows": (ci, []),
+    "ncm_hip_set_gemm_tiles": (None, [ci]),
     "ncm_vq_count_rescores": (None, [ci]),
     "ncm_vq_rescore_counts": (None, [ctypes.POINTER(ctypes.c_longlong), ctypes.POINTER(ctypes.c_longlong)]),
     "tensor_alloc": (vp, [ci, ctypes.POINTER(i64)]),

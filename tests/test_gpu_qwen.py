@@ -235,3 +235,30 @@ def test_sampled_generation_draws_match_oracle(temp, top_k, top_p, monkeypatch):
         assert m.generate_sample(prompt, 4, 0.0, top_k, top_p, seed)[:2] == (m.generate(prompt, 4), seed)
     finally:
         m.close()
+
+
+@pytest.mark.parametrize("H,K", [(8, 2), (4, 4), (16, 1)])
+def test_decode_shapes_vs_oracle(H, K):
+    """The cached decode step (64-key attention chunks and their merge, the
+    workgroup-per-row-pair o and down projections) at other head counts and
+    GQA ratios (4, 1 and 16) and context lengths that leave a chunk partly
+    filled, end one exactly and open the next, against the oracle's full
+    forward over the extended sequence."""
+    cfg = dict(n_layer=2, C=64 * H, H=H, K=K, I=512, V=500)
+    params = weights(9, **cfg)
+    rng = np.random.default_rng(10)
+    m = Model(params, n_ctx=1100, theta=1e6, **cfg)
+    try:
+        for np_ in (70, 127, 640):
+            ids = list(rng.integers(0, cfg["V"], np_ + 3))
+            m.forward(np.array(ids[:np_], np.int32), last_only=True)
+            for s in range(3):
+                pos = np_ + s
+                got = m.decode(ids[pos], pos)
+                ref = O.qwen_forward(params, theta=1e6, ids=np.array(ids[:pos + 1], np.int32), last_only=True,
+                                     **cfg)
+                err = float(np.max(np.abs(got - ref.reshape(-1))))
+                print(f"[gpu] H={H} K={K} pos={pos}: logits max-abs {err:.2e}", flush=True)
+                assert err <= 1e-3, (pos, err)
+    finally:
+        m.close()

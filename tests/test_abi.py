@@ -23,6 +23,20 @@ def test_exports_every_declared_symbol():
     assert sorted(ncmhip._SIGS) == sorted(declared)
 
 
+def test_tape_library_exports_the_reference_prototypes():
+    """libncmhip_tape.so exports every function include/ncm_hip_tape.h
+    declares (the reference's tape names, ncm.h:192-195, 468-522), each one
+    resolved against libncmhip.so."""
+    import re
+    header = open(os.path.join(os.path.dirname(ncmhip.HERE), "include", "ncm_hip_tape.h")).read()
+    header = re.sub(r"/\*.*?\*/", "", header, flags=re.S)
+    declared = re.findall(r"^[A-Za-z_][\w \*]*?\b(\w+)\s*\(", header, flags=re.M)
+    assert {"tape_new", "t_linear", "t_ce", "tape_backward", "t_qkvsplit"} <= set(declared)
+    lib = ctypes.CDLL(os.path.join(ncmhip.HERE, "libncmhip_tape.so"))
+    missing = [n for n in declared if not hasattr(lib, n)]
+    assert not missing, missing
+
+
 def test_bad_arguments_are_errors_not_exits():
     ncmhip.load()
     with pytest.raises(ncmhip.NcmError, match="bad shape"):

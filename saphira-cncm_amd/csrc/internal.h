@@ -127,6 +127,10 @@ int ncm_conv1d_btd(const float *x, const float *W, const float *b, float *y, int
  * (the values of sdpa_fwd_gqa_causal followed by head_merge_fwd). */
 void ncm_sdpa_fwd_causal_merged(const float *q, const float *k, const float *v, float *out, int B, int Hq, int Hkv,
                                 int Tq, int Tkv, int hd);
+/* sdpa_fwd_gqa_merged with one [Tq][Tkv] mask per board (board b's at
+ * masks + b Tq Tkv). */
+void ncm_sdpa_fwd_gqa_merged_bmask(const float *q, const float *k, const float *v, const float *masks, float *out,
+                                   int B, int Hq, int Hkv, int Tq, int Tkv, int hd);
 /* ncm_sdpa_fwd_stats with the heads merged on output: out [B][Tq][Hq hd]. */
 void ncm_sdpa_fwd_stats_merged(const float *q, const float *k, const float *v, const float *mask, float *out,
                                float *stats, int B, int Hq, int Hkv, int Tq, int Tkv, int hd, int causal);

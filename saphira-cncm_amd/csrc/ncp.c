@@ -193,7 +193,6 @@ struct NCPState {
     float *lvl_pos;             /* [T][C] */
     float *mask;                /* [S][S] without pads */
     int *lvl;                   /* [T] level of each target row */
-    int *pad;                   /* [P] pad flags of one board */
     NcpLayer *layer;
     NcpHead head[NCM_MAX_LEVELS];
 };
@@ -254,7 +253,6 @@ void ncp_free(NCPState *m) {
     ncm_hip_free(m->lvl_pos);
     ncm_hip_free(m->mask);
     ncm_hip_free(m->lvl);
-    ncm_hip_free(m->pad);
     free(m->layer);
     free(m);
 }
@@ -467,9 +465,8 @@ NCPState *ncp_load(const NCMConfig *c, WeightStore *ws, VQVAEState *vqvae) {
         m->lvl_pos = (float *)ncm_hip_malloc((size_t)(T > 0 ? T : 1) * C * sizeof(float));
         m->lvl = (int *)ncm_hip_malloc((size_t)(T > 0 ? T : 1) * sizeof(int));
         m->mask = (float *)ncm_hip_malloc((size_t)S * S * sizeof(float));
-        m->pad = (int *)ncm_hip_malloc((size_t)(P > 0 ? P : 1) * sizeof(int));
         int *ldev = (int *)ncm_hip_malloc((size_t)(T > 0 ? T : 1) * sizeof(int));
-        if (!m->lvl_pos || !m->lvl || !m->mask || !m->pad || !ldev) err = err ? err : NCM_E_OOM;
+        if (!m->lvl_pos || !m->lvl || !m->mask || !ldev) err = err ? err : NCM_E_OOM;
         if (!err) {
             int *rel = (int *)malloc((size_t)(T > 0 ? T : 1) * sizeof(int));
             for (int t = 0; rel && t < T; t++) rel[t] = lvl[t] - m->lvl_first;
@@ -493,8 +490,8 @@ NCPState *ncp_load(const NCMConfig *c, WeightStore *ws, VQVAEState *vqvae) {
         }
         if (!err) {
             const int *nopad = NULL;
-            int bd = c->attn_pattern_block_diag, Pi = P, Ti = T;
-            void *a[] = {&m->mask, &m->lvl, &nopad, &Pi, &Ti, &bd};
+            int bd = c->attn_pattern_block_diag, Pi = P, Ti = T, one = 1;
+            void *a[] = {&m->mask, &m->lvl, &nopad, &Pi, &Ti, &bd, &one};
             err = ncm_launch_named("ncp_mask_k", blocks256((int64_t)S * S), 1, 1, 256, a);
         }
         ncm_hip_free(ldev);
@@ -518,8 +515,9 @@ float *ncp_rope_sin(NCPState *m) { return m ? m->rope_sin : NULL; }
 float *ncp_rope_gen_cos(NCPState *m, int k) { return m && k >= 0 && k < m->n_tgt ? m->gcos[k] : NULL; }
 float *ncp_rope_gen_sin(NCPState *m, int k) { return m && k >= 0 && k < m->n_tgt ? m->gsin[k] : NULL; }
 
-/* ncp_block (ncp.c:184-345) on x [nb*S][C] in place */
-static int ncp_block_dev(NCPState *m, const NcpLayer *L, float *x, int nb, const float *mask) {
+/* ncp_block (ncp.c:184-345) on x [nb*S][C] in place; per_board: mask holds
+ * one [S][S] mask per board */
+static int ncp_block_dev(NCPState *m, const NcpLayer *L, float *x, int nb, const float *mask, int per_board) {
     const NCMConfig *c = &m->cfg;
     const int C = m->C, H = m->H, nkv = m->nkv, hd = m->hd, S = m->S, I = L->inner;
     const int64_t R = (int64_t)nb * S, QKV = (int64_t)C + 2 * (int64_t)nkv * hd;
@@ -544,7 +542,10 @@ static int ncp_block_dev(NCPState *m, const NcpLayer *L, float *x, int nb, const
         }
         if (cs) rope_apply(q, k, cs, sn, nb, H, S, hd);
     }
-    sdpa_fwd_gqa_merged(q, k, v, mask, mo, nb, H, hk, S, S, hd);
+    if (per_board)
+        ncm_sdpa_fwd_gqa_merged_bmask(q, k, v, mask, mo, nb, H, hk, S, S, hd);
+    else
+        sdpa_fwd_gqa_merged(q, k, v, mask, mo, nb, H, hk, S, S, hd);
     linear_fwd_ep(mo, L->projw, L->projb, x, x, R, C, C, NCM_ACT_NONE);            /* x += c_proj(.) */
     layernorm_fwd(x, L->ln2w, L->ln2b, ln, R, C);
     if (L->gw)
@@ -556,9 +557,9 @@ static int ncp_block_dev(NCPState *m, const NcpLayer *L, float *x, int nb, const
 }
 
 /* run_stack (ncp.c:347-358): the blocks, then ln_f into out */
-static int ncp_stack_dev(NCPState *m, float *h, float *out, int nb, const float *mask) {
+static int ncp_stack_dev(NCPState *m, float *h, float *out, int nb, const float *mask, int per_board) {
     for (int li = 0; li < m->cfg.n_layer; li++) {
-        int rc = ncp_block_dev(m, &m->layer[li], h, nb, mask);
+        int rc = ncp_block_dev(m, &m->layer[li], h, nb, mask, per_board);
         if (rc) return rc;
     }
     layernorm_fwd(h, m->lnfw, m->lnfb, out, (int64_t)nb * m->S, m->C);
@@ -616,34 +617,34 @@ void ncp_forward(NCPState *m, const float *x, const int *prefix_ids, float *logi
             if (ncm_launch_named("ncp_add_rows_k", blocks256((int64_t)B * P * C), 1, 1, 256, a2)) return;
         }
     }
-    /* boards with padded prefix tokens run one at a time with their own mask
-     * (ncp.c:571-607) */
+    /* with padded prefix tokens every board gets its own mask, its pad keys
+     * masked out (ncp.c:571-607 runs such boards one at a time): the pad
+     * flags of all boards go up in one stream-ordered copy, one launch
+     * builds the B masks, and the stack runs over every board at once */
     int any_pad = 0;
     if (c->prefix_pad_token_id >= 0 && prefix_ids)
         for (int64_t i = 0; i < (int64_t)B * P; i++)
             if (prefix_ids[i] == c->prefix_pad_token_id) any_pad = 1;
     if (!any_pad) {
-        if (ncp_stack_dev(m, h, hf, B, m->mask)) return;
+        if (ncp_stack_dev(m, h, hf, B, m->mask, 0)) return;
     } else {
-        float *bm = A((int64_t)S * S);
-        int *flags = (int *)malloc((size_t)(P > 0 ? P : 1) * sizeof(int));
-        if (!bm || !flags) {
+        float *bm = A((int64_t)B * S * S);
+        int *pad = (int *)A((int64_t)B * P);
+        int *flags = (int *)malloc((size_t)B * P * sizeof(int));
+        if (!bm || !pad || !flags) {
             free(flags);
-            if (bm) ncm_fail(NCM_E_OOM, "ncp_forward: pad flags");
+            if (bm && pad) ncm_fail(NCM_E_OOM, "ncp_forward: pad flags");
             return;
         }
-        for (int b = 0; b < B; b++) {
-            for (int j = 0; j < P; j++) flags[j] = prefix_ids[(int64_t)b * P + j] == c->prefix_pad_token_id;
-            mem_h2d(m->pad, flags, (size_t)P * sizeof(int));
-            int bd = c->attn_pattern_block_diag, Pi = P, Ti = T;
-            void *a[] = {&bm, &m->lvl, &m->pad, &Pi, &Ti, &bd};
-            if (ncm_launch_named("ncp_mask_k", blocks256((int64_t)S * S), 1, 1, 256, a) ||
-                ncp_stack_dev(m, h + (int64_t)b * S * C, hf + (int64_t)b * S * C, 1, bm)) {
-                free(flags);
-                return;
-            }
-        }
+        for (int64_t i = 0; i < (int64_t)B * P; i++) flags[i] = prefix_ids[i] == c->prefix_pad_token_id;
+        int rc = ncm_h2d_async(pad, flags, (size_t)B * P * sizeof(int));
         free(flags);
+        if (rc) return;
+        int bd = c->attn_pattern_block_diag, Pi = P, Ti = T, nb = B;
+        void *a[] = {&bm, &m->lvl, &pad, &Pi, &Ti, &bd, &nb};
+        if (ncm_launch_named("ncp_mask_k", blocks256((int64_t)B * S * S), 1, 1, 256, a) ||
+            ncp_stack_dev(m, h, hf, B, bm, 1))
+            return;
     }
     /* heads per target level (ncp.c:601-637) */
     for (int k = 0; k < m->n_tgt; k++) {

@@ -105,18 +105,22 @@ ncp_qkv_rows_k(const float *__restrict__ qkv, float *__restrict__ q, float *__re
     }
 }
 
-// The additive mask of build_full_mask (ncp.c:361-386) for one board:
+// The additive mask of build_full_mask (ncp.c:361-386) for each of nb boards:
 // prefix rows see only the prefix, target rows see the prefix and the
 // target levels the pattern allows (block_diag: its own level; else levels
-// at or below its own); prefix columns flagged in pad (may be NULL) are -inf
-// for every row (ncp.c:588-600).  lvl [T]: the level of each target row.
+// at or below its own); prefix columns flagged in the board's pad flags (pad
+// may be NULL) are -inf for every row (ncp.c:588-600).  lvl [T]: the level of
+// each target row.
 extern "C" __global__ void __launch_bounds__(256)
 ncp_mask_k(float *__restrict__ mask, const int *__restrict__ lvl, const int *__restrict__ pad, int P, int T,
-           int block_diag) {
+           int block_diag, int nb) {
+    // nb boards: board b's mask at mask + b S S from its pad flags pad + b P
     const int S = P + T;
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= (int64_t)S * S) return;
-    const int r = (int)(i / S), c = (int)(i % S);
+    if (i >= (int64_t)nb * S * S) return;
+    const int b = (int)(i / ((int64_t)S * S)), e = (int)(i - (int64_t)b * S * S);
+    const int r = e / S, c = e % S;
+    if (pad) pad += (int64_t)b * P;
     float v = 0.f;
     if (r < P && c >= P) {
         v = -INFINITY;

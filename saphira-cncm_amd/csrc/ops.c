@@ -229,8 +229,8 @@ typedef struct { int B, Hq, Tq, Tkv, causal; int4 *work; int2 *tiles; int nwork,
 static SplitPlan g_split[4];
 static int g_split_next;
 
-static int sdpa_split(const float *q, const float *k, const float *v, const float *mask, float *out, int B, int Hq,
-                      int Hkv, int Tq, int Tkv, float scale, int causal, int merged) {
+static int sdpa_split(const float *q, const float *k, const float *v, const float *mask, int64_t mask_bs, float *out,
+                      int B, int Hq, int Hkv, int Tq, int Tkv, float scale, int causal, int merged) {
     const int ntiles = (Tq + 63) / 64, C = ncm_cu_count();
     const int64_t BH = (int64_t)B * Hq;
     if (BH * ntiles >= 2 * (int64_t)C || BH > INT_MAX / 4096) return 1;
@@ -311,7 +311,7 @@ static int sdpa_split(const float *q, const float *k, const float *v, const floa
     float *part_o = part, *part_ml = part + (size_t)BH * sp->nslots * 64 * 64;
     int bh = (int)BH, nslots = sp->nslots;
     void *a[] = {&q, &k, &v, &mask, &out, &Hq, &Hkv, &Tq, &Tkv, &scale, &causal, &merged, &sp->work, &bh, &nslots,
-                 &part_o, &part_ml};
+                 &part_o, &part_ml, &mask_bs};
     if (ncm_launch_named("sdpa_hd64_split", (unsigned)(sp->nwork * BH), 1, 1, 256, a)) return -1;
     if (sp->nsplit > 0) {
         void *a2[] = {&sp->tiles, &part_o, &part_ml, &out, &Hq, &Tq, &merged, &nslots};
@@ -320,8 +320,11 @@ static int sdpa_split(const float *q, const float *k, const float *v, const floa
     return 0;
 }
 
-static void sdpa_any(const char *fn, const float *q, const float *k, const float *v, const float *mask, float *out,
-                     int B, int Hq, int Hkv, int Tq, int Tkv, int hd, int causal, int merged, float *stats) {
+/* mask_bs: floats between consecutive boards' masks (0: one [Tq][Tkv] mask
+ * for every board) */
+static void sdpa_any_bm(const char *fn, const float *q, const float *k, const float *v, const float *mask,
+                        int64_t mask_bs, float *out, int B, int Hq, int Hkv, int Tq, int Tkv, int hd, int causal,
+                        int merged, float *stats) {
     if (B < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || Tq < 0 || Tkv <= 0 || hd <= 0 || hd > 256) {
         ncm_fail(NCM_E_ARG, "%s: bad shape B=%d Hq=%d Hkv=%d Tq=%d Tkv=%d hd=%d", fn, B, Hq, Hkv, Tq, Tkv, hd);
         return;
@@ -336,16 +339,36 @@ static void sdpa_any(const char *fn, const float *q, const float *k, const float
     if (ncm_ready()) return;
     float scale = 1.0f / sqrtf((float)hd);
     if (hd == 64 && is_aligned16(q) && is_aligned16(k) && is_aligned16(v) && is_aligned16(out)) {
-        if (!stats && sdpa_split(q, k, v, mask, out, B, Hq, Hkv, Tq, Tkv, scale, causal, merged) <= 0) return;
-        void *a[] = {&q, &k, &v, &mask, &out, &Hq, &Hkv, &Tq, &Tkv, &scale, &causal, &merged, &stats};
+        if (!stats && sdpa_split(q, k, v, mask, mask_bs, out, B, Hq, Hkv, Tq, Tkv, scale, causal, merged) <= 0)
+            return;
+        void *a[] = {&q, &k, &v, &mask, &out, &Hq, &Hkv, &Tq, &Tkv, &scale, &causal, &merged, &stats, &mask_bs};
         ncm_launch_named("sdpa_hd64", (unsigned)Hq, (unsigned)B, (unsigned)((Tq + 63) / 64), 256, a);
     } else if (stats) {
         ncm_fail(NCM_E_ARG, "%s: row statistics need hd = 64 and 16-byte aligned operands", fn);
     } else {
         int64_t rows = (int64_t)B * Hq * Tq;
-        void *a[] = {&q, &k, &v, &mask, &out, &B, &Hq, &Hkv, &Tq, &Tkv, &hd, &scale, &causal, &merged};
+        void *a[] = {&q, &k, &v, &mask, &out, &B, &Hq, &Hkv, &Tq, &Tkv, &hd, &scale, &causal, &merged, &mask_bs};
         ncm_launch_named("sdpa_rows", grid_of(rows, 4), 1, 1, 256, a);
     }
+}
+
+static void sdpa_any(const char *fn, const float *q, const float *k, const float *v, const float *mask, float *out,
+                     int B, int Hq, int Hkv, int Tq, int Tkv, int hd, int causal, int merged, float *stats) {
+    sdpa_any_bm(fn, q, k, v, mask, 0, out, B, Hq, Hkv, Tq, Tkv, hd, causal, merged, stats);
+}
+
+/* sdpa_fwd_gqa_merged with one [Tq][Tkv] mask per board (board b's at mask +
+ * b * Tq * Tkv): the NCP forward's boards with padded prefix tokens, each
+ * with its own key mask, in one launch (ncp.c:571-607 runs them one board
+ * at a time). */
+void ncm_sdpa_fwd_gqa_merged_bmask(const float *q, const float *k, const float *v, const float *masks, float *out,
+                                   int B, int Hq, int Hkv, int Tq, int Tkv, int hd) {
+    if (!masks) {
+        ncm_fail(NCM_E_ARG, "ncm_sdpa_fwd_gqa_merged_bmask: null masks");
+        return;
+    }
+    sdpa_any_bm("ncm_sdpa_fwd_gqa_merged_bmask", q, k, v, masks, (int64_t)Tq * Tkv, out, B, Hq, Hkv, Tq, Tkv, hd, 0,
+                1, NULL);
 }
 
 void sdpa_fwd_gqa(const float *q, const float *k, const float *v, const float *mask, float *out, int B, int Hq,

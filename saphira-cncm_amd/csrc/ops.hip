@@ -441,8 +441,10 @@ __device__ __forceinline__ void sdpa_hd64_body(const float *__restrict__ q, cons
                                                float *__restrict__ out, int Hq, int Hkv, int Tq, int Tkv,
                                                float scale, int causal, int merged, float *__restrict__ stats,
                                                int h, int b, int q0, int kb_lo, int kb_hi,
-                                               float *__restrict__ part_o, float *__restrict__ part_ml) {
+                                               float *__restrict__ part_o, float *__restrict__ part_ml,
+                                               int64_t mask_bs) {
     __shared__ __attribute__((aligned(16))) float sK[SD_T * SD_LD];
+    if (mask) mask += (int64_t)b * mask_bs;   // a board's own mask (mask_bs 0: one mask for all)
     __shared__ __attribute__((aligned(16))) float sV[SD_T * SD_LD];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
@@ -592,12 +594,12 @@ __device__ __forceinline__ void sdpa_hd64_body(const float *__restrict__ q, cons
 extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4)))
 sdpa_hd64(const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
           const float *__restrict__ mask, float *__restrict__ out, int Hq, int Hkv, int Tq, int Tkv,
-          float scale, int causal, int merged, float *__restrict__ stats) {
+          float scale, int causal, int merged, float *__restrict__ stats, int64_t mask_bs) {
     // grid (Hq, B, query tiles), the last query tile first: under a causal
     // mask it has the most key tiles, and dispatching the heaviest workgroups
     // first keeps the chip busy to the end (longest-first order)
     sdpa_hd64_body(q, k, v, mask, out, Hq, Hkv, Tq, Tkv, scale, causal, merged, stats, blockIdx.x, blockIdx.y,
-                   (gridDim.z - 1 - blockIdx.z) * 64, 0, (Tkv + SD_T - 1) / SD_T, nullptr, nullptr);
+                   (gridDim.z - 1 - blockIdx.z) * 64, 0, (Tkv + SD_T - 1) / SD_T, nullptr, nullptr, mask_bs);
 }
 
 // The same over a work list, for grids too small to fill the chip (few (b, h)
@@ -611,14 +613,14 @@ extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_pe
 sdpa_hd64_split(const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
                 const float *__restrict__ mask, float *__restrict__ out, int Hq, int Hkv, int Tq, int Tkv,
                 float scale, int causal, int merged, const int4 *__restrict__ work, int BH, int nslots,
-                float *__restrict__ part_o, float *__restrict__ part_ml) {
+                float *__restrict__ part_o, float *__restrict__ part_ml, int64_t mask_bs) {
     const int bh = blockIdx.x % BH;
     const int4 w = work[blockIdx.x / BH];
     const int h = bh % Hq, b = bh / Hq;
     float *po = w.w < 0 ? nullptr : part_o + ((int64_t)bh * nslots + w.w) * 64 * 64;
     float *pm = w.w < 0 ? nullptr : part_ml + ((int64_t)bh * nslots + w.w) * 64 * 2;
     sdpa_hd64_body(q, k, v, mask, out, Hq, Hkv, Tq, Tkv, scale, causal, merged, nullptr, h, b, w.x * 64, w.y,
-                   w.y + w.z, po, pm);
+                   w.y + w.z, po, pm, mask_bs);
 }
 
 // Merge of the parts of a split query tile: workgroup (tile x of the list
@@ -676,12 +678,13 @@ sdpa_hd64_combine(const int2 *__restrict__ tiles, const float *__restrict__ part
 extern "C" __global__ void __launch_bounds__(256)
 sdpa_rows(const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
           const float *__restrict__ mask, float *__restrict__ out, int B, int Hq, int Hkv, int Tq, int Tkv,
-          int hd, float scale, int causal, int merged) {
+          int hd, float scale, int causal, int merged, int64_t mask_bs) {
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= (int64_t)B * Hq * Tq) return;
     const int tq = (int)(row % Tq);
     const int h = (int)((row / Tq) % Hq), b = (int)(row / ((int64_t)Tq * Hq));
+    if (mask) mask += (int64_t)b * mask_bs;   // a board's own mask (mask_bs 0: one mask for all)
     const int kvh = h / (Hq / Hkv);
     const float *qr = q + row * hd;
     const float *kb = k + ((int64_t)b * Hkv + kvh) * Tkv * hd;

@@ -151,3 +151,28 @@ def test_single_level_driver_equals_reference_api():
     rcfg = O.ncp_single_level_cfg(n_layer, C, H, Kv, V, S)
     got, _ = ncp_device(rcfg, O.ncp_named(params, n_layer, C), np.eye(V, dtype=np.float32)[ids])
     assert bits_equal(got.reshape(B * S, V), drv)
+
+
+@pytest.mark.parametrize("n_head,n_embd", [(2, 128), (4, 96)])
+def test_ncp_padded_prefix_many_boards(n_head, n_embd):
+    """Padded prefix tokens on most of 40 boards: every board gets its own key
+    mask and all boards run as one batch (hd 64: the MFMA attention with the
+    per-board masks; hd 24: the row kernel), against the oracle, which runs
+    the reference's board-by-board loop (ncp.c:571-607)."""
+    cfg = MD.ncp_cfg(n_embd=n_embd, n_head=n_head, n_kv_heads=n_head // 2 or 1, n_inner=2 * n_embd,
+                     prefix_len=8, prefix_pad_token_id=0, attn_pattern_block_diag=0, levels=[1, 4, 16],
+                     vocab_size=[24, 32])
+    named = MD.ncp_named_weights(cfg, seed=23, scale=0.2)
+    rng = np.random.default_rng(24)
+    B, P = 40, 8
+    S = P + 4 + 16
+    x = rng.standard_normal((B, S, cfg["vq_embed_dim"]), dtype=np.float32)
+    pids = rng.integers(1, 9, (B, P)).astype(np.int32)
+    pads = rng.random((B, P)) < 0.4
+    pads[:, 0] = False                    # every board keeps a real prefix token
+    pids[pads] = 0
+    pids[::5] = rng.integers(1, 9, (8, P))   # some boards without pads
+    want = O.ncp_forward_levels(cfg, named, x, pids)
+    got, _ = ncp_device(cfg, named, x, pids)
+    err = compare_logits(got, want, 1e-3)
+    print(f"[ncp] padded prefix, {B} boards, hd {n_embd // n_head}: max-abs {err:.2e}")

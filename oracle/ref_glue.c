@@ -43,7 +43,7 @@ int refg_vq_multiscale(const float *z, const float *E_flat, const int *vocabs, i
                        int B, int L, int D, int *idx, float *z_hat, float *z_rest) {
     if (n_levels <= 0 || n_levels > NCM_MAX_LEVELS) return -1;
     if (!g_arena_ready) {
-        arena_init((size_t)2 << 30);
+        arena_init_default();   /* NCM_ARENA_MB, else 2048 MB */
         g_arena_ready = 1;
     }
     NCMConfig *c = (NCMConfig *)calloc(1, sizeof(NCMConfig));
@@ -93,7 +93,7 @@ int refg_vq_multiscale(const float *z, const float *E_flat, const int *vocabs, i
  * backward case then accumulates into exactly those buffers. */
 static void ensure_arena(void) {
     if (!g_arena_ready) {
-        arena_init((size_t)2 << 30);
+        arena_init_default();   /* NCM_ARENA_MB, else 2048 MB */
         g_arena_ready = 1;
     }
 }

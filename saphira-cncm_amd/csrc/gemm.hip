@@ -1127,80 +1127,8 @@ GEMM_TILE_FIXUP(gemm_64x64_fixup_dw_s, EPI_ACCUM, false, false, false, SEL_NONE)
 // wave 8 fragment reads for 64 MFMAs (4 for 16 on 64 x 64 tiles) and the
 // operand traffic from L2 per FLOP halves.  Two stages of 32 KB: two
 // workgroups share a CU.  Used where whole tiles fill the CUs (no split-K).
-//
-// Slabs: k-contiguous [128 rows][32 k] as the 64-row slabs (pitch 32 floats,
-// float4 group g of row r in slot g ^ (r & 7)); i/j-contiguous [32 k][128
-// cols] at pitch 128 with no swizzle: a wave's fragment read at (k-row kr,
-// columns wn*64 + 4 li .. + 3) is one ds_read_b128 that feeds its four MFMA
-// blocks (block b takes column wn*64 + 4 j + b), and the 16 lanes of a
-// gfx950 ds_read_b128 service group -- {0-3, 12-15, 20-23, 24-27} or {4-7,
-// 8-11, 16-19, 28-31}, lane = 16 lg + li -- then cover the 64 banks once
-// (rows 4 lg apart start at bank 0, columns 4 li span 16 banks per lane
-// quad).
-#define BIG 128
-#define D_SLAB_BIG (BIG * GEMM_BK)
-
-template <bool KC>
-struct DSlabBig {
-    // The wave issues loads 4 * wave + e (e = 0..3) of the slab's sixteen.
-    // k-contiguous: rows 8 q .. 8 q + 7 (8 lanes per row), a row bound per
-    // load; i/j-contiguous: k-rows 2 q, 2 q + 1 (32 lanes per row), one column
-    // bound for all four loads, which sit 2 e k-rows after load 0 (so only
-    // load 0's offset and k bound are kept: registers are scarce here).
-    unsigned voff[KC ? 4 : 1];
-    int klim[KC ? 4 : 1];
-    __device__ __forceinline__ void init(int wave, int lane, int ld, int fix0, int fix_lim, int k_lim) {
-        if (KC) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int r = 8 * (4 * wave + e) + (lane >> 3), g = (lane & 7) ^ (r & 7);
-                voff[e] = fix0 + r < fix_lim ? (unsigned)((fix0 + r) * ld + 4 * g) * 4u : OOB_OFFSET;
-                klim[e] = k_lim - 4 * g;
-            }
-        } else {
-            const int kr = 8 * wave + (lane >> 5), c = lane & 31;
-            voff[0] = fix0 + 4 * c < fix_lim ? (unsigned)(kr * ld + fix0 + 4 * c) * 4u : OOB_OFFSET;
-            klim[0] = k_lim - kr;
-        }
-    }
-    __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rs, float *slab, int wave, int k0, int ld) const {
-        const unsigned dk = KC ? (unsigned)k0 * 4u : (unsigned)k0 * (unsigned)ld * 4u;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            unsigned off;
-            if (KC)
-                off = k0 < klim[e] ? voff[e] + dk : OOB_OFFSET;
-            else   // an out-of-range column stays beyond the buffer after the k-row step
-                off = k0 + 2 * e < klim[0] && voff[0] != OOB_OFFSET ? voff[0] + dk + (unsigned)(2 * e * ld) * 4u
-                                                                   : OOB_OFFSET;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rs, (__attribute__((address_space(3))) void *)(slab + (4 * wave + e) * 256), 16, off, 0, 0, 0);
-        }
-    }
-};
-
-// f[t][s]: the operand value of MFMA block t at step s of chunk kc, for the
-// wave's 64 rows / columns starting at w * 64.
-template <bool KC>
-__device__ __forceinline__ void d_frags_big(const float *slab, int w, int li, int lg, int kc, float (&f)[4][4]) {
-    if (KC) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int r = w * 64 + 16 * t + li;
-            const f4 v = *(const f4 *)(slab + r * GEMM_BK + 4 * ((4 * kc + lg) ^ (r & 7)));
-#pragma unroll
-            for (int s = 0; s < 4; ++s) f[t][s] = v[s];
-        }
-    } else {
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const int kr = 16 * kc + 4 * lg + s;
-            const f4 v = *(const f4 *)(slab + kr * BIG + w * 64 + 4 * li);
-#pragma unroll
-            for (int t = 0; t < 4; ++t) f[t][s] = v[t];
-        }
-    }
-}
+// The 128-row slabs and their fragment reads are mfma_slab.h's DSlabBig and
+// d_frags_big.
 
 // The epilogue of a 128 x 128 tile, one row of MFMA blocks (16 outputs per
 // thread) at a time, so that the loaded operands of all 64 outputs are not

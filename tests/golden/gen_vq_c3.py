@@ -9,8 +9,9 @@ residual updates).  Where the reference was compiled here
 (oracle/_ref/libref.so), its own vq_load + vq_z_to_idx over the same
 codebooks is run too and must give the same codes, z_hat and z_rest.
 
-Run from the repository root: python tests/golden/gen_vq_c3.py
-(about 1-2 minutes on 8 cores for the oracle, ~2 more for the reference)."""
+Run from the repository root: NCM_ARENA_MB=8192 python tests/golden/gen_vq_c3.py
+(the reference's scratch arena must hold the four 1 GiB distance matrices;
+about 1-2 minutes on 8 cores for the oracle, ~2 more for the reference)."""
 import hashlib
 import os
 import sys

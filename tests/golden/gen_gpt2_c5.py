@@ -18,7 +18,7 @@ Stored (gradients are 88.5 M floats, too large for a fixture):
   last element plus 62 seeded draws) and the gradient values there.
 
 Run from the repository root: python tests/golden/gen_gpt2_c5.py
-(about 30-60 minutes on 8 cores, 20 GB of memory)."""
+(about 65 minutes on 8 cores, 32 GB of memory)."""
 import os
 import sys
 import time

@@ -217,7 +217,7 @@ colsum_small(const float *__restrict__ dy, int rows, int N, float *db) {
         double t = red[0][lane];
 #pragma unroll
         for (int w = 1; w < 16; ++w) t += red[w][lane];
-        db[col] += (float)t;
+        db[col] += 0.0f + (float)t;   // the reference adds a zeroed temporary (train_tape.c:708-720)
     }
 }
 
@@ -228,7 +228,7 @@ colsum_final(const double *__restrict__ part, int chunks, int N, float *db) {
     double s = 0.0;
 #pragma unroll 16
     for (int c = 0; c < chunks; ++c) s += part[(int64_t)c * N + col];
-    db[col] += (float)s;
+    db[col] += 0.0f + (float)s;
 }
 
 // Stage 2 over many chunks: a workgroup of 16 waves per 64 columns, wave v
@@ -257,7 +257,7 @@ colsum_final_w(const double *__restrict__ part, int chunks, int N, float *db) {
         double t = red[0][lane];
 #pragma unroll
         for (int w = 1; w < 16; ++w) t += red[w][lane];
-        db[col] += (float)t;
+        db[col] += 0.0f + (float)t;   // the reference adds a zeroed temporary (train_tape.c:708-720)
     }
 }
 
@@ -265,18 +265,22 @@ colsum_final_w(const double *__restrict__ part, int chunks, int N, float *db) {
 // dW[n,k] += sum_r dy[r,n] x[r,k]: the reference's per-output fp64 sum over
 // r ascending, rounded to float and added through a zeroed temporary
 // (train_tape.c:714-720), so this path is bit-exact with the host backward.
-// One thread per 4 consecutive k of one row n; HBM-bound on dW.
+// One thread per 4 consecutive k of one row n; HBM-bound on dW.  With db,
+// the thread of k = 0 also adds the bias gradient db[n] += (float) sum_r
+// dy[r,n] (fp64, r ascending: colsum_small's sum over these rows) from the
+// dy values it loads anyway, so the call needs no second launch.
 template <bool VEC>
 __device__ __forceinline__ void dw_rank_body(const float *__restrict__ dy, const float *__restrict__ x,
-                                             float *dW, int nb, int N, int K) {
+                                             float *dW, float *db, int nb, int N, int K) {
 #pragma clang fp contract(off)
     const int64_t f = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int K4 = (K + 3) / 4;
     if (f >= (int64_t)N * K4) return;
     const int n = (int)(f / K4), k = (int)(f % K4) * 4;
-    double s[4] = {0.0, 0.0, 0.0, 0.0};
+    double s[4] = {0.0, 0.0, 0.0, 0.0}, t = 0.0;
     for (int r = 0; r < nb; ++r) {
         const double g = dy[(int64_t)r * N + n];
+        t += g;
         const float *xr = x + (int64_t)r * K + k;
         if (VEC) {
             f4 v = *(const f4 *)xr;
@@ -296,12 +300,17 @@ __device__ __forceinline__ void dw_rank_body(const float *__restrict__ dy, const
 #pragma unroll
         for (int u = 0; u < 4; ++u) if (k + u < K) o[u] += 0.0f + (float)s[u];
     }
+    if (db != nullptr && k == 0) db[n] += 0.0f + (float)t;
 }
 
 extern "C" __global__ void __launch_bounds__(256)
-dw_rank_v(const float *dy, const float *x, float *dW, int nb, int N, int K) { dw_rank_body<true>(dy, x, dW, nb, N, K); }
+dw_rank_v(const float *dy, const float *x, float *dW, float *db, int nb, int N, int K) {
+    dw_rank_body<true>(dy, x, dW, db, nb, N, K);
+}
 extern "C" __global__ void __launch_bounds__(256)
-dw_rank_s(const float *dy, const float *x, float *dW, int nb, int N, int K) { dw_rank_body<false>(dy, x, dW, nb, N, K); }
+dw_rank_s(const float *dy, const float *x, float *dW, float *db, int nb, int N, int K) {
+    dw_rank_body<false>(dy, x, dW, db, nb, N, K);
+}
 
 // dx[r,k] += sum_n dy[r,n] W[n,k] for r < nb: a transposed GEMV streaming W
 // once.  Block = 4 waves x 256 columns (float4 per lane); the waves take

@@ -544,8 +544,10 @@ void ncm_linear_bwd_ex(const float *x, const float *W, const float *dy, float *d
             int vec = K % 4 == 0 && is_aligned16(x) && is_aligned16(dW);
             int K4 = (K + 3) / 4;
             int64_t n = (int64_t)M * K4;
-            void *a[] = {&dy, &x, &dW, &nb, &M, &K};
+            /* the rank-update kernel also adds db from the dy values it loads */
+            void *a[] = {&dy, &x, &dW, &db, &nb, &M, &K};
             rc = ncm_launch_named(vec ? "dw_rank_v" : "dw_rank_s", (unsigned)((n + 255) / 256), 1, 1, 256, a);
+            db = NULL;
         } else {
             int vec = (M % 4 == 0) && (K % 4 == 0) && is_aligned16(dy) && is_aligned16(x);
             /* the vectorised dW kernel also sums db (from the dy slabs it loads anyway) */

@@ -225,6 +225,27 @@ def test_bias_gradient_inside_dw():
     assert segs_seen == {False, True}
 
 
+def test_bias_gradient_inside_rank_update():
+    """Batch <= 8 with dW requested: the rank-update dW kernel (vectorised and
+    scalar rows) adds db from the dy values it loads, in the same fp64 order
+    as the column-sum kernel, so db equals the db-only call's bit for bit and
+    dW, db equal the oracle's (the reference's host sums) bit for bit."""
+    rng = np.random.default_rng(31)
+    for rows in (1, 2, 5, 8):
+        for N, K in ((1, 8), (63, 12), (130, 7), (2304, 768)):
+            assert ncmhip.linear_plan("dwdb", rows, N, K)[0] == ("dw_rank_v" if K % 4 == 0 else "dw_rank_s")
+            x = rng.standard_normal((rows, K)).astype(np.float32)
+            W = rng.standard_normal((N, K)).astype(np.float32)
+            dy = rng.standard_normal((rows, N)).astype(np.float32)
+            db0 = rng.standard_normal(N).astype(np.float32)
+            dW0 = rng.standard_normal((N, K)).astype(np.float32)
+            _, dW, db = gpu_bwd(x, W, dy, None, dW0, db0)
+            _, _, db_only = gpu_bwd(x, W, dy, None, None, db0)
+            _, ref_dW, ref_db = O.linear_bwd(x, W, dy, dW=dW0, db=db0, want=("dW", "db"))
+            assert bits_equal(db, db_only), (rows, N, K)
+            assert bits_equal(db, ref_db) and bits_equal(dW, ref_dW), (rows, N, K)
+
+
 def test_run_to_run_determinism():
     rng, x, W, b = sweep_inputs(3, 512, 3072, 768)
     a = gpu_fwd(x, W, b)

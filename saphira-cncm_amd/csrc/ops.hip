@@ -1,5 +1,5 @@
 // ops.hip -- row-wise and elementwise kernels around the GEMMs.
-#include "ncm_dev.h"
+#include "mfma_slab.h"
 
 // Greedy id: per row the reference's strict '>' scan from index 0
 // (kernels.c:731-735): index 0 when x[0] is NaN, otherwise the lowest index
@@ -429,6 +429,9 @@ eltwise4_k(const float *a, const float *b, float *y, float s, int64_t n4, int op
 // index 4g + s (d for S^T, key for P V).  Q stays in registers.
 #define SD_T 64
 #define SD_LD (64 + 8)
+// LDS slot of float4 group g (0..15) of row r in the 64-float rows of the
+// flash kernels' K / V tiles (an involution in g for each r)
+__device__ __forceinline__ int sd_slot(int r, int g) { return g ^ (r & 15) ^ (((r >> 2) & 1) << 3); }
 
 // The loop of one workgroup: queries q0 .. q0 + 63 of (b, h) over the key
 // blocks [kb_lo, kb_hi) (64 keys each) of the range the query tile sees.
@@ -443,9 +446,15 @@ __device__ __forceinline__ void sdpa_hd64_body(const float *__restrict__ q, cons
                                                int h, int b, int q0, int kb_lo, int kb_hi,
                                                float *__restrict__ part_o, float *__restrict__ part_ml,
                                                int64_t mask_bs) {
-    __shared__ __attribute__((aligned(16))) float sK[SD_T * SD_LD];
+    // K and V tiles of 64 keys x 64 d, unpadded, float4 group g of key row r
+    // in slot sd_slot(r, g).  A gfx950 ds_read_b128 serves lanes {0-3, 12-15,
+    // 20-23, 24-27} (or {4-7, 8-11, 16-19, 28-31}) together: S^T's reads
+    // (lane li: row 16c + li, group 4kc + lg) and P V's (lane li: row
+    // 16c + 4lg + st, group li) then meet 16 different slots; with the plain
+    // g ^ (r & 15) the P V rows r and r + 4 collided.
+    __shared__ __attribute__((aligned(16))) float sK[SD_T * 64];
     if (mask) mask += (int64_t)b * mask_bs;   // a board's own mask (mask_bs 0: one mask for all)
-    __shared__ __attribute__((aligned(16))) float sV[SD_T * SD_LD];
+    __shared__ __attribute__((aligned(16))) float sV[SD_T * 64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
     const int kvh = h / (Hq / Hkv);
@@ -453,6 +462,21 @@ __device__ __forceinline__ void sdpa_hd64_body(const float *__restrict__ q, cons
     const float *qb = q + ((int64_t)b * Hq + h) * Tq * 64;
     const float *kb = k + ((int64_t)b * Hkv + kvh) * Tkv * 64;
     const float *vb = v + ((int64_t)b * Hkv + kvh) * Tkv * 64;
+    // Tiles go from L2 straight into LDS (buffer_load_dwordx4 ... lds):
+    // load e of wave w fills key rows 4 (4w + e) .. +3, lane l row
+    // 4 (4w + e) + l / 16, slot l % 16; rows past Tkv lie beyond the buffer
+    // and read zero.
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kb, (unsigned)Tkv * 256u), rv = make_rsrc(vb, (unsigned)Tkv * 256u);
+    const int lrow = lane >> 4, lslot = lane & 15;
+    auto issue = [&](__amdgpu_buffer_rsrc_t rs, float *dst, int k0) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int r = 4 * (4 * wave + e) + lrow;
+            const unsigned off = (unsigned)(k0 + r) * 256u + 16u * (unsigned)sd_slot(r, lslot);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rs, (__attribute__((address_space(3))) void *)(dst + (4 * wave + e) * 256), 16, off, 0, 0, 0);
+        }
+    };
 
     // Q^T fragments: query qw + li, d = 16kc + 4g .. +3
     f4 qf[4];
@@ -470,33 +494,22 @@ __device__ __forceinline__ void sdpa_hd64_body(const float *__restrict__ q, cons
     const int coff = Tkv - Tq;   // causal offset of the query positions
     int kend = Tkv;
     if (causal) kend = min(Tkv, q0 + 64 + coff);
-    // K and V tiles (64 keys x 64 d, rows beyond Tkv as zero), staged through
-    // LDS; no register prefetch of the next tile, so the kernel stays under
-    // 128 registers and four workgroups share a CU
+    // Per key tile, two barriers: (1) after S^T and the softmax, once this
+    // wave's V loads have landed: every wave is done reading K and every V
+    // row is in LDS, so the next tile's K loads go out (overlapping P V);
+    // (2) after P V, once the next K has landed: V is free and the next K
+    // is in LDS, so the next V loads go out (overlapping the next S^T and
+    // softmax).
     kend = min(kend, kb_hi * SD_T);
-    for (int k0 = kb_lo * SD_T; k0 < kend; k0 += SD_T) {
-        __syncthreads();
-        // all eight loads in flight at once (keys past Tkv read key Tkv - 1 and
-        // are stored as zero), then the LDS stores.  Thread tid stages rows
-        // tid / 16 + 16 j, columns 4 (tid % 16): the swizzle depends on bits 2
-        // and 3 of the row only, so one LDS offset serves all four rows.
-        f4 kk[4], vv[4];
-        const int r0 = tid >> 4, c0 = (tid & 15) * 4;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int64_t key = min(k0 + r0 + 16 * j, Tkv - 1);
-            kk[j] = *(const f4 *)(kb + key * 64 + c0);
-            vv[j] = *(const f4 *)(vb + key * 64 + c0);
-        }
-        const int so = r0 * SD_LD + LDS_SWZ(r0, c0);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const bool ok = k0 + r0 + 16 * j < Tkv;
-            *(f4 *)(sK + so + 16 * j * SD_LD) = ok ? kk[j] : f4{0.f, 0.f, 0.f, 0.f};
-            *(f4 *)(sV + so + 16 * j * SD_LD) = ok ? vv[j] : f4{0.f, 0.f, 0.f, 0.f};
-        }
-        __syncthreads();
-
+    const int kfirst = kb_lo * SD_T;
+    if (kfirst < kend) {
+        issue(rk, sK, kfirst);
+        issue(rv, sV, kfirst);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
+    __syncthreads();
+    for (int k0 = kfirst; k0 < kend; k0 += SD_T) {
+        const bool more = k0 + SD_T < kend;
         // S^T[c]: keys k0 + 16c + 4lg + r, query my_q
         f4 s[4];
 #pragma unroll
@@ -504,7 +517,7 @@ __device__ __forceinline__ void sdpa_hd64_body(const float *__restrict__ q, cons
             s[c] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kc = 0; kc < 4; ++kc) {
-                const f4 kf = *(const f4 *)(sK + (16 * c + li) * SD_LD + LDS_SWZ((16 * c + li), kc * 16 + 4 * lg));
+                const f4 kf = *(const f4 *)(sK + (16 * c + li) * 64 + 4 * sd_slot(16 * c + li, 4 * kc + lg));
 #pragma unroll
                 for (int st = 0; st < 4; ++st) s[c] = mfma4(kf[st], qf[kc][st], s[c]);
             }
@@ -540,6 +553,14 @@ __device__ __forceinline__ void sdpa_hd64_body(const float *__restrict__ q, cons
         ps += __shfl_xor(ps, 32, 64);
         l_run = l_run * alpha + ps;
         m_run = m_new;
+        // every wave is done reading K and this tile's V is in LDS: the next
+        // K loads go out, overlapping P V (issued after the mask's loads,
+        // which the softmax has waited for)
+        __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's V loads
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        if (more) issue(rk, sK, k0 + SD_T);
+        __builtin_amdgcn_sched_barrier(0);
         // rescale O rows (query qw + 4lg + r) by the alpha held in lane li = 4lg + r
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -552,10 +573,15 @@ __device__ __forceinline__ void sdpa_hd64_body(const float *__restrict__ q, cons
         for (int c = 0; c < 4; ++c)
 #pragma unroll
             for (int st = 0; st < 4; ++st) {
-                const f4 vf = *(const f4 *)(sV + (16 * c + 4 * lg + st) * SD_LD + LDS_SWZ((16 * c + 4 * lg + st), 4 * li));
+                const f4 vf = *(const f4 *)(sV + (16 * c + 4 * lg + st) * 64 + 4 * sd_slot(16 * c + 4 * lg + st, li));
 #pragma unroll
                 for (int u = 0; u < 4; ++u) o[u] = mfma4(s[c][st], vf[u], o[u]);
             }
+        __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's loads of the next K
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        if (more) issue(rv, sV, k0 + SD_T);
+        __builtin_amdgcn_sched_barrier(0);
     }
 
     if (part_o) {   // a part of a split range: unnormalised rows and (max, sum)

@@ -428,7 +428,6 @@ eltwise4_k(const float *a, const float *b, float *y, float s, int64_t n4, int op
 // k-permutation as in the GEMM: MFMA step s gives lane group g the reduction
 // index 4g + s (d for S^T, key for P V).  Q stays in registers.
 #define SD_T 64
-#define SD_LD (64 + 8)
 // LDS slot of float4 group g (0..15) of row r in the 64-float rows of the
 // flash kernels' K / V tiles (an involution in g for each r)
 __device__ __forceinline__ int sd_slot(int r, int g) { return g ^ (r & 15) ^ (((r >> 2) & 1) << 3); }

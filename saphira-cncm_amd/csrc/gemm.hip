@@ -67,7 +67,7 @@ struct GemmArgs {
     int act;
     int res_mul;         // STORE: C = act(acc + bias) * res instead of res + act(acc + bias)
     int tiles_m, tiles_n;
-    int iters;           // BK slabs of the reduction (k loops in groups of 4, the last one possibly partial)
+    int iters;           // BK slabs per tile (a multiple of 4)
     int dp_tiles;        // blocks [0, dp_tiles): one whole tile each
     int segs;            // later blocks: k-segment (u % segs) of tile dp_tiles + u / segs
     unsigned a_bytes, b_bytes;  // extents of A and B for the buffer descriptors
@@ -685,9 +685,9 @@ __device__ __forceinline__ void gemm_tile_body(const GemmArgs &p) {
             unit = ((p.dp_tiles & 7) == 0) ? xcd_remap(j, ntail) : j;
             const int tail = unit / p.segs, seg = unit - tail * p.segs;
             tile = p.dp_tiles + tail;
-            const int q4 = (p.iters + 3) >> 2;   // groups of 4 slabs; the last may be partial
+            const int q4 = p.iters >> 2;
             it0 = (int)((int64_t)seg * q4 / p.segs) * 4;
-            it1 = min((int)((int64_t)(seg + 1) * q4 / p.segs) * 4, p.iters);
+            it1 = (int)((int64_t)(seg + 1) * q4 / p.segs) * 4;
         }
     }
     int tm, tn;
@@ -753,7 +753,6 @@ __device__ __forceinline__ void gemm_tile_body(const GemmArgs &p) {
     for (int kt = it0; kt < it1; kt += 4) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            if (kt + u >= it1) break;   // a partial last group: no MFMAs on slabs past the range
             const int cur = u & 1;   // it0 is a multiple of 4: slab kt+u lives in buffer u & 1
             const float *ca = sA + cur * BM * G_LD, *cb = sB + cur * BN * G_LD;
             float *na = sA + (cur ^ 1) * BM * G_LD, *nb = sB + (cur ^ 1) * BN * G_LD;
@@ -932,9 +931,9 @@ __device__ __forceinline__ void gemm_dma_body(const GemmArgs &pa) {
             unit = ((pa.dp_tiles & 7) == 0) ? xcd_remap(j, ntail) : j;
             const int tail = unit / pa.segs, seg = unit - tail * pa.segs;
             tile = pa.dp_tiles + tail;
-            const int q4 = (pa.iters + 3) >> 2;   // groups of 4 slabs; the last may be partial
+            const int q4 = pa.iters >> 2;
             it0 = (int)((int64_t)seg * q4 / pa.segs) * 4;
-            it1 = min((int)((int64_t)(seg + 1) * q4 / pa.segs) * 4, pa.iters);
+            it1 = (int)((int64_t)(seg + 1) * q4 / pa.segs) * 4;
         }
     }
     int tm, tn;
@@ -1003,7 +1002,6 @@ __device__ __forceinline__ void gemm_dma_body(const GemmArgs &pa) {
         for (int kt = it0; kt < it1; kt += 4) {
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                if (kt + u >= it1) break;   // a partial last group: no MFMAs on slabs past the range
                 // it0 is a multiple of 4: slab kt+u lives in stage u & 1
                 float *const ca = (u & 1) ? sA1 : sA0, *const cb = (u & 1) ? sB1 : sB0;
                 float *const na = (u & 1) ? sA0 : sA1, *const nb = (u & 1) ? sB0 : sB1;
@@ -1250,7 +1248,6 @@ __device__ __forceinline__ void gemm_big_body(const GemmArgs &pa) {
         for (int kt = 0; kt < iters; kt += 4) {
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                if (kt + u >= iters) break;   // a partial last group: no MFMAs on slabs past K
                 float *const ca = (u & 1) ? sA1 : sA0, *const cb = (u & 1) ? sB1 : sB0;
                 float *const na = (u & 1) ? sA0 : sA1, *const nb = (u & 1) ? sB0 : sB1;
                 d_frags_big<AKC>(ca, wm, li, lg, 1, f1a);

@@ -114,9 +114,7 @@ static GemmPlan plan_gemm_uncached(int Mo, int No, int Kred, int slots, int bm, 
     g.tiles_m = (Mo + bm - 1) / bm;
     g.tiles_n = (No + bn - 1) / bn;
     const int groups = Kred > 0 ? (Kred + 4 * BK - 1) / (4 * BK) : 1;
-    /* slabs of the reduction: a tile skips the slabs of a partial last group
-     * of four that lie wholly past K (split segments are whole groups) */
-    g.iters = Kred > 0 ? (Kred + BK - 1) / BK : 1;
+    g.iters = 4 * groups;
     const int T = g.tiles_m * g.tiles_n, C = ncm_cu_count();
     if (slots < C) slots = C;
     /* unsplit: every tile whole */

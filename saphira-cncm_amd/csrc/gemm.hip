@@ -911,8 +911,11 @@ struct BoolTag {
 };
 
 // DB: the dW kernel that also sums the bias gradient (p.db); SEL: per-tile
-// output selection (f3_select, heads_select)
-template <bool AKC, bool BKC, int EPI, bool DB = false, int SEL = SEL_NONE>
+// output selection (f3_select, heads_select); TAIL: p.iters need not be a
+// multiple of 4 -- the slabs of a partial last group that lie wholly past the
+// range are skipped (a separate instance: the check in the unrolled k loop
+// cost the other launches 1.4%).
+template <bool AKC, bool BKC, int EPI, bool DB = false, int SEL = SEL_NONE, bool TAIL = false>
 __device__ __forceinline__ void gemm_dma_body(const GemmArgs &pa) {
     __shared__ __attribute__((aligned(16))) float sm[2 * 2 * D_SLAB];   // [stage][A | B]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -931,9 +934,10 @@ __device__ __forceinline__ void gemm_dma_body(const GemmArgs &pa) {
             unit = ((pa.dp_tiles & 7) == 0) ? xcd_remap(j, ntail) : j;
             const int tail = unit / pa.segs, seg = unit - tail * pa.segs;
             tile = pa.dp_tiles + tail;
-            const int q4 = pa.iters >> 2;
+            const int q4 = (pa.iters + (TAIL ? 3 : 0)) >> 2;
             it0 = (int)((int64_t)seg * q4 / pa.segs) * 4;
             it1 = (int)((int64_t)(seg + 1) * q4 / pa.segs) * 4;
+            if (TAIL) it1 = min(it1, pa.iters);
         }
     }
     int tm, tn;
@@ -1002,6 +1006,9 @@ __device__ __forceinline__ void gemm_dma_body(const GemmArgs &pa) {
         for (int kt = it0; kt < it1; kt += 4) {
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
+                if constexpr (TAIL) {
+                    if (kt + u >= it1) break;
+                }
                 // it0 is a multiple of 4: slab kt+u lives in stage u & 1
                 float *const ca = (u & 1) ? sA1 : sA0, *const cb = (u & 1) ? sB1 : sB0;
                 float *const na = (u & 1) ? sA0 : sA1, *const nb = (u & 1) ? sB0 : sB1;
@@ -1104,6 +1111,11 @@ __device__ __forceinline__ void gemm_dma_body(const GemmArgs &pa) {
         name(GemmArgs p) {                                                                             \
         gemm_dma_body<AKC, BKC, EPI, DB, SEL>(p);                                                      \
     }
+#define GEMM_DMA_TAIL_KERNEL(name, AKC, BKC, EPI, DB, SEL)                                              \
+    extern "C" __global__ void __launch_bounds__(GEMM_NT) __attribute__((amdgpu_waves_per_eu(4)))      \
+        name(GemmArgs p) {                                                                             \
+        gemm_dma_body<AKC, BKC, EPI, DB, SEL, true>(p);                                                \
+    }
 #define GEMM_TILE_FIXUP(name, EPI, IA, IB, DB, SEL) \
     extern "C" __global__ void __launch_bounds__(GEMM_NT) name(GemmArgs p) { gemm_tile_fixup_body<EPI, IA, IB, DB, SEL>(p); }
 GEMM_DMA_KERNEL(gemm_64x64_fwd_v, true, true, EPI_STORE, false, SEL_NONE)
@@ -1112,6 +1124,7 @@ GEMM_DMA_KERNEL(gemm_64x64_fwdh_v, true, true, EPI_STORE, false, SEL_HEADS)  // 
 GEMM_DMA_KERNEL(gemm_64x64_dx_v, true, false, EPI_ACCUM, false, SEL_NONE)
 GEMM_DMA_KERNEL(gemm_64x64_dw_v, false, false, EPI_ACCUM, false, SEL_NONE)
 GEMM_DMA_KERNEL(gemm_64x64_dwb_v, false, false, EPI_ACCUM, true, SEL_NONE)   // dW + db
+GEMM_DMA_TAIL_KERNEL(gemm_64x64_dwbt_v, false, false, EPI_ACCUM, true, SEL_NONE)   // dW + db, partial last group
 GEMM_DMA_KERNEL(gemm_64x64_dxa_v, true, false, EPI_ACT_BWD, false, SEL_NONE) // dX through the activation backward
 GEMM_DMA_KERNEL(gemm_64x64_dxh_v, true, false, EPI_ACCUM, false, SEL_HEADS)  // dX to head-major
 GEMM_DMA_KERNEL(gemm_64x64_gated_v, true, true, EPI_GATED, false, SEL_NONE)

@@ -287,6 +287,10 @@ static int run_gemm_x(int kind, const float *A, const float *B, float *C, const 
         g.dp_tiles = g.blocks = g.tiles_m * g.tiles_n;
         g.segs = 1;
     }
+    /* a dW + db reduction that is not whole groups of four slabs (batch 64 in
+     * the sweep) runs the instance that skips the slabs past it */
+    const int tail = !big && vec && db && Kred % (4 * BK) != 0;
+    if (tail) snprintf(name, sizeof name, "gemm_%dx%d_dwbt_v", bm, bn);
     /* operand extents as stored: A is [Mo][Kred] (k-contiguous) or [Kred][Mo] */
     int64_t ab = kind == L_DW ? extent(Kred, Mo, lda) : extent(Mo, Kred, lda);
     int64_t bb = kind == L_FWD ? extent(No, Kred, ldb) : extent(Kred, No, ldb);
@@ -297,6 +301,7 @@ static int run_gemm_x(int kind, const float *A, const float *B, float *C, const 
                   g.tiles_m, g.tiles_n, g.iters, g.dp_tiles, g.segs, (unsigned)ab, (unsigned)bb, NULL, NULL, beta,
                   db, NULL, ex->pre, ex->bwd_x, ex->bwd_kind, {NULL}, {NULL}, {NULL}, {0}, {0}, ex->hm_T};
     p.res_mul = res_mul;
+    if (tail) p.iters = (Kred + BK - 1) / BK;
     if (ex->W3)
         for (int g = 0; g < 3; g++) {
             p.B3[g] = ex->W3[g];
@@ -709,7 +714,7 @@ int ncm_hip_linear_plan(int op, int64_t batch, int M, int K, char *kernel, size_
     int vec = op == L_FWD ? K % 4 == 0 : (M % 4 == 0 && K % 4 == 0);
     const int bm = TILE_M, bn = TILE_N;
     gemm_name(bm, bn, op, vec, kernel, cap);
-    if (with_db && vec) snprintf(kernel, cap, "gemm_%dx%d_dwb_v", bm, bn);
+    if (with_db && vec) snprintf(kernel, cap, "gemm_%dx%d_%s_v", bm, bn, Kred % (4 * BK) ? "dwbt" : "dwb");
     if ((int64_t)((Mo + bm - 1) / bm) * ((No + bn - 1) / bn) > INT_MAX / 4)
         return ncm_fail(NCM_E_ARG, "ncm_hip_linear_plan: %d x %d output has too many tiles", Mo, No), -1;
     int slots = gemm_slots(kernel);

@@ -207,7 +207,8 @@ def test_bias_gradient_inside_dw():
     for rows, N, K in ((9, 68, 8), (100, 132, 64), (513, 2304, 768), (4096, 132, 8), (1100, 200, 256),
                        (16384, 200, 64)):
         kernel, segs = ncmhip.linear_plan("dwdb", rows, N, K)
-        assert kernel == "gemm_64x64_dwb_v"
+        # (the instance that skips the slabs past a partial last group of four where rows % 128 != 0)
+        assert kernel == ("gemm_64x64_dwb_v" if rows % 128 == 0 else "gemm_64x64_dwbt_v"), (rows, kernel)
         segs_seen.add(segs > 1)
         x = rng.integers(-4, 5, (rows, K)).astype(np.float32)
         W = rng.integers(-4, 5, (N, K)).astype(np.float32)

@@ -315,7 +315,8 @@ dw_rank_s(const float *dy, const float *x, float *dW, float *db, int nb, int N, 
 // dx[r,k] += sum_n dy[r,n] W[n,k] for r < nb: a transposed GEMV streaming W
 // once.  Block = 4 waves x 256 columns (float4 per lane); the waves take
 // interleaved rows n of a chunk of DXT_ROWS rows, LDS combines them, and the
-// chunk partials [chunk][nb][K] are summed in chunk order by dxt_final.
+// chunk partials [chunk][nb][K] are summed by dxt_final (four interleaved
+// wave sums over the chunks, added in wave order).
 #define DXT_ROWS 32
 template <int NB>
 __device__ __forceinline__ void dxt_partial_body(const float *__restrict__ dy, const float *__restrict__ W,
@@ -349,14 +350,28 @@ __device__ __forceinline__ void dxt_partial_body(const float *__restrict__ dy, c
     }
 }
 
+// dx[f] += sum over the chunk partials: a workgroup per 64 outputs, wave w
+// summing chunks w, w + 4, ... (16 loads in flight per pass), the four wave
+// sums added in wave order -- a quarter of the dependent round trips of one
+// thread walking every chunk (up to 152 for a 4864-row W).
 extern "C" __global__ void __launch_bounds__(256)
 dxt_final(const float *__restrict__ part, int chunks, int nb, int K, float *__restrict__ dx) {
-    int64_t f = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (f >= (int64_t)nb * K) return;
+    __shared__ float red[4][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t n = (int64_t)nb * K, f = (int64_t)blockIdx.x * 64 + lane;
+    const int64_t fc = f < n ? f : n - 1;
     float s = 0.f;
-#pragma unroll 16
-    for (int c = 0; c < chunks; ++c) s += part[(int64_t)c * nb * K + f];
-    dx[f] += s;
+    for (int c0 = wave; c0 < chunks; c0 += 64) {
+        float v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] = part[(int64_t)min(c0 + 4 * u, chunks - 1) * n + fc];
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+            if (c0 + 4 * u < chunks) s += v[u];
+    }
+    red[wave][lane] = s;
+    __syncthreads();
+    if (wave == 0 && f < n) dx[f] += ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
 }
 
 #define DXT_KERNEL(NB) \

@@ -513,7 +513,7 @@ static int run_dxt(const float *dy, const float *W, float *dx, int nb, int M, in
         if (rc) return rc;
         int64_t n = (int64_t)c * K;
         void *a2[] = {&part, &chunks, &c, &K, &dxc};
-        if ((rc = ncm_launch_named("dxt_final", (unsigned)((n + 255) / 256), 1, 1, 256, a2))) return rc;
+        if ((rc = ncm_launch_named("dxt_final", (unsigned)((n + 63) / 64), 1, 1, 256, a2))) return rc;
         r0 += c;
     }
     return 0;
